@@ -1,0 +1,125 @@
+// Internal declarations shared by the HIP sources of libingot_hip: the context, error reporting, the packed weight
+// and activation layouts, and the kernel launchers. Not part of the public C ABI (include/ingot_hip.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+#include <string>
+#include <vector>
+
+#include "../../include/ingot_hip.h"
+
+namespace ih {
+
+// ---------------------------------------------------------------------------------------------------------------
+// Errors: every C entry point returns a status and leaves a message in a thread-local string (ih_last_error).
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+#define IH_HIP(expr)                                                                                             \
+  do {                                                                                                           \
+    hipError_t e_ = (expr);                                                                                      \
+    if (e_ != hipSuccess)                                                                                        \
+      return ::ih::fail(IH_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_) + " (" + __FILE__ + ":" + \
+                                        std::to_string(__LINE__) + ")");                                         \
+  } while (0)
+
+#define IH_CHECK(cond, code, msg)                     \
+  do {                                                \
+    if (!(cond)) return ::ih::fail((code), (msg));    \
+  } while (0)
+
+#define IH_TRY(expr)                 \
+  do {                               \
+    int s_ = (expr);                 \
+    if (s_ != IH_OK) return s_;      \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------------------------------
+// bf16 / fp16 on the host (round to nearest even, as Loader/Quant.swift floatToBF16).
+inline float bf16_to_f32(uint16_t v) {
+  uint32_t u = uint32_t(v) << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Layout constants.
+//
+// Quantized matrices are repacked once (at creation) into tiles of 16 output rows × 128 K ("K-blocks"). In a tile
+// each of the 64 lanes of a wave owns 16 contiguous bytes: lane L = 16·qd + n holds row n, and its four 32-bit
+// words are the original words {qd, 4+qd, 8+qd, 12+qd} of that row's K-block (original word w covers K 8w…8w+7).
+// Component t of the lane's 16 bytes therefore covers K [32t + 8qd, +8): MFMA t (16×16×32) consumes component t of
+// every lane, and MFMAs 0–1 cover group 0 (K 0…63) and 2–3 group 1 (K 64…127) of an int4 g64 block; for MXFP4
+// (g32) MFMA t covers group t. A wave's weight load is one 1024-byte contiguous dwordx4 read.
+constexpr int TILE_N = 16;      // output rows per tile
+constexpr int KBLK = 128;       // K per block
+constexpr int MAX_TOK = 32;     // tokens per qmm (two 16-token MFMA tiles)
+
+// Activations (the A operand of every qmm) use the "fragment" layout: for token i and K-block kb, 256 bytes ordered
+// [qd][t][8] where element e of (qd, t) is x[128kb + 32t + 8qd + perm(e)], perm = {0,4,1,5,2,6,3,7} (the order in
+// which one 32-bit word of nibbles turns into four bf16/fp16 pairs). Alongside, the per-group sums of the same
+// (rounded) values: xsum[g][token], fp32, for the affine correction Σ x·(base + q) → s·acc + (b − base·s)·Σx.
+struct ActBuf {
+  void* frag = nullptr;   // [MAX_TOK][nkb][64 B × 4] (bf16 or fp16 elements)
+  float* xsum = nullptr;  // [ngroups64][MAX_TOK]
+  int K = 0, nkb = 0;
+  bool f16 = false;       // element type: fp16 (MXFP4 experts) or bf16 (everything else)
+};
+
+enum QFormat : int { QF_INT4 = 0, QF_MXFP4 = 1 };
+
+}  // namespace ih
+
+// The opaque handles of the C ABI.
+struct ih_qmat {
+  ih_ctx* ctx = nullptr;
+  int format = 0;          // QF_INT4 / QF_MXFP4
+  int E = 1;               // stacked experts
+  int N = 0, K = 0;        // logical shape per expert
+  int Npad = 0;            // rows rounded up to the launch granule
+  int nkb = 0;             // ceil(K / 128)
+  int ktail = 0;           // 1 when K % 128 == 64 (int4) or K % 128 in {32,64,96} (mxfp4): last block is partial
+  void* w = nullptr;       // packed words [E][Npad/16][nkb][64] uint4
+  void* s = nullptr;       // int4: [E][Npad/16][nkb][16] uint2 (s0,b0,s1,b1 bf16); mxfp4: [E][Npad/16][nkb][16] u32
+  size_t wbytes = 0, sbytes = 0;
+  size_t algo_bytes = 0;   // bytes of the source format (MLX) per expert: the roofline's algorithmic bytes
+};
+
+struct ih_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // Split-K scratch of the qmm: partial sums and arrival counters (the counters return to zero by themselves).
+  float* part = nullptr;
+  size_t part_bytes = 0;
+  unsigned* counters = nullptr;
+  size_t n_counters = 0;
+  // Staging for the kernel-level entry points that take a natural-layout activation.
+  ih::ActBuf act;
+  size_t act_cap_k = 0;
+  int cu_count = 256;
+};
+
+namespace ih {
+int fill(ih_ctx* c, void* dst, int byte, size_t bytes);
+int ensure_part(ih_ctx* c, size_t bytes);
+int ensure_act(ih_ctx* c, ActBuf& a, int K, bool f16);
+void free_act(ActBuf& a);
+
+// Launchers (qmm.hip).
+enum QmmOut : int {
+  QO_F32 = 0,        // y[m][n] = v (fp32)
+  QO_F32_ADD = 1,    // y[m][n] += v (fp32 residual)
+  QO_BF16 = 2,       // y[m][n] = bf16(v)
+};
+int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a);
+int launch_act_from_f32(ih_ctx* c, const float* x, int ldx, int M, ActBuf& a);
+int launch_qmm(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, void* y, int ldy, int out_mode);
+int pack_int4(ih_ctx* c, ih_qmat* q, const uint32_t* w_dev, const uint16_t* s_dev, const uint16_t* b_dev);
+}  // namespace ih

@@ -1,0 +1,160 @@
+"""CPU oracle — TEST INFRASTRUCTURE ONLY.
+
+ctypes front end of oracle/liboracle.so (oracle.cpp, a C++17 restatement of the reference's verify-step semantics).
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, as the checker or the
+timed CPU baseline; the product (ingot_amd) never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_lib = None
+
+f32p = C.POINTER(C.c_float)
+u32p = C.POINTER(C.c_uint32)
+u16p = C.POINTER(C.c_uint16)
+u8p = C.POINTER(C.c_uint8)
+i32p = C.POINTER(C.c_int32)
+vp = C.c_void_p
+i32 = C.c_int
+
+
+def build() -> Path:
+    """Compiles liboracle.so with the committed Makefile."""
+    r = subprocess.run(["make", "-s", "-C", str(HERE)], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{r.stdout}\n{r.stderr}")
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: run `make -C oracle`")
+        _lib = C.CDLL(str(LIB_PATH))
+        for name, res, args in _SIGS:
+            if hasattr(_lib, name):
+                f = getattr(_lib, name)
+                f.restype, f.argtypes = res, args
+    return _lib
+
+
+_SIGS = [
+    ("or_bf16_to_f32", C.c_float, [C.c_uint16]),
+    ("or_f32_to_bf16", C.c_uint16, [C.c_float]),
+    ("or_fp4_e2m1", C.c_float, [C.c_uint32]),
+    ("or_e8m0", C.c_float, [C.c_uint8]),
+    ("or_dequant_int4", None, [vp, vp, vp, i32, i32, vp]),
+    ("or_dequant_mxfp4", None, [vp, vp, i32, i32, vp]),
+    ("or_qmm_int4", None, [vp, i32, vp, vp, vp, i32, i32, vp]),
+    ("or_qmm_mxfp4", None, [vp, i32, vp, vp, i32, i32, vp]),
+    ("or_argmax_rows", None, [vp, i32, i32, vp]),
+    ("or_accept", i32, [vp, vp, i32, vp]),
+    ("or_num_threads", i32, []),
+]
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle inputs must be contiguous"
+    return a.ctypes.data
+
+
+# ---- number formats ----------------------------------------------------------------------------------------------
+
+def bf16_to_f32(v: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns (uint16) → float32 (exact)."""
+    return (np.asarray(v, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 → bf16 bit patterns, round to nearest even (Loader/Quant.swift:121-125)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    return bf16_to_f32(f32_to_bf16(x))
+
+
+def fp4_e2m1(q: int) -> float:
+    return float(lib().or_fp4_e2m1(q))
+
+
+def e8m0(s: int) -> float:
+    return float(lib().or_e8m0(s))
+
+
+def dequant_int4(w: np.ndarray, s: np.ndarray, b: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.uint32)
+    s = np.ascontiguousarray(s, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    N, K = w.shape[0], w.shape[1] * 8
+    out = np.empty((N, K), np.float32)
+    lib().or_dequant_int4(_p(w), _p(s), _p(b), N, K, _p(out))
+    return out
+
+
+def dequant_mxfp4(w: np.ndarray, s: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.uint32)
+    s = np.ascontiguousarray(s, np.uint8)
+    N, K = w.shape[0], w.shape[1] * 8
+    out = np.empty((N, K), np.float32)
+    lib().or_dequant_mxfp4(_p(w), _p(s), N, K, _p(out))
+    return out
+
+
+# ---- kernels of the verify step ----------------------------------------------------------------------------------
+
+def qmm_int4(x: np.ndarray, w: np.ndarray, s: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Y[M, N] = X[M, K] · dequant(W)ᵀ in fp32 (X given as float values)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.uint32)
+    s = np.ascontiguousarray(s, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    M, K = x.shape
+    N = w.shape[0]
+    assert w.shape[1] * 8 == K
+    y = np.empty((M, N), np.float32)
+    lib().or_qmm_int4(_p(x), M, _p(w), _p(s), _p(b), N, K, _p(y))
+    return y
+
+
+def qmm_mxfp4(x: np.ndarray, w: np.ndarray, s: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.uint32)
+    s = np.ascontiguousarray(s, np.uint8)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), np.float32)
+    lib().or_qmm_mxfp4(_p(x), M, _p(w), _p(s), N, K, _p(y))
+    return y
+
+
+def argmax_rows(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    rows, N = x.shape
+    out = np.empty(rows, np.uint32)
+    lib().or_argmax_rows(_p(x), rows, N, _p(out))
+    return out
+
+
+def accept(vtok: np.ndarray, top1: np.ndarray) -> tuple[int, np.ndarray]:
+    """Greedy acceptance: (m, emitted tokens [m + 1])."""
+    vtok = np.ascontiguousarray(vtok, np.uint32)
+    top1 = np.ascontiguousarray(top1, np.uint32)
+    B = len(vtok)
+    em = np.zeros(B, np.uint32)
+    m = lib().or_accept(_p(vtok), _p(top1), B, _p(em))
+    return m, em[: m + 1].copy()
+
+
+def num_threads() -> int:
+    return int(lib().or_num_threads())

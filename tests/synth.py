@@ -1,0 +1,43 @@
+"""Seeded synthetic tensors for the tests (numpy; not the product's synthetic-model generator)."""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import f32_to_bf16, bf16_to_f32
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.default_rng(seed)
+
+
+def int4_matrix(g: np.random.Generator, N: int, K: int, E: int | None = None, scale_sd: float = 0.02):
+    """MLX int4 g64: uniform codes, bf16 scale ~ |N(0, scale_sd)|, bias = -8·scale."""
+    shape = (N, K) if E is None else (E, N, K)
+    q = g.integers(0, 16, size=shape, dtype=np.uint32)
+    w = pack_nibbles(q)
+    gs = shape[:-1] + (K // 64,)
+    s = f32_to_bf16(np.abs(g.normal(0, scale_sd, size=gs)).astype(np.float32))
+    b = f32_to_bf16(-8.0 * bf16_to_f32(s))
+    return w, s, b
+
+
+def pack_nibbles(q: np.ndarray) -> np.ndarray:
+    """Codes [..., K] (0..15) → uint32 [..., K/8], value j in bits 4j (low nibble first)."""
+    q = q.astype(np.uint32)
+    sh = q.reshape(q.shape[:-1] + (q.shape[-1] // 8, 8))
+    out = np.zeros(sh.shape[:-1], np.uint32)
+    for j in range(8):
+        out |= sh[..., j] << np.uint32(4 * j)
+    return out
+
+
+def bf16_normal(g: np.random.Generator, shape, sd: float = 1.0):
+    """(bf16 bits, their float values)."""
+    v = f32_to_bf16(g.normal(0, sd, size=shape).astype(np.float32))
+    return v, bf16_to_f32(v)
+
+
+def cosine(a: np.ndarray, b: np.ndarray) -> float:
+    a = a.astype(np.float64).ravel()
+    b = b.astype(np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
