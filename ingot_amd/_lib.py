@@ -173,3 +173,46 @@ class QMat:
         if self.handle:
             lib().ih_qmat_free(self.handle)
             self.handle = None
+
+
+class HipEvents:
+    """HIP events recorded on the library context's stream (libamdhip64 through ctypes)."""
+
+    _hip = None
+
+    @classmethod
+    def hip(cls):
+        if cls._hip is None:
+            h = C.CDLL("libamdhip64.so")
+            h.hipEventCreate.argtypes = [P(vp)]
+            h.hipEventRecord.argtypes = [vp, vp]
+            h.hipEventSynchronize.argtypes = [vp]
+            h.hipEventElapsedTime.argtypes = [P(C.c_float), vp, vp]
+            h.hipEventDestroy.argtypes = [vp]
+            cls._hip = h
+        return cls._hip
+
+    def __init__(self, ctx: Context, n: int):
+        self.stream = ctx.stream
+        self.ev = []
+        for _ in range(n):
+            e = vp()
+            if self.hip().hipEventCreate(C.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            self.ev.append(e.value)
+
+    def record(self, i: int) -> None:
+        if self.hip().hipEventRecord(self.ev[i], self.stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        self.hip().hipEventSynchronize(self.ev[b])
+        t = C.c_float()
+        if self.hip().hipEventElapsedTime(C.byref(t), self.ev[a], self.ev[b]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return t.value
+
+    def close(self) -> None:
+        for e in self.ev:
+            self.hip().hipEventDestroy(e)
+        self.ev = []

@@ -12,9 +12,12 @@
 //     ((w >> 4c) & 0x000F000F | 0x43004300), so the MFMA sums Σ x·(128 + q) exactly in fp32 per group of 64, and the
 //     affine map is applied once per group and output: y += s·acc + (b − 128·s)·Σx. No rounding of the dequantised
 //     weight (the reference rounds it to half); the only rounding is fp32 accumulation.
-//   - Split-K over a fixed number of slices chosen from (N, K) only, never from M, and the slices are summed in slice
-//     order by the last workgroup to arrive: deterministic and row-invariant (row r's bits do not depend on M).
+//   - K is split over the waves of a workgroup (a split chosen from (N, K) only, never from M) and the partial sums are
+//     added in wave order in LDS: deterministic and row-invariant (row r's bits do not depend on M).
 #include "ih_internal.h"
+
+#include <cstdio>
+#include <cstdlib>
 
 namespace ih {
 
@@ -29,13 +32,22 @@ __device__ __forceinline__ unsigned short f2bf(float f) {
   return (unsigned short)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
-// Eight nibbles of one word → eight bf16 values 128 + q in the element order {0,4,1,5,2,6,3,7}.
-__device__ __forceinline__ bf16x8 nib_bf16(unsigned w) {
+// (w & km) | kb in one v_and_or_b32 (LLVM selects a v_and/v_or pair here). km in a VGPR, kb in an SGPR: gfx9 VOP3
+// reads at most one scalar operand.
+__device__ __forceinline__ unsigned and_or(unsigned w, unsigned km, unsigned kb) {
+  unsigned r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(km), "s"(kb));
+  return r;
+}
+
+// Eight nibbles of one word → eight bf16 values 128 + q in the element order {0,4,1,5,2,6,3,7}. km = 0x000F000F,
+// kb = 0x43004300 (runtime values, see QmmParams).
+__device__ __forceinline__ bf16x8 nib_bf16(unsigned w, unsigned km, unsigned kb) {
   u32x4 v;
-  v.x = (w & 0x000F000Fu) | 0x43004300u;
-  v.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  v.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  v.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  v.x = and_or(w, km, kb);
+  v.y = and_or(w >> 4, km, kb);
+  v.z = and_or(w >> 8, km, kb);
+  v.w = and_or(w >> 12, km, kb);
   return __builtin_bit_cast(bf16x8, v);
 }
 
@@ -112,11 +124,18 @@ struct QmmParams {
   const uint2* s;          // packed scale/bias of the expert
   const uint4* xa;         // activation fragments
   const float* xs;         // activation group sums [2·nkb][MAX_TOK]
-  float* part;             // split-K partials [splits][MAX_TOK][Npad]
-  unsigned* counters;      // one per workgroup column
   void* y;
-  int ldy, M, N, Npad, nkb, kps, out_mode;
+  int ldy, M, N, Npad, nkb, out_mode;
+  // The nibble-decode constants 0x000F000F and 0x43004300, passed as arguments so that they live in SGPRs and the
+  // compiler can use the three-operand v_and_or_b32 (gfx9 VOP3 takes no literal constants).
+  unsigned kmask, kbias;
 };
+
+// Buffer resources (base in SGPRs, 32-bit offsets; an offset past num_records reads as zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr unsigned OOB = 0x80000000u;  // offset that reads as zero
 
 __device__ __forceinline__ void qmm_store(const QmmParams& p, int m, int row, float v) {
   if (p.out_mode == QO_F32) {
@@ -129,116 +148,195 @@ __device__ __forceinline__ void qmm_store(const QmmParams& p, int m, int row, fl
   }
 }
 
-// T: 16-token tiles (1 or 2); R: 16-row weight tiles per wave. Workgroup = 4 waves = 64·R rows, one K slice.
-template <int T, int R>
-__global__ __launch_bounds__(256) void qmm_int4_kernel(QmmParams p) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n = lane & 15, qd = lane >> 4;
-  const int tile0 = (blockIdx.x * 4 + wave) * R;
-  const int kb0 = blockIdx.y * p.kps;
-  const int kb1 = min(p.nkb, kb0 + p.kps);
-  f32x4 acc[R][T];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int tt = 0; tt < T; ++tt) acc[r][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+// One K-block's operands of a wave: R weight tiles (+ scale/bias) and the T token tiles of x (+ group sums).
+template <int T, int R, bool X16>
+struct QmmStage {
+  u32x4 w[R];
+  uint2 sb[R];
+  u32x4 x[T][4];
+  f32x4 xs[T][2];
+  u32x4 x16[X16 ? 4 : 1];   // token 16 (VALU path): this lane's 64 bytes of it
+  float xs16[2];
+};
 
-  for (int kb = kb0; kb < kb1; ++kb) {
-    bf16x8 xa[T][4];
-    f32x4 xs[T][2];
-#pragma unroll
-    for (int tt = 0; tt < T; ++tt) {
-      const uint4* src = p.xa + ((size_t(16 * tt + n) * p.nkb + kb) * 4 + qd) * 4;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        uint4 u = src[t];
-        xa[tt][t] = __builtin_bit_cast(bf16x8, u32x4{u.x, u.y, u.z, u.w});
-      }
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-        xs[tt][g] = *reinterpret_cast<const f32x4*>(p.xs + (2 * kb + g) * MAX_TOK + 16 * tt + 4 * qd);
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const size_t tb = size_t(tile0 + r) * p.nkb + kb;
-      const u32x4 wv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.w) + tb * 64 + lane);
-      const uint2 sb = p.s[tb * 16 + n];
-      const float s0 = bf16f(sb.x & 0xFFFFu), s1 = bf16f(sb.y & 0xFFFFu);
-      const float c0 = fmaf(-128.f, s0, bf16f(sb.x >> 16)), c1 = fmaf(-128.f, s1, bf16f(sb.y >> 16));
-      const unsigned ww[4] = {wv[0], wv[1], wv[2], wv[3]};
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const bf16x8 w0 = nib_bf16(ww[2 * g]), w1 = nib_bf16(ww[2 * g + 1]);
-        const float sg = g ? s1 : s0, cg = g ? c1 : c0;
-#pragma unroll
-        for (int tt = 0; tt < T; ++tt) {
-          f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][2 * g], w0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][2 * g + 1], w1, tmp, 0, 0, 0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[r][tt][e] = fmaf(sg, tmp[e], fmaf(cg, xs[tt][g][e], acc[r][tt][e]));
-        }
-      }
-    }
-  }
+// Buffer resources of one launch and the per-lane offsets that do not change along K.
+struct QmmRsrc {
+  __amdgpu_buffer_rsrc_t w, s, x, xs;
+  unsigned xoff[2];   // token row offset of this lane's A operand (OOB for dead tokens), per token tile
+  unsigned xsoff[2];  // group-sum offset of this lane's 4 output tokens (OOB if none live)
+  unsigned x16off, xs16off;
+};
 
-  // Output element (token m = 16·tt + 4·qd + e, row = 16·tile + n).
-  if (gridDim.y == 1) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = (tile0 + r) * 16 + n;
-#pragma unroll
-      for (int tt = 0; tt < T; ++tt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = 16 * tt + 4 * qd + e;
-          if (m < p.M && row < p.N) qmm_store(p, m, row, acc[r][tt][e]);
-        }
-    }
-    return;
-  }
-  float* part = p.part + size_t(blockIdx.y) * MAX_TOK * p.Npad;
+template <int T, int R, bool X16>
+__device__ __forceinline__ void qmm_load(QmmStage<T, R, X16>& st, const QmmParams& p, const QmmRsrc& rs, int tile0,
+                                         int kb, int lane, int n) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = (tile0 + r) * 16 + n;
-#pragma unroll
-    for (int tt = 0; tt < T; ++tt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = 16 * tt + 4 * qd + e;
-        if (m < p.M) part[size_t(m) * p.Npad + row] = acc[r][tt][e];
-      }
+    const unsigned tb = unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kb);
+    st.w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, tb * 1024u + lane * 16u, 0, 0));
+    st.sb[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.s, tb * 128u + n * 8u, 0, 0));
   }
-  __threadfence();
-  __syncthreads();
-  __shared__ unsigned s_last;
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&p.counters[blockIdx.x], 1u);
-    s_last = (prev == gridDim.y - 1) ? 1u : 0u;
-    if (s_last) p.counters[blockIdx.x] = 0u;
+  const unsigned kx = unsigned(kb) * 256u, kxs = unsigned(kb) * (2 * MAX_TOK * 4);
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt) {
+    // Dead token lanes point past the buffer and read zeros (their MFMA outputs are discarded).
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      st.x[tt][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, rs.xoff[tt] + kx + 16 * t, 0, 0));
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+      st.xs[tt][g] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.xs, rs.xsoff[tt] + kxs + g * (MAX_TOK * 4), 0, 0));
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const int rows = 64 * R, base = blockIdx.x * rows;
-  for (int idx = threadIdx.x; idx < p.M * rows; idx += 256) {
-    const int m = idx / rows, row = base + idx % rows;
-    if (row >= p.N) continue;
-    float v = 0.f;
-    for (int sl = 0; sl < (int)gridDim.y; ++sl) v += p.part[(size_t(sl) * MAX_TOK + m) * p.Npad + row];
-    qmm_store(p, m, row, v);
+  if constexpr (X16) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      st.x16[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, rs.x16off + kx + 16 * t, 0, 0));
+    st.xs16[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.xs, rs.xs16off + kxs, 0, 0));
+    st.xs16[1] = __builtin_bit_cast(float,
+                                    __builtin_amdgcn_raw_buffer_load_b32(rs.xs, rs.xs16off + kxs + MAX_TOK * 4, 0, 0));
   }
 }
 
-// Split-K slices for an (Npad, nkb) launch: enough workgroups to cover the device about twice, at least two K-blocks
-// per slice. Depends only on the matrix shape and the device, never on M.
-static void qmm_plan(const ih_ctx* c, int Npad, int nkb, int R, int* splits, int* kps) {
-  const int wgx = Npad / (64 * R);
-  const int target = 2 * c->cu_count;
-  int s = (target + wgx - 1) / wgx;
-  s = std::max(1, std::min(s, nkb / 2 > 0 ? nkb / 2 : 1));
-  int k = (nkb + s - 1) / s;
-  *kps = k;
-  *splits = (nkb + k - 1) / k;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+template <int T, int R, bool X16>
+__device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R], const QmmStage<T, R, X16>& st,
+                                            float qd0, unsigned km, unsigned kbias) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float s0 = bf16f(st.sb[r].x & 0xFFFFu), s1 = bf16f(st.sb[r].y & 0xFFFFu);
+    const float c0 = fmaf(-128.f, s0, bf16f(st.sb[r].x >> 16)), c1 = fmaf(-128.f, s1, bf16f(st.sb[r].y >> 16));
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const bf16x8 w0 = nib_bf16(st.w[r][2 * g], km, kbias), w1 = nib_bf16(st.w[r][2 * g + 1], km, kbias);
+      const float sg = g ? s1 : s0, cg = g ? c1 : c0;
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) {
+        f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g]), w0,
+                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), w1, tmp, 0,
+                                                      0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[r][tt][e] = fmaf(sg, tmp[e], fmaf(cg, st.xs[tt][g][e], acc[r][tt][e]));
+      }
+      if constexpr (X16) {
+        // Token 16 by packed bf16 dot products: this lane's 16 values of the group (its row n, K slice qd); the
+        // group's bias term is added by the qd = 0 lanes only (qd0 = 1 there, 0 elsewhere), the four K slices are
+        // summed across lanes at the end.
+        float d = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const unsigned wr = st.w[r][2 * g + h];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const unsigned wp = and_or(wr >> (4 * j), km, kbias);
+            const unsigned xp = st.x16[2 * g + h][j];
+            d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wp), __builtin_bit_cast(bf16x2, xp), d,
+                                                false);
+          }
+        }
+        acc16[r] = fmaf(sg, d, fmaf(cg * qd0, st.xs16[g], acc16[r]));
+      }
+    }
+  }
+}
+
+// Workgroup = KW waves over the same 16·R rows; wave w takes K-blocks w, w + KW, … (adjacent waves read adjacent
+// 1 KB blocks), with the next block's loads in flight while the current one is multiplied. The KW partial sums are
+// added in wave order through LDS: no cross-workgroup synchronisation (an agent-scope fence on MI355X writes the
+// XCD's L2 back and costs tens of µs) and a summation order that depends only on (N, K).
+// T: MFMA token tiles (tokens 0–15, and 17–31 when T = 2); X16: token 16 present (M ≥ 17), done on VALU.
+template <int T, int R, int KW, bool X16>
+__global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = lane & 15, qd = lane >> 4;
+  const int tile0 = blockIdx.x * R;
+  const float qd0 = qd == 0 ? 1.f : 0.f;
+  f32x4 acc[R][T];
+  float acc16[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc16[r] = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) acc[r][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  QmmRsrc rs;
+  const unsigned tiles_total = unsigned(p.Npad / 16) * unsigned(p.nkb);
+  rs.w = make_rsrc(p.w, tiles_total * 1024u);
+  rs.s = make_rsrc(p.s, tiles_total * 128u);
+  rs.x = make_rsrc(p.xa, unsigned(MAX_TOK) * p.nkb * 256u);
+  rs.xs = make_rsrc(p.xs, unsigned(2 * p.nkb) * MAX_TOK * 4u);
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int tok = 16 * tt + n;
+    const bool live = tt < T && tok < p.M && !(X16 && tok == 16);
+    rs.xoff[tt] = live ? (unsigned(tok) * p.nkb * 256u + qd * 64u) : OOB;
+    rs.xsoff[tt] = (tt < T && 16 * tt + 4 * qd < p.M) ? unsigned(16 * tt + 4 * qd) * 4u : OOB;
+  }
+  rs.x16off = 16u * p.nkb * 256u + qd * 64u;
+  rs.xs16off = 16u * 4u;
+  const unsigned km = p.kmask, kbias = p.kbias;
+
+  QmmStage<T, R, X16> a, b;
+  int kb = wave;
+  if (kb < p.nkb) {
+    qmm_load(a, p, rs, tile0, kb, lane, n);
+    while (true) {
+      if (kb + KW < p.nkb) qmm_load(b, p, rs, tile0, kb + KW, lane, n);
+      qmm_compute(acc, acc16, a, qd0, km, kbias);
+      kb += KW;
+      if (kb >= p.nkb) break;
+      if (kb + KW < p.nkb) qmm_load(a, p, rs, tile0, kb + KW, lane, n);
+      qmm_compute(acc, acc16, b, qd0, km, kbias);
+      kb += KW;
+      if (kb >= p.nkb) break;
+    }
+  }
+
+  // Partial sums of every wave → LDS [wave][r][tt][e][lane], then a fixed-order sum over the waves.
+  // Token 16: sum the four K slices of each row across lanes (qd = lane bits 4–5), fixed order.
+  if constexpr (X16) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      acc16[r] += __shfl_xor(acc16[r], 16);
+      acc16[r] += __shfl_xor(acc16[r], 32);
+    }
+  }
+  constexpr int NEL = R * T * 4 * 64;
+  constexpr int NEL16 = X16 ? R * 16 : 0;
+  __shared__ float red[KW * (NEL + NEL16)];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[wave * (NEL + NEL16) + ((r * T + tt) * 4 + e) * 64 + lane] = acc[r][tt][e];
+  if constexpr (X16) {
+    if (lane < 16) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) red[wave * (NEL + NEL16) + NEL + r * 16 + lane] = acc16[r];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < NEL + NEL16; i += 64 * KW) {
+    int m, row;
+    if (i < NEL) {
+      const int l = i & 63, e = (i >> 6) & 3, tt = (i >> 8) % T, r = (i >> 8) / T;
+      m = 16 * tt + 4 * (l >> 4) + e;
+      row = (tile0 + r) * 16 + (l & 15);
+      if (X16 && m == 16) continue;
+    } else {
+      m = 16;
+      row = tile0 * 16 + (i - NEL);
+    }
+    if (m >= p.M || row >= p.N) continue;
+    float v = red[i];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) v += red[w * (NEL + NEL16) + i];
+    qmm_store(p, m, row, v);
+  }
 }
 
 int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
@@ -253,13 +351,33 @@ int launch_act_from_f32(ih_ctx* c, const float* x, int ldx, int M, ActBuf& a) {
   return IH_OK;
 }
 
+// Launch shape for an (Npad, nkb) matrix: rows per workgroup (16·R) and waves per workgroup (KW, the intra-workgroup
+// split of K). Chosen from the shape only, never from M, so each row's summation order is fixed.
+struct QmmShape { int R, KW; };
+static QmmShape qmm_shape(int Npad, int nkb) {
+  const int NT = Npad / 16;
+  if (NT >= 4096) return {4, 4};
+  if (NT >= 1024) return {2, 4};
+  if (NT >= 512 || nkb < 16) return {1, 4};
+  if (nkb < 64) return {1, 8};
+  return {1, 16};
+}
+
+template <int T, bool X16>
+static void qmm_dispatch(QmmShape sh, int grid, hipStream_t st, const QmmParams& p) {
+  if (sh.R == 4) qmm_int4_kernel<T, 4, 4, X16><<<grid, 256, 0, st>>>(p);
+  else if (sh.R == 2) qmm_int4_kernel<T, 2, 4, X16><<<grid, 256, 0, st>>>(p);
+  else if (sh.KW == 4) qmm_int4_kernel<T, 1, 4, X16><<<grid, 256, 0, st>>>(p);
+  else if (sh.KW == 8) qmm_int4_kernel<T, 1, 8, X16><<<grid, 512, 0, st>>>(p);
+  else qmm_int4_kernel<T, 1, 16, X16><<<grid, 1024, 0, st>>>(p);
+}
+
 int launch_qmm(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, void* y, int ldy, int out_mode) {
   IH_CHECK(W->format == QF_INT4, IH_EINVAL, "qmm: int4 matrix expected");
   IH_CHECK(M >= 1 && M <= MAX_TOK, IH_EINVAL, "qmm: M must be in 1..32");
   IH_CHECK(a.nkb == W->nkb && !a.f16, IH_EINVAL, "qmm: activation K does not match the matrix");
-  const int R = 2;
-  int splits, kps;
-  qmm_plan(c, W->Npad, W->nkb, R, &splits, &kps);
+  QmmShape sh = qmm_shape(W->Npad, W->nkb);
+  if (const char* ov = getenv("IH_QMM_SHAPE")) sscanf(ov, "%d,%d", &sh.R, &sh.KW);  // tuning override
   QmmParams p;
   const size_t tiles_per_e = size_t(W->Npad / 16) * W->nkb;
   p.w = static_cast<const uint4*>(W->w) + tiles_per_e * 64 * expert;
@@ -272,18 +390,13 @@ int launch_qmm(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, 
   p.N = W->N;
   p.Npad = W->Npad;
   p.nkb = W->nkb;
-  p.kps = kps;
   p.out_mode = out_mode;
-  const int wgx = W->Npad / (64 * R);
-  if (splits > 1) {
-    IH_TRY(ensure_part(c, size_t(splits) * MAX_TOK * W->Npad * 4));
-    IH_CHECK(size_t(wgx) <= c->n_counters, IH_EINVAL, "qmm: too many workgroups for the counter array");
-  }
-  p.part = c->part;
-  p.counters = c->counters;
-  dim3 grid(wgx, splits);
-  if (M > 16) qmm_int4_kernel<2, R><<<grid, 256, 0, c->stream>>>(p);
-  else qmm_int4_kernel<1, R><<<grid, 256, 0, c->stream>>>(p);
+  p.kmask = 0x000F000Fu;
+  p.kbias = 0x43004300u;
+  const int grid = W->Npad / (16 * sh.R);
+  if (M > 17) qmm_dispatch<2, true>(sh, grid, c->stream, p);
+  else if (M == 17) qmm_dispatch<1, true>(sh, grid, c->stream, p);
+  else qmm_dispatch<1, false>(sh, grid, c->stream, p);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -41,6 +41,7 @@ def run_qmm(ctx, W, xb, M, out_mode=0, y0=None):
         (16, 1024, 1024, 3),
         (17, 6144, 4096, 4),     # config 1 qkv at k = 16
         (32, 256, 768, 5),
+        (18, 512, 1024, 8),      # token 16 on VALU, tokens 17+ on the second MFMA tile
         (17, 1000, 2880, 6),     # K % 128 == 64 (config 4 hidden), N not a multiple of 16
         (3, 4096, 14336, 7),     # down projection K
     ],
