@@ -83,6 +83,103 @@ size_t ih_qmat_bytes(const ih_qmat* q);
 int ih_qmm_int4(ih_ctx* ctx, const ih_qmat* W, const void* x_bf16_dev, int ldx, int M, void* y_dev, int ldy,
                 int out_mode);
 
+
+/* ---- row kernels -------------------------------------------------------------------------------------------- */
+
+/* out[r] = argmax of row r of x[rows, N] (fp32, device), ties to the lowest index, NaN never wins. argmax_rows,
+ * Sources/Ingot/Shaders/verify.metal:525-547. Enqueued only. */
+int ih_argmax_rows(ih_ctx* ctx, const float* x_dev, int rows, int N, uint32_t* out_dev);
+
+/* Result of greedy acceptance: m accepted drafts, then the emitted tokens vtok[1..m] followed by the new anchor
+ * top1[m] (n_emitted = m + 1). */
+typedef struct ih_accept_result {
+  int m;
+  int n_emitted;
+  uint32_t tokens[IH_MAX_ROWS];
+} ih_accept_result;
+
+/* Greedy acceptance on the host: m = the longest prefix of drafts vtok[1..B-1] with vtok[i+1] == top1[i]. The host form
+ * of generateSpec's acceptance (Sources/Ingot/Generate.swift:155-158). Integer only, no device. */
+int ih_accept(const uint32_t* vtok, const uint32_t* top1, int B, ih_accept_result* out);
+
+/* Round record layout of the device-side acceptance (yy_model.metal:616-617: REC_STRIDE 24, REC_P 20, REC_ROWS 21). */
+#define IH_REC_STRIDE 24
+#define IH_REC_P 20
+#define IH_REC_ROWS 21
+/* Greedy acceptance on the device, one thread, enqueued (spec_accept, Sources/Ingot/Shaders/yy_model.metal:616-642):
+ * st (uint32[8]) = [P, nacc, pend, pendPos, anchor, round, rows]; writes rec[round % ring] = (m, tokens…, [IH_REC_P] = P
+ * before, [IH_REC_ROWS] = rows), advances st (P += m + 1) and sets vtok[0] = the new anchor. rows = 0 reads st[6]. */
+int ih_spec_accept_dev(ih_ctx* ctx, uint32_t* st_dev, uint32_t* vtok_dev, const uint32_t* top1_dev, uint32_t* rec_dev,
+                       int ring, int rows);
+
+/* ---- model and KV cache ------------------------------------------------------------------------------------- */
+
+typedef struct ih_model ih_model;
+typedef struct ih_kv ih_kv;
+
+/* Architecture of a decoder (the ModelDims / ModelSpec fields the verify round reads, Sources/Ingot/Shaders/
+ * aa_dims.metal:1-123). Attention-only layers; dense SwiGLU FFN when n_experts == 0, else a routed MoE. */
+typedef struct ih_model_desc {
+  int n_layers;
+  int hidden;
+  int n_q_heads, n_kv_heads, head_dim; /* head_dim 64 or 128 */
+  int intermediate;                    /* dense FFN intermediate (n_experts == 0) */
+  int vocab;
+  float rope_theta;
+  float rms_eps;
+  int n_experts, top_k, expert_intermediate; /* MoE (n_experts > 0): softmax router, renormalised top-k */
+  int expert_format;                   /* 0 = MLX int4 g64, 1 = MXFP4 (e2m1 + e8m0 per 32) */
+  int router_bias;                     /* router linear bias added to the logits (gpt-oss) */
+  int expert_bias;                     /* per-expert gate/up/down biases (gpt-oss) */
+  int act;                             /* 0 = SiLU(gate)·up, 1 = swiglu_oai (α 1.702, clip swiglu_limit) */
+  float swiglu_limit;
+  int sliding_window;                  /* 0 = none; > 0: even layers use this window (counting the row's own key) */
+  int sinks;                           /* learned attention sinks, one logit per q head */
+  int hadamard_k;                      /* store H·k and rotate q (the reference's default "hadk" scheme) */
+} ih_model_desc;
+
+/* Creates a model with synthetic weights of `desc`'s shapes, deterministically from `seed` (counter-based SplitMix64
+ * streams per tensor; any element is reproducible on the CPU). Replaces HybridModel's loader for the benchmark
+ * configurations (Sources/Ingot/Model.swift); an MLX safetensors loader is a later addition. */
+int ih_model_create_synthetic(ih_ctx* ctx, const ih_model_desc* desc, uint64_t seed, ih_model** out);
+int ih_model_free(ih_model* model);
+/* Algorithmic bytes of the model's weights read by one verify step (all layers, head), MLX format. For MoE models the
+ * experts count once per distinct routed expert, so this returns the dense part only. */
+size_t ih_model_weight_bytes(const ih_model* model);
+
+/* An int8 KV cache for `capacity` positions (int8 K and V per KV head, fp16 scale per token and head). The attention
+ * key chunk is fixed per cache (256 … 2048 keys, from the capacity) so a row's result is the same for every block
+ * size. AttentionLayer's kc/vt/ks/vs (Sources/Ingot/Layers/Attention.swift:272-390). */
+int ih_kv_create(ih_model* model, int capacity, ih_kv** out);
+int ih_kv_free(ih_kv* kv);
+/* Fills positions 0..P-1 of every layer with synthetic int8 K/V (N(0,1) vectors quantised per token and head) and sets
+ * the position to P. */
+int ih_kv_fill_synthetic(ih_kv* kv, int P, uint64_t seed);
+/* Current position P (number of committed tokens). */
+int ih_kv_pos(const ih_kv* kv);
+/* Rollback: sets P back to `pos` (≤ the positions written so far). rewindExtraRound, Generate.swift:515-540. */
+int ih_kv_set_pos(ih_kv* kv, int pos);
+/* Commit: P += n, n ≤ the rows of the last verify step. HybridModel.commit(accepted:), ModelRound.swift:142-146. */
+int ih_kv_commit(ih_kv* kv, int n);
+/* Key chunk of the cache's attention splits. */
+int ih_kv_chunk(const ih_kv* kv);
+
+/* One verify step (HybridModel.encodeVerify, Sources/Ingot/ModelRound.swift:48-82): the B rows tokens[0..B-1] (anchor +
+ * B−1 drafts) at positions P..P+B−1 run through every layer (their K/V are written at those slots) and the head;
+ * top1_out[r] = argmax of row r. logits_out (nullable) receives fp32 [B, vocab]. P is not advanced: call ih_kv_commit
+ * with the accepted count (or leave it to roll the block back). Synchronous. 1 ≤ B ≤ IH_MAX_ROWS, P + B ≤ capacity. */
+int ih_verify_step(ih_model* model, ih_kv* kv, const uint32_t* tokens, int B, float* logits_out, uint32_t* top1_out);
+
+/* The same, enqueued only, with device buffers: tokens_dev (uint32[B]) in, top1_dev (uint32[B]) out. */
+int ih_verify_step_dev(ih_model* model, ih_kv* kv, const uint32_t* tokens_dev, int B, uint32_t* top1_dev);
+
+/* Verify, accept and commit in one call: runs the step on tokens (anchor + drafts), accepts the longest matching draft
+ * prefix, advances P by m + 1 and returns the result (the non-chained round of generateSpec, Generate.swift:104-177). */
+int ih_verify_and_accept(ih_model* model, ih_kv* kv, const uint32_t* tokens, int B, ih_accept_result* out);
+
+/* The model's device scratch of the last step: logits fp32 [rows ≥ B][vocab] (row stride = vocab). */
+const float* ih_model_logits_dev(const ih_model* model);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,23 @@ def _declare(L: C.CDLL) -> None:
         "ih_qmat_free": (i32, [vp]),
         "ih_qmat_bytes": (sz, [vp]),
         "ih_qmm_int4": (i32, [vp, vp, vp, i32, i32, vp, i32, i32]),
+        "ih_argmax_rows": (i32, [vp, vp, i32, i32, vp]),
+        "ih_accept": (i32, [vp, vp, i32, vp]),
+        "ih_spec_accept_dev": (i32, [vp, vp, vp, vp, vp, i32, i32]),
+        "ih_model_create_synthetic": (i32, [vp, vp, C.c_uint64, P(vp)]),
+        "ih_model_free": (i32, [vp]),
+        "ih_model_weight_bytes": (sz, [vp]),
+        "ih_kv_create": (i32, [vp, i32, P(vp)]),
+        "ih_kv_free": (i32, [vp]),
+        "ih_kv_fill_synthetic": (i32, [vp, i32, C.c_uint64]),
+        "ih_kv_pos": (i32, [vp]),
+        "ih_kv_set_pos": (i32, [vp, i32]),
+        "ih_kv_commit": (i32, [vp, i32]),
+        "ih_kv_chunk": (i32, [vp]),
+        "ih_verify_step": (i32, [vp, vp, vp, i32, vp, vp]),
+        "ih_verify_step_dev": (i32, [vp, vp, vp, i32, vp]),
+        "ih_verify_and_accept": (i32, [vp, vp, vp, i32, vp]),
+        "ih_model_logits_dev": (vp, [vp]),
     }
     for name, (res, args) in sig.items():
         if hasattr(L, name):
@@ -216,3 +233,107 @@ class HipEvents:
         for e in self.ev:
             self.hip().hipEventDestroy(e)
         self.ev = []
+
+
+MAX_ROWS = 17
+
+
+class AcceptResult(C.Structure):
+    _fields_ = [("m", C.c_int), ("n_emitted", C.c_int), ("tokens", C.c_uint32 * MAX_ROWS)]
+
+    @property
+    def emitted(self) -> list[int]:
+        return list(self.tokens[: self.n_emitted])
+
+
+class ModelDesc(C.Structure):
+    """ih_model_desc (include/ingot_hip.h)."""
+
+    _fields_ = [
+        ("n_layers", C.c_int), ("hidden", C.c_int), ("n_q_heads", C.c_int), ("n_kv_heads", C.c_int),
+        ("head_dim", C.c_int), ("intermediate", C.c_int), ("vocab", C.c_int), ("rope_theta", C.c_float),
+        ("rms_eps", C.c_float), ("n_experts", C.c_int), ("top_k", C.c_int), ("expert_intermediate", C.c_int),
+        ("expert_format", C.c_int), ("router_bias", C.c_int), ("expert_bias", C.c_int), ("act", C.c_int),
+        ("swiglu_limit", C.c_float), ("sliding_window", C.c_int), ("sinks", C.c_int), ("hadamard_k", C.c_int),
+    ]
+
+    @classmethod
+    def make(cls, **kw) -> "ModelDesc":
+        d = cls(rope_theta=1e6, rms_eps=1e-6, hadamard_k=1, swiglu_limit=7.0)
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return d
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+def accept(vtok, top1) -> AcceptResult:
+    vtok = np.ascontiguousarray(vtok, np.uint32)
+    top1 = np.ascontiguousarray(top1, np.uint32)
+    r = AcceptResult()
+    check(lib().ih_accept(ptr(vtok), ptr(top1), len(vtok), C.byref(r)))
+    return r
+
+
+class Model:
+    """A synthetic-weight model and its KV cache owned by the library."""
+
+    def __init__(self, ctx: Context, desc: ModelDesc, seed: int):
+        self.ctx, self.desc, self.seed = ctx, desc, seed
+        h = vp()
+        check(lib().ih_model_create_synthetic(ctx.handle, C.byref(desc), seed, C.byref(h)))
+        self.handle = h.value
+
+    @property
+    def weight_bytes(self) -> int:
+        return lib().ih_model_weight_bytes(self.handle)
+
+    def free(self) -> None:
+        if self.handle:
+            lib().ih_model_free(self.handle)
+            self.handle = None
+
+
+class KVCache:
+    def __init__(self, model: Model, capacity: int):
+        self.model = model
+        h = vp()
+        check(lib().ih_kv_create(model.handle, capacity, C.byref(h)))
+        self.handle = h.value
+
+    def fill_synthetic(self, P: int, seed: int) -> None:
+        check(lib().ih_kv_fill_synthetic(self.handle, P, seed))
+
+    @property
+    def pos(self) -> int:
+        return lib().ih_kv_pos(self.handle)
+
+    def set_pos(self, p: int) -> None:
+        check(lib().ih_kv_set_pos(self.handle, p))
+
+    def commit(self, n: int) -> None:
+        check(lib().ih_kv_commit(self.handle, n))
+
+    @property
+    def chunk(self) -> int:
+        return lib().ih_kv_chunk(self.handle)
+
+    def verify(self, tokens, want_logits: bool = False):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        top1 = np.zeros(len(t), np.uint32)
+        logits = np.zeros((len(t), self.model.desc.vocab), np.float32) if want_logits else None
+        check(lib().ih_verify_step(self.model.handle, self.handle, ptr(t), len(t),
+                                   ptr(logits) if logits is not None else None, ptr(top1)))
+        return (top1, logits) if want_logits else top1
+
+    def verify_and_accept(self, tokens) -> AcceptResult:
+        t = np.ascontiguousarray(tokens, np.uint32)
+        r = AcceptResult()
+        check(lib().ih_verify_and_accept(self.model.handle, self.handle, ptr(t), len(t), C.byref(r)))
+        return r
+
+    def free(self) -> None:
+        if self.handle:
+            lib().ih_kv_free(self.handle)
+            self.handle = None

@@ -2,6 +2,7 @@
 // the synthetic-data generators.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
 #include <cstdint>
 
 namespace ih {

@@ -1,0 +1,455 @@
+// The verify step: model and KV-cache objects and the per-layer composition of the kernels.
+//
+// Reference: HybridModel.encodeVerify (Sources/Ingot/ModelRound.swift:48-82): embed → per layer (RMSNorm → attention
+// pieces proj/prework/attn/reduce/oproj → RMSNorm → FFN) → head → argmax; commit(accepted:) (:142-146).
+#include <hip/hip_fp16.h>
+
+#include <cmath>
+#include <cstring>
+#include <memory>
+
+#include "act.h"
+#include "attn_args.h"
+#include "ih_internal.h"
+
+namespace ih {
+
+// Launchers of the other translation units.
+int launch_embed(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* h,
+                 int B, int H, int ldh);
+int launch_rmsnorm_act(ih_ctx* c, const float* x, int ldx, const uint16_t* w, int rows, int D, float eps, ActBuf& a);
+int launch_glu_act(ih_ctx* c, const float* gu, int ldg, int rows, int I, int act, float limit, ActBuf& a);
+int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out);
+int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows);
+int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_t K, uint64_t seed, uint64_t tensor,
+               float sd);
+int synth_bf16(ih_ctx* c, uint16_t* out, size_t n, uint64_t seed, uint64_t tensor, float base, float amp);
+int synth_f32(ih_ctx* c, float* out, size_t n, uint64_t seed, uint64_t tensor, float base, float amp);
+int synth_kv(ih_ctx* c, int8_t* kc, int8_t* vc, __half* ks, __half* vs, int KVH, int HD, int cap, int ring, int pos0,
+             int npos, uint64_t seed, uint64_t tensor);
+
+int launch_prework(ih_ctx* c, const AttnArgs& a);
+int launch_attention(ih_ctx* c, const AttnArgs& a);
+int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out);
+
+// Tensor ids of the synthetic model (the generator's stream keys): globals, then 100 per layer.
+enum : uint64_t { T_EMBED = 1, T_FINAL_NORM = 2, T_HEAD = 3 };
+enum : uint64_t { L_ATTN_NORM = 0, L_QKV = 1, L_O = 2, L_MLP_NORM = 3, L_GATE_UP = 4, L_DOWN = 5, L_SINKS = 9 };
+constexpr uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
+constexpr uint64_t kv_tensor(int l) { return 500000 + uint64_t(l); }
+constexpr float W_SD = 0.02f;  // |N(0, 0.02)| scales
+
+}  // namespace ih
+
+using namespace ih;
+
+struct ih_layer {
+  uint16_t* attn_norm = nullptr;
+  uint16_t* mlp_norm = nullptr;
+  float* sinks = nullptr;
+  ih_qmat* qkv = nullptr;
+  ih_qmat* o = nullptr;
+  ih_qmat* gate_up = nullptr;
+  ih_qmat* down = nullptr;
+};
+
+struct ih_model {
+  ih_ctx* ctx = nullptr;
+  ih_model_desc d{};
+  uint64_t seed = 0;
+  std::vector<ih_layer> layers;
+  // Embedding table in MLX int4 layout (a row gather), final norm, head.
+  uint32_t* emb_w = nullptr;
+  uint16_t* emb_s = nullptr;
+  uint16_t* emb_b = nullptr;
+  uint16_t* final_norm = nullptr;
+  ih_qmat* head = nullptr;
+  // Scratch of one step.
+  float* h = nullptr;        // residual [MAX_TOK][H]
+  float* proj = nullptr;     // qkv output [MAX_TOK][QP]
+  float* gu = nullptr;       // gate|up output [MAX_TOK][2I]
+  float* logits = nullptr;   // [MAX_TOK][V]
+  uint32_t* tok = nullptr;   // [MAX_TOK]
+  uint32_t* top1 = nullptr;  // [MAX_TOK]
+  __half* q = nullptr;       // [KVH][Qpad][HD]
+  ActBuf act_h, act_o, act_i;
+  float* opart = nullptr;
+  float2* ml = nullptr;
+  size_t part_splits = 0;    // splits the attention partials can hold
+  int Qpad = 0, QP = 0;
+};
+
+struct ih_kv {
+  ih_model* model = nullptr;
+  int cap = 0, P = 0, written = 0, last_B = 0, chunk = 256;
+  std::vector<int8_t*> kc, vc;
+  std::vector<__half*> ks, vs;
+  std::vector<int> ring;   // per layer: ring slots (sliding-window layers) or 0
+};
+
+namespace ih {
+
+static int dalloc(void** p, size_t bytes) {
+  if (hipMalloc(p, bytes ? bytes : 1) != hipSuccess) return fail(IH_ENOMEM, "allocation of " + std::to_string(bytes) + " bytes failed");
+  return IH_OK;
+}
+
+template <typename T>
+static int dalloc_t(T** p, size_t count) {
+  void* v = nullptr;
+  IH_TRY(dalloc(&v, count * sizeof(T)));
+  *p = static_cast<T*>(v);
+  return IH_OK;
+}
+
+// Staging for the MLX-format tensors the generator writes before they are packed.
+struct Staging {
+  uint32_t* w = nullptr;
+  uint16_t* s = nullptr;
+  uint16_t* b = nullptr;
+  size_t cap_words = 0;
+  int reserve(size_t N, size_t K) {
+    const size_t words = N * K / 8;
+    if (words <= cap_words) return IH_OK;
+    release();
+    IH_TRY(dalloc_t(&w, words));
+    IH_TRY(dalloc_t(&s, N * K / 64));
+    IH_TRY(dalloc_t(&b, N * K / 64));
+    cap_words = words;
+    return IH_OK;
+  }
+  void release() {
+    if (w) (void)hipFree(w);
+    if (s) (void)hipFree(s);
+    if (b) (void)hipFree(b);
+    w = nullptr; s = nullptr; b = nullptr; cap_words = 0;
+  }
+  ~Staging() { release(); }
+};
+
+static int synth_qmat(ih_ctx* c, Staging& st, int N, int K, uint64_t seed, uint64_t tensor, float sd, ih_qmat** out) {
+  IH_TRY(st.reserve(N, K));
+  IH_TRY(synth_int4(c, st.w, st.s, st.b, size_t(N), size_t(K), seed, tensor, sd));
+  return ih_qmat_int4_create_dev(c, st.w, st.s, st.b, 1, N, K, out);
+}
+
+static int check_desc(const ih_model_desc& d) {
+  IH_CHECK(d.n_layers >= 1 && d.hidden >= 64 && d.hidden % 64 == 0, IH_EINVAL, "model: hidden must be a multiple of 64");
+  IH_CHECK(d.head_dim == 64 || d.head_dim == 128, IH_EINVAL, "model: head_dim must be 64 or 128");
+  IH_CHECK(d.n_kv_heads >= 1 && d.n_q_heads % d.n_kv_heads == 0, IH_EINVAL, "model: q heads must be a multiple of kv heads");
+  IH_CHECK(d.n_q_heads * d.head_dim % 64 == 0 && d.n_q_heads * d.head_dim / 8 <= 1024, IH_EINVAL,
+           "model: q_heads·head_dim must be a multiple of 64 and at most 8192");
+  IH_CHECK(d.vocab >= 1 && d.rms_eps > 0 && d.rope_theta > 0, IH_EINVAL, "model: vocab, eps and theta must be positive");
+  IH_CHECK(d.n_experts == 0, IH_EINVAL, "model: MoE layers are not available in this build yet");
+  IH_CHECK(d.intermediate >= 64 && d.intermediate % 64 == 0, IH_EINVAL, "model: intermediate must be a multiple of 64");
+  return IH_OK;
+}
+
+static void model_release(ih_model* m) {
+  if (!m) return;
+  for (auto& L : m->layers) {
+    ih_qmat_free(L.qkv); ih_qmat_free(L.o); ih_qmat_free(L.gate_up); ih_qmat_free(L.down);
+    if (L.attn_norm) (void)hipFree(L.attn_norm);
+    if (L.mlp_norm) (void)hipFree(L.mlp_norm);
+    if (L.sinks) (void)hipFree(L.sinks);
+  }
+  ih_qmat_free(m->head);
+  void* ptrs[] = {m->emb_w, m->emb_s, m->emb_b, m->final_norm, m->h, m->proj, m->gu, m->logits, m->tok, m->top1,
+                  m->q, m->opart, m->ml};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  free_act(m->act_h); free_act(m->act_o); free_act(m->act_i);
+  delete m;
+}
+
+static int ensure_partials(ih_model* m, int splits) {
+  if (size_t(splits) <= m->part_splits) return IH_OK;
+  if (m->opart) (void)hipFree(m->opart);
+  if (m->ml) (void)hipFree(m->ml);
+  m->opart = nullptr; m->ml = nullptr;
+  const auto& d = m->d;
+  IH_TRY(dalloc_t(&m->opart, size_t(d.n_kv_heads) * splits * m->Qpad * d.head_dim));
+  IH_TRY(dalloc_t(&m->ml, size_t(d.n_kv_heads) * splits * m->Qpad));
+  m->part_splits = splits;
+  return IH_OK;
+}
+
+// The sequence of one verify step on B rows whose tokens are in m->tok; top1 → m->top1.
+static int run_step(ih_model* m, ih_kv* kv, int B) {
+  ih_ctx* c = m->ctx;
+  const auto& d = m->d;
+  const int H = d.hidden, QH = d.n_q_heads, KVH = d.n_kv_heads, HD = d.head_dim, I = d.intermediate;
+  IH_TRY(launch_embed(c, m->tok, m->emb_w, m->emb_s, m->emb_b, m->h, B, H, H));
+  const int total = kv->P + B;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const ih_layer& L = m->layers[l];
+    // Attention.
+    IH_TRY(launch_rmsnorm_act(c, m->h, H, L.attn_norm, B, H, d.rms_eps, m->act_h));
+    IH_TRY(launch_qmm(c, L.qkv, 0, m->act_h, B, m->proj, m->QP, QO_F32));
+    AttnArgs a{};
+    a.proj = m->proj;
+    a.ldp = m->QP;
+    a.q = m->q;
+    a.kc = kv->kc[l];
+    a.vc = kv->vc[l];
+    a.ks = kv->ks[l];
+    a.vs = kv->vs[l];
+    a.sinks = L.sinks;
+    a.cap = kv->cap;
+    a.ring = kv->ring[l];
+    a.P = kv->P;
+    a.B = B;
+    a.QH = QH;
+    a.KVH = KVH;
+    a.HD = HD;
+    a.G = QH / KVH;
+    a.Qpad = m->Qpad;
+    a.C = kv->chunk;
+    a.window = a.ring ? d.sliding_window : 0;
+    a.s0 = a.window ? std::max(0, kv->P - a.window + 1) / a.C : 0;
+    a.nsplit = (total + a.C - 1) / a.C - a.s0;
+    a.hadk = d.hadamard_k;
+    a.theta = d.rope_theta;
+    a.scale_log2 = float(1.4426950408889634 / std::sqrt(double(HD)));
+    IH_TRY(ensure_partials(m, a.nsplit));
+    a.opart = m->opart;
+    a.ml = m->ml;
+    IH_TRY(launch_prework(c, a));
+    IH_TRY(launch_attention(c, a));
+    IH_TRY(launch_attn_reduce(c, a, m->act_o));
+    IH_TRY(launch_qmm(c, L.o, 0, m->act_o, B, m->h, H, QO_F32_ADD));
+    // FFN.
+    IH_TRY(launch_rmsnorm_act(c, m->h, H, L.mlp_norm, B, H, d.rms_eps, m->act_h));
+    IH_TRY(launch_qmm(c, L.gate_up, 0, m->act_h, B, m->gu, 2 * I, QO_F32));
+    IH_TRY(launch_glu_act(c, m->gu, 2 * I, B, I, d.act, d.swiglu_limit, m->act_i));
+    IH_TRY(launch_qmm(c, L.down, 0, m->act_i, B, m->h, H, QO_F32_ADD));
+  }
+  IH_TRY(launch_rmsnorm_act(c, m->h, H, m->final_norm, B, H, d.rms_eps, m->act_h));
+  IH_TRY(launch_qmm(c, m->head, 0, m->act_h, B, m->logits, d.vocab, QO_F32));
+  IH_TRY(launch_argmax(c, m->logits, d.vocab, B, d.vocab, m->top1));
+  kv->last_B = B;
+  kv->written = std::max(kv->written, kv->P + B);
+  return IH_OK;
+}
+
+static int check_step(ih_model* m, ih_kv* kv, int B) {
+  IH_CHECK(m && kv && kv->model == m, IH_EINVAL, "verify: model and cache do not belong together");
+  IH_CHECK(B >= 1 && B <= IH_MAX_ROWS, IH_EINVAL, "verify: B must be in 1..17");
+  IH_CHECK(kv->P + B <= kv->cap, IH_EINVAL,
+           "verify: context overflow (P + B = " + std::to_string(kv->P + B) + " > capacity " + std::to_string(kv->cap) + ")");
+  return IH_OK;
+}
+
+}  // namespace ih
+
+extern "C" {
+
+int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t seed, ih_model** out) {
+  IH_CHECK(c && desc && out, IH_EINVAL, "ih_model_create_synthetic: null argument");
+  *out = nullptr;
+  IH_TRY(check_desc(*desc));
+  ih_model* m = new ih_model();
+  m->ctx = c;
+  m->d = *desc;
+  m->seed = seed;
+  const auto& d = m->d;
+  const int H = d.hidden, QH = d.n_q_heads, KVH = d.n_kv_heads, HD = d.head_dim, I = d.intermediate, V = d.vocab;
+  m->QP = (QH + 2 * KVH) * HD;
+  m->Qpad = (QH / KVH * IH_MAX_ROWS + 15) / 16 * 16;
+  int st = IH_OK;
+  auto run = [&](int s) { if (st == IH_OK) st = s; };
+  {
+    Staging stg;
+    m->layers.resize(d.n_layers);
+    for (int l = 0; l < d.n_layers && st == IH_OK; ++l) {
+      ih_layer& L = m->layers[l];
+      run(dalloc_t(&L.attn_norm, H));
+      run(dalloc_t(&L.mlp_norm, H));
+      if (st != IH_OK) break;
+      run(synth_bf16(c, L.attn_norm, H, seed, layer_tensor(l, L_ATTN_NORM), 1.0f, 0.125f));
+      run(synth_bf16(c, L.mlp_norm, H, seed, layer_tensor(l, L_MLP_NORM), 1.0f, 0.125f));
+      if (d.sinks) {
+        run(dalloc_t(&L.sinks, QH));
+        if (st == IH_OK) run(synth_f32(c, L.sinks, QH, seed, layer_tensor(l, L_SINKS), 0.0f, 1.0f));
+      }
+      run(synth_qmat(c, stg, m->QP, H, seed, layer_tensor(l, L_QKV), W_SD, &L.qkv));
+      run(synth_qmat(c, stg, H, QH * HD, seed, layer_tensor(l, L_O), W_SD, &L.o));
+      run(synth_qmat(c, stg, 2 * I, H, seed, layer_tensor(l, L_GATE_UP), W_SD, &L.gate_up));
+      run(synth_qmat(c, stg, H, I, seed, layer_tensor(l, L_DOWN), W_SD, &L.down));
+    }
+    run(synth_qmat(c, stg, V, H, seed, T_HEAD, W_SD, &m->head));
+    if (st == IH_OK) run(hipStreamSynchronize(c->stream) == hipSuccess ? IH_OK : fail(IH_EDEVICE, "model: generation failed"));
+  }
+  run(dalloc_t(&m->emb_w, size_t(V) * H / 8));
+  run(dalloc_t(&m->emb_s, size_t(V) * H / 64));
+  run(dalloc_t(&m->emb_b, size_t(V) * H / 64));
+  run(dalloc_t(&m->final_norm, H));
+  if (st == IH_OK) run(synth_int4(c, m->emb_w, m->emb_s, m->emb_b, V, H, seed, T_EMBED, W_SD));
+  if (st == IH_OK) run(synth_bf16(c, m->final_norm, H, seed, T_FINAL_NORM, 1.0f, 0.125f));
+  run(dalloc_t(&m->h, size_t(MAX_TOK) * H));
+  run(dalloc_t(&m->proj, size_t(MAX_TOK) * m->QP));
+  run(dalloc_t(&m->gu, size_t(MAX_TOK) * 2 * I));
+  run(dalloc_t(&m->logits, size_t(MAX_TOK) * V));
+  run(dalloc_t(&m->tok, MAX_TOK));
+  run(dalloc_t(&m->top1, MAX_TOK));
+  run(dalloc_t(&m->q, size_t(KVH) * m->Qpad * HD));
+  if (st == IH_OK) run(ensure_act(c, m->act_h, H, false));
+  if (st == IH_OK) run(ensure_act(c, m->act_o, QH * HD, false));
+  if (st == IH_OK) run(ensure_act(c, m->act_i, I, false));
+  if (st == IH_OK) run(fill(c, m->q, 0, size_t(KVH) * m->Qpad * HD * 2));
+  if (st == IH_OK) run(hipStreamSynchronize(c->stream) == hipSuccess ? IH_OK : fail(IH_EDEVICE, "model: init failed"));
+  if (st != IH_OK) {
+    model_release(m);
+    return st;
+  }
+  *out = m;
+  return IH_OK;
+}
+
+int ih_model_free(ih_model* m) {
+  if (m) {
+    (void)hipStreamSynchronize(m->ctx->stream);
+    model_release(m);
+  }
+  return IH_OK;
+}
+
+size_t ih_model_weight_bytes(const ih_model* m) {
+  if (!m) return 0;
+  size_t b = ih_qmat_bytes(m->head);
+  for (const auto& L : m->layers)
+    b += ih_qmat_bytes(L.qkv) + ih_qmat_bytes(L.o) + ih_qmat_bytes(L.gate_up) + ih_qmat_bytes(L.down);
+  return b;
+}
+
+int ih_kv_create(ih_model* m, int capacity, ih_kv** out) {
+  IH_CHECK(m && out, IH_EINVAL, "ih_kv_create: null argument");
+  IH_CHECK(capacity >= 1, IH_EINVAL, "ih_kv_create: capacity must be positive");
+  *out = nullptr;
+  const auto& d = m->d;
+  ih_kv* kv = new ih_kv();
+  kv->model = m;
+  kv->cap = capacity;
+  // Key chunk: fixed per cache, about 32 splits at full capacity (256 … 2048).
+  int C = 256;
+  while (C < 2048 && (capacity + C - 1) / C > 32) C *= 2;
+  kv->chunk = C;
+  const int L = d.n_layers, KVH = d.n_kv_heads, HD = d.head_dim;
+  kv->kc.assign(L, nullptr); kv->vc.assign(L, nullptr); kv->ks.assign(L, nullptr); kv->vs.assign(L, nullptr);
+  kv->ring.assign(L, 0);
+  int st = IH_OK;
+  for (int l = 0; l < L && st == IH_OK; ++l) {
+    int slots = capacity;
+    if (d.sliding_window > 0 && l % 2 == 0) {
+      // Ring of a sliding-window layer: the window, a block of new rows and a rejected block, rounded up to the
+      // 32-key blocks of the attention (Attention.swift:272-280 uses W + 2·maxRows rounded to 128).
+      const int ring = (d.sliding_window + 2 * IH_MAX_ROWS + 127) / 128 * 128;
+      if (ring < capacity) { kv->ring[l] = ring; slots = ring; }
+    }
+    if (st == IH_OK) st = dalloc_t(&kv->kc[l], size_t(KVH) * slots * HD);
+    if (st == IH_OK) st = dalloc_t(&kv->vc[l], size_t(KVH) * slots * HD);
+    if (st == IH_OK) st = dalloc_t(&kv->ks[l], size_t(KVH) * slots);
+    if (st == IH_OK) st = dalloc_t(&kv->vs[l], size_t(KVH) * slots);
+    if (st == IH_OK) st = fill(m->ctx, kv->kc[l], 0, size_t(KVH) * slots * HD);
+    if (st == IH_OK) st = fill(m->ctx, kv->vc[l], 0, size_t(KVH) * slots * HD);
+    if (st == IH_OK) st = fill(m->ctx, kv->ks[l], 0, size_t(KVH) * slots * 2);
+    if (st == IH_OK) st = fill(m->ctx, kv->vs[l], 0, size_t(KVH) * slots * 2);
+  }
+  if (st == IH_OK) st = ensure_partials(m, (capacity + C - 1) / C + 1);
+  if (st != IH_OK) {
+    ih_kv_free(kv);
+    return st;
+  }
+  *out = kv;
+  return IH_OK;
+}
+
+int ih_kv_free(ih_kv* kv) {
+  if (!kv) return IH_OK;
+  (void)hipStreamSynchronize(kv->model->ctx->stream);
+  for (size_t l = 0; l < kv->kc.size(); ++l) {
+    if (kv->kc[l]) (void)hipFree(kv->kc[l]);
+    if (kv->vc[l]) (void)hipFree(kv->vc[l]);
+    if (kv->ks[l]) (void)hipFree(kv->ks[l]);
+    if (kv->vs[l]) (void)hipFree(kv->vs[l]);
+  }
+  delete kv;
+  return IH_OK;
+}
+
+int ih_kv_fill_synthetic(ih_kv* kv, int P, uint64_t seed) {
+  IH_CHECK(kv, IH_EINVAL, "ih_kv_fill_synthetic: null cache");
+  IH_CHECK(P >= 0 && P <= kv->cap, IH_EINVAL, "ih_kv_fill_synthetic: P beyond the capacity");
+  ih_model* m = kv->model;
+  const auto& d = m->d;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const int ring = kv->ring[l];
+    // With a ring only the last `ring` positions survive; generate just those.
+    const int first = ring ? std::max(0, P - ring) : 0;
+    IH_TRY(synth_kv(m->ctx, kv->kc[l], kv->vc[l], kv->ks[l], kv->vs[l], d.n_kv_heads, d.head_dim, ring ? ring : kv->cap,
+                    ring, first, P - first, seed, kv_tensor(l)));
+  }
+  IH_HIP(hipStreamSynchronize(m->ctx->stream));
+  kv->P = P;
+  kv->written = P;
+  kv->last_B = 0;
+  return IH_OK;
+}
+
+int ih_kv_pos(const ih_kv* kv) { return kv ? kv->P : -1; }
+
+int ih_kv_chunk(const ih_kv* kv) { return kv ? kv->chunk : 0; }
+
+int ih_kv_set_pos(ih_kv* kv, int pos) {
+  IH_CHECK(kv, IH_EINVAL, "ih_kv_set_pos: null cache");
+  IH_CHECK(pos >= 0 && pos <= kv->written, IH_ESTATE,
+           "ih_kv_set_pos: position " + std::to_string(pos) + " was never written (" + std::to_string(kv->written) + ")");
+  kv->P = pos;
+  kv->last_B = 0;
+  return IH_OK;
+}
+
+int ih_kv_commit(ih_kv* kv, int n) {
+  IH_CHECK(kv, IH_EINVAL, "ih_kv_commit: null cache");
+  IH_CHECK(n >= 0 && n <= kv->last_B, IH_ESTATE,
+           "ih_kv_commit: " + std::to_string(n) + " rows but the last verify step had " + std::to_string(kv->last_B));
+  kv->P += n;
+  kv->last_B = 0;
+  return IH_OK;
+}
+
+int ih_verify_step_dev(ih_model* m, ih_kv* kv, const uint32_t* tokens_dev, int B, uint32_t* top1_dev) {
+  IH_TRY(check_step(m, kv, B));
+  IH_CHECK(tokens_dev && top1_dev, IH_EINVAL, "ih_verify_step_dev: null buffer");
+  IH_HIP(hipMemcpyAsync(m->tok, tokens_dev, B * 4, hipMemcpyDeviceToDevice, m->ctx->stream));
+  IH_TRY(run_step(m, kv, B));
+  IH_HIP(hipMemcpyAsync(top1_dev, m->top1, B * 4, hipMemcpyDeviceToDevice, m->ctx->stream));
+  return IH_OK;
+}
+
+int ih_verify_step(ih_model* m, ih_kv* kv, const uint32_t* tokens, int B, float* logits_out, uint32_t* top1_out) {
+  IH_TRY(check_step(m, kv, B));
+  IH_CHECK(tokens && top1_out, IH_EINVAL, "ih_verify_step: null buffer");
+  for (int i = 0; i < B; ++i)
+    IH_CHECK(tokens[i] < uint32_t(m->d.vocab), IH_EINVAL, "ih_verify_step: token id beyond the vocabulary");
+  hipStream_t s = m->ctx->stream;
+  IH_HIP(hipMemcpyAsync(m->tok, tokens, B * 4, hipMemcpyHostToDevice, s));
+  IH_TRY(run_step(m, kv, B));
+  IH_HIP(hipMemcpyAsync(top1_out, m->top1, B * 4, hipMemcpyDeviceToHost, s));
+  if (logits_out)
+    IH_HIP(hipMemcpyAsync(logits_out, m->logits, size_t(B) * m->d.vocab * 4, hipMemcpyDeviceToHost, s));
+  IH_HIP(hipStreamSynchronize(s));
+  return IH_OK;
+}
+
+int ih_verify_and_accept(ih_model* m, ih_kv* kv, const uint32_t* tokens, int B, ih_accept_result* out) {
+  IH_CHECK(out, IH_EINVAL, "ih_verify_and_accept: null result");
+  uint32_t top1[IH_MAX_ROWS];
+  IH_TRY(ih_verify_step(m, kv, tokens, B, nullptr, top1));
+  IH_TRY(ih_accept(tokens, top1, B, out));
+  return ih_kv_commit(kv, out->m + 1);
+}
+
+const float* ih_model_logits_dev(const ih_model* m) { return m ? m->logits : nullptr; }
+
+}  // extern "C"

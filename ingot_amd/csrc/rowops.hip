@@ -1,0 +1,206 @@
+// Row kernels of the verify round: embedding gather, RMSNorm into the qmm activation layout, the gated activation,
+// vocab-wide argmax and greedy acceptance.
+#include "act.h"
+#include "ih_internal.h"
+
+namespace ih {
+
+// ---------------------------------------------------------------------------------------------------------------
+// Embedding: h[r] = dequant(table[tok[r]]) in fp32 (MLX int4 g64 row). embed_rows, Shaders/yy_model.metal:12-49.
+__global__ void embed_kernel(const uint32_t* __restrict__ tok, const uint32_t* __restrict__ w,
+                             const uint16_t* __restrict__ s, const uint16_t* __restrict__ b, float* __restrict__ h,
+                             int H, int ldh) {
+  const uint32_t t = tok[blockIdx.x];
+  const uint32_t* wr = w + size_t(t) * (H / 8);
+  for (int i = threadIdx.x; i < H / 8; i += blockDim.x) {
+    const uint32_t word = wr[i];
+    const size_t g = size_t(t) * (H / 64) + (i * 8) / 64;
+    const float sc = dbf16(s[g]), bi = dbf16(b[g]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[size_t(blockIdx.x) * ldh + 8 * i + j] = sc * float((word >> (4 * j)) & 15u) + bi;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Block-wide sum in a fixed order (wave partials in LDS, added in wave order).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+// RMSNorm of fp32 rows into the activation layout: x·rsqrt(mean x² + eps)·w, rounded to bf16.
+// rmsnorm_rows, Shaders/verify.metal:501-523 (which writes half; this build's activations are bf16).
+// Grid (rows), 256 threads; one thread per 8-value chunk.
+__global__ __launch_bounds__(256) void rmsnorm_act_kernel(const float* __restrict__ x, int ldx,
+                                                          const uint16_t* __restrict__ w, int D, float eps,
+                                                          uint4* __restrict__ frag, float* __restrict__ xsum, int nkb) {
+  __shared__ float red[8];
+  const int row = blockIdx.x;
+  const float* xr = x + size_t(row) * ldx;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) ss += xr[i] * xr[i];
+  const float tot = block_sum(ss, red);
+  const float r = 1.0f / sqrtf(tot / float(D) + eps);
+  const int nchunk = nkb * 16;
+  for (int c0 = 0; c0 < nchunk; c0 += blockDim.x) {
+    const int c = c0 + threadIdx.x;
+    float v[8];
+    const bool valid = c < D / 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = valid ? xr[8 * c + e] * r * dbf16(w[8 * c + e]) : 0.f;
+    act_store_chunk(frag, xsum, nkb, row, c, v, valid, MAX_TOK);
+  }
+}
+
+// Gated activation of gate|up (fp32 [rows, 2I]: gate in columns 0…I−1, up in I…2I−1) into the activation layout.
+// act 0: SiLU(g)·u = g / (1 + e^−g) · u; act 1: swiglu_oai, (clip(u, ±limit) + 1) · g·σ(1.702·g) with g = min(gate,
+// limit). lab_glu, Shaders/qmm.metal:18-30; dswiglu, Shaders/yy_model.metal:187-199.
+__device__ __forceinline__ float glu(float g, float u, int act, float limit) {
+  if (act == 0) return g / (1.0f + expf(-g)) * u;
+  const float gc = fminf(g, limit), uc = fminf(fmaxf(u, -limit), limit);
+  return gc / (1.0f + expf(-1.702f * gc)) * (uc + 1.0f);
+}
+
+__global__ __launch_bounds__(256) void glu_act_kernel(const float* __restrict__ gu, int ldg, int I, int act,
+                                                      float limit, uint4* __restrict__ frag, float* __restrict__ xsum,
+                                                      int nkb) {
+  const int row = blockIdx.x;
+  const float* gr = gu + size_t(row) * ldg;
+  const int nchunk = nkb * 16;
+  for (int c0 = 0; c0 < nchunk; c0 += blockDim.x) {
+    const int c = c0 + threadIdx.x;
+    float v[8];
+    const bool valid = c < I / 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = valid ? glu(gr[8 * c + e], gr[I + 8 * c + e], act, limit) : 0.f;
+    act_store_chunk(frag, xsum, nkb, row, c, v, valid, MAX_TOK);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// argmax per row, ties to the lowest index, NaN never wins: argmax_rows, Shaders/verify.metal:525-547.
+// Grid (rows), 1024 threads.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int ldx, int N,
+                                                      uint32_t* __restrict__ out) {
+  __shared__ float bv[16];
+  __shared__ uint32_t bi[16];
+  const float* xr = x + size_t(blockIdx.x) * ldx;
+  float m = -INFINITY;
+  uint32_t mi = 0xFFFFFFFFu;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    const float v = xr[i];
+    if (v > m) { m = v; mi = uint32_t(i); }
+  }
+  // Wave reduction: larger value, or equal value and lower index.
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float om = __shfl_xor(m, o);
+    const uint32_t oi = __shfl_xor(mi, o);
+    if (om > m || (om == m && oi < mi)) { m = om; mi = oi; }
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { bv[wave] = m; bi[wave] = mi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = bv[0];
+    uint32_t ix = bi[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i)
+      if (bv[i] > b || (bv[i] == b && bi[i] < ix)) { b = bv[i]; ix = bi[i]; }
+    out[blockIdx.x] = ix == 0xFFFFFFFFu ? 0u : ix;   // all NaN / −inf: index 0, as the reference
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Greedy acceptance on the device, one thread: m = drafts vtok[1..m] that equal top1[0..m−1]; rec[round % ring] = (m,
+// emitted tokens, REC_P = P before, REC_ROWS = rows); st = [P, nacc, pend, pendPos, anchor, round, rows] advanced:
+// P += m + 1 (the commit), anchor = top1[m], vtok[0] = anchor. spec_accept, Shaders/yy_model.metal:616-642.
+__global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const uint32_t nr = rows ? uint32_t(rows) : st[6];
+  uint32_t m = 0;
+  while (m + 1 < nr && vtok[m + 1] == top1[m]) ++m;
+  uint32_t* r = rec + (st[5] % uint32_t(ring)) * IH_REC_STRIDE;
+  r[0] = m;
+  r[IH_REC_ROWS] = nr;
+  for (uint32_t i = 1; i <= m; ++i) r[i] = vtok[i];
+  r[m + 1] = top1[m];
+  r[IH_REC_P] = st[0];
+  st[3] = st[0];
+  st[2] = m + 1;
+  st[0] += m + 1;
+  st[1] = m + 1;
+  st[4] = top1[m];
+  st[5] += 1;
+  vtok[0] = top1[m];
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+int launch_embed(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* h,
+                 int B, int H, int ldh) {
+  embed_kernel<<<B, 256, 0, c->stream>>>(tok, w, s, b, h, H, ldh);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int launch_rmsnorm_act(ih_ctx* c, const float* x, int ldx, const uint16_t* w, int rows, int D, float eps, ActBuf& a) {
+  rmsnorm_act_kernel<<<rows, 256, 0, c->stream>>>(x, ldx, w, D, eps, static_cast<uint4*>(a.frag), a.xsum, a.nkb);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int launch_glu_act(ih_ctx* c, const float* gu, int ldg, int rows, int I, int act, float limit, ActBuf& a) {
+  glu_act_kernel<<<rows, 256, 0, c->stream>>>(gu, ldg, I, act, limit, static_cast<uint4*>(a.frag), a.xsum, a.nkb);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out) {
+  argmax_kernel<<<rows, 1024, 0, c->stream>>>(x, ldx, N, out);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows) {
+  accept_kernel<<<1, 64, 0, c->stream>>>(st, vtok, top1, rec, ring, rows);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+}  // namespace ih
+
+using namespace ih;
+
+extern "C" {
+
+int ih_argmax_rows(ih_ctx* c, const float* x_dev, int rows, int N, uint32_t* out_dev) {
+  IH_CHECK(c && x_dev && out_dev, IH_EINVAL, "ih_argmax_rows: null argument");
+  IH_CHECK(rows >= 1 && N >= 1, IH_EINVAL, "ih_argmax_rows: empty input");
+  return launch_argmax(c, x_dev, N, rows, N, out_dev);
+}
+
+int ih_accept(const uint32_t* vtok, const uint32_t* top1, int B, ih_accept_result* out) {
+  IH_CHECK(vtok && top1 && out, IH_EINVAL, "ih_accept: null argument");
+  IH_CHECK(B >= 1 && B <= IH_MAX_ROWS, IH_EINVAL, "ih_accept: B must be in 1..17");
+  int m = 0;
+  while (m + 1 < B && vtok[m + 1] == top1[m]) ++m;
+  out->m = m;
+  out->n_emitted = m + 1;
+  for (int i = 1; i <= m; ++i) out->tokens[i - 1] = vtok[i];
+  out->tokens[m] = top1[m];
+  for (int i = m + 1; i < IH_MAX_ROWS; ++i) out->tokens[i] = 0;
+  return IH_OK;
+}
+
+int ih_spec_accept_dev(ih_ctx* c, uint32_t* st_dev, uint32_t* vtok_dev, const uint32_t* top1_dev, uint32_t* rec_dev,
+                       int ring, int rows) {
+  IH_CHECK(c && st_dev && vtok_dev && top1_dev && rec_dev, IH_EINVAL, "ih_spec_accept_dev: null argument");
+  IH_CHECK(ring >= 1 && rows >= 0 && rows <= IH_MAX_ROWS, IH_EINVAL, "ih_spec_accept_dev: bad ring or rows");
+  return launch_accept(c, st_dev, vtok_dev, top1_dev, rec_dev, ring, rows);
+}
+
+}  // extern "C"

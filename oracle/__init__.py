@@ -59,6 +59,21 @@ _SIGS = [
     ("or_argmax_rows", None, [vp, i32, i32, vp]),
     ("or_accept", i32, [vp, vp, i32, vp]),
     ("or_num_threads", i32, []),
+    ("or_sm_at", C.c_uint64, [C.c_uint64, C.c_uint64]),
+    ("or_sm_key", C.c_uint64, [C.c_uint64, C.c_uint64]),
+    ("or_sm_normal", C.c_float, [C.c_uint64, C.c_uint64]),
+    ("or_synth_int4", None, [C.c_uint64, C.c_uint64, i32, i32, C.c_float, vp, vp, vp]),
+    ("or_synth_bf16", None, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_float, C.c_float, vp]),
+    ("or_synth_f32", None, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_float, C.c_float, vp]),
+    ("or_f32_to_f16", C.c_uint16, [C.c_float]),
+    ("or_f16_to_f32", C.c_float, [C.c_uint16]),
+    ("or_synth_kv", None, [C.c_uint64, C.c_uint64, i32, i32, i32, i32, vp, vp, vp, vp]),
+    ("or_rmsnorm", None, [vp, i32, i32, vp, C.c_float, vp]),
+    ("or_glu", C.c_float, [C.c_float, C.c_float, i32, C.c_float]),
+    ("or_fwht", None, [vp, i32]),
+    ("or_rope_wht", None, [vp, i32, i32, C.c_float, i32]),
+    ("or_attention", None, [vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp]),
+    ("or_verify_dense", i32, [vp, C.c_uint64, C.c_uint64, i32, vp, i32, vp, vp]),
 ]
 
 
@@ -158,3 +173,72 @@ def accept(vtok: np.ndarray, top1: np.ndarray) -> tuple[int, np.ndarray]:
 
 def num_threads() -> int:
     return int(lib().or_num_threads())
+
+
+# ---- synthetic data and the whole verify step ---------------------------------------------------------------------
+
+def synth_int4(seed: int, tensor: int, N: int, K: int, sd: float = 0.02):
+    w = np.empty((N, K // 8), np.uint32)
+    s = np.empty((N, K // 64), np.uint16)
+    b = np.empty((N, K // 64), np.uint16)
+    lib().or_synth_int4(seed, tensor, N, K, sd, _p(w), _p(s), _p(b))
+    return w, s, b
+
+
+def synth_kv(seed: int, tensor: int, KVH: int, HD: int, pos0: int, npos: int):
+    k = np.empty((KVH, npos, HD), np.int8)
+    v = np.empty((KVH, npos, HD), np.int8)
+    ks = np.empty((KVH, npos), np.uint16)
+    vs = np.empty((KVH, npos), np.uint16)
+    lib().or_synth_kv(seed, tensor, KVH, HD, pos0, npos, _p(k), _p(v), _p(ks), _p(vs))
+    return k, v, ks, vs
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    return np.asarray(h, np.uint16).view(np.float16).astype(np.float32)
+
+
+def rmsnorm(x: np.ndarray, w_bf16: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    out = np.empty_like(x)
+    lib().or_rmsnorm(_p(x), x.shape[0], x.shape[1], _p(w), eps, _p(out))
+    return out
+
+
+def fwht(v: np.ndarray) -> np.ndarray:
+    v = np.array(v, np.float32)
+    lib().or_fwht(_p(v), len(v))
+    return v
+
+
+def rope_wht(x: np.ndarray, pos: int, theta: float, hadk: int) -> np.ndarray:
+    x = np.array(x, np.float32)
+    lib().or_rope_wht(_p(x), len(x), pos, theta, hadk)
+    return x
+
+
+def attention(q, P, QH, KVH, k, v, ks, vs, window=0, sinks=None):
+    """q fp32 [B][QH][HD]; k/v int8 [KVH][npos][HD]; ks/vs fp16 bits [KVH][npos] → [B][QH·HD]."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.int8)
+    v = np.ascontiguousarray(v, np.int8)
+    ks = np.ascontiguousarray(ks, np.uint16)
+    vs = np.ascontiguousarray(vs, np.uint16)
+    B, _, HD = q.shape
+    out = np.empty((B, QH * HD), np.float32)
+    sk = None if sinks is None else np.ascontiguousarray(sinks, np.float32)
+    lib().or_attention(_p(q), B, P, QH, KVH, HD, _p(k), _p(v), _p(ks), _p(vs), k.shape[1], window,
+                       _p(sk) if sk is not None else None, _p(out))
+    return out
+
+
+def verify_dense(desc, seed: int, kv_seed: int, P: int, tokens):
+    """(logits [B][V], top1 [B]) of the synthetic dense model; desc: ingot_amd._lib.ModelDesc (same layout)."""
+    t = np.ascontiguousarray(tokens, np.uint32)
+    B = len(t)
+    logits = np.empty((B, desc.vocab), np.float32)
+    top1 = np.empty(B, np.uint32)
+    rc = lib().or_verify_dense(C.addressof(desc), seed, kv_seed, P, _p(t), B, _p(logits), _p(top1))
+    assert rc == 0
+    return logits, top1

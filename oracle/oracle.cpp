@@ -163,6 +163,317 @@ int or_accept(const uint32_t* vtok, const uint32_t* top1, int B, uint32_t* emitt
   return m;
 }
 
+
+// ---------------------------------------------------------------------------------------------------------------
+// Synthetic data (the benchmark's generator, restated): counter-based SplitMix64 streams. h(key, i) is output i of
+// SplitMix64 seeded with key (the reference's SplitMix64, Sources/Ingot/Sampling.swift:50-62); key = mix(seed·φ +
+// mix(tensor + c)). sm_normal sums the four 16-bit fields of one output, centred, times √3/65536 (≈ N(0,1)).
+static inline uint64_t sm_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+static inline uint64_t sm_key(uint64_t seed, uint64_t tensor) {
+  return sm_mix(seed * 0x9E3779B97F4A7C15ull + sm_mix(tensor + 0x632BE59BD9B4E019ull));
+}
+static inline uint64_t sm_at(uint64_t key, uint64_t i) { return sm_mix(key + (i + 1) * 0x9E3779B97F4A7C15ull); }
+static inline float sm_normal(uint64_t key, uint64_t i) {
+  const uint64_t h = sm_at(key, i);
+  const int s = int(h & 0xFFFF) + int((h >> 16) & 0xFFFF) + int((h >> 32) & 0xFFFF) + int(h >> 48) - 131070;
+  return float(s) * 2.642936E-05f;
+}
+
+uint64_t or_sm_at(uint64_t key, uint64_t i) { return sm_at(key, i); }
+uint64_t or_sm_key(uint64_t seed, uint64_t tensor) { return sm_key(seed, tensor); }
+float or_sm_normal(uint64_t key, uint64_t i) { return sm_normal(key, i); }
+
+// MLX int4 tensor [N, K] of the synthetic model: codes from stream 2·tensor, scales from 2·tensor + 1.
+void or_synth_int4(uint64_t seed, uint64_t tensor, int N, int K, float sd, uint32_t* w, uint16_t* s, uint16_t* b) {
+  const uint64_t kw = sm_key(seed, 2 * tensor), ks = sm_key(seed, 2 * tensor + 1);
+  const size_t nw = size_t(N) * K / 8, ng = size_t(N) * K / 64;
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < nw; ++i) {
+    const uint64_t h = sm_at(kw, i >> 1);
+    w[i] = uint32_t((i & 1) ? (h >> 32) : h);
+  }
+#pragma omp parallel for schedule(static)
+  for (size_t g = 0; g < ng; ++g) {
+    const uint16_t sb = or_f32_to_bf16(std::fabs(sm_normal(ks, g)) * sd);
+    s[g] = sb;
+    b[g] = or_f32_to_bf16(-8.0f * or_bf16_to_f32(sb));
+  }
+}
+
+void or_synth_bf16(uint64_t seed, uint64_t tensor, size_t n, float base, float amp, uint16_t* out) {
+  const uint64_t k = sm_key(seed, 2 * tensor);
+  for (size_t i = 0; i < n; ++i) out[i] = or_f32_to_bf16(base + amp * sm_normal(k, i));
+}
+
+void or_synth_f32(uint64_t seed, uint64_t tensor, size_t n, float base, float amp, float* out) {
+  const uint64_t k = sm_key(seed, 2 * tensor);
+  for (size_t i = 0; i < n; ++i) out[i] = base + amp * sm_normal(k, i);
+}
+
+// fp32 → fp16 bits, round to nearest even (normal, subnormal, overflow to inf).
+uint16_t or_f32_to_f16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const int e = int((u >> 23) & 0xFF) - 127;
+  uint32_t m = u & 0x7FFFFFu;
+  if (((u >> 23) & 0xFF) == 0xFF) return uint16_t(sign | 0x7C00u | (m ? 0x200u : 0u));
+  if (e > 15) return uint16_t(sign | 0x7C00u);
+  if (e >= -14) {
+    uint32_t r = (uint32_t(e + 15) << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    return uint16_t(sign | r);
+  }
+  if (e < -25) return uint16_t(sign);
+  m |= 0x800000u;
+  const int shift = -e - 1;  // e ≤ −15: value = m · 2^(e−23) → units of 2^−24
+  uint32_t r = m >> (shift);
+  const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (r & 1u))) ++r;
+  return uint16_t(sign | r);
+}
+float or_f16_to_f32(uint16_t h) {
+  const uint32_t sign = uint32_t(h & 0x8000u) << 16, e = (h >> 10) & 0x1F, m = h & 0x3FF;
+  float f;
+  if (e == 0) f = std::ldexp(float(m), -24);
+  else if (e == 31) f = m ? std::numeric_limits<float>::quiet_NaN() : std::numeric_limits<float>::infinity();
+  else f = std::ldexp(float(m | 0x400u), int(e) - 25);
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  u |= sign;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// Symmetric int8 of one head vector with an fp16 scale: sc = fp16(amax/127) (1 when amax = 0), q = clamp(rint(x/sc),
+// ±127). CPU.quantI8 (Tests/IngotTests/KernelHarness.swift:249-254) and vattn_prework_i8 (verify_attn_nax.metal:112-139),
+// with the scale stored in fp16 instead of fp32.
+static void quant_i8(const float* x, int n, int8_t* q, uint16_t* sc16) {
+  float amax = 0.f;
+  for (int i = 0; i < n; ++i) amax = std::max(amax, std::fabs(x[i]));
+  const uint16_t h = or_f32_to_f16(amax > 0.f ? amax / 127.0f : 1.0f);
+  const float sc = or_f16_to_f32(h);
+  for (int i = 0; i < n; ++i) q[i] = int8_t(std::min(127.f, std::max(-127.f, std::nearbyint(x[i] / sc))));
+  *sc16 = h;
+}
+
+// Synthetic KV of one layer for positions pos0 … pos0+npos−1: k/v int8 [KVH][npos][HD], scales fp16 bits [KVH][npos].
+void or_synth_kv(uint64_t seed, uint64_t tensor, int KVH, int HD, int pos0, int npos, int8_t* k, int8_t* v,
+                 uint16_t* ks, uint16_t* vs) {
+  const uint64_t kk = sm_key(seed, 2 * tensor), kv = sm_key(seed, 2 * tensor + 1);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int h = 0; h < KVH; ++h)
+    for (int p = 0; p < npos; ++p) {
+      float x[256];
+      const int pos = pos0 + p;
+      const size_t o = (size_t(h) * npos + p);
+      for (int which = 0; which < 2; ++which) {
+        const uint64_t key = which ? kv : kk;
+        for (int d = 0; d < HD; ++d) x[d] = sm_normal(key, ((uint64_t(h) << 24) + uint64_t(pos)) * HD + d);
+        quant_i8(x, HD, (which ? v : k) + o * HD, (which ? vs : ks) + o);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Row operations of the round.
+
+// RMSNorm: bf16(x · 1/sqrt(mean x² + eps) · w). rmsnorm_rows, Sources/Ingot/Shaders/verify.metal:501-523.
+void or_rmsnorm(const float* x, int rows, int D, const uint16_t* w, float eps, float* out) {
+  for (int r = 0; r < rows; ++r) {
+    double ss = 0;
+    for (int i = 0; i < D; ++i) ss += double(x[size_t(r) * D + i]) * x[size_t(r) * D + i];
+    const float rr = 1.0f / std::sqrt(float(ss) / float(D) + eps);
+    for (int i = 0; i < D; ++i)
+      out[size_t(r) * D + i] = or_bf16_to_f32(or_f32_to_bf16(x[size_t(r) * D + i] * rr * or_bf16_to_f32(w[i])));
+  }
+}
+
+// Gated activation (lab_glu, Sources/Ingot/Shaders/qmm.metal:18-30): act 0 = SiLU(g)·u, act 1 = swiglu_oai
+// (CPU.swigluOAI, Tests/IngotTests/KernelHarness.swift:185-188). Output rounded to bf16.
+float or_glu(float g, float u, int act, float limit) {
+  if (act == 0) return g / (1.0f + std::exp(-g)) * u;
+  const float gc = std::min(g, limit), uc = std::min(std::max(u, -limit), limit);
+  return gc / (1.0f + std::exp(-1.702f * gc)) * (uc + 1.0f);
+}
+
+// Unnormalised Sylvester Walsh–Hadamard in place, stages h = 1, 2, 4, … (CPU.fwht, KernelHarness.swift:197-210).
+void or_fwht(float* v, int n) {
+  for (int h = 1; h < n; h *= 2)
+    for (int i = 0; i < n; i += 2 * h)
+      for (int j = i; j < i + h; ++j) {
+        const float a = v[j], b = v[j + h];
+        v[j] = a + b;
+        v[j + h] = a - b;
+      }
+}
+
+// RoPE of one head (non-interleaved halves over all HD dims; angle pos·θ^(−i/(HD/2)) in double), then the orthonormal
+// WHT if hadk. normRope + hadamard, Tests/IngotTests/KernelHarness.swift:379-420; vattn_prework_i8.
+void or_rope_wht(float* x, int HD, int pos, float theta, int hadk) {
+  float y[256];
+  const int RH = HD / 2;
+  for (int d = 0; d < HD; ++d) {
+    const int i = d % RH;
+    const double ang = double(pos) * std::pow(double(theta), -double(i) / double(RH));
+    const float c = float(std::cos(ang)), s = float(std::sin(ang));
+    y[d] = d < RH ? x[d] * c - x[d + RH] * s : x[d] * c + x[d - RH] * s;
+  }
+  if (hadk) {
+    or_fwht(y, HD);
+    const float sc = HD == 128 ? 0.088388347648318441f : (HD == 64 ? 0.125f : 0.0625f);
+    for (int d = 0; d < HD; ++d) y[d] *= sc;
+  }
+  std::memcpy(x, y, sizeof(float) * HD);
+}
+
+// Causal GQA attention of B rows at positions P…P+B−1 over an int8 cache of P+B keys (the block's own keys already
+// written): S = (q·k8)·ks/√HD, masked to key ≤ P + t (and key > P + t − window), softmax with an optional sink logit
+// in the denominator, O = Σ p·vs·v8. AttnFixture.reference (Tests/IngotTests/KernelHarness.swift:420-501).
+// q fp32 [B][QH][HD] (already rounded as the kernel stores it), k/v [KVH][npos][HD], scales fp16 bits; out [B][QH·HD].
+void or_attention(const float* q, int B, int P, int QH, int KVH, int HD, const int8_t* k, const int8_t* v,
+                  const uint16_t* ks, const uint16_t* vs, int npos, int window, const float* sinks, float* out) {
+  const int G = QH / KVH;
+  const float scale = float(1.0 / std::sqrt(double(HD)));
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int t = 0; t < B; ++t)
+    for (int h = 0; h < QH; ++h) {
+      const int kvh = h / G, n = P + t + 1;
+      const int lo = window > 0 ? std::max(0, n - window) : 0;
+      std::vector<float> s(n);
+      const float* qr = q + (size_t(t) * QH + h) * HD;
+      float mx = -std::numeric_limits<float>::infinity();
+      for (int j = lo; j < n; ++j) {
+        const int8_t* kr = k + (size_t(kvh) * npos + j) * HD;
+        float dot = 0.f;
+        for (int d = 0; d < HD; ++d) dot += qr[d] * float(kr[d]);
+        s[j] = dot * or_f16_to_f32(ks[size_t(kvh) * npos + j]) * scale;
+        mx = std::max(mx, s[j]);
+      }
+      if (sinks) mx = std::max(mx, sinks[h]);
+      float l = sinks ? std::exp(sinks[h] - mx) : 0.f;
+      std::vector<float> o(HD, 0.f);
+      for (int j = lo; j < n; ++j) {
+        const float p = std::exp(s[j] - mx);
+        l += p;
+        const float pv = p * or_f16_to_f32(vs[size_t(kvh) * npos + j]);
+        const int8_t* vr = v + (size_t(kvh) * npos + j) * HD;
+        for (int d = 0; d < HD; ++d) o[d] += pv * float(vr[d]);
+      }
+      for (int d = 0; d < HD; ++d) out[size_t(t) * QH * HD + h * HD + d] = o[d] / l;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// The whole verify step of the synthetic dense model (HybridModel.encodeVerify, Sources/Ingot/ModelRound.swift:48-82),
+// with the weights and the KV history regenerated from the seeds. Layout of or_model_desc = ih_model_desc.
+struct or_model_desc {
+  int n_layers, hidden, n_q_heads, n_kv_heads, head_dim, intermediate, vocab;
+  float rope_theta, rms_eps;
+  int n_experts, top_k, expert_intermediate, expert_format, router_bias, expert_bias, act;
+  float swiglu_limit;
+  int sliding_window, sinks, hadamard_k;
+};
+
+static uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
+
+// Y[B, N] = X[B, K] (fp32 values) · Wᵀ of the synthetic int4 tensor `tensor`.
+static void synth_qmm(uint64_t seed, uint64_t tensor, int N, int K, float sd, const float* x, int B, float* y) {
+  std::vector<uint32_t> w(size_t(N) * K / 8);
+  std::vector<uint16_t> s(size_t(N) * K / 64), b(size_t(N) * K / 64);
+  or_synth_int4(seed, tensor, N, K, sd, w.data(), s.data(), b.data());
+  or_qmm_int4(x, B, w.data(), s.data(), b.data(), N, K, y);
+}
+
+// Returns 0 on success. logits [B][vocab], top1 [B]. The cache positions 0…P−1 hold the synthetic KV of kv_seed.
+int or_verify_dense(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, int P, const uint32_t* tokens, int B,
+                    float* logits, uint32_t* top1) {
+  const int H = d->hidden, QH = d->n_q_heads, KVH = d->n_kv_heads, HD = d->head_dim, I = d->intermediate, V = d->vocab;
+  const int QP = (QH + 2 * KVH) * HD, npos = P + B;
+  const float sd = 0.02f;
+  // Embedding rows.
+  std::vector<float> h(size_t(B) * H);
+  {
+    std::vector<uint32_t> w(size_t(V) * H / 8);
+    std::vector<uint16_t> s(size_t(V) * H / 64), b(size_t(V) * H / 64);
+    or_synth_int4(seed, 1, V, H, sd, w.data(), s.data(), b.data());
+    for (int r = 0; r < B; ++r) {
+      std::vector<float> row(H);
+      or_dequant_int4(w.data() + size_t(tokens[r]) * H / 8, s.data() + size_t(tokens[r]) * H / 64,
+                      b.data() + size_t(tokens[r]) * H / 64, 1, H, row.data());
+      std::memcpy(h.data() + size_t(r) * H, row.data(), sizeof(float) * H);
+    }
+  }
+  std::vector<float> x(size_t(B) * H), proj(size_t(B) * QP), q(size_t(B) * QH * HD), att(size_t(B) * QH * HD);
+  std::vector<float> y(size_t(B) * H), gu(size_t(B) * 2 * I), a(size_t(B) * I);
+  std::vector<uint16_t> wn(H);
+  std::vector<int8_t> k(size_t(KVH) * npos * HD), v(size_t(KVH) * npos * HD);
+  std::vector<uint16_t> ks(size_t(KVH) * npos), vs(size_t(KVH) * npos);
+  std::vector<float> sinks(QH);
+  for (int l = 0; l < d->n_layers; ++l) {
+    or_synth_bf16(seed, layer_tensor(l, 0), H, 1.0f, 0.125f, wn.data());
+    or_rmsnorm(h.data(), B, H, wn.data(), d->rms_eps, x.data());
+    synth_qmm(seed, layer_tensor(l, 1), QP, H, sd, x.data(), B, proj.data());
+    // KV history, then this block's keys and values.
+    {
+      std::vector<int8_t> kh(size_t(KVH) * P * HD), vh(size_t(KVH) * P * HD);
+      std::vector<uint16_t> ksh(size_t(KVH) * P), vsh(size_t(KVH) * P);
+      or_synth_kv(kv_seed, 500000 + uint64_t(l), KVH, HD, 0, P, kh.data(), vh.data(), ksh.data(), vsh.data());
+      for (int hh = 0; hh < KVH; ++hh)
+        for (int p = 0; p < P; ++p) {
+          std::memcpy(&k[(size_t(hh) * npos + p) * HD], &kh[(size_t(hh) * P + p) * HD], HD);
+          std::memcpy(&v[(size_t(hh) * npos + p) * HD], &vh[(size_t(hh) * P + p) * HD], HD);
+          ks[size_t(hh) * npos + p] = ksh[size_t(hh) * P + p];
+          vs[size_t(hh) * npos + p] = vsh[size_t(hh) * P + p];
+        }
+    }
+    for (int t = 0; t < B; ++t) {
+      const float* pr = proj.data() + size_t(t) * QP;
+      for (int hh = 0; hh < QH; ++hh) {
+        float xq[256];
+        std::memcpy(xq, pr + hh * HD, sizeof(float) * HD);
+        or_rope_wht(xq, HD, P + t, d->rope_theta, d->hadamard_k);
+        for (int dd = 0; dd < HD; ++dd) q[(size_t(t) * QH + hh) * HD + dd] = or_f16_to_f32(or_f32_to_f16(xq[dd]));
+      }
+      for (int hh = 0; hh < KVH; ++hh) {
+        float xk[256], xv[256];
+        std::memcpy(xk, pr + (QH + hh) * HD, sizeof(float) * HD);
+        std::memcpy(xv, pr + (QH + KVH + hh) * HD, sizeof(float) * HD);
+        or_rope_wht(xk, HD, P + t, d->rope_theta, d->hadamard_k);
+        const size_t o = size_t(hh) * npos + P + t;
+        quant_i8(xk, HD, &k[o * HD], &ks[o]);
+        quant_i8(xv, HD, &v[o * HD], &vs[o]);
+      }
+    }
+    const int window = (d->sliding_window > 0 && l % 2 == 0) ? d->sliding_window : 0;
+    if (d->sinks) or_synth_f32(seed, layer_tensor(l, 9), QH, 0.0f, 1.0f, sinks.data());
+    or_attention(q.data(), B, P, QH, KVH, HD, k.data(), v.data(), ks.data(), vs.data(), npos, window,
+                 d->sinks ? sinks.data() : nullptr, att.data());
+    for (auto& z : att) z = or_bf16_to_f32(or_f32_to_bf16(z));
+    synth_qmm(seed, layer_tensor(l, 2), H, QH * HD, sd, att.data(), B, y.data());
+    for (size_t i = 0; i < h.size(); ++i) h[i] += y[i];
+    or_synth_bf16(seed, layer_tensor(l, 3), H, 1.0f, 0.125f, wn.data());
+    or_rmsnorm(h.data(), B, H, wn.data(), d->rms_eps, x.data());
+    synth_qmm(seed, layer_tensor(l, 4), 2 * I, H, sd, x.data(), B, gu.data());
+    for (int t = 0; t < B; ++t)
+      for (int i = 0; i < I; ++i)
+        a[size_t(t) * I + i] = or_bf16_to_f32(or_f32_to_bf16(
+            or_glu(gu[size_t(t) * 2 * I + i], gu[size_t(t) * 2 * I + I + i], d->act, d->swiglu_limit)));
+    synth_qmm(seed, layer_tensor(l, 5), H, I, sd, a.data(), B, y.data());
+    for (size_t i = 0; i < h.size(); ++i) h[i] += y[i];
+  }
+  or_synth_bf16(seed, 2, H, 1.0f, 0.125f, wn.data());
+  or_rmsnorm(h.data(), B, H, wn.data(), d->rms_eps, x.data());
+  synth_qmm(seed, 3, V, H, sd, x.data(), B, logits);
+  or_argmax_rows(logits, B, V, top1);
+  return 0;
+}
+
 int or_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

@@ -1,0 +1,120 @@
+"""The whole verify step on the GPU against the CPU oracle, on small synthetic dense models.
+
+Reference behaviour: HybridModel.encodeVerify (Sources/Ingot/ModelRound.swift:48-82) and the greedy acceptance /
+commit of generateSpec (Sources/Ingot/Generate.swift:104-177). The reference's own checks of the same properties are
+the attention round vs CPU (Tests/IngotTests/KernelCaseTests.swift:178-206, maxRel 5e-3), row invariance
+(KernelCaseTests.swift:66-86) and rowscheck / gen --check (Sources/ingot-dev/Checks/RowsCheck.swift:6-50).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from ingot_amd._lib import Context, KVCache, Model, ModelDesc, accept
+from synth import cosine
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layers=2, hidden=256, n_q_heads=4, n_kv_heads=2, head_dim=128, intermediate=512, vocab=1000)
+GQA8 = dict(n_layers=2, hidden=512, n_q_heads=8, n_kv_heads=1, head_dim=64, intermediate=256, vocab=777)
+
+
+def logits_close(got, ref):
+    """(max-abs error, cosine) of GPU logits against the fp32 oracle."""
+    err = np.abs(got - ref).max()
+    return err, cosine(got, ref)
+
+
+# Logits tolerance: max-abs ≤ 0.02 + 1% of max|ref|, cosine ≥ 0.9999. Both sides round the activations to bf16 at the
+# same points (norm outputs, attention output, gated activation), so the difference is the occasional one-ulp flip of a
+# bf16 (0.4 %) or int8 KV level where the pre-rounding values differ in the last fp32 bits; at logits of magnitude ~10
+# one bf16 ulp is already 0.06.
+def within_tol(err, cos, scale):
+    return err <= 0.02 + 0.01 * scale and cos >= 0.9999
+
+
+def make(ctx, shape, seed=7, kv_seed=11, P=100, cap=512, **extra):
+    d = ModelDesc.make(**shape, **extra)
+    m = Model(ctx, d, seed)
+    kv = KVCache(m, cap)
+    kv.fill_synthetic(P, kv_seed)
+    return d, m, kv
+
+
+@pytest.mark.parametrize("shape", [SMALL, GQA8], ids=["gqa2-hd128", "gqa8-hd64"])
+@pytest.mark.parametrize("B", [1, 5, 17])
+def test_verify_step_matches_oracle(ctx, shape, B):
+    d, m, kv = make(ctx, shape)
+    try:
+        g = np.random.default_rng(B)
+        toks = g.integers(0, d.vocab, size=B).astype(np.uint32)
+        top1, logits = kv.verify(toks, want_logits=True)
+        ref_logits, ref_top1 = oracle.verify_dense(d, 7, 11, 100, toks)
+        err, cos = logits_close(logits, ref_logits)
+        scale = np.abs(ref_logits).max()
+        # Tolerance: bf16 activations and fp16 P·V on the GPU vs fp32 throughout in the oracle.
+        assert within_tol(err, cos, scale), (err, cos, scale)
+        # argmax: bit-exact unless the oracle's top-2 margin is inside the logit error.
+        srt = np.sort(ref_logits, axis=1)
+        margin = srt[:, -1] - srt[:, -2]
+        for r in range(B):
+            if margin[r] > 2 * err:
+                assert top1[r] == ref_top1[r], (r, margin[r], err)
+        assert np.array_equal(top1, np.argmax(logits, axis=1).astype(np.uint32))
+        assert kv.pos == 100  # not advanced by the verify step
+    finally:
+        kv.free()
+        m.free()
+
+
+def test_row_invariance_and_rollback(ctx):
+    """Row r's logits are bit-identical whatever B and whatever the later rows hold (KernelCaseTests.swift:66-86);
+    a rolled-back block leaves nothing behind (Generate.swift:515-540)."""
+    d, m, kv = make(ctx, SMALL)
+    try:
+        g = np.random.default_rng(3)
+        toks = g.integers(0, d.vocab, size=17).astype(np.uint32)
+        _, full = kv.verify(toks, want_logits=True)
+        for B in (1, 2, 9, 16):
+            _, part = kv.verify(toks[:B], want_logits=True)
+            assert np.array_equal(part.view(np.uint32), full[:B].view(np.uint32)), B
+        other = toks.copy()
+        other[6:] = g.integers(0, d.vocab, size=11)
+        _, mixed = kv.verify(other, want_logits=True)
+        assert np.array_equal(mixed[:6].view(np.uint32), full[:6].view(np.uint32))
+        # Rollback: after verifying junk at P, verifying the original block again gives the original bits.
+        _, again = kv.verify(toks, want_logits=True)
+        assert np.array_equal(again.view(np.uint32), full.view(np.uint32))
+    finally:
+        kv.free()
+        m.free()
+
+
+def test_commit_and_chained_rounds_match_plain_decode(ctx):
+    """Speculative rounds give exactly the greedy tokens of plain one-token decoding (docs/adr/0002, 0005; gen
+    --check): drafts that follow the greedy chain are all accepted, a wrong draft stops acceptance at its row."""
+    d, m, kv = make(ctx, SMALL, P=50)
+    try:
+        # Plain decode: 8 tokens one at a time.
+        tok = 17
+        plain = []
+        for _ in range(8):
+            r = kv.verify_and_accept([tok])
+            assert r.m == 0 and r.n_emitted == 1
+            tok = r.tokens[0]
+            plain.append(tok)
+        assert kv.pos == 58
+        # Speculative: roll back to 50 and verify the chain as drafts; plant a wrong draft after 5.
+        kv.set_pos(50)
+        drafts = [17] + plain[:7]
+        bad = list(drafts)
+        bad[6] = (bad[6] + 1) % d.vocab
+        r = kv.verify_and_accept(bad)
+        assert r.m == 5, r.m
+        assert r.emitted == plain[:6]
+        assert kv.pos == 56
+        # Continue from the new anchor: the remaining plain tokens.
+        r2 = kv.verify_and_accept([r.emitted[-1]] + plain[6:8])
+        assert r2.m == 2 and r2.emitted[:2] == plain[6:8]
+    finally:
+        kv.free()
+        m.free()
