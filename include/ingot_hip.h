@@ -60,6 +60,15 @@ int ih_memcpy_dtod(ih_ctx* ctx, void* dst_dev, const void* src_dev, size_t bytes
 /* Fills with a byte value using a kernel (no hipMemset node, so it is safe inside captured graphs). */
 int ih_fill(ih_ctx* ctx, void* dst_dev, int byte, size_t bytes);
 
+/* Per-kernel-class timing: with timing on, HIP events are recorded on the context's stream around every launch and
+ * ih_timing_read returns, for one class, the summed event time (ms), the launch count and the algorithmic bytes those
+ * launches move. Classes: 0 qmm, 1 attention, 2 attention prework, 3 attention reduce, 4 row kernels (norm, gated
+ * activation, embed), 5 argmax, 6 MoE routing/combine, 7 other. Enabling (or re-enabling) clears the records. The
+ * MI355X stand-in for the reference's GPUTimeline / gen --profile (Sources/Ingot/Timeline.swift:4-40,
+ * Sources/ingot-dev/GenProfile.swift:9-60). */
+int ih_timing_enable(ih_ctx* ctx, int on);
+int ih_timing_read(ih_ctx* ctx, int cls, double* total_ms, int* count, double* bytes);
+
 /* ---- quantized matrices ------------------------------------------------------------------------------------- */
 
 /* An MLX affine 4-bit matrix (group 64): w uint32 [N, K/8] (8 nibbles per word, low nibble first), scales and biases

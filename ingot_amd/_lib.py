@@ -90,6 +90,8 @@ def _declare(L: C.CDLL) -> None:
         "ih_verify_step_dev": (i32, [vp, vp, vp, i32, vp]),
         "ih_verify_and_accept": (i32, [vp, vp, vp, i32, vp]),
         "ih_model_logits_dev": (vp, [vp]),
+        "ih_timing_enable": (i32, [vp, i32]),
+        "ih_timing_read": (i32, [vp, i32, P(C.c_double), P(C.c_int), P(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         if hasattr(L, name):

@@ -314,6 +314,8 @@ __global__ __launch_bounds__(1024) void attn_reduce_kernel(AttnArgs a, uint4* __
 }
 
 int launch_prework(ih_ctx* c, const AttnArgs& a) {
+  TimedLaunch tl(c, TC_PREWORK, double(a.B) * (a.QH + 2 * a.KVH) * a.HD * 4 + double(a.B) * a.KVH * (2 * a.HD + 4) +
+                                    double(a.B) * a.QH * a.HD * 2);
   dim3 grid(a.QH + 2 * a.KVH, a.B);
   prework_kernel<<<grid, a.HD, 0, c->stream>>>(a);
   IH_HIP(hipGetLastError());
@@ -325,6 +327,9 @@ int launch_attention(ih_ctx* c, const AttnArgs& a) {
   const int qtiles = (Q + 15) / 16;
   const int nz = (qtiles + 7) / 8;
   dim3 grid(a.nsplit, a.KVH, nz);
+  // Algorithmic bytes: the int8 K and V and their fp16 scales of every key the launched splits cover, and q.
+  const double keys = double(a.P + a.B) - double(a.s0) * a.C;
+  TimedLaunch tl(c, TC_ATTN, double(a.KVH) * keys * (2 * a.HD + 4) + double(a.KVH) * Q * a.HD * 2);
   if (a.HD == 128) attn_kernel<128><<<grid, 256, 0, c->stream>>>(a);
   else if (a.HD == 64) attn_kernel<64><<<grid, 256, 0, c->stream>>>(a);
   else return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
@@ -335,6 +340,7 @@ int launch_attention(ih_ctx* c, const AttnArgs& a) {
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
   const int threads = a.QH * a.HD / 8;
   IH_CHECK(threads <= 1024 && threads % 64 == 0, IH_EINVAL, "attention reduce: QH·HD/8 must be a multiple of 64 ≤ 1024");
+  TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (a.HD + 2) * 4 + double(a.B) * a.QH * a.HD * 2);
   attn_reduce_kernel<<<a.B, threads, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.xsum, out.nkb);
   IH_HIP(hipGetLastError());
   return IH_OK;

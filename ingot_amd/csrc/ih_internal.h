@@ -92,8 +92,23 @@ struct ih_qmat {
   size_t algo_bytes = 0;   // bytes of the source format (MLX) per expert: the roofline's algorithmic bytes
 };
 
+namespace ih {
+// Per-kernel-class timing (ih_timing_*): events recorded around each launch when enabled.
+enum TimingClass : int { TC_QMM = 0, TC_ATTN = 1, TC_PREWORK = 2, TC_REDUCE = 3, TC_ROWS = 4, TC_ARGMAX = 5, TC_MOE = 6,
+                         TC_OTHER = 7, TC_COUNT = 8 };
+struct TimingRec {
+  int cls;
+  double bytes;
+  hipEvent_t a, b;
+};
+}  // namespace ih
+
 struct ih_ctx {
   int device = 0;
+  bool timing = false;
+  std::vector<ih::TimingRec> trecs;
+  std::vector<hipEvent_t> ev_pool;
+  size_t ev_used = 0;
   hipStream_t stream = nullptr;
   // Split-K scratch of the qmm: partial sums and arrival counters (the counters return to zero by themselves).
   float* part = nullptr;
@@ -107,6 +122,15 @@ struct ih_ctx {
 };
 
 namespace ih {
+// Brackets one launch for ih_timing_* (no-ops unless timing is enabled).
+struct TimedLaunch {
+  ih_ctx* c;
+  int cls;
+  double bytes;
+  hipEvent_t a = nullptr;
+  TimedLaunch(ih_ctx* ctx, int cl, double b);
+  ~TimedLaunch();
+};
 int fill(ih_ctx* c, void* dst, int byte, size_t bytes);
 int ensure_part(ih_ctx* c, size_t bytes);
 int ensure_act(ih_ctx* c, ActBuf& a, int K, bool f16);

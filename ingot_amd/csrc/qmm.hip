@@ -32,12 +32,16 @@ __device__ __forceinline__ unsigned short f2bf(float f) {
   return (unsigned short)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
-// (w & km) | kb in one v_and_or_b32 (LLVM selects a v_and/v_or pair here). km in a VGPR, kb in an SGPR: gfx9 VOP3
-// reads at most one scalar operand.
-__device__ __forceinline__ unsigned and_or(unsigned w, unsigned km, unsigned kb) {
-  unsigned r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(km), "s"(kb));
-  return r;
+// (w & km) | kb. With km in a VGPR (see vgpr_of) and kb in an SGPR, LLVM selects one v_and_or_b32 (gfx9 VOP3 reads at
+// most one scalar operand and no literal). The instruction is not written as inline assembly: the hazard recognizer
+// does not see into asm blocks, and an asm v_and_or_b32 feeding the MFMA operands produced wrong results.
+__device__ __forceinline__ unsigned and_or(unsigned w, unsigned km, unsigned kb) { return (w & km) | kb; }
+
+// A uniform value copied into a VGPR once (an opaque move, so the compiler keeps it in a vector register).
+__device__ __forceinline__ unsigned vgpr_of(unsigned s) {
+  unsigned v;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "s"(s));
+  return v;
 }
 
 // Eight nibbles of one word → eight bf16 values 128 + q in the element order {0,4,1,5,2,6,3,7}. km = 0x000F000F,
@@ -277,7 +281,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   }
   rs.x16off = 16u * p.nkb * 256u + qd * 64u;
   rs.xs16off = 16u * 4u;
-  const unsigned km = p.kmask, kbias = p.kbias;
+  const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
 
   QmmStage<T, R, X16> a, b;
   int kb = wave;
@@ -394,6 +398,9 @@ int launch_qmm(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, 
   p.kmask = 0x000F000Fu;
   p.kbias = 0x43004300u;
   const int grid = W->Npad / (16 * sh.R);
+  // Algorithmic bytes: the matrix in its MLX format, x (bf16) read, y written (read too when accumulating).
+  const double ybytes = double(M) * W->N * (out_mode == QO_BF16 ? 2 : (out_mode == QO_F32_ADD ? 8 : 4));
+  TimedLaunch tl(c, TC_QMM, double(W->algo_bytes) + double(M) * W->K * 2 + ybytes);
   if (M > 17) qmm_dispatch<2, true>(sh, grid, c->stream, p);
   else if (M == 17) qmm_dispatch<1, true>(sh, grid, c->stream, p);
   else qmm_dispatch<1, false>(sh, grid, c->stream, p);

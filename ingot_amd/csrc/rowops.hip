@@ -142,24 +142,28 @@ __global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1
 // ---------------------------------------------------------------------------------------------------------------
 int launch_embed(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* h,
                  int B, int H, int ldh) {
+  TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4));
   embed_kernel<<<B, 256, 0, c->stream>>>(tok, w, s, b, h, H, ldh);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
 
 int launch_rmsnorm_act(ih_ctx* c, const float* x, int ldx, const uint16_t* w, int rows, int D, float eps, ActBuf& a) {
+  TimedLaunch tl(c, TC_ROWS, double(rows) * D * (4 + 2) + D * 2);
   rmsnorm_act_kernel<<<rows, 256, 0, c->stream>>>(x, ldx, w, D, eps, static_cast<uint4*>(a.frag), a.xsum, a.nkb);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
 
 int launch_glu_act(ih_ctx* c, const float* gu, int ldg, int rows, int I, int act, float limit, ActBuf& a) {
+  TimedLaunch tl(c, TC_ROWS, double(rows) * I * (8 + 2));
   glu_act_kernel<<<rows, 256, 0, c->stream>>>(gu, ldg, I, act, limit, static_cast<uint4*>(a.frag), a.xsum, a.nkb);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
 
 int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out) {
+  TimedLaunch tl(c, TC_ARGMAX, double(rows) * N * 4);
   argmax_kernel<<<rows, 1024, 0, c->stream>>>(x, ldx, N, out);
   IH_HIP(hipGetLastError());
   return IH_OK;

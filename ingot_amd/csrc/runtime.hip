@@ -38,6 +38,29 @@ int fill(ih_ctx* c, void* dst, int byte, size_t bytes) {
   return IH_OK;
 }
 
+static hipEvent_t next_event(ih_ctx* c) {
+  if (c->ev_used == c->ev_pool.size()) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    c->ev_pool.push_back(e);
+  }
+  return c->ev_pool[c->ev_used++];
+}
+
+TimedLaunch::TimedLaunch(ih_ctx* ctx, int cl, double b) : c(ctx), cls(cl), bytes(b) {
+  if (!c->timing) return;
+  a = next_event(c);
+  if (a) (void)hipEventRecord(a, c->stream);
+}
+
+TimedLaunch::~TimedLaunch() {
+  if (!c->timing || !a) return;
+  hipEvent_t e = next_event(c);
+  if (!e) return;
+  (void)hipEventRecord(e, c->stream);
+  c->trecs.push_back(TimingRec{cls, bytes, a, e});
+}
+
 int ensure_part(ih_ctx* c, size_t bytes) {
   if (c->part_bytes >= bytes) return IH_OK;
   if (c->part) IH_HIP(hipFree(c->part));
@@ -120,6 +143,7 @@ int ih_ctx_free(ih_ctx* c) {
   if (!c) return IH_OK;
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
+  for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
   if (c->part) (void)hipFree(c->part);
   if (c->counters) (void)hipFree(c->counters);
   free_act(c->act);
@@ -177,6 +201,39 @@ int ih_memcpy_dtod(ih_ctx* c, void* dst, const void* src, size_t n) {
 int ih_fill(ih_ctx* c, void* dst, int byte, size_t n) {
   IH_CHECK(c && (n == 0 || dst), IH_EINVAL, "ih_fill: null argument");
   return fill(c, dst, byte, n);
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int ih_timing_enable(ih_ctx* c, int on) {
+  IH_CHECK(c, IH_EINVAL, "ih_timing_enable: null context");
+  IH_HIP(hipStreamSynchronize(c->stream));
+  c->timing = on != 0;
+  c->trecs.clear();
+  c->ev_used = 0;
+  return IH_OK;
+}
+
+int ih_timing_read(ih_ctx* c, int cls, double* total_ms, int* count, double* bytes) {
+  IH_CHECK(c && total_ms && count && bytes, IH_EINVAL, "ih_timing_read: null argument");
+  IH_CHECK(cls >= 0 && cls < TC_COUNT, IH_EINVAL, "ih_timing_read: unknown class");
+  IH_HIP(hipStreamSynchronize(c->stream));
+  double t = 0, b = 0;
+  int n = 0;
+  for (const auto& r : c->trecs) {
+    if (r.cls != cls) continue;
+    float ms = 0.f;
+    IH_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+    t += ms;
+    b += r.bytes;
+    ++n;
+  }
+  *total_ms = t;
+  *count = n;
+  *bytes = b;
+  return IH_OK;
 }
 
 }  // extern "C"

@@ -74,6 +74,9 @@ _SIGS = [
     ("or_rope_wht", None, [vp, i32, i32, C.c_float, i32]),
     ("or_attention", None, [vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp]),
     ("or_verify_dense", i32, [vp, C.c_uint64, C.c_uint64, i32, vp, i32, vp, vp]),
+    ("or_model_create", vp, [vp, C.c_uint64, C.c_uint64, i32, i32]),
+    ("or_model_verify", i32, [vp, vp, i32, vp, vp]),
+    ("or_model_free", None, [vp]),
 ]
 
 
@@ -242,3 +245,23 @@ def verify_dense(desc, seed: int, kv_seed: int, P: int, tokens):
     rc = lib().or_verify_dense(C.addressof(desc), seed, kv_seed, P, _p(t), B, _p(logits), _p(top1))
     assert rc == 0
     return logits, top1
+
+
+class OracleModel:
+    """The synthetic dense model held in host memory (weights and KV history), for repeated CPU verify steps."""
+
+    def __init__(self, desc, seed: int, kv_seed: int, P: int, max_rows: int = 17):
+        self.desc = desc
+        self.h = lib().or_model_create(C.addressof(desc), seed, kv_seed, P, max_rows)
+
+    def verify(self, tokens):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty((len(t), self.desc.vocab), np.float32)
+        top1 = np.empty(len(t), np.uint32)
+        assert lib().or_model_verify(self.h, _p(t), len(t), _p(logits), _p(top1)) == 0
+        return logits, top1
+
+    def free(self):
+        if self.h:
+            lib().or_model_free(self.h)
+            self.h = None

@@ -382,56 +382,103 @@ struct or_model_desc {
 
 static uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
 
-// Y[B, N] = X[B, K] (fp32 values) · Wᵀ of the synthetic int4 tensor `tensor`.
-static void synth_qmm(uint64_t seed, uint64_t tensor, int N, int K, float sd, const float* x, int B, float* y) {
-  std::vector<uint32_t> w(size_t(N) * K / 8);
-  std::vector<uint16_t> s(size_t(N) * K / 64), b(size_t(N) * K / 64);
-  or_synth_int4(seed, tensor, N, K, sd, w.data(), s.data(), b.data());
-  or_qmm_int4(x, B, w.data(), s.data(), b.data(), N, K, y);
-}
+// A synthetic int4 matrix held in host memory (MLX layout).
+struct QMat {
+  int N = 0, K = 0;
+  std::vector<uint32_t> w;
+  std::vector<uint16_t> s, b;
+  void make(uint64_t seed, uint64_t tensor, int n, int k, float sd) {
+    N = n;
+    K = k;
+    w.resize(size_t(N) * K / 8);
+    s.resize(size_t(N) * K / 64);
+    b.resize(size_t(N) * K / 64);
+    or_synth_int4(seed, tensor, N, K, sd, w.data(), s.data(), b.data());
+  }
+  void apply(const float* x, int B, float* y) const { or_qmm_int4(x, B, w.data(), s.data(), b.data(), N, K, y); }
+};
 
-// Returns 0 on success. logits [B][vocab], top1 [B]. The cache positions 0…P−1 hold the synthetic KV of kv_seed.
-int or_verify_dense(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, int P, const uint32_t* tokens, int B,
-                    float* logits, uint32_t* top1) {
-  const int H = d->hidden, QH = d->n_q_heads, KVH = d->n_kv_heads, HD = d->head_dim, I = d->intermediate, V = d->vocab;
-  const int QP = (QH + 2 * KVH) * HD, npos = P + B;
+struct OrLayer {
+  std::vector<uint16_t> attn_norm, mlp_norm;
+  std::vector<float> sinks;
+  QMat qkv, o, gate_up, down;
+  // KV of positions 0 … P−1 (history) followed by room for the block.
+  std::vector<int8_t> k, v;
+  std::vector<uint16_t> ks, vs;
+};
+
+struct OrModel {
+  or_model_desc d;
+  int P = 0, cap = 0;
+  std::vector<OrLayer> layers;
+  QMat embed, head;
+  std::vector<uint16_t> final_norm;
+};
+
+// Builds the synthetic model in host memory (weights of every layer, KV history of P positions from kv_seed).
+void* or_model_create(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, int P, int max_rows) {
+  OrModel* m = new OrModel();
+  m->d = *d;
+  m->P = P;
+  m->cap = P + max_rows;
+  const int H = d->hidden, QH = d->n_q_heads, KVH = d->n_kv_heads, HD = d->head_dim, I = d->intermediate;
+  const int QP = (QH + 2 * KVH) * HD;
   const float sd = 0.02f;
-  // Embedding rows.
-  std::vector<float> h(size_t(B) * H);
-  {
-    std::vector<uint32_t> w(size_t(V) * H / 8);
-    std::vector<uint16_t> s(size_t(V) * H / 64), b(size_t(V) * H / 64);
-    or_synth_int4(seed, 1, V, H, sd, w.data(), s.data(), b.data());
-    for (int r = 0; r < B; ++r) {
-      std::vector<float> row(H);
-      or_dequant_int4(w.data() + size_t(tokens[r]) * H / 8, s.data() + size_t(tokens[r]) * H / 64,
-                      b.data() + size_t(tokens[r]) * H / 64, 1, H, row.data());
-      std::memcpy(h.data() + size_t(r) * H, row.data(), sizeof(float) * H);
+  m->embed.make(seed, 1, d->vocab, H, sd);
+  m->head.make(seed, 3, d->vocab, H, sd);
+  m->final_norm.resize(H);
+  or_synth_bf16(seed, 2, H, 1.0f, 0.125f, m->final_norm.data());
+  m->layers.resize(d->n_layers);
+  for (int l = 0; l < d->n_layers; ++l) {
+    OrLayer& L = m->layers[l];
+    L.attn_norm.resize(H);
+    L.mlp_norm.resize(H);
+    or_synth_bf16(seed, layer_tensor(l, 0), H, 1.0f, 0.125f, L.attn_norm.data());
+    or_synth_bf16(seed, layer_tensor(l, 3), H, 1.0f, 0.125f, L.mlp_norm.data());
+    if (d->sinks) {
+      L.sinks.resize(QH);
+      or_synth_f32(seed, layer_tensor(l, 9), QH, 0.0f, 1.0f, L.sinks.data());
+    }
+    L.qkv.make(seed, layer_tensor(l, 1), QP, H, sd);
+    L.o.make(seed, layer_tensor(l, 2), H, QH * HD, sd);
+    L.gate_up.make(seed, layer_tensor(l, 4), 2 * I, H, sd);
+    L.down.make(seed, layer_tensor(l, 5), H, I, sd);
+    L.k.resize(size_t(KVH) * m->cap * HD);
+    L.v.resize(size_t(KVH) * m->cap * HD);
+    L.ks.resize(size_t(KVH) * m->cap);
+    L.vs.resize(size_t(KVH) * m->cap);
+    std::vector<int8_t> kh(size_t(KVH) * P * HD), vh(size_t(KVH) * P * HD);
+    std::vector<uint16_t> ksh(size_t(KVH) * P), vsh(size_t(KVH) * P);
+    or_synth_kv(kv_seed, 500000 + uint64_t(l), KVH, HD, 0, P, kh.data(), vh.data(), ksh.data(), vsh.data());
+    for (int hh = 0; hh < KVH; ++hh) {
+      std::memcpy(&L.k[size_t(hh) * m->cap * HD], &kh[size_t(hh) * P * HD], size_t(P) * HD);
+      std::memcpy(&L.v[size_t(hh) * m->cap * HD], &vh[size_t(hh) * P * HD], size_t(P) * HD);
+      std::memcpy(&L.ks[size_t(hh) * m->cap], &ksh[size_t(hh) * P], size_t(P) * 2);
+      std::memcpy(&L.vs[size_t(hh) * m->cap], &vsh[size_t(hh) * P], size_t(P) * 2);
     }
   }
+  return m;
+}
+
+void or_model_free(void* h) { delete static_cast<OrModel*>(h); }
+
+// One verify step of B rows at position P (not advancing it): logits [B][vocab], top1 [B].
+int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint32_t* top1) {
+  OrModel* m = static_cast<OrModel*>(h);
+  const or_model_desc* d = &m->d;
+  const int H = d->hidden, QH = d->n_q_heads, KVH = d->n_kv_heads, HD = d->head_dim, I = d->intermediate;
+  const int QP = (QH + 2 * KVH) * HD, P = m->P, cap = m->cap;
+  if (B < 1 || P + B > cap) return 1;
+  std::vector<float> hres(size_t(B) * H);
+  for (int r = 0; r < B; ++r)
+    or_dequant_int4(m->embed.w.data() + size_t(tokens[r]) * H / 8, m->embed.s.data() + size_t(tokens[r]) * H / 64,
+                    m->embed.b.data() + size_t(tokens[r]) * H / 64, 1, H, hres.data() + size_t(r) * H);
   std::vector<float> x(size_t(B) * H), proj(size_t(B) * QP), q(size_t(B) * QH * HD), att(size_t(B) * QH * HD);
   std::vector<float> y(size_t(B) * H), gu(size_t(B) * 2 * I), a(size_t(B) * I);
-  std::vector<uint16_t> wn(H);
-  std::vector<int8_t> k(size_t(KVH) * npos * HD), v(size_t(KVH) * npos * HD);
-  std::vector<uint16_t> ks(size_t(KVH) * npos), vs(size_t(KVH) * npos);
-  std::vector<float> sinks(QH);
   for (int l = 0; l < d->n_layers; ++l) {
-    or_synth_bf16(seed, layer_tensor(l, 0), H, 1.0f, 0.125f, wn.data());
-    or_rmsnorm(h.data(), B, H, wn.data(), d->rms_eps, x.data());
-    synth_qmm(seed, layer_tensor(l, 1), QP, H, sd, x.data(), B, proj.data());
-    // KV history, then this block's keys and values.
-    {
-      std::vector<int8_t> kh(size_t(KVH) * P * HD), vh(size_t(KVH) * P * HD);
-      std::vector<uint16_t> ksh(size_t(KVH) * P), vsh(size_t(KVH) * P);
-      or_synth_kv(kv_seed, 500000 + uint64_t(l), KVH, HD, 0, P, kh.data(), vh.data(), ksh.data(), vsh.data());
-      for (int hh = 0; hh < KVH; ++hh)
-        for (int p = 0; p < P; ++p) {
-          std::memcpy(&k[(size_t(hh) * npos + p) * HD], &kh[(size_t(hh) * P + p) * HD], HD);
-          std::memcpy(&v[(size_t(hh) * npos + p) * HD], &vh[(size_t(hh) * P + p) * HD], HD);
-          ks[size_t(hh) * npos + p] = ksh[size_t(hh) * P + p];
-          vs[size_t(hh) * npos + p] = vsh[size_t(hh) * P + p];
-        }
-    }
+    OrLayer& L = m->layers[l];
+    or_rmsnorm(hres.data(), B, H, L.attn_norm.data(), d->rms_eps, x.data());
+    L.qkv.apply(x.data(), B, proj.data());
     for (int t = 0; t < B; ++t) {
       const float* pr = proj.data() + size_t(t) * QP;
       for (int hh = 0; hh < QH; ++hh) {
@@ -445,33 +492,39 @@ int or_verify_dense(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, int
         std::memcpy(xk, pr + (QH + hh) * HD, sizeof(float) * HD);
         std::memcpy(xv, pr + (QH + KVH + hh) * HD, sizeof(float) * HD);
         or_rope_wht(xk, HD, P + t, d->rope_theta, d->hadamard_k);
-        const size_t o = size_t(hh) * npos + P + t;
-        quant_i8(xk, HD, &k[o * HD], &ks[o]);
-        quant_i8(xv, HD, &v[o * HD], &vs[o]);
+        const size_t o = size_t(hh) * cap + P + t;
+        quant_i8(xk, HD, &L.k[o * HD], &L.ks[o]);
+        quant_i8(xv, HD, &L.v[o * HD], &L.vs[o]);
       }
     }
     const int window = (d->sliding_window > 0 && l % 2 == 0) ? d->sliding_window : 0;
-    if (d->sinks) or_synth_f32(seed, layer_tensor(l, 9), QH, 0.0f, 1.0f, sinks.data());
-    or_attention(q.data(), B, P, QH, KVH, HD, k.data(), v.data(), ks.data(), vs.data(), npos, window,
-                 d->sinks ? sinks.data() : nullptr, att.data());
+    or_attention(q.data(), B, P, QH, KVH, HD, L.k.data(), L.v.data(), L.ks.data(), L.vs.data(), cap, window,
+                 d->sinks ? L.sinks.data() : nullptr, att.data());
     for (auto& z : att) z = or_bf16_to_f32(or_f32_to_bf16(z));
-    synth_qmm(seed, layer_tensor(l, 2), H, QH * HD, sd, att.data(), B, y.data());
-    for (size_t i = 0; i < h.size(); ++i) h[i] += y[i];
-    or_synth_bf16(seed, layer_tensor(l, 3), H, 1.0f, 0.125f, wn.data());
-    or_rmsnorm(h.data(), B, H, wn.data(), d->rms_eps, x.data());
-    synth_qmm(seed, layer_tensor(l, 4), 2 * I, H, sd, x.data(), B, gu.data());
+    L.o.apply(att.data(), B, y.data());
+    for (size_t i = 0; i < hres.size(); ++i) hres[i] += y[i];
+    or_rmsnorm(hres.data(), B, H, L.mlp_norm.data(), d->rms_eps, x.data());
+    L.gate_up.apply(x.data(), B, gu.data());
     for (int t = 0; t < B; ++t)
       for (int i = 0; i < I; ++i)
         a[size_t(t) * I + i] = or_bf16_to_f32(or_f32_to_bf16(
             or_glu(gu[size_t(t) * 2 * I + i], gu[size_t(t) * 2 * I + I + i], d->act, d->swiglu_limit)));
-    synth_qmm(seed, layer_tensor(l, 5), H, I, sd, a.data(), B, y.data());
-    for (size_t i = 0; i < h.size(); ++i) h[i] += y[i];
+    L.down.apply(a.data(), B, y.data());
+    for (size_t i = 0; i < hres.size(); ++i) hres[i] += y[i];
   }
-  or_synth_bf16(seed, 2, H, 1.0f, 0.125f, wn.data());
-  or_rmsnorm(h.data(), B, H, wn.data(), d->rms_eps, x.data());
-  synth_qmm(seed, 3, V, H, sd, x.data(), B, logits);
-  or_argmax_rows(logits, B, V, top1);
+  or_rmsnorm(hres.data(), B, H, m->final_norm.data(), d->rms_eps, x.data());
+  m->head.apply(x.data(), B, logits);
+  or_argmax_rows(logits, B, d->vocab, top1);
   return 0;
+}
+
+// Convenience: create, one step, free. logits [B][vocab], top1 [B].
+int or_verify_dense(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, int P, const uint32_t* tokens, int B,
+                    float* logits, uint32_t* top1) {
+  void* m = or_model_create(d, seed, kv_seed, P, B);
+  const int rc = or_model_verify(m, tokens, B, logits, top1);
+  or_model_free(m);
+  return rc;
 }
 
 int or_num_threads(void) {

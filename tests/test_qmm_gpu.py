@@ -119,3 +119,26 @@ def test_qmm_rejects_bad_shapes(ctx):
         dy.free()
     finally:
         W.free()
+
+
+# Every launch shape the verify step of config 1 uses (qkv, o, gate|up, down, head) at B = 1, 8 and 17.
+CFG1_SHAPES = [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336), (151936, 4096)]
+
+
+@pytest.mark.parametrize("N,K", CFG1_SHAPES)
+def test_qmm_config1_shapes(ctx, N, K):
+    g = rng(N + K)
+    w, s, b = int4_matrix(g, N, K)
+    xb, xf = bf16_normal(g, (17, K))
+    W = QMat.int4(ctx, w, s, b)
+    try:
+        ref = oracle.qmm_int4(xf, w, s, b)
+        full = run_qmm(ctx, W, xb, 17)
+        assert np.isfinite(full).all()
+        err = np.abs(full - ref).max()
+        assert err <= REL_TOL * np.abs(ref).max() + 1e-6, err
+        for m in (1, 8, 16):
+            part = run_qmm(ctx, W, np.ascontiguousarray(xb[:m]), m)
+            assert np.array_equal(part.view(np.uint32), full[:m].view(np.uint32)), m
+    finally:
+        W.free()
