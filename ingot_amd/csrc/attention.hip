@@ -103,11 +103,21 @@ constexpr int VROW = 32 + 8;   // LDS row of Vᵀ in halves
 // first 16-key tile) or 16 + 4·qd + e − 4 (second tile): the keys each lane holds after the Sᵀ MFMAs.
 __device__ __forceinline__ int vslot(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
 
+// K/V of one 32-key block in flight: per thread one 16-byte K item (key, 16 dims) and one V item (key pair, 8 dims:
+// 8 bytes of each key), so V can be written transposed as 32-bit key pairs.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  constexpr int NC = HD / 32;    // 32-dim chunks (MFMA K steps of Sᵀ)
-  constexpr int NDT = HD / 16;   // 16-dim tiles of Oᵀ
-  constexpr int QTW = 2;         // query tiles per wave (8 per workgroup)
+struct KVStage {
+  uint4 k;
+  uint2 v0, v1;
+  float ks, vs;
+};
+
+template <int HD>
+__global__ __launch_bounds__(512) void attn_kernel(AttnArgs a) {
+  constexpr int NC = HD / 32;           // 32-dim chunks (MFMA K steps of Sᵀ)
+  constexpr int NDT = HD / 16;          // 16-dim tiles of Oᵀ
+  constexpr int KITEMS = 32 * HD / 16;  // 16-byte K items of a block
+  constexpr int VITEMS = 16 * HD / 8;   // (key pair, 8 dims) V items of a block
   __shared__ _Float16 Kf[32 * KROW];
   __shared__ _Float16 Vt[HD * VROW];
   __shared__ float ksf[32], vsf[32];
@@ -115,171 +125,171 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // Partials are stored by launched split (blockIdx.x); the key range is that of split blockIdx.x + s0 (a sliding
   // window does not launch the splits that end before the first row's window).
   const int sidx = blockIdx.x, split = sidx + a.s0, kvh = blockIdx.y;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 15, qd = lane >> 4;
+  const int nthreads = blockDim.x, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
   const int Q = a.G * a.B;
-  const int kend_all = a.P + a.B;
-  const int k0 = split * a.C, k1 = min(k0 + a.C, kend_all);
+  const int k0 = split * a.C, k1 = min(k0 + a.C, a.P + a.B);
 
-  // This wave's query tiles.
-  int qt[QTW];
-  bool qlive[QTW];
+  // One 16-query tile per wave.
+  const int qt = blockIdx.z * (nthreads >> 6) + wave;
+  const bool qlive = 16 * qt < Q;
+  const int m = 16 * qt + j;
+  f16x8 qf[NC];
 #pragma unroll
-  for (int u = 0; u < QTW; ++u) {
-    qt[u] = blockIdx.z * 4 * QTW + wave + 4 * u;
-    qlive[u] = 16 * qt[u] < Q;
-  }
-  f16x8 qf[QTW][NC];
-  f32x4 o[QTW][NDT];
-  float mrun[QTW], lsum[QTW];
-#pragma unroll
-  for (int u = 0; u < QTW; ++u) {
-    mrun[u] = -INFINITY;
-    lsum[u] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[u][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int m = 16 * qt[u] + j;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      if (qlive[u] && m < Q) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(a.q + (size_t(kvh) * a.Qpad + m) * HD + 32 * c + 8 * qd);
-        qf[u][c] = __builtin_bit_cast(f16x8, v);
-      } else {
-        qf[u][c] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
+  for (int c = 0; c < NC; ++c) {
+    if (qlive && m < Q) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(a.q + (size_t(kvh) * a.Qpad + m) * HD + 32 * c + 8 * qd);
+      qf[c] = __builtin_bit_cast(f16x8, v);
+    } else {
+      qf[c] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
+  f32x4 o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mrun = -INFINITY, lsum = 0.f;
+  const int tok = m / a.G;
+  const int lim = a.P + tok;  // last visible key (causal)
+  const int lo_key = a.window > 0 ? lim - a.window + 1 : -2147483647;
 
   const int8_t* kh = a.kc + size_t(kvh) * a.cap * HD;
   const int8_t* vh = a.vc + size_t(kvh) * a.cap * HD;
   const __half* ksh = a.ks + size_t(kvh) * a.cap;
   const __half* vsh = a.vs + size_t(kvh) * a.cap;
+  auto slot_of = [&](int key) { return a.ring ? key % a.ring : key; };
 
-  // Loader mapping: 32 keys × HD bytes of K and of V; each thread moves 16 bytes of each (HD = 128) or 8 (HD = 64).
-  constexpr int BPT = HD / 8;                   // bytes per thread per tensor
-  const int lk = threadIdx.x / (HD / BPT);      // key within the block
-  const int ld0 = (threadIdx.x % (HD / BPT)) * BPT;
-
-  for (int kb = k0; kb < k1; kb += 32) {
-    // Stage the block: keys kb … kb+31 (slots wrap in a ring cache; keys past k1 read as zero and are masked).
-    {
-      const int key = kb + lk;
-      const bool ok = key < k1;
-      const int slot = a.ring ? key % a.ring : key;
-      unsigned kw[BPT / 4], vw[BPT / 4];
+  // Loader items of this thread (at most one K and one V item, since blockDim ≥ 256 for HD 128 and ≥ 128 for 64
+  // is not guaranteed: threads beyond the item count load nothing).
+  const bool hask = tid < KITEMS, hasv = tid < VITEMS;
+  const int kkey = tid / (HD / 16), kcol = (tid % (HD / 16)) * 16;
+  const int vpair = tid / (HD / 8), vcol = (tid % (HD / 8)) * 8;
+  KVStage<HD> st;
+  auto load = [&](int kb) {
+    if (hask) {
+      const int key = kb + kkey;
+      st.k = key < k1 ? *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + kcol) : make_uint4(0, 0, 0, 0);
+    }
+    if (hasv) {
+      const int key0 = kb + 2 * vpair, key1 = key0 + 1;
+      st.v0 = key0 < k1 ? *reinterpret_cast<const uint2*>(vh + size_t(slot_of(key0)) * HD + vcol) : make_uint2(0, 0);
+      st.v1 = key1 < k1 ? *reinterpret_cast<const uint2*>(vh + size_t(slot_of(key1)) * HD + vcol) : make_uint2(0, 0);
+    }
+    if (tid < 32) {
+      const int key = kb + tid;
+      st.ks = key < k1 ? __half2float(ksh[slot_of(key)]) * a.scale_log2 : 0.f;
+      st.vs = key < k1 ? __half2float(vsh[slot_of(key)]) : 0.f;
+    }
+  };
+  auto store = [&]() {
+    if (hask) {
+      const unsigned kw[4] = {st.k.x, st.k.y, st.k.z, st.k.w};
 #pragma unroll
-      for (int i = 0; i < BPT / 4; ++i) {
-        kw[i] = ok ? *reinterpret_cast<const unsigned*>(kh + size_t(slot) * HD + ld0 + 4 * i) : 0u;
-        vw[i] = ok ? *reinterpret_cast<const unsigned*>(vh + size_t(slot) * HD + ld0 + 4 * i) : 0u;
-      }
-      __syncthreads();  // the previous block's readers are done with LDS
-#pragma unroll
-      for (int i = 0; i < BPT / 4; ++i) {
+      for (int i = 0; i < 4; ++i) {
         __half2 lo, hi;
         i8x4_to_h(kw[i], lo, hi);
-        *reinterpret_cast<__half2*>(&Kf[lk * KROW + ld0 + 4 * i]) = lo;
-        *reinterpret_cast<__half2*>(&Kf[lk * KROW + ld0 + 4 * i + 2]) = hi;
-        i8x4_to_h(vw[i], lo, hi);
-        const int vsl = vslot(lk);
-        Vt[(ld0 + 4 * i + 0) * VROW + vsl] = __builtin_bit_cast(_Float16, __low2half(lo));
-        Vt[(ld0 + 4 * i + 1) * VROW + vsl] = __builtin_bit_cast(_Float16, __high2half(lo));
-        Vt[(ld0 + 4 * i + 2) * VROW + vsl] = __builtin_bit_cast(_Float16, __low2half(hi));
-        Vt[(ld0 + 4 * i + 3) * VROW + vsl] = __builtin_bit_cast(_Float16, __high2half(hi));
+        *reinterpret_cast<__half2*>(&Kf[kkey * KROW + kcol + 4 * i]) = lo;
+        *reinterpret_cast<__half2*>(&Kf[kkey * KROW + kcol + 4 * i + 2]) = hi;
       }
-      if (threadIdx.x < 32) {
-        const int key2 = kb + threadIdx.x;
-        const int sl2 = a.ring ? key2 % a.ring : key2;
-        ksf[threadIdx.x] = key2 < k1 ? __half2float(ksh[sl2]) * a.scale_log2 : 0.f;
-        vsf[threadIdx.x] = key2 < k1 ? __half2float(vsh[sl2]) : 0.f;
-      }
-      __syncthreads();
     }
+    if (hasv) {
+      // Keys 2·vpair and 2·vpair + 1 occupy adjacent slots: one 32-bit (key pair) store per dim.
+      const int sl = vslot(2 * vpair);
+      const unsigned a0[2] = {st.v0.x, st.v0.y}, a1[2] = {st.v1.x, st.v1.y};
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        __half2 l0, h0, l1, h1;
+        i8x4_to_h(a0[i], l0, h0);
+        i8x4_to_h(a1[i], l1, h1);
+        const int d = vcol + 4 * i;
+        *reinterpret_cast<__half2*>(&Vt[(d + 0) * VROW + sl]) = __halves2half2(__low2half(l0), __low2half(l1));
+        *reinterpret_cast<__half2*>(&Vt[(d + 1) * VROW + sl]) = __halves2half2(__high2half(l0), __high2half(l1));
+        *reinterpret_cast<__half2*>(&Vt[(d + 2) * VROW + sl]) = __halves2half2(__low2half(h0), __low2half(h1));
+        *reinterpret_cast<__half2*>(&Vt[(d + 3) * VROW + sl]) = __halves2half2(__high2half(h0), __high2half(h1));
+      }
+    }
+    if (tid < 32) {
+      ksf[tid] = st.ks;
+      vsf[tid] = st.vs;
+    }
+  };
 
+  if (k0 < k1) load(k0);
+  for (int kb = k0; kb < k1; kb += 32) {
+    __syncthreads();  // the previous block's readers are done with LDS
+    store();
+    __syncthreads();
+    if (kb + 32 < k1) load(kb + 32);  // next block in flight during this one's products
+    if (!qlive) continue;             // uniform per wave
+    // Sᵀ for the two 16-key tiles: lane (j, qd) holds keys 16h + 4qd + r of query m.
+    f32x4 sacc[2];
 #pragma unroll
-    for (int u = 0; u < QTW; ++u) {
-      if (!qlive[u]) continue;   // uniform per wave
-      // Sᵀ for the two 16-key tiles.
-      f32x4 sacc[2];
+    for (int h = 0; h < 2; ++h) {
+      sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const f16x8 kf = *reinterpret_cast<const f16x8*>(&Kf[(16 * h + j) * KROW + 32 * c + 8 * qd]);
-          sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[u][c], sacc[h], 0, 0, 0);
-        }
+      for (int c = 0; c < NC; ++c) {
+        const f16x8 kf = *reinterpret_cast<const f16x8*>(&Kf[(16 * h + j) * KROW + 32 * c + 8 * qd]);
+        sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[c], sacc[h], 0, 0, 0);
       }
-      // Lane (j, qd) holds keys 16h + 4qd + r of query m = 16·qt + j.
-      const int m = 16 * qt[u] + j;
-      const int tok = m / a.G;
-      const int lim = a.P + tok;  // last visible key (causal)
-      const int lo_key = a.window > 0 ? lim - a.window + 1 : -2147483647;
-      float s[2][4];
-      float mx = -INFINITY;
+    }
+    float s[2][4];
+    float mx = -INFINITY;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int kk = 16 * h + 4 * qd + r, key = kb + kk;
-          const bool vis = m < Q && key < k1 && key <= lim && key >= lo_key;
-          s[h][r] = vis ? sacc[h][r] * ksf[kk] : -INFINITY;
-          mx = fmaxf(mx, s[h][r]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(mrun[u], mx);
-      const float alpha = mnew == -INFINITY ? 1.f : exp2f(mrun[u] - mnew);
-      mrun[u] = mnew;
-      float ps = 0.f;
-      _Float16 pv[8];
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = s[h][r] == -INFINITY ? 0.f : exp2f(s[h][r] - mnew);
-          ps += p;
-          pv[4 * h + r] = (_Float16)(p * vsf[16 * h + 4 * qd + r]);
-        }
-      lsum[u] = lsum[u] * alpha + ps;
-      // Rescale Oᵀ only when some column's maximum moved (alpha = 1 is exact and is skipped).
-      if (__any(alpha != 1.f)) {
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[u][dt] *= alpha;
+      for (int r = 0; r < 4; ++r) {
+        const int kk = 16 * h + 4 * qd + r, key = kb + kk;
+        const bool vis = m < Q && key < k1 && key <= lim && key >= lo_key;
+        s[h][r] = vis ? sacc[h][r] * ksf[kk] : -INFINITY;
+        mx = fmaxf(mx, s[h][r]);
       }
-      f16x8 pb;
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(mrun, mx);
+    const float alpha = mnew == -INFINITY ? 1.f : exp2f(mrun - mnew);
+    mrun = mnew;
+    float ps = 0.f;
+    f16x8 pb;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = pv[e];
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const f16x8 vf = *reinterpret_cast<const f16x8*>(&Vt[(16 * dt + j) * VROW + 8 * qd]);
-        o[u][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb, o[u][dt], 0, 0, 0);
+      for (int r = 0; r < 4; ++r) {
+        const float p = s[h][r] == -INFINITY ? 0.f : exp2f(s[h][r] - mnew);
+        ps += p;
+        pb[4 * h + r] = (_Float16)(p * vsf[16 * h + 4 * qd + r]);
       }
+    lsum = lsum * alpha + ps;
+    // Rescale Oᵀ only when some column's maximum moved (alpha = 1 is exact and is skipped).
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+    }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const f16x8 vf = *reinterpret_cast<const f16x8*>(&Vt[(16 * dt + j) * VROW + 8 * qd]);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb, o[dt], 0, 0, 0);
     }
   }
 
   // Partials of this split: (max, sum) per query and the unnormalised Oᵀ (lane holds dims 16dt + 4qd + r of query m).
+  if (!qlive) return;
+  float l = lsum;
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (m >= Q) return;
   const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
+  if (qd == 0) a.ml[base + m] = make_float2(mrun, l);
 #pragma unroll
-  for (int u = 0; u < QTW; ++u) {
-    if (!qlive[u]) continue;
-    float l = lsum[u];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const int m = 16 * qt[u] + j;
-    if (m >= Q) continue;
-    if (qd == 0) a.ml[base + m] = make_float2(mrun[u], l);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-      *reinterpret_cast<f32x4*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = o[u][dt];
-  }
+  for (int dt = 0; dt < NDT; ++dt)
+    *reinterpret_cast<f32x4*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = o[dt];
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 // Reduction of the splits (vattn_reduce, verify_attn.metal:149-192): M = max over splits (and the sink), L = Σ e^(m−M)·l
 // (+ e^(sink−M)), o = Σ e^(m−M)·O / L, in split order; written into the o_proj activation layout (column h·HD + d).
-// Grid (B), QH·HD/8 threads (one per 8 values).
-__global__ __launch_bounds__(1024) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, float* __restrict__ xsum,
-                                                           int nkb) {
-  const int t = blockIdx.x, c = threadIdx.x, HD = a.HD;
+// Grid (B, QH·HD/512), 64 threads (one per 8 values).
+__global__ __launch_bounds__(64) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, float* __restrict__ xsum,
+                                                         int nkb) {
+  const int t = blockIdx.x, c = blockIdx.y * 64 + threadIdx.x, HD = a.HD;
   const int h = (8 * c) / HD, d0 = (8 * c) % HD;
   const int kvh = h / a.G, m = t * a.G + h % a.G;
   float M = -INFINITY;
@@ -325,23 +335,25 @@ int launch_prework(ih_ctx* c, const AttnArgs& a) {
 int launch_attention(ih_ctx* c, const AttnArgs& a) {
   const int Q = a.G * a.B;
   const int qtiles = (Q + 15) / 16;
-  const int nz = (qtiles + 7) / 8;
+  const int nz = (qtiles + 7) / 8;        // query groups of ≤ 8 tiles, one wave per tile
+  const int waves = (qtiles + nz - 1) / nz;
+  // The block loader needs 32·HD/16 threads (256 for HD 128, 128 for HD 64).
+  const int threads = std::max(64 * waves, a.HD * 2);
   dim3 grid(a.nsplit, a.KVH, nz);
   // Algorithmic bytes: the int8 K and V and their fp16 scales of every key the launched splits cover, and q.
   const double keys = double(a.P + a.B) - double(a.s0) * a.C;
   TimedLaunch tl(c, TC_ATTN, double(a.KVH) * keys * (2 * a.HD + 4) + double(a.KVH) * Q * a.HD * 2);
-  if (a.HD == 128) attn_kernel<128><<<grid, 256, 0, c->stream>>>(a);
-  else if (a.HD == 64) attn_kernel<64><<<grid, 256, 0, c->stream>>>(a);
+  if (a.HD == 128) attn_kernel<128><<<grid, threads, 0, c->stream>>>(a);
+  else if (a.HD == 64) attn_kernel<64><<<grid, threads, 0, c->stream>>>(a);
   else return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
 
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
-  const int threads = a.QH * a.HD / 8;
-  IH_CHECK(threads <= 1024 && threads % 64 == 0, IH_EINVAL, "attention reduce: QH·HD/8 must be a multiple of 64 ≤ 1024");
+  IH_CHECK((a.QH * a.HD) % 512 == 0, IH_EINVAL, "attention reduce: QH·HD must be a multiple of 512");
   TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (a.HD + 2) * 4 + double(a.B) * a.QH * a.HD * 2);
-  attn_reduce_kernel<<<a.B, threads, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.xsum, out.nkb);
+  attn_reduce_kernel<<<dim3(a.B, a.QH * a.HD / 512), 64, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.xsum, out.nkb);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

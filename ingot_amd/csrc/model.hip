@@ -137,8 +137,7 @@ static int check_desc(const ih_model_desc& d) {
   IH_CHECK(d.n_layers >= 1 && d.hidden >= 64 && d.hidden % 64 == 0, IH_EINVAL, "model: hidden must be a multiple of 64");
   IH_CHECK(d.head_dim == 64 || d.head_dim == 128, IH_EINVAL, "model: head_dim must be 64 or 128");
   IH_CHECK(d.n_kv_heads >= 1 && d.n_q_heads % d.n_kv_heads == 0, IH_EINVAL, "model: q heads must be a multiple of kv heads");
-  IH_CHECK(d.n_q_heads * d.head_dim % 64 == 0 && d.n_q_heads * d.head_dim / 8 <= 1024, IH_EINVAL,
-           "model: q_heads·head_dim must be a multiple of 64 and at most 8192");
+  IH_CHECK(d.n_q_heads * d.head_dim % 512 == 0, IH_EINVAL, "model: q_heads·head_dim must be a multiple of 512");
   IH_CHECK(d.vocab >= 1 && d.rms_eps > 0 && d.rope_theta > 0, IH_EINVAL, "model: vocab, eps and theta must be positive");
   IH_CHECK(d.n_experts == 0, IH_EINVAL, "model: MoE layers are not available in this build yet");
   IH_CHECK(d.intermediate >= 64 && d.intermediate % 64 == 0, IH_EINVAL, "model: intermediate must be a multiple of 64");
@@ -330,9 +329,10 @@ int ih_kv_create(ih_model* m, int capacity, ih_kv** out) {
   ih_kv* kv = new ih_kv();
   kv->model = m;
   kv->cap = capacity;
-  // Key chunk: fixed per cache, about 32 splits at full capacity (256 … 2048).
+  // Key chunk: fixed per cache (so a row's result is the same for every block size and every position), at most
+  // about 64 splits at full capacity (256 … 2048 keys).
   int C = 256;
-  while (C < 2048 && (capacity + C - 1) / C > 32) C *= 2;
+  while (C < 2048 && (capacity + C - 1) / C > 64) C *= 2;
   kv->chunk = C;
   const int L = d.n_layers, KVH = d.n_kv_heads, HD = d.head_dim;
   kv->kc.assign(L, nullptr); kv->vc.assign(L, nullptr); kv->ks.assign(L, nullptr); kv->vs.assign(L, nullptr);

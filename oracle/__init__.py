@@ -77,6 +77,14 @@ _SIGS = [
     ("or_model_create", vp, [vp, C.c_uint64, C.c_uint64, i32, i32]),
     ("or_model_verify", i32, [vp, vp, i32, vp, vp]),
     ("or_model_free", None, [vp]),
+    ("or_route", None, [vp, i32, i32, i32, i32, vp, vp, vp, C.c_float, C.c_float, vp, vp]),
+    ("or_expert_union", i32, [vp, i32, i32, i32, vp, vp]),
+    ("or_copy_naive", i32, [vp, i32, i32, i32, i32, vp, vp]),
+    ("or_copy_index_new", vp, [i32]),
+    ("or_copy_index_free", None, [vp]),
+    ("or_copy_index_append", None, [vp, vp, i32]),
+    ("or_copy_index_propose", i32, [vp, i32, vp, vp]),
+    ("or_splitmix64", None, [C.c_uint64, i32, vp]),
 ]
 
 
@@ -265,3 +273,68 @@ class OracleModel:
         if self.h:
             lib().or_model_free(self.h)
             self.h = None
+
+
+# ---- MoE routing and copy-from-context ----------------------------------------------------------------------------
+
+def route(logits, K, sigmoid=False, sel_bias=None, logit_bias=None, pes=None, scale=1.0, eps=0.0):
+    """(expert ids [rows][K] int32, weights [rows][K] fp32)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    rows, E = lg.shape
+    inds = np.empty((rows, K), np.int32)
+    wts = np.empty((rows, K), np.float32)
+
+    def opt(a):
+        return None if a is None else np.ascontiguousarray(a, np.float32)
+
+    sb, lb, pe = opt(sel_bias), opt(logit_bias), opt(pes)
+    lib().or_route(_p(lg), rows, E, K, int(sigmoid), _p(sb) if sb is not None else None,
+                   _p(lb) if lb is not None else None, _p(pe) if pe is not None else None, scale, eps, _p(inds), _p(wts))
+    return inds, wts
+
+
+def expert_union(inds, E):
+    """(entries [U][3] = (expert, start, count), pairs [rows·K][2] = (row, slot))."""
+    inds = np.ascontiguousarray(inds, np.int32)
+    rows, K = inds.shape
+    entries = np.empty((rows * K, 3), np.int32)
+    pairs = np.empty((rows * K, 2), np.int32)
+    U = lib().or_expert_union(_p(inds), rows, K, E, _p(entries), _p(pairs))
+    return entries[:U].copy(), pairs
+
+
+def copy_naive(h, maxK, min_match=3, max_match=64):
+    """(proposal, match length) of the reference's copy rule by brute force."""
+    h = np.ascontiguousarray(h, np.uint32)
+    out = np.empty(max(maxK, 1), np.uint32)
+    m = C.c_int()
+    n = lib().or_copy_naive(_p(h), len(h), maxK, min_match, max_match, _p(out), C.byref(m))
+    return out[:n].copy(), m.value
+
+
+class CopyIndexRef:
+    """The reference's trigram index, restated (test infrastructure)."""
+
+    def __init__(self, capacity=1 << 16):
+        self.h = lib().or_copy_index_new(capacity)
+
+    def append(self, toks):
+        t = np.ascontiguousarray(np.atleast_1d(toks), np.uint32)
+        lib().or_copy_index_append(self.h, _p(t), len(t))
+
+    def propose(self, maxK):
+        out = np.empty(max(maxK, 1), np.uint32)
+        m = C.c_int()
+        n = lib().or_copy_index_propose(self.h, maxK, _p(out), C.byref(m))
+        return out[:n].copy(), m.value
+
+    def free(self):
+        if self.h:
+            lib().or_copy_index_free(self.h)
+            self.h = None
+
+
+def splitmix64(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint64)
+    lib().or_splitmix64(seed, n, _p(out))
+    return out

@@ -527,6 +527,194 @@ int or_verify_dense(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, int
   return rc;
 }
 
+
+// ---------------------------------------------------------------------------------------------------------------
+// MoE router: top-k by score (plus a selection bias), ties to the lower index, NaN logits → −inf; weights from the
+// unbiased scores: softmax over the chosen logits (renormalised top-k) or sigmoid p / (Σp + eps); times `scale` and a
+// per-expert scale. A router linear bias is part of the logits. RouterVector.reference
+// (Tests/IngotTests/KernelCaseRouter.swift:54-80) and vmoe_route (Sources/Ingot/Shaders/verify.metal:160-240).
+void or_route(const float* logits, int rows, int E, int K, int sigmoid, const float* sel_bias, const float* logit_bias,
+              const float* pes, float scale, float eps, int32_t* inds, float* wts) {
+  std::vector<float> l(E), p(E), sel(E);
+  std::vector<int> order(E);
+  for (int r = 0; r < rows; ++r) {
+    for (int e = 0; e < E; ++e) {
+      float v = logits[size_t(r) * E + e] + (logit_bias ? logit_bias[e] : 0.f);
+      if (std::isnan(v)) v = -std::numeric_limits<float>::infinity();
+      l[e] = v;
+      p[e] = sigmoid ? 1.0f / (1.0f + std::exp(-v)) : v;
+      sel[e] = p[e] + (sel_bias ? sel_bias[e] : 0.f);
+      order[e] = e;
+    }
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return sel[a] > sel[b]; });
+    float w[64], sum = 0.f;
+    for (int k = 0; k < K; ++k) {
+      const int e = order[k];
+      w[k] = sigmoid ? p[e] : std::exp(l[e] - l[order[0]]);
+      sum += w[k];
+    }
+    if (sigmoid) sum += eps;
+    for (int k = 0; k < K; ++k) {
+      const int e = order[k];
+      inds[size_t(r) * K + k] = e;
+      wts[size_t(r) * K + k] = w[k] / sum * scale * (pes ? pes[e] : 1.0f);
+    }
+  }
+}
+
+// Expert union of a round by counting sort: entries (expert, start, count) in increasing expert order, pairs (row,
+// slot) in row order inside each expert, slot = the rank k of the expert in the row's top-k. vmoe_route
+// (Sources/Ingot/Shaders/verify.metal:262-318) and MoEPipeline.round (Tests/IngotTests/KernelHarness.swift:630-652).
+// Returns U, the number of distinct experts; entries [U][3], pairs [rows·K][2].
+int or_expert_union(const int32_t* inds, int rows, int K, int E, int32_t* entries, int32_t* pairs) {
+  int U = 0, off = 0;
+  for (int e = 0; e < E; ++e) {
+    int cnt = 0;
+    for (int i = 0; i < rows * K; ++i)
+      if (inds[i] == e) {
+        pairs[2 * (off + cnt)] = i / K;
+        pairs[2 * (off + cnt) + 1] = i % K;
+        ++cnt;
+      }
+    if (cnt == 0) continue;
+    entries[3 * U] = e;
+    entries[3 * U + 1] = off;
+    entries[3 * U + 2] = cnt;
+    ++U;
+    off += cnt;
+  }
+  return U;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Copy-from-context lookup. The rule (CopySpecTests.naive, Tests/IngotTests/CopySpecTests.swift:9-28): among the
+// three most recent earlier occurrences p < cur of the last trigram (the index keeps four ends, the current one
+// included), the one with the longest backward match (at most 64, len ≤ p), ties to the most recent; at least 3;
+// propose h[p+1 … min(cur, p + maxK)]. Returns the proposal length and leaves the match length in *match.
+int or_copy_naive(const uint32_t* h, int n, int maxK, int minMatch, int maxMatch, uint32_t* out, int* match) {
+  *match = 0;
+  if (n < 4 || maxK <= 0) return 0;
+  const int cur = n - 1;
+  int cand[3], nc = 0;
+  for (int p = cur - 1; p >= 2 && nc < 3; --p)
+    if (h[p] == h[cur] && h[p - 1] == h[cur - 1] && h[p - 2] == h[cur - 2]) cand[nc++] = p;
+  int bestEnd = 0, bestLen = 0;
+  for (int i = 0; i < nc; ++i) {
+    const int p = cand[i];
+    int len = 0;
+    while (len < maxMatch && len <= p && h[p - len] == h[cur - len]) ++len;
+    if (len > bestLen) { bestLen = len; bestEnd = p; }
+  }
+  if (bestLen < minMatch) return 0;
+  *match = bestLen;
+  const int end = std::min(cur, bestEnd + maxK);
+  for (int i = bestEnd + 1; i <= end; ++i) out[i - bestEnd - 1] = h[i];
+  return end - bestEnd;
+}
+
+// The reference's index restated (CopyIndex, Sources/Ingot/CopySpec.swift:15-139): a 4-way table of the most recent
+// ends of each trigram key, key = mix(a·φ ^ mix(b + c1) ^ (c << 1)) | 1, open addressing, rebuilt at occupancy > 1/2.
+struct OrCopyIndex {
+  static constexpr int WAYS = 4;
+  int minMatch = 3, maxMatch = 64;
+  std::vector<uint32_t> hist;
+  std::vector<uint64_t> keys;
+  std::vector<uint32_t> pos;
+  std::vector<uint8_t> cnt;
+  size_t mask = 0, used = 0;
+  static uint64_t mix(uint64_t x) {
+    x ^= x >> 33; x *= 0xff51afd7ed558ccdull;
+    x ^= x >> 33; x *= 0xc4ceb9fe1a85ec53ull;
+    return x ^ (x >> 33);
+  }
+  void allocate(size_t tokens) {
+    size_t cap = 1;
+    while (cap < tokens * 2) cap <<= 1;
+    keys.assign(cap, 0);
+    pos.assign(cap * WAYS, 0);
+    cnt.assign(cap, 0);
+    mask = cap - 1;
+    used = 0;
+  }
+  uint64_t key_at(size_t end) const {
+    const uint64_t a = hist[end - 2], b = hist[end - 1], c = hist[end];
+    return mix((a * 0x9E3779B97F4A7C15ull) ^ mix(b + 0x632BE59BD9B4E019ull) ^ (c << 1)) | 1ull;
+  }
+  long find(uint64_t key) const {
+    size_t i = key & mask;
+    while (true) {
+      if (keys[i] == key) return long(i);
+      if (keys[i] == 0) return -1;
+      i = (i + 1) & mask;
+    }
+  }
+  void index(size_t end) {
+    if (used * 2 > keys.size()) { rebuild(hist.size() * 2); return; }
+    const uint64_t key = key_at(end);
+    size_t i = key & mask;
+    while (keys[i] != 0 && keys[i] != key) i = (i + 1) & mask;
+    if (keys[i] == 0) { keys[i] = key; ++used; }
+    const size_t b = i * WAYS;
+    for (int w = WAYS - 1; w > 0; --w) pos[b + w] = pos[b + w - 1];
+    pos[b] = uint32_t(end);
+    if (cnt[i] < WAYS) ++cnt[i];
+  }
+  void rebuild(size_t capacity) {
+    allocate(std::max(capacity, size_t(1) << 16));
+    std::vector<uint32_t> h;
+    h.swap(hist);
+    for (uint32_t t : h) append(t);
+  }
+  void append(uint32_t t) {
+    hist.push_back(t);
+    if (hist.size() >= 3) index(hist.size() - 1);
+  }
+  int propose(int maxK, uint32_t* out, int* match) {
+    *match = 0;
+    const size_t n = hist.size();
+    if (n < 4 || maxK <= 0) return 0;
+    const long s = find(key_at(n - 1));
+    if (s < 0) return 0;
+    const long cur = long(n) - 1;
+    long bestEnd = 0;
+    int bestLen = 0;
+    for (int w = 0; w < cnt[s]; ++w) {
+      const long p = pos[size_t(s) * WAYS + w];
+      if (p >= cur) continue;
+      int len = 0;
+      while (len < maxMatch && len <= p && hist[p - len] == hist[cur - len]) ++len;
+      if (len > bestLen) { bestLen = len; bestEnd = p; }
+    }
+    if (bestLen < minMatch) return 0;
+    *match = bestLen;
+    const long end = std::min(cur, bestEnd + maxK);
+    for (long i = bestEnd + 1; i <= end; ++i) out[i - bestEnd - 1] = hist[i];
+    return int(end - bestEnd);
+  }
+};
+
+void* or_copy_index_new(int capacity) {
+  auto* c = new OrCopyIndex();
+  c->allocate(size_t(capacity));
+  return c;
+}
+void or_copy_index_free(void* h) { delete static_cast<OrCopyIndex*>(h); }
+void or_copy_index_append(void* h, const uint32_t* toks, int n) {
+  for (int i = 0; i < n; ++i) static_cast<OrCopyIndex*>(h)->append(toks[i]);
+}
+int or_copy_index_propose(void* h, int maxK, uint32_t* out, int* match) {
+  return static_cast<OrCopyIndex*>(h)->propose(maxK, out, match);
+}
+
+// SplitMix64 output stream of `seed` (Sources/Ingot/Sampling.swift:50-62), for the reference's randomized tests.
+void or_splitmix64(uint64_t seed, int n, uint64_t* out) {
+  uint64_t s = seed;
+  for (int i = 0; i < n; ++i) {
+    s += 0x9E3779B97F4A7C15ull;
+    out[i] = sm_mix(s);
+  }
+}
+
 int or_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();
