@@ -14,28 +14,16 @@ __device__ __forceinline__ unsigned short dround_bf16(float f) {
   return (unsigned short)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
-// Writes one 8-value chunk c (values x[8c … 8c+7] of token `tok`, already final fp32) into the fragment layout as
-// bf16, and the 64-value group sums. The 8 chunks of a group must be held by 8 consecutive lanes (lane & 7 = c & 7),
-// all lanes of the wave calling together; `valid` false gives zeros.
-__device__ __forceinline__ void act_store_chunk(uint4* frag, float* xsum, int nkb, int tok, int c, const float (&v)[8],
-                                                bool valid, int max_tok) {
-  float r[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = valid ? dbf16(dround_bf16(v[e])) : 0.f;
-  float sum = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-  sum += __shfl_xor(sum, 1);
-  sum += __shfl_xor(sum, 2);
-  sum += __shfl_xor(sum, 4);
-  if (c < nkb * 16) {
-    const int kb = c >> 4, w = c & 15, t = w >> 2, qd = w & 3;
-    unsigned u[4];
-    u[0] = dround_bf16(r[0]) | (unsigned(dround_bf16(r[4])) << 16);
-    u[1] = dround_bf16(r[1]) | (unsigned(dround_bf16(r[5])) << 16);
-    u[2] = dround_bf16(r[2]) | (unsigned(dround_bf16(r[6])) << 16);
-    u[3] = dround_bf16(r[3]) | (unsigned(dround_bf16(r[7])) << 16);
-    frag[((size_t(tok) * nkb + kb) * 4 + qd) * 4 + t] = make_uint4(u[0], u[1], u[2], u[3]);
-    if ((c & 7) == 0) xsum[(c >> 3) * max_tok + tok] = sum;
-  }
+// Writes one 8-value chunk c (values x[8c … 8c+7] of token `tok`, final fp32) into the fragment layout as bf16.
+__device__ __forceinline__ void frag_store_chunk(uint4* frag, int nkb, int tok, int c, const float (&v)[8]) {
+  if (c >= nkb * 16) return;
+  const int kb = c >> 4, w = c & 15, t = w >> 2, qd = w & 3;
+  uint4 u;
+  u.x = dround_bf16(v[0]) | (unsigned(dround_bf16(v[4])) << 16);
+  u.y = dround_bf16(v[1]) | (unsigned(dround_bf16(v[5])) << 16);
+  u.z = dround_bf16(v[2]) | (unsigned(dround_bf16(v[6])) << 16);
+  u.w = dround_bf16(v[3]) | (unsigned(dround_bf16(v[7])) << 16);
+  frag[((size_t(tok) * nkb + kb) * 4 + qd) * 4 + t] = u;
 }
 
 // ---------------------------------------------------------------------------------------------------------------

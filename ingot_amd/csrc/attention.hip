@@ -287,13 +287,14 @@ __global__ __launch_bounds__(512) void attn_kernel(AttnArgs a) {
 // Reduction of the splits (vattn_reduce, verify_attn.metal:149-192): M = max over splits (and the sink), L = Σ e^(m−M)·l
 // (+ e^(sink−M)), o = Σ e^(m−M)·O / L, in split order; written into the o_proj activation layout (column h·HD + d).
 // Grid (B, QH·HD/512), 64 threads (one per 8 values).
-__global__ __launch_bounds__(64) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, float* __restrict__ xsum,
-                                                         int nkb) {
+__global__ __launch_bounds__(64) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb) {
   const int t = blockIdx.x, c = blockIdx.y * 64 + threadIdx.x, HD = a.HD;
   const int h = (8 * c) / HD, d0 = (8 * c) % HD;
   const int kvh = h / a.G, m = t * a.G + h % a.G;
+  const float2* mlh = a.ml + size_t(kvh) * a.nsplit * a.Qpad + m;
   float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.ml[(size_t(kvh) * a.nsplit + s) * a.Qpad + m].x);
+#pragma unroll 8
+  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, mlh[size_t(s) * a.Qpad].x);
   float L = 0.f;
   if (a.sinks) {
     const float sk = a.sinks[h] * 1.4426950408889634f;
@@ -303,14 +304,15 @@ __global__ __launch_bounds__(64) void attn_reduce_kernel(AttnArgs a, uint4* __re
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
+#pragma unroll 4
   for (int s = 0; s < a.nsplit; ++s) {
     const size_t idx = (size_t(kvh) * a.nsplit + s) * a.Qpad + m;
     const float2 v = a.ml[idx];
-    if (v.x == -INFINITY) continue;
-    const float w = exp2f(v.x - M);
-    L += w * v.y;
     const f32x4* src = reinterpret_cast<const f32x4*>(a.opart + idx * HD + d0);
     const f32x4 p0 = src[0], p1 = src[1];
+    // An empty split carries (−inf, 0) and a zero O: its weight is 0.
+    const float w = v.x == -INFINITY ? 0.f : exp2f(v.x - M);
+    L += w * v.y;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       o[e] += w * p0[e];
@@ -320,7 +322,7 @@ __global__ __launch_bounds__(64) void attn_reduce_kernel(AttnArgs a, uint4* __re
   const float inv = 1.0f / L;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] *= inv;
-  act_store_chunk(frag, xsum, nkb, t, c, o, true, MAX_TOK);
+  frag_store_chunk(frag, nkb, t, c, o);
 }
 
 int launch_prework(ih_ctx* c, const AttnArgs& a) {
@@ -353,7 +355,7 @@ int launch_attention(ih_ctx* c, const AttnArgs& a) {
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
   IH_CHECK((a.QH * a.HD) % 512 == 0, IH_EINVAL, "attention reduce: QH·HD must be a multiple of 512");
   TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (a.HD + 2) * 4 + double(a.B) * a.QH * a.HD * 2);
-  attn_reduce_kernel<<<dim3(a.B, a.QH * a.HD / 512), 64, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.xsum, out.nkb);
+  attn_reduce_kernel<<<dim3(a.B, a.QH * a.HD / 512), 64, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.nkb);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -64,11 +64,13 @@ constexpr int MAX_TOK = 32;     // tokens per qmm (two 16-token MFMA tiles)
 
 // Activations (the A operand of every qmm) use the "fragment" layout: for token i and K-block kb, 256 bytes ordered
 // [qd][t][8] where element e of (qd, t) is x[128kb + 32t + 8qd + perm(e)], perm = {0,4,1,5,2,6,3,7} (the order in
-// which one 32-bit word of nibbles turns into four bf16/fp16 pairs). Alongside, the per-group sums of the same
-// (rounded) values: xsum[g][token], fp32, for the affine correction Σ x·(base + q) → s·acc + (b − base·s)·Σx.
+// which one 32-bit word of nibbles turns into four bf16/fp16 pairs). An activation that is an RMSNorm input also
+// carries the sums of squares of its (unnormalised) rows as partials of the producer's workgroups, ss[j][token]:
+// the consumer adds them in order and applies the per-row factor in its epilogue.
 struct ActBuf {
   void* frag = nullptr;   // [MAX_TOK][nkb][64 B × 4] (bf16 or fp16 elements)
-  float* xsum = nullptr;  // [ngroups64][MAX_TOK]
+  float* ss = nullptr;    // [ss_cap][MAX_TOK]
+  int nss = 0, ss_cap = 0;
   int K = 0, nkb = 0;
   bool f16 = false;       // element type: fp16 (MXFP4 experts) or bf16 (everything else)
 };
@@ -86,6 +88,7 @@ struct ih_qmat {
   int Npad = 0;            // rows rounded up to the launch granule
   int nkb = 0;             // ceil(K / 128)
   int ktail = 0;           // 1 when K % 128 == 64 (int4) or K % 128 in {32,64,96} (mxfp4): last block is partial
+  int il8 = 0;             // gate|up rows interleaved by eights (see pack_int4_kernel)
   void* w = nullptr;       // packed words [E][Npad/16][nkb][64] uint4
   void* s = nullptr;       // int4: [E][Npad/16][nkb][16] uint2 (s0,b0,s1,b1 bf16); mxfp4: [E][Npad/16][nkb][16] u32
   size_t wbytes = 0, sbytes = 0;
@@ -137,13 +140,31 @@ int ensure_act(ih_ctx* c, ActBuf& a, int K, bool f16);
 void free_act(ActBuf& a);
 
 // Launchers (qmm.hip).
-enum QmmOut : int {
-  QO_F32 = 0,        // y[m][n] = v (fp32)
-  QO_F32_ADD = 1,    // y[m][n] += v (fp32 residual)
-  QO_BF16 = 2,       // y[m][n] = bf16(v)
+enum QmmMode : int {
+  QM_F32 = 0,         // y[m][n] = v (fp32)
+  QM_F32_ADD = 1,     // y[m][n] += v (fp32 residual)
+  QM_BF16 = 2,        // y[m][n] = bf16(v)
+  QM_F32_SCALE = 3,   // y[m][n] = r_m · v, r_m the RMSNorm factor of input row m
+  QM_RESID_ACT = 4,   // h[m][n] += v; next activation bf16(h ⊙ nw) + its sum-of-squares partials
+  QM_GLU_ACT = 5,     // gated activation of the interleaved gate|up pair (scaled by r_m) → next activation
+};
+constexpr int QO_F32 = QM_F32, QO_F32_ADD = QM_F32_ADD, QO_BF16 = QM_BF16;
+struct QmmEpilogue {
+  int mode = QM_F32;
+  void* y = nullptr;       // output (QM_F32*, QM_BF16) or the residual h (QM_RESID_ACT)
+  int ldy = 0;
+  float eps = 1e-6f;       // RMSNorm eps of the input (QM_F32_SCALE, QM_GLU_ACT)
+  const uint16_t* nw = nullptr;  // next RMSNorm weights (QM_RESID_ACT)
+  ActBuf* act_out = nullptr;     // next activation (QM_RESID_ACT, QM_GLU_ACT)
+  int glu = 0;
+  float limit = 7.0f;
 };
 int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a);
 int launch_act_from_f32(ih_ctx* c, const float* x, int ldx, int M, ActBuf& a);
 int launch_qmm(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, void* y, int ldy, int out_mode);
+int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, const QmmEpilogue& ep);
+int qmm_grid(const ih_qmat* W);
 int pack_int4(ih_ctx* c, ih_qmat* q, const uint32_t* w_dev, const uint16_t* s_dev, const uint16_t* b_dev);
+int qmat_int4_create_dev(ih_ctx* c, const void* w, const void* s, const void* b, int E, int N, int K, int il8,
+                         ih_qmat** out);
 }  // namespace ih

@@ -15,10 +15,8 @@
 namespace ih {
 
 // Launchers of the other translation units.
-int launch_embed(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* h,
-                 int B, int H, int ldh);
-int launch_rmsnorm_act(ih_ctx* c, const float* x, int ldx, const uint16_t* w, int rows, int D, float eps, ActBuf& a);
-int launch_glu_act(ih_ctx* c, const float* gu, int ldg, int rows, int I, int act, float limit, ActBuf& a);
+int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                     float* h, int B, int H, const uint16_t* nw, ActBuf& a);
 int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out);
 int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows);
 int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_t K, uint64_t seed, uint64_t tensor,
@@ -67,12 +65,13 @@ struct ih_model {
   // Scratch of one step.
   float* h = nullptr;        // residual [MAX_TOK][H]
   float* proj = nullptr;     // qkv output [MAX_TOK][QP]
-  float* gu = nullptr;       // gate|up output [MAX_TOK][2I]
   float* logits = nullptr;   // [MAX_TOK][V]
   uint32_t* tok = nullptr;   // [MAX_TOK]
   uint32_t* top1 = nullptr;  // [MAX_TOK]
   __half* q = nullptr;       // [KVH][Qpad][HD]
-  ActBuf act_h, act_o, act_i;
+  // Activations: RMSNorm inputs bf16(h ⊙ w) with their sums of squares (attention / final norm, FFN norm), the
+  // attention output and the gated activation.
+  ActBuf act_attn, act_mlp, act_o, act_i;
   float* opart = nullptr;
   float2* ml = nullptr;
   size_t part_splits = 0;    // splits the attention partials can hold
@@ -127,10 +126,11 @@ struct Staging {
   ~Staging() { release(); }
 };
 
-static int synth_qmat(ih_ctx* c, Staging& st, int N, int K, uint64_t seed, uint64_t tensor, float sd, ih_qmat** out) {
+static int synth_qmat(ih_ctx* c, Staging& st, int N, int K, uint64_t seed, uint64_t tensor, float sd, ih_qmat** out,
+                      int il8 = 0) {
   IH_TRY(st.reserve(N, K));
   IH_TRY(synth_int4(c, st.w, st.s, st.b, size_t(N), size_t(K), seed, tensor, sd));
-  return ih_qmat_int4_create_dev(c, st.w, st.s, st.b, 1, N, K, out);
+  return qmat_int4_create_dev(c, st.w, st.s, st.b, 1, N, K, il8, out);
 }
 
 static int check_desc(const ih_model_desc& d) {
@@ -141,6 +141,7 @@ static int check_desc(const ih_model_desc& d) {
   IH_CHECK(d.vocab >= 1 && d.rms_eps > 0 && d.rope_theta > 0, IH_EINVAL, "model: vocab, eps and theta must be positive");
   IH_CHECK(d.n_experts == 0, IH_EINVAL, "model: MoE layers are not available in this build yet");
   IH_CHECK(d.intermediate >= 64 && d.intermediate % 64 == 0, IH_EINVAL, "model: intermediate must be a multiple of 64");
+  IH_CHECK(d.act == 0 || d.act == 1, IH_EINVAL, "model: act must be 0 (SiLU) or 1 (swiglu_oai)");
   return IH_OK;
 }
 
@@ -153,11 +154,11 @@ static void model_release(ih_model* m) {
     if (L.sinks) (void)hipFree(L.sinks);
   }
   ih_qmat_free(m->head);
-  void* ptrs[] = {m->emb_w, m->emb_s, m->emb_b, m->final_norm, m->h, m->proj, m->gu, m->logits, m->tok, m->top1,
+  void* ptrs[] = {m->emb_w, m->emb_s, m->emb_b, m->final_norm, m->h, m->proj, m->logits, m->tok, m->top1,
                   m->q, m->opart, m->ml};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
-  free_act(m->act_h); free_act(m->act_o); free_act(m->act_i);
+  free_act(m->act_attn); free_act(m->act_mlp); free_act(m->act_o); free_act(m->act_i);
   delete m;
 }
 
@@ -178,13 +179,18 @@ static int run_step(ih_model* m, ih_kv* kv, int B) {
   ih_ctx* c = m->ctx;
   const auto& d = m->d;
   const int H = d.hidden, QH = d.n_q_heads, KVH = d.n_kv_heads, HD = d.head_dim, I = d.intermediate;
-  IH_TRY(launch_embed(c, m->tok, m->emb_w, m->emb_s, m->emb_b, m->h, B, H, H));
+  // The block's rows and the first RMSNorm input.
+  IH_TRY(launch_embed_act(c, m->tok, m->emb_w, m->emb_s, m->emb_b, m->h, B, H, m->layers[0].attn_norm, m->act_attn));
   const int total = kv->P + B;
   for (int l = 0; l < d.n_layers; ++l) {
     const ih_layer& L = m->layers[l];
-    // Attention.
-    IH_TRY(launch_rmsnorm_act(c, m->h, H, L.attn_norm, B, H, d.rms_eps, m->act_h));
-    IH_TRY(launch_qmm(c, L.qkv, 0, m->act_h, B, m->proj, m->QP, QO_F32));
+    // Attention: q|k|v = r · (bf16(h ⊙ w_attn) · Wqkvᵀ).
+    QmmEpilogue eq;
+    eq.mode = QM_F32_SCALE;
+    eq.y = m->proj;
+    eq.ldy = m->QP;
+    eq.eps = d.rms_eps;
+    IH_TRY(launch_qmm_ex(c, L.qkv, 0, m->act_attn, B, eq));
     AttnArgs a{};
     a.proj = m->proj;
     a.ldp = m->QP;
@@ -216,15 +222,37 @@ static int run_step(ih_model* m, ih_kv* kv, int B) {
     IH_TRY(launch_prework(c, a));
     IH_TRY(launch_attention(c, a));
     IH_TRY(launch_attn_reduce(c, a, m->act_o));
-    IH_TRY(launch_qmm(c, L.o, 0, m->act_o, B, m->h, H, QO_F32_ADD));
-    // FFN.
-    IH_TRY(launch_rmsnorm_act(c, m->h, H, L.mlp_norm, B, H, d.rms_eps, m->act_h));
-    IH_TRY(launch_qmm(c, L.gate_up, 0, m->act_h, B, m->gu, 2 * I, QO_F32));
-    IH_TRY(launch_glu_act(c, m->gu, 2 * I, B, I, d.act, d.swiglu_limit, m->act_i));
-    IH_TRY(launch_qmm(c, L.down, 0, m->act_i, B, m->h, H, QO_F32_ADD));
+    // h += o_proj(attention); the FFN's RMSNorm input.
+    QmmEpilogue eo;
+    eo.mode = QM_RESID_ACT;
+    eo.y = m->h;
+    eo.ldy = H;
+    eo.nw = L.mlp_norm;
+    eo.act_out = &m->act_mlp;
+    IH_TRY(launch_qmm_ex(c, L.o, 0, m->act_o, B, eo));
+    // Gated FFN: act(r · gate) · (r · up) straight into the down projection's activation.
+    QmmEpilogue eg;
+    eg.mode = QM_GLU_ACT;
+    eg.eps = d.rms_eps;
+    eg.act_out = &m->act_i;
+    eg.glu = d.act;
+    eg.limit = d.swiglu_limit;
+    IH_TRY(launch_qmm_ex(c, L.gate_up, 0, m->act_mlp, B, eg));
+    // h += down(·); the next layer's (or the final) RMSNorm input.
+    QmmEpilogue ed;
+    ed.mode = QM_RESID_ACT;
+    ed.y = m->h;
+    ed.ldy = H;
+    ed.nw = l + 1 < d.n_layers ? m->layers[l + 1].attn_norm : m->final_norm;
+    ed.act_out = &m->act_attn;
+    IH_TRY(launch_qmm_ex(c, L.down, 0, m->act_i, B, ed));
   }
-  IH_TRY(launch_rmsnorm_act(c, m->h, H, m->final_norm, B, H, d.rms_eps, m->act_h));
-  IH_TRY(launch_qmm(c, m->head, 0, m->act_h, B, m->logits, d.vocab, QO_F32));
+  QmmEpilogue eh;
+  eh.mode = QM_F32_SCALE;
+  eh.y = m->logits;
+  eh.ldy = d.vocab;
+  eh.eps = d.rms_eps;
+  IH_TRY(launch_qmm_ex(c, m->head, 0, m->act_attn, B, eh));
   IH_TRY(launch_argmax(c, m->logits, d.vocab, B, d.vocab, m->top1));
   kv->last_B = B;
   kv->written = std::max(kv->written, kv->P + B);
@@ -273,7 +301,7 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
       }
       run(synth_qmat(c, stg, m->QP, H, seed, layer_tensor(l, L_QKV), W_SD, &L.qkv));
       run(synth_qmat(c, stg, H, QH * HD, seed, layer_tensor(l, L_O), W_SD, &L.o));
-      run(synth_qmat(c, stg, 2 * I, H, seed, layer_tensor(l, L_GATE_UP), W_SD, &L.gate_up));
+      run(synth_qmat(c, stg, 2 * I, H, seed, layer_tensor(l, L_GATE_UP), W_SD, &L.gate_up, 1));
       run(synth_qmat(c, stg, H, I, seed, layer_tensor(l, L_DOWN), W_SD, &L.down));
     }
     run(synth_qmat(c, stg, V, H, seed, T_HEAD, W_SD, &m->head));
@@ -287,12 +315,12 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
   if (st == IH_OK) run(synth_bf16(c, m->final_norm, H, seed, T_FINAL_NORM, 1.0f, 0.125f));
   run(dalloc_t(&m->h, size_t(MAX_TOK) * H));
   run(dalloc_t(&m->proj, size_t(MAX_TOK) * m->QP));
-  run(dalloc_t(&m->gu, size_t(MAX_TOK) * 2 * I));
   run(dalloc_t(&m->logits, size_t(MAX_TOK) * V));
   run(dalloc_t(&m->tok, MAX_TOK));
   run(dalloc_t(&m->top1, MAX_TOK));
   run(dalloc_t(&m->q, size_t(KVH) * m->Qpad * HD));
-  if (st == IH_OK) run(ensure_act(c, m->act_h, H, false));
+  if (st == IH_OK) run(ensure_act(c, m->act_attn, H, false));
+  if (st == IH_OK) run(ensure_act(c, m->act_mlp, H, false));
   if (st == IH_OK) run(ensure_act(c, m->act_o, QH * HD, false));
   if (st == IH_OK) run(ensure_act(c, m->act_i, I, false));
   if (st == IH_OK) run(fill(c, m->q, 0, size_t(KVH) * m->Qpad * HD * 2));

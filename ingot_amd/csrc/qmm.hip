@@ -1,4 +1,5 @@
-// Few-row quantized matmul of the verify step on gfx950: Y[M ≤ 32, N] (+)= X[M, K] · dequant(W)ᵀ.
+// Few-row quantized matmul of the verify step on gfx950: Y[M ≤ 32, N] (+)= X[M, K] · dequant(W)ᵀ, with the epilogues
+// of the round fused in (RMSNorm scale, residual add, gated activation, next activation's layout).
 //
 // Reference: VQMV.encode → vnax_qmv_nf1_sg32 (Sources/Ingot/Layers/Linear.swift:263-445,
 // Sources/Ingot/Shaders/verify_nax.metal:102-176); the arithmetic it stands for is qmv_acc
@@ -6,14 +7,18 @@
 //
 // MI355X design (not a translation of the Metal kernel):
 //   - HBM-bound at M ≤ 17 (≈ 2·M / 0.5625 ≤ 60 FLOP/B). Each wave streams its weight tiles with one contiguous
-//     1024-byte dwordx4 load per 16×128 tile (layout in ih_internal.h) and dequantizes in registers.
+//     1024-byte dwordx4 buffer load per 16×128 tile (layout in ih_internal.h), the next K-block in flight while the
+//     current one is multiplied, and dequantizes in registers.
 //   - The products run on MFMA v_mfma_f32_16x16x32_bf16 with the tokens as the A operand (16 tokens × 32 K) and the
-//     weights as B (32 K × 16 rows). A nibble q becomes the bf16 128 + q with one and-or per pair
-//     ((w >> 4c) & 0x000F000F | 0x43004300), so the MFMA sums Σ x·(128 + q) exactly in fp32 per group of 64, and the
-//     affine map is applied once per group and output: y += s·acc + (b − 128·s)·Σx. No rounding of the dequantised
-//     weight (the reference rounds it to half); the only rounding is fp32 accumulation.
+//     weights as B (32 K × 16 rows). A nibble q becomes the bf16 128 + q with one v_and_or_b32 per pair
+//     ((w >> 4c) & 0x000F000F | 0x43004300), so the MFMA sums Σ x·(128 + q) exactly in fp32 per group of 64; one more
+//     MFMA against a ones operand gives Σ x per group and token in the same layout, and the affine map is applied
+//     once per group and output: y += s·acc + (b − 128·s)·Σx. No rounding of the dequantised weight.
+//   - Token 16 (the 17th row of a k = 16 block) runs on VALU packed bf16 dot products instead of a second, almost
+//     empty MFMA tile; its bits never depend on M.
 //   - K is split over the waves of a workgroup (a split chosen from (N, K) only, never from M) and the partial sums are
 //     added in wave order in LDS: deterministic and row-invariant (row r's bits do not depend on M).
+#include "act.h"
 #include "ih_internal.h"
 
 #include <cstdio>
@@ -22,6 +27,7 @@
 namespace ih {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
@@ -57,24 +63,29 @@ __device__ __forceinline__ bf16x8 nib_bf16(unsigned w, unsigned km, unsigned kb)
 
 // ---------------------------------------------------------------------------------------------------------------
 // Repack an MLX int4 g64 matrix ([E][N][K/8] words, [E][N][K/64] bf16 scales and biases) into the tile layout.
-// Grid (Npad/16 · nkb, E), 64 threads: lane L = 16·qd + n.
+// Grid (Npad/16 · nkb, E), 64 threads: lane L = 16·qd + n. With il8, rows are interleaved by eights for a gate|up pair
+// (N = 2I, gate rows 0…I−1, up rows I…2I−1): tile t holds gate rows 8t…8t+7 then up rows 8t…8t+7, so one tile's
+// outputs are the gate and up of the same 8 columns.
 __global__ void pack_int4_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
                                  const uint16_t* __restrict__ b, uint4* __restrict__ wp, uint2* __restrict__ sp, int N,
-                                 int K, int Npad, int nkb) {
+                                 int K, int Npad, int nkb, int il8) {
   const int lane = threadIdx.x, n = lane & 15, qd = lane >> 4;
   const int tile = blockIdx.x / nkb, kb = blockIdx.x % nkb, e = blockIdx.y;
-  const int row = tile * 16 + n, wpr = K / 8, gpr = K / 64;
+  const int prow = tile * 16 + n;
+  const int row = il8 ? (n < 8 ? 8 * tile + n : N / 2 + 8 * tile + n - 8) : prow;
+  const bool live = il8 ? (8 * tile + (n & 7) < N / 2) : row < N;
+  const int wpr = K / 8, gpr = K / 64;
   const size_t ebase_w = size_t(e) * N * wpr, ebase_s = size_t(e) * N * gpr;
   unsigned v[4];
   for (int t = 0; t < 4; ++t) {
     int wi = kb * 16 + 4 * t + qd;
-    v[t] = (row < N && wi < wpr) ? w[ebase_w + size_t(row) * wpr + wi] : 0u;
+    v[t] = (live && wi < wpr) ? w[ebase_w + size_t(row) * wpr + wi] : 0u;
   }
   const size_t tb = (size_t(e) * (Npad / 16) + tile) * nkb + kb;
   wp[tb * 64 + lane] = make_uint4(v[0], v[1], v[2], v[3]);
   if (qd == 0) {
     unsigned s0 = 0, b0 = 0, s1 = 0, b1 = 0;
-    if (row < N) {
+    if (live) {
       int g0 = 2 * kb, g1 = 2 * kb + 1;
       if (g0 < gpr) { s0 = s[ebase_s + size_t(row) * gpr + g0]; b0 = b[ebase_s + size_t(row) * gpr + g0]; }
       if (g1 < gpr) { s1 = s[ebase_s + size_t(row) * gpr + g1]; b1 = b[ebase_s + size_t(row) * gpr + g1]; }
@@ -84,41 +95,25 @@ __global__ void pack_int4_kernel(const uint32_t* __restrict__ w, const uint16_t*
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Natural-layout activations → fragment layout + per-group sums. Grid (MAX_TOK), 256 threads; one thread per 8
-// values. Rows ≥ M are written as zeros so every MFMA operand is finite.
+// Natural-layout activations → fragment layout. Grid (MAX_TOK), 256 threads; one thread per 8 values. Rows ≥ M are
+// written as zeros.
 template <typename TIn>
-__global__ void act_kernel(const TIn* __restrict__ x, int ldx, int M, int K, int nkb, uint4* __restrict__ frag,
-                           float* __restrict__ xsum) {
+__global__ void act_kernel(const TIn* __restrict__ x, int ldx, int M, int K, int nkb, uint4* __restrict__ frag) {
   const int i = blockIdx.x;
   const int nchunk = nkb * 16;
-  for (int c0 = 0; c0 < nchunk; c0 += blockDim.x) {
-    const int c = c0 + threadIdx.x;
+  for (int c = threadIdx.x; c < nchunk; c += blockDim.x) {
     float v[8];
-    for (int e = 0; e < 8; ++e) v[e] = 0.f;
-    if (i < M && c < K / 8) {
-      for (int e = 0; e < 8; ++e) {
-        float f;
+    const bool valid = i < M && c < K / 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float f = 0.f;
+      if (valid) {
         if constexpr (sizeof(TIn) == 2) f = bf16f(x[size_t(i) * ldx + 8 * c + e]);
-        else f = bf16f(f2bf(x[size_t(i) * ldx + 8 * c + e]));
-        v[e] = f;
+        else f = x[size_t(i) * ldx + 8 * c + e];
       }
+      v[e] = f;
     }
-    // Group sum (64 values = 8 threads), fixed order: own 8 values in order, then a butterfly over the 8 threads.
-    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
-    sum += __shfl_xor(sum, 4);
-    if (c < nchunk) {
-      const int kb = c / 16, w = c % 16, t = w / 4, qd = w % 4;
-      const int pe[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-      unsigned u[4];
-      for (int j = 0; j < 4; ++j) {
-        unsigned lo = f2bf(v[pe[2 * j]]), hi = f2bf(v[pe[2 * j + 1]]);
-        u[j] = lo | (hi << 16);
-      }
-      frag[((size_t(i) * nkb + kb) * 4 + qd) * 4 + t] = make_uint4(u[0], u[1], u[2], u[3]);
-      if ((c & 7) == 0) xsum[(c / 8) * MAX_TOK + i] = sum;
-    }
+    frag_store_chunk(frag, nkb, i, c, v);
   }
 }
 
@@ -127,12 +122,24 @@ struct QmmParams {
   const uint4* w;          // packed words of the expert
   const uint2* s;          // packed scale/bias of the expert
   const uint4* xa;         // activation fragments
-  const float* xs;         // activation group sums [2·nkb][MAX_TOK]
   void* y;
-  int ldy, M, N, Npad, nkb, out_mode;
+  int ldy, M, N, Npad, nkb, mode;
   // The nibble-decode constants 0x000F000F and 0x43004300, passed as arguments so that they live in SGPRs and the
   // compiler can use the three-operand v_and_or_b32 (gfx9 VOP3 takes no literal constants).
   unsigned kmask, kbias;
+  // RMSNorm factor of the input rows (modes QM_F32_SCALE, QM_GLU_ACT): r_t = 1/sqrt(Σ ss_in[j][t] / D + eps).
+  const float* ss_in;
+  int nss_in, D;
+  float eps;
+  // QM_RESID_ACT: h[m][n] += v (fp32, the y pointer), then the next activation bf16(h ⊙ nw) and the sum-of-squares
+  // partial of this workgroup's columns, ss_out[blockIdx.x][t].
+  const uint16_t* nw;
+  uint4* act_out;
+  int act_nkb;
+  float* ss_out;
+  // QM_GLU_ACT: gated activation kind and clip.
+  int glu;
+  float limit;
 };
 
 // Buffer resources (base in SGPRs, 32-bit offsets; an offset past num_records reads as zero).
@@ -141,34 +148,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, unsig
 }
 constexpr unsigned OOB = 0x80000000u;  // offset that reads as zero
 
-__device__ __forceinline__ void qmm_store(const QmmParams& p, int m, int row, float v) {
-  if (p.out_mode == QO_F32) {
-    static_cast<float*>(p.y)[size_t(m) * p.ldy + row] = v;
-  } else if (p.out_mode == QO_F32_ADD) {
-    float* o = static_cast<float*>(p.y) + size_t(m) * p.ldy + row;
-    *o = *o + v;
-  } else {
-    static_cast<unsigned short*>(p.y)[size_t(m) * p.ldy + row] = f2bf(v);
-  }
-}
-
-// One K-block's operands of a wave: R weight tiles (+ scale/bias) and the T token tiles of x (+ group sums).
+// One K-block's operands of a wave: R weight tiles (+ scale/bias) and the token tiles of x.
 template <int T, int R, bool X16>
 struct QmmStage {
   u32x4 w[R];
   uint2 sb[R];
   u32x4 x[T][4];
-  f32x4 xs[T][2];
   u32x4 x16[X16 ? 4 : 1];   // token 16 (VALU path): this lane's 64 bytes of it
-  float xs16[2];
 };
 
-// Buffer resources of one launch and the per-lane offsets that do not change along K.
 struct QmmRsrc {
-  __amdgpu_buffer_rsrc_t w, s, x, xs;
+  __amdgpu_buffer_rsrc_t w, s, x;
   unsigned xoff[2];   // token row offset of this lane's A operand (OOB for dead tokens), per token tile
-  unsigned xsoff[2];  // group-sum offset of this lane's 4 output tokens (OOB if none live)
-  unsigned x16off, xs16off;
+  unsigned x16off;
 };
 
 template <int T, int R, bool X16>
@@ -180,33 +172,48 @@ __device__ __forceinline__ void qmm_load(QmmStage<T, R, X16>& st, const QmmParam
     st.w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, tb * 1024u + lane * 16u, 0, 0));
     st.sb[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.s, tb * 128u + n * 8u, 0, 0));
   }
-  const unsigned kx = unsigned(kb) * 256u, kxs = unsigned(kb) * (2 * MAX_TOK * 4);
+  const unsigned kx = unsigned(kb) * 256u;
 #pragma unroll
-  for (int tt = 0; tt < T; ++tt) {
-    // Dead token lanes point past the buffer and read zeros (their MFMA outputs are discarded).
+  for (int tt = 0; tt < T; ++tt)
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       st.x[tt][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, rs.xoff[tt] + kx + 16 * t, 0, 0));
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-      st.xs[tt][g] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.xs, rs.xsoff[tt] + kxs + g * (MAX_TOK * 4), 0, 0));
-  }
   if constexpr (X16) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       st.x16[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, rs.x16off + kx + 16 * t, 0, 0));
-    st.xs16[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.xs, rs.xs16off + kxs, 0, 0));
-    st.xs16[1] = __builtin_bit_cast(float,
-                                    __builtin_amdgcn_raw_buffer_load_b32(rs.xs, rs.xs16off + kxs + MAX_TOK * 4, 0, 0));
   }
 }
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
 template <int T, int R, bool X16>
 __device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R], const QmmStage<T, R, X16>& st,
-                                            float qd0, unsigned km, unsigned kbias) {
+                                            unsigned km, unsigned kbias, float qd0) {
+  // Σx per group and token (ones operand), in the D layout of the products: lane (n, qd) gets tokens 4qd … 4qd+3.
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  f32x4 xs[T][2];
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g]), ones,
+                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      xs[tt][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), ones, z, 0,
+                                                          0, 0);
+    }
+  // Token 16: Σx per group. Every lane holds token 16's fragment of its K slice (the same for all 16 row lanes), so the
+  // ones MFMA over it gives the whole group's sum in every output element; the qd = 0 lanes add the bias term once.
+  // (A v_dot2c chain against a (1, 1) pair was miscompiled here: LLVM reused one source register for the four
+  // elements of the vector.)
+  float xs16[2] = {0.f, 0.f};
+  if constexpr (X16) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g]), ones,
+                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g + 1]), ones, z, 0, 0, 0);
+      xs16[g] = z[0] * qd0;
+    }
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float s0 = bf16f(st.sb[r].x & 0xFFFFu), s1 = bf16f(st.sb[r].y & 0xFFFFu);
@@ -222,12 +229,9 @@ __device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R
         tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), w1, tmp, 0,
                                                       0, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[r][tt][e] = fmaf(sg, tmp[e], fmaf(cg, st.xs[tt][g][e], acc[r][tt][e]));
+        for (int e = 0; e < 4; ++e) acc[r][tt][e] = fmaf(sg, tmp[e], fmaf(cg, xs[tt][g][e], acc[r][tt][e]));
       }
       if constexpr (X16) {
-        // Token 16 by packed bf16 dot products: this lane's 16 values of the group (its row n, K slice qd); the
-        // group's bias term is added by the qd = 0 lanes only (qd0 = 1 there, 0 elsewhere), the four K slices are
-        // summed across lanes at the end.
         float d = 0.f;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -240,23 +244,29 @@ __device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R
                                                 false);
           }
         }
-        acc16[r] = fmaf(sg, d, fmaf(cg * qd0, st.xs16[g], acc16[r]));
+        acc16[r] = fmaf(sg, d, fmaf(cg, xs16[g], acc16[r]));
       }
     }
   }
 }
 
+__device__ __forceinline__ float glu_f(float g, float u, int act, float limit) {
+  if (act == 0) return g / (1.0f + expf(-g)) * u;
+  const float gc = fminf(g, limit), uc = fminf(fmaxf(u, -limit), limit);
+  return gc / (1.0f + expf(-1.702f * gc)) * (uc + 1.0f);
+}
+
+// T: MFMA token tiles (tokens 0–15, and 17–31 when T = 2); X16: token 16 present (M ≥ 17), done on VALU.
 // Workgroup = KW waves over the same 16·R rows; wave w takes K-blocks w, w + KW, … (adjacent waves read adjacent
 // 1 KB blocks), with the next block's loads in flight while the current one is multiplied. The KW partial sums are
 // added in wave order through LDS: no cross-workgroup synchronisation (an agent-scope fence on MI355X writes the
 // XCD's L2 back and costs tens of µs) and a summation order that depends only on (N, K).
-// T: MFMA token tiles (tokens 0–15, and 17–31 when T = 2); X16: token 16 present (M ≥ 17), done on VALU.
 template <int T, int R, int KW, bool X16>
 __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, qd = lane >> 4;
   const int tile0 = blockIdx.x * R;
-  const float qd0 = qd == 0 ? 1.f : 0.f;
+  __shared__ float rsc[MAX_TOK];
   f32x4 acc[R][T];
   float acc16[R];
 #pragma unroll
@@ -271,35 +281,47 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   rs.w = make_rsrc(p.w, tiles_total * 1024u);
   rs.s = make_rsrc(p.s, tiles_total * 128u);
   rs.x = make_rsrc(p.xa, unsigned(MAX_TOK) * p.nkb * 256u);
-  rs.xs = make_rsrc(p.xs, unsigned(2 * p.nkb) * MAX_TOK * 4u);
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int tok = 16 * tt + n;
     const bool live = tt < T && tok < p.M && !(X16 && tok == 16);
     rs.xoff[tt] = live ? (unsigned(tok) * p.nkb * 256u + qd * 64u) : OOB;
-    rs.xsoff[tt] = (tt < T && 16 * tt + 4 * qd < p.M) ? unsigned(16 * tt + 4 * qd) * 4u : OOB;
   }
   rs.x16off = 16u * p.nkb * 256u + qd * 64u;
-  rs.xs16off = 16u * 4u;
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
+  const float qd0 = qd == 0 ? 1.f : 0.f;
 
   QmmStage<T, R, X16> a, b;
   int kb = wave;
+  if (kb < p.nkb) qmm_load(a, p, rs, tile0, kb, lane, n);
+
+  // RMSNorm factors of the input rows (the norm's sums of squares come in as partials of the producer's workgroups,
+  // added here in a fixed order), while the first loads are in flight.
+  // Wave w takes tokens w, w + KW, …; lane l adds partials l, l + 64, … and the lanes are combined by a fixed
+  // butterfly, so a token's factor does not depend on M or on the launch shape.
+  if (p.ss_in) {
+    for (int t = wave; t < p.M; t += KW) {
+      float ss = 0.f;
+      for (int j = lane; j < p.nss_in; j += 64) ss += p.ss_in[j * MAX_TOK + t];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+      if (lane == 0) rsc[t] = 1.0f / sqrtf(ss / float(p.D) + p.eps);
+    }
+  }
+
   if (kb < p.nkb) {
-    qmm_load(a, p, rs, tile0, kb, lane, n);
     while (true) {
       if (kb + KW < p.nkb) qmm_load(b, p, rs, tile0, kb + KW, lane, n);
-      qmm_compute(acc, acc16, a, qd0, km, kbias);
+      qmm_compute(acc, acc16, a, km, kbias, qd0);
       kb += KW;
       if (kb >= p.nkb) break;
       if (kb + KW < p.nkb) qmm_load(a, p, rs, tile0, kb + KW, lane, n);
-      qmm_compute(acc, acc16, b, qd0, km, kbias);
+      qmm_compute(acc, acc16, b, km, kbias, qd0);
       kb += KW;
       if (kb >= p.nkb) break;
     }
   }
 
-  // Partial sums of every wave → LDS [wave][r][tt][e][lane], then a fixed-order sum over the waves.
   // Token 16: sum the four K slices of each row across lanes (qd = lane bits 4–5), fixed order.
   if constexpr (X16) {
 #pragma unroll
@@ -308,51 +330,99 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       acc16[r] += __shfl_xor(acc16[r], 32);
     }
   }
+  // Partial sums of every wave → LDS [wave][r][tt][e][lane] (+ token 16 [wave][r][row]), then fixed-order sums.
   constexpr int NEL = R * T * 4 * 64;
   constexpr int NEL16 = X16 ? R * 16 : 0;
-  __shared__ float red[KW * (NEL + NEL16)];
+  constexpr int WST = NEL + NEL16;
+  __shared__ float red[KW * WST];
+  __shared__ float ssu[MAX_TOK * 8];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int tt = 0; tt < T; ++tt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) red[wave * (NEL + NEL16) + ((r * T + tt) * 4 + e) * 64 + lane] = acc[r][tt][e];
+      for (int e = 0; e < 4; ++e) red[wave * WST + ((r * T + tt) * 4 + e) * 64 + lane] = acc[r][tt][e];
   if constexpr (X16) {
     if (lane < 16) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) red[wave * (NEL + NEL16) + NEL + r * 16 + lane] = acc16[r];
+      for (int r = 0; r < R; ++r) red[wave * WST + NEL + r * 16 + lane] = acc16[r];
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < NEL + NEL16; i += 64 * KW) {
-    int m, row;
-    if (i < NEL) {
-      const int l = i & 63, e = (i >> 6) & 3, tt = (i >> 8) % T, r = (i >> 8) / T;
-      m = 16 * tt + 4 * (l >> 4) + e;
-      row = (tile0 + r) * 16 + (l & 15);
-      if (X16 && m == 16) continue;
+  // Sum over waves of output (token m, tile r, row rn of the tile).
+  auto val = [&](int m, int r, int rn) -> float {
+    int i;
+    if (X16 && m == 16) {
+      i = NEL + r * 16 + rn;
     } else {
-      m = 16;
-      row = tile0 * 16 + (i - NEL);
+      const int tt = m >> 4, mm = m & 15;
+      i = ((r * T + tt) * 4 + (mm & 3)) * 64 + 16 * (mm >> 2) + rn;
     }
-    if (m >= p.M || row >= p.N) continue;
     float v = red[i];
 #pragma unroll
-    for (int w = 1; w < KW; ++w) v += red[w * (NEL + NEL16) + i];
-    qmm_store(p, m, row, v);
+    for (int w = 1; w < KW; ++w) v += red[w * WST + i];
+    return v;
+  };
+
+  const int nthr = 64 * KW;
+  if (p.mode == QM_RESID_ACT) {
+    // h += v for this workgroup's 16R columns, the next activation bf16(h ⊙ nw) in 8-column chunks, and Σh² per token.
+    const int nch = 2 * R;
+    for (int u = threadIdx.x; u < p.M * nch; u += nthr) {
+      const int m = u / nch, cl = u % nch, r = cl >> 1, half = cl & 1;
+      const int col0 = (tile0 + r) * 16 + 8 * half;
+      float v[8], ss = 0.f;
+      float* hrow = static_cast<float*>(p.y) + size_t(m) * p.ldy;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int col = col0 + j;
+        float hv = 0.f;
+        if (col < p.N) {
+          hv = hrow[col] + val(m, r, 8 * half + j);
+          hrow[col] = hv;
+        }
+        ss += hv * hv;
+        v[j] = col < p.N ? hv * bf16f(p.nw[col]) : 0.f;
+      }
+      ssu[m * 8 + cl] = ss;
+      if (col0 < p.N) frag_store_chunk(p.act_out, p.act_nkb, m, col0 / 8, v);
+    }
+    __syncthreads();
+    if (threadIdx.x < p.M) {
+      float ss = 0.f;
+      for (int cl = 0; cl < nch; ++cl) ss += ssu[threadIdx.x * 8 + cl];
+      p.ss_out[blockIdx.x * MAX_TOK + threadIdx.x] = ss;
+    }
+    return;
   }
-}
-
-int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
-  act_kernel<uint16_t><<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, a.K, a.nkb, static_cast<uint4*>(a.frag), a.xsum);
-  IH_HIP(hipGetLastError());
-  return IH_OK;
-}
-
-int launch_act_from_f32(ih_ctx* c, const float* x, int ldx, int M, ActBuf& a) {
-  act_kernel<float><<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, a.K, a.nkb, static_cast<uint4*>(a.frag), a.xsum);
-  IH_HIP(hipGetLastError());
-  return IH_OK;
+  if (p.mode == QM_GLU_ACT) {
+    // Interleaved gate|up tiles: rows 0–7 gate, 8–15 up of the same 8 columns (chunk tile0 + r of the output).
+    for (int u = threadIdx.x; u < p.M * R; u += nthr) {
+      const int m = u / R, r = u % R;
+      const float rs_ = rsc[m];
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = glu_f(val(m, r, j) * rs_, val(m, r, 8 + j) * rs_, p.glu, p.limit);
+      const int chunk = tile0 + r;
+      if (chunk * 8 < p.N / 2) frag_store_chunk(p.act_out, p.act_nkb, m, chunk, v);
+    }
+    return;
+  }
+  for (int u = threadIdx.x; u < p.M * 16 * R; u += nthr) {
+    const int m = u / (16 * R), rr = u % (16 * R), r = rr >> 4, rn = rr & 15;
+    const int row = (tile0 + r) * 16 + rn;
+    if (row >= p.N) continue;
+    float v = val(m, r, rn);
+    if (p.mode == QM_F32_SCALE) v *= rsc[m];
+    if (p.mode == QM_BF16) {
+      static_cast<unsigned short*>(p.y)[size_t(m) * p.ldy + row] = f2bf(v);
+    } else if (p.mode == QM_F32_ADD) {
+      float* o = static_cast<float*>(p.y) + size_t(m) * p.ldy + row;
+      *o = *o + v;
+    } else {
+      static_cast<float*>(p.y)[size_t(m) * p.ldy + row] = v;
+    }
+  }
 }
 
 // Launch shape for an (Npad, nkb) matrix: rows per workgroup (16·R) and waves per workgroup (KW, the intra-workgroup
@@ -376,36 +446,86 @@ static void qmm_dispatch(QmmShape sh, int grid, hipStream_t st, const QmmParams&
   else qmm_int4_kernel<T, 1, 16, X16><<<grid, 1024, 0, st>>>(p);
 }
 
-int launch_qmm(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, void* y, int ldy, int out_mode) {
+int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
+  act_kernel<uint16_t><<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, a.K, a.nkb, static_cast<uint4*>(a.frag));
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int launch_act_from_f32(ih_ctx* c, const float* x, int ldx, int M, ActBuf& a) {
+  act_kernel<float><<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, a.K, a.nkb, static_cast<uint4*>(a.frag));
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int qmm_grid(const ih_qmat* W) {
+  const QmmShape sh = qmm_shape(W->Npad, W->nkb);
+  return W->Npad / (16 * sh.R);
+}
+
+int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, const QmmEpilogue& ep) {
   IH_CHECK(W->format == QF_INT4, IH_EINVAL, "qmm: int4 matrix expected");
   IH_CHECK(M >= 1 && M <= MAX_TOK, IH_EINVAL, "qmm: M must be in 1..32");
   IH_CHECK(a.nkb == W->nkb && !a.f16, IH_EINVAL, "qmm: activation K does not match the matrix");
   QmmShape sh = qmm_shape(W->Npad, W->nkb);
   if (const char* ov = getenv("IH_QMM_SHAPE")) sscanf(ov, "%d,%d", &sh.R, &sh.KW);  // tuning override
-  QmmParams p;
+  QmmParams p{};
   const size_t tiles_per_e = size_t(W->Npad / 16) * W->nkb;
   p.w = static_cast<const uint4*>(W->w) + tiles_per_e * 64 * expert;
   p.s = static_cast<const uint2*>(W->s) + tiles_per_e * 16 * expert;
   p.xa = static_cast<const uint4*>(a.frag);
-  p.xs = a.xsum;
-  p.y = y;
-  p.ldy = ldy;
+  p.y = ep.y;
+  p.ldy = ep.ldy;
   p.M = M;
   p.N = W->N;
   p.Npad = W->Npad;
   p.nkb = W->nkb;
-  p.out_mode = out_mode;
+  p.mode = ep.mode;
   p.kmask = 0x000F000Fu;
   p.kbias = 0x43004300u;
+  if (ep.mode == QM_F32_SCALE || ep.mode == QM_GLU_ACT) {
+    IH_CHECK(a.ss && a.nss > 0, IH_EINVAL, "qmm: the input activation carries no RMSNorm sums");
+    p.ss_in = a.ss;
+    p.nss_in = a.nss;
+    p.D = a.K;
+    p.eps = ep.eps;
+  }
   const int grid = W->Npad / (16 * sh.R);
+  if (ep.mode == QM_RESID_ACT) {
+    IH_CHECK(ep.act_out && ep.act_out->nkb * KBLK >= W->N && ep.nw, IH_EINVAL, "qmm: residual epilogue needs an output");
+    IH_CHECK(grid <= ep.act_out->ss_cap, IH_EINVAL, "qmm: too many workgroups for the RMSNorm partials");
+    IH_CHECK(2 * sh.R <= 8, IH_EINVAL, "qmm: residual epilogue supports R ≤ 4");
+    p.nw = ep.nw;
+    p.act_out = static_cast<uint4*>(ep.act_out->frag);
+    p.act_nkb = ep.act_out->nkb;
+    p.ss_out = ep.act_out->ss;
+    ep.act_out->nss = grid;
+  }
+  if (ep.mode == QM_GLU_ACT) {
+    IH_CHECK(ep.act_out && ep.act_out->nkb * KBLK >= W->N / 2 && W->il8, IH_EINVAL,
+             "qmm: gated epilogue needs an interleaved gate|up matrix and an output");
+    p.act_out = static_cast<uint4*>(ep.act_out->frag);
+    p.act_nkb = ep.act_out->nkb;
+    p.glu = ep.glu;
+    p.limit = ep.limit;
+  }
   // Algorithmic bytes: the matrix in its MLX format, x (bf16) read, y written (read too when accumulating).
-  const double ybytes = double(M) * W->N * (out_mode == QO_BF16 ? 2 : (out_mode == QO_F32_ADD ? 8 : 4));
+  const double ybytes = double(M) * W->N *
+                        (ep.mode == QM_BF16 ? 2 : (ep.mode == QM_F32_ADD || ep.mode == QM_RESID_ACT ? 8 : 4));
   TimedLaunch tl(c, TC_QMM, double(W->algo_bytes) + double(M) * W->K * 2 + ybytes);
   if (M > 17) qmm_dispatch<2, true>(sh, grid, c->stream, p);
   else if (M == 17) qmm_dispatch<1, true>(sh, grid, c->stream, p);
   else qmm_dispatch<1, false>(sh, grid, c->stream, p);
   IH_HIP(hipGetLastError());
   return IH_OK;
+}
+
+int launch_qmm(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, void* y, int ldy, int out_mode) {
+  QmmEpilogue ep;
+  ep.mode = out_mode;
+  ep.y = y;
+  ep.ldy = ldy;
+  return launch_qmm_ex(c, W, expert, a, M, ep);
 }
 
 static int qmat_alloc(ih_ctx* c, ih_qmat* q) {
@@ -420,7 +540,7 @@ static int qmat_alloc(ih_ctx* c, ih_qmat* q) {
 int pack_int4(ih_ctx* c, ih_qmat* q, const uint32_t* w, const uint16_t* s, const uint16_t* b) {
   dim3 grid((q->Npad / 16) * q->nkb, q->E);
   pack_int4_kernel<<<grid, 64, 0, c->stream>>>(w, s, b, static_cast<uint4*>(q->w), static_cast<uint2*>(q->s), q->N,
-                                               q->K, q->Npad, q->nkb);
+                                               q->K, q->Npad, q->nkb, q->il8);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
@@ -439,19 +559,15 @@ static ih_qmat* new_qmat_int4(ih_ctx* c, int E, int N, int K) {
   return q;
 }
 
-}  // namespace ih
-
-using namespace ih;
-
-extern "C" {
-
-int ih_qmat_int4_create_dev(ih_ctx* c, const void* w, const void* s, const void* b, int E, int N, int K,
-                            ih_qmat** out) {
+int qmat_int4_create_dev(ih_ctx* c, const void* w, const void* s, const void* b, int E, int N, int K, int il8,
+                         ih_qmat** out) {
   IH_CHECK(c && w && s && b && out, IH_EINVAL, "ih_qmat_int4_create_dev: null argument");
   IH_CHECK(E >= 1 && N >= 1 && K >= 64 && K % 64 == 0, IH_EINVAL,
            "ih_qmat_int4_create_dev: need E, N >= 1 and K a positive multiple of 64");
+  IH_CHECK(!il8 || N % 16 == 0, IH_EINVAL, "qmat: an interleaved gate|up matrix needs N a multiple of 16");
   *out = nullptr;
   ih_qmat* q = new_qmat_int4(c, E, N, K);
+  q->il8 = il8;
   int st = qmat_alloc(c, q);
   if (st == IH_OK) st = pack_int4(c, q, static_cast<const uint32_t*>(w), static_cast<const uint16_t*>(s),
                                   static_cast<const uint16_t*>(b));
@@ -461,6 +577,17 @@ int ih_qmat_int4_create_dev(ih_ctx* c, const void* w, const void* s, const void*
   }
   *out = q;
   return IH_OK;
+}
+
+}  // namespace ih
+
+using namespace ih;
+
+extern "C" {
+
+int ih_qmat_int4_create_dev(ih_ctx* c, const void* w, const void* s, const void* b, int E, int N, int K,
+                            ih_qmat** out) {
+  return qmat_int4_create_dev(c, w, s, b, E, N, K, 0, out);
 }
 
 int ih_qmat_int4_create(ih_ctx* c, const uint32_t* w, const uint16_t* s, const uint16_t* b, int E, int N, int K,

@@ -6,81 +6,37 @@
 namespace ih {
 
 // ---------------------------------------------------------------------------------------------------------------
-// Embedding: h[r] = dequant(table[tok[r]]) in fp32 (MLX int4 g64 row). embed_rows, Shaders/yy_model.metal:12-49.
-__global__ void embed_kernel(const uint32_t* __restrict__ tok, const uint32_t* __restrict__ w,
-                             const uint16_t* __restrict__ s, const uint16_t* __restrict__ b, float* __restrict__ h,
-                             int H, int ldh) {
-  const uint32_t t = tok[blockIdx.x];
+// Embedding of the block's rows: h[r] = dequant(table[tok[r]]) in fp32 (MLX int4 g64 row; embed_rows,
+// Shaders/yy_model.metal:12-49), and the first layer's RMSNorm input: the activation bf16(h ⊙ w) and Σh² per row
+// (one partial). Grid (rows), 256 threads; one thread per 8 values.
+__global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restrict__ tok, const uint32_t* __restrict__ w,
+                                                        const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
+                                                        float* __restrict__ h, int H, int ldh,
+                                                        const uint16_t* __restrict__ nw, uint4* __restrict__ frag,
+                                                        int nkb, float* __restrict__ ss_out) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const uint32_t t = tok[row];
   const uint32_t* wr = w + size_t(t) * (H / 8);
-  for (int i = threadIdx.x; i < H / 8; i += blockDim.x) {
-    const uint32_t word = wr[i];
-    const size_t g = size_t(t) * (H / 64) + (i * 8) / 64;
-    const float sc = dbf16(s[g]), bi = dbf16(b[g]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) h[size_t(blockIdx.x) * ldh + 8 * i + j] = sc * float((word >> (4 * j)) & 15u) + bi;
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// Block-wide sum in a fixed order (wave partials in LDS, added in wave order).
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int i = 0; i < nw; ++i) t += red[i];
-  return t;
-}
-
-// RMSNorm of fp32 rows into the activation layout: x·rsqrt(mean x² + eps)·w, rounded to bf16.
-// rmsnorm_rows, Shaders/verify.metal:501-523 (which writes half; this build's activations are bf16).
-// Grid (rows), 256 threads; one thread per 8-value chunk.
-__global__ __launch_bounds__(256) void rmsnorm_act_kernel(const float* __restrict__ x, int ldx,
-                                                          const uint16_t* __restrict__ w, int D, float eps,
-                                                          uint4* __restrict__ frag, float* __restrict__ xsum, int nkb) {
-  __shared__ float red[8];
-  const int row = blockIdx.x;
-  const float* xr = x + size_t(row) * ldx;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < D; i += blockDim.x) ss += xr[i] * xr[i];
-  const float tot = block_sum(ss, red);
-  const float r = 1.0f / sqrtf(tot / float(D) + eps);
-  const int nchunk = nkb * 16;
-  for (int c0 = 0; c0 < nchunk; c0 += blockDim.x) {
-    const int c = c0 + threadIdx.x;
+  for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
+    const uint32_t word = wr[c];
+    const size_t g = size_t(t) * (H / 64) + c / 8;
+    const float sc = dbf16(s[g]), bi = dbf16(b[g]);
     float v[8];
-    const bool valid = c < D / 8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = valid ? xr[8 * c + e] * r * dbf16(w[8 * c + e]) : 0.f;
-    act_store_chunk(frag, xsum, nkb, row, c, v, valid, MAX_TOK);
+    for (int j = 0; j < 8; ++j) {
+      const float x = sc * float((word >> (4 * j)) & 15u) + bi;
+      h[size_t(row) * ldh + 8 * c + j] = x;
+      ss += x * x;
+      v[j] = x * dbf16(nw[8 * c + j]);
+    }
+    frag_store_chunk(frag, nkb, row, c, v);
   }
-}
-
-// Gated activation of gate|up (fp32 [rows, 2I]: gate in columns 0…I−1, up in I…2I−1) into the activation layout.
-// act 0: SiLU(g)·u = g / (1 + e^−g) · u; act 1: swiglu_oai, (clip(u, ±limit) + 1) · g·σ(1.702·g) with g = min(gate,
-// limit). lab_glu, Shaders/qmm.metal:18-30; dswiglu, Shaders/yy_model.metal:187-199.
-__device__ __forceinline__ float glu(float g, float u, int act, float limit) {
-  if (act == 0) return g / (1.0f + expf(-g)) * u;
-  const float gc = fminf(g, limit), uc = fminf(fmaxf(u, -limit), limit);
-  return gc / (1.0f + expf(-1.702f * gc)) * (uc + 1.0f);
-}
-
-__global__ __launch_bounds__(256) void glu_act_kernel(const float* __restrict__ gu, int ldg, int I, int act,
-                                                      float limit, uint4* __restrict__ frag, float* __restrict__ xsum,
-                                                      int nkb) {
-  const int row = blockIdx.x;
-  const float* gr = gu + size_t(row) * ldg;
-  const int nchunk = nkb * 16;
-  for (int c0 = 0; c0 < nchunk; c0 += blockDim.x) {
-    const int c = c0 + threadIdx.x;
-    float v[8];
-    const bool valid = c < I / 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = valid ? glu(gr[8 * c + e], gr[I + 8 * c + e], act, limit) : 0.f;
-    act_store_chunk(frag, xsum, nkb, row, c, v, valid, MAX_TOK);
-  }
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  if (threadIdx.x == 0) ss_out[row] = ((red[0] + red[1]) + (red[2] + red[3]));
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -140,25 +96,12 @@ __global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-int launch_embed(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* h,
-                 int B, int H, int ldh) {
-  TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4));
-  embed_kernel<<<B, 256, 0, c->stream>>>(tok, w, s, b, h, H, ldh);
+int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                     float* h, int B, int H, const uint16_t* nw, ActBuf& a) {
+  TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4 + 2));
+  embed_act_kernel<<<B, 256, 0, c->stream>>>(tok, w, s, b, h, H, H, nw, static_cast<uint4*>(a.frag), a.nkb, a.ss);
   IH_HIP(hipGetLastError());
-  return IH_OK;
-}
-
-int launch_rmsnorm_act(ih_ctx* c, const float* x, int ldx, const uint16_t* w, int rows, int D, float eps, ActBuf& a) {
-  TimedLaunch tl(c, TC_ROWS, double(rows) * D * (4 + 2) + D * 2);
-  rmsnorm_act_kernel<<<rows, 256, 0, c->stream>>>(x, ldx, w, D, eps, static_cast<uint4*>(a.frag), a.xsum, a.nkb);
-  IH_HIP(hipGetLastError());
-  return IH_OK;
-}
-
-int launch_glu_act(ih_ctx* c, const float* gu, int ldg, int rows, int I, int act, float limit, ActBuf& a) {
-  TimedLaunch tl(c, TC_ROWS, double(rows) * I * (8 + 2));
-  glu_act_kernel<<<rows, 256, 0, c->stream>>>(gu, ldg, I, act, limit, static_cast<uint4*>(a.frag), a.xsum, a.nkb);
-  IH_HIP(hipGetLastError());
+  a.nss = 1;
   return IH_OK;
 }
 

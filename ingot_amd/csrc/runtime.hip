@@ -73,7 +73,7 @@ int ensure_part(ih_ctx* c, size_t bytes) {
 
 void free_act(ActBuf& a) {
   if (a.frag) (void)hipFree(a.frag);
-  if (a.xsum) (void)hipFree(a.xsum);
+  if (a.ss) (void)hipFree(a.ss);
   a = ActBuf();
 }
 
@@ -86,13 +86,15 @@ int ensure_act(ih_ctx* c, ActBuf& a, int K, bool f16) {
     return IH_OK;
   }
   free_act(a);
-  size_t fb = size_t(MAX_TOK) * nkb * 256, sb = size_t(2 * nkb) * MAX_TOK * 4;
-  if (hipMalloc(&a.frag, fb) != hipSuccess || hipMalloc(&a.xsum, sb) != hipSuccess) {
+  const int ss_cap = 4096;
+  size_t fb = size_t(MAX_TOK) * nkb * 256, sb = size_t(ss_cap) * MAX_TOK * 4;
+  if (hipMalloc(&a.frag, fb) != hipSuccess || hipMalloc(&a.ss, sb) != hipSuccess) {
     free_act(a);
     return fail(IH_ENOMEM, "activation buffer allocation failed");
   }
   IH_TRY(fill(c, a.frag, 0, fb));
-  IH_TRY(fill(c, a.xsum, 0, sb));
+  IH_TRY(fill(c, a.ss, 0, sb));
+  a.ss_cap = ss_cap;
   a.K = K;
   a.nkb = nkb;
   a.f16 = f16;

@@ -294,6 +294,24 @@ void or_rmsnorm(const float* x, int rows, int D, const uint16_t* w, float eps, f
   }
 }
 
+// RMSNorm split as the verify step computes it: the matmul input is x = bf16(h ⊙ w) and the per-row factor
+// r = 1/sqrt(mean h² + eps) multiplies the matmul output (RMSNorm is a per-row scale, so
+// (h·r ⊙ w)·Wᵀ = r · ((h ⊙ w)·Wᵀ); only the bf16 rounding point moves). rmsnorm_rows (verify.metal:501-523).
+void or_rms_split(const float* h, int rows, int D, const uint16_t* w, float eps, float* x, float* r) {
+  for (int i = 0; i < rows; ++i) {
+    double ss = 0;
+    for (int j = 0; j < D; ++j) ss += double(h[size_t(i) * D + j]) * h[size_t(i) * D + j];
+    r[i] = 1.0f / std::sqrt(float(ss) / float(D) + eps);
+    for (int j = 0; j < D; ++j)
+      x[size_t(i) * D + j] = or_bf16_to_f32(or_f32_to_bf16(h[size_t(i) * D + j] * or_bf16_to_f32(w[j])));
+  }
+}
+
+static void scale_rows(float* y, int rows, int N, const float* r) {
+  for (int i = 0; i < rows; ++i)
+    for (int j = 0; j < N; ++j) y[size_t(i) * N + j] *= r[i];
+}
+
 // Gated activation (lab_glu, Sources/Ingot/Shaders/qmm.metal:18-30): act 0 = SiLU(g)·u, act 1 = swiglu_oai
 // (CPU.swigluOAI, Tests/IngotTests/KernelHarness.swift:185-188). Output rounded to bf16.
 float or_glu(float g, float u, int act, float limit) {
@@ -474,11 +492,12 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
     or_dequant_int4(m->embed.w.data() + size_t(tokens[r]) * H / 8, m->embed.s.data() + size_t(tokens[r]) * H / 64,
                     m->embed.b.data() + size_t(tokens[r]) * H / 64, 1, H, hres.data() + size_t(r) * H);
   std::vector<float> x(size_t(B) * H), proj(size_t(B) * QP), q(size_t(B) * QH * HD), att(size_t(B) * QH * HD);
-  std::vector<float> y(size_t(B) * H), gu(size_t(B) * 2 * I), a(size_t(B) * I);
+  std::vector<float> y(size_t(B) * H), gu(size_t(B) * 2 * I), a(size_t(B) * I), rr(B);
   for (int l = 0; l < d->n_layers; ++l) {
     OrLayer& L = m->layers[l];
-    or_rmsnorm(hres.data(), B, H, L.attn_norm.data(), d->rms_eps, x.data());
+    or_rms_split(hres.data(), B, H, L.attn_norm.data(), d->rms_eps, x.data(), rr.data());
     L.qkv.apply(x.data(), B, proj.data());
+    scale_rows(proj.data(), B, QP, rr.data());
     for (int t = 0; t < B; ++t) {
       const float* pr = proj.data() + size_t(t) * QP;
       for (int hh = 0; hh < QH; ++hh) {
@@ -503,8 +522,9 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
     for (auto& z : att) z = or_bf16_to_f32(or_f32_to_bf16(z));
     L.o.apply(att.data(), B, y.data());
     for (size_t i = 0; i < hres.size(); ++i) hres[i] += y[i];
-    or_rmsnorm(hres.data(), B, H, L.mlp_norm.data(), d->rms_eps, x.data());
+    or_rms_split(hres.data(), B, H, L.mlp_norm.data(), d->rms_eps, x.data(), rr.data());
     L.gate_up.apply(x.data(), B, gu.data());
+    scale_rows(gu.data(), B, 2 * I, rr.data());
     for (int t = 0; t < B; ++t)
       for (int i = 0; i < I; ++i)
         a[size_t(t) * I + i] = or_bf16_to_f32(or_f32_to_bf16(
@@ -512,8 +532,9 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
     L.down.apply(a.data(), B, y.data());
     for (size_t i = 0; i < hres.size(); ++i) hres[i] += y[i];
   }
-  or_rmsnorm(hres.data(), B, H, m->final_norm.data(), d->rms_eps, x.data());
+  or_rms_split(hres.data(), B, H, m->final_norm.data(), d->rms_eps, x.data(), rr.data());
   m->head.apply(x.data(), B, logits);
+  scale_rows(logits, B, d->vocab, rr.data());
   or_argmax_rows(logits, B, d->vocab, top1);
   return 0;
 }
