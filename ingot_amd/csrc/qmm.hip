@@ -166,23 +166,34 @@ struct QmmRsrc {
 template <int T, int R, bool X16>
 __device__ __forceinline__ void qmm_load(QmmStage<T, R, X16>& st, const QmmParams& p, const QmmRsrc& rs, int tile0,
                                          int kb, int lane, int n) {
+  // Past the last K-block every offset is forced out of range (offsets stay below 2^31, so OR-ing OOB keeps them out):
+  // the loads are issued unconditionally, read zeros without touching memory, and the loop body is one basic block
+  // with a fixed number of loads in flight, so the wait before each multiply covers only the stage it reads.
+  const unsigned oob = kb < p.nkb ? 0u : OOB;
+  // The scheduling barriers keep the stage's loads together, ahead of the multiply of the previous stage (LLVM's
+  // scheduler otherwise sinks them toward their use and the prefetch distance collapses).
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const unsigned tb = unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kb);
-    st.w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, tb * 1024u + lane * 16u, 0, 0));
-    st.sb[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.s, tb * 128u + n * 8u, 0, 0));
+    st.w[r] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, (tb * 1024u + lane * 16u) | oob, 0, 0));
+    st.sb[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.s, (tb * 128u + n * 8u) | oob, 0, 0));
   }
   const unsigned kx = unsigned(kb) * 256u;
 #pragma unroll
   for (int tt = 0; tt < T; ++tt)
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      st.x[tt][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, rs.xoff[tt] + kx + 16 * t, 0, 0));
+      st.x[tt][t] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.xoff[tt] + kx + 16 * t) | oob, 0, 0));
   if constexpr (X16) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      st.x16[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, rs.x16off + kx + 16 * t, 0, 0));
+      st.x16[t] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.x16off + kx + 16 * t) | oob, 0, 0));
   }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int T, int R, bool X16>
@@ -263,7 +274,8 @@ __device__ __forceinline__ float glu_f(float g, float u, int act, float limit) {
 // XCD's L2 back and costs tens of µs) and a summation order that depends only on (N, K).
 template <int T, int R, int KW, bool X16>
 __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // The wave index is uniform: readfirstlane keeps it (and the K-block loop) in scalar registers and scalar branches.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, qd = lane >> 4;
   const int tile0 = blockIdx.x * R;
   __shared__ float rsc[MAX_TOK];
@@ -293,10 +305,24 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 
   QmmStage<T, R, X16> a, b;
   int kb = wave;
-  if (kb < p.nkb) qmm_load(a, p, rs, tile0, kb, lane, n);
+  qmm_load(a, p, rs, tile0, kb, lane, n);
+
+  // This wave's K-blocks: wave, wave + KW, … (nk of them), two per trip of a loop with a single exit (a loop with
+  // two exits is structurized into a join that the wait-count pass treats as a back edge with the other stage's loads
+  // still pending, which serialises every trip). Loads past the end read zeros.
+  const int nk = kb < p.nkb ? (p.nkb - kb + KW - 1) / KW : 0;
+  for (int it = 0; it < nk / 2; ++it) {
+    qmm_load(b, p, rs, tile0, kb + KW, lane, n);
+    qmm_compute(acc, acc16, a, km, kbias, qd0);
+    qmm_load(a, p, rs, tile0, kb + 2 * KW, lane, n);
+    qmm_compute(acc, acc16, b, km, kbias, qd0);
+    kb += 2 * KW;
+  }
+  if (nk & 1) qmm_compute(acc, acc16, a, km, kbias, qd0);
 
   // RMSNorm factors of the input rows (the norm's sums of squares come in as partials of the producer's workgroups,
-  // added here in a fixed order), while the first loads are in flight.
+  // added here in a fixed order). After the K loop: loads with a data-dependent count ahead of it would make the
+  // compiler's wait counts at the loop head conservative.
   // Wave w takes tokens w, w + KW, …; lane l adds partials l, l + 64, … and the lanes are combined by a fixed
   // butterfly, so a token's factor does not depend on M or on the launch shape.
   if (p.ss_in) {
@@ -306,19 +332,6 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
       if (lane == 0) rsc[t] = 1.0f / sqrtf(ss / float(p.D) + p.eps);
-    }
-  }
-
-  if (kb < p.nkb) {
-    while (true) {
-      if (kb + KW < p.nkb) qmm_load(b, p, rs, tile0, kb + KW, lane, n);
-      qmm_compute(acc, acc16, a, km, kbias, qd0);
-      kb += KW;
-      if (kb >= p.nkb) break;
-      if (kb + KW < p.nkb) qmm_load(a, p, rs, tile0, kb + KW, lane, n);
-      qmm_compute(acc, acc16, b, km, kbias, qd0);
-      kb += KW;
-      if (kb >= p.nkb) break;
     }
   }
 
