@@ -189,6 +189,35 @@ int ih_verify_and_accept(ih_model* model, ih_kv* kv, const uint32_t* tokens, int
 /* The model's device scratch of the last step: logits fp32 [rows ≥ B][vocab] (row stride = vocab). */
 const float* ih_model_logits_dev(const ih_model* model);
 
+/* ---- Copy-from-context drafting (CopyIndex, Sources/Ingot/CopySpec.swift:15-139) ------------------------------
+ * Rule: the current trigram is the last three tokens (ending at cur = n − 1). Among the three most recent earlier
+ * ends p < cur of that trigram, take the longest backward match (at most max_match, at most p + 1 tokens), ties to the
+ * more recent; a match shorter than min_match (≥ 3) proposes nothing; otherwise the proposal is
+ * hist[p + 1 … min(cur, p + max_k)]. */
+typedef struct ih_copy_index ih_copy_index;
+
+/* Host index of a token history: CopyIndex.init(minMatch:maxMatch:capacity:) (CopySpec.swift:28-32). */
+int ih_copy_index_create(int min_match, int max_match, int capacity, ih_copy_index** out);
+int ih_copy_index_free(ih_copy_index* index);
+/* CopyIndex.append (CopySpec.swift:99-106). */
+int ih_copy_index_append(ih_copy_index* index, const uint32_t* tokens, int n);
+/* CopyIndex.sync(to:) (CopySpec.swift:108-121): appends the missing tail when the indexed history is a prefix of
+ * tokens, otherwise starts over. */
+int ih_copy_index_sync(ih_copy_index* index, const uint32_t* tokens, int n);
+/* CopyIndex.reset (CopySpec.swift:93-97). */
+int ih_copy_index_reset(ih_copy_index* index);
+/* Number of tokens indexed (CopyIndex.hist.count). */
+int ih_copy_index_len(const ih_copy_index* index);
+/* CopyIndex.propose(maxK:) and lastMatch (CopySpec.swift:123-138): writes *n_out ≤ max_k tokens to out and the match
+ * length (0 when nothing is proposed) to *match_out. */
+int ih_copy_index_propose(const ih_copy_index* index, int max_k, uint32_t* out, int* n_out, int* match_out);
+/* The same rule as one scan of a device-resident history hist_dev[n] (n ≥ 4), with no index: out_dev receives
+ * [count, match, end p (or 0xFFFFFFFF), 0, tokens[max_k]] (max_k ≤ 4096). If vtok_dev is not null it also receives the
+ * verify block of `rows` (≤ 17) entries: [hist[cur], proposal…, hist[cur] as padding]. Asynchronous on the ctx stream.
+ * The GPU counterpart of propose() for a history that already lives in HBM. */
+int ih_copy_lookup_dev(ih_ctx* ctx, const uint32_t* hist_dev, int n, int max_k, int min_match, int max_match,
+                       uint32_t* out_dev, uint32_t* vtok_dev, int rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -90,6 +90,14 @@ def _declare(L: C.CDLL) -> None:
         "ih_verify_step_dev": (i32, [vp, vp, vp, i32, vp]),
         "ih_verify_and_accept": (i32, [vp, vp, vp, i32, vp]),
         "ih_model_logits_dev": (vp, [vp]),
+        "ih_copy_index_create": (i32, [i32, i32, i32, P(vp)]),
+        "ih_copy_index_free": (i32, [vp]),
+        "ih_copy_index_append": (i32, [vp, vp, i32]),
+        "ih_copy_index_sync": (i32, [vp, vp, i32]),
+        "ih_copy_index_reset": (i32, [vp]),
+        "ih_copy_index_len": (i32, [vp]),
+        "ih_copy_index_propose": (i32, [vp, i32, vp, P(i32), P(i32)]),
+        "ih_copy_lookup_dev": (i32, [vp, vp, i32, i32, i32, i32, vp, vp, i32]),
         "ih_timing_enable": (i32, [vp, i32]),
         "ih_timing_read": (i32, [vp, i32, P(C.c_double), P(C.c_int), P(C.c_double)]),
     }
@@ -339,3 +347,58 @@ class KVCache:
         if self.handle:
             lib().ih_kv_free(self.handle)
             self.handle = None
+
+
+class CopyIndex:
+    """Host trigram index of a token history (ih_copy_index_*; CopyIndex, Sources/Ingot/CopySpec.swift:15-139)."""
+
+    def __init__(self, min_match: int = 3, max_match: int = 64, capacity: int = 1 << 16):
+        h = vp()
+        check(lib().ih_copy_index_create(min_match, max_match, capacity, C.byref(h)))
+        self.handle = h.value
+        self.last_match = 0
+
+    def append(self, tokens) -> None:
+        a = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
+        check(lib().ih_copy_index_append(self.handle, ptr(a), a.size))
+
+    def sync(self, tokens) -> None:
+        a = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
+        check(lib().ih_copy_index_sync(self.handle, ptr(a), a.size))
+
+    def reset(self) -> None:
+        check(lib().ih_copy_index_reset(self.handle))
+
+    def __len__(self) -> int:
+        return lib().ih_copy_index_len(self.handle)
+
+    def propose(self, max_k: int) -> list[int]:
+        out = np.zeros(max(max_k, 1), np.uint32)
+        n, m = C.c_int(), C.c_int()
+        check(lib().ih_copy_index_propose(self.handle, max_k, ptr(out), C.byref(n), C.byref(m)))
+        self.last_match = m.value
+        return [int(x) for x in out[: n.value]]
+
+    def free(self) -> None:
+        if self.handle:
+            lib().ih_copy_index_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:  # noqa: BLE001
+            pass
+
+
+def copy_lookup_dev(ctx: "Context", hist_dev: "DeviceBuffer", n: int, max_k: int, min_match: int = 3,
+                    max_match: int = 64, vtok_dev: "DeviceBuffer | None" = None, rows: int = 0):
+    """Device scan (ih_copy_lookup_dev): returns (proposal, match, end p or -1)."""
+    out = ctx.buffer((4 + max_k) * 4)
+    check(lib().ih_copy_lookup_dev(ctx.handle, hist_dev.ptr, n, max_k, min_match, max_match, out.ptr,
+                                   vtok_dev.ptr if vtok_dev is not None else None, rows))
+    o = out.download(np.uint32, (4 + max_k,))
+    out.free()
+    cnt = int(o[0])
+    end = int(o[2]) if cnt else -1
+    return [int(x) for x in o[4: 4 + cnt]], int(o[1]), end

@@ -41,3 +41,25 @@ def cosine(a: np.ndarray, b: np.ndarray) -> float:
     a = a.astype(np.float64).ravel()
     b = b.astype(np.float64).ravel()
     return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
+
+
+def zipf_context(seed: int, n: int = 131072, vocab: int = 151936, s: float = 1.1, spans: int = 64,
+                 span_len: int = 32, tail: int = 8):
+    """Config 2's context: int32 ids drawn Zipf(s) over the vocab (rank r has weight r^-s, id = rank - 1), with
+    `spans` repeated spans of `span_len` tokens (each copied from an earlier position to a later one), ending with
+    the first `tail` tokens of one more copy of the last planted span, so the trailing trigram has a long earlier
+    match. Returns (context uint32 [n], the span's source position)."""
+    g = np.random.default_rng(seed)
+    w = np.arange(1, vocab + 1, dtype=np.float64) ** -s
+    cdf = np.cumsum(w)
+    cdf /= cdf[-1]
+    h = np.searchsorted(cdf, g.random(n), side="right").astype(np.uint32)
+    h = np.minimum(h, vocab - 1)
+    body = n - tail
+    src = 0
+    for _ in range(spans):
+        src = int(g.integers(0, body // 2 - span_len))
+        dst = int(g.integers(body // 2, body - span_len))
+        h[dst:dst + span_len] = h[src:src + span_len]
+    h[body:] = h[src:src + tail]
+    return h, src
