@@ -90,6 +90,7 @@ def _declare(L: C.CDLL) -> None:
         "ih_verify_step_dev": (i32, [vp, vp, vp, i32, vp]),
         "ih_verify_and_accept": (i32, [vp, vp, vp, i32, vp]),
         "ih_model_logits_dev": (vp, [vp]),
+        "ih_kv_create_chunked": (i32, [vp, i32, i32, P(vp)]),
         "ih_copy_index_create": (i32, [i32, i32, i32, P(vp)]),
         "ih_copy_index_free": (i32, [vp]),
         "ih_copy_index_append": (i32, [vp, vp, i32]),
@@ -306,10 +307,10 @@ class Model:
 
 
 class KVCache:
-    def __init__(self, model: Model, capacity: int):
+    def __init__(self, model: Model, capacity: int, chunk: int = 0):
         self.model = model
         h = vp()
-        check(lib().ih_kv_create(model.handle, capacity, C.byref(h)))
+        check(lib().ih_kv_create_chunked(model.handle, capacity, chunk, C.byref(h)))
         self.handle = h.value
 
     def fill_synthetic(self, P: int, seed: int) -> None:

@@ -9,12 +9,14 @@
 // (per token and head, symmetric). K holds H·k (orthonormal Walsh–Hadamard of the roped key) when hadk is set, and q is
 // rotated the same way, so (Hq)·(Hk) = q·k.
 //
-// MI355X design: one workgroup per (key split, KV head, query group) with 4 waves. Each 32-key block of the split is
-// read once by the workgroup, converted int8 → fp16 exactly into LDS (K key-major, V transposed), and every wave runs
-// its 16-query tiles over it: Sᵀ = K·Qᵀ (v_mfma_f32_16x16x32_f16, keys as rows so each lane holds 4 keys of one query),
-// online softmax in base 2 per query column, P stays in registers as the B operand of Oᵀ += Vᵀ·Pᵀ. A query's result
-// does not depend on the other rows of the block: blocks start at fixed key positions, the split boundaries are fixed
-// multiples of C, and the splits are combined in split order.
+// MI355X design: one workgroup (8 waves) per (key split, KV head); the split size C is fixed per cache so that all
+// splits of all heads are one workgroup per CU. A split is staged through LDS in sub-chunks (288 keys at HD 128): every
+// thread issues its loads of the whole sub-chunk at once (the next sub-chunk is in flight during this one's products),
+// converts int8 → fp16 exactly into LDS (K key-major, V transposed), and each wave runs its 16-query tiles over 64-key
+// blocks: Sᵀ = K·Qᵀ (v_mfma_f32_16x16x32_f16, keys as rows so each lane holds 4 keys of one query), online softmax in
+// base 2 per query column, P stays in registers as the B operand of Oᵀ += Vᵀ·Pᵀ. A split writes O/l in fp16 with its
+// (max, sum); the reduction merges the splits in a fixed order. A query's result does not depend on the other rows of
+// the block: blocks start at fixed key positions and the split boundaries are fixed multiples of C.
 #include <hip/hip_fp16.h>
 
 #include "act.h"
@@ -96,233 +98,372 @@ __device__ __forceinline__ void i8x4_to_h(unsigned w, __half2& lo, __half2& hi) 
   hi = __hsub2(__builtin_bit_cast(__half2, h), off);
 }
 
-constexpr int KROW = 128 + 8;  // LDS row of K in halves (HD ≤ 128, padded)
-constexpr int VROW = 32 + 8;   // LDS row of Vᵀ in halves
+// Four int8 words of four consecutive keys (bytes = dims 4w … 4w+3) → four words of four keys per dim (bytes = keys).
+__device__ __forceinline__ void transpose4x4(unsigned a, unsigned b, unsigned c, unsigned d, unsigned (&o)[4]) {
+  const unsigned t0 = __builtin_amdgcn_perm(b, a, 0x05010400u), t1 = __builtin_amdgcn_perm(b, a, 0x07030602u);
+  const unsigned u0 = __builtin_amdgcn_perm(d, c, 0x05010400u), u1 = __builtin_amdgcn_perm(d, c, 0x07030602u);
+  o[0] = __builtin_amdgcn_perm(u0, t0, 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(u0, t0, 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(u1, t1, 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(u1, t1, 0x07060302u);
+}
+
+constexpr int ATT_THREADS = 512;       // 8 waves: all load, the first ceil(tiles / TPW) compute
+// Keys staged in LDS at a time (a multiple of 32): fp16 K (HD + 8 halves a row) and Vᵀ (SUB + 8 halves a row) fill
+// ≤ 156 KB of the 160 KB LDS.
+template <int HD> constexpr int sub_keys() { return HD == 128 ? 288 : 512; }
+template <int HD> constexpr int krow() { return HD + 8; }
 
 // Slot of key k (0…31) in a 32-key block of Vᵀ: the PV MFMA pairs lane group qd's element e with key 4·qd + e (e < 4,
-// first 16-key tile) or 16 + 4·qd + e − 4 (second tile): the keys each lane holds after the Sᵀ MFMAs.
+// first 16-key tile) or 16 + 4·qd + e − 4 (second tile): the keys each lane holds after the Sᵀ MFMAs. Four consecutive
+// keys from a multiple of 4 occupy four consecutive slots.
 __device__ __forceinline__ int vslot(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
 
-// K/V of one 32-key block in flight: per thread one 16-byte K item (key, 16 dims) and one V item (key pair, 8 dims:
-// 8 bytes of each key), so V can be written transposed as 32-bit key pairs.
+// One sub-chunk of K and V in flight in registers: per thread up to KI K items (one key, 16 dims), up to VI V items
+// (four keys, 16 dims) and up to SI keys' two scales.
 template <int HD>
-struct KVStage {
-  uint4 k;
-  uint2 v0, v1;
-  float ks, vs;
+struct SubStage {
+  static constexpr int SUB = sub_keys<HD>();
+  static constexpr int KITEMS = SUB * (HD / 16), VITEMS = (SUB / 4) * (HD / 16);
+  static constexpr int KI = (KITEMS + ATT_THREADS - 1) / ATT_THREADS;
+  static constexpr int VI = (VITEMS + ATT_THREADS - 1) / ATT_THREADS;
+  static constexpr int SI = (SUB + ATT_THREADS - 1) / ATT_THREADS;
+  uint4 k[KI];
+  uint4 v[VI][4];
+  __half ks[SI], vs[SI];
 };
 
-template <int HD>
-__global__ __launch_bounds__(512) void attn_kernel(AttnArgs a) {
-  constexpr int NC = HD / 32;           // 32-dim chunks (MFMA K steps of Sᵀ)
-  constexpr int NDT = HD / 16;          // 16-dim tiles of Oᵀ
-  constexpr int KITEMS = 32 * HD / 16;  // 16-byte K items of a block
-  constexpr int VITEMS = 16 * HD / 8;   // (key pair, 8 dims) V items of a block
-  __shared__ _Float16 Kf[32 * KROW];
+// One workgroup per (split of C keys, KV head): every query row of the head's group (G·B ≤ 16·8·TPW) in one pass.
+// The split is staged through LDS in sub-chunks of SUB keys: all of a sub-chunk's loads are issued together (the
+// next sub-chunk is in flight while this one is multiplied), converted int8 → fp16 once into LDS (K key-major, V
+// transposed), then each wave runs its query tiles over 64-key blocks with an online softmax in base 2.
+template <int HD, int TPW, bool RING>
+__global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
+  using Stage = SubStage<HD>;
+  constexpr int SUB = Stage::SUB;
+  constexpr int VROW = SUB + 8;  // LDS row of Vᵀ in halves
+  constexpr int NC = HD / 32;    // 32-dim chunks (MFMA K steps of Sᵀ)
+  constexpr int NDT = HD / 16;   // 16-dim tiles of Oᵀ
+  constexpr int KR = krow<HD>();
+  constexpr int KPK = HD / 16;   // K items per key
+  __shared__ _Float16 Kf[SUB * KR];
   __shared__ _Float16 Vt[HD * VROW];
-  __shared__ float ksf[32], vsf[32];
+  // Scales of the staged keys; 64 zero entries past SUB so a 64-key block never indexes out of range.
+  __shared__ __attribute__((aligned(16))) float ksf[SUB + 64], vsf[SUB + 64];
 
-  // Partials are stored by launched split (blockIdx.x); the key range is that of split blockIdx.x + s0 (a sliding
-  // window does not launch the splits that end before the first row's window).
   const int sidx = blockIdx.x, split = sidx + a.s0, kvh = blockIdx.y;
-  const int nthreads = blockDim.x, tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
   const int Q = a.G * a.B;
   const int k0 = split * a.C, k1 = min(k0 + a.C, a.P + a.B);
-
-  // One 16-query tile per wave.
-  const int qt = blockIdx.z * (nthreads >> 6) + wave;
-  const bool qlive = 16 * qt < Q;
-  const int m = 16 * qt + j;
-  f16x8 qf[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    if (qlive && m < Q) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(a.q + (size_t(kvh) * a.Qpad + m) * HD + 32 * c + 8 * qd);
-      qf[c] = __builtin_bit_cast(f16x8, v);
-    } else {
-      qf[c] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-  }
-  f32x4 o[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float mrun = -INFINITY, lsum = 0.f;
-  const int tok = m / a.G;
-  const int lim = a.P + tok;  // last visible key (causal)
-  const int lo_key = a.window > 0 ? lim - a.window + 1 : -2147483647;
 
   const int8_t* kh = a.kc + size_t(kvh) * a.cap * HD;
   const int8_t* vh = a.vc + size_t(kvh) * a.cap * HD;
   const __half* ksh = a.ks + size_t(kvh) * a.cap;
   const __half* vsh = a.vs + size_t(kvh) * a.cap;
-  auto slot_of = [&](int key) { return a.ring ? key % a.ring : key; };
+  const int ring = a.ring;
+  auto slot_of = [ring](int key) { return RING ? key % ring : key; };
 
-  // Loader items of this thread (at most one K and one V item, since blockDim ≥ 256 for HD 128 and ≥ 128 for 64
-  // is not guaranteed: threads beyond the item count load nothing).
-  const bool hask = tid < KITEMS, hasv = tid < VITEMS;
-  const int kkey = tid / (HD / 16), kcol = (tid % (HD / 16)) * 16;
-  const int vpair = tid / (HD / 8), vcol = (tid % (HD / 8)) * 8;
-  KVStage<HD> st;
+  // Query tiles of this wave: wave + 8·tt.
+  f16x8 qf[TPW][NC];
+  f32x4 o[TPW][NDT];
+  float mrun[TPW], lsum[TPW];
+  int lim[TPW], lo_key[TPW], tile_hi[TPW], tile_lo[TPW], tile_lo_lim[TPW], tile_hi_lo[TPW];
+  bool live[TPW];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int qt = wave + 8 * tt, m = 16 * qt + j;
+    live[tt] = 16 * qt < Q;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (live[tt] && m < Q)
+        qf[tt][c] = __builtin_bit_cast(
+            f16x8, *reinterpret_cast<const u32x4*>(a.q + (size_t(kvh) * a.Qpad + m) * HD + 32 * c + 8 * qd));
+      else
+        qf[tt][c] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[tt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    mrun[tt] = -INFINITY;
+    lsum[tt] = 0.f;
+    lim[tt] = m < Q ? a.P + m / a.G : -1;  // last visible key (causal); −1: padding row sees nothing
+    lo_key[tt] = a.window > 0 ? lim[tt] - a.window + 1 : -2147483647;
+    tile_hi[tt] = live[tt] ? a.P + min(16 * qt + 15, Q - 1) / a.G : -1;
+    tile_lo[tt] = a.window > 0 ? a.P + (16 * qt) / a.G - a.window + 1 : -2147483647;
+    // Keys every row of the tile sees: up to the first row's causal limit (−1 if the tile has padding rows, which see
+    // nothing and need the mask), from the last row's window start.
+    tile_lo_lim[tt] = (live[tt] && 16 * qt + 15 < Q) ? a.P + (16 * qt) / a.G : -1;
+    tile_hi_lo[tt] = a.window > 0 ? tile_hi[tt] - a.window + 1 : -2147483647;
+  }
+
+  Stage st;
   auto load = [&](int kb) {
-    if (hask) {
-      const int key = kb + kkey;
-      st.k = key < k1 ? *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + kcol) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < Stage::KI; ++i) {
+      const int item = tid + ATT_THREADS * i, key = kb + item / KPK, col = (item % KPK) * 16;
+      st.k[i] = (item < Stage::KITEMS && key < k1)
+                    ? *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + col)
+                    : make_uint4(0, 0, 0, 0);
     }
-    if (hasv) {
-      const int key0 = kb + 2 * vpair, key1 = key0 + 1;
-      st.v0 = key0 < k1 ? *reinterpret_cast<const uint2*>(vh + size_t(slot_of(key0)) * HD + vcol) : make_uint2(0, 0);
-      st.v1 = key1 < k1 ? *reinterpret_cast<const uint2*>(vh + size_t(slot_of(key1)) * HD + vcol) : make_uint2(0, 0);
+#pragma unroll
+    for (int i = 0; i < Stage::VI; ++i) {
+      const int item = tid + ATT_THREADS * i, q4 = item / KPK, col = (item % KPK) * 16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = kb + 4 * q4 + e;
+        st.v[i][e] = (item < Stage::VITEMS && key < k1)
+                         ? *reinterpret_cast<const uint4*>(vh + size_t(slot_of(key)) * HD + col)
+                         : make_uint4(0, 0, 0, 0);
+      }
     }
-    if (tid < 32) {
-      const int key = kb + tid;
-      st.ks = key < k1 ? __half2float(ksh[slot_of(key)]) * a.scale_log2 : 0.f;
-      st.vs = key < k1 ? __half2float(vsh[slot_of(key)]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < Stage::SI; ++i) {
+      const int kk = tid + ATT_THREADS * i, key = kb + kk;
+      // Keys past the split read scale 0: their V contributes 0 and their scores are masked.
+      const bool ok = kk < SUB && key < k1;
+      st.ks[i] = ok ? ksh[slot_of(key)] : __float2half(0.f);
+      st.vs[i] = ok ? vsh[slot_of(key)] : __float2half(0.f);
     }
   };
   auto store = [&]() {
-    if (hask) {
-      const unsigned kw[4] = {st.k.x, st.k.y, st.k.z, st.k.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        __half2 lo, hi;
-        i8x4_to_h(kw[i], lo, hi);
-        *reinterpret_cast<__half2*>(&Kf[kkey * KROW + kcol + 4 * i]) = lo;
-        *reinterpret_cast<__half2*>(&Kf[kkey * KROW + kcol + 4 * i + 2]) = hi;
+    for (int i = 0; i < Stage::KI; ++i) {
+      const int item = tid + ATT_THREADS * i, key = item / KPK, col = (item % KPK) * 16;
+      if (item >= Stage::KITEMS) continue;
+      const unsigned kw[4] = {st.k[i].x, st.k[i].y, st.k[i].z, st.k[i].w};
+      u32x4 h0, h1;
+      __half2 lo, hi;
+      i8x4_to_h(kw[0], lo, hi); h0.x = __builtin_bit_cast(unsigned, lo); h0.y = __builtin_bit_cast(unsigned, hi);
+      i8x4_to_h(kw[1], lo, hi); h0.z = __builtin_bit_cast(unsigned, lo); h0.w = __builtin_bit_cast(unsigned, hi);
+      i8x4_to_h(kw[2], lo, hi); h1.x = __builtin_bit_cast(unsigned, lo); h1.y = __builtin_bit_cast(unsigned, hi);
+      i8x4_to_h(kw[3], lo, hi); h1.z = __builtin_bit_cast(unsigned, lo); h1.w = __builtin_bit_cast(unsigned, hi);
+      *reinterpret_cast<u32x4*>(&Kf[key * KR + col]) = h0;
+      *reinterpret_cast<u32x4*>(&Kf[key * KR + col + 8]) = h1;
+    }
+#pragma unroll
+    for (int i = 0; i < Stage::VI; ++i) {
+      const int item = tid + ATT_THREADS * i, q4 = item / KPK, col = (item % KPK) * 16;
+      if (item >= Stage::VITEMS) continue;
+      const int slot = 32 * (q4 >> 3) + vslot(4 * (q4 & 7));
+      const unsigned* v0 = reinterpret_cast<const unsigned*>(&st.v[i][0]);
+      const unsigned* v1 = reinterpret_cast<const unsigned*>(&st.v[i][1]);
+      const unsigned* v2 = reinterpret_cast<const unsigned*>(&st.v[i][2]);
+      const unsigned* v3 = reinterpret_cast<const unsigned*>(&st.v[i][3]);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        unsigned t[4];
+        transpose4x4(v0[w], v1[w], v2[w], v3[w], t);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          __half2 lo, hi;
+          i8x4_to_h(t[e], lo, hi);
+          uint2 pr;
+          pr.x = __builtin_bit_cast(unsigned, lo);
+          pr.y = __builtin_bit_cast(unsigned, hi);
+          *reinterpret_cast<uint2*>(&Vt[(col + 4 * w + e) * VROW + slot]) = pr;
+        }
       }
     }
-    if (hasv) {
-      // Keys 2·vpair and 2·vpair + 1 occupy adjacent slots: one 32-bit (key pair) store per dim.
-      const int sl = vslot(2 * vpair);
-      const unsigned a0[2] = {st.v0.x, st.v0.y}, a1[2] = {st.v1.x, st.v1.y};
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        __half2 l0, h0, l1, h1;
-        i8x4_to_h(a0[i], l0, h0);
-        i8x4_to_h(a1[i], l1, h1);
-        const int d = vcol + 4 * i;
-        *reinterpret_cast<__half2*>(&Vt[(d + 0) * VROW + sl]) = __halves2half2(__low2half(l0), __low2half(l1));
-        *reinterpret_cast<__half2*>(&Vt[(d + 1) * VROW + sl]) = __halves2half2(__high2half(l0), __high2half(l1));
-        *reinterpret_cast<__half2*>(&Vt[(d + 2) * VROW + sl]) = __halves2half2(__low2half(h0), __low2half(h1));
-        *reinterpret_cast<__half2*>(&Vt[(d + 3) * VROW + sl]) = __halves2half2(__high2half(h0), __high2half(h1));
+    for (int i = 0; i < Stage::SI; ++i) {
+      const int kk = tid + ATT_THREADS * i;
+      if (kk < SUB) {
+        ksf[kk] = __half2float(st.ks[i]) * a.scale_log2;
+        vsf[kk] = __half2float(st.vs[i]);
       }
-    }
-    if (tid < 32) {
-      ksf[tid] = st.ks;
-      vsf[tid] = st.vs;
     }
   };
+  if (tid < 64) {
+    ksf[SUB + tid] = 0.f;
+    vsf[SUB + tid] = 0.f;
+  }
 
   if (k0 < k1) load(k0);
-  for (int kb = k0; kb < k1; kb += 32) {
-    __syncthreads();  // the previous block's readers are done with LDS
+  for (int kb = k0; kb < k1; kb += SUB) {
+    if (kb != k0) __syncthreads();  // every wave is done with the previous sub-chunk
     store();
     __syncthreads();
-    if (kb + 32 < k1) load(kb + 32);  // next block in flight during this one's products
-    if (!qlive) continue;             // uniform per wave
-    // Sᵀ for the two 16-key tiles: lane (j, qd) holds keys 16h + 4qd + r of query m.
-    f32x4 sacc[2];
+    if (kb + SUB < k1) load(kb + SUB);
+    const int nkeys = min(SUB, k1 - kb);  // keys of this sub-chunk (a multiple of 32 staged, the rest zero)
+    const int nblk = (nkeys + 63) / 64;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int tt = 0; tt < TPW; ++tt) {
+      if (!live[tt]) continue;  // uniform per wave
+      for (int b = 0; b < nblk; ++b) {
+        const int kk0 = 64 * b;
+        // Skip blocks no row of the tile can see (wave-uniform: past the last row's causal limit, or wholly before
+        // the first row's window).
+        if (kb + kk0 > tile_hi[tt] || kb + kk0 + 63 < tile_lo[tt]) continue;
+        const bool half2 = kk0 + 32 < nkeys;  // the block's second 32 keys are staged (uniform)
+        // All K fragments of the block first, then the four Sᵀ tiles as interleaved independent MFMA chains.
+        f16x8 kf[4][NC];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const f16x8 kf = *reinterpret_cast<const f16x8*>(&Kf[(16 * h + j) * KROW + 32 * c + 8 * qd]);
-        sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[c], sacc[h], 0, 0, 0);
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+            kf[h][c] = *reinterpret_cast<const f16x8*>(&Kf[(kk0 + 16 * h + j) * KR + 32 * c + 8 * qd]);
+        f32x4 sacc[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int h = 0; h < 4; ++h) sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h][c], qf[tt][c], sacc[h], 0, 0, 0);
+        // Vᵀ fragments of the block, read while the softmax runs (the second half only when it is staged). With two
+        // query tiles a wave has no registers for them: they are read at the products instead.
+        auto vread = [&](int hs, int dt) {
+          return *reinterpret_cast<const f16x8*>(&Vt[(16 * dt + j) * VROW + (hs && half2 ? kk0 + 32 : kk0) + 8 * qd]);
+        };
+        f16x8 vf[2][NDT];
+        if constexpr (TPW == 1) {
+#pragma unroll
+          for (int hs = 0; hs < 2; ++hs)
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) vf[hs][dt] = vread(hs, dt);
+        }
+        // This lane's keys kk0 + 16h + 4qd + r: their scales as one 16-byte LDS read per tile, unconditionally (a
+        // conditional read becomes a branch with its own wait).
+        f32x4 ksv[4], vsv[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          ksv[h] = *reinterpret_cast<const f32x4*>(&ksf[kk0 + 16 * h + 4 * qd]);
+          vsv[h] = *reinterpret_cast<const f32x4*>(&vsf[kk0 + 16 * h + 4 * qd]);
+        }
+        float s[4][4];
+        float mx = -INFINITY;
+        // Every key of the block visible to every row of the tile (the common case): no per-key mask.
+        const bool full = kk0 + 64 <= nkeys && kb + kk0 + 63 <= tile_lo_lim[tt] && kb + kk0 >= tile_hi_lo[tt];
+        if (full) {
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              s[h][r] = sacc[h][r] * ksv[h][r];
+              mx = fmaxf(mx, s[h][r]);
+            }
+        } else {
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int kk = kk0 + 16 * h + 4 * qd + r, key = kb + kk;
+              const bool vis = kk < nkeys && key <= lim[tt] && key >= lo_key[tt];
+              s[h][r] = vis ? sacc[h][r] * ksv[h][r] : -INFINITY;
+              mx = fmaxf(mx, s[h][r]);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mnew = fmaxf(mrun[tt], mx);
+        const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[tt] - mnew);
+        mrun[tt] = mnew;
+        float ps = 0.f;
+        f16x8 pb[2];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            // v_exp_f32 directly: exp2(−inf) = 0, and no range reduction is needed for arguments ≤ 0.
+            const float p = __builtin_amdgcn_exp2f(s[h][r] - mnew);
+            ps += p;
+            pb[h >> 1][4 * (h & 1) + r] = (_Float16)(p * vsv[h][r]);
+          }
+        lsum[tt] = lsum[tt] * alpha + ps;
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) o[tt][dt] *= alpha;
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+          o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(TPW == 1 ? vf[0][dt] : vread(0, dt), pb[0], o[tt][dt], 0, 0, 0);
+        if (half2) {
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+            o[tt][dt] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(TPW == 1 ? vf[1][dt] : vread(1, dt), pb[1], o[tt][dt], 0, 0, 0);
+        }
       }
-    }
-    float s[2][4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int kk = 16 * h + 4 * qd + r, key = kb + kk;
-        const bool vis = m < Q && key < k1 && key <= lim && key >= lo_key;
-        s[h][r] = vis ? sacc[h][r] * ksf[kk] : -INFINITY;
-        mx = fmaxf(mx, s[h][r]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mnew = fmaxf(mrun, mx);
-    const float alpha = mnew == -INFINITY ? 1.f : exp2f(mrun - mnew);
-    mrun = mnew;
-    float ps = 0.f;
-    f16x8 pb;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = s[h][r] == -INFINITY ? 0.f : exp2f(s[h][r] - mnew);
-        ps += p;
-        pb[4 * h + r] = (_Float16)(p * vsf[16 * h + 4 * qd + r]);
-      }
-    lsum = lsum * alpha + ps;
-    // Rescale Oᵀ only when some column's maximum moved (alpha = 1 is exact and is skipped).
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
-    }
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const f16x8 vf = *reinterpret_cast<const f16x8*>(&Vt[(16 * dt + j) * VROW + 8 * qd]);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb, o[dt], 0, 0, 0);
     }
   }
 
-  // Partials of this split: (max, sum) per query and the unnormalised Oᵀ (lane holds dims 16dt + 4qd + r of query m).
-  if (!qlive) return;
-  float l = lsum;
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (m >= Q) return;
-  const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
-  if (qd == 0) a.ml[base + m] = make_float2(mrun, l);
+  // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-    *reinterpret_cast<f32x4*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = o[dt];
+  for (int tt = 0; tt < TPW; ++tt) {
+    if (!live[tt]) continue;
+    float l = lsum[tt];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const int m = 16 * (wave + 8 * tt) + j;
+    if (m >= Q) continue;
+    const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
+    if (qd == 0) a.ml[base + m] = make_float2(mrun[tt], l);
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      __half2 p0 = __floats2half2_rn(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
+      __half2 p1 = __floats2half2_rn(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
+      uint2 w;
+      w.x = __builtin_bit_cast(unsigned, p0);
+      w.y = __builtin_bit_cast(unsigned, p1);
+      *reinterpret_cast<uint2*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = w;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 // Reduction of the splits (vattn_reduce, verify_attn.metal:149-192): M = max over splits (and the sink), L = Σ e^(m−M)·l
-// (+ e^(sink−M)), o = Σ e^(m−M)·O / L, in split order; written into the o_proj activation layout (column h·HD + d).
-// Grid (B, QH·HD/512), 64 threads (one per 8 values).
-__global__ __launch_bounds__(64) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb) {
-  const int t = blockIdx.x, c = blockIdx.y * 64 + threadIdx.x, HD = a.HD;
-  const int h = (8 * c) / HD, d0 = (8 * c) % HD;
+// (+ e^(sink−M)), o = Σ e^(m−M)·l·ō / L with ō = O/l the split's normalised partial; written into the o_proj
+// activation layout (column h·HD + d). One wave per (row, q head): lane = (split group sg, 8-dim group dg); a lane
+// merges splits sg, sg + SG, … (all its loads in flight), then the SG groups are merged by a fixed butterfly.
+// Grid (B, QH/4), 256 threads.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb) {
+  constexpr int DG = HD / 8, SG = 64 / DG;
+  const int t = blockIdx.x, h = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int dg = lane % DG, sg = lane / DG;
   const int kvh = h / a.G, m = t * a.G + h % a.G;
   const float2* mlh = a.ml + size_t(kvh) * a.nsplit * a.Qpad + m;
+  // Pass 1: this lane's maximum.
   float M = -INFINITY;
-#pragma unroll 8
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, mlh[size_t(s) * a.Qpad].x);
-  float L = 0.f;
-  if (a.sinks) {
-    const float sk = a.sinks[h] * 1.4426950408889634f;
-    M = fmaxf(M, sk);
-    L = exp2f(sk - M);
-  }
+  for (int s = sg; s < a.nsplit; s += SG) M = fmaxf(M, mlh[size_t(s) * a.Qpad].x);
+  if (sg == 0 && a.sinks) M = fmaxf(M, a.sinks[h] * 1.4426950408889634f);
+  // Pass 2: weights relative to it (an empty split has m = −inf, l = 0 and weight 0).
+  float L = (sg == 0 && a.sinks) ? exp2f(a.sinks[h] * 1.4426950408889634f - M) : 0.f;
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
-#pragma unroll 4
-  for (int s = 0; s < a.nsplit; ++s) {
+  for (int s = sg; s < a.nsplit; s += SG) {
     const size_t idx = (size_t(kvh) * a.nsplit + s) * a.Qpad + m;
     const float2 v = a.ml[idx];
-    const f32x4* src = reinterpret_cast<const f32x4*>(a.opart + idx * HD + d0);
-    const f32x4 p0 = src[0], p1 = src[1];
-    // An empty split carries (−inf, 0) and a zero O: its weight is 0.
-    const float w = v.x == -INFINITY ? 0.f : exp2f(v.x - M);
-    L += w * v.y;
+    const uint4 raw = *reinterpret_cast<const uint4*>(a.opart + idx * HD + 8 * dg);
+    const float w = v.x == -INFINITY ? 0.f : exp2f(v.x - M) * v.y;
+    L += w;
+    const unsigned rw[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      o[e] += w * p0[e];
-      o[4 + e] += w * p1[e];
+      const float2 f = __half22float2(__builtin_bit_cast(__half2, rw[e]));
+      o[2 * e] += w * f.x;
+      o[2 * e + 1] += w * f.y;
     }
   }
-  const float inv = 1.0f / L;
+  // Merge the split groups (lanes dg + DG·sg): butterfly over sg, fixed order.
+#pragma unroll
+  for (int x = DG; x < 64; x <<= 1) {
+    const float Mo = __shfl_xor(M, x), Lo = __shfl_xor(L, x);
+    const float Mn = fmaxf(M, Mo);
+    const float ca = M == -INFINITY ? 0.f : exp2f(M - Mn), cb = Mo == -INFINITY ? 0.f : exp2f(Mo - Mn);
+    L = L * ca + Lo * cb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float oo = __shfl_xor(o[e], x);
+      o[e] = o[e] * ca + oo * cb;
+    }
+    M = Mn;
+  }
+  if (sg != 0) return;
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] *= inv;
-  frag_store_chunk(frag, nkb, t, c, o);
+  frag_store_chunk(frag, nkb, t, (h * HD) / 8 + dg, o);
 }
 
 int launch_prework(ih_ctx* c, const AttnArgs& a) {
@@ -337,25 +478,33 @@ int launch_prework(ih_ctx* c, const AttnArgs& a) {
 int launch_attention(ih_ctx* c, const AttnArgs& a) {
   const int Q = a.G * a.B;
   const int qtiles = (Q + 15) / 16;
-  const int nz = (qtiles + 7) / 8;        // query groups of ≤ 8 tiles, one wave per tile
-  const int waves = (qtiles + nz - 1) / nz;
-  // The block loader needs 32·HD/16 threads (256 for HD 128, 128 for HD 64).
-  const int threads = std::max(64 * waves, a.HD * 2);
-  dim3 grid(a.nsplit, a.KVH, nz);
+  IH_CHECK(qtiles <= 16, IH_EINVAL, "attention: at most 256 query rows per KV head");
+  dim3 grid(a.nsplit, a.KVH);
   // Algorithmic bytes: the int8 K and V and their fp16 scales of every key the launched splits cover, and q.
   const double keys = double(a.P + a.B) - double(a.s0) * a.C;
   TimedLaunch tl(c, TC_ATTN, double(a.KVH) * keys * (2 * a.HD + 4) + double(a.KVH) * Q * a.HD * 2);
-  if (a.HD == 128) attn_kernel<128><<<grid, threads, 0, c->stream>>>(a);
-  else if (a.HD == 64) attn_kernel<64><<<grid, threads, 0, c->stream>>>(a);
-  else return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
+  const bool two = qtiles > 8, ring = a.ring != 0;
+  auto go = [&](auto kern) { kern<<<grid, ATT_THREADS, 0, c->stream>>>(a); };
+  if (a.HD == 128) {
+    if (two) ring ? go(attn_kernel<128, 2, true>) : go(attn_kernel<128, 2, false>);
+    else ring ? go(attn_kernel<128, 1, true>) : go(attn_kernel<128, 1, false>);
+  } else if (a.HD == 64) {
+    if (two) ring ? go(attn_kernel<64, 2, true>) : go(attn_kernel<64, 2, false>);
+    else ring ? go(attn_kernel<64, 1, true>) : go(attn_kernel<64, 1, false>);
+  } else {
+    return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
+  }
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
 
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
-  IH_CHECK((a.QH * a.HD) % 512 == 0, IH_EINVAL, "attention reduce: QH·HD must be a multiple of 512");
-  TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (a.HD + 2) * 4 + double(a.B) * a.QH * a.HD * 2);
-  attn_reduce_kernel<<<dim3(a.B, a.QH * a.HD / 512), 64, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.nkb);
+  IH_CHECK(a.QH % 4 == 0, IH_EINVAL, "attention reduce: the q head count must be a multiple of 4");
+  TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (2 * a.HD + 8) + double(a.B) * a.QH * a.HD * 2);
+  const dim3 grid(a.B, a.QH / 4);
+  if (a.HD == 128) attn_reduce_kernel<128><<<grid, 256, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.nkb);
+  else if (a.HD == 64) attn_reduce_kernel<64><<<grid, 256, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.nkb);
+  else return fail(IH_EINVAL, "attention reduce: head_dim must be 64 or 128");
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -14,7 +14,7 @@ struct AttnArgs {
   __half* ks;          // [KVH][cap]
   __half* vs;          // [KVH][cap]
   const float* sinks;  // [QH] natural-log logits or null
-  float* opart;        // [KVH][nsplit][Qpad][HD] (nsplit = launched splits)
+  __half* opart;       // [KVH][nsplit][Qpad][HD] fp16 O/l of each split (nsplit = launched splits)
   float2* ml;          // [KVH][nsplit][Qpad] (running max in log2 units, sum)
   int cap, ring, P, B, QH, KVH, HD, G, Qpad;
   int C, nsplit, s0, window, hadk;

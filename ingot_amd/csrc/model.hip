@@ -72,7 +72,7 @@ struct ih_model {
   // Activations: RMSNorm inputs bf16(h ⊙ w) with their sums of squares (attention / final norm, FFN norm), the
   // attention output and the gated activation.
   ActBuf act_attn, act_mlp, act_o, act_i;
-  float* opart = nullptr;
+  __half* opart = nullptr;
   float2* ml = nullptr;
   size_t part_splits = 0;    // splits the attention partials can hold
   int Qpad = 0, QP = 0;
@@ -349,18 +349,25 @@ size_t ih_model_weight_bytes(const ih_model* m) {
   return b;
 }
 
-int ih_kv_create(ih_model* m, int capacity, ih_kv** out) {
+int ih_kv_create(ih_model* m, int capacity, ih_kv** out) { return ih_kv_create_chunked(m, capacity, 0, out); }
+
+int ih_kv_create_chunked(ih_model* m, int capacity, int chunk, ih_kv** out) {
   IH_CHECK(m && out, IH_EINVAL, "ih_kv_create: null argument");
   IH_CHECK(capacity >= 1, IH_EINVAL, "ih_kv_create: capacity must be positive");
+  IH_CHECK(chunk == 0 || (chunk >= 32 && chunk % 16 == 0), IH_EINVAL,
+           "ih_kv_create_chunked: chunk must be 0 (automatic) or a multiple of 16, at least 32");
   *out = nullptr;
   const auto& d = m->d;
   ih_kv* kv = new ih_kv();
   kv->model = m;
   kv->cap = capacity;
-  // Key chunk: fixed per cache (so a row's result is the same for every block size and every position), at most
-  // about 64 splits at full capacity (256 … 2048 keys).
-  int C = 256;
-  while (C < 2048 && (capacity + C - 1) / C > 64) C *= 2;
+  // Key chunk: fixed per cache, so a row's result is the same for every block size and every position (the splits
+  // are fixed key ranges [s·C, (s+1)·C)). At full capacity the splits of all KV heads are one workgroup per CU: C =
+  // capacity / (CUs / KV heads), rounded up to 16 keys, at least 64.
+  const int per_head = std::max(1, m->ctx->cu_count / std::max(1, d.n_kv_heads));
+  int C = (capacity + per_head - 1) / per_head;
+  C = std::max(64, (C + 15) / 16 * 16);
+  if (chunk) C = chunk;
   kv->chunk = C;
   const int L = d.n_layers, KVH = d.n_kv_heads, HD = d.head_dim;
   kv->kc.assign(L, nullptr); kv->vc.assign(L, nullptr); kv->ks.assign(L, nullptr); kv->vs.assign(L, nullptr);

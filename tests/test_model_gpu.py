@@ -32,10 +32,10 @@ def within_tol(err, cos, scale):
     return err <= 0.02 + 0.01 * scale and cos >= 0.9999
 
 
-def make(ctx, shape, seed=7, kv_seed=11, P=100, cap=512, **extra):
+def make(ctx, shape, seed=7, kv_seed=11, P=100, cap=512, chunk=0, **extra):
     d = ModelDesc.make(**shape, **extra)
     m = Model(ctx, d, seed)
-    kv = KVCache(m, cap)
+    kv = KVCache(m, cap, chunk)
     kv.fill_synthetic(P, kv_seed)
     return d, m, kv
 
@@ -61,6 +61,30 @@ def test_verify_step_matches_oracle(ctx, shape, B):
                 assert top1[r] == ref_top1[r], (r, margin[r], err)
         assert np.array_equal(top1, np.argmax(logits, axis=1).astype(np.uint32))
         assert kv.pos == 100  # not advanced by the verify step
+    finally:
+        kv.free()
+        m.free()
+
+
+@pytest.mark.parametrize("shape", [SMALL, GQA8], ids=["gqa2-hd128", "gqa8-hd64"])
+@pytest.mark.parametrize("chunk", [48, 1024, 0])
+def test_verify_step_long_context_chunks(ctx, shape, chunk):
+    """P = 1500 with key chunks of 48 (31 splits, partial last 64-key block), 1024 (several LDS sub-chunks per split)
+    and automatic: the same oracle tolerance, and the three chunkings agree with each other within it."""
+    d, m, kv = make(ctx, shape, P=1500, cap=1600, chunk=chunk)
+    try:
+        if chunk:
+            assert kv.chunk == chunk
+        toks = np.random.default_rng(chunk + 1).integers(0, d.vocab, size=17).astype(np.uint32)
+        top1, logits = kv.verify(toks, want_logits=True)
+        ref_logits, ref_top1 = oracle.verify_dense(d, 7, 11, 1500, toks)
+        err, cos = logits_close(logits, ref_logits)
+        assert within_tol(err, cos, np.abs(ref_logits).max()), (err, cos)
+        srt = np.sort(ref_logits, axis=1)
+        margin = srt[:, -1] - srt[:, -2]
+        for r in range(17):
+            if margin[r] > 2 * err:
+                assert top1[r] == ref_top1[r], (r, margin[r], err)
     finally:
         kv.free()
         m.free()
