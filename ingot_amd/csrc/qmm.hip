@@ -272,7 +272,7 @@ __device__ __forceinline__ float glu_f(float g, float u, int act, float limit) {
 // 1 KB blocks), with the next block's loads in flight while the current one is multiplied. The KW partial sums are
 // added in wave order through LDS: no cross-workgroup synchronisation (an agent-scope fence on MI355X writes the
 // XCD's L2 back and costs tens of µs) and a summation order that depends only on (N, K).
-template <int T, int R, int KW, bool X16>
+template <int T, int R, int KW, bool X16, int NS>
 __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   // The wave index is uniform: readfirstlane keeps it (and the K-block loop) in scalar registers and scalar branches.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -303,22 +303,24 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
   const float qd0 = qd == 0 ? 1.f : 0.f;
 
-  QmmStage<T, R, X16> a, b;
+  // NS stages of loads in flight. This wave's K-blocks are wave, wave + KW, … (nk of them), NS per trip of a loop
+  // with a single exit (a loop with two exits is structurized into a join that the wait-count pass treats as a back
+  // edge with other stages' loads still pending, which serialises every trip). Stages past the end are loaded out of
+  // range: zero weights and scales, so their products add exact zeros (the count depends only on the shape).
+  QmmStage<T, R, X16> st[NS];
   int kb = wave;
-  qmm_load(a, p, rs, tile0, kb, lane, n);
-
-  // This wave's K-blocks: wave, wave + KW, … (nk of them), two per trip of a loop with a single exit (a loop with
-  // two exits is structurized into a join that the wait-count pass treats as a back edge with the other stage's loads
-  // still pending, which serialises every trip). Loads past the end read zeros.
+#pragma unroll
+  for (int s = 0; s < NS; ++s) qmm_load(st[s], p, rs, tile0, kb + s * KW, lane, n);
   const int nk = kb < p.nkb ? (p.nkb - kb + KW - 1) / KW : 0;
-  for (int it = 0; it < nk / 2; ++it) {
-    qmm_load(b, p, rs, tile0, kb + KW, lane, n);
-    qmm_compute(acc, acc16, a, km, kbias, qd0);
-    qmm_load(a, p, rs, tile0, kb + 2 * KW, lane, n);
-    qmm_compute(acc, acc16, b, km, kbias, qd0);
-    kb += 2 * KW;
+  const int trips = (nk + NS - 1) / NS;
+  for (int it = 0; it < trips; ++it) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      qmm_compute(acc, acc16, st[s], km, kbias, qd0);
+      qmm_load(st[s], p, rs, tile0, kb + (s + NS) * KW, lane, n);
+    }
+    kb += NS * KW;
   }
-  if (nk & 1) qmm_compute(acc, acc16, a, km, kbias, qd0);
 
   // RMSNorm factors of the input rows (the norm's sums of squares come in as partials of the producer's workgroups,
   // added here in a fixed order). After the K loop: loads with a data-dependent count ahead of it would make the
@@ -440,23 +442,30 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 
 // Launch shape for an (Npad, nkb) matrix: rows per workgroup (16·R) and waves per workgroup (KW, the intra-workgroup
 // split of K). Chosen from the shape only, never from M, so each row's summation order is fixed.
-struct QmmShape { int R, KW; };
+struct QmmShape { int R, KW, NS; };
 static QmmShape qmm_shape(int Npad, int nkb) {
   const int NT = Npad / 16;
-  if (NT >= 4096) return {4, 4};
-  if (NT >= 1024) return {2, 4};
-  if (NT >= 512 || nkb < 16) return {1, 4};
-  if (nkb < 64) return {1, 8};
-  return {1, 16};
+  if (NT >= 4096) return {4, 4, 2};
+  if (NT >= 1024) return {2, 4, 2};
+  if (NT >= 512 || nkb < 16) return {1, 4, 2};
+  if (nkb < 64) return {1, 8, 2};
+  return {1, 16, 2};
 }
 
 template <int T, bool X16>
 static void qmm_dispatch(QmmShape sh, int grid, hipStream_t st, const QmmParams& p) {
-  if (sh.R == 4) qmm_int4_kernel<T, 4, 4, X16><<<grid, 256, 0, st>>>(p);
-  else if (sh.R == 2) qmm_int4_kernel<T, 2, 4, X16><<<grid, 256, 0, st>>>(p);
-  else if (sh.KW == 4) qmm_int4_kernel<T, 1, 4, X16><<<grid, 256, 0, st>>>(p);
-  else if (sh.KW == 8) qmm_int4_kernel<T, 1, 8, X16><<<grid, 512, 0, st>>>(p);
-  else qmm_int4_kernel<T, 1, 16, X16><<<grid, 1024, 0, st>>>(p);
+#define IH_QMM_CASE(R_, KW_, NS_)                                                                  \
+  if (sh.R == R_ && sh.KW == KW_ && sh.NS == NS_) {                                                \
+    qmm_int4_kernel<T, R_, KW_, X16, NS_><<<grid, 64 * KW_, 0, st>>>(p);                            \
+    return;                                                                                        \
+  }
+  IH_QMM_CASE(4, 4, 2) IH_QMM_CASE(4, 4, 3)
+  IH_QMM_CASE(2, 4, 2) IH_QMM_CASE(2, 4, 3) IH_QMM_CASE(2, 4, 4)
+  IH_QMM_CASE(1, 4, 2) IH_QMM_CASE(1, 4, 4)
+  IH_QMM_CASE(1, 8, 2) IH_QMM_CASE(1, 8, 4)
+  IH_QMM_CASE(1, 16, 2) IH_QMM_CASE(1, 16, 4)
+#undef IH_QMM_CASE
+  qmm_int4_kernel<T, 1, 4, X16, 2><<<grid, 256, 0, st>>>(p);
 }
 
 int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
@@ -481,7 +490,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   IH_CHECK(M >= 1 && M <= MAX_TOK, IH_EINVAL, "qmm: M must be in 1..32");
   IH_CHECK(a.nkb == W->nkb && !a.f16, IH_EINVAL, "qmm: activation K does not match the matrix");
   QmmShape sh = qmm_shape(W->Npad, W->nkb);
-  if (const char* ov = getenv("IH_QMM_SHAPE")) sscanf(ov, "%d,%d", &sh.R, &sh.KW);  // tuning override
+  if (const char* ov = getenv("IH_QMM_SHAPE")) sscanf(ov, "%d,%d,%d", &sh.R, &sh.KW, &sh.NS);  // tuning override
   QmmParams p{};
   const size_t tiles_per_e = size_t(W->Npad / 16) * W->nkb;
   p.w = static_cast<const uint4*>(W->w) + tiles_per_e * 64 * expert;
