@@ -193,6 +193,34 @@ int ih_verify_and_accept(ih_model* model, ih_kv* kv, const uint32_t* tokens, int
 /* The model's device scratch of the last step: logits fp32 [rows ≥ B][vocab] (row stride = vocab). */
 const float* ih_model_logits_dev(const ih_model* model);
 
+/* ---- MXFP4 matrices and the MoE pieces (MoELayer.encode, Sources/Ingot/Layers/MoE.swift:346-428) ------------------ */
+
+/* MLX mxfp4 matrix: e2m1 codes uint32 [E][N][K/8] (8 per word, low nibble first) and e8m0 scales uint8 [E][N][K/32];
+ * w = 2^(s − 127) · e2m1(q) (Loader/Quant.swift:9-12,176-202; qmm_nax_moe.metal:280-288). K a multiple of 32.
+ * Replaces the MoE expert weights of MoELayer (MoE.swift:90-160). */
+int ih_qmat_mxfp4_create(ih_ctx* ctx, const uint32_t* w, const uint8_t* scales, int E, int N, int K, ih_qmat** out);
+int ih_qmat_mxfp4_create_dev(ih_ctx* ctx, const void* w_dev, const void* scales_dev, int E, int N, int K,
+                             ih_qmat** out);
+/* 0 = int4 g64, 1 = mxfp4, −1 for null. */
+int ih_qmat_format(const ih_qmat* q);
+/* y fp32 [M][ldy] = x [M][ldx] · dequant(W[expert])ᵀ for either format; x bf16 (fed to the MXFP4 product as fp16, as
+ * the reference's half activations, verify_nax.metal:78-79). The per-expert qmv of vnax_moe_gateup / down
+ * (verify_nax.metal:258-509) with every row routed to one expert. */
+int ih_qmm_expert(ih_ctx* ctx, const ih_qmat* W, int expert, const void* x_bf16_dev, int ldx, int M, float* y_dev,
+                  int ldy);
+/* vmoe_route (verify.metal:160-319): for each of `rows` rows of logits fp32 [rows][ldl] (+ bias [E] if not null, NaN →
+ * −inf), the top-k experts (ties to the lower index) and weights = softmax over the chosen logits (× pes[e] if not
+ * null); then the expert union by counting sort. Device outputs: nent[1] = U; entries [U][3] = (expert, first pair,
+ * pairs) in increasing expert order; x_row [rows·k] = the row of each pair (pairs in row order inside an expert);
+ * pair_w [rows·k]; row_pair [rows][k] = the pair of (row, slot). E ≤ 256, k ≤ 16, rows ≤ 32. */
+int ih_moe_route(ih_ctx* ctx, const float* logits_dev, int ldl, int rows, int E, int K, const float* bias_dev,
+                 const float* pes_dev, int* nent_dev, int* entries_dev, int* x_row_dev, float* pair_w_dev,
+                 int* row_pair_dev);
+/* The gathered per-expert product of a routed round (one launch for all experts, the union read on the device):
+ * y fp32 [pair][ldy] = x[x_row[pair]] · dequant(W[expert of pair])ᵀ, x bf16 [rows][ldx]. */
+int ih_qmm_gathered(ih_ctx* ctx, const ih_qmat* W, const void* x_bf16_dev, int ldx, int rows, int K_top,
+                    const int* nent_dev, const int* entries_dev, const int* x_row_dev, float* y_dev, int ldy);
+
 /* ---- Copy-from-context drafting (CopyIndex, Sources/Ingot/CopySpec.swift:15-139) ------------------------------
  * Rule: the current trigram is the last three tokens (ending at cur = n − 1). Among the three most recent earlier
  * ends p < cur of that trigram, take the longest backward match (at most max_match, at most p + 1 tokens), ties to the

@@ -91,6 +91,12 @@ def _declare(L: C.CDLL) -> None:
         "ih_verify_and_accept": (i32, [vp, vp, vp, i32, vp]),
         "ih_model_logits_dev": (vp, [vp]),
         "ih_kv_create_chunked": (i32, [vp, i32, i32, P(vp)]),
+        "ih_qmat_mxfp4_create": (i32, [vp, vp, vp, i32, i32, i32, P(vp)]),
+        "ih_qmat_mxfp4_create_dev": (i32, [vp, vp, vp, i32, i32, i32, P(vp)]),
+        "ih_qmat_format": (i32, [vp]),
+        "ih_qmm_expert": (i32, [vp, vp, i32, vp, i32, i32, vp, i32]),
+        "ih_moe_route": (i32, [vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp]),
+        "ih_qmm_gathered": (i32, [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, i32]),
         "ih_copy_index_create": (i32, [i32, i32, i32, P(vp)]),
         "ih_copy_index_free": (i32, [vp]),
         "ih_copy_index_append": (i32, [vp, vp, i32]),
@@ -192,6 +198,29 @@ class QMat:
         h = vp()
         check(lib().ih_qmat_int4_create(ctx.handle, ptr(w), ptr(s), ptr(b), E, N, K, C.byref(h)))
         return cls(ctx, h.value, N, K, E)
+
+    @classmethod
+    def mxfp4(cls, ctx: Context, w: np.ndarray, s: np.ndarray) -> "QMat":
+        """MLX mxfp4: codes uint32 [(E,) N, K/8], e8m0 scales uint8 [(E,) N, K/32]."""
+        w = np.ascontiguousarray(w, dtype=np.uint32)
+        s = np.ascontiguousarray(s, dtype=np.uint8)
+        E = 1 if w.ndim == 2 else w.shape[0]
+        N, K = w.shape[-2], w.shape[-1] * 8
+        h = vp()
+        check(lib().ih_qmat_mxfp4_create(ctx.handle, ptr(w), ptr(s), E, N, K, C.byref(h)))
+        return cls(ctx, h.value, N, K, E)
+
+    @property
+    def format(self) -> int:
+        return lib().ih_qmat_format(self.handle)
+
+    def expert(self, x_dev: "DeviceBuffer", M: int, expert: int = 0) -> np.ndarray:
+        """y = x[M, K] (bf16 on the device) · W[expert]ᵀ, fp32 [M, N]."""
+        y = self.ctx.buffer(M * self.N * 4)
+        check(lib().ih_qmm_expert(self.ctx.handle, self.handle, expert, x_dev.ptr, self.K, M, y.ptr, self.N))
+        out = y.download(np.float32, (M, self.N))
+        y.free()
+        return out
 
     @property
     def nbytes(self) -> int:
@@ -403,3 +432,44 @@ def copy_lookup_dev(ctx: "Context", hist_dev: "DeviceBuffer", n: int, max_k: int
     cnt = int(o[0])
     end = int(o[2]) if cnt else -1
     return [int(x) for x in o[4: 4 + cnt]], int(o[1]), end
+
+
+class Routing:
+    """Device outputs of ih_moe_route for `rows` rows and top-k."""
+
+    def __init__(self, ctx: Context, rows: int, K: int, E: int):
+        self.ctx, self.rows, self.K, self.E = ctx, rows, K, E
+        n = rows * K
+        self.nent = ctx.buffer(4)
+        self.entries = ctx.buffer(3 * max(E, 1) * 4)
+        self.x_row = ctx.buffer(n * 4)
+        self.pair_w = ctx.buffer(n * 4)
+        self.row_pair = ctx.buffer(n * 4)
+
+    def route(self, logits_dev: "DeviceBuffer", ldl: int, bias_dev=None, pes_dev=None) -> "Routing":
+        check(lib().ih_moe_route(self.ctx.handle, logits_dev.ptr, ldl, self.rows, self.E, self.K,
+                                 bias_dev.ptr if bias_dev is not None else None,
+                                 pes_dev.ptr if pes_dev is not None else None, self.nent.ptr, self.entries.ptr,
+                                 self.x_row.ptr, self.pair_w.ptr, self.row_pair.ptr))
+        return self
+
+    def download(self):
+        U = int(self.nent.download(np.int32, (1,))[0])
+        n = self.rows * self.K
+        return dict(U=U, entries=self.entries.download(np.int32, (self.E, 3))[:U],
+                    x_row=self.x_row.download(np.int32, (n,)), pair_w=self.pair_w.download(np.float32, (n,)),
+                    row_pair=self.row_pair.download(np.int32, (self.rows, self.K)))
+
+    def gathered(self, W: QMat, x_dev: "DeviceBuffer") -> np.ndarray:
+        """y [rows·k, N] fp32 of ih_qmm_gathered (by pair)."""
+        n = self.rows * self.K
+        y = self.ctx.buffer(n * W.N * 4).fill(0)
+        check(lib().ih_qmm_gathered(self.ctx.handle, W.handle, x_dev.ptr, W.K, self.rows, self.K, self.nent.ptr,
+                                    self.entries.ptr, self.x_row.ptr, y.ptr, W.N))
+        out = y.download(np.float32, (n, W.N))
+        y.free()
+        return out
+
+    def free(self) -> None:
+        for b in (self.nent, self.entries, self.x_row, self.pair_w, self.row_pair):
+            b.free()

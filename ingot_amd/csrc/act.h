@@ -26,6 +26,24 @@ __device__ __forceinline__ void frag_store_chunk(uint4* frag, int nkb, int tok, 
   frag[((size_t(tok) * nkb + kb) * 4 + qd) * 4 + t] = u;
 }
 
+// The same chunk as fp16 (round to nearest even): the activation of MXFP4 experts, whose MFMA runs in fp16.
+__device__ __forceinline__ void frag_store_chunk_f16(uint4* frag, int nkb, int tok, int c, const float (&v)[8]) {
+  if (c >= nkb * 16) return;
+  const int kb = c >> 4, w = c & 15, t = w >> 2, qd = w & 3;
+  auto h = [](float f) { return unsigned(__half_as_ushort(__float2half_rn(f))); };
+  uint4 u;
+  u.x = h(v[0]) | (h(v[4]) << 16);
+  u.y = h(v[1]) | (h(v[5]) << 16);
+  u.z = h(v[2]) | (h(v[6]) << 16);
+  u.w = h(v[3]) | (h(v[7]) << 16);
+  frag[((size_t(tok) * nkb + kb) * 4 + qd) * 4 + t] = u;
+}
+
+__device__ __forceinline__ void frag_store(bool f16, uint4* frag, int nkb, int tok, int c, const float (&v)[8]) {
+  if (f16) frag_store_chunk_f16(frag, nkb, tok, c, v);
+  else frag_store_chunk(frag, nkb, tok, c, v);
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Synthetic data: SplitMix64 streams keyed by (seed, tensor id). h(key, i) is output i of SplitMix64 seeded with key
 // (Sources/Ingot/Sampling.swift:50-62 is the reference's generator).

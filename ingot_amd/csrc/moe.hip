@@ -1,0 +1,616 @@
+// MoE block of the verify round on gfx950: MXFP4 weights, the router's top-k and expert union, the gathered per-expert
+// quantized matmuls (gate|up with the gated activation, down) and the slot-ordered combine with the residual.
+//
+// Reference: MoELayer.encode (Sources/Ingot/Layers/MoE.swift:346-428): router qmv → vmoe_route
+// (Sources/Ingot/Shaders/verify.metal:160-319) → vnax_moe_gateup (Shaders/verify_nax.metal:258-359) →
+// vnax_moe_down_split (:419-509) → vmoe_combine9 (:527-540); MXFP4 decode lab_e8m0x / lab_fp4x2
+// (Shaders/qmm_nax_moe.metal:280-288).
+//
+// MI355X design:
+//   - One launch covers every expert of the round: the grid is (row tiles, expert slots) with as many slots as the
+//     union can have (min(E, B·k)); a workgroup reads the union's size on the device and returns when its slot is
+//     unused, so the host never waits for the routing. A slot's tokens are gathered through a row map: the round's
+//     rows for gate|up, the expert's own pair rows for down.
+//   - Weights stream as 16-row × 128-K tiles, one 1024-byte dwordx4 load per wave and tile (the dense qmm's layout),
+//     K split over the waves of the workgroup and added in wave order in LDS.
+//   - int4 g64: bf16 MFMA on 128 + q with the affine map applied per group (as the dense qmm). MXFP4: an e2m1 code
+//     becomes its exact fp16 value with one v_perm_b32 table lookup per pair and the sign OR-ed in; the MFMA runs in
+//     fp16 against fp16 activations, and one e8m0 scale per 32 K (= one MFMA step) multiplies the step's products.
+#include "act.h"
+#include "ih_internal.h"
+#include "qmm_common.h"
+
+namespace ih {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------------------------------------------
+// Repack an MLX mxfp4 matrix (codes [E][N][K/8] u32, low nibble first; e8m0 scales [E][N][K/32] u8) into the tile
+// layout: codes exactly as the int4 tiles (pack_int4_kernel), scales one u32 per row and K-block holding the four
+// e8m0 bytes of its 32-K groups. Rows past N and groups past K read 0 (code 0 is +0). il8: interleave a gate|up pair
+// by eights as the int4 pack does. Grid (Npad/16 · nkb, E), 64 threads.
+__global__ void pack_mxfp4_kernel(const uint32_t* __restrict__ w, const uint8_t* __restrict__ s, uint4* __restrict__ wp,
+                                  uint32_t* __restrict__ sp, int N, int K, int Npad, int nkb, int il8) {
+  const int lane = threadIdx.x, n = lane & 15, qd = lane >> 4;
+  const int tile = blockIdx.x / nkb, kb = blockIdx.x % nkb, e = blockIdx.y;
+  const int prow = tile * 16 + n;
+  const int row = il8 ? (n < 8 ? 8 * tile + n : N / 2 + 8 * tile + n - 8) : prow;
+  const bool live = il8 ? (8 * tile + (n & 7) < N / 2) : row < N;
+  const int wpr = K / 8, gpr = K / 32;
+  const size_t ebase_w = size_t(e) * N * wpr, ebase_s = size_t(e) * N * gpr;
+  unsigned v[4];
+  for (int t = 0; t < 4; ++t) {
+    const int wi = kb * 16 + 4 * t + qd;
+    v[t] = (live && wi < wpr) ? w[ebase_w + size_t(row) * wpr + wi] : 0u;
+  }
+  const size_t tb = (size_t(e) * (Npad / 16) + tile) * nkb + kb;
+  wp[tb * 64 + lane] = make_uint4(v[0], v[1], v[2], v[3]);
+  if (qd == 0) {
+    unsigned sc = 0;
+    for (int g = 0; g < 4; ++g) {
+      const int gi = 4 * kb + g;
+      if (live && gi < gpr) sc |= unsigned(s[ebase_s + size_t(row) * gpr + gi]) << (8 * g);
+    }
+    sp[tb * 16 + n] = sc;
+  }
+}
+
+// Eight e2m1 codes of one word → eight fp16 values in the element order {0,4,1,5,2,6,3,7}: pair c = (code c, code
+// c+4) = bits (4c, 4c+16) of w >> 4c. The magnitude (3 bits) selects the fp16 high byte from the table {0x00, 0x38,
+// 0x3C, 0x3E, 0x40, 0x42, 0x44, 0x46} (0, .5, 1, 1.5, 2, 3, 4, 6; low bytes are 0) with one v_perm_b32; the sign bit
+// goes to bit 15.
+__device__ __forceinline__ f16x8 e2m1_f16(unsigned w) {
+  u32x4 v;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const unsigned x = w >> (4 * c);
+    const unsigned sel = ((x & 0x00070007u) << 8) | 0x000C000Cu;  // bytes 1, 3 ← table[m]; bytes 0, 2 ← 0
+    const unsigned mag = __builtin_amdgcn_perm(0x46444240u, 0x3E3C3800u, sel);
+    v[c] = mag | ((x & 0x00080008u) << 12);
+  }
+  return __builtin_bit_cast(f16x8, v);
+}
+
+// 2^(e − 127) for an e8m0 byte (255 → NaN), exact in fp32 (e = 0 → 2^-127, a subnormal).
+__device__ __forceinline__ float e8m0f(unsigned e) {
+  return e == 0 ? __uint_as_float(0x00400000u) : (e == 255 ? __uint_as_float(0x7FC00000u) : __uint_as_float(e << 23));
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+enum GatherMode : int {
+  GM_F32 = 0,   // y[pair][row] = r · v
+  GM_GLU = 1,   // gated activation of the interleaved gate|up pair (r · v + bias) → h fragment of the pair
+  GM_DOWN = 2,  // y[pair][row] = v + bias
+};
+
+struct GatherParams {
+  const uint4* w;          // all experts' tiles
+  const void* s;           // all experts' scales (int4: uint2 per row, mxfp4: u32 per row)
+  unsigned tiles_per_e;    // (Npad / 16) · nkb
+  unsigned E;
+  const uint4* xa;         // activation fragments (bf16 for int4, fp16 for mxfp4)
+  int x_nkb, x_tokens;     // fragment K-blocks; tokens the fragment buffer holds
+  const int* x_row;        // pair → activation row (null: the pair index itself)
+  const int* entries;      // [U][3] (expert, first pair, pairs); null: one entry (dense_e, 0, M)
+  const int* nent;         // U on the device (null: 1)
+  int dense_e, M;
+  int N, Npad, nkb, mode;
+  void* y;
+  int ldy;
+  // RMSNorm factor of the activation rows (router and gate|up): r_t = 1/sqrt(Σ ss_in[j][t] / D + eps).
+  const float* ss_in;
+  int nss_in, D, nrows;
+  float eps;
+  uint4* h_out;            // GM_GLU: next activation (fragments), by pair
+  int h_nkb, h_f16, glu;
+  float limit;
+  const uint16_t* bias;    // bf16; GM_GLU: [E][2·(N/2)] gate then up; GM_DOWN: [E][N]; null: none
+  unsigned kmask, kbias;
+};
+
+constexpr int GKW = 4;  // waves per workgroup (K split)
+
+template <int FMT>
+struct GStage {
+  u32x4 w;
+  uint2 s;     // int4: (s0|b0<<16, s1|b1<<16); mxfp4: .x = four e8m0 bytes
+  u32x4 x[2][4];
+};
+
+// Rows × (one slot of the round): grid (Npad/16, slots), 64·GKW threads.
+template <int FMT>
+__global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
+  const int u = blockIdx.y;
+  const int U = p.nent ? __builtin_amdgcn_readfirstlane(p.nent[0]) : 1;
+  if (u >= U) return;
+  int e, start, cnt;
+  if (p.entries) {
+    e = p.entries[3 * u];
+    start = p.entries[3 * u + 1];
+    cnt = p.entries[3 * u + 2];
+  } else {
+    e = p.dense_e;
+    start = 0;
+    cnt = p.M;
+  }
+  e = __builtin_amdgcn_readfirstlane(e);
+  start = __builtin_amdgcn_readfirstlane(start);
+  cnt = __builtin_amdgcn_readfirstlane(cnt);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int n = lane & 15, qd = lane >> 4;
+  const int tile = blockIdx.x;
+  const bool two = cnt > 16;  // second token tile (uniform)
+  __shared__ float rsc[MAX_TOK];
+  __shared__ int arow_s[MAX_TOK];
+
+  const size_t tb0 = size_t(e) * p.tiles_per_e + size_t(tile) * p.nkb;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + tb0 * 64, unsigned(p.nkb) * 1024u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.s) + tb0 * (FMT == QF_INT4 ? 128 : 64),
+                                              unsigned(p.nkb) * (FMT == QF_INT4 ? 128u : 64u));
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.xa, unsigned(p.x_tokens) * p.x_nkb * 256u);
+  unsigned xoff[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int j = 16 * tt + n;
+    const int ar = j < cnt ? (p.x_row ? p.x_row[start + j] : start + j) : -1;
+    xoff[tt] = ar >= 0 ? unsigned(ar) * p.x_nkb * 256u + qd * 64u : OOB;
+  }
+  if (threadIdx.x < MAX_TOK) {
+    const int j = threadIdx.x;
+    arow_s[j] = j < cnt ? (p.x_row ? p.x_row[start + j] : start + j) : 0;
+  }
+
+  auto load = [&](GStage<FMT>& st, int kb) {
+    const unsigned oob = kb < p.nkb ? 0u : OOB;
+    __builtin_amdgcn_sched_barrier(0);
+    st.w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (kb * 1024u + lane * 16u) | oob, 0, 0));
+    if constexpr (FMT == QF_INT4)
+      st.s = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, (kb * 128u + n * 8u) | oob, 0, 0));
+    else
+      st.s.x = __builtin_amdgcn_raw_buffer_load_b32(rs, (kb * 64u + n * 4u) | oob, 0, 0);
+    const unsigned kx = unsigned(kb) * 256u;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      st.x[0][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xoff[0] + kx + 16 * t) | oob, 0, 0));
+      st.x[1][t] = two ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xoff[1] + kx + 16 * t) | oob, 0, 0))
+                       : u32x4{0u, 0u, 0u, 0u};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
+  auto compute = [&](const GStage<FMT>& st) {
+    if constexpr (FMT == QF_INT4) {
+      const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+      const float s0 = bf16f(st.s.x & 0xFFFFu), s1 = bf16f(st.s.y & 0xFFFFu);
+      const float c0 = fmaf(-128.f, s0, bf16f(st.s.x >> 16)), c1 = fmaf(-128.f, s1, bf16f(st.s.y >> 16));
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const bf16x8 w0 = nib_bf16(st.w[2 * g], km, kbias), w1 = nib_bf16(st.w[2 * g + 1], km, kbias);
+        const float sg = g ? s1 : s0, cg = g ? c1 : c0;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          if (tt == 1 && !two) continue;
+          f32x4 xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g]), ones,
+                                                             f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), ones, xs, 0, 0,
+                                                       0);
+          f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g]), w0,
+                                                              f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), w1, tmp, 0, 0,
+                                                        0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[tt][q] = fmaf(sg, tmp[q], fmaf(cg, xs[q], acc[tt][q]));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const f16x8 wf = e2m1_f16(st.w[t]);
+        const float sc = e8m0f((st.s.x >> (8 * t)) & 0xFFu);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          if (tt == 1 && !two) continue;
+          const f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, st.x[tt][t]), wf,
+                                                                   f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[tt][q] = fmaf(sc, tmp[q], acc[tt][q]);
+        }
+      }
+    }
+  };
+
+  // K-blocks wave, wave + GKW, …; two stages; single-exit loop (loads past the end read zeros).
+  GStage<FMT> a, b;
+  int kb = wave;
+  load(a, kb);
+  const int nk = kb < p.nkb ? (p.nkb - kb + GKW - 1) / GKW : 0;
+  for (int it = 0; it < nk / 2; ++it) {
+    load(b, kb + GKW);
+    compute(a);
+    load(a, kb + 2 * GKW);
+    compute(b);
+    kb += 2 * GKW;
+  }
+  if (nk & 1) compute(a);
+
+  // RMSNorm factors of the activation rows.
+  if (p.ss_in) {
+    for (int t = wave; t < p.nrows; t += GKW) {
+      float ss = 0.f;
+      for (int j = lane; j < p.nss_in; j += 64) ss += p.ss_in[j * MAX_TOK + t];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+      if (lane == 0) rsc[t] = 1.0f / sqrtf(ss / float(p.D) + p.eps);
+    }
+  }
+
+  // Waves' partial sums → LDS [wave][tt][q][lane], then added in wave order.
+  __shared__ float red[GKW * 2 * 4 * 64];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[((wave * 2 + tt) * 4 + q) * 64 + lane] = acc[tt][q];
+  __syncthreads();
+  auto val = [&](int j, int rn) {
+    const int tt = j >> 4, jj = j & 15;
+    const int i = (tt * 4 + (jj & 3)) * 64 + 16 * (jj >> 2) + rn;
+    float v = red[i];
+#pragma unroll
+    for (int w = 1; w < GKW; ++w) v += red[w * 2 * 4 * 64 + i];
+    return v;
+  };
+  const int nthr = 64 * GKW;
+  if (p.mode == GM_GLU) {
+    // Interleaved tile: rows 0–7 gate, 8–15 up of the same 8 columns (output chunk `tile`).
+    const int I = p.N / 2;
+    for (int j = threadIdx.x; j < cnt; j += nthr) {
+      const float r = p.ss_in ? rsc[arow_s[j]] : 1.f;
+      float v[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int col = 8 * tile + c;
+        float g = val(j, c) * r, uu = val(j, 8 + c) * r;
+        if (p.bias && col < I) {
+          g += bf16f(p.bias[size_t(e) * 2 * I + col]);
+          uu += bf16f(p.bias[size_t(e) * 2 * I + I + col]);
+        }
+        v[c] = col < I ? glu_f(g, uu, p.glu, p.limit) : 0.f;
+      }
+      if (8 * tile < I) frag_store(p.h_f16 != 0, p.h_out, p.h_nkb, start + j, tile, v);
+    }
+    return;
+  }
+  for (int q = threadIdx.x; q < cnt * 16; q += nthr) {
+    const int j = q >> 4, rn = q & 15;
+    const int row = tile * 16 + rn;
+    if (row >= p.N) continue;
+    float v = val(j, rn);
+    if (p.mode == GM_F32 && p.ss_in) v *= rsc[arow_s[j]];
+    if (p.mode == GM_DOWN && p.bias) v += bf16f(p.bias[size_t(e) * p.N + row]);
+    static_cast<float*>(p.y)[size_t(start + j) * p.ldy + row] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Routing of the round (vmoe_route, verify.metal:160-319; RouterVector.reference, KernelCaseRouter.swift:54-80):
+// logits + router bias (NaN → −inf); top-k by value, ties to the lower expert index; weights = softmax over the chosen
+// logits, times an optional per-expert scale. Then the expert union by counting sort: entries (expert, first pair, pairs) in increasing expert order,
+// pairs in row order inside an expert; x_row[pair] = its row, pair_w[pair] = its weight, row_pair[row·k + slot] = its
+// pair. One workgroup of 256 threads (E ≤ 256, k ≤ 16, rows ≤ 32).
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int ldl, int rows, int E, int K,
+                                                        const float* __restrict__ bias, const float* __restrict__ pes,
+                                                        int* __restrict__ nent,
+                                                        int* __restrict__ entries, int* __restrict__ x_row,
+                                                        float* __restrict__ pair_w, int* __restrict__ row_pair) {
+  __shared__ int inds[MAX_TOK * 16];
+  __shared__ float wts[MAX_TOK * 16];
+  __shared__ int cnt_s[256], start_s[256], slot_s[256];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int r = wave; r < rows; r += 4) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ex = lane + 64 * i;
+      float x = -INFINITY;
+      if (ex < E) {
+        x = logits[size_t(r) * ldl + ex] + (bias ? bias[ex] : 0.f);
+        if (x != x) x = -INFINITY;
+      }
+      v[i] = x;
+    }
+    float chosen[16];
+    unsigned taken = 0;  // bit i: expert lane + 64·i already chosen
+    for (int k = 0; k < K; ++k) {
+      // Best untaken expert of this lane (value, then lower index), then of the wave. A −inf logit (or NaN) still
+      // ranks, so rows with fewer than k finite logits pick the lowest remaining indices.
+      float bv = -INFINITY;
+      int bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ex = lane + 64 * i;
+        if (ex < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && ex < bi))) {
+          bv = v[i];
+          bi = ex;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      chosen[k] = bv;
+      if (lane == 0) inds[r * K + k] = bi;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (lane + 64 * i == bi) taken |= 1u << i;
+    }
+    if (lane == 0) {
+      float sum = 0.f;
+      for (int k = 0; k < K; ++k) sum += expf(chosen[k] - chosen[0]);
+      for (int k = 0; k < K; ++k)
+        wts[r * K + k] = expf(chosen[k] - chosen[0]) / sum * (pes ? pes[inds[r * K + k]] : 1.0f);
+    }
+  }
+  __syncthreads();
+  // Counting sort by expert: thread ex counts its pairs; exclusive scans give the first pair and the entry slot.
+  const int nrk = rows * K;
+  int c = 0;
+  if (tid < E)
+    for (int i = 0; i < nrk; ++i) c += inds[i] == tid;
+  cnt_s[tid] = tid < E ? c : 0;
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0, slot = 0;
+    for (int ex = 0; ex < E; ++ex) {
+      start_s[ex] = off;
+      slot_s[ex] = slot;
+      off += cnt_s[ex];
+      slot += cnt_s[ex] > 0;
+    }
+    nent[0] = slot;
+  }
+  __syncthreads();
+  if (tid < E && c > 0) {
+    const int st = start_s[tid], sl = slot_s[tid];
+    entries[3 * sl] = tid;
+    entries[3 * sl + 1] = st;
+    entries[3 * sl + 2] = c;
+    int j = 0;
+    for (int i = 0; i < nrk; ++i)
+      if (inds[i] == tid) {
+        const int pr = st + j++;
+        x_row[pr] = i / K;
+        pair_w[pr] = wts[i];
+        row_pair[i] = pr;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Combine (vmoe_combine9, verify_nax.metal:527-540) fused with the residual and the next RMSNorm input: for row r,
+// y = Σ_slot w·o[pair(r, slot)] in slot order, h[r] += y, the next activation (h ⊙ nw, bf16 or fp16) and Σh² (one
+// partial per row). Grid (rows), 256 threads; one thread per 8 columns.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ o, int ldo, const int* __restrict__ row_pair,
+                                                          const float* __restrict__ pair_w, int K, float* __restrict__ h,
+                                                          int ldh, int H, const uint16_t* __restrict__ nw,
+                                                          uint4* __restrict__ act, int act_nkb, int act_f16,
+                                                          float* __restrict__ ss_out) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int col = 8 * c + j;
+      float y = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const int pr = row_pair[r * K + k];
+        y += pair_w[pr] * o[size_t(pr) * ldo + col];
+      }
+      const float hv = h[size_t(r) * ldh + col] + y;
+      h[size_t(r) * ldh + col] = hv;
+      ss += hv * hv;
+      v[j] = hv * bf16f(nw[col]);
+    }
+    frag_store(act_f16 != 0, act, act_nkb, r, c, v);
+  }
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  if (threadIdx.x == 0) ss_out[r] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Host side.
+
+int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slots, double bytes) {
+  GatherParams p = base;
+  p.w = static_cast<const uint4*>(W->w);
+  p.s = W->s;
+  p.tiles_per_e = unsigned(W->Npad / 16) * unsigned(W->nkb);
+  p.E = unsigned(W->E);
+  p.N = W->N;
+  p.Npad = W->Npad;
+  p.nkb = W->nkb;
+  p.kmask = 0x000F000Fu;
+  p.kbias = 0x43004300u;
+  IH_CHECK(p.x_nkb == W->nkb, IH_EINVAL, "gathered qmm: activation K does not match the matrix");
+  IH_CHECK(size_t(W->E) * p.tiles_per_e * 1024u < (size_t(1) << 31), IH_EINVAL,
+           "gathered qmm: stacked matrix above 2 GiB");
+  TimedLaunch tl(c, TC_MOE, bytes);
+  const dim3 grid(W->Npad / 16, slots);
+  if (W->format == QF_INT4) qmm_gather_kernel<QF_INT4><<<grid, 64 * GKW, 0, c->stream>>>(p);
+  else qmm_gather_kernel<QF_MXFP4><<<grid, 64 * GKW, 0, c->stream>>>(p);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K, const float* bias,
+                     const float* pes, int* nent, int* entries, int* x_row, float* pair_w, int* row_pair) {
+  IH_CHECK(E >= 1 && E <= 256 && K >= 1 && K <= 16 && K <= E && rows >= 1 && rows <= MAX_TOK, IH_EINVAL,
+           "moe route: need E ≤ 256, 1 ≤ k ≤ min(16, E), 1 ≤ rows ≤ 32");
+  TimedLaunch tl(c, TC_MOE, double(rows) * E * 4);
+  moe_route_kernel<<<1, 256, 0, c->stream>>>(logits, ldl, rows, E, K, bias, pes, nent, entries, x_row, pair_w,
+                                             row_pair);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, const float* pair_w, int K, int rows,
+                       float* h, int H, const uint16_t* nw, ActBuf& act) {
+  IH_CHECK(H % 8 == 0, IH_EINVAL, "moe combine: hidden size must be a multiple of 8");
+  TimedLaunch tl(c, TC_MOE, double(rows) * H * (4.0 * K + 8 + 2));
+  moe_combine_kernel<<<rows, 256, 0, c->stream>>>(o, ldo, row_pair, pair_w, K, h, H, H, nw,
+                                                  static_cast<uint4*>(act.frag), act.nkb, act.f16 ? 1 : 0, act.ss);
+  IH_HIP(hipGetLastError());
+  act.nss = 1;
+  return IH_OK;
+}
+
+int pack_mxfp4(ih_ctx* c, ih_qmat* q, const uint32_t* w, const uint8_t* s) {
+  dim3 grid((q->Npad / 16) * q->nkb, q->E);
+  pack_mxfp4_kernel<<<grid, 64, 0, c->stream>>>(w, s, static_cast<uint4*>(q->w), static_cast<uint32_t*>(q->s), q->N,
+                                                q->K, q->Npad, q->nkb, q->il8);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int qmat_mxfp4_create_dev(ih_ctx* c, const void* w, const void* s, int E, int N, int K, int il8, ih_qmat** out) {
+  IH_CHECK(c && w && s && out, IH_EINVAL, "ih_qmat_mxfp4_create_dev: null argument");
+  IH_CHECK(E >= 1 && N >= 1 && K >= 32 && K % 32 == 0, IH_EINVAL,
+           "ih_qmat_mxfp4_create_dev: need E, N ≥ 1 and K a positive multiple of 32");
+  IH_CHECK(!il8 || N % 16 == 0, IH_EINVAL, "qmat: an interleaved gate|up matrix needs N a multiple of 16");
+  *out = nullptr;
+  ih_qmat* q = new ih_qmat();
+  q->ctx = c;
+  q->format = QF_MXFP4;
+  q->E = E;
+  q->N = N;
+  q->K = K;
+  q->Npad = (N + 255) / 256 * 256;
+  q->nkb = (K + KBLK - 1) / KBLK;
+  q->ktail = (K % KBLK) ? 1 : 0;
+  q->il8 = il8;
+  q->algo_bytes = size_t(N) * K / 2 + size_t(N) * (K / 32);
+  const size_t tiles = size_t(E) * (q->Npad / 16) * q->nkb;
+  q->wbytes = tiles * 1024;
+  q->sbytes = tiles * 64;
+  int st = IH_OK;
+  if (hipMalloc(&q->w, q->wbytes) != hipSuccess || hipMalloc(&q->s, q->sbytes) != hipSuccess)
+    st = fail(IH_ENOMEM, "ih_qmat_mxfp4_create_dev: allocation failed");
+  if (st == IH_OK) st = pack_mxfp4(c, q, static_cast<const uint32_t*>(w), static_cast<const uint8_t*>(s));
+  if (st != IH_OK) {
+    ih_qmat_free(q);
+    return st;
+  }
+  *out = q;
+  return IH_OK;
+}
+
+// Natural bf16 rows → fragments (bf16 or fp16 elements). Grid (tokens), 256 threads.
+__global__ void act_gather_kernel(const uint16_t* __restrict__ x, int ldx, int M, int K, int nkb, int f16,
+                                  uint4* __restrict__ frag) {
+  const int i = blockIdx.x;
+  for (int cc = threadIdx.x; cc < nkb * 16; cc += blockDim.x) {
+    float v[8];
+    const bool valid = i < M && cc < K / 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = valid ? bf16f(x[size_t(i) * ldx + 8 * cc + e]) : 0.f;
+    frag_store(f16 != 0, frag, nkb, i, cc, v);
+  }
+}
+
+int stage_act_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, int K, bool f16, ActBuf& a) {
+  IH_TRY(ensure_act(c, a, K, f16));
+  act_gather_kernel<<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, K, a.nkb, f16 ? 1 : 0, static_cast<uint4*>(a.frag));
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+}  // namespace ih
+
+using namespace ih;
+
+extern "C" {
+
+int ih_qmat_mxfp4_create_dev(ih_ctx* c, const void* w, const void* s, int E, int N, int K, ih_qmat** out) {
+  return qmat_mxfp4_create_dev(c, w, s, E, N, K, 0, out);
+}
+
+int ih_qmat_mxfp4_create(ih_ctx* c, const uint32_t* w, const uint8_t* s, int E, int N, int K, ih_qmat** out) {
+  IH_CHECK(c && w && s && out, IH_EINVAL, "ih_qmat_mxfp4_create: null argument");
+  IH_CHECK(E >= 1 && N >= 1 && K >= 32 && K % 32 == 0, IH_EINVAL,
+           "ih_qmat_mxfp4_create: need E, N ≥ 1 and K a positive multiple of 32");
+  const size_t wb = size_t(E) * N * (K / 8) * 4, sb = size_t(E) * N * (K / 32);
+  void *dw = nullptr, *ds = nullptr;
+  int st = IH_OK;
+  if (hipMalloc(&dw, wb) != hipSuccess || hipMalloc(&ds, sb) != hipSuccess)
+    st = fail(IH_ENOMEM, "ih_qmat_mxfp4_create: staging allocation failed");
+  if (st == IH_OK && (hipMemcpyAsync(dw, w, wb, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+                      hipMemcpyAsync(ds, s, sb, hipMemcpyHostToDevice, c->stream) != hipSuccess))
+    st = fail(IH_EDEVICE, "ih_qmat_mxfp4_create: upload failed");
+  if (st == IH_OK) st = ih_qmat_mxfp4_create_dev(c, dw, ds, E, N, K, out);
+  (void)hipStreamSynchronize(c->stream);
+  if (dw) (void)hipFree(dw);
+  if (ds) (void)hipFree(ds);
+  return st;
+}
+
+int ih_qmat_format(const ih_qmat* q) { return q ? q->format : -1; }
+
+int ih_qmm_expert(ih_ctx* c, const ih_qmat* W, int expert, const void* x, int ldx, int M, float* y, int ldy) {
+  IH_CHECK(c && W && x && y, IH_EINVAL, "ih_qmm_expert: null argument");
+  IH_CHECK(M >= 1 && M <= MAX_TOK, IH_EINVAL, "ih_qmm_expert: M must be in 1..32");
+  IH_CHECK(expert >= 0 && expert < W->E, IH_EINVAL, "ih_qmm_expert: expert out of range");
+  IH_CHECK(ldx >= W->K && ldy >= W->N, IH_EINVAL, "ih_qmm_expert: leading dimension smaller than the row");
+  const bool f16 = W->format == QF_MXFP4;
+  IH_TRY(stage_act_bf16(c, static_cast<const uint16_t*>(x), ldx, M, W->K, f16, c->act));
+  GatherParams p{};
+  p.xa = static_cast<const uint4*>(c->act.frag);
+  p.x_nkb = c->act.nkb;
+  p.x_tokens = MAX_TOK;
+  p.dense_e = expert;
+  p.M = M;
+  p.mode = GM_F32;
+  p.y = y;
+  p.ldy = ldy;
+  return launch_gather(c, W, p, 1, double(W->algo_bytes) + double(M) * W->K * 2 + double(M) * W->N * 4);
+}
+
+int ih_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K, const float* bias, const float* pes,
+                 int* nent, int* entries, int* x_row, float* pair_w, int* row_pair) {
+  IH_CHECK(c && logits && nent && entries && x_row && pair_w && row_pair, IH_EINVAL, "ih_moe_route: null argument");
+  IH_CHECK(ldl >= E, IH_EINVAL, "ih_moe_route: ldl < E");
+  return launch_moe_route(c, logits, ldl, rows, E, K, bias, pes, nent, entries, x_row, pair_w, row_pair);
+}
+
+int ih_qmm_gathered(ih_ctx* c, const ih_qmat* W, const void* x, int ldx, int rows, int K_top, const int* nent,
+                    const int* entries, const int* x_row, float* y, int ldy) {
+  IH_CHECK(c && W && x && nent && entries && x_row && y, IH_EINVAL, "ih_qmm_gathered: null argument");
+  IH_CHECK(rows >= 1 && rows <= MAX_TOK && K_top >= 1 && K_top <= 16, IH_EINVAL,
+           "ih_qmm_gathered: rows must be in 1..32 and k in 1..16");
+  IH_CHECK(ldx >= W->K && ldy >= W->N, IH_EINVAL, "ih_qmm_gathered: leading dimension smaller than the row");
+  const bool f16 = W->format == QF_MXFP4;
+  IH_TRY(stage_act_bf16(c, static_cast<const uint16_t*>(x), ldx, rows, W->K, f16, c->act));
+  GatherParams p{};
+  p.xa = static_cast<const uint4*>(c->act.frag);
+  p.x_nkb = c->act.nkb;
+  p.x_tokens = MAX_TOK;
+  p.x_row = x_row;
+  p.entries = entries;
+  p.nent = nent;
+  p.mode = GM_F32;
+  p.y = y;
+  p.ldy = ldy;
+  const int slots = std::min(W->E, rows * K_top);
+  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots);
+}
+
+}  // extern "C"

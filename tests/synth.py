@@ -63,3 +63,12 @@ def zipf_context(seed: int, n: int = 131072, vocab: int = 151936, s: float = 1.1
         h[dst:dst + span_len] = h[src:src + span_len]
     h[body:] = h[src:src + tail]
     return h, src
+
+
+def mxfp4_matrix(g: np.random.Generator, N: int, K: int, E: int | None = None, lo: int = 119, hi: int = 125):
+    """MLX mxfp4: uniform e2m1 codes (8 per uint32, low nibble first), e8m0 scales uniform in [lo, hi]
+    (2^-8 … 2^-2 by default)."""
+    shape = (N, K) if E is None else (E, N, K)
+    q = g.integers(0, 16, size=shape, dtype=np.uint32)
+    s = g.integers(lo, hi + 1, size=shape[:-1] + (K // 32,), dtype=np.uint8)
+    return pack_nibbles(q), s
