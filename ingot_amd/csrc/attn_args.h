@@ -16,7 +16,7 @@ struct AttnArgs {
   const float* sinks;  // [QH] natural-log logits or null
   __half* opart;       // [KVH][nsplit][Qpad][HD] fp16 O/l of each split (nsplit = launched splits)
   float2* ml;          // [KVH][nsplit][Qpad] (running max in log2 units, sum)
-  int cap, ring, P, B, QH, KVH, HD, G, Qpad;
+  int cap, ring, P, B, QH, KVH, HD, G, Qpad;  // cap: slots per head (the ring size of a sliding-window layer)
   int C, nsplit, s0, window, hadk;
   float theta, scale_log2;
 };

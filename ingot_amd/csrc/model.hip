@@ -22,6 +22,9 @@ int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1,
 int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_t K, uint64_t seed, uint64_t tensor,
                float sd);
 int synth_bf16(ih_ctx* c, uint16_t* out, size_t n, uint64_t seed, uint64_t tensor, float base, float amp);
+int synth_mxfp4(ih_ctx* c, uint32_t* w, uint8_t* s, size_t N, size_t K, uint64_t seed, uint64_t tensor);
+int qmat_mxfp4_create_dev(ih_ctx* c, const void* w, const void* s, int E, int N, int K, int il8, ih_qmat** out);
+struct GatherParams;
 int synth_f32(ih_ctx* c, float* out, size_t n, uint64_t seed, uint64_t tensor, float base, float amp);
 int synth_kv(ih_ctx* c, int8_t* kc, int8_t* vc, __half* ks, __half* vs, int KVH, int HD, int cap, int ring, int pos0,
              int npos, uint64_t seed, uint64_t tensor);
@@ -29,11 +32,27 @@ int synth_kv(ih_ctx* c, int8_t* kc, int8_t* vc, __half* ks, __half* vs, int KVH,
 int launch_prework(ih_ctx* c, const AttnArgs& a);
 int launch_attention(ih_ctx* c, const AttnArgs& a);
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out);
+int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K, const float* bias,
+                     const float* pes, int* nent, int* entries, int* x_row, float* pair_w, int* row_pair);
+int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, const float* pair_w, int K, int rows,
+                       float* h, int H, const uint16_t* nw, ActBuf& act);
+int launch_moe_router(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, float eps, float* logits, int ldl);
+int launch_moe_gate_up(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, int K_top, float eps,
+                       const int* nent, const int* entries, const int* x_row, const uint16_t* bias, int glu,
+                       float limit, void* h_frag, int h_nkb, int h_tokens, bool h_f16);
+int launch_moe_down(ih_ctx* c, const ih_qmat* W, const void* h_frag, int h_nkb, int h_tokens, bool h_f16, int rows,
+                    int K_top, const int* nent, const int* entries, const uint16_t* bias, float* o, int ldo);
 
 // Tensor ids of the synthetic model (the generator's stream keys): globals, then 100 per layer.
 enum : uint64_t { T_EMBED = 1, T_FINAL_NORM = 2, T_HEAD = 3 };
-enum : uint64_t { L_ATTN_NORM = 0, L_QKV = 1, L_O = 2, L_MLP_NORM = 3, L_GATE_UP = 4, L_DOWN = 5, L_SINKS = 9 };
+enum : uint64_t { L_ATTN_NORM = 0, L_QKV = 1, L_O = 2, L_MLP_NORM = 3, L_GATE_UP = 4, L_DOWN = 5, L_ROUTER = 6,
+                  L_ROUTER_BIAS = 7, L_SINKS = 9 };
 constexpr uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
+// Experts: 3·10^6 + 10^4·layer + 10^3·kind + expert (kinds: gate|up, down, gate|up bias, down bias).
+enum : uint64_t { X_GATE_UP = 0, X_DOWN = 1, X_GU_BIAS = 2, X_DOWN_BIAS = 3 };
+constexpr uint64_t expert_tensor(int l, uint64_t kind, int e) {
+  return 3000000 + 10000 * uint64_t(l) + 1000 * kind + uint64_t(e);
+}
 constexpr uint64_t kv_tensor(int l) { return 500000 + uint64_t(l); }
 constexpr float W_SD = 0.02f;  // |N(0, 0.02)| scales
 
@@ -47,8 +66,14 @@ struct ih_layer {
   float* sinks = nullptr;
   ih_qmat* qkv = nullptr;
   ih_qmat* o = nullptr;
+  // Dense FFN: gate|up [2I][H] (interleaved by eights), down [H][I]. MoE: the same, stacked over E experts (I = the
+  // expert intermediate), plus the router [E][H] in the experts' format and the optional biases.
   ih_qmat* gate_up = nullptr;
   ih_qmat* down = nullptr;
+  ih_qmat* router = nullptr;
+  float* router_bias = nullptr;   // [E]
+  uint16_t* gu_bias = nullptr;    // bf16 [E][2I] (gate then up)
+  uint16_t* down_bias = nullptr;  // bf16 [E][H]
 };
 
 struct ih_model {
@@ -76,6 +101,17 @@ struct ih_model {
   float2* ml = nullptr;
   size_t part_splits = 0;    // splits the attention partials can hold
   int Qpad = 0, QP = 0;
+  // MoE scratch: router logits [MAX_TOK][E], the routing of the round, the pairs' gated activations (fragments, one
+  // "token" per pair) and their down outputs [pairs][H].
+  float* rlogits = nullptr;
+  int* nent = nullptr;
+  int* entries = nullptr;
+  int* x_row = nullptr;
+  float* pair_w = nullptr;
+  int* row_pair = nullptr;
+  void* hpair = nullptr;
+  float* opair = nullptr;
+  int hpair_nkb = 0, max_pairs = 0;
 };
 
 struct ih_kv {
@@ -133,14 +169,43 @@ static int synth_qmat(ih_ctx* c, Staging& st, int N, int K, uint64_t seed, uint6
   return qmat_int4_create_dev(c, st.w, st.s, st.b, 1, N, K, il8, out);
 }
 
+// E stacked matrices [E][N][K] in `fmt`, matrix e from tensor id tensor_of(e). The staging holds all E in MLX layout
+// (an MXFP4 matrix's e8m0 bytes fit the int4 scale slot: N·K/32 bytes).
+template <typename F>
+static int synth_stack(ih_ctx* c, Staging& st, int fmt, int E, int N, int K, uint64_t seed, F tensor_of, float sd,
+                       int il8, ih_qmat** out) {
+  IH_TRY(st.reserve(size_t(E) * N, K));
+  const size_t wpe = size_t(N) * K / 8, spe = size_t(N) * K / 64;
+  for (int e = 0; e < E; ++e) {
+    if (fmt == QF_MXFP4)
+      IH_TRY(synth_mxfp4(c, st.w + e * wpe, reinterpret_cast<uint8_t*>(st.s) + e * (2 * spe), size_t(N), size_t(K),
+                         seed, tensor_of(e)));
+    else
+      IH_TRY(synth_int4(c, st.w + e * wpe, st.s + e * spe, st.b + e * spe, size_t(N), size_t(K), seed, tensor_of(e),
+                        sd));
+  }
+  if (fmt == QF_MXFP4) return qmat_mxfp4_create_dev(c, st.w, st.s, E, N, K, il8, out);
+  return qmat_int4_create_dev(c, st.w, st.s, st.b, E, N, K, il8, out);
+}
+
 static int check_desc(const ih_model_desc& d) {
   IH_CHECK(d.n_layers >= 1 && d.hidden >= 64 && d.hidden % 64 == 0, IH_EINVAL, "model: hidden must be a multiple of 64");
   IH_CHECK(d.head_dim == 64 || d.head_dim == 128, IH_EINVAL, "model: head_dim must be 64 or 128");
   IH_CHECK(d.n_kv_heads >= 1 && d.n_q_heads % d.n_kv_heads == 0, IH_EINVAL, "model: q heads must be a multiple of kv heads");
   IH_CHECK(d.n_q_heads * d.head_dim % 512 == 0, IH_EINVAL, "model: q_heads·head_dim must be a multiple of 512");
   IH_CHECK(d.vocab >= 1 && d.rms_eps > 0 && d.rope_theta > 0, IH_EINVAL, "model: vocab, eps and theta must be positive");
-  IH_CHECK(d.n_experts == 0, IH_EINVAL, "model: MoE layers are not available in this build yet");
-  IH_CHECK(d.intermediate >= 64 && d.intermediate % 64 == 0, IH_EINVAL, "model: intermediate must be a multiple of 64");
+  if (d.n_experts > 0) {
+    IH_CHECK(d.n_experts <= 256 && d.top_k >= 1 && d.top_k <= 16 && d.top_k <= d.n_experts, IH_EINVAL,
+             "model: need 1 ≤ top_k ≤ min(16, n_experts) and n_experts ≤ 256");
+    IH_CHECK(d.expert_format == QF_INT4 || d.expert_format == QF_MXFP4, IH_EINVAL,
+             "model: expert_format must be 0 (int4) or 1 (mxfp4)");
+    const int g = d.expert_format == QF_INT4 ? 64 : 32;
+    IH_CHECK(d.expert_intermediate >= g && d.expert_intermediate % g == 0 && d.expert_intermediate % 8 == 0,
+             IH_EINVAL, "model: expert_intermediate must be a multiple of the quantization group");
+  } else {
+    IH_CHECK(d.intermediate >= 64 && d.intermediate % 64 == 0, IH_EINVAL,
+             "model: intermediate must be a multiple of 64");
+  }
   IH_CHECK(d.act == 0 || d.act == 1, IH_EINVAL, "model: act must be 0 (SiLU) or 1 (swiglu_oai)");
   return IH_OK;
 }
@@ -148,14 +213,15 @@ static int check_desc(const ih_model_desc& d) {
 static void model_release(ih_model* m) {
   if (!m) return;
   for (auto& L : m->layers) {
-    ih_qmat_free(L.qkv); ih_qmat_free(L.o); ih_qmat_free(L.gate_up); ih_qmat_free(L.down);
-    if (L.attn_norm) (void)hipFree(L.attn_norm);
-    if (L.mlp_norm) (void)hipFree(L.mlp_norm);
-    if (L.sinks) (void)hipFree(L.sinks);
+    ih_qmat_free(L.qkv); ih_qmat_free(L.o); ih_qmat_free(L.gate_up); ih_qmat_free(L.down); ih_qmat_free(L.router);
+    void* lp[] = {L.attn_norm, L.mlp_norm, L.sinks, L.router_bias, L.gu_bias, L.down_bias};
+    for (void* p : lp)
+      if (p) (void)hipFree(p);
   }
   ih_qmat_free(m->head);
   void* ptrs[] = {m->emb_w, m->emb_s, m->emb_b, m->final_norm, m->h, m->proj, m->logits, m->tok, m->top1,
-                  m->q, m->opart, m->ml};
+                  m->q, m->opart, m->ml, m->rlogits, m->nent, m->entries, m->x_row, m->pair_w, m->row_pair,
+                  m->hpair, m->opair};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   free_act(m->act_attn); free_act(m->act_mlp); free_act(m->act_o); free_act(m->act_i);
@@ -200,8 +266,8 @@ static int run_step(ih_model* m, ih_kv* kv, int B) {
     a.ks = kv->ks[l];
     a.vs = kv->vs[l];
     a.sinks = L.sinks;
-    a.cap = kv->cap;
     a.ring = kv->ring[l];
+    a.cap = a.ring ? a.ring : kv->cap;  // slots per head of this layer's cache (the ring of a sliding-window layer)
     a.P = kv->P;
     a.B = B;
     a.QH = QH;
@@ -230,6 +296,22 @@ static int run_step(ih_model* m, ih_kv* kv, int B) {
     eo.nw = L.mlp_norm;
     eo.act_out = &m->act_mlp;
     IH_TRY(launch_qmm_ex(c, L.o, 0, m->act_o, B, eo));
+    const uint16_t* next_norm = l + 1 < d.n_layers ? m->layers[l + 1].attn_norm : m->final_norm;
+    if (d.n_experts > 0) {
+      // MoE: router → top-k and union → gathered gate|up with the gated activation → gathered down → combine with
+      // the residual into the next RMSNorm input.
+      const int E = d.n_experts, K = d.top_k;
+      const bool f16 = d.expert_format == QF_MXFP4;
+      IH_TRY(launch_moe_router(c, L.router, m->act_mlp, B, d.rms_eps, m->rlogits, E));
+      IH_TRY(launch_moe_route(c, m->rlogits, E, B, E, K, L.router_bias, nullptr, m->nent, m->entries, m->x_row,
+                              m->pair_w, m->row_pair));
+      IH_TRY(launch_moe_gate_up(c, L.gate_up, m->act_mlp, B, K, d.rms_eps, m->nent, m->entries, m->x_row, L.gu_bias,
+                                d.act, d.swiglu_limit, m->hpair, m->hpair_nkb, m->max_pairs, f16));
+      IH_TRY(launch_moe_down(c, L.down, m->hpair, m->hpair_nkb, m->max_pairs, f16, B, K, m->nent, m->entries,
+                             L.down_bias, m->opair, H));
+      IH_TRY(launch_moe_combine(c, m->opair, H, m->row_pair, m->pair_w, K, B, m->h, H, next_norm, m->act_attn));
+      continue;
+    }
     // Gated FFN: act(r · gate) · (r · up) straight into the down projection's activation.
     QmmEpilogue eg;
     eg.mode = QM_GLU_ACT;
@@ -243,7 +325,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B) {
     ed.mode = QM_RESID_ACT;
     ed.y = m->h;
     ed.ldy = H;
-    ed.nw = l + 1 < d.n_layers ? m->layers[l + 1].attn_norm : m->final_norm;
+    ed.nw = next_norm;
     ed.act_out = &m->act_attn;
     IH_TRY(launch_qmm_ex(c, L.down, 0, m->act_i, B, ed));
   }
@@ -301,8 +383,31 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
       }
       run(synth_qmat(c, stg, m->QP, H, seed, layer_tensor(l, L_QKV), W_SD, &L.qkv));
       run(synth_qmat(c, stg, H, QH * HD, seed, layer_tensor(l, L_O), W_SD, &L.o));
-      run(synth_qmat(c, stg, 2 * I, H, seed, layer_tensor(l, L_GATE_UP), W_SD, &L.gate_up, 1));
-      run(synth_qmat(c, stg, H, I, seed, layer_tensor(l, L_DOWN), W_SD, &L.down));
+      if (d.n_experts > 0) {
+        const int E = d.n_experts, IE = d.expert_intermediate, fmt = d.expert_format;
+        run(synth_stack(c, stg, fmt, 1, E, H, seed, [&](int) { return layer_tensor(l, L_ROUTER); }, W_SD, 0,
+                        &L.router));
+        run(synth_stack(c, stg, fmt, E, 2 * IE, H, seed, [&](int e) { return expert_tensor(l, X_GATE_UP, e); }, W_SD,
+                        1, &L.gate_up));
+        run(synth_stack(c, stg, fmt, E, H, IE, seed, [&](int e) { return expert_tensor(l, X_DOWN, e); }, W_SD, 0,
+                        &L.down));
+        if (d.router_bias) {
+          run(dalloc_t(&L.router_bias, E));
+          if (st == IH_OK) run(synth_f32(c, L.router_bias, E, seed, layer_tensor(l, L_ROUTER_BIAS), 0.0f, 0.5f));
+        }
+        if (d.expert_bias) {
+          run(dalloc_t(&L.gu_bias, size_t(E) * 2 * IE));
+          run(dalloc_t(&L.down_bias, size_t(E) * H));
+          for (int e = 0; e < E && st == IH_OK; ++e) {
+            run(synth_bf16(c, L.gu_bias + size_t(e) * 2 * IE, 2 * IE, seed, expert_tensor(l, X_GU_BIAS, e), 0.0f,
+                           0.1f));
+            run(synth_bf16(c, L.down_bias + size_t(e) * H, H, seed, expert_tensor(l, X_DOWN_BIAS, e), 0.0f, 0.1f));
+          }
+        }
+      } else {
+        run(synth_qmat(c, stg, 2 * I, H, seed, layer_tensor(l, L_GATE_UP), W_SD, &L.gate_up, 1));
+        run(synth_qmat(c, stg, H, I, seed, layer_tensor(l, L_DOWN), W_SD, &L.down));
+      }
     }
     run(synth_qmat(c, stg, V, H, seed, T_HEAD, W_SD, &m->head));
     if (st == IH_OK) run(hipStreamSynchronize(c->stream) == hipSuccess ? IH_OK : fail(IH_EDEVICE, "model: generation failed"));
@@ -319,10 +424,26 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
   run(dalloc_t(&m->tok, MAX_TOK));
   run(dalloc_t(&m->top1, MAX_TOK));
   run(dalloc_t(&m->q, size_t(KVH) * m->Qpad * HD));
+  const bool moe = d.n_experts > 0, moe_f16 = moe && d.expert_format == QF_MXFP4;
   if (st == IH_OK) run(ensure_act(c, m->act_attn, H, false));
-  if (st == IH_OK) run(ensure_act(c, m->act_mlp, H, false));
+  if (st == IH_OK) run(ensure_act(c, m->act_mlp, H, moe_f16));
   if (st == IH_OK) run(ensure_act(c, m->act_o, QH * HD, false));
-  if (st == IH_OK) run(ensure_act(c, m->act_i, I, false));
+  if (st == IH_OK && !moe) run(ensure_act(c, m->act_i, I, false));
+  if (moe) {
+    const int E = d.n_experts, IE = d.expert_intermediate;
+    m->max_pairs = IH_MAX_ROWS * d.top_k;
+    m->hpair_nkb = (IE + KBLK - 1) / KBLK;
+    run(dalloc_t(&m->rlogits, size_t(MAX_TOK) * E));
+    run(dalloc_t(&m->nent, 1));
+    run(dalloc_t(&m->entries, size_t(3) * E));
+    run(dalloc_t(&m->x_row, m->max_pairs));
+    run(dalloc_t(&m->pair_w, m->max_pairs));
+    run(dalloc_t(&m->row_pair, m->max_pairs));
+    const size_t hb = size_t(m->max_pairs) * m->hpair_nkb * 256;
+    run(dalloc(&m->hpair, hb));
+    run(dalloc_t(&m->opair, size_t(m->max_pairs) * H));
+    if (st == IH_OK) run(fill(c, m->hpair, 0, hb));
+  }
   if (st == IH_OK) run(fill(c, m->q, 0, size_t(KVH) * m->Qpad * HD * 2));
   if (st == IH_OK) run(hipStreamSynchronize(c->stream) == hipSuccess ? IH_OK : fail(IH_EDEVICE, "model: init failed"));
   if (st != IH_OK) {
@@ -345,7 +466,8 @@ size_t ih_model_weight_bytes(const ih_model* m) {
   if (!m) return 0;
   size_t b = ih_qmat_bytes(m->head);
   for (const auto& L : m->layers)
-    b += ih_qmat_bytes(L.qkv) + ih_qmat_bytes(L.o) + ih_qmat_bytes(L.gate_up) + ih_qmat_bytes(L.down);
+    b += ih_qmat_bytes(L.qkv) + ih_qmat_bytes(L.o) + ih_qmat_bytes(L.gate_up) + ih_qmat_bytes(L.down) +
+         ih_qmat_bytes(L.router);
   return b;
 }
 

@@ -474,6 +474,72 @@ int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, 
   return IH_OK;
 }
 
+// The model's MoE launches. Router: logits fp32 [rows][ldl] = r · (x · Wᵀ) (one dense slot).
+int launch_moe_router(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, float eps, float* logits, int ldl) {
+  GatherParams p{};
+  p.xa = static_cast<const uint4*>(x.frag);
+  p.x_nkb = x.nkb;
+  p.x_tokens = MAX_TOK;
+  p.dense_e = 0;
+  p.M = rows;
+  p.mode = GM_F32;
+  p.y = logits;
+  p.ldy = ldl;
+  p.ss_in = x.ss;
+  p.nss_in = x.nss;
+  p.D = x.K;
+  p.nrows = rows;
+  p.eps = eps;
+  return launch_gather(c, W, p, 1, double(W->algo_bytes) + double(rows) * W->N * 4);
+}
+
+// Gate|up of every pair: h[pair] = act(r·g + bg, r·u + bu) as fragments (one token per pair).
+int launch_moe_gate_up(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, int K_top, float eps, const int* nent,
+                       const int* entries, const int* x_row, const uint16_t* bias, int glu, float limit, void* h_frag,
+                       int h_nkb, int h_tokens, bool h_f16) {
+  IH_CHECK(W->il8, IH_EINVAL, "moe gate|up: the matrix must be interleaved by eights");
+  GatherParams p{};
+  p.xa = static_cast<const uint4*>(x.frag);
+  p.x_nkb = x.nkb;
+  p.x_tokens = MAX_TOK;
+  p.x_row = x_row;
+  p.entries = entries;
+  p.nent = nent;
+  p.mode = GM_GLU;
+  p.ss_in = x.ss;
+  p.nss_in = x.nss;
+  p.D = x.K;
+  p.nrows = rows;
+  p.eps = eps;
+  p.h_out = static_cast<uint4*>(h_frag);
+  p.h_nkb = h_nkb;
+  p.h_f16 = h_f16 ? 1 : 0;
+  p.glu = glu;
+  p.limit = limit;
+  p.bias = bias;
+  (void)h_tokens;
+  const int slots = std::min(W->E, rows * K_top);
+  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots);
+}
+
+// Down of every pair: o[pair] = h[pair] · Wdᵀ + bd (fp32).
+int launch_moe_down(ih_ctx* c, const ih_qmat* W, const void* h_frag, int h_nkb, int h_tokens, bool h_f16, int rows,
+                    int K_top, const int* nent, const int* entries, const uint16_t* bias, float* o, int ldo) {
+  (void)h_f16;
+  GatherParams p{};
+  p.xa = static_cast<const uint4*>(h_frag);
+  p.x_nkb = h_nkb;
+  p.x_tokens = h_tokens;
+  p.entries = entries;
+  p.nent = nent;
+  p.mode = GM_DOWN;
+  p.y = o;
+  p.ldy = ldo;
+  p.bias = bias;
+  const int slots = std::min(W->E, rows * K_top);
+  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots);
+}
+
 int pack_mxfp4(ih_ctx* c, ih_qmat* q, const uint32_t* w, const uint8_t* s) {
   dim3 grid((q->Npad / 16) * q->nkb, q->E);
   pack_mxfp4_kernel<<<grid, 64, 0, c->stream>>>(w, s, static_cast<uint4*>(q->w), static_cast<uint32_t*>(q->s), q->N,

@@ -106,6 +106,7 @@ struct QmmParams {
   // QM_GLU_ACT: gated activation kind and clip.
   int glu;
   float limit;
+  int act_f16;  // the next activation in fp16 (the input of MXFP4 experts) instead of bf16
 };
 
 // One K-block's operands of a wave: R weight tiles (+ scale/bias) and the token tiles of x.
@@ -355,7 +356,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
         v[j] = col < p.N ? hv * bf16f(p.nw[col]) : 0.f;
       }
       ssu[m * 8 + cl] = ss;
-      if (col0 < p.N) frag_store_chunk(p.act_out, p.act_nkb, m, col0 / 8, v);
+      if (col0 < p.N) frag_store(p.act_f16 != 0, p.act_out, p.act_nkb, m, col0 / 8, v);
     }
     __syncthreads();
     if (threadIdx.x < p.M) {
@@ -374,7 +375,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = glu_f(val(m, r, j) * rs_, val(m, r, 8 + j) * rs_, p.glu, p.limit);
       const int chunk = tile0 + r;
-      if (chunk * 8 < p.N / 2) frag_store_chunk(p.act_out, p.act_nkb, m, chunk, v);
+      if (chunk * 8 < p.N / 2) frag_store(p.act_f16 != 0, p.act_out, p.act_nkb, m, chunk, v);
     }
     return;
   }
@@ -475,6 +476,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
     p.nw = ep.nw;
     p.act_out = static_cast<uint4*>(ep.act_out->frag);
     p.act_nkb = ep.act_out->nkb;
+    p.act_f16 = ep.act_out->f16 ? 1 : 0;
     p.ss_out = ep.act_out->ss;
     ep.act_out->nss = grid;
   }
@@ -483,6 +485,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
              "qmm: gated epilogue needs an interleaved gate|up matrix and an output");
     p.act_out = static_cast<uint4*>(ep.act_out->frag);
     p.act_nkb = ep.act_out->nkb;
+    p.act_f16 = ep.act_out->f16 ? 1 : 0;
     p.glu = ep.glu;
     p.limit = ep.limit;
   }

@@ -4,6 +4,7 @@
 //
 //   int4 codes   word j of a tensor = 32-bit half (j & 1) of h(key_w, j >> 1)            (uniform nibbles 0..15)
 //   scales       bf16(|n(key_s, g)| · sd), n ≈ N(0,1) (act.h sm_normal), biases bf16(−8 · scale)  (BASELINE cfg 0)
+//   mxfp4        codes as int4; e8m0 scale of group g = 119 + h(key_s, g) mod 7      (2^-8 … 2^-2, BASELINE cfg 4)
 //   norm weights bf16(1 + 0.125 · n(key, i))
 //   KV           per (head, position): x_d = n(key, ((head << 24) + pos) · HD + d), symmetric int8 with fp16 scale
 //                sc = fp16(amax / 127) (1 when amax = 0), q = clamp(rint(x / sc), ±127)
@@ -25,6 +26,16 @@ __global__ void synth_int4_kernel(uint32_t* w, uint16_t* s, uint16_t* b, size_t 
     s[g] = sb;
     b[g] = dround_bf16(-8.0f * dbf16(sb));
   }
+}
+
+__global__ void synth_mxfp4_kernel(uint32_t* w, uint8_t* s, size_t nwords, size_t ngroups, uint64_t kw, uint64_t ks) {
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nwords; i += stride) {
+    const uint64_t h = sm_at(kw, i >> 1);
+    w[i] = uint32_t((i & 1) ? (h >> 32) : h);
+  }
+  for (size_t g = size_t(blockIdx.x) * blockDim.x + threadIdx.x; g < ngroups; g += stride)
+    s[g] = uint8_t(119 + sm_at(ks, g) % 7);
 }
 
 __global__ void synth_bf16_kernel(uint16_t* out, size_t n, uint64_t key, float base, float amp) {
@@ -72,6 +83,14 @@ int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_
   const size_t nw = N * K / 8, ng = N * K / 64;
   synth_int4_kernel<<<grid_for(nw), 256, 0, c->stream>>>(w, s, b, nw, ng, sm_key(seed, 2 * tensor),
                                                          sm_key(seed, 2 * tensor + 1), sd);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int synth_mxfp4(ih_ctx* c, uint32_t* w, uint8_t* s, size_t N, size_t K, uint64_t seed, uint64_t tensor) {
+  const size_t nw = N * K / 8, ng = N * K / 32;
+  synth_mxfp4_kernel<<<grid_for(nw), 256, 0, c->stream>>>(w, s, nw, ng, sm_key(seed, 2 * tensor),
+                                                          sm_key(seed, 2 * tensor + 1));
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -204,6 +204,18 @@ void or_synth_int4(uint64_t seed, uint64_t tensor, int N, int K, float sd, uint3
   }
 }
 
+// MLX mxfp4 tensor [N, K] of the synthetic model: codes as or_synth_int4; e8m0 of group g = 119 + h(key_s, g) mod 7.
+void or_synth_mxfp4(uint64_t seed, uint64_t tensor, int N, int K, uint32_t* w, uint8_t* s) {
+  const uint64_t kw = sm_key(seed, 2 * tensor), ks = sm_key(seed, 2 * tensor + 1);
+  const size_t nw = size_t(N) * K / 8, ng = size_t(N) * K / 32;
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < nw; ++i) {
+    const uint64_t h = sm_at(kw, i >> 1);
+    w[i] = uint32_t((i & 1) ? (h >> 32) : h);
+  }
+  for (size_t g = 0; g < ng; ++g) s[g] = uint8_t(119 + sm_at(ks, g) % 7);
+}
+
 void or_synth_bf16(uint64_t seed, uint64_t tensor, size_t n, float base, float amp, uint16_t* out) {
   const uint64_t k = sm_key(seed, 2 * tensor);
   for (size_t i = 0; i < n; ++i) out[i] = or_f32_to_bf16(base + amp * sm_normal(k, i));
@@ -304,6 +316,18 @@ void or_rms_split(const float* h, int rows, int D, const uint16_t* w, float eps,
     r[i] = 1.0f / std::sqrt(float(ss) / float(D) + eps);
     for (int j = 0; j < D; ++j)
       x[size_t(i) * D + j] = or_bf16_to_f32(or_f32_to_bf16(h[size_t(i) * D + j] * or_bf16_to_f32(w[j])));
+  }
+}
+
+// The same with the matmul input rounded to fp16 (the input of MXFP4 experts, whose products run in fp16 as the
+// reference's half activations, verify_nax.metal:78-79).
+void or_rms_split_f16(const float* h, int rows, int D, const uint16_t* w, float eps, float* x, float* r) {
+  for (int i = 0; i < rows; ++i) {
+    double ss = 0;
+    for (int j = 0; j < D; ++j) ss += double(h[size_t(i) * D + j]) * h[size_t(i) * D + j];
+    r[i] = 1.0f / std::sqrt(float(ss) / float(D) + eps);
+    for (int j = 0; j < D; ++j)
+      x[size_t(i) * D + j] = or_f16_to_f32(or_f32_to_f16(h[size_t(i) * D + j] * or_bf16_to_f32(w[j])));
   }
 }
 
@@ -416,10 +440,41 @@ struct QMat {
   void apply(const float* x, int B, float* y) const { or_qmm_int4(x, B, w.data(), s.data(), b.data(), N, K, y); }
 };
 
+// An int4 or mxfp4 matrix (MoE experts and router).
+struct AnyMat {
+  int fmt = 0, N = 0, K = 0;
+  QMat q4;
+  std::vector<uint32_t> w;
+  std::vector<uint8_t> s;
+  void make(int f, uint64_t seed, uint64_t tensor, int n, int k, float sd) {
+    fmt = f;
+    N = n;
+    K = k;
+    if (fmt == 0) {
+      q4.make(seed, tensor, n, k, sd);
+      return;
+    }
+    w.resize(size_t(N) * K / 8);
+    s.resize(size_t(N) * K / 32);
+    or_synth_mxfp4(seed, tensor, N, K, w.data(), s.data());
+  }
+  void apply(const float* x, int B, float* y) const {
+    if (fmt == 0) q4.apply(x, B, y);
+    else or_qmm_mxfp4(x, B, w.data(), s.data(), N, K, y);
+  }
+};
+
+static uint64_t expert_tensor(int l, uint64_t kind, int e) { return 3000000 + 10000 * uint64_t(l) + 1000 * kind + e; }
+
 struct OrLayer {
   std::vector<uint16_t> attn_norm, mlp_norm;
   std::vector<float> sinks;
   QMat qkv, o, gate_up, down;
+  // MoE: router [E][H], per expert gate|up [2I][H] (gate rows then up rows) and down [H][I], optional biases.
+  AnyMat router;
+  std::vector<AnyMat> egu, edn;
+  std::vector<float> router_bias;
+  std::vector<uint16_t> gu_bias, dn_bias;
   // KV of positions 0 … P−1 (history) followed by room for the block.
   std::vector<int8_t> k, v;
   std::vector<uint16_t> ks, vs;
@@ -459,8 +514,31 @@ void* or_model_create(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, i
     }
     L.qkv.make(seed, layer_tensor(l, 1), QP, H, sd);
     L.o.make(seed, layer_tensor(l, 2), H, QH * HD, sd);
-    L.gate_up.make(seed, layer_tensor(l, 4), 2 * I, H, sd);
-    L.down.make(seed, layer_tensor(l, 5), H, I, sd);
+    if (d->n_experts > 0) {
+      const int E = d->n_experts, IE = d->expert_intermediate, f = d->expert_format;
+      L.router.make(f, seed, layer_tensor(l, 6), E, H, sd);
+      L.egu.resize(E);
+      L.edn.resize(E);
+      for (int e = 0; e < E; ++e) {
+        L.egu[e].make(f, seed, expert_tensor(l, 0, e), 2 * IE, H, sd);
+        L.edn[e].make(f, seed, expert_tensor(l, 1, e), H, IE, sd);
+      }
+      if (d->router_bias) {
+        L.router_bias.resize(E);
+        or_synth_f32(seed, layer_tensor(l, 7), E, 0.0f, 0.5f, L.router_bias.data());
+      }
+      if (d->expert_bias) {
+        L.gu_bias.resize(size_t(E) * 2 * IE);
+        L.dn_bias.resize(size_t(E) * H);
+        for (int e = 0; e < E; ++e) {
+          or_synth_bf16(seed, expert_tensor(l, 2, e), 2 * IE, 0.0f, 0.1f, L.gu_bias.data() + size_t(e) * 2 * IE);
+          or_synth_bf16(seed, expert_tensor(l, 3, e), H, 0.0f, 0.1f, L.dn_bias.data() + size_t(e) * H);
+        }
+      }
+    } else {
+      L.gate_up.make(seed, layer_tensor(l, 4), 2 * I, H, sd);
+      L.down.make(seed, layer_tensor(l, 5), H, I, sd);
+    }
     L.k.resize(size_t(KVH) * m->cap * HD);
     L.v.resize(size_t(KVH) * m->cap * HD);
     L.ks.resize(size_t(KVH) * m->cap);
@@ -479,6 +557,67 @@ void* or_model_create(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, i
 }
 
 void or_model_free(void* h) { delete static_cast<OrModel*>(h); }
+
+void or_route(const float* logits, int rows, int E, int K, int sigmoid, const float* sel_bias, const float* logit_bias,
+              const float* pes, float scale, float eps, int32_t* inds, float* wts);
+int or_expert_union(const int32_t* inds, int rows, int K, int E, int32_t* entries, int32_t* pairs);
+
+// The MoE FFN of one layer (MoELayer.encode, Sources/Ingot/Layers/MoE.swift:346-428; MoEReference,
+// Tests/IngotTests/KernelHarness.swift:720-766): x = round(h ⊙ w) and r as the RMSNorm split (fp16 for MXFP4 experts,
+// bf16 for int4), router logits r·(x·Wrᵀ) (+ router bias), softmax top-k and the expert union; per pair h_p =
+// round(act(r·g + bg, r·u + bu)), o_p = h_p·Wdᵀ + bd; y[row] = Σ_slot w·o in slot order; h += y.
+static void moe_forward(const or_model_desc* d, const OrLayer& L, float* hres, int B) {
+  const int H = d->hidden, E = d->n_experts, K = d->top_k, IE = d->expert_intermediate;
+  const bool f16 = d->expert_format == 1;
+  auto round_act = [&](float v) { return f16 ? or_f16_to_f32(or_f32_to_f16(v)) : or_bf16_to_f32(or_f32_to_bf16(v)); };
+  std::vector<float> x(size_t(B) * H), rr(B), lg(size_t(B) * E);
+  if (f16) or_rms_split_f16(hres, B, H, L.mlp_norm.data(), d->rms_eps, x.data(), rr.data());
+  else or_rms_split(hres, B, H, L.mlp_norm.data(), d->rms_eps, x.data(), rr.data());
+  L.router.apply(x.data(), B, lg.data());
+  scale_rows(lg.data(), B, E, rr.data());
+  std::vector<int32_t> inds(size_t(B) * K), entries(size_t(B) * K * 3), pairs(size_t(B) * K * 2);
+  std::vector<float> wts(size_t(B) * K);
+  or_route(lg.data(), B, E, K, 0, nullptr, L.router_bias.empty() ? nullptr : L.router_bias.data(), nullptr, 1.0f, 0.0f,
+           inds.data(), wts.data());
+  const int U = or_expert_union(inds.data(), B, K, E, entries.data(), pairs.data());
+  std::vector<float> o(size_t(B) * K * H);
+  std::vector<int> pair_of(size_t(B) * K);
+  for (int u = 0; u < U; ++u) {
+    const int e = entries[3 * u], start = entries[3 * u + 1], cnt = entries[3 * u + 2];
+    std::vector<float> xe(size_t(cnt) * H), gu(size_t(cnt) * 2 * IE), he(size_t(cnt) * IE), oe(size_t(cnt) * H);
+    for (int j = 0; j < cnt; ++j) {
+      const int r = pairs[2 * (start + j)];
+      pair_of[size_t(r) * K + pairs[2 * (start + j) + 1]] = start + j;
+      std::memcpy(&xe[size_t(j) * H], &x[size_t(r) * H], sizeof(float) * H);
+    }
+    L.egu[e].apply(xe.data(), cnt, gu.data());
+    for (int j = 0; j < cnt; ++j) {
+      const int r = pairs[2 * (start + j)];
+      for (int i = 0; i < IE; ++i) {
+        float g = gu[size_t(j) * 2 * IE + i] * rr[r], uu = gu[size_t(j) * 2 * IE + IE + i] * rr[r];
+        if (!L.gu_bias.empty()) {
+          g += or_bf16_to_f32(L.gu_bias[size_t(e) * 2 * IE + i]);
+          uu += or_bf16_to_f32(L.gu_bias[size_t(e) * 2 * IE + IE + i]);
+        }
+        he[size_t(j) * IE + i] = round_act(or_glu(g, uu, d->act, d->swiglu_limit));
+      }
+    }
+    L.edn[e].apply(he.data(), cnt, oe.data());
+    for (int j = 0; j < cnt; ++j)
+      for (int c = 0; c < H; ++c)
+        o[size_t(start + j) * H + c] =
+            oe[size_t(j) * H + c] + (L.dn_bias.empty() ? 0.f : or_bf16_to_f32(L.dn_bias[size_t(e) * H + c]));
+  }
+  for (int r = 0; r < B; ++r)
+    for (int c = 0; c < H; ++c) {
+      float y = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const int pr = pair_of[size_t(r) * K + k];
+        y += wts[size_t(r) * K + k] * o[size_t(pr) * H + c];
+      }
+      hres[size_t(r) * H + c] += y;
+    }
+}
 
 // One verify step of B rows at position P (not advancing it): logits [B][vocab], top1 [B].
 int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint32_t* top1) {
@@ -522,6 +661,10 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
     for (auto& z : att) z = or_bf16_to_f32(or_f32_to_bf16(z));
     L.o.apply(att.data(), B, y.data());
     for (size_t i = 0; i < hres.size(); ++i) hres[i] += y[i];
+    if (d->n_experts > 0) {
+      moe_forward(d, L, hres.data(), B);
+      continue;
+    }
     or_rms_split(hres.data(), B, H, L.mlp_norm.data(), d->rms_eps, x.data(), rr.data());
     L.gate_up.apply(x.data(), B, gu.data());
     scale_rows(gu.data(), B, 2 * I, rr.data());

@@ -346,3 +346,18 @@ def test_oracle_model_row_causality():
     la, ta = m.verify(toks)
     m.free()
     assert np.array_equal(la, l5) and np.array_equal(ta, t5)
+
+
+def test_moe_oracle_sensitivity_to_last_bit_changes():
+    """The MoE model's logits move by a few hundredths under a one-part-in-10^7 change of RoPE θ (rounding flips of the
+    bf16 activations and int8 KV, amplified by the softmax router across two layers), while the dense model's move less:
+    the measured basis of the wider tolerance of the two-layer MoE GPU test."""
+    from ingot_amd._lib import ModelDesc
+
+    shape = dict(n_layers=2, hidden=256, n_q_heads=4, n_kv_heads=2, head_dim=128, intermediate=0, vocab=1000,
+                 n_experts=8, top_k=2, expert_intermediate=128, expert_format=0)
+    toks = np.random.default_rng(17).integers(0, 1000, size=17).astype(np.uint32)
+    a, _ = oracle.verify_dense(ModelDesc.make(**shape), 7, 11, 100, toks)
+    b, _ = oracle.verify_dense(ModelDesc.make(**shape, rope_theta=1e6 * (1 + 1e-7)), 7, 11, 100, toks)
+    d = np.abs(a - b).max()
+    assert 0.02 < d < 0.05 + 0.03 * np.abs(a).max(), d
