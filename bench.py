@@ -1,14 +1,19 @@
 #!/usr/bin/env python3
-"""Benchmark of the speculative-decoding verify step on one MI355X (BASELINE.json metric, configuration 1).
+"""Benchmark of the speculative-decoding verify step on one MI355X (BASELINE.json metric).
 
-A step is one verify round of k = 16 drafts (B = 17 rows) of the 8B-class 4-bit dense model at 8192 positions of
-int8 KV: the block runs through all 32 layers and the head (its K/V written at P…P+16), the device-side greedy
-acceptance takes the longest draft prefix, and the block is rolled back (P restored) so every step sees the same
-context. Drafts are planted to agree with the greedy chain for L = 0…16 tokens (cycling over the steps), and the bench
-checks that the accepted length equals L.
+Default (the headline line): configuration 1 — one verify round of k = 16 drafts (B = 17 rows) of the 8B-class 4-bit
+dense model at 8192 positions of int8 KV: the block runs through all 32 layers and the head (its K/V written at
+P…P+16), the device-side greedy acceptance takes the longest draft prefix, and the block is rolled back (P restored) so
+every step sees the same context. Drafts are planted to agree with the greedy chain for L = 0…16 tokens (cycling over
+the steps), and the bench checks that the accepted length equals L.
 
-Printed: one JSON line (the driver's contract) with `roofline` (the dominant kernel, the int4 qmm, from HIP events on
-the library's stream) and `cpu_baseline` (the C++ oracle on the host, same workload, one full step).
+Other workloads (--config): configuration 2 (copy-from-context lookup over 131,072 Zipf ids writing the verify block,
+then the config-1 model at 32K positions), 3 (48-layer MoE, 128 experts top-8, int4, 16K) and 4 (24-layer MXFP4 MoE,
+32 experts top-4, sinks, alternating 128-token sliding window, B = 9, 64K).
+
+Printed: one JSON line (the driver's contract) with `roofline` (the dominant kernel class, from HIP events on the
+library's stream) and `cpu_baseline` (the C++ oracle on the host, same workload, one full step; configuration 1 only by
+default, since the MoE models take tens of GB of host memory in the oracle's fp32 path).
 
 Synthetic weights and KV (seeded, counter-based SplitMix64; the reference's checkpoints are not available).
 """
@@ -17,7 +22,6 @@ from __future__ import annotations
 import argparse
 import ctypes as C
 import json
-import os
 import sys
 import time
 from pathlib import Path
@@ -30,18 +34,24 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 METRIC = "verify-step µs & tok/s at k=16, 4-bit; qmm/attn HBM GB/s vs 8 TB/s peak"
 
+DENSE8B = dict(n_layers=32, hidden=4096, n_q_heads=32, n_kv_heads=8, head_dim=128, intermediate=14336, vocab=151936)
 CONFIGS = {
-    # hidden 4096, 32 q / 8 KV heads of 128, SwiGLU 14336, 32 layers, vocab 151936, RoPE θ 1e6,
-    # RMSNorm eps 1e-6, MLX int4 g64 everywhere; k + 1 = 17 rows over 8192 int8 KV positions.
-    "dense8b-8k": dict(
-        desc=dict(n_layers=32, hidden=4096, n_q_heads=32, n_kv_heads=8, head_dim=128, intermediate=14336,
-                  vocab=151936),
-        P=8192, B=17),
-    # The same model at 32K positions (the verify leg of config 2).
-    "dense8b-32k": dict(
-        desc=dict(n_layers=32, hidden=4096, n_q_heads=32, n_kv_heads=8, head_dim=128, intermediate=14336,
-                  vocab=151936),
-        P=32768, B=17),
+    # Config 1: hidden 4096, 32 q / 8 KV heads of 128, SwiGLU 14336, 32 layers, vocab 151936, RoPE θ 1e6, RMSNorm eps
+    # 1e-6, MLX int4 g64 everywhere; k + 1 = 17 rows over 8192 int8 KV positions.
+    "dense8b-8k": dict(desc=DENSE8B, P=8192, B=17, label="config 1: verify k=16 (B=17) at P=8192"),
+    # Config 2: copy-from-context lookup over 131,072 ids, proposing 16, then the config-1 model at 32K positions.
+    "copy-dense8b-32k": dict(desc=DENSE8B, P=32768, B=17, copy=131072,
+                             label="config 2: copy lookup over 131072 ids + verify k=16 at P=32768"),
+    # Config 3: 48 layers, hidden 2048, 32 q / 4 KV heads of 128, 128 experts top-8 (softmax), expert SwiGLU 768, int4.
+    "moe-e128-16k": dict(desc=dict(n_layers=48, hidden=2048, n_q_heads=32, n_kv_heads=4, head_dim=128, intermediate=0,
+                                   vocab=151936, n_experts=128, top_k=8, expert_intermediate=768, expert_format=0),
+                         P=16384, B=17, label="config 3: MoE E128 top-8 verify k=16 at P=16384"),
+    # Config 4: 24 layers, hidden 2880, 64 q / 8 KV heads of 64, sinks, alternating 128-token sliding window / full,
+    # 32 MXFP4 experts top-4 with intermediate 2880, router and expert biases, swiglu_oai, vocab 201088; B = 9.
+    "mxfp4-moe-64k": dict(desc=dict(n_layers=24, hidden=2880, n_q_heads=64, n_kv_heads=8, head_dim=64, intermediate=0,
+                                    vocab=201088, n_experts=32, top_k=4, expert_intermediate=2880, expert_format=1,
+                                    router_bias=1, expert_bias=1, act=1, sinks=1, sliding_window=128),
+                          P=65536, B=9, label="config 4: MXFP4 MoE E32 top-4 verify k=8 at P=65536"),
 }
 
 SEED, KV_SEED, ANCHOR = 2026, 11, 1234
@@ -58,6 +68,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--config", default="dense8b-8k", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-baseline", action="store_true", help="also for the non-default configurations")
     ap.add_argument("--no-kernel-profile", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -65,48 +76,79 @@ def main() -> int:
               "across GPUs only by design, see DESIGN.md)", file=sys.stderr)
         return 2
 
-    from ingot_amd._lib import (Context, HipEvents, KVCache, Model, ModelDesc, check, lib, ptr)
+    from ingot_amd._lib import Context, HipEvents, KVCache, Model, ModelDesc, check, lib
 
     cfg = CONFIGS[args.config]
+    d = cfg["desc"]
     P, B = cfg["P"], cfg["B"]
     k = B - 1
     ctx = Context(0)
-    desc = ModelDesc.make(**cfg["desc"])
+    desc = ModelDesc.make(**d)
     t0 = time.time()
     model = Model(ctx, desc, SEED)
     kv = KVCache(model, P + 2 * B)
     kv.fill_synthetic(P, KV_SEED)
-    log(f"[bench] model {args.config} built in {time.time() - t0:.1f}s; weights {model.weight_bytes / 1e9:.3f} GB")
+    log(f"[bench] model {args.config} built in {time.time() - t0:.1f}s; weights {model.weight_bytes / 1e9:.3f} GB, "
+        f"key chunk {kv.chunk}")
 
-    # Greedy chain from the anchor (plain one-row steps), then back to P.
-    chain = []
-    tok = ANCHOR
-    for _ in range(k + 1):
-        r = kv.verify_and_accept([tok])
-        tok = r.tokens[0]
-        chain.append(tok)
-    kv.set_pos(P)
-    rng = np.random.default_rng(SEED)
-    blocks = np.zeros((k + 1, B), np.uint32)
-    for L in range(k + 1):
-        blk = [ANCHOR] + chain[:L]
-        if L < k:
-            blk.append((chain[L] + 1) % desc.vocab)  # first wrong draft
-            blk += list(rng.integers(0, desc.vocab, size=B - len(blk)))
-        blocks[L] = blk
-    d_blocks = ctx.to_device(blocks)
     d_vtok = ctx.buffer(B * 4)
     d_top1 = ctx.buffer(B * 4)
     d_st = ctx.to_device(np.zeros(8, np.uint32))
     RING = 64
     d_rec = ctx.buffer(RING * 24 * 4).fill(0)
+    copy_n = cfg.get("copy")
 
-    def step(i: int) -> None:
-        L = i % (k + 1)
-        check(lib().ih_memcpy_dtod(ctx.handle, d_vtok.ptr, d_blocks.ptr + L * B * 4, B * 4))
-        check(lib().ih_verify_step_dev(model.handle, kv.handle, d_vtok.ptr, B, d_top1.ptr))
-        check(lib().ih_spec_accept_dev(ctx.handle, d_st.ptr, d_vtok.ptr, d_top1.ptr, d_rec.ptr, RING, B))
-        # Rollback: the verify step does not advance the host position, so the next step sees P again.
+    if copy_n:
+        # Config 2: the copy drafter proposes from the context; the verify block is written on the device.
+        sys.path.insert(0, str(ROOT / "tests"))
+        from synth import zipf_context
+
+        hist, _ = zipf_context(SEED, n=copy_n, vocab=d["vocab"])
+        d_hist = ctx.to_device(hist)
+        d_copy = ctx.buffer((4 + k) * 4)
+        blocks = None
+        planted = None
+
+        def step(i: int) -> None:
+            check(lib().ih_copy_lookup_dev(ctx.handle, d_hist.ptr, copy_n, k, 3, 64, d_copy.ptr, d_vtok.ptr, B))
+            check(lib().ih_verify_step_dev(model.handle, kv.handle, d_vtok.ptr, B, d_top1.ptr))
+            check(lib().ih_spec_accept_dev(ctx.handle, d_st.ptr, d_vtok.ptr, d_top1.ptr, d_rec.ptr, RING, B))
+    else:
+        # Greedy chain from the anchor (plain one-row steps), then back to P; plant L = 0…k agreeing drafts.
+        chain = []
+        tok = ANCHOR
+        for _ in range(k + 1):
+            r = kv.verify_and_accept([tok])
+            tok = r.tokens[0]
+            chain.append(tok)
+        kv.set_pos(P)
+        rng = np.random.default_rng(SEED)
+        blocks = np.zeros((k + 1, B), np.uint32)
+        for L in range(k + 1):
+            blk = [ANCHOR] + chain[:L]
+            if L < k:
+                blk.append((chain[L] + 1) % d["vocab"])  # first wrong draft
+                blk += list(rng.integers(0, d["vocab"], size=B - len(blk)))
+            blocks[L] = blk
+        d_blocks = ctx.to_device(blocks)
+        log(f"[bench] greedy chain: {chain}")
+        # MoE: the synthetic greedy chain repeats tokens, and identical rows route identically; the timed blocks carry
+        # distinct random drafts (the routing of real draft text), and the planted blocks are checked in an untimed
+        # pass. The step's cost does not depend on how many drafts are accepted (every row is verified).
+        d_timed = d_blocks
+        if d.get("n_experts"):
+            rnd = blocks.copy()
+            rnd[:, 1:] = rng.integers(0, d["vocab"], size=(k + 1, B - 1))
+            d_timed = ctx.to_device(rnd)
+
+        def one(src, L):
+            check(lib().ih_memcpy_dtod(ctx.handle, d_vtok.ptr, src.ptr + L * B * 4, B * 4))
+            check(lib().ih_verify_step_dev(model.handle, kv.handle, d_vtok.ptr, B, d_top1.ptr))
+            check(lib().ih_spec_accept_dev(ctx.handle, d_st.ptr, d_vtok.ptr, d_top1.ptr, d_rec.ptr, RING, B))
+            # Rollback: the verify step does not advance the host position, so the next step sees P again.
+
+        def step(i: int) -> None:
+            one(d_timed, i % (k + 1))
 
     for i in range(args.warmup):
         step(i)
@@ -121,12 +163,30 @@ def main() -> int:
     ms_total = ev.elapsed_ms(0, 1)
     ctx.sync()
     ms = ms_total / args.steps
+    # MoE: distinct experts per layer of the last timed step (the bytes actually streamed).
+    U = None
+    if d.get("n_experts"):
+        u = np.zeros(d["n_layers"], np.int32)
+        check(lib().ih_model_moe_union(model.handle, u.ctypes.data))
+        U = u.tolist()
+    if blocks is not None and d.get("n_experts"):
+        # Acceptance check on the planted blocks (untimed).
+        d_st.upload(np.zeros(8, np.uint32))
+        for i in range(k + 1):
+            one(d_blocks, i)
+        ctx.sync()
     rec = d_rec.download(np.uint32, (RING, 24))
-    accepted = [int(rec[i % RING][0]) for i in range(min(args.steps, RING))]
-    planted = [i % (k + 1) for i in range(min(args.steps, RING))]
-    accept_ok = accepted == planted
-    tok_per_L = {L: (L + 1) / (ms / 1e3) for L in range(k + 1)}
-    tok_s = float(np.mean(list(tok_per_L.values())))
+    nrec = k + 1 if (blocks is not None and d.get("n_experts")) else min(args.steps, RING)
+    accepted = [int(rec[i % RING][0]) for i in range(nrec)]
+    if blocks is not None:
+        planted = [i % (k + 1) for i in range(nrec)]
+        accept_ok = accepted == planted
+        tok_per_L = {L: (L + 1) / (ms / 1e3) for L in range(k + 1)}
+        tok_s = float(np.mean(list(tok_per_L.values())))
+    else:
+        accept_ok = None
+        tok_per_L = {}
+        tok_s = float(np.mean([a + 1 for a in accepted])) / (ms / 1e3)
 
     # Per-kernel-class timing in a second, instrumented pass of the same steps.
     classes = {}
@@ -146,25 +206,52 @@ def main() -> int:
                                   gbs=by.value / (t.value * 1e6), bytes_per_step=by.value / args.steps)
         check(lib().ih_timing_enable(ctx.handle, 0))
 
-    # Algorithmic bytes of one step: weights (MLX int4), KV of all layers, logits write + read.
-    d = cfg["desc"]
-    kv_bytes = d["n_layers"] * d["n_kv_heads"] * (P + B) * (2 * d["head_dim"] + 4)
+    # Algorithmic bytes of one step: weights actually read (MLX formats; MoE: the routed experts), the KV of every
+    # layer (a sliding-window layer reads the window), logits written and read.
+    L_, H, KVH, HD = d["n_layers"], d["hidden"], d["n_kv_heads"], d["head_dim"]
+    per_expert = 0.0
+    weight_bytes = float(model.weight_bytes)
+    if d.get("n_experts"):
+        IE, E = d["expert_intermediate"], d["n_experts"]
+        bpw = 0.5625 if d.get("expert_format", 0) == 0 else 0.53125
+        per_expert = 3 * IE * H * bpw
+        weight_bytes = weight_bytes - L_ * E * per_expert + sum(U) * per_expert
+    kv_bytes = 0.0
+    for l in range(L_):
+        keys = P + B
+        if d.get("sliding_window") and l % 2 == 0:
+            keys = min(keys, d["sliding_window"] + B - 1)
+        kv_bytes += KVH * keys * (2 * HD + 4)
     logit_bytes = 2 * B * d["vocab"] * 4
-    step_bytes = model.weight_bytes + kv_bytes + logit_bytes
+    step_bytes = weight_bytes + kv_bytes + logit_bytes
+
     roofline = None
-    if "qmm" in classes:
-        q = classes["qmm"]
-        roofline = dict(bound="hbm", achieved=round(q["gbs"], 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                        frac=round(q["gbs"] / HBM_PEAK_GBS, 4), traffic=None, kernel="qmm_int4",
+    dom = max((n for n in ("qmm", "moe", "attention") if n in classes), key=lambda n: classes[n]["ms_per_step"],
+              default=None)
+    if dom:
+        q = classes[dom]
+        by = q["bytes_per_step"]
+        if dom == "moe":
+            # The gathered launches are sized for every expert slot; the bytes streamed are the routed experts'.
+            by = sum(U) * per_expert
+        gbs = by / (q["ms_per_step"] * 1e6)
+        roofline = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
+                        kernel={"qmm": "qmm_int4", "moe": "qmm_gather (MoE experts)", "attention": "attn"}[dom],
                         avg_launch_us=round(q["ms_per_step"] / q["launches_per_step"] * 1e3, 2),
-                        bytes_per_launch=round(q["bytes_per_step"] / q["launches_per_step"]))
+                        bytes_per_launch=round(by / q["launches_per_step"]))
+        traffic = _traffic(args.config, dom)
+        if traffic is not None:
+            roofline["traffic"] = traffic
 
     cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(desc, P, blocks[k])
+    if not args.no_cpu_baseline and (args.config == "dense8b-8k" or args.cpu_baseline):
+        cpu = cpu_baseline(desc, P, blocks[k] if blocks is not None else np.full(B, ANCHOR, np.uint32))
 
-    model_name = f"synthetic 8B-class dense int4 g64 ({d['n_layers']}L h{d['hidden']} {d['n_q_heads']}q/" \
-                 f"{d['n_kv_heads']}kv hd{d['head_dim']} I{d['intermediate']} V{d['vocab']})"
+    model_name = (f"synthetic {d['n_layers']}L h{d['hidden']} {d['n_q_heads']}q/{d['n_kv_heads']}kv hd{d['head_dim']} "
+                  + (f"E{d['n_experts']} top-{d['top_k']} I{d['expert_intermediate']} "
+                     f"{'mxfp4' if d.get('expert_format') else 'int4'} experts" if d.get("n_experts")
+                     else f"I{d['intermediate']} int4 g64") + f" V{d['vocab']}")
     out = {
         "metric": METRIC,
         "value": round(tok_s, 1),
@@ -177,20 +264,25 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4-g64 weights, bf16 activations, fp32 accumulate, int8 KV",
+        "dtype": "int4-g64/mxfp4 weights, bf16 (fp16 for mxfp4) activations, fp32 accumulate, int8 KV",
         "data": "synthetic (seeded SplitMix64 weights, N(0,1) int8 KV, planted drafts)",
-        "config": {"workload": f"config 1: verify k=16 (B=17) at P={P}", "model": model_name, "k": k,
-                   "context": P, "parallelism": "single GPU"},
+        "config": {"workload": cfg["label"], "model": model_name, "k": k, "context": P, "parallelism": "single GPU"},
         "tok_s_per_L": {str(L): round(v, 1) for L, v in tok_per_L.items()},
         "accepted_equals_planted": accept_ok,
         "accepted": accepted[: k + 1],
         "step_hbm_gbs": round(step_bytes / (ms * 1e6), 1),
         "step_roofline_frac": round(step_bytes / (ms * 1e6) / HBM_PEAK_GBS, 4),
-        "step_algorithmic_bytes": step_bytes,
+        "step_algorithmic_bytes": round(step_bytes),
         "kernels": {n: {kk: round(vv, 3) for kk, vv in v.items()} for n, v in classes.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    if U is not None:
+        out["moe_distinct_experts_per_layer"] = {"mean": round(float(np.mean(U)), 2), "min": min(U), "max": max(U)}
+    if copy_n:
+        out["copy_lookup"] = copy_lookup_timing(ctx, lib, check, d_hist, copy_n, k, d_copy, d_vtok, B)
+    if d.get("n_experts"):
+        out["moe_experts_iid_routing"] = moe_iid_timing(ctx, d, B)
     print(json.dumps(out), flush=True)
     kv.free()
     model.free()
@@ -198,9 +290,98 @@ def main() -> int:
     return 0
 
 
+def _traffic(config: str, dom: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter runs (profiles/), if any."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        t = json.loads(f.read_text())
+        return t.get(config, {}).get(dom)
+    except (ValueError, OSError):
+        return None
+
+
+def copy_lookup_timing(ctx, lib, check, d_hist, n, k, d_copy, d_vtok, B) -> dict:
+    """Device copy lookup alone over the config-2 context: µs per call and the context scan's GB/s."""
+    from ingot_amd._lib import HipEvents
+
+    for _ in range(5):
+        check(lib().ih_copy_lookup_dev(ctx.handle, d_hist.ptr, n, k, 3, 64, d_copy.ptr, d_vtok.ptr, B))
+    ev = HipEvents(ctx, 2)
+    ctx.sync()
+    reps = 50
+    ev.record(0)
+    for _ in range(reps):
+        check(lib().ih_copy_lookup_dev(ctx.handle, d_hist.ptr, n, k, 3, 64, d_copy.ptr, d_vtok.ptr, B))
+    ev.record(1)
+    us = ev.elapsed_ms(0, 1) / reps * 1e3
+    ctx.sync()
+    out = d_copy.download(np.uint32, (4 + k,))
+    return {"us": round(us, 2), "context_gbs": round(n * 4 / (us * 1e3), 1), "proposed": int(out[0]),
+            "match": int(out[1])}
+
+
+def moe_iid_timing(ctx, d: dict, B: int) -> dict:
+    """The expert streaming of one MoE layer under the routing config 3/4 describe (router logits i.i.d. N(0,1)):
+    routing + gathered gate|up + gathered down through the kernel-level entry points on stacked synthetic experts of
+    the configuration's shapes; µs per layer and the GB/s of the routed experts' bytes. (The synthetic model's own
+    router sees rows whose residual stream is dominated by attention outputs shared across the block, so its union is
+    much smaller; see moe_distinct_experts_per_layer.)"""
+    from ingot_amd._lib import HipEvents, QMat, Routing, check, lib
+
+    E, K, H, IE, fmt = d["n_experts"], d["top_k"], d["hidden"], d["expert_intermediate"], d.get("expert_format", 0)
+    g = np.random.default_rng(5)
+
+    def mat(N, Kd):
+        if fmt == 0:
+            q = g.integers(0, 2**32, size=(E, N, Kd // 8), dtype=np.uint32)
+            sc = np.full((E, N, Kd // 64), 0x3C00, np.uint16)
+            return QMat.int4(ctx, q, sc, sc)
+        q = g.integers(0, 2**32, size=(E, N, Kd // 8), dtype=np.uint32)
+        return QMat.mxfp4(ctx, q, np.full((E, N, Kd // 32), 122, np.uint8))
+
+    gu, dn = mat(2 * IE, H), mat(H, IE)
+    x = ctx.to_device(np.full((B, max(H, IE)), 0x3F80, np.uint16))
+    logits = ctx.to_device(g.normal(0, 1, size=(B, E)).astype(np.float32))
+    R = Routing(ctx, B, K, E).route(logits, E)
+    U = R.download()["U"]
+    ygu = ctx.buffer(B * K * 2 * IE * 4)
+    ydn = ctx.buffer(B * K * H * 4)
+
+    def layer():
+        check(lib().ih_moe_route(ctx.handle, logits.ptr, E, B, E, K, None, None, R.nent.ptr, R.entries.ptr,
+                                 R.x_row.ptr, R.pair_w.ptr, R.row_pair.ptr))
+        check(lib().ih_qmm_gathered(ctx.handle, gu.handle, x.ptr, max(H, IE), B, K, R.nent.ptr, R.entries.ptr,
+                                    R.x_row.ptr, ygu.ptr, 2 * IE))
+        check(lib().ih_qmm_gathered(ctx.handle, dn.handle, x.ptr, max(H, IE), B, K, R.nent.ptr, R.entries.ptr,
+                                    R.x_row.ptr, ydn.ptr, H))
+
+    for _ in range(3):
+        layer()
+    ev = HipEvents(ctx, 2)
+    ctx.sync()
+    reps = 20
+    ev.record(0)
+    for _ in range(reps):
+        layer()
+    ev.record(1)
+    us = ev.elapsed_ms(0, 1) / reps * 1e3
+    ctx.sync()
+    bpw = 0.5625 if fmt == 0 else 0.53125
+    by = U * 3 * IE * H * bpw
+    for b in (x, logits, ygu, ydn):
+        b.free()
+    R.free()
+    gu.free()
+    dn.free()
+    return {"U": int(U), "us_per_layer": round(us, 2), "expert_bytes": round(by), "gbs": round(by / (us * 1e3), 1),
+            "note": "kernel-level: x staged as bf16 rows by each gathered call (adds a small conversion launch)"}
+
+
 def cpu_baseline(desc, P: int, tokens) -> dict | None:
     """The C++ oracle (fp32 dequant + matmul) on the host: the full model with resident weights, one verify step of
-    the same B = 17 block at the same P; tok/s as for the GPU (mean accepted + 1 over L = 0…16 → 9 tokens)."""
+    the same block at the same P; tok/s as for the GPU (mean accepted + 1 over L = 0…k → (k + 2) / 2 tokens)."""
     try:
         import oracle
     except Exception as e:  # noqa: BLE001

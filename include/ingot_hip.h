@@ -190,6 +190,10 @@ int ih_verify_step_dev(ih_model* model, ih_kv* kv, const uint32_t* tokens_dev, i
  * prefix, advances P by m + 1 and returns the result (the non-chained round of generateSpec, Generate.swift:104-177). */
 int ih_verify_and_accept(ih_model* model, ih_kv* kv, const uint32_t* tokens, int B, ih_accept_result* out);
 
+/* MoE models: the number of distinct experts U of each layer in the last step (u_out[n_layers]); synchronises. The
+ * per-round union of vmoe_route (verify.metal:262-318), for the bytes actually streamed. */
+int ih_model_moe_union(const ih_model* model, int* u_out);
+
 /* The model's device scratch of the last step: logits fp32 [rows ≥ B][vocab] (row stride = vocab). */
 const float* ih_model_logits_dev(const ih_model* model);
 

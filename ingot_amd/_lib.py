@@ -91,6 +91,7 @@ def _declare(L: C.CDLL) -> None:
         "ih_verify_and_accept": (i32, [vp, vp, vp, i32, vp]),
         "ih_model_logits_dev": (vp, [vp]),
         "ih_kv_create_chunked": (i32, [vp, i32, i32, P(vp)]),
+        "ih_model_moe_union": (i32, [vp, vp]),
         "ih_qmat_mxfp4_create": (i32, [vp, vp, vp, i32, i32, i32, P(vp)]),
         "ih_qmat_mxfp4_create_dev": (i32, [vp, vp, vp, i32, i32, i32, P(vp)]),
         "ih_qmat_format": (i32, [vp]),

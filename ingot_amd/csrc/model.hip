@@ -303,11 +303,12 @@ static int run_step(ih_model* m, ih_kv* kv, int B) {
       const int E = d.n_experts, K = d.top_k;
       const bool f16 = d.expert_format == QF_MXFP4;
       IH_TRY(launch_moe_router(c, L.router, m->act_mlp, B, d.rms_eps, m->rlogits, E));
-      IH_TRY(launch_moe_route(c, m->rlogits, E, B, E, K, L.router_bias, nullptr, m->nent, m->entries, m->x_row,
+      int* nent = m->nent + l;  // one union count per layer, kept for ih_model_moe_union
+      IH_TRY(launch_moe_route(c, m->rlogits, E, B, E, K, L.router_bias, nullptr, nent, m->entries, m->x_row,
                               m->pair_w, m->row_pair));
-      IH_TRY(launch_moe_gate_up(c, L.gate_up, m->act_mlp, B, K, d.rms_eps, m->nent, m->entries, m->x_row, L.gu_bias,
+      IH_TRY(launch_moe_gate_up(c, L.gate_up, m->act_mlp, B, K, d.rms_eps, nent, m->entries, m->x_row, L.gu_bias,
                                 d.act, d.swiglu_limit, m->hpair, m->hpair_nkb, m->max_pairs, f16));
-      IH_TRY(launch_moe_down(c, L.down, m->hpair, m->hpair_nkb, m->max_pairs, f16, B, K, m->nent, m->entries,
+      IH_TRY(launch_moe_down(c, L.down, m->hpair, m->hpair_nkb, m->max_pairs, f16, B, K, nent, m->entries,
                              L.down_bias, m->opair, H));
       IH_TRY(launch_moe_combine(c, m->opair, H, m->row_pair, m->pair_w, K, B, m->h, H, next_norm, m->act_attn));
       continue;
@@ -434,7 +435,7 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
     m->max_pairs = IH_MAX_ROWS * d.top_k;
     m->hpair_nkb = (IE + KBLK - 1) / KBLK;
     run(dalloc_t(&m->rlogits, size_t(MAX_TOK) * E));
-    run(dalloc_t(&m->nent, 1));
+    run(dalloc_t(&m->nent, d.n_layers));
     run(dalloc_t(&m->entries, size_t(3) * E));
     run(dalloc_t(&m->x_row, m->max_pairs));
     run(dalloc_t(&m->pair_w, m->max_pairs));
@@ -605,6 +606,14 @@ int ih_verify_and_accept(ih_model* m, ih_kv* kv, const uint32_t* tokens, int B, 
   IH_TRY(ih_verify_step(m, kv, tokens, B, nullptr, top1));
   IH_TRY(ih_accept(tokens, top1, B, out));
   return ih_kv_commit(kv, out->m + 1);
+}
+
+int ih_model_moe_union(const ih_model* m, int* u_out) {
+  IH_CHECK(m && u_out, IH_EINVAL, "ih_model_moe_union: null argument");
+  IH_CHECK(m->d.n_experts > 0, IH_EINVAL, "ih_model_moe_union: not a MoE model");
+  IH_HIP(hipStreamSynchronize(m->ctx->stream));
+  IH_HIP(hipMemcpy(u_out, m->nent, sizeof(int) * m->d.n_layers, hipMemcpyDeviceToHost));
+  return IH_OK;
 }
 
 const float* ih_model_logits_dev(const ih_model* m) { return m ? m->logits : nullptr; }
