@@ -70,7 +70,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-baseline", action="store_true", help="also for the non-default configurations")
     ap.add_argument("--no-kernel-profile", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only copy BYTES device-to-device 4 times (the reference kernel that scales the HBM counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the verify step shards "
               "across GPUs only by design, see DESIGN.md)", file=sys.stderr)
@@ -377,6 +381,24 @@ def moe_iid_timing(ctx, d: dict, B: int) -> dict:
     dn.free()
     return {"U": int(U), "us_per_layer": round(us, 2), "expert_bytes": round(by), "gbs": round(by / (us * 1e3), 1),
             "note": "kernel-level: x staged as bf16 rows by each gathered call (adds a small conversion launch)"}
+
+
+def copy_calibration(nbytes: int) -> int:
+    """A plain device copy of known size (HIP's copy kernel through ih_memcpy_dtod), 4 times: rocprofv3's FETCH_SIZE
+    and WRITE_SIZE per dispatch over it, against nbytes, give the scale factor for the counters of the other kernels."""
+    from ingot_amd._lib import Context, check, lib
+
+    ctx = Context(0)
+    a, b = ctx.buffer(nbytes).fill(1), ctx.buffer(nbytes)
+    ctx.sync()
+    for _ in range(4):
+        check(lib().ih_memcpy_dtod(ctx.handle, b.ptr, a.ptr, nbytes))
+    ctx.sync()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "dispatches": 4}), flush=True)
+    a.free()
+    b.free()
+    ctx.close()
+    return 0
 
 
 def cpu_baseline(desc, P: int, tokens) -> dict | None:

@@ -470,7 +470,7 @@ int launch_prework(ih_ctx* c, const AttnArgs& a) {
   TimedLaunch tl(c, TC_PREWORK, double(a.B) * (a.QH + 2 * a.KVH) * a.HD * 4 + double(a.B) * a.KVH * (2 * a.HD + 4) +
                                     double(a.B) * a.QH * a.HD * 2);
   dim3 grid(a.QH + 2 * a.KVH, a.B);
-  prework_kernel<<<grid, a.HD, 0, c->stream>>>(a);
+  tlaunch(tl, prework_kernel, grid, dim3(a.HD), 0, c->stream, a);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
@@ -484,7 +484,7 @@ int launch_attention(ih_ctx* c, const AttnArgs& a) {
   const double keys = double(a.P + a.B) - double(a.s0) * a.C;
   TimedLaunch tl(c, TC_ATTN, double(a.KVH) * keys * (2 * a.HD + 4) + double(a.KVH) * Q * a.HD * 2);
   const bool two = qtiles > 8, ring = a.ring != 0;
-  auto go = [&](auto kern) { kern<<<grid, ATT_THREADS, 0, c->stream>>>(a); };
+  auto go = [&](auto kern) { tlaunch(tl, kern, grid, dim3(ATT_THREADS), 0, c->stream, a); };
   if (a.HD == 128) {
     if (two) ring ? go(attn_kernel<128, 2, true>) : go(attn_kernel<128, 2, false>);
     else ring ? go(attn_kernel<128, 1, true>) : go(attn_kernel<128, 1, false>);
@@ -502,8 +502,9 @@ int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
   IH_CHECK(a.QH % 4 == 0, IH_EINVAL, "attention reduce: the q head count must be a multiple of 4");
   TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (2 * a.HD + 8) + double(a.B) * a.QH * a.HD * 2);
   const dim3 grid(a.B, a.QH / 4);
-  if (a.HD == 128) attn_reduce_kernel<128><<<grid, 256, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.nkb);
-  else if (a.HD == 64) attn_reduce_kernel<64><<<grid, 256, 0, c->stream>>>(a, static_cast<uint4*>(out.frag), out.nkb);
+  uint4* of = static_cast<uint4*>(out.frag);
+  if (a.HD == 128) tlaunch(tl, attn_reduce_kernel<128>, grid, dim3(256), 0, c->stream, a, of, out.nkb);
+  else if (a.HD == 64) tlaunch(tl, attn_reduce_kernel<64>, grid, dim3(256), 0, c->stream, a, of, out.nkb);
   else return fail(IH_EINVAL, "attention reduce: head_dim must be 64 or 128");
   IH_HIP(hipGetLastError());
   return IH_OK;

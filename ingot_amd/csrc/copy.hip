@@ -205,7 +205,7 @@ int launch_copy_lookup(ih_ctx* c, const uint32_t* h, int n, int max_k, int min_m
   int* part = reinterpret_cast<int*>(c->part);
   {
     TimedLaunch tl(c, TC_OTHER, double(n) * 4);
-    copy_scan_kernel<<<nparts, COPY_THREADS, 0, c->stream>>>(h, n, part);
+    tlaunch(tl, copy_scan_kernel, dim3(nparts), dim3(COPY_THREADS), 0, c->stream, h, n, part);
     IH_HIP(hipGetLastError());
   }
   copy_pick_kernel<<<1, 64, 0, c->stream>>>(h, n, part, nparts, max_k, min_match, max_match, out, vtok, rows);

@@ -1,6 +1,7 @@
 // Internal declarations shared by the HIP sources of libingot_hip: the context, error reporting, the packed weight
 // and activation layouts, and the kernel launchers. Not part of the public C ABI (include/ingot_hip.h).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include <cstddef>
@@ -125,15 +126,23 @@ struct ih_ctx {
 };
 
 namespace ih {
-// Brackets one launch for ih_timing_* (no-ops unless timing is enabled).
+// Times one launch for ih_timing_* (no-op unless timing is enabled): the launch goes through tlaunch, which hands the
+// start/stop events to hipExtLaunchKernel so that they stamp the kernel's own dispatch (no event packets between
+// kernels, whose gaps would otherwise be counted).
 struct TimedLaunch {
   ih_ctx* c;
   int cls;
   double bytes;
-  hipEvent_t a = nullptr;
+  hipEvent_t a = nullptr, b = nullptr;
   TimedLaunch(ih_ctx* ctx, int cl, double b);
   ~TimedLaunch();
 };
+
+template <typename F, typename... Args>
+inline void tlaunch(const TimedLaunch& tl, F kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s,
+                    Args... args) {
+  hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, tl.a, tl.b, 0u, args...);
+}
 int fill(ih_ctx* c, void* dst, int byte, size_t bytes);
 int ensure_part(ih_ctx* c, size_t bytes);
 int ensure_act(ih_ctx* c, ActBuf& a, int K, bool f16);

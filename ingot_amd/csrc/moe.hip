@@ -446,8 +446,8 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
            "gathered qmm: stacked matrix above 2 GiB");
   TimedLaunch tl(c, TC_MOE, bytes);
   const dim3 grid(W->Npad / 16, slots);
-  if (W->format == QF_INT4) qmm_gather_kernel<QF_INT4><<<grid, 64 * GKW, 0, c->stream>>>(p);
-  else qmm_gather_kernel<QF_MXFP4><<<grid, 64 * GKW, 0, c->stream>>>(p);
+  if (W->format == QF_INT4) tlaunch(tl, qmm_gather_kernel<QF_INT4>, grid, dim3(64 * GKW), 0, c->stream, p);
+  else tlaunch(tl, qmm_gather_kernel<QF_MXFP4>, grid, dim3(64 * GKW), 0, c->stream, p);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
@@ -457,8 +457,8 @@ int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, i
   IH_CHECK(E >= 1 && E <= 256 && K >= 1 && K <= 16 && K <= E && rows >= 1 && rows <= MAX_TOK, IH_EINVAL,
            "moe route: need E ≤ 256, 1 ≤ k ≤ min(16, E), 1 ≤ rows ≤ 32");
   TimedLaunch tl(c, TC_MOE, double(rows) * E * 4);
-  moe_route_kernel<<<1, 256, 0, c->stream>>>(logits, ldl, rows, E, K, bias, pes, nent, entries, x_row, pair_w,
-                                             row_pair);
+  tlaunch(tl, moe_route_kernel, dim3(1), dim3(256), 0, c->stream, logits, ldl, rows, E, K, bias, pes, nent, entries,
+          x_row, pair_w, row_pair);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
@@ -467,8 +467,8 @@ int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, 
                        float* h, int H, const uint16_t* nw, ActBuf& act) {
   IH_CHECK(H % 8 == 0, IH_EINVAL, "moe combine: hidden size must be a multiple of 8");
   TimedLaunch tl(c, TC_MOE, double(rows) * H * (4.0 * K + 8 + 2));
-  moe_combine_kernel<<<rows, 256, 0, c->stream>>>(o, ldo, row_pair, pair_w, K, h, H, H, nw,
-                                                  static_cast<uint4*>(act.frag), act.nkb, act.f16 ? 1 : 0, act.ss);
+  tlaunch(tl, moe_combine_kernel, dim3(rows), dim3(256), 0, c->stream, o, ldo, row_pair, pair_w, K, h, H, H, nw,
+          static_cast<uint4*>(act.frag), act.nkb, act.f16 ? 1 : 0, act.ss);
   IH_HIP(hipGetLastError());
   act.nss = 1;
   return IH_OK;

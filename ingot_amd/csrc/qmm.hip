@@ -409,10 +409,10 @@ static QmmShape qmm_shape(int Npad, int nkb) {
 }
 
 template <int T, bool X16>
-static void qmm_dispatch(QmmShape sh, int grid, hipStream_t st, const QmmParams& p) {
+static void qmm_dispatch(const TimedLaunch& tl, QmmShape sh, int grid, hipStream_t st, const QmmParams& p) {
 #define IH_QMM_CASE(R_, KW_, NS_)                                                                  \
   if (sh.R == R_ && sh.KW == KW_ && sh.NS == NS_) {                                                \
-    qmm_int4_kernel<T, R_, KW_, X16, NS_><<<grid, 64 * KW_, 0, st>>>(p);                            \
+    tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, NS_>, dim3(grid), dim3(64 * KW_), 0, st, p);      \
     return;                                                                                        \
   }
   IH_QMM_CASE(4, 4, 2) IH_QMM_CASE(4, 4, 3)
@@ -421,7 +421,7 @@ static void qmm_dispatch(QmmShape sh, int grid, hipStream_t st, const QmmParams&
   IH_QMM_CASE(1, 8, 2) IH_QMM_CASE(1, 8, 4)
   IH_QMM_CASE(1, 16, 2) IH_QMM_CASE(1, 16, 4)
 #undef IH_QMM_CASE
-  qmm_int4_kernel<T, 1, 4, X16, 2><<<grid, 256, 0, st>>>(p);
+  tlaunch(tl, qmm_int4_kernel<T, 1, 4, X16, 2>, dim3(grid), dim3(256), 0, st, p);
 }
 
 int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
@@ -493,9 +493,9 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   const double ybytes = double(M) * W->N *
                         (ep.mode == QM_BF16 ? 2 : (ep.mode == QM_F32_ADD || ep.mode == QM_RESID_ACT ? 8 : 4));
   TimedLaunch tl(c, TC_QMM, double(W->algo_bytes) + double(M) * W->K * 2 + ybytes);
-  if (M > 17) qmm_dispatch<2, true>(sh, grid, c->stream, p);
-  else if (M == 17) qmm_dispatch<1, true>(sh, grid, c->stream, p);
-  else qmm_dispatch<1, false>(sh, grid, c->stream, p);
+  if (M > 17) qmm_dispatch<2, true>(tl, sh, grid, c->stream, p);
+  else if (M == 17) qmm_dispatch<1, true>(tl, sh, grid, c->stream, p);
+  else qmm_dispatch<1, false>(tl, sh, grid, c->stream, p);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

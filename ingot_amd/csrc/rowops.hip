@@ -99,7 +99,8 @@ __global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                      float* h, int B, int H, const uint16_t* nw, ActBuf& a) {
   TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4 + 2));
-  embed_act_kernel<<<B, 256, 0, c->stream>>>(tok, w, s, b, h, H, H, nw, static_cast<uint4*>(a.frag), a.nkb, a.ss);
+  tlaunch(tl, embed_act_kernel, dim3(B), dim3(256), 0, c->stream, tok, w, s, b, h, H, H, nw, static_cast<uint4*>(a.frag),
+          a.nkb, a.ss);
   IH_HIP(hipGetLastError());
   a.nss = 1;
   return IH_OK;
@@ -107,7 +108,7 @@ int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const ui
 
 int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out) {
   TimedLaunch tl(c, TC_ARGMAX, double(rows) * N * 4);
-  argmax_kernel<<<rows, 1024, 0, c->stream>>>(x, ldx, N, out);
+  tlaunch(tl, argmax_kernel, dim3(rows), dim3(1024), 0, c->stream, x, ldx, N, out);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -47,18 +47,15 @@ static hipEvent_t next_event(ih_ctx* c) {
   return c->ev_pool[c->ev_used++];
 }
 
-TimedLaunch::TimedLaunch(ih_ctx* ctx, int cl, double b) : c(ctx), cls(cl), bytes(b) {
+TimedLaunch::TimedLaunch(ih_ctx* ctx, int cl, double by) : c(ctx), cls(cl), bytes(by) {
   if (!c->timing) return;
   a = next_event(c);
-  if (a) (void)hipEventRecord(a, c->stream);
+  b = next_event(c);
+  if (!a || !b) a = b = nullptr;
 }
 
 TimedLaunch::~TimedLaunch() {
-  if (!c->timing || !a) return;
-  hipEvent_t e = next_event(c);
-  if (!e) return;
-  (void)hipEventRecord(e, c->stream);
-  c->trecs.push_back(TimingRec{cls, bytes, a, e});
+  if (a && b) c->trecs.push_back(TimingRec{cls, bytes, a, b});
 }
 
 int ensure_part(ih_ctx* c, size_t bytes) {
