@@ -14,8 +14,15 @@ __device__ __forceinline__ unsigned short dround_bf16(float f) {
   return (unsigned short)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
+// Fragment layout (ih_internal.h): 16-byte unit of (K-block kb, token tok, MFMA step t, lane group qd) in a buffer of
+// ntile 16-token tiles. One (kb, tile, t) is 1024 contiguous bytes [token 16][qd 4][8 values]: the A operand of one
+// MFMA step for a whole wave, read as one coalesced dwordx4 load.
+__device__ __forceinline__ size_t frag_index(int ntile, int kb, int tok, int t, int qd) {
+  return ((size_t(kb) * ntile + (tok >> 4)) * 4 + t) * 64 + (tok & 15) * 4 + qd;
+}
+
 // Writes one 8-value chunk c (values x[8c … 8c+7] of token `tok`, final fp32) into the fragment layout as bf16.
-__device__ __forceinline__ void frag_store_chunk(uint4* frag, int nkb, int tok, int c, const float (&v)[8]) {
+__device__ __forceinline__ void frag_store_chunk(uint4* frag, int nkb, int ntile, int tok, int c, const float (&v)[8]) {
   if (c >= nkb * 16) return;
   const int kb = c >> 4, w = c & 15, t = w >> 2, qd = w & 3;
   uint4 u;
@@ -23,11 +30,12 @@ __device__ __forceinline__ void frag_store_chunk(uint4* frag, int nkb, int tok, 
   u.y = dround_bf16(v[1]) | (unsigned(dround_bf16(v[5])) << 16);
   u.z = dround_bf16(v[2]) | (unsigned(dround_bf16(v[6])) << 16);
   u.w = dround_bf16(v[3]) | (unsigned(dround_bf16(v[7])) << 16);
-  frag[((size_t(tok) * nkb + kb) * 4 + qd) * 4 + t] = u;
+  frag[frag_index(ntile, kb, tok, t, qd)] = u;
 }
 
 // The same chunk as fp16 (round to nearest even): the activation of MXFP4 experts, whose MFMA runs in fp16.
-__device__ __forceinline__ void frag_store_chunk_f16(uint4* frag, int nkb, int tok, int c, const float (&v)[8]) {
+__device__ __forceinline__ void frag_store_chunk_f16(uint4* frag, int nkb, int ntile, int tok, int c,
+                                                     const float (&v)[8]) {
   if (c >= nkb * 16) return;
   const int kb = c >> 4, w = c & 15, t = w >> 2, qd = w & 3;
   auto h = [](float f) { return unsigned(__half_as_ushort(__float2half_rn(f))); };
@@ -36,12 +44,13 @@ __device__ __forceinline__ void frag_store_chunk_f16(uint4* frag, int nkb, int t
   u.y = h(v[1]) | (h(v[5]) << 16);
   u.z = h(v[2]) | (h(v[6]) << 16);
   u.w = h(v[3]) | (h(v[7]) << 16);
-  frag[((size_t(tok) * nkb + kb) * 4 + qd) * 4 + t] = u;
+  frag[frag_index(ntile, kb, tok, t, qd)] = u;
 }
 
-__device__ __forceinline__ void frag_store(bool f16, uint4* frag, int nkb, int tok, int c, const float (&v)[8]) {
-  if (f16) frag_store_chunk_f16(frag, nkb, tok, c, v);
-  else frag_store_chunk(frag, nkb, tok, c, v);
+__device__ __forceinline__ void frag_store(bool f16, uint4* frag, int nkb, int ntile, int tok, int c,
+                                           const float (&v)[8]) {
+  if (f16) frag_store_chunk_f16(frag, nkb, ntile, tok, c, v);
+  else frag_store_chunk(frag, nkb, ntile, tok, c, v);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -416,7 +416,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 // merges splits sg, sg + SG, … (all its loads in flight), then the SG groups are merged by a fixed butterfly.
 // Grid (B, QH/4), 256 threads.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb) {
+__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb, int ntile) {
   constexpr int DG = HD / 8, SG = 64 / DG;
   const int t = blockIdx.x, h = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int dg = lane % DG, sg = lane / DG;
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __r
   const float inv = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] *= inv;
-  frag_store_chunk(frag, nkb, t, (h * HD) / 8 + dg, o);
+  frag_store_chunk(frag, nkb, ntile, t, (h * HD) / 8 + dg, o);
 }
 
 int launch_prework(ih_ctx* c, const AttnArgs& a) {
@@ -503,8 +503,8 @@ int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
   TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (2 * a.HD + 8) + double(a.B) * a.QH * a.HD * 2);
   const dim3 grid(a.B, a.QH / 4);
   uint4* of = static_cast<uint4*>(out.frag);
-  if (a.HD == 128) tlaunch(tl, attn_reduce_kernel<128>, grid, dim3(256), 0, c->stream, a, of, out.nkb);
-  else if (a.HD == 64) tlaunch(tl, attn_reduce_kernel<64>, grid, dim3(256), 0, c->stream, a, of, out.nkb);
+  if (a.HD == 128) tlaunch(tl, attn_reduce_kernel<128>, grid, dim3(256), 0, c->stream, a, of, out.nkb, out.ntile);
+  else if (a.HD == 64) tlaunch(tl, attn_reduce_kernel<64>, grid, dim3(256), 0, c->stream, a, of, out.nkb, out.ntile);
   else return fail(IH_EINVAL, "attention reduce: head_dim must be 64 or 128");
   IH_HIP(hipGetLastError());
   return IH_OK;

@@ -63,13 +63,16 @@ constexpr int TILE_N = 16;      // output rows per tile
 constexpr int KBLK = 128;       // K per block
 constexpr int MAX_TOK = 32;     // tokens per qmm (two 16-token MFMA tiles)
 
-// Activations (the A operand of every qmm) use the "fragment" layout: for token i and K-block kb, 256 bytes ordered
-// [qd][t][8] where element e of (qd, t) is x[128kb + 32t + 8qd + perm(e)], perm = {0,4,1,5,2,6,3,7} (the order in
-// which one 32-bit word of nibbles turns into four bf16/fp16 pairs). An activation that is an RMSNorm input also
+// Activations (the A operand of every qmm) use the "fragment" layout: tokens in tiles of 16; for K-block kb, token tile
+// g and MFMA step t, 1024 contiguous bytes [token 16][qd 4][8 values], element e of (token i, qd) being
+// x[128kb + 32t + 8qd + perm(e)], perm = {0,4,1,5,2,6,3,7} (the order in which one 32-bit word of nibbles turns into
+// four bf16/fp16 pairs). A wave's A operand of one MFMA step is then one contiguous 1 KB read; blocks are ordered
+// [kb][g][t]. An activation that is an RMSNorm input also
 // carries the sums of squares of its (unnormalised) rows as partials of the producer's workgroups, ss[j][token]:
 // the consumer adds them in order and applies the per-row factor in its epilogue.
 struct ActBuf {
-  void* frag = nullptr;   // [MAX_TOK][nkb][64 B × 4] (bf16 or fp16 elements)
+  void* frag = nullptr;   // [nkb][ntile][4][1 KB] (bf16 or fp16 elements)
+  int ntile = MAX_TOK / 16;
   float* ss = nullptr;    // [ss_cap][MAX_TOK]
   int nss = 0, ss_cap = 0;
   int K = 0, nkb = 0;

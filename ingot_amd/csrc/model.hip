@@ -432,7 +432,7 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
   if (st == IH_OK && !moe) run(ensure_act(c, m->act_i, I, false));
   if (moe) {
     const int E = d.n_experts, IE = d.expert_intermediate;
-    m->max_pairs = IH_MAX_ROWS * d.top_k;
+    m->max_pairs = (IH_MAX_ROWS * d.top_k + 15) / 16 * 16;  // pair "tokens" of the fragment layout, whole tiles
     m->hpair_nkb = (IE + KBLK - 1) / KBLK;
     run(dalloc_t(&m->rlogits, size_t(MAX_TOK) * E));
     run(dalloc_t(&m->nent, d.n_layers));

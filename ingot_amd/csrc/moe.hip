@@ -89,7 +89,7 @@ struct GatherParams {
   unsigned tiles_per_e;    // (Npad / 16) · nkb
   unsigned E;
   const uint4* xa;         // activation fragments (bf16 for int4, fp16 for mxfp4)
-  int x_nkb, x_tokens;     // fragment K-blocks; tokens the fragment buffer holds
+  int x_nkb, x_tokens;     // fragment K-blocks; tokens the fragment buffer holds (a multiple of 16)
   const int* x_row;        // pair → activation row (null: the pair index itself)
   const int* entries;      // [U][3] (expert, first pair, pairs); null: one entry (dense_e, 0, M)
   const int* nent;         // U on the device (null: 1)
@@ -102,7 +102,7 @@ struct GatherParams {
   int nss_in, D, nrows;
   float eps;
   uint4* h_out;            // GM_GLU: next activation (fragments), by pair
-  int h_nkb, h_f16, glu;
+  int h_nkb, h_ntile, h_f16, glu;
   float limit;
   const uint16_t* bias;    // bf16; GM_GLU: [E][2·(N/2)] gate then up; GM_DOWN: [E][N]; null: none
   unsigned kmask, kbias;
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
   for (int tt = 0; tt < 2; ++tt) {
     const int j = 16 * tt + n;
     const int ar = j < cnt ? (p.x_row ? p.x_row[start + j] : start + j) : -1;
-    xoff[tt] = ar >= 0 ? unsigned(ar) * p.x_nkb * 256u + qd * 64u : OOB;
+    xoff[tt] = ar >= 0 ? unsigned(ar >> 4) * 4096u + unsigned(ar & 15) * 64u + qd * 16u : OOB;
   }
   if (threadIdx.x < MAX_TOK) {
     const int j = threadIdx.x;
@@ -168,11 +168,11 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
       st.s = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, (kb * 128u + n * 8u) | oob, 0, 0));
     else
       st.s.x = __builtin_amdgcn_raw_buffer_load_b32(rs, (kb * 64u + n * 4u) | oob, 0, 0);
-    const unsigned kx = unsigned(kb) * 256u;
+    const unsigned kx = unsigned(kb) * unsigned(p.x_tokens / 16) * 4096u;  // [kb][tile][t][1 KB]
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      st.x[0][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xoff[0] + kx + 16 * t) | oob, 0, 0));
-      st.x[1][t] = two ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xoff[1] + kx + 16 * t) | oob, 0, 0))
+      st.x[0][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xoff[0] + kx + 1024 * t) | oob, 0, 0));
+      st.x[1][t] = two ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xoff[1] + kx + 1024 * t) | oob, 0, 0))
                        : u32x4{0u, 0u, 0u, 0u};
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
         }
         v[c] = col < I ? glu_f(g, uu, p.glu, p.limit) : 0.f;
       }
-      if (8 * tile < I) frag_store(p.h_f16 != 0, p.h_out, p.h_nkb, start + j, tile, v);
+      if (8 * tile < I) frag_store(p.h_f16 != 0, p.h_out, p.h_nkb, p.h_ntile, start + j, tile, v);
     }
     return;
   }
@@ -399,8 +399,8 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ o, int ldo, const int* __restrict__ row_pair,
                                                           const float* __restrict__ pair_w, int K, float* __restrict__ h,
                                                           int ldh, int H, const uint16_t* __restrict__ nw,
-                                                          uint4* __restrict__ act, int act_nkb, int act_f16,
-                                                          float* __restrict__ ss_out) {
+                                                          uint4* __restrict__ act, int act_nkb, int act_ntile,
+                                                          int act_f16, float* __restrict__ ss_out) {
   __shared__ float red[4];
   const int r = blockIdx.x;
   float ss = 0.f;
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
       ss += hv * hv;
       v[j] = hv * bf16f(nw[col]);
     }
-    frag_store(act_f16 != 0, act, act_nkb, r, c, v);
+    frag_store(act_f16 != 0, act, act_nkb, act_ntile, r, c, v);
   }
   for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
@@ -468,7 +468,7 @@ int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, 
   IH_CHECK(H % 8 == 0, IH_EINVAL, "moe combine: hidden size must be a multiple of 8");
   TimedLaunch tl(c, TC_MOE, double(rows) * H * (4.0 * K + 8 + 2));
   tlaunch(tl, moe_combine_kernel, dim3(rows), dim3(256), 0, c->stream, o, ldo, row_pair, pair_w, K, h, H, H, nw,
-          static_cast<uint4*>(act.frag), act.nkb, act.f16 ? 1 : 0, act.ss);
+          static_cast<uint4*>(act.frag), act.nkb, act.ntile, act.f16 ? 1 : 0, act.ss);
   IH_HIP(hipGetLastError());
   act.nss = 1;
   return IH_OK;
@@ -513,11 +513,11 @@ int launch_moe_gate_up(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, i
   p.eps = eps;
   p.h_out = static_cast<uint4*>(h_frag);
   p.h_nkb = h_nkb;
+  p.h_ntile = h_tokens / 16;
   p.h_f16 = h_f16 ? 1 : 0;
   p.glu = glu;
   p.limit = limit;
   p.bias = bias;
-  (void)h_tokens;
   const int slots = std::min(W->E, rows * K_top);
   return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots);
 }
@@ -581,7 +581,7 @@ int qmat_mxfp4_create_dev(ih_ctx* c, const void* w, const void* s, int E, int N,
 }
 
 // Natural bf16 rows → fragments (bf16 or fp16 elements). Grid (tokens), 256 threads.
-__global__ void act_gather_kernel(const uint16_t* __restrict__ x, int ldx, int M, int K, int nkb, int f16,
+__global__ void act_gather_kernel(const uint16_t* __restrict__ x, int ldx, int M, int K, int nkb, int ntile, int f16,
                                   uint4* __restrict__ frag) {
   const int i = blockIdx.x;
   for (int cc = threadIdx.x; cc < nkb * 16; cc += blockDim.x) {
@@ -589,13 +589,14 @@ __global__ void act_gather_kernel(const uint16_t* __restrict__ x, int ldx, int M
     const bool valid = i < M && cc < K / 8;
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = valid ? bf16f(x[size_t(i) * ldx + 8 * cc + e]) : 0.f;
-    frag_store(f16 != 0, frag, nkb, i, cc, v);
+    frag_store(f16 != 0, frag, nkb, ntile, i, cc, v);
   }
 }
 
 int stage_act_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, int K, bool f16, ActBuf& a) {
   IH_TRY(ensure_act(c, a, K, f16));
-  act_gather_kernel<<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, K, a.nkb, f16 ? 1 : 0, static_cast<uint4*>(a.frag));
+  act_gather_kernel<<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, K, a.nkb, a.ntile, f16 ? 1 : 0,
+                                                    static_cast<uint4*>(a.frag));
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -64,7 +64,7 @@ __global__ void pack_int4_kernel(const uint32_t* __restrict__ w, const uint16_t*
 // Natural-layout activations → fragment layout. Grid (MAX_TOK), 256 threads; one thread per 8 values. Rows ≥ M are
 // written as zeros.
 template <typename TIn>
-__global__ void act_kernel(const TIn* __restrict__ x, int ldx, int M, int K, int nkb, uint4* __restrict__ frag) {
+__global__ void act_kernel(const TIn* __restrict__ x, int ldx, int M, int K, int nkb, int ntile, uint4* __restrict__ frag) {
   const int i = blockIdx.x;
   const int nchunk = nkb * 16;
   for (int c = threadIdx.x; c < nchunk; c += blockDim.x) {
@@ -79,7 +79,7 @@ __global__ void act_kernel(const TIn* __restrict__ x, int ldx, int M, int K, int
       }
       v[e] = f;
     }
-    frag_store_chunk(frag, nkb, i, c, v);
+    frag_store_chunk(frag, nkb, ntile, i, c, v);
   }
 }
 
@@ -120,8 +120,8 @@ struct QmmStage {
 
 struct QmmRsrc {
   __amdgpu_buffer_rsrc_t w, s, x;
-  unsigned xoff[2];   // token row offset of this lane's A operand (OOB for dead tokens), per token tile
-  unsigned x16off;
+  unsigned xoff[2];   // this lane's offset in a K-block's fragments (OOB for dead tokens), per token tile
+  unsigned x16off;    // token 16 (VALU path): its 16 bytes of the lane's qd
 };
 
 template <int T, int R, bool X16>
@@ -141,18 +141,18 @@ __device__ __forceinline__ void qmm_load(QmmStage<T, R, X16>& st, const QmmParam
         u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, (tb * 1024u + lane * 16u) | oob, 0, 0));
     st.sb[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.s, (tb * 128u + n * 8u) | oob, 0, 0));
   }
-  const unsigned kx = unsigned(kb) * 256u;
+  const unsigned kx = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u;  // [kb][tile][t][1 KB]
 #pragma unroll
   for (int tt = 0; tt < T; ++tt)
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       st.x[tt][t] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.xoff[tt] + kx + 16 * t) | oob, 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.xoff[tt] + kx + 1024 * t) | oob, 0, 0));
   if constexpr (X16) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       st.x16[t] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.x16off + kx + 16 * t) | oob, 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.x16off + kx + 1024 * t) | oob, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -253,9 +253,9 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   for (int tt = 0; tt < 2; ++tt) {
     const int tok = 16 * tt + n;
     const bool live = tt < T && tok < p.M && !(X16 && tok == 16);
-    rs.xoff[tt] = live ? (unsigned(tok) * p.nkb * 256u + qd * 64u) : OOB;
+    rs.xoff[tt] = live ? (unsigned(tt) * 4096u + n * 64u + qd * 16u) : OOB;
   }
-  rs.x16off = 16u * p.nkb * 256u + qd * 64u;
+  rs.x16off = 4096u + qd * 16u;  // tile 1, token 0 of the tile
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
   const float qd0 = qd == 0 ? 1.f : 0.f;
 
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
         v[j] = col < p.N ? hv * bf16f(p.nw[col]) : 0.f;
       }
       ssu[m * 8 + cl] = ss;
-      if (col0 < p.N) frag_store(p.act_f16 != 0, p.act_out, p.act_nkb, m, col0 / 8, v);
+      if (col0 < p.N) frag_store(p.act_f16 != 0, p.act_out, p.act_nkb, MAX_TOK / 16, m, col0 / 8, v);
     }
     __syncthreads();
     if (threadIdx.x < p.M) {
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = glu_f(val(m, r, j) * rs_, val(m, r, 8 + j) * rs_, p.glu, p.limit);
       const int chunk = tile0 + r;
-      if (chunk * 8 < p.N / 2) frag_store(p.act_f16 != 0, p.act_out, p.act_nkb, m, chunk, v);
+      if (chunk * 8 < p.N / 2) frag_store(p.act_f16 != 0, p.act_out, p.act_nkb, MAX_TOK / 16, m, chunk, v);
     }
     return;
   }
@@ -425,13 +425,13 @@ static void qmm_dispatch(const TimedLaunch& tl, QmmShape sh, int grid, hipStream
 }
 
 int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
-  act_kernel<uint16_t><<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, a.K, a.nkb, static_cast<uint4*>(a.frag));
+  act_kernel<uint16_t><<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, a.K, a.nkb, a.ntile, static_cast<uint4*>(a.frag));
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
 
 int launch_act_from_f32(ih_ctx* c, const float* x, int ldx, int M, ActBuf& a) {
-  act_kernel<float><<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, a.K, a.nkb, static_cast<uint4*>(a.frag));
+  act_kernel<float><<<MAX_TOK, 256, 0, c->stream>>>(x, ldx, M, a.K, a.nkb, a.ntile, static_cast<uint4*>(a.frag));
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -13,7 +13,7 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
                                                         const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
                                                         float* __restrict__ h, int H, int ldh,
                                                         const uint16_t* __restrict__ nw, uint4* __restrict__ frag,
-                                                        int nkb, float* __restrict__ ss_out) {
+                                                        int nkb, int ntile, float* __restrict__ ss_out) {
   __shared__ float red[4];
   const int row = blockIdx.x;
   const uint32_t t = tok[row];
@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
       ss += x * x;
       v[j] = x * dbf16(nw[8 * c + j]);
     }
-    frag_store_chunk(frag, nkb, row, c, v);
+    frag_store_chunk(frag, nkb, ntile, row, c, v);
   }
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
@@ -100,7 +100,7 @@ int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const ui
                      float* h, int B, int H, const uint16_t* nw, ActBuf& a) {
   TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4 + 2));
   tlaunch(tl, embed_act_kernel, dim3(B), dim3(256), 0, c->stream, tok, w, s, b, h, H, H, nw, static_cast<uint4*>(a.frag),
-          a.nkb, a.ss);
+          a.nkb, a.ntile, a.ss);
   IH_HIP(hipGetLastError());
   a.nss = 1;
   return IH_OK;
