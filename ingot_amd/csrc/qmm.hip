@@ -14,8 +14,10 @@
 //     ((w >> 4c) & 0x000F000F | 0x43004300), so the MFMA sums Σ x·(128 + q) exactly in fp32 per group of 64; one more
 //     MFMA against a ones operand gives Σ x per group and token in the same layout, and the affine map is applied
 //     once per group and output: y += s·acc + (b − 128·s)·Σx. No rounding of the dequantised weight.
-//   - Token 16 (the 17th row of a k = 16 block) runs on VALU packed bf16 dot products instead of a second, almost
-//     empty MFMA tile; its bits never depend on M.
+//   - Token 16 (the 17th row of a k = 16 block) is the only live row of a second MFMA token tile whose A operand
+//     comes from LDS (token 16 staged once per workgroup, zeros for the other rows), so it costs no extra
+//     vector-memory instructions and one output element of VALU work. Each MFMA output element depends only on its
+//     own A row, so its bits are those of the M > 17 path (two full token tiles) and never depend on M.
 //   - K is split over the waves of a workgroup (a split chosen from (N, K) only, never from M) and the partial sums are
 //     added in wave order in LDS: deterministic and row-invariant (row r's bits do not depend on M).
 #include "act.h"
@@ -109,30 +111,33 @@ struct QmmParams {
   int act_f16;  // the next activation in fp16 (the input of MXFP4 experts) instead of bf16
 };
 
-// One K-block's operands of a wave: R weight tiles (+ scale/bias) and the token tiles of x.
-template <int T, int R, bool X16>
-struct QmmStage {
+// One K-block's operands of a wave, in two rings of different depth: the weight tiles (+ scale/bias) come from HBM
+// and are prefetched far ahead; the token fragments of x are L2 hits and need only a short lead.
+template <int R>
+struct QmmW {
   u32x4 w[R];
   uint2 sb[R];
+};
+template <int T, bool X16>
+struct QmmX {
   u32x4 x[T][4];
-  u32x4 x16[X16 ? 4 : 1];   // token 16 (VALU path): this lane's 64 bytes of it
+  u32x4 x16[X16 ? 4 : 1];   // token 16's A operand (rows 1–15 zero), from LDS
 };
 
 struct QmmRsrc {
   __amdgpu_buffer_rsrc_t w, s, x;
   unsigned xoff[2];   // this lane's offset in a K-block's fragments (OOB for dead tokens), per token tile
-  unsigned x16off;    // token 16 (VALU path): its 16 bytes of the lane's qd
 };
 
-template <int T, int R, bool X16>
-__device__ __forceinline__ void qmm_load(QmmStage<T, R, X16>& st, const QmmParams& p, const QmmRsrc& rs, int tile0,
-                                         int kb, int lane, int n) {
-  // Past the last K-block every offset is forced out of range (offsets stay below 2^31, so OR-ing OOB keeps them out):
-  // the loads are issued unconditionally, read zeros without touching memory, and the loop body is one basic block
-  // with a fixed number of loads in flight, so the wait before each multiply covers only the stage it reads.
+// Past the last K-block every offset is forced out of range (offsets stay below 2^31, so OR-ing OOB keeps them out):
+// the loads are issued unconditionally, read zeros without touching memory, and the loop body is one basic block
+// with a fixed number of loads in flight, so the wait before each multiply covers only the stage it reads.
+// The scheduling barriers keep a stage's loads together, ahead of the multiply that follows (LLVM's scheduler
+// otherwise sinks them toward their use and the prefetch distance collapses).
+template <int R>
+__device__ __forceinline__ void qmm_load_w(QmmW<R>& st, const QmmParams& p, const QmmRsrc& rs, int tile0, int kb,
+                                           int lane, int n) {
   const unsigned oob = kb < p.nkb ? 0u : OOB;
-  // The scheduling barriers keep the stage's loads together, ahead of the multiply of the previous stage (LLVM's
-  // scheduler otherwise sinks them toward their use and the prefetch distance collapses).
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -141,7 +146,18 @@ __device__ __forceinline__ void qmm_load(QmmStage<T, R, X16>& st, const QmmParam
         u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, (tb * 1024u + lane * 16u) | oob, 0, 0));
     st.sb[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.s, (tb * 128u + n * 8u) | oob, 0, 0));
   }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Token 16 is staged in LDS once per workgroup (x16s: [kb][t][qd] 16 bytes, block nkb all zeros): all 16 row lanes of
+// a lane group read the same 16 bytes, a broadcast read, where a buffer load would spend a full vector-memory
+// instruction per MFMA step on 64 distinct bytes.
+template <int T, bool X16>
+__device__ __forceinline__ void qmm_load_x(QmmX<T, X16>& st, const QmmParams& p, const QmmRsrc& rs, int kb,
+                                           const u32x4* x16s, int n, int qd) {
+  const unsigned oob = kb < p.nkb ? 0u : OOB;
   const unsigned kx = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u;  // [kb][tile][t][1 KB]
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int tt = 0; tt < T; ++tt)
 #pragma unroll
@@ -149,17 +165,49 @@ __device__ __forceinline__ void qmm_load(QmmStage<T, R, X16>& st, const QmmParam
       st.x[tt][t] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.xoff[tt] + kx + 1024 * t) | oob, 0, 0));
   if constexpr (X16) {
+    // The A operand of the second token tile: row 0 (lanes n = 0) is token 16, rows 1–15 read the zero block.
+    const int kq = (kb < p.nkb && n == 0) ? kb : p.nkb;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      st.x16[t] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.x16off + kx + 1024 * t) | oob, 0, 0));
+    for (int t = 0; t < 4; ++t) st.x16[t] = x16s[(kq * 4 + t) * 4 + qd];
   }
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Stage token 16 of every K-block into LDS (entries e = (kb·4 + t)·4 + qd, 16 bytes each, the fragment bytes at
+// kb·(MAX_TOK/16)·4096 + 4096 + 1024·t + 16·qd), and zero block nkb: eight loads per thread, issued before the weight
+// prologue so that their latency overlaps it, then stored after it. Straight-line code with a fixed number of loads:
+// a loop here would make the wait counts of everything after it conservative. Shapes whose (nkb + 1)·16 entries
+// exceed 8·NTHR take the two-tile path instead.
+template <int NTHR>
+struct QmmX16Stage {
+  u32x4 v[8];
+};
+
+__device__ __forceinline__ u32x4 qmm_x16_entry(const QmmParams& p, const QmmRsrc& rs, int e) {
+  const int kb = e >> 4, t = (e >> 2) & 3, qd = e & 3;
+  const unsigned off = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * qd;
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, kb < p.nkb ? off : OOB, 0, 0));
+}
+
+template <int NTHR>
+__device__ __forceinline__ void qmm_x16_issue(QmmX16Stage<NTHR>& st, const QmmParams& p, const QmmRsrc& rs) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st.v[j] = qmm_x16_entry(p, rs, j * NTHR + int(threadIdx.x));
+}
+
+template <int NTHR>
+__device__ __forceinline__ void qmm_x16_commit(const QmmX16Stage<NTHR>& st, u32x4* x16s, const QmmParams& p) {
+  const int ne = (p.nkb + 1) * 16;  // at most 8·NTHR (checked at launch)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = j * NTHR + int(threadIdx.x);
+    if (e < ne) x16s[e] = st.v[j];
+  }
+}
+
 template <int T, int R, bool X16>
-__device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R], const QmmStage<T, R, X16>& st,
-                                            unsigned km, unsigned kbias, float qd0) {
+__device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R], const QmmW<R>& sw,
+                                            const QmmX<T, X16>& st, unsigned km, unsigned kbias) {
   // Σx per group and token (ones operand), in the D layout of the products: lane (n, qd) gets tokens 4qd … 4qd+3.
   const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
   f32x4 xs[T][2];
@@ -172,10 +220,8 @@ __device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R
       xs[tt][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), ones, z, 0,
                                                           0, 0);
     }
-  // Token 16: Σx per group. Every lane holds token 16's fragment of its K slice (the same for all 16 row lanes), so the
-  // ones MFMA over it gives the whole group's sum in every output element; the qd = 0 lanes add the bias term once.
-  // (A v_dot2c chain against a (1, 1) pair was miscompiled here: LLVM reused one source register for the four
-  // elements of the vector.)
+  // Token 16 (X16): a second token tile whose only live row is token 16; Σx per group lands in element 0 of the
+  // qd = 0 lanes, like every other output of that token.
   float xs16[2] = {0.f, 0.f};
   if constexpr (X16) {
 #pragma unroll
@@ -183,16 +229,16 @@ __device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R
       f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g]), ones,
                                                         f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
       z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g + 1]), ones, z, 0, 0, 0);
-      xs16[g] = z[0] * qd0;
+      xs16[g] = z[0];
     }
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float s0 = bf16f(st.sb[r].x & 0xFFFFu), s1 = bf16f(st.sb[r].y & 0xFFFFu);
-    const float c0 = fmaf(-128.f, s0, bf16f(st.sb[r].x >> 16)), c1 = fmaf(-128.f, s1, bf16f(st.sb[r].y >> 16));
+    const float s0 = bf16f(sw.sb[r].x & 0xFFFFu), s1 = bf16f(sw.sb[r].y & 0xFFFFu);
+    const float c0 = fmaf(-128.f, s0, bf16f(sw.sb[r].x >> 16)), c1 = fmaf(-128.f, s1, bf16f(sw.sb[r].y >> 16));
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      const bf16x8 w0 = nib_bf16(st.w[r][2 * g], km, kbias), w1 = nib_bf16(st.w[r][2 * g + 1], km, kbias);
+      const bf16x8 w0 = nib_bf16(sw.w[r][2 * g], km, kbias), w1 = nib_bf16(sw.w[r][2 * g + 1], km, kbias);
       const float sg = g ? s1 : s0, cg = g ? c1 : c0;
 #pragma unroll
       for (int tt = 0; tt < T; ++tt) {
@@ -204,32 +250,26 @@ __device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R
         for (int e = 0; e < 4; ++e) acc[r][tt][e] = fmaf(sg, tmp[e], fmaf(cg, xs[tt][g][e], acc[r][tt][e]));
       }
       if constexpr (X16) {
-        float d = 0.f;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const unsigned wr = st.w[r][2 * g + h];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const unsigned wp = and_or(wr >> (4 * j), km, kbias);
-            const unsigned xp = st.x16[2 * g + h][j];
-            d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wp), __builtin_bit_cast(bf16x2, xp), d,
-                                                false);
-          }
-        }
-        acc16[r] = fmaf(sg, d, fmaf(cg, xs16[g], acc16[r]));
+        f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g]), w0,
+                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g + 1]), w1, tmp, 0, 0,
+                                                      0);
+        acc16[r] = fmaf(sg, tmp[0], fmaf(cg, xs16[g], acc16[r]));
       }
     }
   }
 }
 
 
-// T: MFMA token tiles (tokens 0–15, and 17–31 when T = 2); X16: token 16 present (M ≥ 17), done on VALU.
+// T: MFMA token tiles loaded from memory (tokens 0–15, and 16–31 when T = 2); X16 (with T = 1, M = 17): token 16
+// as a second tile from LDS.
 // Workgroup = KW waves over the same 16·R rows; wave w takes K-blocks w, w + KW, … (adjacent waves read adjacent
 // 1 KB blocks), with the next block's loads in flight while the current one is multiplied. The KW partial sums are
 // added in wave order through LDS: no cross-workgroup synchronisation (an agent-scope fence on MI355X writes the
 // XCD's L2 back and costs tens of µs) and a summation order that depends only on (N, K).
-template <int T, int R, int KW, bool X16, int NS>
+template <int T, int R, int KW, bool X16, int DW, int DX>
 __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
+  static_assert(DW % DX == 0, "the x ring depth divides the weight ring depth");
   // The wave index is uniform: readfirstlane keeps it (and the K-block loop) in scalar registers and scalar branches.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, qd = lane >> 4;
@@ -252,30 +292,45 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int tok = 16 * tt + n;
-    const bool live = tt < T && tok < p.M && !(X16 && tok == 16);
+    const bool live = tt < T && tok < p.M;
     rs.xoff[tt] = live ? (unsigned(tt) * 4096u + n * 64u + qd * 16u) : OOB;
   }
-  rs.x16off = 4096u + qd * 16u;  // tile 1, token 0 of the tile
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
-  const float qd0 = qd == 0 ? 1.f : 0.f;
 
-  // NS stages of loads in flight. This wave's K-blocks are wave, wave + KW, … (nk of them), NS per trip of a loop
-  // with a single exit (a loop with two exits is structurized into a join that the wait-count pass treats as a back
-  // edge with other stages' loads still pending, which serialises every trip). Stages past the end are loaded out of
-  // range: zero weights and scales, so their products add exact zeros (the count depends only on the shape).
-  QmmStage<T, R, X16> st[NS];
+  // DW K-blocks of weights and DX of x in flight. This wave's K-blocks are wave, wave + KW, … (nk of them), DW per
+  // trip of a loop with a single exit (a loop with two exits is structurized into a join that the wait-count pass
+  // treats as a back edge with other stages' loads still pending, which serialises every trip). Stages past the end
+  // are loaded out of range: zero weights and scales, so their products add exact zeros (the count depends only on
+  // the shape).
+  // Prologue in the order of the steady state (x(j) issued DX stages ahead of its use, w(j) DW stages ahead, x before
+  // w within a stage), so the wait counts at the loop head are those of every later trip.
+  extern __shared__ u32x4 x16s[];
+  QmmX16Stage<64 * KW> x16st;
+  if constexpr (X16) qmm_x16_issue(x16st, p, rs);
+  QmmW<R> sw[DW];
+  QmmX<T, X16> sx[DX];
   int kb = wave;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) qmm_load(st[s], p, rs, tile0, kb + s * KW, lane, n);
+  for (int t = -DW; t < -DX; ++t) qmm_load_w(sw[t + DW], p, rs, tile0, kb + (t + DW) * KW, lane, n);
+  if constexpr (X16) {
+    qmm_x16_commit(x16st, x16s, p);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = -DX; t < 0; ++t) {
+    qmm_load_x(sx[t + DX], p, rs, kb + (t + DX) * KW, x16s, n, qd);
+    qmm_load_w(sw[t + DW], p, rs, tile0, kb + (t + DW) * KW, lane, n);
+  }
   const int nk = kb < p.nkb ? (p.nkb - kb + KW - 1) / KW : 0;
-  const int trips = (nk + NS - 1) / NS;
+  const int trips = (nk + DW - 1) / DW;
   for (int it = 0; it < trips; ++it) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      qmm_compute(acc, acc16, st[s], km, kbias, qd0);
-      qmm_load(st[s], p, rs, tile0, kb + (s + NS) * KW, lane, n);
+    for (int s = 0; s < DW; ++s) {
+      qmm_compute(acc, acc16, sw[s], sx[s % DX], km, kbias);
+      qmm_load_x(sx[s % DX], p, rs, kb + (s + DX) * KW, x16s, n, qd);
+      qmm_load_w(sw[s], p, rs, tile0, kb + (s + DW) * KW, lane, n);
     }
-    kb += NS * KW;
+    kb += DW * KW;
   }
 
   // RMSNorm factors of the input rows (the norm's sums of squares come in as partials of the producer's workgroups,
@@ -293,14 +348,6 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     }
   }
 
-  // Token 16: sum the four K slices of each row across lanes (qd = lane bits 4–5), fixed order.
-  if constexpr (X16) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      acc16[r] += __shfl_xor(acc16[r], 16);
-      acc16[r] += __shfl_xor(acc16[r], 32);
-    }
-  }
   // Partial sums of every wave → LDS [wave][r][tt][e][lane] (+ token 16 [wave][r][row]), then fixed-order sums.
   constexpr int NEL = R * T * 4 * 64;
   constexpr int NEL16 = X16 ? R * 16 : 0;
@@ -398,30 +445,32 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 
 // Launch shape for an (Npad, nkb) matrix: rows per workgroup (16·R) and waves per workgroup (KW, the intra-workgroup
 // split of K). Chosen from the shape only, never from M, so each row's summation order is fixed.
-struct QmmShape { int R, KW, NS; };
+struct QmmShape { int R, KW, DW, DX; };
 static QmmShape qmm_shape(int Npad, int nkb) {
+  // Measured at M = 16/17 on gfx950, cold weights (8B shapes): four row tiles per wave when there are enough tiles
+  // to fill the chip (fewer activation bytes per weight byte), two for mid-sized N, one for N ≤ 4096.
   const int NT = Npad / 16;
-  if (NT >= 4096) return {4, 4, 2};
-  if (NT >= 1024) return {2, 4, 2};
-  if (NT >= 512 || nkb < 16) return {1, 4, 2};
-  if (nkb < 64) return {1, 8, 2};
-  return {1, 16, 2};
+  (void)nkb;
+  if (NT >= 1536) return {4, 4, 2, 2};
+  if (NT >= 384) return {2, 4, 4, 2};
+  return {1, 4, 4, 2};
 }
 
 template <int T, bool X16>
 static void qmm_dispatch(const TimedLaunch& tl, QmmShape sh, int grid, hipStream_t st, const QmmParams& p) {
-#define IH_QMM_CASE(R_, KW_, NS_)                                                                  \
-  if (sh.R == R_ && sh.KW == KW_ && sh.NS == NS_) {                                                \
-    tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, NS_>, dim3(grid), dim3(64 * KW_), 0, st, p);      \
-    return;                                                                                        \
+  const size_t shm = X16 ? size_t(p.nkb + 1) * 256 : 0;  // token 16 staged in LDS
+#define IH_QMM_CASE(R_, KW_, DW_, DX_)                                                                \
+  if (sh.R == R_ && sh.KW == KW_ && sh.DW == DW_ && sh.DX == DX_) {                                  \
+    tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, DW_, DX_>, dim3(grid), dim3(64 * KW_), shm, st, p); \
+    return;                                                                                          \
   }
-  IH_QMM_CASE(4, 4, 2) IH_QMM_CASE(4, 4, 3)
-  IH_QMM_CASE(2, 4, 2) IH_QMM_CASE(2, 4, 3) IH_QMM_CASE(2, 4, 4)
-  IH_QMM_CASE(1, 4, 2) IH_QMM_CASE(1, 4, 4)
-  IH_QMM_CASE(1, 8, 2) IH_QMM_CASE(1, 8, 4)
-  IH_QMM_CASE(1, 16, 2) IH_QMM_CASE(1, 16, 4)
+  IH_QMM_CASE(1, 4, 4, 2) IH_QMM_CASE(1, 4, 8, 2) IH_QMM_CASE(1, 8, 4, 2) IH_QMM_CASE(1, 8, 8, 2)
+  IH_QMM_CASE(1, 16, 4, 2)
+  IH_QMM_CASE(2, 4, 2, 2) IH_QMM_CASE(2, 4, 4, 2) IH_QMM_CASE(2, 4, 8, 2) IH_QMM_CASE(2, 8, 4, 2)
+  IH_QMM_CASE(2, 8, 8, 2)
+  IH_QMM_CASE(4, 4, 2, 2) IH_QMM_CASE(4, 4, 4, 2) IH_QMM_CASE(4, 8, 4, 2)
 #undef IH_QMM_CASE
-  tlaunch(tl, qmm_int4_kernel<T, 1, 4, X16, 2>, dim3(grid), dim3(256), 0, st, p);
+  tlaunch(tl, qmm_int4_kernel<T, 1, 8, X16, 8, 2>, dim3(grid), dim3(512), shm, st, p);
 }
 
 int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
@@ -446,7 +495,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   IH_CHECK(M >= 1 && M <= MAX_TOK, IH_EINVAL, "qmm: M must be in 1..32");
   IH_CHECK(a.nkb == W->nkb && !a.f16, IH_EINVAL, "qmm: activation K does not match the matrix");
   QmmShape sh = qmm_shape(W->Npad, W->nkb);
-  if (const char* ov = getenv("IH_QMM_SHAPE")) sscanf(ov, "%d,%d,%d", &sh.R, &sh.KW, &sh.NS);  // tuning override
+  if (const char* ov = getenv("IH_QMM_SHAPE")) sscanf(ov, "%d,%d,%d,%d", &sh.R, &sh.KW, &sh.DW, &sh.DX);  // tuning override
   QmmParams p{};
   const size_t tiles_per_e = size_t(W->Npad / 16) * W->nkb;
   p.w = static_cast<const uint4*>(W->w) + tiles_per_e * 64 * expert;
@@ -493,8 +542,9 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   const double ybytes = double(M) * W->N *
                         (ep.mode == QM_BF16 ? 2 : (ep.mode == QM_F32_ADD || ep.mode == QM_RESID_ACT ? 8 : 4));
   TimedLaunch tl(c, TC_QMM, double(W->algo_bytes) + double(M) * W->K * 2 + ybytes);
-  if (M > 17) qmm_dispatch<2, true>(tl, sh, grid, c->stream, p);
-  else if (M == 17) qmm_dispatch<1, true>(tl, sh, grid, c->stream, p);
+  if (M > 17) qmm_dispatch<2, false>(tl, sh, grid, c->stream, p);
+  else if (M == 17 && (W->nkb + 1) * 16 <= 8 * 64 * sh.KW) qmm_dispatch<1, true>(tl, sh, grid, c->stream, p);
+  else if (M == 17) qmm_dispatch<2, false>(tl, sh, grid, c->stream, p);  // K too long to stage token 16 in LDS
   else qmm_dispatch<1, false>(tl, sh, grid, c->stream, p);
   IH_HIP(hipGetLastError());
   return IH_OK;
