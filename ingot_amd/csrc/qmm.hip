@@ -111,17 +111,18 @@ struct QmmParams {
   int act_f16;  // the next activation in fp16 (the input of MXFP4 experts) instead of bf16
 };
 
-// One K-block's operands of a wave, in two rings of different depth: the weight tiles (+ scale/bias) come from HBM
-// and are prefetched far ahead; the token fragments of x are L2 hits and need only a short lead.
+// One K-block's operands of a wave, in two rings of different depth: the weight tiles come from HBM and are
+// prefetched far ahead; the token fragments of x (L2 hits) and the LDS-staged token 16 and scale/bias words need only
+// a short lead.
 template <int R>
 struct QmmW {
   u32x4 w[R];
-  uint2 sb[R];
 };
-template <int T, bool X16>
+template <int T, int R, bool X16>
 struct QmmX {
   u32x4 x[T][4];
   u32x4 x16[X16 ? 4 : 1];   // token 16's A operand (rows 1–15 zero), from LDS
+  uint2 sb[R];              // scale | bias << 16 of the two groups of the K-block, row n of each tile, from LDS
 };
 
 struct QmmRsrc {
@@ -144,7 +145,6 @@ __device__ __forceinline__ void qmm_load_w(QmmW<R>& st, const QmmParams& p, cons
     const unsigned tb = unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kb);
     st.w[r] = __builtin_bit_cast(
         u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, (tb * 1024u + lane * 16u) | oob, 0, 0));
-    st.sb[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.s, (tb * 128u + n * 8u) | oob, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -152,9 +152,9 @@ __device__ __forceinline__ void qmm_load_w(QmmW<R>& st, const QmmParams& p, cons
 // Token 16 is staged in LDS once per workgroup (x16s: [kb][t][qd] 16 bytes, block nkb all zeros): all 16 row lanes of
 // a lane group read the same 16 bytes, a broadcast read, where a buffer load would spend a full vector-memory
 // instruction per MFMA step on 64 distinct bytes.
-template <int T, bool X16>
-__device__ __forceinline__ void qmm_load_x(QmmX<T, X16>& st, const QmmParams& p, const QmmRsrc& rs, int kb,
-                                           const u32x4* x16s, int n, int qd) {
+template <int T, int R, bool X16>
+__device__ __forceinline__ void qmm_load_x(QmmX<T, R, X16>& st, const QmmParams& p, const QmmRsrc& rs, int kb,
+                                           const u32x4* x16s, const uint2* sbs, int n, int qd) {
   const unsigned oob = kb < p.nkb ? 0u : OOB;
   const unsigned kx = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u;  // [kb][tile][t][1 KB]
   __builtin_amdgcn_sched_barrier(0);
@@ -170,44 +170,69 @@ __device__ __forceinline__ void qmm_load_x(QmmX<T, X16>& st, const QmmParams& p,
 #pragma unroll
     for (int t = 0; t < 4; ++t) st.x16[t] = x16s[(kq * 4 + t) * 4 + qd];
   }
+  // Past the last K-block the scales read the zero block that follows the staged words (the weights are zero there
+  // too, and the bias term must not add c·Σx): an address select, so the loop body stays one basic block.
+  const bool kin = kb < p.nkb;
+#pragma unroll
+  for (int r = 0; r < R; ++r) st.sb[r] = sbs[(kin ? (r * p.nkb + kb) * 16 : R * p.nkb * 16) + n];
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Stage token 16 of every K-block into LDS (entries e = (kb·4 + t)·4 + qd, 16 bytes each, the fragment bytes at
-// kb·(MAX_TOK/16)·4096 + 4096 + 1024·t + 16·qd), and zero block nkb: eight loads per thread, issued before the weight
-// prologue so that their latency overlaps it, then stored after it. Straight-line code with a fixed number of loads:
-// a loop here would make the wait counts of everything after it conservative. Shapes whose (nkb + 1)·16 entries
-// exceed 8·NTHR take the two-tile path instead.
-template <int NTHR>
-struct QmmX16Stage {
-  u32x4 v[8];
+// Workgroup staging in LDS, loaded once for all KW waves: token 16 of every K-block (X16; entries
+// e = (kb·4 + t)·4 + qd, 16 bytes each, the fragment bytes at kb·(MAX_TOK/16)·4096 + 4096 + 1024·t + 16·qd, then a
+// zero block nkb) and the scale/bias words of the workgroup's R tiles (contiguous in the packed layout:
+// [tile][kb][row] 8 bytes, from tile0·nkb·128). Eight loads per thread for each, issued before the weight prologue so
+// that their latency overlaps it, stored after it. Straight-line code with a fixed number of loads: a loop here would
+// make the wait counts of everything after it conservative. The launch checks that both fit in 8·NTHR entries.
+template <int NTHR, bool X16>
+struct QmmStage {
+  u32x4 v16[X16 ? 8 : 1];
+  u32x4 vsb[8];
 };
 
-__device__ __forceinline__ u32x4 qmm_x16_entry(const QmmParams& p, const QmmRsrc& rs, int e) {
-  const int kb = e >> 4, t = (e >> 2) & 3, qd = e & 3;
-  const unsigned off = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * qd;
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, kb < p.nkb ? off : OOB, 0, 0));
-}
-
-template <int NTHR>
-__device__ __forceinline__ void qmm_x16_issue(QmmX16Stage<NTHR>& st, const QmmParams& p, const QmmRsrc& rs) {
+template <int NTHR, bool X16>
+__device__ __forceinline__ void qmm_stage_issue(QmmStage<NTHR, X16>& st, const QmmParams& p, const QmmRsrc& rs,
+                                                int tile0, int R) {
+  if constexpr (X16) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) st.v[j] = qmm_x16_entry(p, rs, j * NTHR + int(threadIdx.x));
+    for (int j = 0; j < 8; ++j) {
+      const int e = j * NTHR + int(threadIdx.x);
+      const int kb = e >> 4, t = (e >> 2) & 3, qd = e & 3;
+      const unsigned off = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * qd;
+      st.v16[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, kb < p.nkb ? off : OOB, 0, 0));
+    }
+  }
+  const unsigned nsb = unsigned(R) * unsigned(p.nkb) * 8u, base = unsigned(tile0) * unsigned(p.nkb) * 128u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const unsigned e = unsigned(j * NTHR) + threadIdx.x;
+    st.vsb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.s, e < nsb ? base + e * 16u : OOB, 0, 0));
+  }
 }
 
-template <int NTHR>
-__device__ __forceinline__ void qmm_x16_commit(const QmmX16Stage<NTHR>& st, u32x4* x16s, const QmmParams& p) {
-  const int ne = (p.nkb + 1) * 16;  // at most 8·NTHR (checked at launch)
+template <int NTHR, bool X16>
+__device__ __forceinline__ void qmm_stage_commit(const QmmStage<NTHR, X16>& st, u32x4* x16s, u32x4* sbs,
+                                                 const QmmParams& p, int R) {
+  if constexpr (X16) {
+    const int ne = (p.nkb + 1) * 16;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = j * NTHR + int(threadIdx.x);
+      if (e < ne) x16s[e] = st.v16[j];
+    }
+  }
+  const int nsb = R * p.nkb * 8;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int e = j * NTHR + int(threadIdx.x);
-    if (e < ne) x16s[e] = st.v[j];
+    if (e < nsb) sbs[e] = st.vsb[j];
   }
+  if (threadIdx.x < 8) sbs[nsb + threadIdx.x] = u32x4{0u, 0u, 0u, 0u};  // the zero block (16 rows × 8 bytes)
 }
 
 template <int T, int R, bool X16>
 __device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R], const QmmW<R>& sw,
-                                            const QmmX<T, X16>& st, unsigned km, unsigned kbias) {
+                                            const QmmX<T, R, X16>& st, unsigned km, unsigned kbias) {
   // Σx per group and token (ones operand), in the D layout of the products: lane (n, qd) gets tokens 4qd … 4qd+3.
   const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
   f32x4 xs[T][2];
@@ -234,8 +259,8 @@ __device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float s0 = bf16f(sw.sb[r].x & 0xFFFFu), s1 = bf16f(sw.sb[r].y & 0xFFFFu);
-    const float c0 = fmaf(-128.f, s0, bf16f(sw.sb[r].x >> 16)), c1 = fmaf(-128.f, s1, bf16f(sw.sb[r].y >> 16));
+    const float s0 = bf16f(st.sb[r].x & 0xFFFFu), s1 = bf16f(st.sb[r].y & 0xFFFFu);
+    const float c0 = fmaf(-128.f, s0, bf16f(st.sb[r].x >> 16)), c1 = fmaf(-128.f, s1, bf16f(st.sb[r].y >> 16));
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const bf16x8 w0 = nib_bf16(sw.w[r][2 * g], km, kbias), w1 = nib_bf16(sw.w[r][2 * g + 1], km, kbias);
@@ -304,21 +329,22 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   // the shape).
   // Prologue in the order of the steady state (x(j) issued DX stages ahead of its use, w(j) DW stages ahead, x before
   // w within a stage), so the wait counts at the loop head are those of every later trip.
-  extern __shared__ u32x4 x16s[];
-  QmmX16Stage<64 * KW> x16st;
-  if constexpr (X16) qmm_x16_issue(x16st, p, rs);
+  extern __shared__ u32x4 stage_lds[];
+  u32x4* const x16s = stage_lds;
+  u32x4* const sbs = stage_lds + (X16 ? (p.nkb + 1) * 16 : 0);
+  QmmStage<64 * KW, X16> stg;
+  qmm_stage_issue(stg, p, rs, tile0, R);
   QmmW<R> sw[DW];
-  QmmX<T, X16> sx[DX];
+  QmmX<T, R, X16> sx[DX];
   int kb = wave;
 #pragma unroll
   for (int t = -DW; t < -DX; ++t) qmm_load_w(sw[t + DW], p, rs, tile0, kb + (t + DW) * KW, lane, n);
-  if constexpr (X16) {
-    qmm_x16_commit(x16st, x16s, p);
-    __syncthreads();
-  }
+  qmm_stage_commit(stg, x16s, sbs, p, R);
+  __syncthreads();
+  const uint2* const sbv = reinterpret_cast<const uint2*>(sbs);
 #pragma unroll
   for (int t = -DX; t < 0; ++t) {
-    qmm_load_x(sx[t + DX], p, rs, kb + (t + DX) * KW, x16s, n, qd);
+    qmm_load_x(sx[t + DX], p, rs, kb + (t + DX) * KW, x16s, sbv, n, qd);
     qmm_load_w(sw[t + DW], p, rs, tile0, kb + (t + DW) * KW, lane, n);
   }
   const int nk = kb < p.nkb ? (p.nkb - kb + KW - 1) / KW : 0;
@@ -327,7 +353,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 #pragma unroll
     for (int s = 0; s < DW; ++s) {
       qmm_compute(acc, acc16, sw[s], sx[s % DX], km, kbias);
-      qmm_load_x(sx[s % DX], p, rs, kb + (s + DX) * KW, x16s, n, qd);
+      qmm_load_x(sx[s % DX], p, rs, kb + (s + DX) * KW, x16s, sbv, n, qd);
       qmm_load_w(sw[s], p, rs, tile0, kb + (s + DW) * KW, lane, n);
     }
     kb += DW * KW;
@@ -450,27 +476,30 @@ static QmmShape qmm_shape(int Npad, int nkb) {
   // Measured at M = 16/17 on gfx950, cold weights (8B shapes): four row tiles per wave when there are enough tiles
   // to fill the chip (fewer activation bytes per weight byte), two for mid-sized N, one for N ≤ 4096.
   const int NT = Npad / 16;
-  (void)nkb;
-  if (NT >= 1536) return {4, 4, 2, 2};
-  if (NT >= 384) return {2, 4, 4, 2};
-  return {1, 4, 4, 2};
+  QmmShape sh = NT >= 1536 ? QmmShape{4, 4, 2, 1} : NT >= 384 ? QmmShape{2, 4, 4, 2} : QmmShape{1, 4, 4, 2};
+  // The workgroup's scale/bias words (R·nkb·128 bytes) are staged in LDS by eight 16-byte loads per thread.
+  while (sh.R > 1 && sh.R * nkb > 64 * sh.KW) sh.R /= 2;
+  if (sh.R * nkb > 64 * sh.KW) sh = QmmShape{1, 16, 4, 2};
+  return sh;
 }
 
 template <int T, bool X16>
-static void qmm_dispatch(const TimedLaunch& tl, QmmShape sh, int grid, hipStream_t st, const QmmParams& p) {
-  const size_t shm = X16 ? size_t(p.nkb + 1) * 256 : 0;  // token 16 staged in LDS
+static bool qmm_dispatch(const TimedLaunch& tl, QmmShape sh, int grid, hipStream_t st, const QmmParams& p) {
+  // LDS staging: token 16 (X16) and the scale/bias words of the workgroup's R tiles.
+  const size_t shm16 = (X16 ? size_t(p.nkb + 1) * 256 : 0) + 128, shsb = size_t(p.nkb) * 128;
 #define IH_QMM_CASE(R_, KW_, DW_, DX_)                                                                \
   if (sh.R == R_ && sh.KW == KW_ && sh.DW == DW_ && sh.DX == DX_) {                                  \
-    tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, DW_, DX_>, dim3(grid), dim3(64 * KW_), shm, st, p); \
-    return;                                                                                          \
+    tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, DW_, DX_>, dim3(grid), dim3(64 * KW_), shm16 + R_ * shsb, st, p); \
+    return true;                                                                                          \
   }
-  IH_QMM_CASE(1, 4, 4, 2) IH_QMM_CASE(1, 4, 8, 2) IH_QMM_CASE(1, 8, 4, 2) IH_QMM_CASE(1, 8, 8, 2)
-  IH_QMM_CASE(1, 16, 4, 2)
-  IH_QMM_CASE(2, 4, 2, 2) IH_QMM_CASE(2, 4, 4, 2) IH_QMM_CASE(2, 4, 8, 2) IH_QMM_CASE(2, 8, 4, 2)
-  IH_QMM_CASE(2, 8, 8, 2)
-  IH_QMM_CASE(4, 4, 2, 2) IH_QMM_CASE(4, 4, 4, 2) IH_QMM_CASE(4, 8, 4, 2)
+  IH_QMM_CASE(1, 4, 1, 1) IH_QMM_CASE(1, 4, 2, 1) IH_QMM_CASE(1, 4, 2, 2) IH_QMM_CASE(1, 4, 4, 2)
+  IH_QMM_CASE(1, 8, 1, 1) IH_QMM_CASE(1, 8, 2, 1) IH_QMM_CASE(1, 8, 4, 2) IH_QMM_CASE(1, 16, 4, 2)
+  IH_QMM_CASE(2, 4, 1, 1) IH_QMM_CASE(2, 4, 2, 1) IH_QMM_CASE(2, 4, 2, 2) IH_QMM_CASE(2, 4, 4, 2)
+  IH_QMM_CASE(2, 8, 1, 1) IH_QMM_CASE(2, 8, 2, 1)
+  IH_QMM_CASE(4, 4, 1, 1) IH_QMM_CASE(4, 4, 2, 1) IH_QMM_CASE(4, 4, 2, 2) IH_QMM_CASE(4, 2, 1, 1)
+  IH_QMM_CASE(8, 4, 1, 1) IH_QMM_CASE(8, 2, 1, 1)
 #undef IH_QMM_CASE
-  tlaunch(tl, qmm_int4_kernel<T, 1, 8, X16, 8, 2>, dim3(grid), dim3(512), shm, st, p);
+  return false;  // not an instantiated shape
 }
 
 int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
@@ -517,6 +546,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
     p.D = a.K;
     p.eps = ep.eps;
   }
+  IH_CHECK(sh.R * W->nkb <= 64 * sh.KW, IH_EINVAL, "qmm: the scale/bias staging does not fit this launch shape");
   const int grid = W->Npad / (16 * sh.R);
   if (ep.mode == QM_RESID_ACT) {
     IH_CHECK(ep.act_out && ep.act_out->nkb * KBLK >= W->N && ep.nw, IH_EINVAL, "qmm: residual epilogue needs an output");
@@ -542,10 +572,12 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   const double ybytes = double(M) * W->N *
                         (ep.mode == QM_BF16 ? 2 : (ep.mode == QM_F32_ADD || ep.mode == QM_RESID_ACT ? 8 : 4));
   TimedLaunch tl(c, TC_QMM, double(W->algo_bytes) + double(M) * W->K * 2 + ybytes);
-  if (M > 17) qmm_dispatch<2, false>(tl, sh, grid, c->stream, p);
-  else if (M == 17 && (W->nkb + 1) * 16 <= 8 * 64 * sh.KW) qmm_dispatch<1, true>(tl, sh, grid, c->stream, p);
-  else if (M == 17) qmm_dispatch<2, false>(tl, sh, grid, c->stream, p);  // K too long to stage token 16 in LDS
-  else qmm_dispatch<1, false>(tl, sh, grid, c->stream, p);
+  bool ok;
+  if (M > 17) ok = qmm_dispatch<2, false>(tl, sh, grid, c->stream, p);
+  else if (M == 17 && (W->nkb + 1) * 16 <= 8 * 64 * sh.KW) ok = qmm_dispatch<1, true>(tl, sh, grid, c->stream, p);
+  else if (M == 17) ok = qmm_dispatch<2, false>(tl, sh, grid, c->stream, p);  // K too long to stage token 16 in LDS
+  else ok = qmm_dispatch<1, false>(tl, sh, grid, c->stream, p);
+  IH_CHECK(ok, IH_EINVAL, "qmm: launch shape not instantiated");
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
