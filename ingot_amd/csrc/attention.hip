@@ -294,32 +294,24 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
         // the first row's window).
         if (kb + kk0 > tile_hi[tt] || kb + kk0 + 63 < tile_lo[tt]) continue;
         const bool half2 = kk0 + 32 < nkeys;  // the block's second 32 keys are staged (uniform)
-        // All K fragments of the block first, then the four Sᵀ tiles as interleaved independent MFMA chains.
-        f16x8 kf[4][NC];
-#pragma unroll
-        for (int h = 0; h < 4; ++h)
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-            kf[h][c] = *reinterpret_cast<const f16x8*>(&Kf[(kk0 + 16 * h + j) * KR + 32 * c + 8 * qd]);
+        // The four Sᵀ tiles as interleaved independent MFMA chains, K fragments read one 32-dim step at a time (all
+        // of a block's fragments at once need more registers than the wave has next to the sub-chunk in flight).
         f32x4 sacc[4];
 #pragma unroll
         for (int h = 0; h < 4; ++h) sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
+        for (int c = 0; c < NC; ++c) {
+          f16x8 kf[4];
 #pragma unroll
-          for (int h = 0; h < 4; ++h) sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h][c], qf[tt][c], sacc[h], 0, 0, 0);
-        // Vᵀ fragments of the block, read while the softmax runs (the second half only when it is staged). With two
-        // query tiles a wave has no registers for them: they are read at the products instead.
+          for (int h = 0; h < 4; ++h)
+            kf[h] = *reinterpret_cast<const f16x8*>(&Kf[(kk0 + 16 * h + j) * KR + 32 * c + 8 * qd]);
+#pragma unroll
+          for (int h = 0; h < 4; ++h) sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h], qf[tt][c], sacc[h], 0, 0, 0);
+        }
+        // Vᵀ fragments are read at the products (the second half only when it is staged).
         auto vread = [&](int hs, int dt) {
           return *reinterpret_cast<const f16x8*>(&Vt[(16 * dt + j) * VROW + (hs && half2 ? kk0 + 32 : kk0) + 8 * qd]);
         };
-        f16x8 vf[2][NDT];
-        if constexpr (TPW == 1) {
-#pragma unroll
-          for (int hs = 0; hs < 2; ++hs)
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) vf[hs][dt] = vread(hs, dt);
-        }
         // This lane's keys kk0 + 16h + 4qd + r: their scales as one 16-byte LDS read per tile, unconditionally (a
         // conditional read becomes a branch with its own wait).
         f32x4 ksv[4], vsv[4];
@@ -374,12 +366,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
-          o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(TPW == 1 ? vf[0][dt] : vread(0, dt), pb[0], o[tt][dt], 0, 0, 0);
+          o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(0, dt), pb[0], o[tt][dt], 0, 0, 0);
         if (half2) {
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt)
             o[tt][dt] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(TPW == 1 ? vf[1][dt] : vread(1, dt), pb[1], o[tt][dt], 0, 0, 0);
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(1, dt), pb[1], o[tt][dt], 0, 0, 0);
         }
       }
     }
@@ -413,37 +405,56 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 // Reduction of the splits (vattn_reduce, verify_attn.metal:149-192): M = max over splits (and the sink), L = Σ e^(m−M)·l
 // (+ e^(sink−M)), o = Σ e^(m−M)·l·ō / L with ō = O/l the split's normalised partial; written into the o_proj
 // activation layout (column h·HD + d). One wave per (row, q head): lane = (split group sg, 8-dim group dg); a lane
-// merges splits sg, sg + SG, … (all its loads in flight), then the SG groups are merged by a fixed butterfly.
-// Grid (B, QH/4), 256 threads.
+// merges splits sg, sg + SG, … in batches of NB whose loads are all issued before any is used (a load per trip of a
+// runtime loop would wait out a memory latency per split), keeping a running (M, L, o) rescaled per batch; then the
+// SG groups are merged by a fixed butterfly. Grid (B, QH/4), 256 threads.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb, int ntile) {
-  constexpr int DG = HD / 8, SG = 64 / DG;
+  constexpr int DG = HD / 8, SG = 64 / DG, NB = 8;
   const int t = blockIdx.x, h = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int dg = lane % DG, sg = lane / DG;
   const int kvh = h / a.G, m = t * a.G + h % a.G;
-  const float2* mlh = a.ml + size_t(kvh) * a.nsplit * a.Qpad + m;
-  // Pass 1: this lane's maximum.
-  float M = -INFINITY;
-  for (int s = sg; s < a.nsplit; s += SG) M = fmaxf(M, mlh[size_t(s) * a.Qpad].x);
-  if (sg == 0 && a.sinks) M = fmaxf(M, a.sinks[h] * 1.4426950408889634f);
-  // Pass 2: weights relative to it (an empty split has m = −inf, l = 0 and weight 0).
-  float L = (sg == 0 && a.sinks) ? exp2f(a.sinks[h] * 1.4426950408889634f - M) : 0.f;
+  // The sink is a split with weight e^(sink−M) and no value.
+  float M = -INFINITY, L = 0.f;
+  if (sg == 0 && a.sinks) {
+    M = a.sinks[h] * 1.4426950408889634f;
+    L = 1.f;
+  }
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
-  for (int s = sg; s < a.nsplit; s += SG) {
-    const size_t idx = (size_t(kvh) * a.nsplit + s) * a.Qpad + m;
-    const float2 v = a.ml[idx];
-    const uint4 raw = *reinterpret_cast<const uint4*>(a.opart + idx * HD + 8 * dg);
-    const float w = v.x == -INFINITY ? 0.f : exp2f(v.x - M) * v.y;
-    L += w;
-    const unsigned rw[4] = {raw.x, raw.y, raw.z, raw.w};
+  for (int s0 = sg; s0 < a.nsplit; s0 += NB * SG) {
+    float2 v[NB];
+    uint4 raw[NB];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float2 f = __half22float2(__builtin_bit_cast(__half2, rw[e]));
-      o[2 * e] += w * f.x;
-      o[2 * e + 1] += w * f.y;
+    for (int i = 0; i < NB; ++i) {
+      const int s = s0 + i * SG;
+      const bool ok = s < a.nsplit;
+      const size_t idx = (size_t(kvh) * a.nsplit + (ok ? s : 0)) * a.Qpad + m;
+      v[i] = a.ml[idx];
+      raw[i] = *reinterpret_cast<const uint4*>(a.opart + idx * HD + 8 * dg);
+      if (!ok) v[i].x = -INFINITY;  // an empty split (m = −inf, l = 0) has weight 0
     }
+    float Mb = M;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) Mb = fmaxf(Mb, v[i].x);
+    const float ca = M == -INFINITY ? 0.f : exp2f(M - Mb);
+    L *= ca;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= ca;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const float w = v[i].x == -INFINITY ? 0.f : exp2f(v[i].x - Mb) * v[i].y;
+      L += w;
+      const unsigned rw[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float2 f = __half22float2(__builtin_bit_cast(__half2, rw[e]));
+        o[2 * e] += w * f.x;
+        o[2 * e + 1] += w * f.y;
+      }
+    }
+    M = Mb;
   }
   // Merge the split groups (lanes dg + DG·sg): butterfly over sg, fixed order.
 #pragma unroll
