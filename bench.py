@@ -199,7 +199,7 @@ def main() -> int:
         for i in range(args.steps):
             step(i)
         ctx.sync()
-        names = ["qmm", "attention", "attn_prework", "attn_reduce", "rows", "argmax", "moe", "other"]
+        names = ["qmm", "attention", "attn_prework", "attn_reduce", "rows", "argmax", "moe", "other", "qmm_finish"]
         for c, n in enumerate(names):
             t = C.c_double()
             cnt = C.c_int()

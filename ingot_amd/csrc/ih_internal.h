@@ -68,12 +68,14 @@ constexpr int MAX_TOK = 32;     // tokens per qmm (two 16-token MFMA tiles)
 // x[128kb + 32t + 8qd + perm(e)], perm = {0,4,1,5,2,6,3,7} (the order in which one 32-bit word of nibbles turns into
 // four bf16/fp16 pairs). A wave's A operand of one MFMA step is then one contiguous 1 KB read; blocks are ordered
 // [kb][g][t]. An activation that is an RMSNorm input also
-// carries the sums of squares of its (unnormalised) rows as partials of the producer's workgroups, ss[j][token]:
-// the consumer adds them in order and applies the per-row factor in its epilogue.
+// carries the sums of squares of its (unnormalised) rows as partials of the producer's workgroups, ss[token][j]
+// (token-major, SS_CAP partials per row, so that one row's partials are one contiguous read): the consumer adds them
+// in order and applies the per-row factor in its epilogue.
+constexpr int SS_CAP = 4096;
 struct ActBuf {
   void* frag = nullptr;   // [nkb][ntile][4][1 KB] (bf16 or fp16 elements)
   int ntile = MAX_TOK / 16;
-  float* ss = nullptr;    // [ss_cap][MAX_TOK]
+  float* ss = nullptr;    // [MAX_TOK][SS_CAP]
   int nss = 0, ss_cap = 0;
   int K = 0, nkb = 0;
   bool f16 = false;       // element type: fp16 (MXFP4 experts) or bf16 (everything else)
@@ -102,7 +104,7 @@ struct ih_qmat {
 namespace ih {
 // Per-kernel-class timing (ih_timing_*): events recorded around each launch when enabled.
 enum TimingClass : int { TC_QMM = 0, TC_ATTN = 1, TC_PREWORK = 2, TC_REDUCE = 3, TC_ROWS = 4, TC_ARGMAX = 5, TC_MOE = 6,
-                         TC_OTHER = 7, TC_COUNT = 8 };
+                         TC_OTHER = 7, TC_QMM_FINISH = 8, TC_COUNT = 9 };
 struct TimingRec {
   int cls;
   double bytes;
@@ -117,11 +119,12 @@ struct ih_ctx {
   std::vector<hipEvent_t> ev_pool;
   size_t ev_used = 0;
   hipStream_t stream = nullptr;
-  // Split-K scratch of the qmm: partial sums and arrival counters (the counters return to zero by themselves).
+  // Scratch of the copy-lookup reduction (ensure_part).
   float* part = nullptr;
   size_t part_bytes = 0;
-  unsigned* counters = nullptr;
-  size_t n_counters = 0;
+  // Split-K partial sums of the qmm ([split][MAX_TOK][Npad] fp32), grown on demand.
+  float* qpart = nullptr;
+  size_t qpart_bytes = 0;
   // Staging for the kernel-level entry points that take a natural-layout activation.
   ih::ActBuf act;
   size_t act_cap_k = 0;
@@ -159,6 +162,7 @@ enum QmmMode : int {
   QM_F32_SCALE = 3,   // y[m][n] = r_m · v, r_m the RMSNorm factor of input row m
   QM_RESID_ACT = 4,   // h[m][n] += v; next activation bf16(h ⊙ nw) + its sum-of-squares partials
   QM_GLU_ACT = 5,     // gated activation of the interleaved gate|up pair (scaled by r_m) → next activation
+  QM_PART = 6,        // split-K partial sums (qmm_finish_kernel adds them and runs the epilogue)
 };
 constexpr int QO_F32 = QM_F32, QO_F32_ADD = QM_F32_ADD, QO_BF16 = QM_BF16;
 struct QmmEpilogue {

@@ -97,7 +97,7 @@ struct GatherParams {
   int N, Npad, nkb, mode;
   void* y;
   int ldy;
-  // RMSNorm factor of the activation rows (router and gate|up): r_t = 1/sqrt(Σ ss_in[j][t] / D + eps).
+  // RMSNorm factor of the activation rows (router and gate|up): r_t = 1/sqrt(Σ ss_in[t][j] / D + eps).
   const float* ss_in;
   int nss_in, D, nrows;
   float eps;
@@ -236,15 +236,7 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
   if (nk & 1) compute(a);
 
   // RMSNorm factors of the activation rows.
-  if (p.ss_in) {
-    for (int t = wave; t < p.nrows; t += GKW) {
-      float ss = 0.f;
-      for (int j = lane; j < p.nss_in; j += 64) ss += p.ss_in[j * MAX_TOK + t];
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-      if (lane == 0) rsc[t] = 1.0f / sqrtf(ss / float(p.D) + p.eps);
-    }
-  }
+  if (p.ss_in) rms_factors(p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.nrows, rsc, wave, GKW, lane);
 
   // Waves' partial sums → LDS [wave][tt][q][lane], then added in wave order.
   __shared__ float red[GKW * 2 * 4 * 64];
@@ -424,7 +416,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
-  if (threadIdx.x == 0) ss_out[r] = (red[0] + red[1]) + (red[2] + red[3]);
+  if (threadIdx.x == 0) ss_out[size_t(r) * SS_CAP] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

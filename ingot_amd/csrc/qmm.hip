@@ -24,6 +24,7 @@
 #include "ih_internal.h"
 #include "qmm_common.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 
@@ -95,12 +96,12 @@ struct QmmParams {
   // The nibble-decode constants 0x000F000F and 0x43004300, passed as arguments so that they live in SGPRs and the
   // compiler can use the three-operand v_and_or_b32 (gfx9 VOP3 takes no literal constants).
   unsigned kmask, kbias;
-  // RMSNorm factor of the input rows (modes QM_F32_SCALE, QM_GLU_ACT): r_t = 1/sqrt(Σ ss_in[j][t] / D + eps).
+  // RMSNorm factor of the input rows (modes QM_F32_SCALE, QM_GLU_ACT): r_t = 1/sqrt(Σ ss_in[t][j] / D + eps).
   const float* ss_in;
   int nss_in, D;
   float eps;
   // QM_RESID_ACT: h[m][n] += v (fp32, the y pointer), then the next activation bf16(h ⊙ nw) and the sum-of-squares
-  // partial of this workgroup's columns, ss_out[blockIdx.x][t].
+  // partial of this workgroup's columns, ss_out[t][blockIdx.x].
   const uint16_t* nw;
   uint4* act_out;
   int act_nkb;
@@ -109,312 +110,46 @@ struct QmmParams {
   int glu;
   float limit;
   int act_f16;  // the next activation in fp16 (the input of MXFP4 experts) instead of bf16
+  // K split over workgroups (gridDim.y > 1): partial sums [split][MAX_TOK][Npad], added in split order by
+  // qmm_finish_kernel, which then runs the epilogue.
+  float* part;
+  int nsplit;
 };
 
-// One K-block's operands of a wave, in two rings of different depth: the weight tiles come from HBM and are
-// prefetched far ahead; the token fragments of x (L2 hits) and the LDS-staged token 16 and scale/bias words need only
-// a short lead.
+// The epilogue of the R tiles tile0 … tile0+R−1 of a workgroup of nthr threads, given val(m, r, rn) = the finished
+// product of token m and row rn of tile r. rsc holds the RMSNorm factors (modes QM_F32_SCALE, QM_GLU_ACT); ssu is
+// LDS scratch of MAX_TOK·2R floats; wg indexes this workgroup's sum-of-squares partial (QM_RESID_ACT).
+// QM_RESID_ACT: a thread's first work item (token m, 8 columns) of the residual epilogue, its h and norm weights
+// loaded at kernel entry so that their latency overlaps the main loop.
+struct ResidPrefetch {
+  float h[8];
+  float nw[8];
+};
 template <int R>
-struct QmmW {
-  u32x4 w[R];
-};
-template <int T, int R, bool X16>
-struct QmmX {
-  u32x4 x[T][4];
-  u32x4 x16[X16 ? 4 : 1];   // token 16's A operand (rows 1–15 zero), from LDS
-  uint2 sb[R];              // scale | bias << 16 of the two groups of the K-block, row n of each tile, from LDS
-};
-
-struct QmmRsrc {
-  __amdgpu_buffer_rsrc_t w, s, x;
-  unsigned xoff[2];   // this lane's offset in a K-block's fragments (OOB for dead tokens), per token tile
-};
-
-// Past the last K-block every offset is forced out of range (offsets stay below 2^31, so OR-ing OOB keeps them out):
-// the loads are issued unconditionally, read zeros without touching memory, and the loop body is one basic block
-// with a fixed number of loads in flight, so the wait before each multiply covers only the stage it reads.
-// The scheduling barriers keep a stage's loads together, ahead of the multiply that follows (LLVM's scheduler
-// otherwise sinks them toward their use and the prefetch distance collapses).
-template <int R>
-__device__ __forceinline__ void qmm_load_w(QmmW<R>& st, const QmmParams& p, const QmmRsrc& rs, int tile0, int kb,
-                                           int lane, int n) {
-  const unsigned oob = kb < p.nkb ? 0u : OOB;
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const unsigned tb = unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kb);
-    st.w[r] = __builtin_bit_cast(
-        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, (tb * 1024u + lane * 16u) | oob, 0, 0));
-  }
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// Token 16 is staged in LDS once per workgroup (x16s: [kb][t][qd] 16 bytes, block nkb all zeros): all 16 row lanes of
-// a lane group read the same 16 bytes, a broadcast read, where a buffer load would spend a full vector-memory
-// instruction per MFMA step on 64 distinct bytes.
-template <int T, int R, bool X16>
-__device__ __forceinline__ void qmm_load_x(QmmX<T, R, X16>& st, const QmmParams& p, const QmmRsrc& rs, int kb,
-                                           const u32x4* x16s, const uint2* sbs, int n, int qd) {
-  const unsigned oob = kb < p.nkb ? 0u : OOB;
-  const unsigned kx = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u;  // [kb][tile][t][1 KB]
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int tt = 0; tt < T; ++tt)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      st.x[tt][t] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, (rs.xoff[tt] + kx + 1024 * t) | oob, 0, 0));
-  if constexpr (X16) {
-    // The A operand of the second token tile: row 0 (lanes n = 0) is token 16, rows 1–15 read the zero block.
-    const int kq = (kb < p.nkb && n == 0) ? kb : p.nkb;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) st.x16[t] = x16s[(kq * 4 + t) * 4 + qd];
-  }
-  // Past the last K-block the scales read the zero block that follows the staged words (the weights are zero there
-  // too, and the bias term must not add c·Σx): an address select, so the loop body stays one basic block.
-  const bool kin = kb < p.nkb;
-#pragma unroll
-  for (int r = 0; r < R; ++r) st.sb[r] = sbs[(kin ? (r * p.nkb + kb) * 16 : R * p.nkb * 16) + n];
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// Workgroup staging in LDS, loaded once for all KW waves: token 16 of every K-block (X16; entries
-// e = (kb·4 + t)·4 + qd, 16 bytes each, the fragment bytes at kb·(MAX_TOK/16)·4096 + 4096 + 1024·t + 16·qd, then a
-// zero block nkb) and the scale/bias words of the workgroup's R tiles (contiguous in the packed layout:
-// [tile][kb][row] 8 bytes, from tile0·nkb·128). Eight loads per thread for each, issued before the weight prologue so
-// that their latency overlaps it, stored after it. Straight-line code with a fixed number of loads: a loop here would
-// make the wait counts of everything after it conservative. The launch checks that both fit in 8·NTHR entries.
-template <int NTHR, bool X16>
-struct QmmStage {
-  u32x4 v16[X16 ? 8 : 1];
-  u32x4 vsb[8];
-};
-
-template <int NTHR, bool X16>
-__device__ __forceinline__ void qmm_stage_issue(QmmStage<NTHR, X16>& st, const QmmParams& p, const QmmRsrc& rs,
-                                                int tile0, int R) {
-  if constexpr (X16) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = j * NTHR + int(threadIdx.x);
-      const int kb = e >> 4, t = (e >> 2) & 3, qd = e & 3;
-      const unsigned off = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * qd;
-      st.v16[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.x, kb < p.nkb ? off : OOB, 0, 0));
-    }
-  }
-  const unsigned nsb = unsigned(R) * unsigned(p.nkb) * 8u, base = unsigned(tile0) * unsigned(p.nkb) * 128u;
+__device__ __forceinline__ void resid_prefetch(ResidPrefetch& pf, const QmmParams& p, int tile0) {
+  constexpr int nch = 2 * R;
+  const int u = threadIdx.x;
+  if (u >= p.M * nch) return;
+  const int m = u / nch, cl = u % nch, col0 = (tile0 + (cl >> 1)) * 16 + 8 * (cl & 1);
+  const float* hrow = static_cast<const float*>(p.y) + size_t(m) * p.ldy;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const unsigned e = unsigned(j * NTHR) + threadIdx.x;
-    st.vsb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.s, e < nsb ? base + e * 16u : OOB, 0, 0));
+    const int col = min(col0 + j, p.N - 1);
+    pf.h[j] = hrow[col];
+    pf.nw[j] = bf16f(p.nw[col]);
   }
 }
 
-template <int NTHR, bool X16>
-__device__ __forceinline__ void qmm_stage_commit(const QmmStage<NTHR, X16>& st, u32x4* x16s, u32x4* sbs,
-                                                 const QmmParams& p, int R) {
-  if constexpr (X16) {
-    const int ne = (p.nkb + 1) * 16;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = j * NTHR + int(threadIdx.x);
-      if (e < ne) x16s[e] = st.v16[j];
-    }
-  }
-  const int nsb = R * p.nkb * 8;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = j * NTHR + int(threadIdx.x);
-    if (e < nsb) sbs[e] = st.vsb[j];
-  }
-  if (threadIdx.x < 8) sbs[nsb + threadIdx.x] = u32x4{0u, 0u, 0u, 0u};  // the zero block (16 rows × 8 bytes)
-}
-
-template <int T, int R, bool X16>
-__device__ __forceinline__ void qmm_compute(f32x4 (&acc)[R][T], float (&acc16)[R], const QmmW<R>& sw,
-                                            const QmmX<T, R, X16>& st, unsigned km, unsigned kbias) {
-  // Σx per group and token (ones operand), in the D layout of the products: lane (n, qd) gets tokens 4qd … 4qd+3.
-  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
-  f32x4 xs[T][2];
-#pragma unroll
-  for (int tt = 0; tt < T; ++tt)
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g]), ones,
-                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-      xs[tt][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), ones, z, 0,
-                                                          0, 0);
-    }
-  // Token 16 (X16): a second token tile whose only live row is token 16; Σx per group lands in element 0 of the
-  // qd = 0 lanes, like every other output of that token.
-  float xs16[2] = {0.f, 0.f};
-  if constexpr (X16) {
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g]), ones,
-                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-      z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g + 1]), ones, z, 0, 0, 0);
-      xs16[g] = z[0];
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float s0 = bf16f(st.sb[r].x & 0xFFFFu), s1 = bf16f(st.sb[r].y & 0xFFFFu);
-    const float c0 = fmaf(-128.f, s0, bf16f(st.sb[r].x >> 16)), c1 = fmaf(-128.f, s1, bf16f(st.sb[r].y >> 16));
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const bf16x8 w0 = nib_bf16(sw.w[r][2 * g], km, kbias), w1 = nib_bf16(sw.w[r][2 * g + 1], km, kbias);
-      const float sg = g ? s1 : s0, cg = g ? c1 : c0;
-#pragma unroll
-      for (int tt = 0; tt < T; ++tt) {
-        f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g]), w0,
-                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), w1, tmp, 0,
-                                                      0, 0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[r][tt][e] = fmaf(sg, tmp[e], fmaf(cg, xs[tt][g][e], acc[r][tt][e]));
-      }
-      if constexpr (X16) {
-        f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g]), w0,
-                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x16[2 * g + 1]), w1, tmp, 0, 0,
-                                                      0);
-        acc16[r] = fmaf(sg, tmp[0], fmaf(cg, xs16[g], acc16[r]));
-      }
-    }
-  }
-}
-
-
-// T: MFMA token tiles loaded from memory (tokens 0–15, and 16–31 when T = 2); X16 (with T = 1, M = 17): token 16
-// as a second tile from LDS.
-// Workgroup = KW waves over the same 16·R rows; wave w takes K-blocks w, w + KW, … (adjacent waves read adjacent
-// 1 KB blocks), with the next block's loads in flight while the current one is multiplied. The KW partial sums are
-// added in wave order through LDS: no cross-workgroup synchronisation (an agent-scope fence on MI355X writes the
-// XCD's L2 back and costs tens of µs) and a summation order that depends only on (N, K).
-template <int T, int R, int KW, bool X16, int DW, int DX>
-__global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
-  static_assert(DW % DX == 0, "the x ring depth divides the weight ring depth");
-  // The wave index is uniform: readfirstlane keeps it (and the K-block loop) in scalar registers and scalar branches.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int n = lane & 15, qd = lane >> 4;
-  const int tile0 = blockIdx.x * R;
-  __shared__ float rsc[MAX_TOK];
-  f32x4 acc[R][T];
-  float acc16[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    acc16[r] = 0.f;
-#pragma unroll
-    for (int tt = 0; tt < T; ++tt) acc[r][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  QmmRsrc rs;
-  const unsigned tiles_total = unsigned(p.Npad / 16) * unsigned(p.nkb);
-  rs.w = make_rsrc(p.w, tiles_total * 1024u);
-  rs.s = make_rsrc(p.s, tiles_total * 128u);
-  rs.x = make_rsrc(p.xa, unsigned(MAX_TOK) * p.nkb * 256u);
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int tok = 16 * tt + n;
-    const bool live = tt < T && tok < p.M;
-    rs.xoff[tt] = live ? (unsigned(tt) * 4096u + n * 64u + qd * 16u) : OOB;
-  }
-  const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
-
-  // DW K-blocks of weights and DX of x in flight. This wave's K-blocks are wave, wave + KW, … (nk of them), DW per
-  // trip of a loop with a single exit (a loop with two exits is structurized into a join that the wait-count pass
-  // treats as a back edge with other stages' loads still pending, which serialises every trip). Stages past the end
-  // are loaded out of range: zero weights and scales, so their products add exact zeros (the count depends only on
-  // the shape).
-  // Prologue in the order of the steady state (x(j) issued DX stages ahead of its use, w(j) DW stages ahead, x before
-  // w within a stage), so the wait counts at the loop head are those of every later trip.
-  extern __shared__ u32x4 stage_lds[];
-  u32x4* const x16s = stage_lds;
-  u32x4* const sbs = stage_lds + (X16 ? (p.nkb + 1) * 16 : 0);
-  QmmStage<64 * KW, X16> stg;
-  qmm_stage_issue(stg, p, rs, tile0, R);
-  QmmW<R> sw[DW];
-  QmmX<T, R, X16> sx[DX];
-  int kb = wave;
-#pragma unroll
-  for (int t = -DW; t < -DX; ++t) qmm_load_w(sw[t + DW], p, rs, tile0, kb + (t + DW) * KW, lane, n);
-  qmm_stage_commit(stg, x16s, sbs, p, R);
-  __syncthreads();
-  const uint2* const sbv = reinterpret_cast<const uint2*>(sbs);
-#pragma unroll
-  for (int t = -DX; t < 0; ++t) {
-    qmm_load_x(sx[t + DX], p, rs, kb + (t + DX) * KW, x16s, sbv, n, qd);
-    qmm_load_w(sw[t + DW], p, rs, tile0, kb + (t + DW) * KW, lane, n);
-  }
-  const int nk = kb < p.nkb ? (p.nkb - kb + KW - 1) / KW : 0;
-  const int trips = (nk + DW - 1) / DW;
-  for (int it = 0; it < trips; ++it) {
-#pragma unroll
-    for (int s = 0; s < DW; ++s) {
-      qmm_compute(acc, acc16, sw[s], sx[s % DX], km, kbias);
-      qmm_load_x(sx[s % DX], p, rs, kb + (s + DX) * KW, x16s, sbv, n, qd);
-      qmm_load_w(sw[s], p, rs, tile0, kb + (s + DW) * KW, lane, n);
-    }
-    kb += DW * KW;
-  }
-
-  // RMSNorm factors of the input rows (the norm's sums of squares come in as partials of the producer's workgroups,
-  // added here in a fixed order). After the K loop: loads with a data-dependent count ahead of it would make the
-  // compiler's wait counts at the loop head conservative.
-  // Wave w takes tokens w, w + KW, …; lane l adds partials l, l + 64, … and the lanes are combined by a fixed
-  // butterfly, so a token's factor does not depend on M or on the launch shape.
-  if (p.ss_in) {
-    for (int t = wave; t < p.M; t += KW) {
-      float ss = 0.f;
-      for (int j = lane; j < p.nss_in; j += 64) ss += p.ss_in[j * MAX_TOK + t];
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-      if (lane == 0) rsc[t] = 1.0f / sqrtf(ss / float(p.D) + p.eps);
-    }
-  }
-
-  // Partial sums of every wave → LDS [wave][r][tt][e][lane] (+ token 16 [wave][r][row]), then fixed-order sums.
-  constexpr int NEL = R * T * 4 * 64;
-  constexpr int NEL16 = X16 ? R * 16 : 0;
-  constexpr int WST = NEL + NEL16;
-  __shared__ float red[KW * WST];
-  __shared__ float ssu[MAX_TOK * 8];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int tt = 0; tt < T; ++tt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) red[wave * WST + ((r * T + tt) * 4 + e) * 64 + lane] = acc[r][tt][e];
-  if constexpr (X16) {
-    if (lane < 16) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) red[wave * WST + NEL + r * 16 + lane] = acc16[r];
-    }
-  }
-  __syncthreads();
-  // Sum over waves of output (token m, tile r, row rn of the tile).
-  auto val = [&](int m, int r, int rn) -> float {
-    int i;
-    if (X16 && m == 16) {
-      i = NEL + r * 16 + rn;
-    } else {
-      const int tt = m >> 4, mm = m & 15;
-      i = ((r * T + tt) * 4 + (mm & 3)) * 64 + 16 * (mm >> 2) + rn;
-    }
-    float v = red[i];
-#pragma unroll
-    for (int w = 1; w < KW; ++w) v += red[w * WST + i];
-    return v;
-  };
-
-  const int nthr = 64 * KW;
-  if (p.mode == QM_RESID_ACT) {
-    // h += v for this workgroup's 16R columns, the next activation bf16(h ⊙ nw) in 8-column chunks, and Σh² per token.
-    const int nch = 2 * R;
+template <int R, int MODE, typename V>
+__device__ __forceinline__ void qmm_epilogue(const QmmParams& p, int tile0, V val, const float* rsc, float* ssu,
+                                             int nthr, int wg, const ResidPrefetch* rpf = nullptr) {
+  if constexpr (MODE == QM_RESID_ACT) {
+    // h += v for the 16R columns, the next activation bf16(h ⊙ nw) in 8-column chunks, and Σh² per token.
+    constexpr int nch = 2 * R;
     for (int u = threadIdx.x; u < p.M * nch; u += nthr) {
       const int m = u / nch, cl = u % nch, r = cl >> 1, half = cl & 1;
       const int col0 = (tile0 + r) * 16 + 8 * half;
+      const bool pre = rpf && u == int(threadIdx.x);
       float v[8], ss = 0.f;
       float* hrow = static_cast<float*>(p.y) + size_t(m) * p.ldy;
 #pragma unroll
@@ -422,24 +157,24 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
         const int col = col0 + j;
         float hv = 0.f;
         if (col < p.N) {
-          hv = hrow[col] + val(m, r, 8 * half + j);
+          hv = (pre ? rpf->h[j] : hrow[col]) + val(m, r, 8 * half + j);
           hrow[col] = hv;
         }
         ss += hv * hv;
-        v[j] = col < p.N ? hv * bf16f(p.nw[col]) : 0.f;
+        v[j] = col < p.N ? hv * (pre ? rpf->nw[j] : bf16f(p.nw[col])) : 0.f;
       }
-      ssu[m * 8 + cl] = ss;
+      ssu[m * nch + cl] = ss;
       if (col0 < p.N) frag_store(p.act_f16 != 0, p.act_out, p.act_nkb, MAX_TOK / 16, m, col0 / 8, v);
     }
     __syncthreads();
-    if (threadIdx.x < p.M) {
+    if (int(threadIdx.x) < p.M) {
       float ss = 0.f;
-      for (int cl = 0; cl < nch; ++cl) ss += ssu[threadIdx.x * 8 + cl];
-      p.ss_out[blockIdx.x * MAX_TOK + threadIdx.x] = ss;
+      for (int cl = 0; cl < nch; ++cl) ss += ssu[threadIdx.x * nch + cl];
+      p.ss_out[threadIdx.x * SS_CAP + wg] = ss;
     }
     return;
   }
-  if (p.mode == QM_GLU_ACT) {
+  if constexpr (MODE == QM_GLU_ACT) {
     // Interleaved gate|up tiles: rows 0–7 gate, 8–15 up of the same 8 columns (chunk tile0 + r of the output).
     for (int u = threadIdx.x; u < p.M * R; u += nthr) {
       const int m = u / R, r = u % R;
@@ -457,10 +192,10 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     const int row = (tile0 + r) * 16 + rn;
     if (row >= p.N) continue;
     float v = val(m, r, rn);
-    if (p.mode == QM_F32_SCALE) v *= rsc[m];
-    if (p.mode == QM_BF16) {
+    if constexpr (MODE == QM_F32_SCALE) v *= rsc[m];
+    if constexpr (MODE == QM_BF16) {
       static_cast<unsigned short*>(p.y)[size_t(m) * p.ldy + row] = f2bf(v);
-    } else if (p.mode == QM_F32_ADD) {
+    } else if constexpr (MODE == QM_F32_ADD) {
       float* o = static_cast<float*>(p.y) + size_t(m) * p.ldy + row;
       *o = *o + v;
     } else {
@@ -469,37 +204,367 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   }
 }
 
-// Launch shape for an (Npad, nkb) matrix: rows per workgroup (16·R) and waves per workgroup (KW, the intra-workgroup
-// split of K). Chosen from the shape only, never from M, so each row's summation order is fixed.
-struct QmmShape { int R, KW, DW, DX; };
+// T: MFMA token tiles loaded from memory (tokens 0–15, and 16–31 when T = 2); X16 (with T = 1, M = 17): token 16 as
+// a second tile whose A operand comes from LDS.
+//
+// Workgroup (blockIdx.x, blockIdx.y) = KW waves over the 16·R rows of tiles R·blockIdx.x …; the K range is split over
+// gridDim.y workgroups and, inside one, over its waves: wave w streams the KPW consecutive K-blocks from
+// (blockIdx.y·KW + w)·KPW through a D-deep register ring (the loads of K-block i + D go out as K-block i is
+// multiplied). R tiles per wave share each x fragment, so x traffic per weight byte falls as 1/R (one tile per wave
+// re-reads x ~4× the weight bytes from L2).
+// VALU budget. At M = 17 the products are cheap on MFMA; the VALU work per 16 × 128 tile (nibble decode 28, the
+// per-group affine map 20, scale words 6) is ~55 % of the tile's HBM time at full speed, so nothing else may run on
+// the VALU in the loop: every K-dependent offset is a scalar (buffer loads take the K-block as soffset, the LDS reads
+// as an immediate of an unrolled trip), and the ring's last D K-blocks are peeled rather than guarded.
+// The KW partial sums are added in wave order through LDS; with gridDim.y > 1 each workgroup writes its sum to
+// p.part and qmm_finish_kernel adds the splits in order. No atomics and no cross-workgroup fences (an agent-scope
+// release on MI355X writes back the XCD's L2: ~15 µs per launch), and a row's summation order depends only on
+// (N, K), never on M.
+template <int T, int R, int KW, bool X16, int D, int KPW, int MODE>
+__global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
+  static_assert(KPW % D == 0, "the ring depth divides the K-blocks of a wave");
+  // The wave index is uniform: readfirstlane keeps it (and everything derived from it) in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int n = lane & 15, qd = lane >> 4;
+  const int tile0 = blockIdx.x * R;
+  constexpr int nk = KPW;                                // K-blocks of every wave
+  constexpr int nkw = KW * nk;                           // K-blocks of the workgroup
+  const int kwg = int(blockIdx.y) * nkw;                 // first K-block of the workgroup
+  const int kb0 = kwg + wave * nk;                       // first K-block of this wave
+  const unsigned tiles_total = unsigned(p.Npad / 16) * unsigned(p.nkb);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, tiles_total * 1024u), rsb = make_rsrc(p.s, tiles_total * 128u),
+                               rx = make_rsrc(p.xa, unsigned(MAX_TOK) * p.nkb * 256u);
+  const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
+
+  // Workgroup staging in LDS, written once behind one barrier: the scale/bias words of the R tiles over the
+  // workgroup's K-blocks ([r][kl][row] 8 bytes) and token 16 of those K-blocks as [kl][t][row ∈ {token 16, zeros}][qd]
+  // 16 bytes, so that lane (n, qd) reads row n ≠ 0 ? zeros : token 16 from an address that depends on the K-block
+  // only through an immediate. They are issued before the weights and waited for first: their latency overlaps the
+  // weight stream.
+  // Epilogue inputs that another kernel just wrote, requested first (consumed after the main loop).
+  // Rows per wave of the RMSNorm prefetch: M ≤ 16 (T = 1), 17 (X16) or 32 (T = 2).
+  // Rows per wave of the RMSNorm prefetch: M ≤ 16 (T = 1), 17 (X16) or 32 (T = 2); more than eight (one-wave
+  // workgroups) are read after the loop instead.
+  constexpr int NR = ((T == 2 ? 32 : X16 ? 17 : 16) + KW - 1) / KW;
+  constexpr bool RMS = MODE == QM_F32_SCALE || MODE == QM_GLU_ACT, RMS_PRE = RMS && NR <= 8;
+  RmsPrefetch<RMS_PRE ? NR : 1> rpf;
+  ResidPrefetch hpf;
+  if constexpr (RMS_PRE)
+    if (p.ss_in) rms_prefetch(rpf, p.ss_in, SS_CAP, p.M, wave, KW, lane);
+  if constexpr (MODE == QM_RESID_ACT) resid_prefetch<R>(hpf, p, tile0);
+
+  __shared__ u32x4 ssb[R * nkw * 8];
+  __shared__ u32x4 s16[X16 ? nkw * 32 : 1];
+  __shared__ float rsc[MAX_TOK];
+  constexpr int nsb = R * nkw * 8;
+  constexpr int NSB = (nsb + 64 * KW - 1) / (64 * KW), N16 = X16 ? (nkw * 16 + 64 * KW - 1) / (64 * KW) : 1;
+  u32x4 vsb[NSB], v16[N16];
+#pragma unroll
+  for (int j = 0; j < NSB; ++j) {
+    const int e = j * 64 * KW + int(threadIdx.x), r = e / (nkw * 8), kl = (e >> 3) % nkw;
+    const unsigned off = (unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kwg + kl)) * 128u + unsigned(e & 7) * 16u;
+    vsb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, e < nsb ? off : OOB, 0, 0));
+  }
+  if constexpr (X16) {
+#pragma unroll
+    for (int j = 0; j < N16; ++j) {
+      const int e = j * 64 * KW + int(threadIdx.x), kl = e >> 4, t = (e >> 2) & 3, q = e & 3, kb = kwg + kl;
+      const unsigned off = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * q;
+      v16[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, kl < nkw ? off : OOB, 0, 0));
+    }
+  }
+
+  unsigned xoff[T];
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt)
+    xoff[tt] = (16 * tt + n < p.M) ? (unsigned(tt) * 4096u + n * 64u + qd * 16u) : OOB;
+  const unsigned woff = unsigned(lane) * 16u;
+
+  u32x4 wv[D][R], xv[D][T][4];
+  // One ring stage: the weight tiles and x of K-block kb. Every offset that depends on kb is a scalar.
+  auto load_stage = [&](int d, int kb) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        xv[d][tt][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rx, xoff[tt], kb * (MAX_TOK / 16) * 4096 + 1024 * t, 0));
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      wv[d][r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rw, woff, ((tile0 + r) * p.nkb + kb) * 1024, 0));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) load_stage(d, kb0 + d);
+
+#pragma unroll
+  for (int j = 0; j < NSB; ++j) {
+    const int e = j * 64 * KW + int(threadIdx.x);
+    if (e < nsb) ssb[e] = vsb[j];
+  }
+  if constexpr (X16) {
+#pragma unroll
+    for (int j = 0; j < N16; ++j) {
+      const int e = j * 64 * KW + int(threadIdx.x), kl = e >> 4, t = (e >> 2) & 3, q = e & 3;
+      if (kl < nkw) {
+        s16[(kl * 4 + t) * 8 + q] = v16[j];
+        s16[(kl * 4 + t) * 8 + 4 + q] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[R][T];
+  float acc16[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc16[r] = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) acc[r][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
+  const u32x4* const s16l = s16 + (n ? 4 : 0) + qd;  // this lane's row of the token-16 staging
+  const uint2* const sbl = reinterpret_cast<const uint2*>(ssb) + n;  // row n of the staged scale/bias words
+
+  // Products of ring stage d (K-block kl of the workgroup, kl = wave·nk + i).
+  auto compute = [&](int d, int kl) {
+    u32x4 x16[X16 ? 4 : 1];
+    if constexpr (X16) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) x16[t] = s16l[(kl * 4 + t) * 8];
+    }
+    // Σx per group and token (ones operand), in the D layout of the products: lane (n, qd) gets tokens 4qd … 4qd+3.
+    f32x4 xs[T][2];
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[d][tt][2 * g]), ones, zero4,
+                                                          0, 0, 0);
+        xs[tt][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[d][tt][2 * g + 1]), ones,
+                                                            z, 0, 0, 0);
+      }
+    // Token 16: a second token tile whose only live row is token 16; its Σx per group lands in element 0 of the
+    // qd = 0 lanes, like every other output of that token.
+    float xs16[2] = {0.f, 0.f};
+    if constexpr (X16) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x16[2 * g]), ones, zero4, 0, 0,
+                                                          0);
+        z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x16[2 * g + 1]), ones, z, 0, 0, 0);
+        xs16[g] = z[0];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint2 sb = sbl[(r * nkw + kl) * 16];
+      const float s0 = __uint_as_float(sb.x << 16), s1 = __uint_as_float(sb.y << 16);
+      const float c0 = fmaf(-128.f, s0, __uint_as_float(sb.x & 0xFFFF0000u));
+      const float c1 = fmaf(-128.f, s1, __uint_as_float(sb.y & 0xFFFF0000u));
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const bf16x8 w0 = nib_bf16(wv[d][r][2 * g], km, kbias), w1 = nib_bf16(wv[d][r][2 * g + 1], km, kbias);
+        const float sg = g ? s1 : s0, cg = g ? c1 : c0;
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) {
+          f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[d][tt][2 * g]), w0,
+                                                              zero4, 0, 0, 0);
+          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[d][tt][2 * g + 1]), w1, tmp, 0,
+                                                        0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[r][tt][e] = fmaf(sg, tmp[e], fmaf(cg, xs[tt][g][e], acc[r][tt][e]));
+        }
+        if constexpr (X16) {
+          f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x16[2 * g]), w0, zero4, 0,
+                                                              0, 0);
+          tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x16[2 * g + 1]), w1, tmp, 0, 0,
+                                                        0);
+          acc16[r] = fmaf(sg, tmp[0], fmaf(cg, xs16[g], acc16[r]));
+        }
+      }
+      // One tile at a time: without the fence the scheduler decodes every tile's nibbles ahead of the products and
+      // the decoded operands (16 VGPRs per tile) exhaust the register file at R = 7.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // The ring: trips of D K-blocks, each multiplied from its stage and the stage refilled D K-blocks ahead, then the
+  // last D K-blocks without refills (nk is a multiple of D, which the launch checks; nk = D loads everything at
+  // entry).
+  const int kl0 = wave * nk;
+  int i = 0;
+#pragma unroll 1
+  for (; i < nk - D; i += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      compute(d, kl0 + i + d);
+      load_stage(d, kb0 + i + d + D);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) compute(d, kl0 + i + d);
+
+  // Partial sums of every wave → LDS [wave][r][tt][e][lane] (+ token 16 [wave][r][row]), then fixed-order sums.
+  constexpr int NEL = R * T * 4 * 64;
+  constexpr int NEL16 = X16 ? R * 16 : 0;
+  constexpr int WST = NEL + NEL16;
+  __shared__ float red[KW * WST];
+  __shared__ float ssu[MAX_TOK * 2 * R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[wave * WST + ((r * T + tt) * 4 + e) * 64 + lane] = acc[r][tt][e];
+  if constexpr (X16) {
+    if (lane < 16) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) red[wave * WST + NEL + r * 16 + lane] = acc16[r];
+    }
+  }
+  // The RMSNorm factors of the input rows, once the accumulators are in LDS (their loads and shuffles would otherwise
+  // keep every accumulator live across them).
+  if constexpr (RMS_PRE) {
+    if (p.ss_in) rms_finish(rpf, p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, KW, lane);
+  } else if constexpr (RMS) {
+    if (p.ss_in) rms_factors(p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, KW, lane);
+  }
+  __syncthreads();
+  // Sum over waves of output (token m, tile r, row rn of the tile).
+  auto val = [&](int m, int r, int rn) -> float {
+    int i;
+    if (X16 && m == 16) {
+      i = NEL + r * 16 + rn;
+    } else {
+      const int tt = m >> 4, mm = m & 15;
+      i = ((r * T + tt) * 4 + (mm & 3)) * 64 + 16 * (mm >> 2) + rn;
+    }
+    float v = red[i];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) v += red[w * WST + i];
+    return v;
+  };
+  if constexpr (MODE == QM_PART) {
+    float* part = p.part + size_t(blockIdx.y) * MAX_TOK * p.Npad;
+    for (int u = threadIdx.x; u < p.M * 16 * R; u += 64 * KW) {
+      const int m = u / (16 * R), rr = u % (16 * R);
+      part[size_t(m) * p.Npad + tile0 * 16 + rr] = val(m, rr >> 4, rr & 15);
+    }
+  } else {
+    qmm_epilogue<R, MODE>(p, tile0, val, rsc, ssu, 64 * KW, blockIdx.x, &hpf);
+  }
+}
+
+// Adds the split partial sums in split order and runs the epilogue: workgroup = 4 tiles (64 rows), 256 threads.
+constexpr int FIN_R = 4;
+__global__ __launch_bounds__(256) void qmm_finish_kernel(QmmParams p) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tile0 = blockIdx.x * FIN_R;
+  __shared__ float rsc[MAX_TOK];
+  __shared__ float ssu[MAX_TOK * 2 * FIN_R];
+  if (p.ss_in) rms_factors(p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, 4, lane);
+  __syncthreads();
+  const size_t sstride = size_t(MAX_TOK) * p.Npad;
+  auto val = [&](int m, int r, int rn) -> float {
+    const float* q = p.part + size_t(m) * p.Npad + (tile0 + r) * 16 + rn;
+    float v = q[0];
+    for (int s = 1; s < p.nsplit; ++s) v += q[s * sstride];
+    return v;
+  };
+  switch (p.mode) {
+    case QM_F32: qmm_epilogue<FIN_R, QM_F32>(p, tile0, val, rsc, ssu, 256, blockIdx.x); break;
+    case QM_F32_ADD: qmm_epilogue<FIN_R, QM_F32_ADD>(p, tile0, val, rsc, ssu, 256, blockIdx.x); break;
+    case QM_BF16: qmm_epilogue<FIN_R, QM_BF16>(p, tile0, val, rsc, ssu, 256, blockIdx.x); break;
+    case QM_F32_SCALE: qmm_epilogue<FIN_R, QM_F32_SCALE>(p, tile0, val, rsc, ssu, 256, blockIdx.x); break;
+    case QM_RESID_ACT: qmm_epilogue<FIN_R, QM_RESID_ACT>(p, tile0, val, rsc, ssu, 256, blockIdx.x); break;
+    case QM_GLU_ACT: qmm_epilogue<FIN_R, QM_GLU_ACT>(p, tile0, val, rsc, ssu, 256, blockIdx.x); break;
+    default: break;
+  }
+}
+
+// Launch shape for an (Npad, nkb) matrix: R row tiles per wave, KW waves per workgroup, ring depth D, kpw K-blocks per
+// wave, and ks = nkb / (KW·kpw) workgroups splitting K. Chosen from the shape only, never from M, so each row's
+// summation order is fixed. The K range must tile exactly (ks·KW·kpw = nkb, kpw a multiple of D): every load of the
+// ring stays inside the matrix.
+struct QmmShape { int R, KW, D, kpw, ks; };
+static bool qmm_shape_ok(const QmmShape& sh, int Npad, int nkb) {
+  return sh.R >= 1 && sh.KW >= 1 && sh.D >= 1 && sh.kpw >= sh.D && sh.kpw % sh.D == 0 && sh.kpw <= 32 &&
+         sh.R * sh.kpw <= 64 && (Npad / 16) % sh.R == 0 && sh.ks * sh.KW * sh.kpw == nkb;
+}
+// The instantiated (R, KW, KPW) shapes (qmm_dispatch_mode lists the same set).
+static constexpr int kQmmShapes[][3] = {{1, 16, 2}, {2, 16, 2}, {2, 8, 4}, {4, 8, 4}, {4, 4, 8}, {7, 4, 8},
+                                        {1, 14, 8}, {1, 8, 14}, {4, 4, 2}, {2, 8, 2}, {4, 8, 2}, {1, 1, 1},
+                                        {2, 1, 1},  {4, 1, 1},  {7, 1, 1}};
 static QmmShape qmm_shape(int Npad, int nkb) {
-  // Measured at M = 16/17 on gfx950, cold weights (8B shapes): four row tiles per wave when there are enough tiles
-  // to fill the chip (fewer activation bytes per weight byte), two for mid-sized N, one for N ≤ 4096.
   const int NT = Npad / 16;
-  QmmShape sh = NT >= 1536 ? QmmShape{4, 4, 2, 1} : NT >= 384 ? QmmShape{2, 4, 4, 2} : QmmShape{1, 4, 4, 2};
-  // The workgroup's scale/bias words (R·nkb·128 bytes) are staged in LDS by eight 16-byte loads per thread.
-  while (sh.R > 1 && sh.R * nkb > 64 * sh.KW) sh.R /= 2;
-  if (sh.R * nkb > 64 * sh.KW) sh = QmmShape{1, 16, 4, 2};
-  return sh;
+  // Rows: R tiles per wave share x, and the workgroup count NT / R should be about one round over the 256 CUs (a
+  // partial second round doubles the time of the CUs that run it): 7 for gate|up (1792 tiles → 256 workgroups), 4
+  // for the vocabulary head (~9 rounds), 2 for qkv (192), 1 for o and down (256).
+  int rp[4] = {1, 2, 0, 0};
+  if (NT % 7 == 0 && NT / 7 >= 192 && NT / 7 <= 320) { rp[0] = 7; rp[1] = 4; rp[2] = 2; rp[3] = 1; }
+  else if (NT >= 2048) { rp[0] = 4; rp[1] = 2; rp[2] = 1; }
+  else if (NT > 256) { rp[0] = 2; rp[1] = 1; }
+  // K: the whole range in one workgroup when a shape tiles it (16 waves × 2 K-blocks at K = 4096; a ring of 8 or 14
+  // K-blocks per wave for longer K), else split over workgroups.
+  for (int pass = 0; pass < 2; ++pass)
+    for (int R : rp) {
+      if (R == 0) continue;
+      for (const auto& c : kQmmShapes) {
+        if (c[0] != R || c[1] == 1) continue;
+        const int span = c[1] * c[2];
+        if (nkb % span) continue;
+        const QmmShape sh{R, c[1], c[2] % 2 ? 1 : 2, c[2], nkb / span};
+        if ((pass == 0 && sh.ks != 1) || !qmm_shape_ok(sh, Npad, nkb)) continue;
+        return sh;
+      }
+    }
+  // K-block counts without a fitting factor: one wave per workgroup, one K-block per wave.
+  for (int R : rp)
+    if (R && (Npad / 16) % R == 0) return QmmShape{R, 1, 1, 1, nkb};
+  return QmmShape{1, 1, 1, 1, nkb};
+}
+
+template <int T, int R, int KW, bool X16, int KPW>
+constexpr bool qmm_fits() {
+  return 4 * KW * (R * T * 256 + (X16 ? R * 16 : 0)) + 4 * MAX_TOK * (2 * R + 1) + R * KW * KPW * 128 +
+             (X16 ? KW * KPW * 512 : 0) <= 128 * 1024;
+}
+
+// Instantiated launch shapes (R, KW, KPW; D = 2 when KPW is even) for each epilogue. Epilogues are compile-time:
+// the code of every mode in one kernel raised its register demand past the ring's (302 VGPRs at R = 7, KW = 4).
+// The kernel-level modes (QM_F32, QM_F32_ADD, QM_BF16) run as QM_PART + qmm_finish_kernel.
+template <int T, bool X16, int MODE>
+static bool qmm_dispatch_mode(const TimedLaunch& tl, QmmShape sh, dim3 grid, hipStream_t st, const QmmParams& p) {
+#define IH_QMM_CASE(R_, KW_, KPW_)                                                                          \
+  if constexpr (qmm_fits<T, R_, KW_, X16, KPW_>()) {                                                        \
+    if (sh.R == R_ && sh.KW == KW_ && sh.kpw == KPW_) {                                                     \
+      tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, (KPW_ % 2 ? 1 : 2), KPW_, MODE>, grid, dim3(64 * KW_), 0, \
+              st, p);                                                                                       \
+      return true;                                                                                          \
+    }                                                                                                       \
+  }
+  // K = 4096 (32 K-blocks); K = 14336 (112); K = 2048 (16); and the one-wave fallback.
+  IH_QMM_CASE(1, 16, 2) IH_QMM_CASE(2, 16, 2) IH_QMM_CASE(2, 8, 4) IH_QMM_CASE(4, 8, 4) IH_QMM_CASE(4, 4, 8)
+  IH_QMM_CASE(7, 4, 8) IH_QMM_CASE(1, 14, 8) IH_QMM_CASE(1, 8, 14) IH_QMM_CASE(4, 4, 2) IH_QMM_CASE(2, 8, 2)
+  IH_QMM_CASE(4, 8, 2) IH_QMM_CASE(1, 1, 1) IH_QMM_CASE(2, 1, 1) IH_QMM_CASE(4, 1, 1) IH_QMM_CASE(7, 1, 1)
+#undef IH_QMM_CASE
+  return false;  // not an instantiated shape
 }
 
 template <int T, bool X16>
-static bool qmm_dispatch(const TimedLaunch& tl, QmmShape sh, int grid, hipStream_t st, const QmmParams& p) {
-  // LDS staging: token 16 (X16) and the scale/bias words of the workgroup's R tiles.
-  const size_t shm16 = (X16 ? size_t(p.nkb + 1) * 256 : 0) + 128, shsb = size_t(p.nkb) * 128;
-#define IH_QMM_CASE(R_, KW_, DW_, DX_)                                                                \
-  if (sh.R == R_ && sh.KW == KW_ && sh.DW == DW_ && sh.DX == DX_) {                                  \
-    tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, DW_, DX_>, dim3(grid), dim3(64 * KW_), shm16 + R_ * shsb, st, p); \
-    return true;                                                                                          \
+static bool qmm_dispatch(const TimedLaunch& tl, QmmShape sh, dim3 grid, hipStream_t st, const QmmParams& p,
+                         int mode) {
+  switch (mode) {
+    case QM_F32_SCALE: return qmm_dispatch_mode<T, X16, QM_F32_SCALE>(tl, sh, grid, st, p);
+    case QM_RESID_ACT: return qmm_dispatch_mode<T, X16, QM_RESID_ACT>(tl, sh, grid, st, p);
+    case QM_GLU_ACT: return qmm_dispatch_mode<T, X16, QM_GLU_ACT>(tl, sh, grid, st, p);
+    case QM_PART: return qmm_dispatch_mode<T, X16, QM_PART>(tl, sh, grid, st, p);
+    default: return false;
   }
-  IH_QMM_CASE(1, 4, 1, 1) IH_QMM_CASE(1, 4, 2, 1) IH_QMM_CASE(1, 4, 2, 2) IH_QMM_CASE(1, 4, 4, 2)
-  IH_QMM_CASE(1, 8, 1, 1) IH_QMM_CASE(1, 8, 2, 1) IH_QMM_CASE(1, 8, 4, 2) IH_QMM_CASE(1, 16, 4, 2)
-  IH_QMM_CASE(2, 4, 1, 1) IH_QMM_CASE(2, 4, 2, 1) IH_QMM_CASE(2, 4, 2, 2) IH_QMM_CASE(2, 4, 4, 2)
-  IH_QMM_CASE(2, 8, 1, 1) IH_QMM_CASE(2, 8, 2, 1)
-  IH_QMM_CASE(4, 4, 1, 1) IH_QMM_CASE(4, 4, 2, 1) IH_QMM_CASE(4, 4, 2, 2) IH_QMM_CASE(4, 2, 1, 1)
-  IH_QMM_CASE(8, 4, 1, 1) IH_QMM_CASE(8, 2, 1, 1)
-#undef IH_QMM_CASE
-  return false;  // not an instantiated shape
 }
 
 int launch_act_from_bf16(ih_ctx* c, const uint16_t* x, int ldx, int M, ActBuf& a) {
@@ -519,12 +584,35 @@ int qmm_grid(const ih_qmat* W) {
   return W->Npad / (16 * sh.R);
 }
 
+// Split-K partial sums: grown on demand, the stream drained before an old buffer is freed.
+static int ensure_qpart(ih_ctx* c, size_t bytes) {
+  if (c->qpart_bytes >= bytes) return IH_OK;
+  IH_HIP(hipStreamSynchronize(c->stream));
+  if (c->qpart) IH_HIP(hipFree(c->qpart));
+  c->qpart = nullptr;
+  c->qpart_bytes = 0;
+  if (hipMalloc(&c->qpart, bytes) != hipSuccess) return fail(IH_ENOMEM, "qmm: split-K partial allocation failed");
+  c->qpart_bytes = bytes;
+  return IH_OK;
+}
+
 int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int M, const QmmEpilogue& ep) {
   IH_CHECK(W->format == QF_INT4, IH_EINVAL, "qmm: int4 matrix expected");
   IH_CHECK(M >= 1 && M <= MAX_TOK, IH_EINVAL, "qmm: M must be in 1..32");
   IH_CHECK(a.nkb == W->nkb && !a.f16, IH_EINVAL, "qmm: activation K does not match the matrix");
   QmmShape sh = qmm_shape(W->Npad, W->nkb);
-  if (const char* ov = getenv("IH_QMM_SHAPE")) sscanf(ov, "%d,%d,%d,%d", &sh.R, &sh.KW, &sh.DW, &sh.DX);  // tuning override
+  if (const char* ov = getenv("IH_QMM_SHAPE")) {  // tuning override for every matrix: R,KW,kpw
+    if (sscanf(ov, "%d,%d,%d", &sh.R, &sh.KW, &sh.kpw) == 3) {
+      sh.D = sh.kpw % 2 ? 1 : 2;
+      sh.ks = W->nkb / std::max(1, sh.KW * sh.kpw);
+    }
+  }
+  IH_CHECK(qmm_shape_ok(sh, W->Npad, W->nkb), IH_EINVAL, "qmm: launch shape does not tile the matrix");
+  const int ks = sh.ks;
+  // The kernel runs the epilogue itself when it sees the whole K range and the mode is one of the step's fused
+  // epilogues; otherwise it writes partial sums and qmm_finish_kernel adds them and applies the mode.
+  const bool finish = ks > 1 || !(ep.mode == QM_F32_SCALE || ep.mode == QM_RESID_ACT || ep.mode == QM_GLU_ACT);
+  const int kmode = finish ? int(QM_PART) : ep.mode;
   QmmParams p{};
   const size_t tiles_per_e = size_t(W->Npad / 16) * W->nkb;
   p.w = static_cast<const uint4*>(W->w) + tiles_per_e * 64 * expert;
@@ -539,6 +627,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   p.mode = ep.mode;
   p.kmask = 0x000F000Fu;
   p.kbias = 0x43004300u;
+  p.nsplit = ks;
   if (ep.mode == QM_F32_SCALE || ep.mode == QM_GLU_ACT) {
     IH_CHECK(a.ss && a.nss > 0, IH_EINVAL, "qmm: the input activation carries no RMSNorm sums");
     p.ss_in = a.ss;
@@ -546,18 +635,18 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
     p.D = a.K;
     p.eps = ep.eps;
   }
-  IH_CHECK(sh.R * W->nkb <= 64 * sh.KW, IH_EINVAL, "qmm: the scale/bias staging does not fit this launch shape");
-  const int grid = W->Npad / (16 * sh.R);
+  // Workgroups that write the epilogue: the qmm's own (one split) or the finisher's (4 tiles each).
+  const int grid_x = W->Npad / (16 * sh.R);
+  const int egrid = finish ? W->Npad / (16 * FIN_R) : grid_x;
   if (ep.mode == QM_RESID_ACT) {
     IH_CHECK(ep.act_out && ep.act_out->nkb * KBLK >= W->N && ep.nw, IH_EINVAL, "qmm: residual epilogue needs an output");
-    IH_CHECK(grid <= ep.act_out->ss_cap, IH_EINVAL, "qmm: too many workgroups for the RMSNorm partials");
-    IH_CHECK(2 * sh.R <= 8, IH_EINVAL, "qmm: residual epilogue supports R ≤ 4");
+    IH_CHECK(egrid <= ep.act_out->ss_cap, IH_EINVAL, "qmm: too many workgroups for the RMSNorm partials");
     p.nw = ep.nw;
     p.act_out = static_cast<uint4*>(ep.act_out->frag);
     p.act_nkb = ep.act_out->nkb;
     p.act_f16 = ep.act_out->f16 ? 1 : 0;
     p.ss_out = ep.act_out->ss;
-    ep.act_out->nss = grid;
+    ep.act_out->nss = egrid;
   }
   if (ep.mode == QM_GLU_ACT) {
     IH_CHECK(ep.act_out && ep.act_out->nkb * KBLK >= W->N / 2 && W->il8, IH_EINVAL,
@@ -568,17 +657,28 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
     p.glu = ep.glu;
     p.limit = ep.limit;
   }
+  if (finish) {
+    IH_TRY(ensure_qpart(c, size_t(ks) * MAX_TOK * W->Npad * sizeof(float)));
+    p.part = c->qpart;
+  }
   // Algorithmic bytes: the matrix in its MLX format, x (bf16) read, y written (read too when accumulating).
   const double ybytes = double(M) * W->N *
                         (ep.mode == QM_BF16 ? 2 : (ep.mode == QM_F32_ADD || ep.mode == QM_RESID_ACT ? 8 : 4));
-  TimedLaunch tl(c, TC_QMM, double(W->algo_bytes) + double(M) * W->K * 2 + ybytes);
-  bool ok;
-  if (M > 17) ok = qmm_dispatch<2, false>(tl, sh, grid, c->stream, p);
-  else if (M == 17 && (W->nkb + 1) * 16 <= 8 * 64 * sh.KW) ok = qmm_dispatch<1, true>(tl, sh, grid, c->stream, p);
-  else if (M == 17) ok = qmm_dispatch<2, false>(tl, sh, grid, c->stream, p);  // K too long to stage token 16 in LDS
-  else ok = qmm_dispatch<1, false>(tl, sh, grid, c->stream, p);
-  IH_CHECK(ok, IH_EINVAL, "qmm: launch shape not instantiated");
-  IH_HIP(hipGetLastError());
+  {
+    TimedLaunch tl(c, TC_QMM, double(W->algo_bytes) + double(M) * W->K * 2 + (finish ? 0.0 : ybytes));
+    const dim3 grid(grid_x, ks);
+    bool ok;
+    if (M > 17) ok = qmm_dispatch<2, false>(tl, sh, grid, c->stream, p, kmode);
+    else if (M == 17) ok = qmm_dispatch<1, true>(tl, sh, grid, c->stream, p, kmode);
+    else ok = qmm_dispatch<1, false>(tl, sh, grid, c->stream, p, kmode);
+    IH_CHECK(ok, IH_EINVAL, "qmm: launch shape not instantiated");
+    IH_HIP(hipGetLastError());
+  }
+  if (finish) {
+    TimedLaunch tl(c, TC_QMM_FINISH, double(ks) * M * W->N * 4 + ybytes);
+    tlaunch(tl, qmm_finish_kernel, dim3(egrid), dim3(256), 0, c->stream, p);
+    IH_HIP(hipGetLastError());
+  }
   return IH_OK;
 }
 

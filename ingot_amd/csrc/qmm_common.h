@@ -55,4 +55,60 @@ __device__ __forceinline__ float glu_f(float g, float u, int act, float limit) {
   return gc / (1.0f + expf(-1.702f * gc)) * (uc + 1.0f);
 }
 
+// RMSNorm factors of M ≤ 32 activation rows from the producers' sum-of-squares partials, token-major with leading
+// dimension ld (ss_in[t·ld + j], j < nss ≤ ld, ld a multiple of 256): rsc[t] = 1/sqrt(Σ_j ss_in[t][j] / D + eps).
+// Wave w of nwaves takes rows w, w + nwaves, …; lane l adds partials 4l … 4l+3, then 256 + 4l …, in order, and the
+// lanes are combined by a fixed butterfly, so a row's factor depends neither on M nor on the caller's launch shape.
+// One 16-byte load per lane covers 256 partials of a row. Split in two so that a kernel can issue the first chunk of
+// its rows (NR per wave) at entry and finish after its main loop: the partials were just written by another kernel,
+// and their latency then hides under the weight stream.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+template <int NR>  // rows per wave
+struct RmsPrefetch {
+  f32x4v v[NR];
+};
+template <int NR>
+__device__ __forceinline__ void rms_prefetch(RmsPrefetch<NR>& pf, const float* __restrict__ ss_in, int ld, int M,
+                                             int wave, int nwaves, int lane) {
+  const int nt = (M - wave + nwaves - 1) / nwaves;  // rows of this wave (wave-uniform, at most NR)
+#pragma unroll
+  for (int k = 0; k < NR; ++k)
+    if (k < nt) pf.v[k] = *reinterpret_cast<const f32x4v*>(ss_in + size_t(wave + k * nwaves) * ld + 4 * lane);
+}
+template <int NR>
+__device__ __forceinline__ void rms_finish(const RmsPrefetch<NR>& pf, const float* __restrict__ ss_in, int ld, int nss,
+                                           int D, float eps, int M, float* rsc, int wave, int nwaves, int lane) {
+  const int nt = (M - wave + nwaves - 1) / nwaves;
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    if (k >= nt) break;
+    float ss = 0.f;
+    for (int j0 = 0; j0 < nss; j0 += 256) {
+      const int j = j0 + 4 * lane;
+      const f32x4v v =
+          j0 == 0 ? pf.v[k] : *reinterpret_cast<const f32x4v*>(ss_in + size_t(wave + k * nwaves) * ld + j);
+      ss += j < nss ? v[0] : 0.f;
+      ss += j + 1 < nss ? v[1] : 0.f;
+      ss += j + 2 < nss ? v[2] : 0.f;
+      ss += j + 3 < nss ? v[3] : 0.f;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) rsc[wave + k * nwaves] = 1.0f / sqrtf(ss / float(D) + eps);
+  }
+}
+// Both halves at once, rows in groups of eight (callers without a main loop to hide the latency under).
+__device__ __forceinline__ void rms_factors(const float* __restrict__ ss_in, int ld, int nss, int D, float eps, int M,
+                                            float* rsc, int wave, int nwaves, int lane) {
+  const int nt = (M - wave + nwaves - 1) / nwaves;
+  for (int k0 = 0; k0 < nt; k0 += 8) {
+    // Rows wave + (k0 + k)·nwaves, k < 8: the same function on the rows from k0·nwaves on.
+    const float* base = ss_in + size_t(k0) * nwaves * ld;
+    const int Mk = M - k0 * nwaves;
+    RmsPrefetch<8> pf;
+    rms_prefetch(pf, base, ld, Mk, wave, nwaves, lane);
+    rms_finish(pf, base, ld, nss, D, eps, Mk, rsc + k0 * nwaves, wave, nwaves, lane);
+  }
+}
+
 }  // namespace ih

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
-  if (threadIdx.x == 0) ss_out[row] = ((red[0] + red[1]) + (red[2] + red[3]));
+  if (threadIdx.x == 0) ss_out[size_t(row) * SS_CAP] = ((red[0] + red[1]) + (red[2] + red[3]));
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -83,7 +83,7 @@ int ensure_act(ih_ctx* c, ActBuf& a, int K, bool f16) {
     return IH_OK;
   }
   free_act(a);
-  const int ss_cap = 4096;
+  const int ss_cap = SS_CAP;
   size_t fb = size_t(MAX_TOK) * nkb * 256, sb = size_t(ss_cap) * MAX_TOK * 4;
   if (hipMalloc(&a.frag, fb) != hipSuccess || hipMalloc(&a.ss, sb) != hipSuccess) {
     free_act(a);
@@ -126,14 +126,6 @@ int ih_init(int device, ih_ctx** out) {
     delete c;
     return fail(IH_EDEVICE, "ih_init: stream creation failed");
   }
-  c->n_counters = 1 << 16;
-  if (hipMalloc(&c->counters, c->n_counters * sizeof(unsigned)) != hipSuccess) {
-    (void)hipStreamDestroy(c->stream);
-    delete c;
-    return fail(IH_ENOMEM, "ih_init: counter allocation failed");
-  }
-  int s = fill(c, c->counters, 0, c->n_counters * sizeof(unsigned));
-  if (s != IH_OK) return s;
   *out = c;
   return IH_OK;
 }
@@ -144,7 +136,7 @@ int ih_ctx_free(ih_ctx* c) {
   (void)hipStreamSynchronize(c->stream);
   for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
   if (c->part) (void)hipFree(c->part);
-  if (c->counters) (void)hipFree(c->counters);
+  if (c->qpart) (void)hipFree(c->qpart);
   free_act(c->act);
   (void)hipStreamDestroy(c->stream);
   delete c;
