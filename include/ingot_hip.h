@@ -160,7 +160,7 @@ size_t ih_model_weight_bytes(const ih_model* model);
  * key chunk is fixed per cache (256 … 2048 keys, from the capacity) so a row's result is the same for every block
  * size. AttentionLayer's kc/vt/ks/vs (Sources/Ingot/Layers/Attention.swift:272-390). */
 int ih_kv_create(ih_model* model, int capacity, ih_kv** out);
-/* The same with an explicit key chunk C (a multiple of 16, ≥ 32; 0 = automatic). Attention splits the keys into the
+/* The same with an explicit key chunk C (a positive multiple of 32; 0 = automatic). Attention splits the keys into the
  * fixed ranges [s·C, (s+1)·C) and merges them in order (pattn_i8 chunks, Attention.swift:389-390); the automatic C
  * gives one workgroup per CU over all KV heads at full capacity. */
 int ih_kv_create_chunked(ih_model* model, int capacity, int chunk, ih_kv** out);

@@ -10,14 +10,15 @@
 // rotated the same way, so (Hq)·(Hk) = q·k.
 //
 // MI355X design: one workgroup (8 waves) per (key split, KV head); the split size C is fixed per cache so that all
-// splits of all heads are one workgroup per CU. A split is staged through LDS in sub-chunks (288 keys at HD 128): every
-// thread issues its loads of the whole sub-chunk at once (the next sub-chunk is in flight during this one's products),
-// converts int8 → fp16 exactly into LDS (K key-major, V transposed), and each wave runs its 16-query tiles over 64-key
-// blocks: Sᵀ = K·Qᵀ (v_mfma_f32_16x16x32_f16, keys as rows so each lane holds 4 keys of one query), online softmax in
+// splits of all heads are one workgroup per CU. A split streams through LDS in pieces of 64 keys: every thread issues
+// the loads of all its pieces at entry, each piece is converted int8 → fp16 exactly into one of two LDS buffers (K
+// key-major, V transposed) as soon as it lands, and each wave runs its 16-query tiles over the piece: Sᵀ = K·Qᵀ (v_mfma_f32_16x16x32_f16, keys as rows so each lane holds 4 keys of one query), online softmax in
 // base 2 per query column, P stays in registers as the B operand of Oᵀ += Vᵀ·Pᵀ. A split writes O/l in fp16 with its
 // (max, sum); the reduction merges the splits in a fixed order. A query's result does not depend on the other rows of
 // the block: blocks start at fixed key positions and the split boundaries are fixed multiples of C.
 #include <hip/hip_fp16.h>
+
+#include <algorithm>
 
 #include "act.h"
 #include "attn_args.h"
@@ -82,7 +83,8 @@ __global__ void prework_kernel(AttnArgs a) {
   const int8_t qv = int8_t(fminf(127.f, fmaxf(-127.f, rintf(x / sc))));
   const bool isk = slot < a.QH + a.KVH;
   const int h = isk ? slot - a.QH : slot - a.QH - a.KVH;
-  (isk ? a.kc : a.vc)[(size_t(h) * a.cap + kpos) * HD + d] = qv;
+  if (isk) a.kc[(size_t(h) * a.cap + kpos) * HD + d] = qv;
+  else a.vc[v_index(h, kpos, d, HD, a.vld)] = qv;
   if (d == 0) (isk ? a.ks : a.vs)[size_t(h) * a.cap + kpos] = sc16;
 }
 
@@ -98,58 +100,35 @@ __device__ __forceinline__ void i8x4_to_h(unsigned w, __half2& lo, __half2& hi) 
   hi = __hsub2(__builtin_bit_cast(__half2, h), off);
 }
 
-// Four int8 words of four consecutive keys (bytes = dims 4w … 4w+3) → four words of four keys per dim (bytes = keys).
-__device__ __forceinline__ void transpose4x4(unsigned a, unsigned b, unsigned c, unsigned d, unsigned (&o)[4]) {
-  const unsigned t0 = __builtin_amdgcn_perm(b, a, 0x05010400u), t1 = __builtin_amdgcn_perm(b, a, 0x07030602u);
-  const unsigned u0 = __builtin_amdgcn_perm(d, c, 0x05010400u), u1 = __builtin_amdgcn_perm(d, c, 0x07030602u);
-  o[0] = __builtin_amdgcn_perm(u0, t0, 0x05040100u);
-  o[1] = __builtin_amdgcn_perm(u0, t0, 0x07060302u);
-  o[2] = __builtin_amdgcn_perm(u1, t1, 0x05040100u);
-  o[3] = __builtin_amdgcn_perm(u1, t1, 0x07060302u);
-}
-
-constexpr int ATT_THREADS = 512;       // 8 waves: all load, the first ceil(tiles / TPW) compute
-// Keys staged in LDS at a time (a multiple of 32): fp16 K (HD + 8 halves a row) and Vᵀ (SUB + 8 halves a row) fill
-// ≤ 156 KB of the 160 KB LDS.
-template <int HD> constexpr int sub_keys() { return HD == 128 ? 288 : 512; }
+constexpr int ATT_THREADS = 512;  // 8 waves: all load and convert, the first ceil(tiles / TPW) multiply
+constexpr int PIECE = 64;         // keys per pipelined piece of a split
+constexpr int MAX_PIECES = 8;     // pieces whose loads are in flight together (a batch)
 template <int HD> constexpr int krow() { return HD + 8; }
+constexpr int VROW = PIECE + 8;   // LDS row of Vᵀ in halves
 
-// Slot of key k (0…31) in a 32-key block of Vᵀ: the PV MFMA pairs lane group qd's element e with key 4·qd + e (e < 4,
-// first 16-key tile) or 16 + 4·qd + e − 4 (second tile): the keys each lane holds after the Sᵀ MFMAs. Four consecutive
-// keys from a multiple of 4 occupy four consecutive slots.
-__device__ __forceinline__ int vslot(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
-
-// One sub-chunk of K and V in flight in registers: per thread up to KI K items (one key, 16 dims), up to VI V items
-// (four keys, 16 dims) and up to SI keys' two scales.
-template <int HD>
-struct SubStage {
-  static constexpr int SUB = sub_keys<HD>();
-  static constexpr int KITEMS = SUB * (HD / 16), VITEMS = (SUB / 4) * (HD / 16);
-  static constexpr int KI = (KITEMS + ATT_THREADS - 1) / ATT_THREADS;
-  static constexpr int VI = (VITEMS + ATT_THREADS - 1) / ATT_THREADS;
-  static constexpr int SI = (SUB + ATT_THREADS - 1) / ATT_THREADS;
-  uint4 k[KI];
-  uint4 v[VI][4];
-  __half ks[SI], vs[SI];
+// One piece of 64 keys in flight in registers, per thread: one K item (a key's 16 dims), one V item (16 key positions
+// of one dim of the transposed cache) and, for threads < 64, one key's two scales.
+struct PieceRegs {
+  uint4 k, v;
+  __half ks, vs;
 };
 
 // One workgroup per (split of C keys, KV head): every query row of the head's group (G·B ≤ 16·8·TPW) in one pass.
-// The split is staged through LDS in sub-chunks of SUB keys: all of a sub-chunk's loads are issued together (the
-// next sub-chunk is in flight while this one is multiplied), converted int8 → fp16 once into LDS (K key-major, V
-// transposed), then each wave runs its query tiles over 64-key blocks with an online softmax in base 2.
-template <int HD, int TPW, bool RING>
+// The split streams through LDS in pieces of 64 keys: the loads of up to eight pieces are issued together (in piece
+// order, so the wait for piece p covers only pieces ≤ p), each piece is converted int8 → fp16 into one of two LDS buffers (K
+// key-major, V transposed) as soon as its loads land, and the waves multiply it while the later pieces are still on
+// their way; one barrier per piece (the buffer written for piece p + 2 was last read for piece p, before the barrier
+// of piece p + 1). Each wave runs its 16-query tiles over the piece with an online softmax in base 2.
+template <int HD, int TPW, bool RING, int NP>
 __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
-  using Stage = SubStage<HD>;
-  constexpr int SUB = Stage::SUB;
-  constexpr int VROW = SUB + 8;  // LDS row of Vᵀ in halves
   constexpr int NC = HD / 32;    // 32-dim chunks (MFMA K steps of Sᵀ)
   constexpr int NDT = HD / 16;   // 16-dim tiles of Oᵀ
   constexpr int KR = krow<HD>();
   constexpr int KPK = HD / 16;   // K items per key
-  __shared__ _Float16 Kf[SUB * KR];
-  __shared__ _Float16 Vt[HD * VROW];
-  // Scales of the staged keys; 64 zero entries past SUB so a 64-key block never indexes out of range.
-  __shared__ __attribute__((aligned(16))) float ksf[SUB + 64], vsf[SUB + 64];
+  constexpr int KITEMS = PIECE * KPK, VITEMS = HD * (PIECE / 16);
+  __shared__ _Float16 Kf[2][PIECE * KR];
+  __shared__ _Float16 Vt[2][HD * VROW];
+  __shared__ __attribute__((aligned(16))) float ksf[2][PIECE], vsf[2][PIECE];
 
   const int sidx = blockIdx.x, split = sidx + a.s0, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
@@ -157,11 +136,39 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   const int k0 = split * a.C, k1 = min(k0 + a.C, a.P + a.B);
 
   const int8_t* kh = a.kc + size_t(kvh) * a.cap * HD;
-  const int8_t* vh = a.vc + size_t(kvh) * a.cap * HD;
+  const int8_t* vh = a.vc + size_t(kvh) * HD * a.vld;
   const __half* ksh = a.ks + size_t(kvh) * a.cap;
   const __half* vsh = a.vs + size_t(kvh) * a.cap;
   const int ring = a.ring;
   auto slot_of = [ring](int key) { return RING ? key % ring : key; };
+
+  // The loads of a batch of NP pieces (keys kbase + 64p …) go out together, in piece order; keys past k1 read key
+  // k1 − 1 (their scales are zero and their scores masked).
+  PieceRegs pr[NP];
+  auto load_batch = [&](int kbase) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int kb = kbase + PIECE * p;
+      if (tid < KITEMS) {
+        const int key = min(kb + tid / KPK, k1 - 1), col = (tid % KPK) * 16;
+        pr[p].k = *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + col);
+      }
+      if (tid < VITEMS) {
+        // 16 positions of one dim; a 32-slot block wholly past k1 is not read (its keys are masked, scale zero).
+        const int dim = tid / (PIECE / 16), pc = tid % (PIECE / 16), pos = kb + 16 * pc;
+        pr[p].v = (pos & ~31) < k1 ? *reinterpret_cast<const uint4*>(vh + size_t(dim) * a.vld + slot_of(pos & ~31) +
+                                                                     (pos & 31))
+                                   : make_uint4(0, 0, 0, 0);
+      }
+      if (tid < PIECE) {
+        const int key = kb + tid;
+        const bool ok = key < k1;
+        pr[p].ks = ok ? ksh[slot_of(key)] : __float2half(0.f);
+        pr[p].vs = ok ? vsh[slot_of(key)] : __float2half(0.f);
+      }
+    }
+  };
+  if (k0 < k1) load_batch(k0);
 
   // Query tiles of this wave: wave + 8·tt.
   f16x8 qf[TPW][NC];
@@ -195,186 +202,147 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     tile_hi_lo[tt] = a.window > 0 ? tile_hi[tt] - a.window + 1 : -2147483647;
   }
 
-  Stage st;
-  auto load = [&](int kb) {
-#pragma unroll
-    for (int i = 0; i < Stage::KI; ++i) {
-      const int item = tid + ATT_THREADS * i, key = kb + item / KPK, col = (item % KPK) * 16;
-      st.k[i] = (item < Stage::KITEMS && key < k1)
-                    ? *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + col)
-                    : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < Stage::VI; ++i) {
-      const int item = tid + ATT_THREADS * i, q4 = item / KPK, col = (item % KPK) * 16;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = kb + 4 * q4 + e;
-        st.v[i][e] = (item < Stage::VITEMS && key < k1)
-                         ? *reinterpret_cast<const uint4*>(vh + size_t(slot_of(key)) * HD + col)
-                         : make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < Stage::SI; ++i) {
-      const int kk = tid + ATT_THREADS * i, key = kb + kk;
-      // Keys past the split read scale 0: their V contributes 0 and their scores are masked.
-      const bool ok = kk < SUB && key < k1;
-      st.ks[i] = ok ? ksh[slot_of(key)] : __float2half(0.f);
-      st.vs[i] = ok ? vsh[slot_of(key)] : __float2half(0.f);
-    }
-  };
-  auto store = [&]() {
-#pragma unroll
-    for (int i = 0; i < Stage::KI; ++i) {
-      const int item = tid + ATT_THREADS * i, key = item / KPK, col = (item % KPK) * 16;
-      if (item >= Stage::KITEMS) continue;
-      const unsigned kw[4] = {st.k[i].x, st.k[i].y, st.k[i].z, st.k[i].w};
+  // Piece p → LDS buffer b.
+  auto store = [&](const PieceRegs& r, int b) {
+    if (tid < KITEMS) {
+      const int key = tid / KPK, col = (tid % KPK) * 16;
+      const unsigned kw[4] = {r.k.x, r.k.y, r.k.z, r.k.w};
       u32x4 h0, h1;
       __half2 lo, hi;
       i8x4_to_h(kw[0], lo, hi); h0.x = __builtin_bit_cast(unsigned, lo); h0.y = __builtin_bit_cast(unsigned, hi);
       i8x4_to_h(kw[1], lo, hi); h0.z = __builtin_bit_cast(unsigned, lo); h0.w = __builtin_bit_cast(unsigned, hi);
       i8x4_to_h(kw[2], lo, hi); h1.x = __builtin_bit_cast(unsigned, lo); h1.y = __builtin_bit_cast(unsigned, hi);
       i8x4_to_h(kw[3], lo, hi); h1.z = __builtin_bit_cast(unsigned, lo); h1.w = __builtin_bit_cast(unsigned, hi);
-      *reinterpret_cast<u32x4*>(&Kf[key * KR + col]) = h0;
-      *reinterpret_cast<u32x4*>(&Kf[key * KR + col + 8]) = h1;
+      *reinterpret_cast<u32x4*>(&Kf[b][key * KR + col]) = h0;
+      *reinterpret_cast<u32x4*>(&Kf[b][key * KR + col + 8]) = h1;
     }
-#pragma unroll
-    for (int i = 0; i < Stage::VI; ++i) {
-      const int item = tid + ATT_THREADS * i, q4 = item / KPK, col = (item % KPK) * 16;
-      if (item >= Stage::VITEMS) continue;
-      const int slot = 32 * (q4 >> 3) + vslot(4 * (q4 & 7));
-      const unsigned* v0 = reinterpret_cast<const unsigned*>(&st.v[i][0]);
-      const unsigned* v1 = reinterpret_cast<const unsigned*>(&st.v[i][1]);
-      const unsigned* v2 = reinterpret_cast<const unsigned*>(&st.v[i][2]);
-      const unsigned* v3 = reinterpret_cast<const unsigned*>(&st.v[i][3]);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        unsigned t[4];
-        transpose4x4(v0[w], v1[w], v2[w], v3[w], t);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          __half2 lo, hi;
-          i8x4_to_h(t[e], lo, hi);
-          uint2 pr;
-          pr.x = __builtin_bit_cast(unsigned, lo);
-          pr.y = __builtin_bit_cast(unsigned, hi);
-          *reinterpret_cast<uint2*>(&Vt[(col + 4 * w + e) * VROW + slot]) = pr;
-        }
-      }
+    if (tid < VITEMS) {
+      const int dim = tid / (PIECE / 16), pc = tid % (PIECE / 16);
+      const unsigned vw[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+      u32x4 h0, h1;
+      __half2 lo, hi;
+      i8x4_to_h(vw[0], lo, hi); h0.x = __builtin_bit_cast(unsigned, lo); h0.y = __builtin_bit_cast(unsigned, hi);
+      i8x4_to_h(vw[1], lo, hi); h0.z = __builtin_bit_cast(unsigned, lo); h0.w = __builtin_bit_cast(unsigned, hi);
+      i8x4_to_h(vw[2], lo, hi); h1.x = __builtin_bit_cast(unsigned, lo); h1.y = __builtin_bit_cast(unsigned, hi);
+      i8x4_to_h(vw[3], lo, hi); h1.z = __builtin_bit_cast(unsigned, lo); h1.w = __builtin_bit_cast(unsigned, hi);
+      *reinterpret_cast<u32x4*>(&Vt[b][dim * VROW + 16 * pc]) = h0;
+      *reinterpret_cast<u32x4*>(&Vt[b][dim * VROW + 16 * pc + 8]) = h1;
     }
-#pragma unroll
-    for (int i = 0; i < Stage::SI; ++i) {
-      const int kk = tid + ATT_THREADS * i;
-      if (kk < SUB) {
-        ksf[kk] = __half2float(st.ks[i]) * a.scale_log2;
-        vsf[kk] = __half2float(st.vs[i]);
-      }
+    if (tid < PIECE) {
+      ksf[b][tid] = __half2float(r.ks) * a.scale_log2;
+      vsf[b][tid] = __half2float(r.vs);
     }
   };
-  if (tid < 64) {
-    ksf[SUB + tid] = 0.f;
-    vsf[SUB + tid] = 0.f;
-  }
 
-  if (k0 < k1) load(k0);
-  for (int kb = k0; kb < k1; kb += SUB) {
-    if (kb != k0) __syncthreads();  // every wave is done with the previous sub-chunk
-    store();
-    __syncthreads();
-    if (kb + SUB < k1) load(kb + SUB);
-    const int nkeys = min(SUB, k1 - kb);  // keys of this sub-chunk (a multiple of 32 staged, the rest zero)
-    const int nblk = (nkeys + 63) / 64;
+  // The products of piece (buffer b) with keys kb …, nkeys of them staged (the rest are zero and masked).
+  auto piece_products = [&](int b, int kb, int nkeys) {
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt) {
       if (!live[tt]) continue;  // uniform per wave
-      for (int b = 0; b < nblk; ++b) {
-        const int kk0 = 64 * b;
-        // Skip blocks no row of the tile can see (wave-uniform: past the last row's causal limit, or wholly before
-        // the first row's window).
-        if (kb + kk0 > tile_hi[tt] || kb + kk0 + 63 < tile_lo[tt]) continue;
-        const bool half2 = kk0 + 32 < nkeys;  // the block's second 32 keys are staged (uniform)
-        // The four Sᵀ tiles as interleaved independent MFMA chains, K fragments read one 32-dim step at a time (all
-        // of a block's fragments at once need more registers than the wave has next to the sub-chunk in flight).
-        f32x4 sacc[4];
+      // Skip a piece no row of the tile can see (wave-uniform: past the last row's causal limit, or wholly before the
+      // first row's window).
+      if (kb > tile_hi[tt] || kb + 63 < tile_lo[tt]) continue;
+      const bool half2 = 32 < nkeys;  // the piece's second 32 keys are staged (uniform)
+      // The four Sᵀ tiles as interleaved independent MFMA chains, K fragments read one 32-dim step at a time.
+      f32x4 sacc[4];
 #pragma unroll
-        for (int h = 0; h < 4; ++h) sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int h = 0; h < 4; ++h) sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          f16x8 kf[4];
+      for (int c = 0; c < NC; ++c) {
+        f16x8 kf[4];
 #pragma unroll
-          for (int h = 0; h < 4; ++h)
-            kf[h] = *reinterpret_cast<const f16x8*>(&Kf[(kk0 + 16 * h + j) * KR + 32 * c + 8 * qd]);
+        for (int h = 0; h < 4; ++h)
+          kf[h] = *reinterpret_cast<const f16x8*>(&Kf[b][(16 * h + j) * KR + 32 * c + 8 * qd]);
 #pragma unroll
-          for (int h = 0; h < 4; ++h) sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h], qf[tt][c], sacc[h], 0, 0, 0);
-        }
-        // Vᵀ fragments are read at the products (the second half only when it is staged).
-        auto vread = [&](int hs, int dt) {
-          return *reinterpret_cast<const f16x8*>(&Vt[(16 * dt + j) * VROW + (hs && half2 ? kk0 + 32 : kk0) + 8 * qd]);
-        };
-        // This lane's keys kk0 + 16h + 4qd + r: their scales as one 16-byte LDS read per tile, unconditionally (a
-        // conditional read becomes a branch with its own wait).
-        f32x4 ksv[4], vsv[4];
+        for (int h = 0; h < 4; ++h) sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h], qf[tt][c], sacc[h], 0, 0, 0);
+      }
+      // Vᵀ fragments are read at the products (the second half only when it is staged).
+      auto vread = [&](int hs, int dt) {
+        return *reinterpret_cast<const f16x8*>(&Vt[b][(16 * dt + j) * VROW + (hs && half2 ? 32 : 0) + 8 * qd]);
+      };
+      // This lane's keys 16h + 4qd + r: their scales as one 16-byte LDS read per tile.
+      f32x4 ksv[4], vsv[4];
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          ksv[h] = *reinterpret_cast<const f32x4*>(&ksf[kk0 + 16 * h + 4 * qd]);
-          vsv[h] = *reinterpret_cast<const f32x4*>(&vsf[kk0 + 16 * h + 4 * qd]);
-        }
-        float s[4][4];
-        float mx = -INFINITY;
-        // Every key of the block visible to every row of the tile (the common case): no per-key mask.
-        const bool full = kk0 + 64 <= nkeys && kb + kk0 + 63 <= tile_lo_lim[tt] && kb + kk0 >= tile_hi_lo[tt];
-        if (full) {
-#pragma unroll
-          for (int h = 0; h < 4; ++h)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              s[h][r] = sacc[h][r] * ksv[h][r];
-              mx = fmaxf(mx, s[h][r]);
-            }
-        } else {
-#pragma unroll
-          for (int h = 0; h < 4; ++h)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int kk = kk0 + 16 * h + 4 * qd + r, key = kb + kk;
-              const bool vis = kk < nkeys && key <= lim[tt] && key >= lo_key[tt];
-              s[h][r] = vis ? sacc[h][r] * ksv[h][r] : -INFINITY;
-              mx = fmaxf(mx, s[h][r]);
-            }
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = fmaxf(mrun[tt], mx);
-        const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[tt] - mnew);
-        mrun[tt] = mnew;
-        float ps = 0.f;
-        f16x8 pb[2];
+      for (int h = 0; h < 4; ++h) {
+        ksv[h] = *reinterpret_cast<const f32x4*>(&ksf[b][16 * h + 4 * qd]);
+        vsv[h] = *reinterpret_cast<const f32x4*>(&vsf[b][16 * h + 4 * qd]);
+      }
+      float s[4][4];
+      float mx = -INFINITY;
+      // Every key of the piece visible to every row of the tile (the common case): no per-key mask.
+      const bool full = nkeys == PIECE && kb + 63 <= tile_lo_lim[tt] && kb >= tile_hi_lo[tt];
+      if (full) {
 #pragma unroll
         for (int h = 0; h < 4; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            // v_exp_f32 directly: exp2(−inf) = 0, and no range reduction is needed for arguments ≤ 0.
-            const float p = __builtin_amdgcn_exp2f(s[h][r] - mnew);
-            ps += p;
-            pb[h >> 1][4 * (h & 1) + r] = (_Float16)(p * vsv[h][r]);
+            s[h][r] = sacc[h][r] * ksv[h][r];
+            mx = fmaxf(mx, s[h][r]);
           }
-        lsum[tt] = lsum[tt] * alpha + ps;
-        if (__any(alpha != 1.f)) {
+      } else {
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) o[tt][dt] *= alpha;
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int kk = 16 * h + 4 * qd + r, key = kb + kk;
+            const bool vis = kk < nkeys && key <= lim[tt] && key >= lo_key[tt];
+            s[h][r] = vis ? sacc[h][r] * ksv[h][r] : -INFINITY;
+            mx = fmaxf(mx, s[h][r]);
+          }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(mrun[tt], mx);
+      const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[tt] - mnew);
+      mrun[tt] = mnew;
+      // A row that has seen no key yet (every score −inf, e.g. a split wholly past its causal limit) takes exponents
+      // against 0, not −inf: exp2(−inf − (−inf)) would be NaN.
+      const float mref = mnew == -INFINITY ? 0.f : mnew;
+      float ps = 0.f;
+      f16x8 pb[2];
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          // v_exp_f32 directly: exp2(−inf) = 0, and no range reduction is needed for arguments ≤ 0.
+          const float pv = __builtin_amdgcn_exp2f(s[h][r] - mref);
+          ps += pv;
+          pb[h >> 1][4 * (h & 1) + r] = (_Float16)(pv * vsv[h][r]);
         }
+      lsum[tt] = lsum[tt] * alpha + ps;
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[tt][dt] *= alpha;
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+        o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(0, dt), pb[0], o[tt][dt], 0, 0, 0);
+      if (half2) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
-          o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(0, dt), pb[0], o[tt][dt], 0, 0, 0);
-        if (half2) {
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt)
-            o[tt][dt] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(1, dt), pb[1], o[tt][dt], 0, 0, 0);
-        }
+          o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(1, dt), pb[1], o[tt][dt], 0, 0, 0);
       }
     }
+  };
+
+  // Batches of NP pieces (one batch unless the split exceeds 64·NP keys). Pieces alternate between the two LDS
+  // buffers; the barrier before a batch's loads keeps every wave's last reads of the batch before them.
+  int npc = 0;  // pieces processed so far (buffer parity)
+  for (int kbase = k0; kbase < k1; kbase += NP * PIECE) {
+    if (kbase != k0) {
+      __syncthreads();
+      load_batch(kbase);
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int kb = kbase + PIECE * p;
+      if (kb >= k1) break;  // uniform: the split's last piece was p − 1
+      const int b = (npc + p) & 1;
+      store(pr[p], b);
+      __syncthreads();
+      piece_products(b, kb, min(PIECE, k1 - kb));
+    }
+    npc += NP;
   }
 
   // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
@@ -486,25 +454,39 @@ int launch_prework(ih_ctx* c, const AttnArgs& a) {
   return IH_OK;
 }
 
+template <int HD, int TPW, bool RING>
+static bool launch_attn_np(const TimedLaunch& tl, dim3 grid, hipStream_t st, const AttnArgs& a, int np) {
+  switch (np) {
+#define IH_ATT_NP(N) \
+  case N: tlaunch(tl, attn_kernel<HD, TPW, RING, N>, grid, dim3(ATT_THREADS), 0, st, a); return true;
+    IH_ATT_NP(1) IH_ATT_NP(2) IH_ATT_NP(3) IH_ATT_NP(4) IH_ATT_NP(5) IH_ATT_NP(6) IH_ATT_NP(7) IH_ATT_NP(8)
+#undef IH_ATT_NP
+    default: return false;
+  }
+}
+
 int launch_attention(ih_ctx* c, const AttnArgs& a) {
   const int Q = a.G * a.B;
   const int qtiles = (Q + 15) / 16;
   IH_CHECK(qtiles <= 16, IH_EINVAL, "attention: at most 256 query rows per KV head");
+  const int np = std::min(MAX_PIECES, (a.C + PIECE - 1) / PIECE);  // pieces per batch
   dim3 grid(a.nsplit, a.KVH);
   // Algorithmic bytes: the int8 K and V and their fp16 scales of every key the launched splits cover, and q.
   const double keys = double(a.P + a.B) - double(a.s0) * a.C;
   TimedLaunch tl(c, TC_ATTN, double(a.KVH) * keys * (2 * a.HD + 4) + double(a.KVH) * Q * a.HD * 2);
   const bool two = qtiles > 8, ring = a.ring != 0;
-  auto go = [&](auto kern) { tlaunch(tl, kern, grid, dim3(ATT_THREADS), 0, c->stream, a); };
+  const int npb = two ? std::min(np, 4) : np;  // two tiles per wave hold fewer pieces in registers
+  bool ok;
   if (a.HD == 128) {
-    if (two) ring ? go(attn_kernel<128, 2, true>) : go(attn_kernel<128, 2, false>);
-    else ring ? go(attn_kernel<128, 1, true>) : go(attn_kernel<128, 1, false>);
+    if (two) ok = ring ? launch_attn_np<128, 2, true>(tl, grid, c->stream, a, npb) : launch_attn_np<128, 2, false>(tl, grid, c->stream, a, npb);
+    else ok = ring ? launch_attn_np<128, 1, true>(tl, grid, c->stream, a, np) : launch_attn_np<128, 1, false>(tl, grid, c->stream, a, np);
   } else if (a.HD == 64) {
-    if (two) ring ? go(attn_kernel<64, 2, true>) : go(attn_kernel<64, 2, false>);
-    else ring ? go(attn_kernel<64, 1, true>) : go(attn_kernel<64, 1, false>);
+    if (two) ok = ring ? launch_attn_np<64, 2, true>(tl, grid, c->stream, a, npb) : launch_attn_np<64, 2, false>(tl, grid, c->stream, a, npb);
+    else ok = ring ? launch_attn_np<64, 1, true>(tl, grid, c->stream, a, np) : launch_attn_np<64, 1, false>(tl, grid, c->stream, a, np);
   } else {
     return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
   }
+  IH_CHECK(ok, IH_EINVAL, "attention: unsupported key chunk");
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -5,18 +5,32 @@
 
 namespace ih {
 
+// Position of key k (0…31) in a 32-slot block of transposed V: the PV MFMA pairs lane group qd's element e with key
+// 4·qd + e (e < 4, first 16-key tile) or 16 + 4·qd + e − 4 (second tile), the keys each lane holds after the Sᵀ MFMAs,
+// so one lane's 8 keys of a block are 8 consecutive bytes. Four consecutive keys from a multiple of 4 occupy four
+// consecutive positions.
+__host__ __device__ __forceinline__ int vslot(int k) {
+  return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3);
+}
+// Byte of V[head][slot][d] in the transposed cache with rows of vld (cap rounded up to 32) slots.
+__host__ __device__ __forceinline__ size_t v_index(int h, int slot, int d, int HD, int vld) {
+  return (size_t(h) * HD + d) * vld + (slot & ~31) + vslot(slot & 31);
+}
+__host__ __device__ __forceinline__ int v_row(int cap) { return (cap + 31) & ~31; }
+
 struct AttnArgs {
   const float* proj;   // [B][ldp] = q heads | k heads | v heads (fp32, the qkv qmm output)
   int ldp;
   __half* q;           // [KVH][Qpad][HD] fp16, query m = t·G + (h mod G)
   int8_t* kc;          // [KVH][cap][HD]
-  int8_t* vc;          // [KVH][cap][HD]
+  int8_t* vc;          // [KVH][HD][vld]: V transposed, slots permuted within 32-slot blocks (v_index)
   __half* ks;          // [KVH][cap]
   __half* vs;          // [KVH][cap]
   const float* sinks;  // [QH] natural-log logits or null
   __half* opart;       // [KVH][nsplit][Qpad][HD] fp16 O/l of each split (nsplit = launched splits)
   float2* ml;          // [KVH][nsplit][Qpad] (running max in log2 units, sum)
   int cap, ring, P, B, QH, KVH, HD, G, Qpad;  // cap: slots per head (the ring size of a sliding-window layer)
+  int vld;                                    // row of the transposed V: cap rounded up to 32
   int C, nsplit, s0, window, hadk;
   float theta, scale_log2;
 };

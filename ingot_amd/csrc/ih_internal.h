@@ -119,7 +119,7 @@ struct ih_ctx {
   std::vector<hipEvent_t> ev_pool;
   size_t ev_used = 0;
   hipStream_t stream = nullptr;
-  // Scratch of the copy-lookup reduction (ensure_part).
+  // Scratch of the copy-lookup reduction and the argmax chunk partials (ensure_part).
   float* part = nullptr;
   size_t part_bytes = 0;
   // Split-K partial sums of the qmm ([split][MAX_TOK][Npad] fp32), grown on demand.

@@ -5,6 +5,7 @@
 #include <hip/hip_fp16.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 
@@ -268,6 +269,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B) {
     a.sinks = L.sinks;
     a.ring = kv->ring[l];
     a.cap = a.ring ? a.ring : kv->cap;  // slots per head of this layer's cache (the ring of a sliding-window layer)
+    a.vld = v_row(a.cap);
     a.P = kv->P;
     a.B = B;
     a.QH = QH;
@@ -477,8 +479,8 @@ int ih_kv_create(ih_model* m, int capacity, ih_kv** out) { return ih_kv_create_c
 int ih_kv_create_chunked(ih_model* m, int capacity, int chunk, ih_kv** out) {
   IH_CHECK(m && out, IH_EINVAL, "ih_kv_create: null argument");
   IH_CHECK(capacity >= 1, IH_EINVAL, "ih_kv_create: capacity must be positive");
-  IH_CHECK(chunk == 0 || (chunk >= 32 && chunk % 16 == 0), IH_EINVAL,
-           "ih_kv_create_chunked: chunk must be 0 (automatic) or a multiple of 16, at least 32");
+  IH_CHECK(chunk == 0 || (chunk >= 32 && chunk % 32 == 0), IH_EINVAL,
+           "ih_kv_create_chunked: chunk must be 0 (automatic) or a positive multiple of 32");
   *out = nullptr;
   const auto& d = m->d;
   ih_kv* kv = new ih_kv();
@@ -486,10 +488,11 @@ int ih_kv_create_chunked(ih_model* m, int capacity, int chunk, ih_kv** out) {
   kv->cap = capacity;
   // Key chunk: fixed per cache, so a row's result is the same for every block size and every position (the splits
   // are fixed key ranges [s·C, (s+1)·C)). At full capacity the splits of all KV heads are one workgroup per CU: C =
-  // capacity / (CUs / KV heads), rounded up to 16 keys, at least 64.
+  // capacity / (CUs / KV heads), rounded up to the 32-key blocks of the transposed V, at least 64.
   const int per_head = std::max(1, m->ctx->cu_count / std::max(1, d.n_kv_heads));
   int C = (capacity + per_head - 1) / per_head;
-  C = std::max(64, (C + 15) / 16 * 16);
+  C = std::max(64, (C + 31) / 32 * 32);
+  if (const char* ov = getenv("IH_ATTN_CHUNK")) C = std::max(32, atoi(ov) / 32 * 32);  // tuning override
   if (chunk) C = chunk;
   kv->chunk = C;
   const int L = d.n_layers, KVH = d.n_kv_heads, HD = d.head_dim;
@@ -505,11 +508,11 @@ int ih_kv_create_chunked(ih_model* m, int capacity, int chunk, ih_kv** out) {
       if (ring < capacity) { kv->ring[l] = ring; slots = ring; }
     }
     if (st == IH_OK) st = dalloc_t(&kv->kc[l], size_t(KVH) * slots * HD);
-    if (st == IH_OK) st = dalloc_t(&kv->vc[l], size_t(KVH) * slots * HD);
+    if (st == IH_OK) st = dalloc_t(&kv->vc[l], size_t(KVH) * HD * v_row(slots));
     if (st == IH_OK) st = dalloc_t(&kv->ks[l], size_t(KVH) * slots);
     if (st == IH_OK) st = dalloc_t(&kv->vs[l], size_t(KVH) * slots);
     if (st == IH_OK) st = fill(m->ctx, kv->kc[l], 0, size_t(KVH) * slots * HD);
-    if (st == IH_OK) st = fill(m->ctx, kv->vc[l], 0, size_t(KVH) * slots * HD);
+    if (st == IH_OK) st = fill(m->ctx, kv->vc[l], 0, size_t(KVH) * HD * v_row(slots));
     if (st == IH_OK) st = fill(m->ctx, kv->ks[l], 0, size_t(KVH) * slots * 2);
     if (st == IH_OK) st = fill(m->ctx, kv->vs[l], 0, size_t(KVH) * slots * 2);
   }

@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstring>
 #include <cstdlib>
 
 namespace ih {
@@ -228,23 +229,16 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   const int n = lane & 15, qd = lane >> 4;
   const int tile0 = blockIdx.x * R;
   constexpr int nk = KPW;                                // K-blocks of every wave
-  constexpr int nkw = KW * nk;                           // K-blocks of the workgroup
-  const int kwg = int(blockIdx.y) * nkw;                 // first K-block of the workgroup
+  const int kwg = int(blockIdx.y) * KW * nk;             // first K-block of the workgroup
   const int kb0 = kwg + wave * nk;                       // first K-block of this wave
   const unsigned tiles_total = unsigned(p.Npad / 16) * unsigned(p.nkb);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, tiles_total * 1024u), rsb = make_rsrc(p.s, tiles_total * 128u),
                                rx = make_rsrc(p.xa, unsigned(MAX_TOK) * p.nkb * 256u);
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
 
-  // Workgroup staging in LDS, written once behind one barrier: the scale/bias words of the R tiles over the
-  // workgroup's K-blocks ([r][kl][row] 8 bytes) and token 16 of those K-blocks as [kl][t][row ∈ {token 16, zeros}][qd]
-  // 16 bytes, so that lane (n, qd) reads row n ≠ 0 ? zeros : token 16 from an address that depends on the K-block
-  // only through an immediate. They are issued before the weights and waited for first: their latency overlaps the
-  // weight stream.
-  // Epilogue inputs that another kernel just wrote, requested first (consumed after the main loop).
-  // Rows per wave of the RMSNorm prefetch: M ≤ 16 (T = 1), 17 (X16) or 32 (T = 2).
-  // Rows per wave of the RMSNorm prefetch: M ≤ 16 (T = 1), 17 (X16) or 32 (T = 2); more than eight (one-wave
-  // workgroups) are read after the loop instead.
+  // Epilogue inputs that another kernel just wrote, requested first (consumed after the main loop). Rows per wave of
+  // the RMSNorm prefetch: M ≤ 16 (T = 1), 17 (X16) or 32 (T = 2); more than eight (one-wave workgroups) are read after
+  // the loop instead.
   constexpr int NR = ((T == 2 ? 32 : X16 ? 17 : 16) + KW - 1) / KW;
   constexpr bool RMS = MODE == QM_F32_SCALE || MODE == QM_GLU_ACT, RMS_PRE = RMS && NR <= 8;
   RmsPrefetch<RMS_PRE ? NR : 1> rpf;
@@ -253,24 +247,30 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     if (p.ss_in) rms_prefetch(rpf, p.ss_in, SS_CAP, p.M, wave, KW, lane);
   if constexpr (MODE == QM_RESID_ACT) resid_prefetch<R>(hpf, p, tile0);
 
-  __shared__ u32x4 ssb[R * nkw * 8];
-  __shared__ u32x4 s16[X16 ? nkw * 32 : 1];
+  // Wave-private staging in LDS: the scale/bias words of the R tiles over this wave's K-blocks ([r][i][row] 8 bytes)
+  // and token 16 of those K-blocks as [i][t][row ∈ {token 16, zeros}][qd] 16 bytes, so that lane (n, qd) reads
+  // row n ≠ 0 ? zeros : token 16 from an address that depends on the K-block only through an immediate. The loads go
+  // out first and only they are waited for before the LDS writes; no barrier: one wave's LDS operations complete in
+  // order and no other wave reads the region (a workgroup barrier here made every wave wait for the slowest wave's
+  // staging, queued behind all of the workgroup's first weight stages).
+  __shared__ u32x4 ssb[KW][R * nk * 8];
+  __shared__ u32x4 s16[KW][X16 ? nk * 32 : 1];
   __shared__ float rsc[MAX_TOK];
-  constexpr int nsb = R * nkw * 8;
-  constexpr int NSB = (nsb + 64 * KW - 1) / (64 * KW), N16 = X16 ? (nkw * 16 + 64 * KW - 1) / (64 * KW) : 1;
+  constexpr int nsb = R * nk * 8;
+  constexpr int NSB = (nsb + 63) / 64, N16 = X16 ? (nk * 16 + 63) / 64 : 1;
   u32x4 vsb[NSB], v16[N16];
 #pragma unroll
   for (int j = 0; j < NSB; ++j) {
-    const int e = j * 64 * KW + int(threadIdx.x), r = e / (nkw * 8), kl = (e >> 3) % nkw;
-    const unsigned off = (unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kwg + kl)) * 128u + unsigned(e & 7) * 16u;
+    const int e = j * 64 + lane, r = e / (nk * 8), i = (e >> 3) % nk;
+    const unsigned off = (unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kb0 + i)) * 128u + unsigned(e & 7) * 16u;
     vsb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, e < nsb ? off : OOB, 0, 0));
   }
   if constexpr (X16) {
 #pragma unroll
     for (int j = 0; j < N16; ++j) {
-      const int e = j * 64 * KW + int(threadIdx.x), kl = e >> 4, t = (e >> 2) & 3, q = e & 3, kb = kwg + kl;
-      const unsigned off = unsigned(kb) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * q;
-      v16[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, kl < nkw ? off : OOB, 0, 0));
+      const int e = j * 64 + lane, i = e >> 4, t = (e >> 2) & 3, q = e & 3;
+      const unsigned off = unsigned(kb0 + i) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * q;
+      v16[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, i < nk ? off : OOB, 0, 0));
     }
   }
 
@@ -301,20 +301,19 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 
 #pragma unroll
   for (int j = 0; j < NSB; ++j) {
-    const int e = j * 64 * KW + int(threadIdx.x);
-    if (e < nsb) ssb[e] = vsb[j];
+    const int e = j * 64 + lane;
+    if (e < nsb) ssb[wave][e] = vsb[j];
   }
   if constexpr (X16) {
 #pragma unroll
     for (int j = 0; j < N16; ++j) {
-      const int e = j * 64 * KW + int(threadIdx.x), kl = e >> 4, t = (e >> 2) & 3, q = e & 3;
-      if (kl < nkw) {
-        s16[(kl * 4 + t) * 8 + q] = v16[j];
-        s16[(kl * 4 + t) * 8 + 4 + q] = u32x4{0u, 0u, 0u, 0u};
+      const int e = j * 64 + lane, i = e >> 4, t = (e >> 2) & 3, q = e & 3;
+      if (i < nk) {
+        s16[wave][(i * 4 + t) * 8 + q] = v16[j];
+        s16[wave][(i * 4 + t) * 8 + 4 + q] = u32x4{0u, 0u, 0u, 0u};
       }
     }
   }
-  __syncthreads();
 
   f32x4 acc[R][T];
   float acc16[R];
@@ -326,10 +325,10 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   }
   const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
   const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
-  const u32x4* const s16l = s16 + (n ? 4 : 0) + qd;  // this lane's row of the token-16 staging
-  const uint2* const sbl = reinterpret_cast<const uint2*>(ssb) + n;  // row n of the staged scale/bias words
+  const u32x4* const s16l = &s16[wave][0] + (n ? 4 : 0) + qd;  // this lane's row of the token-16 staging
+  const uint2* const sbl = reinterpret_cast<const uint2*>(&ssb[wave][0]) + n;  // row n of the staged scale words
 
-  // Products of ring stage d (K-block kl of the workgroup, kl = wave·nk + i).
+  // Products of ring stage d (K-block kl of this wave, 0 ≤ kl < nk).
   auto compute = [&](int d, int kl) {
     u32x4 x16[X16 ? 4 : 1];
     if constexpr (X16) {
@@ -361,7 +360,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint2 sb = sbl[(r * nkw + kl) * 16];
+      const uint2 sb = sbl[(r * nk + kl) * 16];
       const float s0 = __uint_as_float(sb.x << 16), s1 = __uint_as_float(sb.y << 16);
       const float c0 = fmaf(-128.f, s0, __uint_as_float(sb.x & 0xFFFF0000u));
       const float c1 = fmaf(-128.f, s1, __uint_as_float(sb.y & 0xFFFF0000u));
@@ -395,18 +394,17 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   // The ring: trips of D K-blocks, each multiplied from its stage and the stage refilled D K-blocks ahead, then the
   // last D K-blocks without refills (nk is a multiple of D, which the launch checks; nk = D loads everything at
   // entry).
-  const int kl0 = wave * nk;
   int i = 0;
 #pragma unroll 1
   for (; i < nk - D; i += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      compute(d, kl0 + i + d);
+      compute(d, i + d);
       load_stage(d, kb0 + i + d + D);
     }
   }
 #pragma unroll
-  for (int d = 0; d < D; ++d) compute(d, kl0 + i + d);
+  for (int d = 0; d < D; ++d) compute(d, i + d);
 
   // Partial sums of every wave → LDS [wave][r][tt][e][lane] (+ token 16 [wave][r][row]), then fixed-order sums.
   constexpr int NEL = R * T * 4 * 64;
@@ -497,7 +495,7 @@ static bool qmm_shape_ok(const QmmShape& sh, int Npad, int nkb) {
 }
 // The instantiated (R, KW, KPW) shapes (qmm_dispatch_mode lists the same set).
 static constexpr int kQmmShapes[][3] = {{1, 16, 2}, {2, 16, 2}, {2, 8, 4}, {4, 8, 4}, {4, 4, 8}, {7, 4, 8},
-                                        {1, 14, 8}, {1, 8, 14}, {4, 4, 2}, {2, 8, 2}, {4, 8, 2}, {1, 1, 1},
+                                        {1, 8, 14}, {1, 14, 8}, {4, 4, 2}, {2, 8, 2}, {4, 8, 2}, {1, 1, 1},
                                         {2, 1, 1},  {4, 1, 1},  {7, 1, 1}};
 static QmmShape qmm_shape(int Npad, int nkb) {
   const int NT = Npad / 16;
@@ -601,10 +599,17 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   IH_CHECK(M >= 1 && M <= MAX_TOK, IH_EINVAL, "qmm: M must be in 1..32");
   IH_CHECK(a.nkb == W->nkb && !a.f16, IH_EINVAL, "qmm: activation K does not match the matrix");
   QmmShape sh = qmm_shape(W->Npad, W->nkb);
-  if (const char* ov = getenv("IH_QMM_SHAPE")) {  // tuning override for every matrix: R,KW,kpw
-    if (sscanf(ov, "%d,%d,%d", &sh.R, &sh.KW, &sh.kpw) == 3) {
-      sh.D = sh.kpw % 2 ? 1 : 2;
-      sh.ks = W->nkb / std::max(1, sh.KW * sh.kpw);
+  // Tuning overrides: IH_QMM_SHAPE = "R,KW,kpw" for every matrix, IH_QMM_SHAPES = "N:K=R,KW,kpw;…" per matrix.
+  auto apply = [&](int R, int KW, int kpw) {
+    sh = QmmShape{R, KW, kpw % 2 ? 1 : 2, kpw, W->nkb / std::max(1, KW * kpw)};
+  };
+  int oR, oKW, okpw;
+  if (const char* ov = getenv("IH_QMM_SHAPE"))
+    if (sscanf(ov, "%d,%d,%d", &oR, &oKW, &okpw) == 3) apply(oR, oKW, okpw);
+  if (const char* ov = getenv("IH_QMM_SHAPES")) {
+    for (const char* q = ov; q && *q; q = strchr(q, ';') ? strchr(q, ';') + 1 : nullptr) {
+      int n, k;
+      if (sscanf(q, "%d:%d=%d,%d,%d", &n, &k, &oR, &oKW, &okpw) == 5 && n == W->N && k == W->K) apply(oR, oKW, okpw);
     }
   }
   IH_CHECK(qmm_shape_ok(sh, W->Npad, W->nkb), IH_EINVAL, "qmm: launch shape does not tile the matrix");

@@ -40,24 +40,58 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// argmax per row, ties to the lowest index, NaN never wins: argmax_rows, Shaders/verify.metal:525-547.
-// Grid (rows), 1024 threads.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int ldx, int N,
-                                                      uint32_t* __restrict__ out) {
-  __shared__ float bv[16];
-  __shared__ uint32_t bi[16];
-  const float* xr = x + size_t(blockIdx.x) * ldx;
+// argmax per row, ties to the lowest index, NaN never wins: argmax_rows, Shaders/verify.metal:525-547. Two passes: grid
+// (rows, ARGMAX_CHUNKS) workgroups of 256 threads each reduce a contiguous chunk of the row with 16-byte loads, four
+// in flight per thread (a row per workgroup left 17 CUs to stream 10 MB one load at a time), then one wave per row
+// merges the chunks in order.
+constexpr int ARGMAX_CHUNKS = 16;
+
+// (v, i) beats (m, mi): larger value, or equal value and lower index; NaN never beats.
+__device__ __forceinline__ bool am_better(float v, uint32_t i, float m, uint32_t mi) {
+  return v > m || (v == m && i < mi);
+}
+
+__global__ __launch_bounds__(256) void argmax_chunk_kernel(const float* __restrict__ x, int ldx, int N,
+                                                           float2* __restrict__ part) {
+  __shared__ float bv[4];
+  __shared__ uint32_t bi[4];
+  const int row = blockIdx.x, ch = blockIdx.y;
+  const int per = (N + ARGMAX_CHUNKS - 1) / ARGMAX_CHUNKS;
+  const int c0 = ch * per, c1 = min(N, c0 + per);
+  const float* xr = x + size_t(row) * ldx;
   float m = -INFINITY;
   uint32_t mi = 0xFFFFFFFFu;
-  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+  // Aligned 16-byte body [a0, a1) of the chunk (ldx and the row start are 16-byte aligned when ldx % 4 == 0), scalar
+  // head and tail.
+  const int a0 = (ldx % 4 == 0) ? min(c1, (c0 + 3) & ~3) : c1, a1 = (ldx % 4 == 0) ? max(a0, c1 & ~3) : c1;
+  for (int i = c0 + int(threadIdx.x); i < a0; i += 256) {
     const float v = xr[i];
-    if (v > m) { m = v; mi = uint32_t(i); }
+    if (am_better(v, uint32_t(i), m, mi)) { m = v; mi = uint32_t(i); }
   }
-  // Wave reduction: larger value, or equal value and lower index.
+  for (int i0 = a0 + 4 * int(threadIdx.x); i0 < a1; i0 += 4 * 256 * 4) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + 4 * 256 * u;
+      v[u] = i < a1 ? *reinterpret_cast<const float4*>(xr + i) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t i = uint32_t(i0 + 4 * 256 * u);
+      if (am_better(v[u].x, i, m, mi)) { m = v[u].x; mi = i; }
+      if (am_better(v[u].y, i + 1, m, mi)) { m = v[u].y; mi = i + 1; }
+      if (am_better(v[u].z, i + 2, m, mi)) { m = v[u].z; mi = i + 2; }
+      if (am_better(v[u].w, i + 3, m, mi)) { m = v[u].w; mi = i + 3; }
+    }
+  }
+  for (int i = a1 + int(threadIdx.x); i < c1; i += 256) {
+    const float v = xr[i];
+    if (am_better(v, uint32_t(i), m, mi)) { m = v; mi = uint32_t(i); }
+  }
   for (int o = 32; o >= 1; o >>= 1) {
     const float om = __shfl_xor(m, o);
     const uint32_t oi = __shfl_xor(mi, o);
-    if (om > m || (om == m && oi < mi)) { m = om; mi = oi; }
+    if (am_better(om, oi, m, mi)) { m = om; mi = oi; }
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { bv[wave] = m; bi[wave] = mi; }
@@ -65,10 +99,27 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
   if (threadIdx.x == 0) {
     float b = bv[0];
     uint32_t ix = bi[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); ++i)
-      if (bv[i] > b || (bv[i] == b && bi[i] < ix)) { b = bv[i]; ix = bi[i]; }
-    out[blockIdx.x] = ix == 0xFFFFFFFFu ? 0u : ix;   // all NaN / −inf: index 0, as the reference
+    for (int w = 1; w < 4; ++w)
+      if (am_better(bv[w], bi[w], b, ix)) { b = bv[w]; ix = bi[w]; }
+    part[row * ARGMAX_CHUNKS + ch] = make_float2(b, __uint_as_float(ix));
   }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float2* __restrict__ part, uint32_t* __restrict__ out) {
+  const int row = blockIdx.x, l = threadIdx.x;
+  float m = -INFINITY;
+  uint32_t mi = 0xFFFFFFFFu;
+  if (l < ARGMAX_CHUNKS) {
+    const float2 p = part[row * ARGMAX_CHUNKS + l];
+    m = p.x;
+    mi = __float_as_uint(p.y);
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float om = __shfl_xor(m, o);
+    const uint32_t oi = __shfl_xor(mi, o);
+    if (am_better(om, oi, m, mi)) { m = om; mi = oi; }
+  }
+  if (l == 0) out[row] = mi == 0xFFFFFFFFu ? 0u : mi;  // all NaN / −inf: index 0, as the reference
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -107,8 +158,12 @@ int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const ui
 }
 
 int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out) {
+  IH_TRY(ensure_part(c, size_t(rows) * ARGMAX_CHUNKS * sizeof(float2)));
+  float2* part = reinterpret_cast<float2*>(c->part);
   TimedLaunch tl(c, TC_ARGMAX, double(rows) * N * 4);
-  tlaunch(tl, argmax_kernel, dim3(rows), dim3(1024), 0, c->stream, x, ldx, N, out);
+  tlaunch(tl, argmax_chunk_kernel, dim3(rows, ARGMAX_CHUNKS), dim3(256), 0, c->stream, x, ldx, N, part);
+  IH_HIP(hipGetLastError());
+  argmax_final_kernel<<<rows, 64, 0, c->stream>>>(part, out);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }

@@ -60,6 +60,7 @@ TimedLaunch::~TimedLaunch() {
 
 int ensure_part(ih_ctx* c, size_t bytes) {
   if (c->part_bytes >= bytes) return IH_OK;
+  IH_HIP(hipStreamSynchronize(c->stream));  // kernels already queued may still read the old buffer
   if (c->part) IH_HIP(hipFree(c->part));
   c->part = nullptr;
   c->part_bytes = 0;

@@ -9,6 +9,7 @@
 //   KV           per (head, position): x_d = n(key, ((head << 24) + pos) · HD + d), symmetric int8 with fp16 scale
 //                sc = fp16(amax / 127) (1 when amax = 0), q = clamp(rint(x / sc), ±127)
 #include "act.h"
+#include "attn_args.h"
 #include "ih_internal.h"
 
 namespace ih {
@@ -50,8 +51,8 @@ __global__ void synth_f32_kernel(float* out, size_t n, uint64_t key, float base,
     out[i] = base + amp * sm_normal(key, i);
 }
 
-// One block per (position, KV head): HD threads (64 or 128). K and V of the cache layout [head][slot][HD] int8 and the
-// fp16 scales [head][slot].
+// One block per (position, KV head): HD threads (64 or 128). K of the cache layout [head][slot][HD] int8, V transposed
+// [head][HD][vld] (v_index), and the fp16 scales [head][slot].
 __global__ void synth_kv_kernel(int8_t* kc, int8_t* vc, __half* ks, __half* vs, int HD, int cap, int ring, int pos0,
                                 uint64_t kk, uint64_t kv) {
   __shared__ float red[4];
@@ -70,8 +71,8 @@ __global__ void synth_kv_kernel(int8_t* kc, int8_t* vc, __half* ks, __half* vs, 
     const __half sc16 = __float2half_rn(amax > 0.f ? amax / 127.0f : 1.0f);
     const float sc = __half2float(sc16);
     const float q = fminf(127.f, fmaxf(-127.f, rintf(x / sc)));
-    int8_t* dst = which ? vc : kc;
-    dst[(size_t(h) * cap + slot) * HD + d] = int8_t(q);
+    if (which) vc[v_index(h, slot, d, HD, v_row(cap))] = int8_t(q);
+    else kc[(size_t(h) * cap + slot) * HD + d] = int8_t(q);
     if (d == 0) (which ? vs : ks)[size_t(h) * cap + slot] = sc16;
   }
 }

@@ -109,10 +109,10 @@ def test_moe_two_layers_within_routing_sensitivity(ctx):
 
 
 @pytest.mark.parametrize("shape", [SMALL, GQA8], ids=["gqa2-hd128", "gqa8-hd64"])
-@pytest.mark.parametrize("chunk", [48, 1024, 0])
+@pytest.mark.parametrize("chunk", [32, 96, 1024, 0])
 def test_verify_step_long_context_chunks(ctx, shape, chunk):
-    """P = 1500 with key chunks of 48 (31 splits, partial last 64-key block), 1024 (several LDS sub-chunks per split)
-    and automatic: the same oracle tolerance, and the three chunkings agree with each other within it."""
+    """P = 1500 with key chunks of 32 (48 splits, half-filled 64-key pieces), 96 (16 splits, a partial last piece per
+    split), 1024 (two batches of pieces per split) and automatic: the same oracle tolerance."""
     d, m, kv = make(ctx, shape, P=1500, cap=1600, chunk=chunk)
     try:
         if chunk:
