@@ -17,7 +17,7 @@ namespace ih {
 
 // Launchers of the other translation units.
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                     float* h, int B, int H, const uint16_t* nw, ActBuf& a);
+                     float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a);
 int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out);
 int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows);
 int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_t K, uint64_t seed, uint64_t tensor,
@@ -241,13 +241,14 @@ static int ensure_partials(ih_model* m, int splits) {
   return IH_OK;
 }
 
-// The sequence of one verify step on B rows whose tokens are in m->tok; top1 → m->top1.
-static int run_step(ih_model* m, ih_kv* kv, int B) {
+// The sequence of one verify step on B rows whose tokens are in tok (device); top1 → top1 (device).
+static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t* top1) {
   ih_ctx* c = m->ctx;
   const auto& d = m->d;
   const int H = d.hidden, QH = d.n_q_heads, KVH = d.n_kv_heads, HD = d.head_dim, I = d.intermediate;
   // The block's rows and the first RMSNorm input.
-  IH_TRY(launch_embed_act(c, m->tok, m->emb_w, m->emb_s, m->emb_b, m->h, B, H, m->layers[0].attn_norm, m->act_attn));
+  IH_TRY(launch_embed_act(c, tok, m->emb_w, m->emb_s, m->emb_b, m->h, B, H, d.vocab, m->layers[0].attn_norm,
+                          m->act_attn));
   const int total = kv->P + B;
   for (int l = 0; l < d.n_layers; ++l) {
     const ih_layer& L = m->layers[l];
@@ -338,7 +339,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B) {
   eh.ldy = d.vocab;
   eh.eps = d.rms_eps;
   IH_TRY(launch_qmm_ex(c, m->head, 0, m->act_attn, B, eh));
-  IH_TRY(launch_argmax(c, m->logits, d.vocab, B, d.vocab, m->top1));
+  IH_TRY(launch_argmax(c, m->logits, d.vocab, B, d.vocab, top1));
   kv->last_B = B;
   kv->written = std::max(kv->written, kv->P + B);
   return IH_OK;
@@ -582,9 +583,7 @@ int ih_kv_commit(ih_kv* kv, int n) {
 int ih_verify_step_dev(ih_model* m, ih_kv* kv, const uint32_t* tokens_dev, int B, uint32_t* top1_dev) {
   IH_TRY(check_step(m, kv, B));
   IH_CHECK(tokens_dev && top1_dev, IH_EINVAL, "ih_verify_step_dev: null buffer");
-  IH_HIP(hipMemcpyAsync(m->tok, tokens_dev, B * 4, hipMemcpyDeviceToDevice, m->ctx->stream));
-  IH_TRY(run_step(m, kv, B));
-  IH_HIP(hipMemcpyAsync(top1_dev, m->top1, B * 4, hipMemcpyDeviceToDevice, m->ctx->stream));
+  IH_TRY(run_step(m, kv, B, tokens_dev, top1_dev));
   return IH_OK;
 }
 
@@ -595,7 +594,7 @@ int ih_verify_step(ih_model* m, ih_kv* kv, const uint32_t* tokens, int B, float*
     IH_CHECK(tokens[i] < uint32_t(m->d.vocab), IH_EINVAL, "ih_verify_step: token id beyond the vocabulary");
   hipStream_t s = m->ctx->stream;
   IH_HIP(hipMemcpyAsync(m->tok, tokens, B * 4, hipMemcpyHostToDevice, s));
-  IH_TRY(run_step(m, kv, B));
+  IH_TRY(run_step(m, kv, B, m->tok, m->top1));
   IH_HIP(hipMemcpyAsync(top1_out, m->top1, B * 4, hipMemcpyDeviceToHost, s));
   if (logits_out)
     IH_HIP(hipMemcpyAsync(logits_out, m->logits, size_t(B) * m->d.vocab * 4, hipMemcpyDeviceToHost, s));

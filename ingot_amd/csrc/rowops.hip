@@ -13,10 +13,12 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
                                                         const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
                                                         float* __restrict__ h, int H, int ldh,
                                                         const uint16_t* __restrict__ nw, uint4* __restrict__ frag,
-                                                        int nkb, int ntile, float* __restrict__ ss_out) {
+                                                        int nkb, int ntile, float* __restrict__ ss_out, int V) {
   __shared__ float red[4];
   const int row = blockIdx.x;
-  const uint32_t t = tok[row];
+  // Ids beyond the vocabulary (the device entry points cannot check them on the host) read the last row instead of
+  // memory past the table.
+  const uint32_t t = min(tok[row], uint32_t(V - 1));
   const uint32_t* wr = w + size_t(t) * (H / 8);
   float ss = 0.f;
   for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
@@ -148,10 +150,10 @@ __global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1
 
 // ---------------------------------------------------------------------------------------------------------------
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                     float* h, int B, int H, const uint16_t* nw, ActBuf& a) {
+                     float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a) {
   TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4 + 2));
   tlaunch(tl, embed_act_kernel, dim3(B), dim3(256), 0, c->stream, tok, w, s, b, h, H, H, nw, static_cast<uint4*>(a.frag),
-          a.nkb, a.ntile, a.ss);
+          a.nkb, a.ntile, a.ss, V);
   IH_HIP(hipGetLastError());
   a.nss = 1;
   return IH_OK;
