@@ -35,7 +35,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------------------------------------------------------
 // Prework: grid (QH + 2·KVH, B), HD threads. vattn_prework_i8 (verify_attn_nax.metal:47-146) without QK-norm and gate
 // (the configurations have neither): RoPE on all HD dims (non-interleaved halves, angle pos·θ^(−i/(HD/2)) evaluated in
-// double), orthonormal WHT (Sylvester order, stages 1, 2, 4, …, then ×1/√HD) of q and k, int8 quantisation of k and v
+// double once per step into the table a.rope), orthonormal WHT (Sylvester order, stages 1, 2, 4, …, then ×1/√HD) of q and k, int8 quantisation of k and v
 // per (token, head): sc = fp16(amax/127) (1 when amax = 0), q = clamp(rint(x/sc), ±127), written at slot P + t.
 __global__ void prework_kernel(AttnArgs a) {
   __shared__ float xs[256];
@@ -52,8 +52,8 @@ __global__ void prework_kernel(AttnArgs a) {
     xs[d] = x;
     __syncthreads();
     const int RH = HD / 2, i = d % RH;
-    const double ang = double(pos) * pow(double(a.theta), -double(i) / double(RH));
-    const float cs = float(cos(ang)), sn = float(sin(ang));
+    const float2 cs_sn = a.rope[t * RH + i];  // (cos, sin) of pos·θ^(−i/RH), from the step's table
+    const float cs = cs_sn.x, sn = cs_sn.y;
     x = d < RH ? x * cs - xs[d + RH] * sn : x * cs + xs[d - RH] * sn;
     if (a.hadk) {
       for (int h = 1; h < HD; h <<= 1) {

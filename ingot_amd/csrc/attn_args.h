@@ -22,6 +22,7 @@ struct AttnArgs {
   const float* proj;   // [B][ldp] = q heads | k heads | v heads (fp32, the qkv qmm output)
   int ldp;
   __half* q;           // [KVH][Qpad][HD] fp16, query m = t·G + (h mod G)
+  const float2* rope;  // [B][HD/2] (cos, sin) of the angle pos·θ^(−i/(HD/2)), pos = P + t
   int8_t* kc;          // [KVH][cap][HD]
   int8_t* vc;          // [KVH][HD][vld]: V transposed, slots permuted within 32-slot blocks (v_index)
   __half* ks;          // [KVH][cap]

@@ -17,7 +17,8 @@ namespace ih {
 
 // Launchers of the other translation units.
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                     float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a);
+                     float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a, float2* rope, int P, float theta,
+                     int RH);
 int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out);
 int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows);
 int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_t K, uint64_t seed, uint64_t tensor,
@@ -95,6 +96,7 @@ struct ih_model {
   uint32_t* tok = nullptr;   // [MAX_TOK]
   uint32_t* top1 = nullptr;  // [MAX_TOK]
   __half* q = nullptr;       // [KVH][Qpad][HD]
+  float2* rope = nullptr;    // [IH_MAX_ROWS][HD/2] (cos, sin) of the step's positions
   // Activations: RMSNorm inputs bf16(h ⊙ w) with their sums of squares (attention / final norm, FFN norm), the
   // attention output and the gated activation.
   ActBuf act_attn, act_mlp, act_o, act_i;
@@ -221,7 +223,7 @@ static void model_release(ih_model* m) {
   }
   ih_qmat_free(m->head);
   void* ptrs[] = {m->emb_w, m->emb_s, m->emb_b, m->final_norm, m->h, m->proj, m->logits, m->tok, m->top1,
-                  m->q, m->opart, m->ml, m->rlogits, m->nent, m->entries, m->x_row, m->pair_w, m->row_pair,
+                  m->q, m->rope, m->opart, m->ml, m->rlogits, m->nent, m->entries, m->x_row, m->pair_w, m->row_pair,
                   m->hpair, m->opair};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
@@ -248,7 +250,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
   const int H = d.hidden, QH = d.n_q_heads, KVH = d.n_kv_heads, HD = d.head_dim, I = d.intermediate;
   // The block's rows and the first RMSNorm input.
   IH_TRY(launch_embed_act(c, tok, m->emb_w, m->emb_s, m->emb_b, m->h, B, H, d.vocab, m->layers[0].attn_norm,
-                          m->act_attn));
+                          m->act_attn, m->rope, kv->P, d.rope_theta, HD / 2));
   const int total = kv->P + B;
   for (int l = 0; l < d.n_layers; ++l) {
     const ih_layer& L = m->layers[l];
@@ -263,6 +265,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
     a.proj = m->proj;
     a.ldp = m->QP;
     a.q = m->q;
+    a.rope = m->rope;
     a.kc = kv->kc[l];
     a.vc = kv->vc[l];
     a.ks = kv->ks[l];
@@ -428,6 +431,7 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
   run(dalloc_t(&m->tok, MAX_TOK));
   run(dalloc_t(&m->top1, MAX_TOK));
   run(dalloc_t(&m->q, size_t(KVH) * m->Qpad * HD));
+  run(dalloc_t(&m->rope, size_t(IH_MAX_ROWS) * (HD / 2)));
   const bool moe = d.n_experts > 0, moe_f16 = moe && d.expert_format == QF_MXFP4;
   if (st == IH_OK) run(ensure_act(c, m->act_attn, H, false));
   if (st == IH_OK) run(ensure_act(c, m->act_mlp, H, moe_f16));

@@ -8,14 +8,21 @@ namespace ih {
 // ---------------------------------------------------------------------------------------------------------------
 // Embedding of the block's rows: h[r] = dequant(table[tok[r]]) in fp32 (MLX int4 g64 row; embed_rows,
 // Shaders/yy_model.metal:12-49), and the first layer's RMSNorm input: the activation bf16(h ⊙ w) and Σh² per row
-// (one partial). Grid (rows), 256 threads; one thread per 8 values.
+// (one partial). Also the step's RoPE table (the rotation angles depend only on the position, so every layer's
+// prework reads them): rope[r][i] = (cos, sin)(pos · θ^(−i/RH)), pos = P + r, evaluated in double. Grid (rows), 256
+// threads; one thread per 8 values.
 __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restrict__ tok, const uint32_t* __restrict__ w,
                                                         const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
                                                         float* __restrict__ h, int H, int ldh,
                                                         const uint16_t* __restrict__ nw, uint4* __restrict__ frag,
-                                                        int nkb, int ntile, float* __restrict__ ss_out, int V) {
+                                                        int nkb, int ntile, float* __restrict__ ss_out, int V,
+                                                        float2* __restrict__ rope, int P, float theta, int RH) {
   __shared__ float red[4];
   const int row = blockIdx.x;
+  for (int i = threadIdx.x; i < RH; i += blockDim.x) {
+    const double ang = double(P + row) * pow(double(theta), -double(i) / double(RH));
+    rope[row * RH + i] = make_float2(float(cos(ang)), float(sin(ang)));
+  }
   // Ids beyond the vocabulary (the device entry points cannot check them on the host) read the last row instead of
   // memory past the table.
   const uint32_t t = min(tok[row], uint32_t(V - 1));
@@ -150,10 +157,11 @@ __global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1
 
 // ---------------------------------------------------------------------------------------------------------------
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                     float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a) {
+                     float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a, float2* rope, int P, float theta,
+                     int RH) {
   TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4 + 2));
   tlaunch(tl, embed_act_kernel, dim3(B), dim3(256), 0, c->stream, tok, w, s, b, h, H, H, nw, static_cast<uint4*>(a.frag),
-          a.nkb, a.ntile, a.ss, V);
+          a.nkb, a.ntile, a.ss, V, rope, P, theta, RH);
   IH_HIP(hipGetLastError());
   a.nss = 1;
   return IH_OK;
