@@ -143,7 +143,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   auto slot_of = [ring](int key) { return RING ? key % ring : key; };
 
   // The loads of a batch of NP pieces (keys kbase + 64p …) go out together, in piece order; keys past k1 read key
-  // k1 − 1 (their scales are zero and their scores masked).
+  // k1 − 1 (their scales are zeroed at the conversion and their scores masked). No load's value goes through a
+  // select: the compiler would wait for that load before issuing the next piece's.
   PieceRegs pr[NP];
   auto load_batch = [&](int kbase) {
 #pragma unroll
@@ -154,17 +155,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
         pr[p].k = *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + col);
       }
       if (tid < VITEMS) {
-        // 16 positions of one dim; a 32-slot block wholly past k1 is not read (its keys are masked, scale zero).
+        // 16 positions of one dim; a 32-slot block wholly past k1 reads the last one instead (its keys are masked and
+        // their scales zeroed at the conversion).
         const int dim = tid / (PIECE / 16), pc = tid % (PIECE / 16), pos = kb + 16 * pc;
-        pr[p].v = (pos & ~31) < k1 ? *reinterpret_cast<const uint4*>(vh + size_t(dim) * a.vld + slot_of(pos & ~31) +
-                                                                     (pos & 31))
-                                   : make_uint4(0, 0, 0, 0);
+        const int blk = min(pos & ~31, (k1 - 1) & ~31);
+        pr[p].v = *reinterpret_cast<const uint4*>(vh + size_t(dim) * a.vld + slot_of(blk) + (pos & 31));
       }
       if (tid < PIECE) {
-        const int key = kb + tid;
-        const bool ok = key < k1;
-        pr[p].ks = ok ? ksh[slot_of(key)] : __float2half(0.f);
-        pr[p].vs = ok ? vsh[slot_of(key)] : __float2half(0.f);
+        const int key = min(kb + tid, k1 - 1);
+        pr[p].ks = ksh[slot_of(key)];
+        pr[p].vs = vsh[slot_of(key)];
       }
     }
   };
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   }
 
   // Piece p → LDS buffer b.
-  auto store = [&](const PieceRegs& r, int b) {
+  auto store = [&](const PieceRegs& r, int b, int kb) {
     if (tid < KITEMS) {
       const int key = tid / KPK, col = (tid % KPK) * 16;
       const unsigned kw[4] = {r.k.x, r.k.y, r.k.z, r.k.w};
@@ -229,8 +229,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       *reinterpret_cast<u32x4*>(&Vt[b][dim * VROW + 16 * pc + 8]) = h1;
     }
     if (tid < PIECE) {
-      ksf[b][tid] = __half2float(r.ks) * a.scale_log2;
-      vsf[b][tid] = __half2float(r.vs);
+      const bool ok = kb + tid < k1;
+      ksf[b][tid] = ok ? __half2float(r.ks) * a.scale_log2 : 0.f;
+      vsf[b][tid] = ok ? __half2float(r.vs) : 0.f;
     }
   };
 
@@ -338,7 +339,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       const int kb = kbase + PIECE * p;
       if (kb >= k1) break;  // uniform: the split's last piece was p − 1
       const int b = (npc + p) & 1;
-      store(pr[p], b);
+      store(pr[p], b, kb);
       __syncthreads();
       piece_products(b, kb, min(PIECE, k1 - kb));
     }
