@@ -100,6 +100,15 @@ __device__ __forceinline__ void i8x4_to_h(unsigned w, __half2& lo, __half2& hi) 
   hi = __hsub2(__builtin_bit_cast(__half2, h), off);
 }
 
+// Max over the 4 lanes of a query column (lanes j, j + 16, j + 32, j + 48) with the gfx950 lane swaps (no LDS round
+// trip, unlike a shuffle).
+__device__ __forceinline__ float row_max4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 constexpr int ATT_THREADS = 512;  // 8 waves: all load and convert, the first ceil(tiles / TPW) multiply
 constexpr int PIECE = 64;         // keys per pipelined piece of a split
 constexpr int MAX_PIECES = 8;     // pieces whose loads are in flight together (a batch)
@@ -170,7 +179,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   };
   if (k0 < k1) load_batch(k0);
 
-  // Query tiles of this wave: wave + 8·tt.
+  // Query tiles of this wave: wave + 8·tt. With exactly 5 tiles (TPW = 1) the fifth is shared by waves 4-7, wave
+  // 4 + h taking the 16-key sub-tile h of every piece, so that no SIMD carries two tiles; their four (max, sum, O)
+  // states are merged at the end.
+  const bool sp5 = TPW == 1 && (Q + 15) / 16 == 5;  // workgroup-uniform
+  const bool helper = sp5 && wave >= 4;            // wave-uniform
+  const int hsub = wave - 4;
   f16x8 qf[TPW][NC];
   f32x4 o[TPW][NDT];
   float mrun[TPW], lsum[TPW];
@@ -178,7 +192,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   bool live[TPW];
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
-    const int qt = wave + 8 * tt, m = 16 * qt + j;
+    const int qt = helper ? 4 : wave + 8 * tt, m = 16 * qt + j;
     live[tt] = 16 * qt < Q;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -236,7 +250,63 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   };
 
   // The products of piece (buffer b) with keys kb …, nkeys of them staged (the rest are zero and masked).
+  // A helper wave's share of tile 4 in a piece: Sᵀ of its 16 keys (v_mfma_f32_16x16x32_f16), the online softmax on
+  // them, Oᵀ += Vᵀ·Pᵀ with v_mfma_f32_16x16x16_f16 (lane group qd holds keys 4qd … 4qd + 3 of the sub-tile, whose Vᵀ
+  // positions in the permuted 32-slot block are 8qd + 4·(h mod 2) …).
+  auto helper_products = [&](int b, int kb, int nkeys) {
+    if (kb > tile_hi[0] || kb + 63 < tile_lo[0]) return;
+    const int h = hsub;
+    if (16 * h >= nkeys) return;  // every key of the sub-tile is past the split (all masked)
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const f16x8 kf = *reinterpret_cast<const f16x8*>(&Kf[b][(16 * h + j) * KR + 32 * c + 8 * qd]);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][c], sacc, 0, 0, 0);
+    }
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    f16x4 vf[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+      vf[dt] = *reinterpret_cast<const f16x4*>(&Vt[b][(16 * dt + j) * VROW + 32 * (h >> 1) + 8 * qd + 4 * (h & 1)]);
+    const f32x4 ksv = *reinterpret_cast<const f32x4*>(&ksf[b][16 * h + 4 * qd]);
+    const f32x4 vsv = *reinterpret_cast<const f32x4*>(&vsf[b][16 * h + 4 * qd]);
+    float sv[4];
+    float mx = -INFINITY;
+    const bool full = nkeys == PIECE && kb + 63 <= tile_lo_lim[0] && kb >= tile_hi_lo[0];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kk = 16 * h + 4 * qd + r, key = kb + kk;
+      const bool vis = full || (kk < nkeys && key <= lim[0] && key >= lo_key[0]);
+      sv[r] = vis ? sacc[r] * ksv[r] : -INFINITY;
+      mx = fmaxf(mx, sv[r]);
+    }
+    mx = row_max4(mx);
+    const float mnew = fmaxf(mrun[0], mx);
+    const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[0] - mnew);
+    mrun[0] = mnew;
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    float ps = 0.f;
+    f16x4 pb;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pv = __builtin_amdgcn_exp2f(sv[r] - mref);
+      ps += pv;
+      pb[r] = (_Float16)(pv * vsv[r]);
+    }
+    lsum[0] = lsum[0] * alpha + ps;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[0][dt] *= alpha;
+    }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[dt], pb, o[0][dt], 0, 0, 0);
+  };
+
   auto piece_products = [&](int b, int kb, int nkeys) {
+    if (helper) {
+      helper_products(b, kb, nkeys);
+      return;
+    }
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt) {
       if (!live[tt]) continue;  // uniform per wave
@@ -257,10 +327,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int h = 0; h < 4; ++h) sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h], qf[tt][c], sacc[h], 0, 0, 0);
       }
-      // Vᵀ fragments are read at the products (the second half only when it is staged).
+      // Vᵀ fragments of the first 32 keys, read before the softmax so they have landed by the products (the second
+      // half's are read at its products, when it is staged).
       auto vread = [&](int hs, int dt) {
         return *reinterpret_cast<const f16x8*>(&Vt[b][(16 * dt + j) * VROW + (hs && half2 ? 32 : 0) + 8 * qd]);
       };
+      f16x8 vf0[NDT];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) vf0[dt] = vread(0, dt);
       // This lane's keys 16h + 4qd + r: their scales as one 16-byte LDS read per tile.
       f32x4 ksv[4], vsv[4];
 #pragma unroll
@@ -291,8 +365,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
             mx = fmaxf(mx, s[h][r]);
           }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = row_max4(mx);
       const float mnew = fmaxf(mrun[tt], mx);
       const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[tt] - mnew);
       mrun[tt] = mnew;
@@ -317,7 +390,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       }
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
-        o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(0, dt), pb[0], o[tt][dt], 0, 0, 0);
+        o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf0[dt], pb[0], o[tt][dt], 0, 0, 0);
       if (half2) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
@@ -346,14 +419,63 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     npc += NP;
   }
 
+  // Tile 4's helper states merged into wave 4's (through the K staging buffer, free after the last piece): M = max
+  // of the maxima, L = Σ 2^(m_i − M)·l_i, O = Σ 2^(m_i − M)·O_i, in helper order.
+  if (sp5) {
+    float l = lsum[0];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    constexpr int HST = 16 * HD + 32;  // floats per helper state: O [dim][query], then (max, sum) per query
+    float* scr = reinterpret_cast<float*>(&Kf[0][0]);
+    static_assert(3 * HST * 4 <= sizeof(Kf), "the merge scratch fits the K staging buffers");
+    __syncthreads();  // every wave is past its last piece
+    if (helper && hsub > 0) {
+      float* st = scr + (hsub - 1) * HST;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st[(16 * dt + 4 * qd + r) * 16 + j] = o[0][dt][r];
+      if (qd == 0) {
+        st[16 * HD + j] = mrun[0];
+        st[16 * HD + 16 + j] = l;
+      }
+    }
+    __syncthreads();
+    if (helper && hsub == 0) {
+      float M = mrun[0];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) M = fmaxf(M, scr[i * HST + 16 * HD + j]);
+      const float w0 = mrun[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrun[0] - M);
+      float L = w0 * l;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[0][dt] *= w0;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const float mi = scr[i * HST + 16 * HD + j];
+        const float wi = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - M);
+        L += wi * scr[i * HST + 16 * HD + 16 + j];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[0][dt][r] += wi * scr[i * HST + (16 * dt + 4 * qd + r) * 16 + j];
+      }
+      mrun[0] = M;
+      lsum[0] = L;  // already the row's total
+    }
+    if (helper && hsub > 0) return;
+    if (!helper) lsum[0] = l;
+  }
+
   // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
     if (!live[tt]) continue;
     float l = lsum[tt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const int m = 16 * (wave + 8 * tt) + j;
+    if (!sp5) {
+      l += __shfl_xor(l, 16);
+      l += __shfl_xor(l, 32);
+    }
+    const int m = 16 * ((helper ? 4 : wave) + 8 * tt) + j;
     if (m >= Q) continue;
     const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
     if (qd == 0) a.ml[base + m] = make_float2(mrun[tt], l);
