@@ -19,6 +19,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "act.h"
 #include "attn_args.h"
@@ -111,7 +112,7 @@ __device__ __forceinline__ float row_max4(float x) {
 
 constexpr int ATT_THREADS = 512;  // 8 waves: all load and convert, the first ceil(tiles / TPW) multiply
 constexpr int PIECE = 64;         // keys per pipelined piece of a split
-constexpr int MAX_PIECES = 8;     // pieces whose loads are in flight together (a batch)
+constexpr int MAX_PIECES = 8;     // deepest ring of pieces in flight
 template <int HD> constexpr int krow() { return HD + 8; }
 constexpr int VROW = PIECE + 8;   // LDS row of Vᵀ in halves
 
@@ -123,11 +124,10 @@ struct PieceRegs {
 };
 
 // One workgroup per (split of C keys, KV head): every query row of the head's group (G·B ≤ 16·8·TPW) in one pass.
-// The split streams through LDS in pieces of 64 keys: the loads of up to eight pieces are issued together (in piece
-// order, so the wait for piece p covers only pieces ≤ p), each piece is converted int8 → fp16 into one of two LDS buffers (K
-// key-major, V transposed) as soon as its loads land, and the waves multiply it while the later pieces are still on
-// their way; one barrier per piece (the buffer written for piece p + 2 was last read for piece p, before the barrier
-// of piece p + 1). Each wave runs its 16-query tiles over the piece with an online softmax in base 2.
+// The split streams through LDS in pieces of 64 keys from a ring of NP pieces in registers (piece q + NP requested once
+// piece q is converted), each piece converted int8 → fp16 into one of two LDS buffers (K key-major, V transposed) and
+// multiplied while the later pieces are on their way; one barrier per piece (the buffer written for piece q + 2 was
+// last read for piece q, before the barrier of piece q + 1). Each wave runs its 16-query tiles over the piece with an online softmax in base 2.
 template <int HD, int TPW, bool RING, int NP>
 __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   constexpr int NC = HD / 32;    // 32-dim chunks (MFMA K steps of Sᵀ)
@@ -155,29 +155,30 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   // k1 − 1 (their scales are zeroed at the conversion and their scores masked). No load's value goes through a
   // select: the compiler would wait for that load before issuing the next piece's.
   PieceRegs pr[NP];
-  auto load_batch = [&](int kbase) {
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const int kb = kbase + PIECE * p;
-      if (tid < KITEMS) {
-        const int key = min(kb + tid / KPK, k1 - 1), col = (tid % KPK) * 16;
-        pr[p].k = *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + col);
-      }
-      if (tid < VITEMS) {
-        // 16 positions of one dim; a 32-slot block wholly past k1 reads the last one instead (its keys are masked and
-        // their scales zeroed at the conversion).
-        const int dim = tid / (PIECE / 16), pc = tid % (PIECE / 16), pos = kb + 16 * pc;
-        const int blk = min(pos & ~31, (k1 - 1) & ~31);
-        pr[p].v = *reinterpret_cast<const uint4*>(vh + size_t(dim) * a.vld + slot_of(blk) + (pos & 31));
-      }
-      if (tid < PIECE) {
-        const int key = min(kb + tid, k1 - 1);
-        pr[p].ks = ksh[slot_of(key)];
-        pr[p].vs = vsh[slot_of(key)];
-      }
+  auto load_piece = [&](PieceRegs& r, int q) {
+    const int kb = k0 + PIECE * q;
+    if (tid < KITEMS) {
+      const int key = min(kb + tid / KPK, k1 - 1), col = (tid % KPK) * 16;
+      r.k = *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + col);
+    }
+    if (tid < VITEMS) {
+      // 16 positions of one dim; a 32-slot block wholly past k1 reads the last one instead (its keys are masked and
+      // their scales zeroed at the conversion).
+      const int dim = tid / (PIECE / 16), pc = tid % (PIECE / 16), pos = kb + 16 * pc;
+      const int blk = min(pos & ~31, (k1 - 1) & ~31);
+      r.v = *reinterpret_cast<const uint4*>(vh + size_t(dim) * a.vld + slot_of(blk) + (pos & 31));
+    }
+    if (tid < PIECE) {
+      const int key = min(kb + tid, k1 - 1);
+      r.ks = ksh[slot_of(key)];
+      r.vs = vsh[slot_of(key)];
     }
   };
-  if (k0 < k1) load_batch(k0);
+  // A ring of NP pieces: piece q in pr[q mod NP], refilled with piece q + NP as soon as piece q is converted (a
+  // piece past the last re-reads the last one). The first piece lands without waiting for the whole split.
+  const int npieces = (k1 - k0 + PIECE - 1) / PIECE;  // ≥ 1 for every launched split
+#pragma unroll
+  for (int p = 0; p < NP; ++p) load_piece(pr[p], min(p, npieces - 1));
 
   // Query tiles of this wave: wave + 8·tt. With exactly 5 tiles (TPW = 1) the fifth is shared by waves 4-7, wave
   // 4 + h taking the 16-key sub-tile h of every piece, so that no SIMD carries two tiles; their four (max, sum, O)
@@ -401,22 +402,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 
   // Batches of NP pieces (one batch unless the split exceeds 64·NP keys). Pieces alternate between the two LDS
   // buffers; the barrier before a batch's loads keeps every wave's last reads of the batch before them.
-  int npc = 0;  // pieces processed so far (buffer parity)
-  for (int kbase = k0; kbase < k1; kbase += NP * PIECE) {
-    if (kbase != k0) {
-      __syncthreads();
-      load_batch(kbase);
-    }
+  for (int base = 0; base < npieces; base += NP) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      const int kb = kbase + PIECE * p;
-      if (kb >= k1) break;  // uniform: the split's last piece was p − 1
-      const int b = (npc + p) & 1;
+      const int q = base + p;
+      if (q >= npieces) break;  // uniform
+      const int kb = k0 + PIECE * q, b = q & 1;
       store(pr[p], b, kb);
+      load_piece(pr[p], min(q + NP, npieces - 1));
       __syncthreads();
       piece_products(b, kb, min(PIECE, k1 - kb));
     }
-    npc += NP;
   }
 
   // Tile 4's helper states merged into wave 4's (through the K staging buffer, free after the last piece): M = max
@@ -592,7 +588,12 @@ int launch_attention(ih_ctx* c, const AttnArgs& a) {
   const int Q = a.G * a.B;
   const int qtiles = (Q + 15) / 16;
   IH_CHECK(qtiles <= 16, IH_EINVAL, "attention: at most 256 query rows per KV head");
-  const int np = std::min(MAX_PIECES, (a.C + PIECE - 1) / PIECE);  // pieces per batch
+  // Ring depth: pieces in flight per thread (IH_ATTN_RING: tuning override).
+  static const int ring_np = [] {
+    const char* v = getenv("IH_ATTN_RING");
+    return v ? std::max(1, std::min(MAX_PIECES, atoi(v))) : 2;
+  }();
+  const int np = std::min(ring_np, (a.C + PIECE - 1) / PIECE);
   dim3 grid(a.nsplit, a.KVH);
   // Algorithmic bytes: the int8 K and V and their fp16 scales of every key the launched splits cover, and q.
   const double keys = double(a.P + a.B) - double(a.s0) * a.C;
