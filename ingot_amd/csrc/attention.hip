@@ -34,59 +34,75 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // AttnArgs: attn_args.h.
 
 // ---------------------------------------------------------------------------------------------------------------
-// Prework: grid (QH + 2·KVH, B), HD threads. vattn_prework_i8 (verify_attn_nax.metal:47-146) without QK-norm and gate
-// (the configurations have neither): RoPE on all HD dims (non-interleaved halves, angle pos·θ^(−i/(HD/2)) evaluated in
-// double once per step into the table a.rope), orthonormal WHT (Sylvester order, stages 1, 2, 4, …, then ×1/√HD) of q and k, int8 quantisation of k and v
+// Prework: vattn_prework_i8 (verify_attn_nax.metal:47-146) without QK-norm and gate (the configurations have neither):
+// RoPE on all HD dims (non-interleaved halves, angle pos·θ^(−i/(HD/2)) evaluated in double once per step into the
+// table a.rope), orthonormal WHT of q and k when hadk (Sylvester order: stages h = 1, 2, 4, …, HD/2 with
+// x[d] ← x[d] + x[d^h] where d & h = 0 and x[d^h] − x[d] where d & h ≠ 0, then ×1/√HD), int8 quantisation of k and v
 // per (token, head): sc = fp16(amax/127) (1 when amax = 0), q = clamp(rint(x/sc), ±127), written at slot P + t.
-__global__ void prework_kernel(AttnArgs a) {
-  __shared__ float xs[256];
-  __shared__ float red[4];
-  const int slot = blockIdx.x, t = blockIdx.y, d = threadIdx.x, HD = a.HD;
-  int col;
-  if (slot < a.QH) col = slot * HD + d;
-  else if (slot < a.QH + a.KVH) col = a.QH * HD + (slot - a.QH) * HD + d;
-  else col = (a.QH + a.KVH) * HD + (slot - a.QH - a.KVH) * HD + d;
-  float x = a.proj[size_t(t) * a.ldp + col];
-  const int pos = a.P + t;
-  const int kpos = a.ring ? pos % a.ring : pos;
-  if (slot < a.QH + a.KVH) {
-    xs[d] = x;
-    __syncthreads();
-    const int RH = HD / 2, i = d % RH;
-    const float2 cs_sn = a.rope[t * RH + i];  // (cos, sin) of pos·θ^(−i/RH), from the step's table
-    const float cs = cs_sn.x, sn = cs_sn.y;
-    x = d < RH ? x * cs - xs[d + RH] * sn : x * cs + xs[d - RH] * sn;
-    if (a.hadk) {
-      for (int h = 1; h < HD; h <<= 1) {
-        __syncthreads();
-        xs[d] = x;
-        __syncthreads();
-        const float o = xs[d ^ h];
-        x = (d & h) ? o - x : x + o;
-      }
-      x *= HD == 128 ? 0.088388347648318441f : (HD == 64 ? 0.125f : 0.0625f);
+// One wave per (head slot, token), lane l holding dims l + 64e: the RoPE partner of dim d is d ± HD/2 (the lane's
+// other value at HD 128, the lane 32 away at HD 64), WHT stages h < 64 are lane shuffles and h = 64 is in-lane — no
+// LDS, no barrier. Grid (ceil((QH + 2·KVH) / 4), B), 256 threads.
+template <int HD>
+__global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
+  constexpr int NE = HD / 64, RH = HD / 2;
+  const int slot = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y, lane = threadIdx.x & 63;
+  if (slot >= a.QH + 2 * a.KVH) return;  // wave-uniform
+  const bool isq = slot < a.QH, isk = !isq && slot < a.QH + a.KVH;
+  const float* row = a.proj + size_t(t) * a.ldp + size_t(slot) * HD;  // q heads | k heads | v heads
+  float x[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) x[e] = row[lane + 64 * e];
+  if (isq || isk) {
+    const float2 cs = a.rope[t * RH + (lane % RH)];
+    if constexpr (NE == 2) {
+      const float xl = x[0], xh = x[1];
+      x[0] = xl * cs.x - xh * cs.y;
+      x[1] = xh * cs.x + xl * cs.y;
+    } else {
+      const float o = __shfl_xor(x[0], RH);
+      x[0] = lane < RH ? x[0] * cs.x - o * cs.y : x[0] * cs.x + o * cs.y;
     }
-    if (slot < a.QH) {
+    if (a.hadk) {
+#pragma unroll
+      for (int h = 1; h < 64; h <<= 1)
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+          const float o = __shfl_xor(x[e], h);
+          x[e] = (lane & h) ? o - x[e] : x[e] + o;
+        }
+      if constexpr (NE == 2) {
+        const float x0 = x[0], x1 = x[1];
+        x[0] = x0 + x1;
+        x[1] = x0 - x1;
+      }
+#pragma unroll
+      for (int e = 0; e < NE; ++e) x[e] *= HD == 128 ? 0.088388347648318441f : 0.125f;
+    }
+    if (isq) {
       const int kvh = slot / a.G;
-      a.q[(size_t(kvh) * a.Qpad + t * a.G + slot % a.G) * HD + d] = __float2half_rn(x);
+      __half* q = a.q + (size_t(kvh) * a.Qpad + t * a.G + slot % a.G) * HD;
+#pragma unroll
+      for (int e = 0; e < NE; ++e) q[lane + 64 * e] = __float2half_rn(x[e]);
       return;
     }
   }
   // K or V: symmetric int8 with one fp16 scale per (token, head).
-  float am = fabsf(x);
+  float am = 0.f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) am = fmaxf(am, fabsf(x[e]));
   for (int o = 32; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-  if ((d & 63) == 0) red[d >> 6] = am;
-  __syncthreads();
-  float amax = red[0];
-  for (int w = 1; w < HD / 64; ++w) amax = fmaxf(amax, red[w]);
-  const __half sc16 = __float2half_rn(amax > 0.f ? amax / 127.0f : 1.0f);
+  const __half sc16 = __float2half_rn(am > 0.f ? am / 127.0f : 1.0f);
   const float sc = __half2float(sc16);
-  const int8_t qv = int8_t(fminf(127.f, fmaxf(-127.f, rintf(x / sc))));
-  const bool isk = slot < a.QH + a.KVH;
   const int h = isk ? slot - a.QH : slot - a.QH - a.KVH;
-  if (isk) a.kc[(size_t(h) * a.cap + kpos) * HD + d] = qv;
-  else a.vc[v_index(h, kpos, d, HD, a.vld)] = qv;
-  if (d == 0) (isk ? a.ks : a.vs)[size_t(h) * a.cap + kpos] = sc16;
+  const int pos = a.P + t, kpos = a.ring ? pos % a.ring : pos;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const int d = lane + 64 * e;
+    const int8_t qv = int8_t(fminf(127.f, fmaxf(-127.f, rintf(x[e] / sc))));
+    if (isk) a.kc[(size_t(h) * a.cap + kpos) * HD + d] = qv;
+    else a.vc[v_index(h, kpos, d, HD, a.vld)] = qv;
+  }
+  if (lane == 0) (isk ? a.ks : a.vs)[size_t(h) * a.cap + kpos] = sc16;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -567,8 +583,10 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __r
 int launch_prework(ih_ctx* c, const AttnArgs& a) {
   TimedLaunch tl(c, TC_PREWORK, double(a.B) * (a.QH + 2 * a.KVH) * a.HD * 4 + double(a.B) * a.KVH * (2 * a.HD + 4) +
                                     double(a.B) * a.QH * a.HD * 2);
-  dim3 grid(a.QH + 2 * a.KVH, a.B);
-  tlaunch(tl, prework_kernel, grid, dim3(a.HD), 0, c->stream, a);
+  dim3 grid((a.QH + 2 * a.KVH + 3) / 4, a.B);
+  if (a.HD == 128) tlaunch(tl, prework_kernel<128>, grid, dim3(256), 0, c->stream, a);
+  else if (a.HD == 64) tlaunch(tl, prework_kernel<64>, grid, dim3(256), 0, c->stream, a);
+  else return fail(IH_EINVAL, "attention prework: head_dim must be 64 or 128");
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
