@@ -494,7 +494,7 @@ static bool qmm_shape_ok(const QmmShape& sh, int Npad, int nkb) {
          sh.R * sh.kpw <= 64 && (Npad / 16) % sh.R == 0 && sh.ks * sh.KW * sh.kpw == nkb;
 }
 // The instantiated (R, KW, KPW) shapes (qmm_dispatch_mode lists the same set).
-static constexpr int kQmmShapes[][3] = {{1, 16, 2}, {2, 16, 2}, {2, 8, 4}, {4, 8, 4}, {4, 4, 8}, {7, 4, 8},
+static constexpr int kQmmShapes[][3] = {{1, 16, 2}, {2, 16, 2}, {2, 8, 4}, {4, 4, 8}, {4, 8, 4}, {7, 4, 8},
                                         {1, 8, 14}, {1, 14, 8}, {4, 4, 2}, {2, 8, 2}, {4, 8, 2}, {1, 1, 1},
                                         {2, 1, 1},  {4, 1, 1},  {7, 1, 1}};
 static QmmShape qmm_shape(int Npad, int nkb) {
