@@ -151,9 +151,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   constexpr int KR = krow<HD>();
   constexpr int KPK = HD / 16;   // K items per key
   constexpr int KITEMS = PIECE * KPK, VITEMS = HD * (PIECE / 16);
-  __shared__ _Float16 Kf[2][PIECE * KR];
-  __shared__ _Float16 Vt[2][HD * VROW];
-  __shared__ __attribute__((aligned(16))) float ksf[2][PIECE], vsf[2][PIECE];
+  // Four LDS buffers: with a ring of two, the pieces go in pairs (one barrier per pair, pairs alternating between
+  // buffers {0, 1} and {2, 3}); otherwise one piece per barrier through buffers 0 and 1.
+  constexpr int NBUF = NP == 2 ? 4 : 2;
+  __shared__ _Float16 Kf[NBUF][PIECE * KR];
+  __shared__ _Float16 Vt[NBUF][HD * VROW];
+  __shared__ __attribute__((aligned(16))) float ksf[NBUF][PIECE], vsf[NBUF][PIECE];
 
   const int sidx = blockIdx.x, split = sidx + a.s0, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
@@ -418,16 +421,34 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 
   // Batches of NP pieces (one batch unless the split exceeds 64·NP keys). Pieces alternate between the two LDS
   // buffers; the barrier before a batch's loads keeps every wave's last reads of the batch before them.
-  for (int base = 0; base < npieces; base += NP) {
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const int q = base + p;
-      if (q >= npieces) break;  // uniform
-      const int kb = k0 + PIECE * q, b = q & 1;
-      store(pr[p], b, kb);
-      load_piece(pr[p], min(q + NP, npieces - 1));
+  if constexpr (NP == 2) {
+    // Pairs of pieces: both converted (pair i into buffers 2(i mod 2) and 2(i mod 2) + 1, last read by pair i − 2,
+    // before the barrier of pair i − 1), one barrier, both multiplied.
+    for (int q = 0; q < npieces; q += 2) {
+      const bool two = q + 1 < npieces;  // uniform
+      const int b0 = q & 2, kb0 = k0 + PIECE * q, kb1 = kb0 + PIECE;
+      store(pr[0], b0, kb0);
+      load_piece(pr[0], min(q + 2, npieces - 1));
+      if (two) {
+        store(pr[1], b0 + 1, kb1);
+        load_piece(pr[1], min(q + 3, npieces - 1));
+      }
       __syncthreads();
-      piece_products(b, kb, min(PIECE, k1 - kb));
+      piece_products(b0, kb0, min(PIECE, k1 - kb0));
+      if (two) piece_products(b0 + 1, kb1, min(PIECE, k1 - kb1));
+    }
+  } else {
+    for (int base = 0; base < npieces; base += NP) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int q = base + p;
+        if (q >= npieces) break;  // uniform
+        const int kb = k0 + PIECE * q, b = q & 1;
+        store(pr[p], b, kb);
+        load_piece(pr[p], min(q + NP, npieces - 1));
+        __syncthreads();
+        piece_products(b, kb, min(PIECE, k1 - kb));
+      }
     }
   }
 
