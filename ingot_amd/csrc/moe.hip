@@ -288,99 +288,88 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
 // ---------------------------------------------------------------------------------------------------------------
 // Routing of the round (vmoe_route, verify.metal:160-319; RouterVector.reference, KernelCaseRouter.swift:54-80):
 // logits + router bias (NaN → −inf); top-k by value, ties to the lower expert index; weights = softmax over the chosen
-// logits, times an optional per-expert scale. Then the expert union by counting sort: entries (expert, first pair, pairs) in increasing expert order,
-// pairs in row order inside an expert; x_row[pair] = its row, pair_w[pair] = its weight, row_pair[row·k + slot] = its
-// pair. One workgroup of 256 threads (E ≤ 256, k ≤ 16, rows ≤ 32).
-__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int ldl, int rows, int E, int K,
-                                                        const float* __restrict__ bias, const float* __restrict__ pes,
-                                                        int* __restrict__ nent,
-                                                        int* __restrict__ entries, int* __restrict__ x_row,
-                                                        float* __restrict__ pair_w, int* __restrict__ row_pair) {
+// logits, times an optional per-expert scale. Then the expert union by counting sort: entries (expert, first pair,
+// pairs) in increasing expert order, pairs in row order inside an expert; x_row[pair] = its row, pair_w[pair] = its
+// weight, row_pair[row·k + slot] = its pair. One workgroup of 1024 threads (E ≤ 256, k ≤ 16, rows ≤ 32): a wave per
+// row for the top-k, a thread per (row, slot) pair and per expert for the rest — no step is serial over the block.
+__global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict__ logits, int ldl, int rows, int E,
+                                                         int K, const float* __restrict__ bias,
+                                                         const float* __restrict__ pes, int* __restrict__ nent,
+                                                         int* __restrict__ entries, int* __restrict__ x_row,
+                                                         float* __restrict__ pair_w, int* __restrict__ row_pair) {
+  __shared__ float lg[MAX_TOK][256];
   __shared__ int inds[MAX_TOK * 16];
-  __shared__ float wts[MAX_TOK * 16];
+  __shared__ float chosen[MAX_TOK * 16];
   __shared__ int cnt_s[256], start_s[256], slot_s[256];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int r = wave; r < rows; r += 4) {
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ex = lane + 64 * i;
-      float x = -INFINITY;
-      if (ex < E) {
-        x = logits[size_t(r) * ldl + ex] + (bias ? bias[ex] : 0.f);
-        if (x != x) x = -INFINITY;
-      }
-      v[i] = x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+  // Logits (+ router bias), NaN → −inf, one row per wave at a time.
+  for (int r = wave; r < rows; r += nw)
+    for (int ex = lane; ex < E; ex += 64) {
+      float x = logits[size_t(r) * ldl + ex] + (bias ? bias[ex] : 0.f);
+      lg[r][ex] = x != x ? -INFINITY : x;
     }
-    float chosen[16];
-    unsigned taken = 0;  // bit i: expert lane + 64·i already chosen
-    for (int k = 0; k < K; ++k) {
-      // Best untaken expert of this lane (value, then lower index), then of the wave. A −inf logit (or NaN) still
-      // ranks, so rows with fewer than k finite logits pick the lowest remaining indices.
-      float bv = -INFINITY;
-      int bi = 0x7FFFFFFF;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ex = lane + 64 * i;
-        if (ex < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && ex < bi))) {
-          bv = v[i];
-          bi = ex;
-        }
-      }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      chosen[k] = bv;
-      if (lane == 0) inds[r * K + k] = bi;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (lane + 64 * i == bi) taken |= 1u << i;
-    }
-    if (lane == 0) {
-      float sum = 0.f;
-      for (int k = 0; k < K; ++k) sum += expf(chosen[k] - chosen[0]);
-      for (int k = 0; k < K; ++k)
-        wts[r * K + k] = expf(chosen[k] - chosen[0]) / sum * (pes ? pes[inds[r * K + k]] : 1.0f);
-    }
-  }
   __syncthreads();
-  // Counting sort by expert: thread ex counts its pairs; exclusive scans give the first pair and the entry slot.
+  // Top-k by rank: expert e of row r takes slot rank(e) = #{e' : x[e'] > x[e] or (x[e'] = x[e] and e' < e)} when that
+  // is below k — the k successive "largest, then lowest index" picks (a −inf logit still ranks, so rows with fewer than
+  // k finite logits take the lowest remaining indices).
+  for (int r = wave; r < rows; r += nw)
+    for (int ex = lane; ex < E; ex += 64) {
+      const float v = lg[r][ex];
+      int rank = 0;
+      for (int e = 0; e < E; ++e) {
+        const float u = lg[r][e];
+        rank += (u > v || (u == v && e < ex)) ? 1 : 0;
+      }
+      if (rank < K) {
+        inds[r * K + rank] = ex;
+        chosen[r * K + rank] = v;
+      }
+    }
+  __syncthreads();
+  // Weights: softmax over the row's k chosen logits (summed in slot order from the largest), × the per-expert scale.
   const int nrk = rows * K;
+  float wgt = 0.f;
+  if (tid < nrk) {
+    const int r = tid / K, k = tid % K;
+    float sum = 0.f;
+    for (int kk = 0; kk < K; ++kk) sum += expf(chosen[r * K + kk] - chosen[r * K]);
+    wgt = expf(chosen[tid] - chosen[r * K]) / sum * (pes ? pes[inds[tid]] : 1.0f);
+    (void)k;
+  }
+  // Counting sort by expert: pairs per expert, then first pair and entry slot by exclusive scans (each thread scans the
+  // counts below its expert).
   int c = 0;
   if (tid < E)
     for (int i = 0; i < nrk; ++i) c += inds[i] == tid;
-  cnt_s[tid] = tid < E ? c : 0;
+  if (tid < 256) cnt_s[tid] = tid < E ? c : 0;
   __syncthreads();
-  if (tid == 0) {
+  if (tid < E) {
     int off = 0, slot = 0;
-    for (int ex = 0; ex < E; ++ex) {
-      start_s[ex] = off;
-      slot_s[ex] = slot;
-      off += cnt_s[ex];
-      slot += cnt_s[ex] > 0;
+    for (int e = 0; e < tid; ++e) {
+      off += cnt_s[e];
+      slot += cnt_s[e] > 0;
     }
-    nent[0] = slot;
+    start_s[tid] = off;
+    slot_s[tid] = slot;
+    if (tid == E - 1) nent[0] = slot + (c > 0);
   }
   __syncthreads();
   if (tid < E && c > 0) {
-    const int st = start_s[tid], sl = slot_s[tid];
+    const int sl = slot_s[tid];
     entries[3 * sl] = tid;
-    entries[3 * sl + 1] = st;
+    entries[3 * sl + 1] = start_s[tid];
     entries[3 * sl + 2] = c;
+  }
+  // Pair i (row-major (row, slot) order) of expert e goes to start[e] + #{i' < i : inds[i'] = e}: row order within
+  // the expert.
+  if (tid < nrk) {
+    const int e = inds[tid];
     int j = 0;
-    for (int i = 0; i < nrk; ++i)
-      if (inds[i] == tid) {
-        const int pr = st + j++;
-        x_row[pr] = i / K;
-        pair_w[pr] = wts[i];
-        row_pair[i] = pr;
-      }
+    for (int i = 0; i < tid; ++i) j += inds[i] == e;
+    const int pr = start_s[e] + j;
+    x_row[pr] = tid / K;
+    pair_w[pr] = wgt;
+    row_pair[tid] = pr;
   }
 }
 
@@ -449,7 +438,7 @@ int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, i
   IH_CHECK(E >= 1 && E <= 256 && K >= 1 && K <= 16 && K <= E && rows >= 1 && rows <= MAX_TOK, IH_EINVAL,
            "moe route: need E ≤ 256, 1 ≤ k ≤ min(16, E), 1 ≤ rows ≤ 32");
   TimedLaunch tl(c, TC_MOE, double(rows) * E * 4);
-  tlaunch(tl, moe_route_kernel, dim3(1), dim3(256), 0, c->stream, logits, ldl, rows, E, K, bias, pes, nent, entries,
+  tlaunch(tl, moe_route_kernel, dim3(1), dim3(1024), 0, c->stream, logits, ldl, rows, E, K, bias, pes, nent, entries,
           x_row, pair_w, row_pair);
   IH_HIP(hipGetLastError());
   return IH_OK;
