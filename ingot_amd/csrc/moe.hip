@@ -297,57 +297,99 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
                                                          const float* __restrict__ pes, int* __restrict__ nent,
                                                          int* __restrict__ entries, int* __restrict__ x_row,
                                                          float* __restrict__ pair_w, int* __restrict__ row_pair) {
-  __shared__ float lg[MAX_TOK][256];
-  __shared__ int inds[MAX_TOK * 16];
+  // Padded so every scan below reads 16 bytes at a time: logits past E are −inf (they rank after every expert and
+  // never change a rank: a tie with them goes to the lower index), indices past the pairs are −1, counts past E 0.
+  __shared__ __attribute__((aligned(16))) float lg[MAX_TOK][256];
+  __shared__ __attribute__((aligned(16))) int inds[MAX_TOK * 16];
   __shared__ float chosen[MAX_TOK * 16];
-  __shared__ int cnt_s[256], start_s[256], slot_s[256];
+  __shared__ __attribute__((aligned(16))) int cnt_s[256];
+  __shared__ int start_s[256], slot_s[256];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+  const int E4 = (E + 3) & ~3, nrk = rows * K, nrk4 = (nrk + 3) & ~3;
   // Logits (+ router bias), NaN → −inf, one row per wave at a time.
   for (int r = wave; r < rows; r += nw)
-    for (int ex = lane; ex < E; ex += 64) {
-      float x = logits[size_t(r) * ldl + ex] + (bias ? bias[ex] : 0.f);
-      lg[r][ex] = x != x ? -INFINITY : x;
+    for (int ex = lane; ex < E4; ex += 64) {
+      float x = -INFINITY;
+      if (ex < E) {
+        x = logits[size_t(r) * ldl + ex] + (bias ? bias[ex] : 0.f);
+        if (x != x) x = -INFINITY;
+      }
+      lg[r][ex] = x;
     }
+  if (tid < nrk4) inds[tid] = -1;
   __syncthreads();
-  // Top-k by rank: expert e of row r takes slot rank(e) = #{e' : x[e'] > x[e] or (x[e'] = x[e] and e' < e)} when that
-  // is below k — the k successive "largest, then lowest index" picks (a −inf logit still ranks, so rows with fewer than
-  // k finite logits take the lowest remaining indices).
-  for (int r = wave; r < rows; r += nw)
-    for (int ex = lane; ex < E; ex += 64) {
-      const float v = lg[r][ex];
-      int rank = 0;
-      for (int e = 0; e < E; ++e) {
-        const float u = lg[r][e];
-        rank += (u > v || (u == v && e < ex)) ? 1 : 0;
+  // Top-k: k rounds per row (one wave per row) of "largest logit, then lowest index" among the experts not yet chosen
+  // (a −inf logit still ranks, so rows with fewer than k finite logits take the lowest remaining indices): each lane's
+  // best untaken expert, then a butterfly over the wave.
+  for (int r = wave; r < rows; r += nw) {
+    constexpr int NE = 4;  // experts per lane (E ≤ 256)
+    float v[NE];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) v[i] = lane + 64 * i < E ? lg[r][lane + 64 * i] : -INFINITY;
+    unsigned taken = 0;  // bit i: expert lane + 64·i already chosen
+    for (int k = 0; k < K; ++k) {
+      float bv = -INFINITY;
+      int bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        const int ex = lane + 64 * i;
+        if (ex < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && ex < bi))) {
+          bv = v[i];
+          bi = ex;
+        }
       }
-      if (rank < K) {
-        inds[r * K + rank] = ex;
-        chosen[r * K + rank] = v;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
       }
+      if (lane == 0) {
+        inds[r * K + k] = bi;
+        chosen[r * K + k] = bv;
+      }
+#pragma unroll
+      for (int i = 0; i < NE; ++i)
+        if (lane + 64 * i == bi) taken |= 1u << i;
     }
+  }
   __syncthreads();
   // Weights: softmax over the row's k chosen logits (summed in slot order from the largest), × the per-expert scale.
-  const int nrk = rows * K;
   float wgt = 0.f;
   if (tid < nrk) {
-    const int r = tid / K, k = tid % K;
+    const int r = tid / K;
     float sum = 0.f;
     for (int kk = 0; kk < K; ++kk) sum += expf(chosen[r * K + kk] - chosen[r * K]);
     wgt = expf(chosen[tid] - chosen[r * K]) / sum * (pes ? pes[inds[tid]] : 1.0f);
-    (void)k;
   }
   // Counting sort by expert: pairs per expert, then first pair and entry slot by exclusive scans (each thread scans the
   // counts below its expert).
+  const int4* inds4 = reinterpret_cast<const int4*>(inds);
   int c = 0;
-  if (tid < E)
-    for (int i = 0; i < nrk; ++i) c += inds[i] == tid;
+  if (tid < E) {
+#pragma unroll 4
+    for (int i4 = 0; i4 < nrk4 / 4; ++i4) {
+      const int4 w = inds4[i4];
+      c += (w.x == tid) + (w.y == tid) + (w.z == tid) + (w.w == tid);
+    }
+  }
   if (tid < 256) cnt_s[tid] = tid < E ? c : 0;
   __syncthreads();
   if (tid < E) {
+    const int4* c4 = reinterpret_cast<const int4*>(cnt_s);
     int off = 0, slot = 0;
-    for (int e = 0; e < tid; ++e) {
-      off += cnt_s[e];
-      slot += cnt_s[e] > 0;
+    for (int e4 = 0; e4 < (tid + 3) / 4; ++e4) {
+      const int4 w = c4[e4];
+      const int ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (4 * e4 + q < tid) {
+          off += ww[q];
+          slot += ww[q] > 0;
+        }
     }
     start_s[tid] = off;
     slot_s[tid] = slot;
@@ -365,7 +407,11 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
   if (tid < nrk) {
     const int e = inds[tid];
     int j = 0;
-    for (int i = 0; i < tid; ++i) j += inds[i] == e;
+    for (int i4 = 0; i4 < (tid + 3) / 4; ++i4) {
+      const int4 w = inds4[i4];
+      j += (w.x == e && 4 * i4 < tid) + (w.y == e && 4 * i4 + 1 < tid) + (w.z == e && 4 * i4 + 2 < tid) +
+           (w.w == e && 4 * i4 + 3 < tid);
+    }
     const int pr = start_s[e] + j;
     x_row[pr] = tid / K;
     pair_w[pr] = wgt;
