@@ -290,70 +290,95 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
 // logits + router bias (NaN → −inf); top-k by value, ties to the lower expert index; weights = softmax over the chosen
 // logits, times an optional per-expert scale. Then the expert union by counting sort: entries (expert, first pair,
 // pairs) in increasing expert order, pairs in row order inside an expert; x_row[pair] = its row, pair_w[pair] = its
-// weight, row_pair[row·k + slot] = its pair. One workgroup of 1024 threads (E ≤ 256, k ≤ 16, rows ≤ 32): a wave per
-// row for the top-k, a thread per (row, slot) pair and per expert for the rest — no step is serial over the block.
+// weight, row_pair[row·k + slot] = its pair. One workgroup of 1024 threads (E ≤ 256, k ≤ 16, rows ≤ 32).
+//
+// The top-k takes k rounds of a 32-lane (value, index) reduction per row, lanes 0-31 and 32-63 of a wave holding two
+// rows, so the 16 waves cover every row at once; the reductions are register-to-register (DPP within 16 lanes, then
+// a swap of the two 16-lane rows). A row picks an expert at most once, so an expert's rows fit one 32-bit mask (rows
+// ≤ 32): its pair count is the mask's population and a pair's place among the expert's pairs is the population below
+// its row. The exclusive scans over experts (first pair, entry slot) come from wave ballots of the count's bits.
+namespace {
+// Partner value of a DPP lane pattern (all 64 lanes active).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(x, x, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ void best_step(float& v, int& i) {
+  const float ov = __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+  const int oi = dpp_i<CTRL>(i);
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+// (largest value, then lowest index) over each 32-lane half of the wave; every lane of the half ends with it.
+__device__ __forceinline__ void best32(float& v, int& i) {
+  best_step<0xB1>(v, i);   // quad_perm [1,0,3,2]
+  best_step<0x4E>(v, i);   // quad_perm [2,3,0,1]
+  best_step<0x141>(v, i);  // row_half_mirror
+  best_step<0x140>(v, i);  // row_mirror
+  // Rows 0↔1 and 2↔3: each lane gets its own value and its partner row's, in an order it cannot tell apart.
+  const auto sv = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const auto si = __builtin_amdgcn_permlane16_swap(unsigned(i), unsigned(i), false, false);
+  const float v0 = __uint_as_float(sv[0]), v1 = __uint_as_float(sv[1]);
+  const int i0 = int(si[0]), i1 = int(si[1]);
+  const bool one = v1 > v0 || (v1 == v0 && i1 < i0);
+  v = one ? v1 : v0;
+  i = one ? i1 : i0;
+}
+}  // namespace
+
 __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict__ logits, int ldl, int rows, int E,
                                                          int K, const float* __restrict__ bias,
                                                          const float* __restrict__ pes, int* __restrict__ nent,
                                                          int* __restrict__ entries, int* __restrict__ x_row,
                                                          float* __restrict__ pair_w, int* __restrict__ row_pair) {
-  // Padded so every scan below reads 16 bytes at a time: logits past E are −inf (they rank after every expert and
-  // never change a rank: a tie with them goes to the lower index), indices past the pairs are −1, counts past E 0.
-  __shared__ __attribute__((aligned(16))) float lg[MAX_TOK][256];
-  __shared__ __attribute__((aligned(16))) int inds[MAX_TOK * 16];
+  __shared__ float lg[MAX_TOK][256];
+  __shared__ int inds[MAX_TOK * 16];
   __shared__ float chosen[MAX_TOK * 16];
-  __shared__ __attribute__((aligned(16))) int cnt_s[256];
-  __shared__ int start_s[256], slot_s[256];
+  __shared__ unsigned rmask[256];  // bit r: row r chose the expert
+  __shared__ int lstart[256], lslot[256], wpairs[4], wslots[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
-  const int E4 = (E + 3) & ~3, nrk = rows * K, nrk4 = (nrk + 3) & ~3;
+  const int nrk = rows * K;
   // Logits (+ router bias), NaN → −inf, one row per wave at a time.
   for (int r = wave; r < rows; r += nw)
-    for (int ex = lane; ex < E4; ex += 64) {
-      float x = -INFINITY;
-      if (ex < E) {
-        x = logits[size_t(r) * ldl + ex] + (bias ? bias[ex] : 0.f);
-        if (x != x) x = -INFINITY;
-      }
-      lg[r][ex] = x;
+    for (int ex = lane; ex < E; ex += 64) {
+      float x = logits[size_t(r) * ldl + ex] + (bias ? bias[ex] : 0.f);
+      lg[r][ex] = x != x ? -INFINITY : x;
     }
-  if (tid < nrk4) inds[tid] = -1;
+  if (tid < 256) rmask[tid] = 0u;
   __syncthreads();
-  // Top-k: k rounds per row (one wave per row) of "largest logit, then lowest index" among the experts not yet chosen
-  // (a −inf logit still ranks, so rows with fewer than k finite logits take the lowest remaining indices): each lane's
-  // best untaken expert, then a butterfly over the wave.
-  for (int r = wave; r < rows; r += nw) {
-    constexpr int NE = 4;  // experts per lane (E ≤ 256)
+  // Top-k: k rounds of "largest logit, then lowest index" among the experts not yet chosen (a −inf logit still ranks,
+  // so a row with fewer than k finite logits takes the lowest remaining indices). Lane l of a half holds experts
+  // l + 32·i. Every lane runs every round (rows past the last repeat it and write nothing).
+  {
+    constexpr int NE = 8;
+    const int r = 2 * wave + (lane >> 5), hl = lane & 31, rr = min(r, rows - 1);
     float v[NE];
 #pragma unroll
-    for (int i = 0; i < NE; ++i) v[i] = lane + 64 * i < E ? lg[r][lane + 64 * i] : -INFINITY;
-    unsigned taken = 0;  // bit i: expert lane + 64·i already chosen
+    for (int i = 0; i < NE; ++i) v[i] = hl + 32 * i < E ? lg[rr][hl + 32 * i] : -INFINITY;
+    unsigned taken = 0;  // bit i: expert hl + 32·i already chosen
     for (int k = 0; k < K; ++k) {
       float bv = -INFINITY;
       int bi = 0x7FFFFFFF;
 #pragma unroll
       for (int i = 0; i < NE; ++i) {
-        const int ex = lane + 64 * i;
+        const int ex = hl + 32 * i;
         if (ex < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && ex < bi))) {
           bv = v[i];
           bi = ex;
         }
       }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      if (lane == 0) {
+      best32(bv, bi);
+      if (hl == 0 && r < rows) {
         inds[r * K + k] = bi;
         chosen[r * K + k] = bv;
+        atomicOr(&rmask[bi], 1u << r);
       }
 #pragma unroll
       for (int i = 0; i < NE; ++i)
-        if (lane + 64 * i == bi) taken |= 1u << i;
+        if (hl + 32 * i == bi) taken |= 1u << i;
     }
   }
   __syncthreads();
@@ -365,57 +390,47 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
     for (int kk = 0; kk < K; ++kk) sum += expf(chosen[r * K + kk] - chosen[r * K]);
     wgt = expf(chosen[tid] - chosen[r * K]) / sum * (pes ? pes[inds[tid]] : 1.0f);
   }
-  // Counting sort by expert: pairs per expert, then first pair and entry slot by exclusive scans (each thread scans the
-  // counts below its expert).
-  const int4* inds4 = reinterpret_cast<const int4*>(inds);
+  // Expert tid (waves 0-3): pairs c ≤ 32; the exclusive scans of c and of (c > 0) inside the wave from ballots of
+  // c's six bits, the wave totals through LDS.
   int c = 0;
-  if (tid < E) {
-#pragma unroll 4
-    for (int i4 = 0; i4 < nrk4 / 4; ++i4) {
-      const int4 w = inds4[i4];
-      c += (w.x == tid) + (w.y == tid) + (w.z == tid) + (w.w == tid);
-    }
-  }
-  if (tid < 256) cnt_s[tid] = tid < E ? c : 0;
-  __syncthreads();
-  if (tid < E) {
-    const int4* c4 = reinterpret_cast<const int4*>(cnt_s);
-    int off = 0, slot = 0;
-    for (int e4 = 0; e4 < (tid + 3) / 4; ++e4) {
-      const int4 w = c4[e4];
-      const int ww[4] = {w.x, w.y, w.z, w.w};
+  if (wave < 4) {
+    c = tid < E ? __popc(rmask[tid]) : 0;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    int off = 0, tot = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (4 * e4 + q < tid) {
-          off += ww[q];
-          slot += ww[q] > 0;
-        }
+    for (int bit = 0; bit < 6; ++bit) {
+      const unsigned long long m = __ballot((c >> bit) & 1);
+      off += __popcll(m & below) << bit;
+      tot += __popcll(m) << bit;
     }
-    start_s[tid] = off;
-    slot_s[tid] = slot;
-    if (tid == E - 1) nent[0] = slot + (c > 0);
+    const unsigned long long nz = __ballot(c > 0);
+    lstart[tid] = off;
+    lslot[tid] = __popcll(nz & below);
+    if (lane == 0) {
+      wpairs[wave] = tot;
+      wslots[wave] = __popcll(nz);
+    }
   }
   __syncthreads();
   if (tid < E && c > 0) {
-    const int sl = slot_s[tid];
+    int sl = lslot[tid], st = lstart[tid];
+    for (int w = 0; w < wave; ++w) {
+      sl += wslots[w];
+      st += wpairs[w];
+    }
     entries[3 * sl] = tid;
-    entries[3 * sl + 1] = start_s[tid];
+    entries[3 * sl + 1] = st;
     entries[3 * sl + 2] = c;
   }
-  // Pair i (row-major (row, slot) order) of expert e goes to start[e] + #{i' < i : inds[i'] = e}: row order within
-  // the expert.
+  if (tid == 0) nent[0] = (wslots[0] + wslots[1]) + (wslots[2] + wslots[3]);
+  // Pair (row r, slot) of expert e goes to first[e] + #{rows r' < r that chose e}.
   if (tid < nrk) {
-    const int e = inds[tid];
-    int j = 0;
-    for (int i4 = 0; i4 < (tid + 3) / 4; ++i4) {
-      const int4 w = inds4[i4];
-      j += (w.x == e && 4 * i4 < tid) + (w.y == e && 4 * i4 + 1 < tid) + (w.z == e && 4 * i4 + 2 < tid) +
-           (w.w == e && 4 * i4 + 3 < tid);
-    }
-    const int pr = start_s[e] + j;
-    x_row[pr] = tid / K;
-    pair_w[pr] = wgt;
-    row_pair[tid] = pr;
+    const int e = inds[tid], r = tid / K;
+    int st = lstart[e] + __popc(rmask[e] & ((1u << r) - 1u));
+    for (int w = 0; w < (e >> 6); ++w) st += wpairs[w];
+    x_row[st] = r;
+    pair_w[st] = wgt;
+    row_pair[tid] = st;
   }
 }
 
