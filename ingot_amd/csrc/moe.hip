@@ -437,36 +437,66 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
 // ---------------------------------------------------------------------------------------------------------------
 // Combine (vmoe_combine9, verify_nax.metal:527-540) fused with the residual and the next RMSNorm input: for row r,
 // y = Σ_slot w·o[pair(r, slot)] in slot order, h[r] += y, the next activation (h ⊙ nw, bf16 or fp16) and Σh² (one
-// partial per row). Grid (rows), 256 threads; one thread per 8 columns.
-__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ o, int ldo, const int* __restrict__ row_pair,
-                                                          const float* __restrict__ pair_w, int K, float* __restrict__ h,
-                                                          int ldh, int H, const uint16_t* __restrict__ nw,
-                                                          uint4* __restrict__ act, int act_nkb, int act_ntile,
-                                                          int act_f16, float* __restrict__ ss_out) {
-  __shared__ float red[4];
-  const int r = blockIdx.x;
+// partial per row). Grid (rows), one thread per 8 columns (up to 1024; a thread takes further chunks past that). The
+// row's pair numbers and weights are read once into LDS; h and o move 16 bytes at a time.
+__global__ __launch_bounds__(1024) void moe_combine_kernel(const float* __restrict__ o, int ldo,
+                                                           const int* __restrict__ row_pair,
+                                                           const float* __restrict__ pair_w, int K,
+                                                           float* __restrict__ h, int ldh, int H,
+                                                           const uint16_t* __restrict__ nw, uint4* __restrict__ act,
+                                                           int act_nkb, int act_ntile, int act_f16,
+                                                           float* __restrict__ ss_out) {
+  __shared__ float red[16];
+  __shared__ int prs[16];
+  __shared__ float ws[16];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  if (tid < K) {
+    const int pr = row_pair[r * K + tid];
+    prs[tid] = pr;
+    ws[tid] = pair_w[pr];
+  }
+  __syncthreads();
   float ss = 0.f;
-  for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
+  for (int c = tid; c < H / 8; c += blockDim.x) {
+    float4* hp = reinterpret_cast<float4*>(h + size_t(r) * ldh + 8 * c);
+    const float4 h0 = hp[0], h1 = hp[1];
+    float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int k = 0; k < K; ++k) {
+      const float w = ws[k];
+      const float4* op = reinterpret_cast<const float4*>(o + size_t(prs[k]) * ldo + 8 * c);
+      const float4 a = op[0], b = op[1];
+      y[0] += w * a.x;
+      y[1] += w * a.y;
+      y[2] += w * a.z;
+      y[3] += w * a.w;
+      y[4] += w * b.x;
+      y[5] += w * b.y;
+      y[6] += w * b.z;
+      y[7] += w * b.w;
+    }
+    const float hv[8] = {h0.x + y[0], h0.y + y[1], h0.z + y[2], h0.w + y[3],
+                         h1.x + y[4], h1.y + y[5], h1.z + y[6], h1.w + y[7]};
+    hp[0] = float4{hv[0], hv[1], hv[2], hv[3]};
+    hp[1] = float4{hv[4], hv[5], hv[6], hv[7]};
+    const uint4 nv = reinterpret_cast<const uint4*>(nw)[c];
+    const unsigned nwu[4] = {nv.x, nv.y, nv.z, nv.w};
     float v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int col = 8 * c + j;
-      float y = 0.f;
-      for (int k = 0; k < K; ++k) {
-        const int pr = row_pair[r * K + k];
-        y += pair_w[pr] * o[size_t(pr) * ldo + col];
-      }
-      const float hv = h[size_t(r) * ldh + col] + y;
-      h[size_t(r) * ldh + col] = hv;
-      ss += hv * hv;
-      v[j] = hv * bf16f(nw[col]);
+      ss += hv[j] * hv[j];
+      v[j] = hv[j] * bf16f(uint16_t(nwu[j >> 1] >> (16 * (j & 1))));
     }
     frag_store(act_f16 != 0, act, act_nkb, act_ntile, r, c, v);
   }
   for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
-  if (threadIdx.x == 0) ss_out[size_t(r) * SS_CAP] = (red[0] + red[1]) + (red[2] + red[3]);
+  if (tid == 0) {
+    float t = 0.f;
+    for (int w = 0; w < int(blockDim.x >> 6); ++w) t += red[w];
+    ss_out[size_t(r) * SS_CAP] = t;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -509,7 +539,11 @@ int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, 
                        float* h, int H, const uint16_t* nw, ActBuf& act) {
   IH_CHECK(H % 8 == 0, IH_EINVAL, "moe combine: hidden size must be a multiple of 8");
   TimedLaunch tl(c, TC_MOE, double(rows) * H * (4.0 * K + 8 + 2));
-  tlaunch(tl, moe_combine_kernel, dim3(rows), dim3(256), 0, c->stream, o, ldo, row_pair, pair_w, K, h, H, H, nw,
+  IH_CHECK(ldo % 4 == 0 && K <= 16 && reinterpret_cast<uintptr_t>(o) % 16 == 0 &&
+               reinterpret_cast<uintptr_t>(h) % 16 == 0 && reinterpret_cast<uintptr_t>(nw) % 16 == 0,
+           IH_EINVAL, "moe combine: o, h and the norm weights must be 16-byte aligned, k ≤ 16");
+  const int threads = std::min(1024, (H / 8 + 63) / 64 * 64);
+  tlaunch(tl, moe_combine_kernel, dim3(rows), dim3(threads), 0, c->stream, o, ldo, row_pair, pair_w, K, h, H, H, nw,
           static_cast<uint4*>(act.frag), act.nkb, act.ntile, act.f16 ? 1 : 0, act.ss);
   IH_HIP(hipGetLastError());
   act.nss = 1;
