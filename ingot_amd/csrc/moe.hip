@@ -298,37 +298,41 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
 // ≤ 32): its pair count is the mask's population and a pair's place among the expert's pairs is the population below
 // its row. The exclusive scans over experts (first pair, entry slot) come from wave ballots of the count's bits.
 namespace {
-// Partner value of a DPP lane pattern (all 64 lanes active).
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int x) {
-  return __builtin_amdgcn_update_dpp(x, x, CTRL, 0xF, 0xF, false);
+// Top-k key: the logit in the high word, mapped so that unsigned order is float order (−0 taken as +0; −inf maps
+// above 0, so 0 means "taken"), and ~expert in the low word, so that the larger key is the larger logit, then the
+// lower expert.
+__device__ __forceinline__ unsigned long long topk_key(float x, int ex) {
+  const unsigned b = __float_as_uint(x == 0.f ? 0.f : x);
+  const unsigned u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (static_cast<unsigned long long>(u) << 32) | unsigned(~ex);
 }
-template <int CTRL>
-__device__ __forceinline__ void best_step(float& v, int& i) {
-  const float ov = __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
-  const int oi = dpp_i<CTRL>(i);
-  if (ov > v || (ov == v && oi < i)) {
-    v = ov;
-    i = oi;
-  }
+__device__ __forceinline__ float topk_value(unsigned long long k) {
+  const unsigned u = unsigned(k >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
 }
-// (largest value, then lowest index) over each 32-lane half of the wave; every lane of the half ends with it.
-__device__ __forceinline__ void best32(float& v, int& i) {
-  best_step<0xB1>(v, i);   // quad_perm [1,0,3,2]
-  best_step<0x4E>(v, i);   // quad_perm [2,3,0,1]
-  best_step<0x141>(v, i);  // row_half_mirror
-  best_step<0x140>(v, i);  // row_mirror
-  // Rows 0↔1 and 2↔3: each lane gets its own value and its partner row's, in an order it cannot tell apart.
-  const auto sv = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  const auto si = __builtin_amdgcn_permlane16_swap(unsigned(i), unsigned(i), false, false);
-  const float v0 = __uint_as_float(sv[0]), v1 = __uint_as_float(sv[1]);
-  const int i0 = int(si[0]), i1 = int(si[1]);
-  const bool one = v1 > v0 || (v1 == v0 && i1 < i0);
-  v = one ? v1 : v0;
-  i = one ? i1 : i0;
+__device__ __forceinline__ unsigned long long kmax(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+// Partner key of a DPP lane pattern (all 64 lanes active).
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_k(unsigned long long k) {
+  const int lo = __builtin_amdgcn_update_dpp(int(unsigned(k)), int(unsigned(k)), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(int(unsigned(k >> 32)), int(unsigned(k >> 32)), CTRL, 0xF, 0xF, false);
+  return (static_cast<unsigned long long>(unsigned(hi)) << 32) | unsigned(lo);
+}
+// Largest key over each 32-lane half of the wave; every lane of the half ends with it.
+__device__ __forceinline__ unsigned long long best32(unsigned long long k) {
+  k = kmax(k, dpp_k<0xB1>(k));   // quad_perm [1,0,3,2]
+  k = kmax(k, dpp_k<0x4E>(k));   // quad_perm [2,3,0,1]
+  k = kmax(k, dpp_k<0x141>(k));  // row_half_mirror
+  k = kmax(k, dpp_k<0x140>(k));  // row_mirror
+  // Rows 0↔1 and 2↔3: each lane gets its own key and its partner row's, in an order it cannot tell apart.
+  const auto lo = __builtin_amdgcn_permlane16_swap(unsigned(k), unsigned(k), false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap(unsigned(k >> 32), unsigned(k >> 32), false, false);
+  return kmax((static_cast<unsigned long long>(hi[0]) << 32) | lo[0],
+              (static_cast<unsigned long long>(hi[1]) << 32) | lo[1]);
 }
 }  // namespace
 
+template <int NE>
 __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict__ logits, int ldl, int rows, int E,
                                                          int K, const float* __restrict__ bias,
                                                          const float* __restrict__ pes, int* __restrict__ nent,
@@ -351,34 +355,27 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
   __syncthreads();
   // Top-k: k rounds of "largest logit, then lowest index" among the experts not yet chosen (a −inf logit still ranks,
   // so a row with fewer than k finite logits takes the lowest remaining indices). Lane l of a half holds experts
-  // l + 32·i. Every lane runs every round (rows past the last repeat it and write nothing).
-  {
-    constexpr int NE = 8;
+  // l + 32·i (NE of them: E ≤ 32·NE). Both halves of a wave run every round (a row past the last repeats the last
+  // row and writes nothing); waves past the rows skip it.
+  if (2 * wave < rows) {
     const int r = 2 * wave + (lane >> 5), hl = lane & 31, rr = min(r, rows - 1);
-    float v[NE];
+    unsigned long long key[NE];  // 0: out of range or already chosen
 #pragma unroll
-    for (int i = 0; i < NE; ++i) v[i] = hl + 32 * i < E ? lg[rr][hl + 32 * i] : -INFINITY;
-    unsigned taken = 0;  // bit i: expert hl + 32·i already chosen
+    for (int i = 0; i < NE; ++i) key[i] = hl + 32 * i < E ? topk_key(lg[rr][hl + 32 * i], hl + 32 * i) : 0ull;
     for (int k = 0; k < K; ++k) {
-      float bv = -INFINITY;
-      int bi = 0x7FFFFFFF;
+      unsigned long long bk = key[0];
 #pragma unroll
-      for (int i = 0; i < NE; ++i) {
-        const int ex = hl + 32 * i;
-        if (ex < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && ex < bi))) {
-          bv = v[i];
-          bi = ex;
-        }
-      }
-      best32(bv, bi);
+      for (int i = 1; i < NE; ++i) bk = kmax(bk, key[i]);
+      bk = best32(bk);
+      const int bi = int(~unsigned(bk));
       if (hl == 0 && r < rows) {
         inds[r * K + k] = bi;
-        chosen[r * K + k] = bv;
+        chosen[r * K + k] = topk_value(bk);
         atomicOr(&rmask[bi], 1u << r);
       }
 #pragma unroll
       for (int i = 0; i < NE; ++i)
-        if (hl + 32 * i == bi) taken |= 1u << i;
+        if (hl + 32 * i == bi) key[i] = 0ull;
     }
   }
   __syncthreads();
@@ -529,7 +526,8 @@ int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, i
   IH_CHECK(E >= 1 && E <= 256 && K >= 1 && K <= 16 && K <= E && rows >= 1 && rows <= MAX_TOK, IH_EINVAL,
            "moe route: need E ≤ 256, 1 ≤ k ≤ min(16, E), 1 ≤ rows ≤ 32");
   TimedLaunch tl(c, TC_MOE, double(rows) * E * 4);
-  tlaunch(tl, moe_route_kernel, dim3(1), dim3(1024), 0, c->stream, logits, ldl, rows, E, K, bias, pes, nent, entries,
+  auto kern = E <= 128 ? moe_route_kernel<4> : moe_route_kernel<8>;
+  tlaunch(tl, kern, dim3(1), dim3(1024), 0, c->stream, logits, ldl, rows, E, K, bias, pes, nent, entries,
           x_row, pair_w, row_pair);
   IH_HIP(hipGetLastError());
   return IH_OK;
