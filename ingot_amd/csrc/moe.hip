@@ -550,6 +550,16 @@ int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, 
 
 // The model's MoE launches. Router: logits fp32 [rows][ldl] = r · (x · Wᵀ) (one dense slot).
 int launch_moe_router(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, float eps, float* logits, int ldl) {
+  // An int4 router runs on the dense qmm, whose workgroups split K across waves (the matrix is a few hundred KB:
+  // one memory round trip instead of a walk over its K-blocks).
+  if (W->format == QF_INT4 && W->E == 1) {
+    QmmEpilogue ep;
+    ep.mode = QM_F32_SCALE;
+    ep.y = logits;
+    ep.ldy = ldl;
+    ep.eps = eps;
+    return launch_qmm_ex(c, W, 0, x, rows, ep);
+  }
   GatherParams p{};
   p.xa = static_cast<const uint4*>(x.frag);
   p.x_nkb = x.nkb;
