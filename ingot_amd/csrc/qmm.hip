@@ -263,14 +263,16 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   for (int j = 0; j < NSB; ++j) {
     const int e = j * 64 + lane, r = e / (nk * 8), i = (e >> 3) % nk;
     const unsigned off = (unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kb0 + i)) * 128u + unsigned(e & 7) * 16u;
-    vsb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, e < nsb ? off : OOB, 0, 0));
+    const bool in = e < nsb && kb0 + i < p.nkb;  // K-blocks past the matrix: zero scale and bias, no contribution
+    vsb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, in ? off : OOB, 0, 0));
   }
   if constexpr (X16) {
 #pragma unroll
     for (int j = 0; j < N16; ++j) {
       const int e = j * 64 + lane, i = e >> 4, t = (e >> 2) & 3, q = e & 3;
       const unsigned off = unsigned(kb0 + i) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * q;
-      v16[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, i < nk ? off : OOB, 0, 0));
+      v16[j] = __builtin_bit_cast(u32x4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(rx, i < nk && kb0 + i < p.nkb ? off : OOB, 0, 0));
     }
   }
 
@@ -283,6 +285,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   u32x4 wv[D][R], xv[D][T][4];
   // One ring stage: the weight tiles and x of K-block kb. Every offset that depends on kb is a scalar.
   auto load_stage = [&](int d, int kb) {
+    kb = kb < p.nkb ? kb : p.nkb - 1;  // a ragged last wave re-reads the last K-block; its scales are zero
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int tt = 0; tt < T; ++tt)
@@ -486,17 +489,21 @@ __global__ __launch_bounds__(256) void qmm_finish_kernel(QmmParams p) {
 
 // Launch shape for an (Npad, nkb) matrix: R row tiles per wave, KW waves per workgroup, ring depth D, kpw K-blocks per
 // wave, and ks = nkb / (KW·kpw) workgroups splitting K. Chosen from the shape only, never from M, so each row's
-// summation order is fixed. The K range must tile exactly (ks·KW·kpw = nkb, kpw a multiple of D): every load of the
-// ring stays inside the matrix.
+// summation order is fixed. The K range tiles exactly (ks·KW·kpw = nkb, kpw a multiple of D), or, in one split, the
+// last wave runs past the end by less than its kpw: its K-blocks past the matrix re-stream the last block (clamped,
+// so every load stays inside the matrix) with zero scale and bias words, which add exactly nothing.
 struct QmmShape { int R, KW, D, kpw, ks; };
+constexpr int qmm_ring_depth(int kpw) { return kpw % 2 == 0 ? 2 : kpw <= 3 ? kpw : 1; }
 static bool qmm_shape_ok(const QmmShape& sh, int Npad, int nkb) {
+  const int span = sh.KW * sh.kpw;
   return sh.R >= 1 && sh.KW >= 1 && sh.D >= 1 && sh.kpw >= sh.D && sh.kpw % sh.D == 0 && sh.kpw <= 32 &&
-         sh.R * sh.kpw <= 64 && (Npad / 16) % sh.R == 0 && sh.ks * sh.KW * sh.kpw == nkb;
+         sh.R * sh.kpw <= 64 && (Npad / 16) % sh.R == 0 &&
+         (sh.ks * span == nkb || (sh.ks == 1 && span > nkb && span - nkb < sh.kpw));
 }
 // The instantiated (R, KW, KPW) shapes (qmm_dispatch_mode lists the same set).
 static constexpr int kQmmShapes[][3] = {{1, 16, 2}, {2, 16, 2}, {2, 8, 4}, {4, 4, 8}, {4, 8, 4}, {7, 4, 8},
                                         {1, 8, 14}, {1, 14, 8}, {4, 4, 2}, {2, 8, 2}, {4, 8, 2}, {1, 1, 1},
-                                        {2, 1, 1},  {4, 1, 1},  {7, 1, 1}};
+                                        {2, 1, 1},  {4, 1, 1},  {7, 1, 1},  {2, 8, 3},  {4, 8, 3}};
 static QmmShape qmm_shape(int Npad, int nkb) {
   const int NT = Npad / 16;
   // Rows: R tiles per wave share x, and the workgroup count NT / R should be about one round over the 256 CUs (a
@@ -515,12 +522,20 @@ static QmmShape qmm_shape(int Npad, int nkb) {
         if (c[0] != R || c[1] == 1) continue;
         const int span = c[1] * c[2];
         if (nkb % span) continue;
-        const QmmShape sh{R, c[1], c[2] % 2 ? 1 : 2, c[2], nkb / span};
+        const QmmShape sh{R, c[1], qmm_ring_depth(c[2]), c[2], nkb / span};
         if ((pass == 0 && sh.ks != 1) || !qmm_shape_ok(sh, Npad, nkb)) continue;
         return sh;
       }
     }
-  // K-block counts without a fitting factor: one wave per workgroup, one K-block per wave.
+  // K-block counts without a fitting factor: one split whose last wave runs past the end by less than its kpw.
+  for (int R : rp)
+    if (R)
+      for (const auto& c : kQmmShapes) {
+        if (c[0] != R || c[1] == 1) continue;
+        const QmmShape sh{R, c[1], qmm_ring_depth(c[2]), c[2], 1};
+        if (c[1] * c[2] > nkb && qmm_shape_ok(sh, Npad, nkb)) return sh;
+      }
+  // Otherwise one wave per workgroup, one K-block per wave.
   for (int R : rp)
     if (R && (Npad / 16) % R == 0) return QmmShape{R, 1, 1, 1, nkb};
   return QmmShape{1, 1, 1, 1, nkb};
@@ -532,7 +547,7 @@ constexpr bool qmm_fits() {
              (X16 ? KW * KPW * 512 : 0) <= 128 * 1024;
 }
 
-// Instantiated launch shapes (R, KW, KPW; D = 2 when KPW is even) for each epilogue. Epilogues are compile-time:
+// Instantiated launch shapes (R, KW, KPW; ring depth qmm_ring_depth(KPW)) for each epilogue. Epilogues are compile-time:
 // the code of every mode in one kernel raised its register demand past the ring's (302 VGPRs at R = 7, KW = 4).
 // The kernel-level modes (QM_F32, QM_F32_ADD, QM_BF16) run as QM_PART + qmm_finish_kernel.
 template <int T, bool X16, int MODE>
@@ -540,15 +555,15 @@ static bool qmm_dispatch_mode(const TimedLaunch& tl, QmmShape sh, dim3 grid, hip
 #define IH_QMM_CASE(R_, KW_, KPW_)                                                                          \
   if constexpr (qmm_fits<T, R_, KW_, X16, KPW_>()) {                                                        \
     if (sh.R == R_ && sh.KW == KW_ && sh.kpw == KPW_) {                                                     \
-      tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, (KPW_ % 2 ? 1 : 2), KPW_, MODE>, grid, dim3(64 * KW_), 0, \
+      tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, qmm_ring_depth(KPW_), KPW_, MODE>, grid, dim3(64 * KW_), 0, \
               st, p);                                                                                       \
       return true;                                                                                          \
     }                                                                                                       \
   }
-  // K = 4096 (32 K-blocks); K = 14336 (112); K = 2048 (16); and the one-wave fallback.
+  // K = 4096 (32 K-blocks); K = 14336 (112); K = 2048 (16); K = 2880 (23, ragged); and the one-wave fallback.
   IH_QMM_CASE(1, 16, 2) IH_QMM_CASE(2, 16, 2) IH_QMM_CASE(2, 8, 4) IH_QMM_CASE(4, 8, 4) IH_QMM_CASE(4, 4, 8)
   IH_QMM_CASE(7, 4, 8) IH_QMM_CASE(1, 14, 8) IH_QMM_CASE(1, 8, 14) IH_QMM_CASE(4, 4, 2) IH_QMM_CASE(2, 8, 2)
-  IH_QMM_CASE(4, 8, 2) IH_QMM_CASE(1, 1, 1) IH_QMM_CASE(2, 1, 1) IH_QMM_CASE(4, 1, 1) IH_QMM_CASE(7, 1, 1)
+  IH_QMM_CASE(4, 8, 2) IH_QMM_CASE(2, 8, 3) IH_QMM_CASE(4, 8, 3) IH_QMM_CASE(1, 1, 1) IH_QMM_CASE(2, 1, 1) IH_QMM_CASE(4, 1, 1) IH_QMM_CASE(7, 1, 1)
 #undef IH_QMM_CASE
   return false;  // not an instantiated shape
 }
@@ -601,7 +616,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   QmmShape sh = qmm_shape(W->Npad, W->nkb);
   // Tuning overrides: IH_QMM_SHAPE = "R,KW,kpw" for every matrix, IH_QMM_SHAPES = "N:K=R,KW,kpw;…" per matrix.
   auto apply = [&](int R, int KW, int kpw) {
-    sh = QmmShape{R, KW, kpw % 2 ? 1 : 2, kpw, W->nkb / std::max(1, KW * kpw)};
+    sh = QmmShape{R, KW, qmm_ring_depth(kpw), kpw, std::max(1, W->nkb / std::max(1, KW * kpw))};
   };
   int oR, oKW, okpw;
   if (const char* ov = getenv("IH_QMM_SHAPE"))
