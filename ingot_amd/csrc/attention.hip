@@ -34,14 +34,59 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // AttnArgs: attn_args.h.
 
 // ---------------------------------------------------------------------------------------------------------------
+// x of lane (lane ^ H) without an LDS round trip (every lane of the wave active), from lane patterns that are their
+// own inverse: DPP quad permutations and row mirrors within 16-lane rows (xor 4 = half-row mirror i ^ 7, then quad
+// reversal i ^ 3; xor 8 = row mirror i ^ 15, then half-row mirror), the gfx950 row swaps for 16 and 32, which leave a
+// lane its own value in one result and its partner's in the other (the partner's is the one that is not the lane's
+// own bits; if both are, they are equal).
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int b) {
+  return __builtin_amdgcn_update_dpp(b, b, CTRL, 0xF, 0xF, false);
+}
+template <int H>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int b = __float_as_int(v);
+  if constexpr (H == 1) {
+    return __int_as_float(dpp_mov<0xB1>(b));  // quad_perm [1,0,3,2]
+  } else if constexpr (H == 2) {
+    return __int_as_float(dpp_mov<0x4E>(b));  // quad_perm [2,3,0,1]
+  } else if constexpr (H == 4) {
+    return __int_as_float(dpp_mov<0x1B>(dpp_mov<0x141>(b)));  // row_half_mirror, then quad_perm [3,2,1,0]
+  } else if constexpr (H == 8) {
+    return __int_as_float(dpp_mov<0x141>(dpp_mov<0x140>(b)));  // row_mirror, then row_half_mirror
+  } else {
+    static_assert(H == 16 || H == 32, "lane_xor: H is a power of two below 64");
+    unsigned p0, p1;
+    if constexpr (H == 16) {
+      const auto sw = __builtin_amdgcn_permlane16_swap(unsigned(b), unsigned(b), false, false);
+      p0 = sw[0];
+      p1 = sw[1];
+    } else {
+      const auto sw = __builtin_amdgcn_permlane32_swap(unsigned(b), unsigned(b), false, false);
+      p0 = sw[0];
+      p1 = sw[1];
+    }
+    return __uint_as_float(p0 == unsigned(b) ? p1 : p0);
+  }
+}
+// One Walsh–Hadamard butterfly stage over lanes at distance H.
+template <int H, int NE>
+__device__ __forceinline__ void wht_stage(float (&x)[NE], int lane) {
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const float o = lane_xor<H>(x[e]);
+    x[e] = (lane & H) ? o - x[e] : x[e] + o;
+  }
+}
+
 // Prework: vattn_prework_i8 (verify_attn_nax.metal:47-146) without QK-norm and gate (the configurations have neither):
 // RoPE on all HD dims (non-interleaved halves, angle pos·θ^(−i/(HD/2)) evaluated in double once per step into the
 // table a.rope), orthonormal WHT of q and k when hadk (Sylvester order: stages h = 1, 2, 4, …, HD/2 with
 // x[d] ← x[d] + x[d^h] where d & h = 0 and x[d^h] − x[d] where d & h ≠ 0, then ×1/√HD), int8 quantisation of k and v
 // per (token, head): sc = fp16(amax/127) (1 when amax = 0), q = clamp(rint(x/sc), ±127), written at slot P + t.
 // One wave per (head slot, token), lane l holding dims l + 64e: the RoPE partner of dim d is d ± HD/2 (the lane's
-// other value at HD 128, the lane 32 away at HD 64), WHT stages h < 64 are lane shuffles and h = 64 is in-lane — no
-// LDS, no barrier. Grid (ceil((QH + 2·KVH) / 4), B), 256 threads.
+// other value at HD 128, the lane 32 away at HD 64), WHT stages h < 64 are lane exchanges (lane_xor) and h = 64 is
+// in-lane — no LDS, no barrier. Grid (ceil((QH + 2·KVH) / 4), B), 256 threads.
 template <int HD>
 __global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
   constexpr int NE = HD / 64, RH = HD / 2;
@@ -59,17 +104,16 @@ __global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
       x[0] = xl * cs.x - xh * cs.y;
       x[1] = xh * cs.x + xl * cs.y;
     } else {
-      const float o = __shfl_xor(x[0], RH);
+      const float o = lane_xor<RH>(x[0]);
       x[0] = lane < RH ? x[0] * cs.x - o * cs.y : x[0] * cs.x + o * cs.y;
     }
     if (a.hadk) {
-#pragma unroll
-      for (int h = 1; h < 64; h <<= 1)
-#pragma unroll
-        for (int e = 0; e < NE; ++e) {
-          const float o = __shfl_xor(x[e], h);
-          x[e] = (lane & h) ? o - x[e] : x[e] + o;
-        }
+      wht_stage<1>(x, lane);
+      wht_stage<2>(x, lane);
+      wht_stage<4>(x, lane);
+      wht_stage<8>(x, lane);
+      wht_stage<16>(x, lane);
+      wht_stage<32>(x, lane);
       if constexpr (NE == 2) {
         const float x0 = x[0], x1 = x[1];
         x[0] = x0 + x1;
@@ -90,7 +134,12 @@ __global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
   float am = 0.f;
 #pragma unroll
   for (int e = 0; e < NE; ++e) am = fmaxf(am, fabsf(x[e]));
-  for (int o = 32; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+  am = fmaxf(am, lane_xor<32>(am));
+  am = fmaxf(am, lane_xor<16>(am));
+  am = fmaxf(am, lane_xor<8>(am));
+  am = fmaxf(am, lane_xor<4>(am));
+  am = fmaxf(am, lane_xor<2>(am));
+  am = fmaxf(am, lane_xor<1>(am));
   const __half sc16 = __float2half_rn(am > 0.f ? am / 127.0f : 1.0f);
   const float sc = __half2float(sc16);
   const int h = isk ? slot - a.QH : slot - a.QH - a.KVH;
