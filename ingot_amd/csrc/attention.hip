@@ -630,19 +630,22 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __r
     M = Mb;
   }
   // Merge the split groups (lanes dg + DG·sg): butterfly over sg, fixed order.
-#pragma unroll
-  for (int x = DG; x < 64; x <<= 1) {
-    const float Mo = __shfl_xor(M, x), Lo = __shfl_xor(L, x);
+  auto merge = [&](auto xc) {
+    constexpr int X = decltype(xc)::value;
+    const float Mo = lane_xor<X>(M), Lo = lane_xor<X>(L);
     const float Mn = fmaxf(M, Mo);
     const float ca = M == -INFINITY ? 0.f : exp2f(M - Mn), cb = Mo == -INFINITY ? 0.f : exp2f(Mo - Mn);
     L = L * ca + Lo * cb;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float oo = __shfl_xor(o[e], x);
+      const float oo = lane_xor<X>(o[e]);
       o[e] = o[e] * ca + oo * cb;
     }
     M = Mn;
-  }
+  };
+  if constexpr (DG <= 8) merge(std::integral_constant<int, 8>{});
+  merge(std::integral_constant<int, 16>{});
+  merge(std::integral_constant<int, 32>{});
   if (sg != 0) return;
   const float inv = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
