@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
+#include "lanes.h"
+
 namespace ih {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -92,8 +94,12 @@ __device__ __forceinline__ void rms_finish(const RmsPrefetch<NR>& pf, const floa
       ss += j + 2 < nss ? v[2] : 0.f;
       ss += j + 3 < nss ? v[3] : 0.f;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    ss += lane_xor<32>(ss);
+    ss += lane_xor<16>(ss);
+    ss += lane_xor<8>(ss);
+    ss += lane_xor<4>(ss);
+    ss += lane_xor<2>(ss);
+    ss += lane_xor<1>(ss);
     if (lane == 0) rsc[wave + k * nwaves] = 1.0f / sqrtf(ss / float(D) + eps);
   }
 }
