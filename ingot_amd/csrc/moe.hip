@@ -486,7 +486,12 @@ __global__ __launch_bounds__(1024) void moe_combine_kernel(const float* __restri
     }
     frag_store(act_f16 != 0, act, act_nkb, act_ntile, r, c, v);
   }
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  ss += lane_xor<32>(ss);
+  ss += lane_xor<16>(ss);
+  ss += lane_xor<8>(ss);
+  ss += lane_xor<4>(ss);
+  ss += lane_xor<2>(ss);
+  ss += lane_xor<1>(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   if (tid == 0) {
