@@ -45,6 +45,7 @@ def run_qmm(ctx, W, xb, M, out_mode=0, y0=None):
         (17, 1000, 2880, 6),     # K % 128 == 64 (config 4 hidden), N not a multiple of 16
         (17, 5120, 2880, 9),     # 23 K-blocks in one split of 8 waves × 3: the last wave's third block is past K
         (5, 32768, 2880, 10),    # the same with 4 row tiles per wave (vocabulary-sized N)
+        (32, 512, 2880, 12),     # the same with two 16-token tiles (M = 32)
         (3, 4096, 14336, 7),     # down projection K
     ],
 )
