@@ -76,8 +76,8 @@ def main() -> int:
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the verify step shards "
-              "across GPUs only by design, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (sharding the verify step "
+              "across GPUs is designed, not built)", file=sys.stderr)
         return 2
 
     from ingot_amd._lib import Context, HipEvents, KVCache, Model, ModelDesc, check, lib
