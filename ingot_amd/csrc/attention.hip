@@ -176,7 +176,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   const int sidx = blockIdx.x, split = sidx + a.s0, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
   const int Q = a.G * a.B;
-  const int k0 = split * a.C, k1 = min(k0 + a.C, a.P + a.B);
+  // Keys [k0, k1) of the split. In a sliding-window layer every row's window starts at or after P − window + 1, so
+  // the split starts there (rounded down to 64 keys, which keeps pieces and the 32-slot V blocks aligned): the keys
+  // before it are masked for every row and add nothing.
+  const int k1 = min(split * a.C + a.C, a.P + a.B);
+  const int k0 = a.window > 0 ? max(split * a.C, (a.P - a.window + 1) & ~63) : split * a.C;
 
   const int8_t* kh = a.kc + size_t(kvh) * a.cap * HD;
   const int8_t* vh = a.vc + size_t(kvh) * HD * a.vld;

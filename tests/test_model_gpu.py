@@ -111,11 +111,13 @@ def test_moe_two_layers_within_routing_sensitivity(ctx):
             m.free()
 
 
-@pytest.mark.parametrize("shape", [SMALL, GQA8, GQA4], ids=["gqa2-hd128", "gqa8-hd64", "gqa4-hd128"])
+@pytest.mark.parametrize("shape", [SMALL, GQA8, GQA4, SWA], ids=["gqa2-hd128", "gqa8-hd64", "gqa4-hd128", "swa16-sinks"])
 @pytest.mark.parametrize("chunk", [32, 96, 1024, 0])
 def test_verify_step_long_context_chunks(ctx, shape, chunk):
     """P = 1500 with key chunks of 32 (48 splits, half-filled 64-key pieces), 96 (16 splits, a partial last piece per
-    split), 1024 (16 pieces per split through the ring) and automatic: the same oracle tolerance. A row whose oracle
+    split), 1024 (16 pieces per split through the ring) and automatic: the same oracle tolerance. In the sliding-window
+    shape (window 16, sinks) the split holding the window starts at the window rounded down to 64 keys (1472 with
+    the 1024-key chunk), not at the split's first key. A row whose oracle
     logits are themselves ill-conditioned (an int8 or bf16 rounding tie on the way: a one-part-in-10^7 change of RoPE θ
     moves them by more than 0.05) is held to the tolerance plus 5 × that measured movement instead; the GQA4 shape's
     token set at the automatic chunk has two such rows (0.11 and 0.07 under the perturbation)."""
