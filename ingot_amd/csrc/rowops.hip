@@ -1,6 +1,7 @@
 // Row kernels of the verify round: embedding gather, RMSNorm into the qmm activation layout, the gated activation,
 // vocab-wide argmax and greedy acceptance.
 #include "act.h"
+#include "lanes.h"
 #include "ih_internal.h"
 
 namespace ih {
@@ -42,7 +43,12 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
     }
     frag_store_chunk(frag, nkb, ntile, row, c, v);
   }
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  ss += lane_xor<32>(ss);
+  ss += lane_xor<16>(ss);
+  ss += lane_xor<8>(ss);
+  ss += lane_xor<4>(ss);
+  ss += lane_xor<2>(ss);
+  ss += lane_xor<1>(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   if (threadIdx.x == 0) ss_out[size_t(row) * SS_CAP] = ((red[0] + red[1]) + (red[2] + red[3]));
@@ -58,6 +64,22 @@ constexpr int ARGMAX_CHUNKS = 16;
 // (v, i) beats (m, mi): larger value, or equal value and lower index; NaN never beats.
 __device__ __forceinline__ bool am_better(float v, uint32_t i, float m, uint32_t mi) {
   return v > m || (v == m && i < mi);
+}
+
+// (value, index) maximum over the wave under am_better, partners at distance 32, 16, …, 1 (every lane active).
+__device__ __forceinline__ void am_butterfly(float& m, uint32_t& mi) {
+  auto step = [&](auto hc) {
+    constexpr int H = decltype(hc)::value;
+    const float om = lane_xor<H>(m);
+    const uint32_t oi = __float_as_uint(lane_xor<H>(__uint_as_float(mi)));
+    if (am_better(om, oi, m, mi)) { m = om; mi = oi; }
+  };
+  step(std::integral_constant<int, 32>{});
+  step(std::integral_constant<int, 16>{});
+  step(std::integral_constant<int, 8>{});
+  step(std::integral_constant<int, 4>{});
+  step(std::integral_constant<int, 2>{});
+  step(std::integral_constant<int, 1>{});
 }
 
 __global__ __launch_bounds__(256) void argmax_chunk_kernel(const float* __restrict__ x, int ldx, int N,
@@ -97,11 +119,7 @@ __global__ __launch_bounds__(256) void argmax_chunk_kernel(const float* __restri
     const float v = xr[i];
     if (am_better(v, uint32_t(i), m, mi)) { m = v; mi = uint32_t(i); }
   }
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float om = __shfl_xor(m, o);
-    const uint32_t oi = __shfl_xor(mi, o);
-    if (am_better(om, oi, m, mi)) { m = om; mi = oi; }
-  }
+  am_butterfly(m, mi);
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { bv[wave] = m; bi[wave] = mi; }
   __syncthreads();
@@ -123,11 +141,7 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float2* __restri
     m = p.x;
     mi = __float_as_uint(p.y);
   }
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float om = __shfl_xor(m, o);
-    const uint32_t oi = __shfl_xor(mi, o);
-    if (am_better(om, oi, m, mi)) { m = om; mi = oi; }
-  }
+  am_butterfly(m, mi);
   if (l == 0) out[row] = mi == 0xFFFFFFFFu ? 0u : mi;  // all NaN / −inf: index 0, as the reference
 }
 
