@@ -180,7 +180,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   // the split starts there (rounded down to 64 keys, which keeps pieces and the 32-slot V blocks aligned): the keys
   // before it are masked for every row and add nothing.
   const int k1 = min(split * a.C + a.C, a.P + a.B);
-  const int k0 = a.window > 0 ? max(split * a.C, (a.P - a.window + 1) & ~63) : split * a.C;
+  // The skip is a whole number of 64-key pieces counted from the split's own start, so the pieces (and the order in
+  // which the online softmax meets the keys) are the same for every P: a row's bits do not depend on the block.
+  const int k0 = a.window > 0 ? split * a.C + (max(0, a.P - a.window + 1 - split * a.C) & ~63) : split * a.C;
 
   const int8_t* kh = a.kc + size_t(kvh) * a.cap * HD;
   const int8_t* vh = a.vc + size_t(kvh) * HD * a.vld;
@@ -554,15 +556,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 template <int HD>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb, int ntile) {
   constexpr int DG = HD / 8, SG = 64 / DG, NB = 8;
+  static_assert(DG == 8 || DG == 16, "the split-group merge below runs the stages 8/16/32 of HD 64 and 128");
   const int t = blockIdx.x, h = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int dg = lane % DG, sg = lane / DG;
   const int kvh = h / a.G, m = t * a.G + h % a.G;
-  // The sink is a split with weight e^(sink−M) and no value.
   float M = -INFINITY, L = 0.f;
-  if (sg == 0 && a.sinks) {
-    M = a.sinks[h] * 1.4426950408889634f;
-    L = 1.f;
-  }
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
@@ -617,6 +615,16 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __r
   merge(std::integral_constant<int, 16>{});
   merge(std::integral_constant<int, 32>{});
   if (sg != 0) return;
+  // The sink is a last split with weight e^(sink−M) and no value, merged after the splits' tree so that its place
+  // does not depend on which split a window starts in (the same bits for a row whatever the block's P).
+  if (a.sinks) {
+    const float ms = a.sinks[h] * 1.4426950408889634f;
+    const float Mn = fmaxf(M, ms);
+    const float ca = M == -INFINITY ? 0.f : exp2f(M - Mn);
+    L = L * ca + exp2f(ms - Mn);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= ca;
+  }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] *= inv;

@@ -61,9 +61,10 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
 // merges the chunks in order.
 constexpr int ARGMAX_CHUNKS = 16;
 
-// (v, i) beats (m, mi): larger value, or equal value and lower index; NaN never beats.
+// (v, i) beats (m, mi): larger value, or equal value and lower index. NaN never beats, and −inf never takes an index
+// (the reference scans from (−inf, 0) with a strict >, so a row of −inf and NaN gives index 0).
 __device__ __forceinline__ bool am_better(float v, uint32_t i, float m, uint32_t mi) {
-  return v > m || (v == m && i < mi);
+  return v > m || (v == m && i < mi && v != -INFINITY);
 }
 
 // (value, index) maximum over the wave under am_better, partners at distance 32, 16, …, 1 (every lane active).
@@ -151,7 +152,8 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float2* __restri
 // P += m + 1 (the commit), anchor = top1[m], vtok[0] = anchor. spec_accept, Shaders/yy_model.metal:616-642.
 __global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  const uint32_t nr = rows ? uint32_t(rows) : st[6];
+  // Rows from the round state (rows = 0) are clamped to 1…IH_MAX_ROWS: vtok, top1 and a record hold at most that many.
+  const uint32_t nr = rows ? uint32_t(rows) : min(max(st[6], 1u), uint32_t(IH_MAX_ROWS));
   uint32_t m = 0;
   while (m + 1 < nr && vtok[m + 1] == top1[m]) ++m;
   uint32_t* r = rec + (st[5] % uint32_t(ring)) * IH_REC_STRIDE;
