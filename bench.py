@@ -12,8 +12,10 @@ then the config-1 model at 32K positions), 3 (48-layer MoE, 128 experts top-8, i
 32 experts top-4, sinks, alternating 128-token sliding window, B = 9, 64K).
 
 Printed: one JSON line (the driver's contract) with `roofline` (the dominant kernel class, from HIP events on the
-library's stream) and `cpu_baseline` (the C++ oracle on the host, same workload, one full step; configuration 1 only by
-default, since the MoE models take tens of GB of host memory in the oracle's fp32 path).
+library's stream) and `cpu_baseline` (the C++ oracle on the host, same workload and block: median of 5 full steps after a
+warm-up, with the GPU's top-1 and logits on that block compared against the oracle's; configuration 1 only by default).
+With the default configuration the same line also carries side measurements: `config0_qmm_accept` (config 0's single
+qmm and acceptance) and `other_configs` (configurations 2, 3 and 4, ten timed steps each).
 
 Synthetic weights and KV (seeded, counter-based SplitMix64; the reference's checkpoints are not available).
 """
@@ -70,6 +72,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-baseline", action="store_true", help="also for the non-default configurations")
     ap.add_argument("--no-kernel-profile", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the side measurements (config 0's qmm, the other configurations' step times)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only copy BYTES device-to-device 4 times (the reference kernel that scales the HBM counters)")
     args = ap.parse_args()
@@ -80,19 +84,46 @@ def main() -> int:
               "across GPUs is designed, not built)", file=sys.stderr)
         return 2
 
-    from ingot_amd._lib import Context, HipEvents, KVCache, Model, ModelDesc, check, lib
+    from ingot_amd._lib import Context
 
-    cfg = CONFIGS[args.config]
+    ctx = Context(0)
+    want_cpu = not args.no_cpu_baseline and (args.config == "dense8b-8k" or args.cpu_baseline)
+    out = run_config(ctx, args.config, args.steps, args.warmup, profile=not args.no_kernel_profile, cpu=want_cpu)
+    if not args.no_extra and args.config == "dense8b-8k":
+        # Side measurements in the same run (not the headline `value`): config 0's single qmm, and the step time of
+        # every other configuration (fewer steps each).
+        out["config0_qmm_accept"] = config0(ctx)
+        others = {}
+        for name in CONFIGS:
+            if name == args.config:
+                continue
+            r = run_config(ctx, name, 10, 2, profile=True, cpu=False)
+            keep = ("ms_per_step", "value", "step_hbm_gbs", "step_roofline_frac", "step_algorithmic_bytes",
+                    "moe_distinct_experts_per_layer", "moe_experts_iid_routing", "copy_lookup", "accepted_equals_planted",
+                    "step_bytes_iid_routing", "step_roofline_frac_iid_routing")
+            others[name] = {k: r[k] for k in keep if k in r}
+            others[name]["workload"] = r["config"]["workload"]
+            others[name]["kernels_ms_per_step"] = {k: v["ms_per_step"] for k, v in r["kernels"].items()}
+        out["other_configs"] = others
+    print(json.dumps(out), flush=True)
+    ctx.close()
+    return 0
+
+
+def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bool) -> dict:
+    """Builds one configuration's model and cache, times `steps` verify rounds and returns the JSON line's fields."""
+    from ingot_amd._lib import HipEvents, KVCache, Model, ModelDesc, check, lib
+
+    cfg = CONFIGS[config]
     d = cfg["desc"]
     P, B = cfg["P"], cfg["B"]
     k = B - 1
-    ctx = Context(0)
     desc = ModelDesc.make(**d)
     t0 = time.time()
     model = Model(ctx, desc, SEED)
     kv = KVCache(model, P + 2 * B)
     kv.fill_synthetic(P, KV_SEED)
-    log(f"[bench] model {args.config} built in {time.time() - t0:.1f}s; weights {model.weight_bytes / 1e9:.3f} GB, "
+    log(f"[bench] model {config} built in {time.time() - t0:.1f}s; weights {model.weight_bytes / 1e9:.3f} GB, "
         f"key chunk {kv.chunk}")
 
     d_vtok = ctx.buffer(B * 4)
@@ -101,6 +132,7 @@ def main() -> int:
     RING = 64
     d_rec = ctx.buffer(RING * 24 * 4).fill(0)
     copy_n = cfg.get("copy")
+    bufs = [d_vtok, d_top1, d_st, d_rec]
 
     if copy_n:
         # Config 2: the copy drafter proposes from the context; the verify block is written on the device.
@@ -110,8 +142,8 @@ def main() -> int:
         hist, _ = zipf_context(SEED, n=copy_n, vocab=d["vocab"])
         d_hist = ctx.to_device(hist)
         d_copy = ctx.buffer((4 + k) * 4)
+        bufs += [d_hist, d_copy]
         blocks = None
-        planted = None
 
         def step(i: int) -> None:
             check(lib().ih_copy_lookup_dev(ctx.handle, d_hist.ptr, copy_n, k, 3, 64, d_copy.ptr, d_vtok.ptr, B))
@@ -135,6 +167,7 @@ def main() -> int:
                 blk += list(rng.integers(0, d["vocab"], size=B - len(blk)))
             blocks[L] = blk
         d_blocks = ctx.to_device(blocks)
+        bufs.append(d_blocks)
         log(f"[bench] greedy chain: {chain}")
         # MoE: the synthetic greedy chain repeats tokens, and identical rows route identically; the timed blocks carry
         # distinct random drafts (the routing of real draft text), and the planted blocks are checked in an untimed
@@ -144,6 +177,7 @@ def main() -> int:
             rnd = blocks.copy()
             rnd[:, 1:] = rng.integers(0, d["vocab"], size=(k + 1, B - 1))
             d_timed = ctx.to_device(rnd)
+            bufs.append(d_timed)
 
         def one(src, L):
             check(lib().ih_memcpy_dtod(ctx.handle, d_vtok.ptr, src.ptr + L * B * 4, B * 4))
@@ -154,19 +188,20 @@ def main() -> int:
         def step(i: int) -> None:
             one(d_timed, i % (k + 1))
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     ctx.sync()
     d_st.upload(np.zeros(8, np.uint32))
     ev = HipEvents(ctx, 2)
     ctx.sync()
     ev.record(0)
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     ev.record(1)
     ms_total = ev.elapsed_ms(0, 1)
     ctx.sync()
-    ms = ms_total / args.steps
+    ev.close()
+    ms = ms_total / steps
     # MoE: distinct experts per layer of the last timed step (the bytes actually streamed).
     U = None
     if d.get("n_experts"):
@@ -180,7 +215,7 @@ def main() -> int:
             one(d_blocks, i)
         ctx.sync()
     rec = d_rec.download(np.uint32, (RING, 24))
-    nrec = k + 1 if (blocks is not None and d.get("n_experts")) else min(args.steps, RING)
+    nrec = k + 1 if (blocks is not None and d.get("n_experts")) else min(steps, RING)
     accepted = [int(rec[i % RING][0]) for i in range(nrec)]
     if blocks is not None:
         planted = [i % (k + 1) for i in range(nrec)]
@@ -194,9 +229,9 @@ def main() -> int:
 
     # Per-kernel-class timing in a second, instrumented pass of the same steps.
     classes = {}
-    if not args.no_kernel_profile:
+    if profile:
         check(lib().ih_timing_enable(ctx.handle, 1))
-        for i in range(args.steps):
+        for i in range(steps):
             step(i)
         ctx.sync()
         names = ["qmm", "attention", "attn_prework", "attn_reduce", "rows", "argmax", "moe", "other", "qmm_finish"]
@@ -206,8 +241,8 @@ def main() -> int:
             by = C.c_double()
             check(lib().ih_timing_read(ctx.handle, c, C.byref(t), C.byref(cnt), C.byref(by)))
             if cnt.value:
-                classes[n] = dict(ms_per_step=t.value / args.steps, launches_per_step=cnt.value / args.steps,
-                                  gbs=by.value / (t.value * 1e6), bytes_per_step=by.value / args.steps)
+                classes[n] = dict(ms_per_step=t.value / steps, launches_per_step=cnt.value / steps,
+                                  gbs=by.value / (t.value * 1e6), bytes_per_step=by.value / steps)
         check(lib().ih_timing_enable(ctx.handle, 0))
 
     # Algorithmic bytes of one step: weights actually read (MLX formats; MoE: the routed experts), the KV of every
@@ -215,11 +250,14 @@ def main() -> int:
     L_, H, KVH, HD = d["n_layers"], d["hidden"], d["n_kv_heads"], d["head_dim"]
     per_expert = 0.0
     weight_bytes = float(model.weight_bytes)
+    iid = None
     if d.get("n_experts"):
         IE, E = d["expert_intermediate"], d["n_experts"]
         bpw = 0.5625 if d.get("expert_format", 0) == 0 else 0.53125
         per_expert = 3 * IE * H * bpw
-        weight_bytes = weight_bytes - L_ * E * per_expert + sum(U) * per_expert
+        dense_part = weight_bytes - L_ * E * per_expert
+        weight_bytes = dense_part + sum(U) * per_expert
+        iid = moe_iid_timing(ctx, d, B)
     kv_bytes = 0.0
     for l in range(L_):
         keys = P + B
@@ -244,13 +282,13 @@ def main() -> int:
                         kernel={"qmm": "qmm_int4", "moe": "qmm_gather (MoE experts)", "attention": "attn"}[dom],
                         avg_launch_us=round(q["ms_per_step"] / q["launches_per_step"] * 1e3, 2),
                         bytes_per_launch=round(by / q["launches_per_step"]))
-        traffic = _traffic(args.config, dom)
+        traffic = _traffic(config, dom)
         if traffic is not None:
             roofline["traffic"] = traffic
 
-    cpu = None
-    if not args.no_cpu_baseline and (args.config == "dense8b-8k" or args.cpu_baseline):
-        cpu = cpu_baseline(desc, P, blocks[k] if blocks is not None else np.full(B, ANCHOR, np.uint32))
+    cpu_res = None
+    if cpu:
+        cpu_res = cpu_baseline(desc, P, blocks[k] if blocks is not None else np.full(B, ANCHOR, np.uint32), kv)
 
     model_name = (f"synthetic {d['n_layers']}L h{d['hidden']} {d['n_q_heads']}q/{d['n_kv_heads']}kv hd{d['head_dim']} "
                   + (f"E{d['n_experts']} top-{d['top_k']} I{d['expert_intermediate']} "
@@ -261,8 +299,8 @@ def main() -> int:
         "value": round(tok_s, 1),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms, 4),
         "us_per_step": round(ms * 1e3, 1),
         "higher_is_better": True,
@@ -279,19 +317,94 @@ def main() -> int:
         "step_algorithmic_bytes": round(step_bytes),
         "kernels": {n: {kk: round(vv, 3) for kk, vv in v.items()} for n, v in classes.items()},
         "roofline": roofline,
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_res,
     }
     if U is not None:
         out["moe_distinct_experts_per_layer"] = {"mean": round(float(np.mean(U)), 2), "min": min(U), "max": max(U)}
+        out["moe_experts_iid_routing"] = iid
+        # The step's bytes had the router seen i.i.d. N(0,1) logits (U from that routing), at this step's time.
+        iid_bytes = step_bytes - sum(U) * per_expert + L_ * iid["U"] * per_expert
+        out["step_bytes_iid_routing"] = round(iid_bytes)
+        out["step_roofline_frac_iid_routing"] = round(iid_bytes / (ms * 1e6) / HBM_PEAK_GBS, 4)
     if copy_n:
         out["copy_lookup"] = copy_lookup_timing(ctx, lib, check, d_hist, copy_n, k, d_copy, d_vtok, B)
-    if d.get("n_experts"):
-        out["moe_experts_iid_routing"] = moe_iid_timing(ctx, d, B)
-    print(json.dumps(out), flush=True)
+    for b in bufs:
+        b.free()
     kv.free()
     model.free()
-    ctx.close()
-    return 0
+    return out
+
+
+def config0(ctx) -> dict:
+    """Config 0: one verify-step qmm, X bf16 [8, 4096] · int4 g64 W [4096, 4096] (codes uniform, scale |N(0, 0.02)|,
+    bias −8·scale), bf16 out, then argmax over logits [8, 32000] and the acceptance of 7 drafts. GB/s of the
+    algorithmic 9,568,256 bytes, for a single launch (synchronised before and after) and for 64 back-to-back calls."""
+    from ingot_amd._lib import HipEvents, QMat, check, lib
+
+    def bf16(a):
+        u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    g = np.random.default_rng(SEED)
+    N = K = 4096
+    M = 8
+    q = g.integers(0, 2**32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
+    sb = bf16(np.abs(g.normal(0, 0.02, size=(N, K // 64))))
+    bb = bf16(-8 * (sb.astype(np.uint32) << 16).view(np.float32))
+    W = QMat.int4(ctx, q, sb, bb)
+    x = ctx.to_device(bf16(g.normal(0, 1, size=(M, K))))
+    y = ctx.buffer(M * N * 2)
+    algo = 9568256
+    ev = HipEvents(ctx, 2)
+    check(lib().ih_timing_enable(ctx.handle, 1))
+    single = []
+    for _ in range(20):
+        ctx.sync()
+        ev.record(0)
+        check(lib().ih_qmm_int4(ctx.handle, W.handle, x.ptr, K, M, y.ptr, N, 2))
+        ev.record(1)
+        single.append(ev.elapsed_ms(0, 1))
+    ctx.sync()
+    t = C.c_double()
+    cnt = C.c_int()
+    by = C.c_double()
+    check(lib().ih_timing_read(ctx.handle, 0, C.byref(t), C.byref(cnt), C.byref(by)))
+    kernel_us = t.value / cnt.value * 1e3
+    check(lib().ih_timing_enable(ctx.handle, 0))
+    ctx.sync()
+    ev.record(0)
+    for _ in range(64):
+        check(lib().ih_qmm_int4(ctx.handle, W.handle, x.ptr, K, M, y.ptr, N, 2))
+    ev.record(1)
+    b2b_us = ev.elapsed_ms(0, 1) / 64 * 1e3
+    # Acceptance over [8, 32000] N(0,1) logits, drafts 1..3 forced to the argmax of rows 0..2.
+    logits = g.normal(0, 1, size=(8, 32000)).astype(np.float32)
+    top = np.argmax(logits, axis=1).astype(np.uint32)
+    vtok = g.integers(0, 32000, size=8).astype(np.uint32)
+    vtok[1:4] = top[:3]
+    dl, dt, dv = ctx.to_device(logits), ctx.buffer(8 * 4), ctx.to_device(vtok)
+    d_st, d_rec = ctx.to_device(np.zeros(8, np.uint32)), ctx.buffer(24 * 4)
+    ctx.sync()
+    ev.record(0)
+    reps = 50
+    for _ in range(reps):
+        check(lib().ih_argmax_rows(ctx.handle, dl.ptr, 8, 32000, dt.ptr))
+        check(lib().ih_spec_accept_dev(ctx.handle, d_st.ptr, dv.ptr, dt.ptr, d_rec.ptr, 1, 8))
+    ev.record(1)
+    acc_us = ev.elapsed_ms(0, 1) / reps * 1e3
+    m = int(d_rec.download(np.uint32, (24,))[0])
+    gpu_top = dt.download(np.uint32, (8,))
+    ev.close()
+    for b in (x, y, dl, dt, dv, d_st, d_rec):
+        b.free()
+    W.free()
+    return {"qmm_single_call_us": round(float(np.median(single)) * 1e3, 2),
+            "qmm_kernel_us": round(kernel_us, 2), "qmm_kernel_gbs": round(algo / (kernel_us * 1e3), 1),
+            "qmm_back_to_back_us": round(b2b_us, 2), "qmm_back_to_back_gbs": round(algo / (b2b_us * 1e3), 1),
+            "qmm_algorithmic_bytes": algo,
+            "note": "a call = bf16 rows to the activation layout + the qmm launch",
+            "argmax_accept_us": round(acc_us, 2), "accepted_m": m,
+            "argmax_equal": bool(np.array_equal(gpu_top, top))}
 
 
 def _traffic(config: str, dom: str):
@@ -401,9 +514,21 @@ def copy_calibration(nbytes: int) -> int:
     return 0
 
 
-def cpu_baseline(desc, P: int, tokens) -> dict | None:
-    """The C++ oracle (fp32 dequant + matmul) on the host: the full model with resident weights, one verify step of
-    the same block at the same P; tok/s as for the GPU (mean accepted + 1 over L = 0…k → (k + 2) / 2 tokens)."""
+def cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(desc, P: int, tokens, kv) -> dict | None:
+    """The C++ oracle (fp32 dequant + matmul) on the host: the full model with resident weights, verify steps of the
+    same block at the same P — one warm-up, then the median of 5 timed steps; tok/s as for the GPU (mean accepted + 1
+    over L = 0…k → (k + 2) / 2 tokens). The same block on the GPU (ih_verify_step) is compared with the oracle's:
+    top-1 equality, rows whose oracle top-2 margin is inside twice the logit error, max-abs and cosine of the logits."""
     try:
         import oracle
     except Exception as e:  # noqa: BLE001
@@ -412,17 +537,32 @@ def cpu_baseline(desc, P: int, tokens) -> dict | None:
     t0 = time.time()
     m = oracle.OracleModel(desc, SEED, KV_SEED, P)
     t1 = time.time()
-    m.verify(tokens)
-    t2 = time.time()
+    ref_logits, ref_top1 = m.verify(tokens)  # warm-up
+    times = []
+    for _ in range(5):
+        a = time.time()
+        m.verify(tokens)
+        times.append(time.time() - a)
     m.free()
-    step_s = t2 - t1
+    step_s = float(np.median(times))
+    top1, logits = kv.verify(tokens, want_logits=True)
+    err = float(np.abs(logits - ref_logits).max())
+    a64, b64 = logits.astype(np.float64).ravel(), ref_logits.astype(np.float64).ravel()
+    cos = float(a64 @ b64 / (np.linalg.norm(a64) * np.linalg.norm(b64)))
+    srt = np.sort(ref_logits, axis=1)
+    near = (srt[:, -1] - srt[:, -2]) <= 2 * err
     k = len(tokens) - 1
     mean_tokens = (k + 2) / 2.0
-    log(f"[bench] cpu baseline: model built in {t1 - t0:.1f}s, one step {step_s:.2f}s")
+    log(f"[bench] cpu baseline: model built in {t1 - t0:.1f}s, steps {[round(t, 2) for t in times]}")
     return {"value": round(mean_tokens / step_s, 3), "unit": "tok/s", "cores": oracle.num_threads(),
-            "kind": "port", "sample": f"one full verify step (B={len(tokens)}, all {desc.n_layers} layers + head, "
-                                      f"P={P}) of the C++ oracle with resident weights; {step_s:.2f} s/step",
-            "s_per_step": round(step_s, 3)}
+            "cpu_model": cpu_model_name(), "kind": "port",
+            "sample": f"full verify step (B={len(tokens)}, all {desc.n_layers} layers + head, P={P}) of the C++ oracle "
+                      f"with resident weights: median of 5 after 1 warm-up, {step_s:.2f} s/step",
+            "s_per_step": round(step_s, 3), "s_per_step_runs": [round(t, 3) for t in times],
+            "oracle_top1_equal": bool(np.array_equal(top1, ref_top1)),
+            "oracle_top1_equal_outside_near_ties": bool(np.array_equal(top1[~near], ref_top1[~near])),
+            "near_tie_rows": int(near.sum()), "logits_max_abs": round(err, 4),
+            "logits_rel": round(err / float(np.abs(ref_logits).max()), 5), "logits_cosine": round(cos, 7)}
 
 
 if __name__ == "__main__":

@@ -63,12 +63,14 @@ _SIGS = [
     ("or_sm_key", C.c_uint64, [C.c_uint64, C.c_uint64]),
     ("or_sm_normal", C.c_float, [C.c_uint64, C.c_uint64]),
     ("or_synth_int4", None, [C.c_uint64, C.c_uint64, i32, i32, C.c_float, vp, vp, vp]),
+    ("or_synth_mxfp4", None, [C.c_uint64, C.c_uint64, i32, i32, vp, vp]),
     ("or_synth_bf16", None, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_float, C.c_float, vp]),
     ("or_synth_f32", None, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_float, C.c_float, vp]),
     ("or_f32_to_f16", C.c_uint16, [C.c_float]),
     ("or_f16_to_f32", C.c_float, [C.c_uint16]),
     ("or_synth_kv", None, [C.c_uint64, C.c_uint64, i32, i32, i32, i32, vp, vp, vp, vp]),
     ("or_rmsnorm", None, [vp, i32, i32, vp, C.c_float, vp]),
+    ("or_rms_split", None, [vp, i32, i32, vp, C.c_float, vp, vp]),
     ("or_glu", C.c_float, [C.c_float, C.c_float, i32, C.c_float]),
     ("or_fwht", None, [vp, i32]),
     ("or_rope_wht", None, [vp, i32, i32, C.c_float, i32]),

@@ -1,0 +1,123 @@
+"""The whole verify step at the benchmark configurations' full sizes on the GPU against the CPU oracle.
+
+Config 1 exactly (32 layers, hidden 4096, vocab 151936, B = 17, P = 8192), config 2's verify (the same model at
+P = 32768) and full-width two-layer slices of configs 3 (E128 top-8 int4 MoE, P = 16384) and 4 (MXFP4 MoE with sinks
+and the alternating 128-key window, B = 9, P = 65536). Logits against the oracle's fp32 within the stated tolerance,
+top-1 bit-exact on every row whose oracle top-2 margin exceeds twice the logit error (the rows inside it are counted
+and reported), and the accepted prefix of a greedy chain planted as drafts bit-exact against oracle.accept on the
+oracle's own top-1. The reference's own checks of these properties: the attention round vs CPU
+(Tests/IngotTests/KernelCaseTests.swift:178-206) and rowscheck / gen --check (Sources/ingot-dev/Checks/RowsCheck.swift).
+"""
+import json
+import os
+import time
+
+import numpy as np
+import pytest
+
+import oracle
+from ingot_amd._lib import KVCache, Model, ModelDesc, accept
+from synth import cosine
+
+pytestmark = pytest.mark.gpu
+
+DENSE8B = dict(n_layers=32, hidden=4096, n_q_heads=32, n_kv_heads=8, head_dim=128, intermediate=14336, vocab=151936)
+MOE3 = dict(n_layers=2, hidden=2048, n_q_heads=32, n_kv_heads=4, head_dim=128, intermediate=0, vocab=151936,
+            n_experts=128, top_k=8, expert_intermediate=768, expert_format=0)
+MOE4 = dict(n_layers=2, hidden=2880, n_q_heads=64, n_kv_heads=8, head_dim=64, intermediate=0, vocab=201088,
+            n_experts=32, top_k=4, expert_intermediate=2880, expert_format=1, router_bias=1, expert_bias=1, act=1,
+            sinks=1, sliding_window=128)
+CASES = {
+    "cfg1-dense8b-P8192": (DENSE8B, 8192, 17),
+    "cfg2-dense8b-P32768": (DENSE8B, 32768, 17),
+    "cfg3-moe-e128-2L-P16384": (MOE3, 16384, 17),
+    "cfg4-mxfp4-moe-2L-P65536": (MOE4, 65536, 9),
+}
+SEED, KV_SEED = 2026, 11
+
+# Logits tolerance. Dense: max-abs ≤ 1% of max |ref| and cosine ≥ 0.9999. Both sides round the activations to bf16
+# at the same points, so the difference is the occasional one-ulp flip of a bf16 (2^-8 relative) or of an int8 KV
+# level where the pre-rounding values differ in the last fp32 bits; at config 1's logit scale (~70) one bf16 ulp of a
+# logit is 0.25–0.5. MoE: the softmax router turns such flips into changed expert weights (and near a tie into a
+# changed expert), measured as up to 3% of the scale on the small MoE models; cosine ≥ 0.999.
+TOL = {"dense": (0.01, 0.9999), "moe": (0.03, 0.999)}
+
+
+def report(name, **kv):
+    """Measured figures of a case, printed and appended to gpurun_out/fullsize.jsonl when that folder exists."""
+    line = json.dumps({"case": name, **kv})
+    print(line, flush=True)
+    if os.path.isdir("gpurun_out"):
+        with open("gpurun_out/fullsize.jsonl", "a") as f:
+            f.write(line + "\n")
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_fullsize_verify_matches_oracle(ctx, name):
+    shape, P, B = CASES[name]
+    print(f"[fullsize] {name}: building", flush=True)
+    d = ModelDesc.make(**shape)
+    m = Model(ctx, d, SEED)
+    kv = KVCache(m, P + 2 * B)
+    try:
+        kv.fill_synthetic(P, KV_SEED)
+        toks = np.random.default_rng(P + B).integers(0, d.vocab, size=B).astype(np.uint32)
+        top1, logits = kv.verify(toks, want_logits=True)
+        t0 = time.time()
+        om = oracle.OracleModel(d, SEED, KV_SEED, P)
+        t1 = time.time()
+        ref_logits, ref_top1 = om.verify(toks)
+        t2 = time.time()
+        err = float(np.abs(logits - ref_logits).max())
+        cos = cosine(logits, ref_logits)
+        scale = float(np.abs(ref_logits).max())
+        srt = np.sort(ref_logits, axis=1)
+        margin = srt[:, -1] - srt[:, -2]
+        sure = margin > 2 * err
+        flips = int(np.sum(top1[sure] != ref_top1[sure]))
+        near_ties = int(np.sum(~sure))
+        near_tie_flips = int(np.sum(top1[~sure] != ref_top1[~sure]))
+        report(name, max_abs=err, rel=err / scale, cosine=cos, scale=scale, near_tie_rows=near_ties,
+               near_tie_flips=near_tie_flips, flips=flips, oracle_build_s=round(t1 - t0, 2),
+               oracle_step_s=round(t2 - t1, 2), top1=top1.tolist(), ref_top1=ref_top1.tolist())
+        rel_tol, cos_tol = TOL["moe" if shape.get("n_experts") else "dense"]
+        assert err <= rel_tol * scale and cos >= cos_tol, (err, scale, cos)
+        assert flips == 0, (top1, ref_top1, margin, err)
+        assert np.array_equal(top1, np.argmax(logits, axis=1).astype(np.uint32))
+
+        # Greedy chain planted as drafts: iterate block[i + 1] = top1[i] until it is a fixed point (row i's top-1 depends
+        # only on rows ≤ i, so B − 1 iterations suffice), then the oracle's top-1 on that block must give the same
+        # accepted prefix, all B − 1 drafts; with a wrong draft planted at L, both accept exactly L. A row whose
+        # oracle top-2 margin is inside twice the block's logit error may flip (a near tie): the accepted prefix must
+        # then agree up to the first such row, and the case is reported.
+        blk = toks.copy()
+        for _ in range(B - 1):
+            t = kv.verify(blk)
+            blk[1:] = t[:-1]
+        gt, gl = kv.verify(blk, want_logits=True)
+        assert np.array_equal(blk[1:], gt[:-1])
+        ol, ot = om.verify(blk)
+        berr = float(np.abs(gl - ol).max())
+        bs = np.sort(ol, axis=1)
+        tie = (bs[:, -1] - bs[:, -2]) <= 2 * berr
+        first_tie = int(np.argmax(tie)) if tie.any() else B
+        assert np.array_equal(gt[~tie], ot[~tie])
+        gm, om_m = accept(blk, gt).m, oracle.accept(blk, ot)[0]
+        report(name + " chain", block_max_abs=berr, near_tie_rows=tie.nonzero()[0].tolist(), gpu_m=gm, oracle_m=om_m)
+        assert gm == B - 1
+        assert om_m == B - 1 or om_m >= first_tie
+        L = B // 3
+        bad = blk.copy()
+        bad[L + 1] = (bad[L + 1] + 1) % d.vocab
+        gb = kv.verify(bad)
+        _, ob = om.verify(bad)
+        r = accept(bad, gb)
+        om_, oem = oracle.accept(bad, ob)
+        assert r.m == L
+        if first_tie >= L:
+            assert om_ == L and r.emitted[:L] == list(oem[:L])
+        om.free()
+        assert kv.pos == P
+    finally:
+        kv.free()
+        m.free()

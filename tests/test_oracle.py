@@ -92,6 +92,10 @@ def test_qmm_mxfp4_against_float64_matmul():
 def test_argmax_ties_and_nan():
     x = np.array([[1, 3, 3, 2], [np.nan, 1, np.nan, 1], [-np.inf] * 4, [0, -0.0, 0, 0]], np.float32)
     assert list(oracle.argmax_rows(x)) == [1, 1, 0, 0]
+    # -inf never takes an index (a scan from (-inf, 0) with a strict >, verify.metal:537): NaN mixed with -inf gives 0,
+    # a finite value behind -inf and NaN wins.
+    z = np.array([[np.nan, -np.inf, np.nan, -np.inf], [-np.inf, np.nan, -5.0, -np.inf]], np.float32)
+    assert list(oracle.argmax_rows(z)) == [0, 2]
     g = rng(4)
     y = g.normal(size=(7, 1000)).astype(np.float32)
     assert np.array_equal(oracle.argmax_rows(y), np.argmax(y, axis=1))
