@@ -99,6 +99,15 @@ int ih_qmm_int4(ih_ctx* ctx, const ih_qmat* W, const void* x_bf16_dev, int ldx, 
  * Sources/Ingot/Shaders/verify.metal:525-547. Enqueued only. */
 int ih_argmax_rows(ih_ctx* ctx, const float* x_dev, int rows, int N, uint32_t* out_dev);
 
+/* ih_argmax_rows without any allocation. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The chunk
+ * partials live in a static per-device array of IH_ARGMAX_NOALLOC_MAX_ROWS × 16 (value, index) pairs (32 KiB, held
+ * by each GPU the library runs on until the process ends); rows beyond IH_ARGMAX_NOALLOC_MAX_ROWS are IH_EINVAL.
+ * Every call on one GPU shares that array: calls that overlap on one GPU (other streams, other contexts) race.
+ * Same results as ih_argmax_rows. Enqueued only. */
+#define IH_ARGMAX_NOALLOC_MAX_ROWS 256
+int ih_argmax_rows_noalloc(ih_ctx* ctx, const float* x_dev, int rows, int N, uint32_t* out_dev);
+
 /* Result of greedy acceptance: m accepted drafts, then the emitted tokens vtok[1..m] followed by the new anchor
  * top1[m] (n_emitted = m + 1). */
 typedef struct ih_accept_result {

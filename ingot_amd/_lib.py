@@ -74,6 +74,7 @@ def _declare(L: C.CDLL) -> None:
         "ih_qmat_bytes": (sz, [vp]),
         "ih_qmm_int4": (i32, [vp, vp, vp, i32, i32, vp, i32, i32]),
         "ih_argmax_rows": (i32, [vp, vp, i32, i32, vp]),
+        "ih_argmax_rows_noalloc": (i32, [vp, vp, i32, i32, vp]),
         "ih_accept": (i32, [vp, vp, i32, vp]),
         "ih_spec_accept_dev": (i32, [vp, vp, vp, vp, vp, i32, i32]),
         "ih_model_create_synthetic": (i32, [vp, vp, C.c_uint64, P(vp)]),

@@ -129,6 +129,8 @@ struct ih_ctx {
   ih::ActBuf act;
   size_t act_cap_k = 0;
   int cu_count = 256;
+  // Device address of the static argmax scratch on this context's device (ih_argmax_rows_noalloc).
+  void* noalloc_scratch = nullptr;
 };
 
 namespace ih {
@@ -150,6 +152,7 @@ inline void tlaunch(const TimedLaunch& tl, F kernel, dim3 grid, dim3 block, unsi
   hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, tl.a, tl.b, 0u, args...);
 }
 int fill(ih_ctx* c, void* dst, int byte, size_t bytes);
+int init_noalloc_scratch(ih_ctx* c);
 int ensure_part(ih_ctx* c, size_t bytes);
 int ensure_act(ih_ctx* c, ActBuf& a, int K, bool f16);
 void free_act(ActBuf& a);

@@ -194,6 +194,19 @@ int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t*
   return IH_OK;
 }
 
+// Chunk partials of ih_argmax_rows_noalloc: a static per-device array instead of the context's allocated scratch. Host
+// code never passes `scratch` itself (in host code the name is a stand-in, not a device address): init_noalloc_scratch
+// stores its device address, from hipGetSymbolAddress with the context's device current, and the kernels get that.
+static __device__ __align__(256) float2 scratch[IH_ARGMAX_NOALLOC_MAX_ROWS * ARGMAX_CHUNKS];
+
+int init_noalloc_scratch(ih_ctx* c) {
+  void* p = nullptr;
+  IH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  IH_CHECK(p != nullptr, IH_EDEVICE, "ih_init: no device address for the static argmax scratch");
+  c->noalloc_scratch = p;
+  return IH_OK;
+}
+
 int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows) {
   accept_kernel<<<1, 64, 0, c->stream>>>(st, vtok, top1, rec, ring, rows);
   IH_HIP(hipGetLastError());
@@ -210,6 +223,22 @@ int ih_argmax_rows(ih_ctx* c, const float* x_dev, int rows, int N, uint32_t* out
   IH_CHECK(c && x_dev && out_dev, IH_EINVAL, "ih_argmax_rows: null argument");
   IH_CHECK(rows >= 1 && N >= 1, IH_EINVAL, "ih_argmax_rows: empty input");
   return launch_argmax(c, x_dev, N, rows, N, out_dev);
+}
+
+int ih_argmax_rows_noalloc(ih_ctx* c, const float* x_dev, int rows, int N, uint32_t* out_dev) {
+  IH_CHECK(c && x_dev && out_dev, IH_EINVAL, "ih_argmax_rows_noalloc: null argument");
+  IH_CHECK(rows >= 1 && N >= 1, IH_EINVAL, "ih_argmax_rows_noalloc: empty input");
+  IH_CHECK(rows <= IH_ARGMAX_NOALLOC_MAX_ROWS, IH_EINVAL,
+           "ih_argmax_rows_noalloc: " + std::to_string(rows) + " rows exceed the static scratch (" +
+               std::to_string(IH_ARGMAX_NOALLOC_MAX_ROWS) + " rows)");
+  IH_CHECK(c->noalloc_scratch, IH_ESTATE, "ih_argmax_rows_noalloc: the context has no static scratch");
+  // Every partial the final pass reads is written by the chunk pass of the same call: nothing to clear.
+  float2* part = static_cast<float2*>(c->noalloc_scratch);
+  argmax_chunk_kernel<<<dim3(rows, ARGMAX_CHUNKS), 256, 0, c->stream>>>(x_dev, N, N, part);
+  IH_HIP(hipGetLastError());
+  argmax_final_kernel<<<rows, 64, 0, c->stream>>>(part, out_dev);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
 }
 
 int ih_accept(const uint32_t* vtok, const uint32_t* top1, int B, ih_accept_result* out) {

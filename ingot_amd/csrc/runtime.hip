@@ -127,6 +127,11 @@ int ih_init(int device, ih_ctx** out) {
     delete c;
     return fail(IH_EDEVICE, "ih_init: stream creation failed");
   }
+  if (int st = init_noalloc_scratch(c); st != IH_OK) {
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return st;
+  }
   *out = c;
   return IH_OK;
 }
