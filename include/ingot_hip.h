@@ -195,6 +195,48 @@ int ih_verify_step(ih_model* model, ih_kv* kv, const uint32_t* tokens, int B, fl
 /* The same, enqueued only, with device buffers: tokens_dev (uint32[B]) in, top1_dev (uint32[B]) out. */
 int ih_verify_step_dev(ih_model* model, ih_kv* kv, const uint32_t* tokens_dev, int B, uint32_t* top1_dev);
 
+/* One verify step whose position is read on the device from st_dev[0] (the round state of ih_spec_accept_dev), so the
+ * host can enqueue round N+1 before round N's acceptance is known: the chained rounds of decodeSpec
+ * (Sources/Ingot/Generate.swift:240-504), where the reference's attention reads ctx = st[0]
+ * (Shaders/verify_attn_nax.metal:77). The launches are sized for pos_min ≤ P ≤ pos_max (pos_max + B ≤ capacity); a
+ * device P outside that range sets st_dev[7] = 1 and the step writes nothing outside the cache. The K/V rows go to
+ * P…P+B−1; the host position of kv is not changed (ih_kv_set_pos afterwards). Enqueued only. */
+int ih_verify_step_chained(ih_model* model, ih_kv* kv, const uint32_t* tokens_dev, int B, uint32_t* top1_dev,
+                           uint32_t* st_dev, int pos_min, int pos_max);
+
+/* Positions the cache holds. */
+int ih_kv_capacity(const ih_kv* kv);
+
+/* Options and result of ih_decode_greedy. */
+typedef struct ih_decode_opts {
+  int max_tokens;              /* emitted tokens to stop at, `first` included (≥ 1) */
+  const uint32_t* stop_tokens; /* a stop token ends the output (it is emitted) */
+  int n_stop;
+  int rows;                    /* verify rows per round: 1 = plain chained decoding, 2…17 = anchor + copy drafts */
+  int min_match, max_match;    /* copy-from-context rule (CopyIndex minMatch / maxMatch; ≥ 3) */
+  int inflight;                /* rounds enqueued ahead of the record the host reads (1…7) */
+} ih_decode_opts;
+#define IH_FINISH_LENGTH 0
+#define IH_FINISH_STOP 1
+#define IH_FINISH_CONTEXT 2
+typedef struct ih_decode_stats {
+  int rounds;    /* verify rounds whose records were read */
+  int drafted;   /* draft rows verified in them */
+  int accepted;  /* drafts accepted */
+  int emitted;   /* tokens written to out */
+  int finish;    /* IH_FINISH_* */
+} ih_decode_stats;
+
+/* Greedy speculative decoding with the round state on the device (HybridModel.decodeSpec, Generate.swift:240-504,
+ * greedy): `first` is the first emitted token, to sit at the cache's position P (history[0…P−1] are the tokens of
+ * positions 0…P−1, needed only by the copy drafter, rows > 1). Each round runs copy lookup → verify (position from the
+ * device state) → acceptance, enqueued `inflight` rounds ahead of the host; the host reads the rounds' records, stops
+ * at a stop token, max_tokens or the cache's end, and rolls the cache back to the position of the last emitted token
+ * (rewindExtraRound, Generate.swift:515-540), so the next call continues from it. out[0…n_out−1] are the emitted
+ * tokens, identical to one-row greedy decoding. */
+int ih_decode_greedy(ih_model* model, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first,
+                     const ih_decode_opts* opts, uint32_t* out, int out_cap, int* n_out, ih_decode_stats* stats);
+
 /* Verify, accept and commit in one call: runs the step on tokens (anchor + drafts), accepts the longest matching draft
  * prefix, advances P by m + 1 and returns the result (the non-chained round of generateSpec, Generate.swift:104-177). */
 int ih_verify_and_accept(ih_model* model, ih_kv* kv, const uint32_t* tokens, int B, ih_accept_result* out);

@@ -107,6 +107,9 @@ def _declare(L: C.CDLL) -> None:
         "ih_copy_index_len": (i32, [vp]),
         "ih_copy_index_propose": (i32, [vp, i32, vp, P(i32), P(i32)]),
         "ih_copy_lookup_dev": (i32, [vp, vp, i32, i32, i32, i32, vp, vp, i32]),
+        "ih_verify_step_chained": (i32, [vp, vp, vp, i32, vp, vp, i32, i32]),
+        "ih_kv_capacity": (i32, [vp]),
+        "ih_decode_greedy": (i32, [vp, vp, vp, i32, C.c_uint32, vp, vp, i32, P(i32), vp]),
         "ih_timing_enable": (i32, [vp, i32]),
         "ih_timing_read": (i32, [vp, i32, P(C.c_double), P(C.c_int), P(C.c_double)]),
     }
@@ -310,6 +313,21 @@ class ModelDesc(C.Structure):
         return {f: getattr(self, f) for f, _ in self._fields_}
 
 
+class DecodeOpts(C.Structure):
+    """ih_decode_opts (include/ingot_hip.h)."""
+
+    _fields_ = [("max_tokens", C.c_int), ("stop_tokens", vp), ("n_stop", C.c_int), ("rows", C.c_int),
+                ("min_match", C.c_int), ("max_match", C.c_int), ("inflight", C.c_int)]
+
+
+class DecodeStats(C.Structure):
+    _fields_ = [("rounds", C.c_int), ("drafted", C.c_int), ("accepted", C.c_int), ("emitted", C.c_int),
+                ("finish", C.c_int)]
+
+
+FINISH_LENGTH, FINISH_STOP, FINISH_CONTEXT = 0, 1, 2
+
+
 def accept(vtok, top1) -> AcceptResult:
     vtok = np.ascontiguousarray(vtok, np.uint32)
     top1 = np.ascontiguousarray(top1, np.uint32)
@@ -368,6 +386,25 @@ class KVCache:
         check(lib().ih_verify_step(self.model.handle, self.handle, ptr(t), len(t),
                                    ptr(logits) if logits is not None else None, ptr(top1)))
         return (top1, logits) if want_logits else top1
+
+    @property
+    def capacity(self) -> int:
+        return lib().ih_kv_capacity(self.handle)
+
+    def decode_greedy(self, first: int, max_tokens: int, rows: int = 1, history=None, stop=(), inflight: int = 2,
+                      min_match: int = 3, max_match: int = 64):
+        """Chained greedy decoding (ih_decode_greedy): (emitted tokens, DecodeStats)."""
+        stop_a = np.ascontiguousarray(np.asarray(stop, np.uint32).reshape(-1))
+        o = DecodeOpts(max_tokens=max_tokens, stop_tokens=ptr(stop_a) if stop_a.size else None, n_stop=stop_a.size,
+                       rows=rows, min_match=min_match, max_match=max_match, inflight=inflight)
+        hist = None if history is None else np.ascontiguousarray(np.asarray(history, np.uint32))
+        out = np.zeros(max_tokens, np.uint32)
+        n = C.c_int()
+        st = DecodeStats()
+        check(lib().ih_decode_greedy(self.model.handle, self.handle, ptr(hist) if hist is not None else None,
+                                     0 if hist is None else hist.size, first, C.byref(o), ptr(out), max_tokens,
+                                     C.byref(n), C.byref(st)))
+        return [int(x) for x in out[: n.value]], st
 
     def verify_and_accept(self, tokens) -> AcceptResult:
         t = np.ascontiguousarray(tokens, np.uint32)

@@ -57,6 +57,10 @@ template <int HD>
 __global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
   constexpr int NE = HD / 64, RH = HD / 2;
   const int slot = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y, lane = threadIdx.x & 63;
+  if (a.pos_dev && blockIdx.x == 0 && t == 0 && threadIdx.x == 0) {
+    const uint32_t p = a.pos_dev[0];
+    if (p < uint32_t(a.pos_min) || p > uint32_t(a.pos_max)) a.flag_dev[0] = 1u;
+  }
   if (slot >= a.QH + 2 * a.KVH) return;  // wave-uniform
   const bool isq = slot < a.QH, isk = !isq && slot < a.QH + a.KVH;
   const float* row = a.proj + size_t(t) * a.ldp + size_t(slot) * HD;  // q heads | k heads | v heads
@@ -109,7 +113,8 @@ __global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
   const __half sc16 = __float2half_rn(am > 0.f ? am / 127.0f : 1.0f);
   const float sc = __half2float(sc16);
   const int h = isk ? slot - a.QH : slot - a.QH - a.KVH;
-  const int pos = a.P + t, kpos = a.ring ? pos % a.ring : pos;
+  const int pos = attn_pos(a).P + t, kpos = a.ring ? pos % a.ring : pos;
+  if (!a.ring && pos >= a.cap) return;  // a device position beyond the range the step was sized for (flagged)
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
     const int d = lane + 64 * e;
@@ -173,16 +178,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   __shared__ _Float16 Vt[NBUF][HD * VROW];
   __shared__ __attribute__((aligned(16))) float ksf[NBUF][PIECE], vsf[NBUF][PIECE];
 
-  const int sidx = blockIdx.x, split = sidx + a.s0, kvh = blockIdx.y;
+  const AttnPos ap = attn_pos(a);
+  const int P = ap.P;
+  const int sidx = blockIdx.x, split = sidx + ap.s0, kvh = blockIdx.y;
+  if (sidx >= ap.nsplit) return;  // launched for a later position than the step's (chained rounds): no keys
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
   const int Q = a.G * a.B;
   // Keys [k0, k1) of the split. In a sliding-window layer every row's window starts at or after P − window + 1, so
   // the split starts there (rounded down to 64 keys, which keeps pieces and the 32-slot V blocks aligned): the keys
   // before it are masked for every row and add nothing.
-  const int k1 = min(split * a.C + a.C, a.P + a.B);
+  const int k1 = min(split * a.C + a.C, P + a.B);
   // The skip is a whole number of 64-key pieces counted from the split's own start, so the pieces (and the order in
   // which the online softmax meets the keys) are the same for every P: a row's bits do not depend on the block.
-  const int k0 = a.window > 0 ? split * a.C + (max(0, a.P - a.window + 1 - split * a.C) & ~63) : split * a.C;
+  const int k0 = a.window > 0 ? split * a.C + (max(0, P - a.window + 1 - split * a.C) & ~63) : split * a.C;
 
   const int8_t* kh = a.kc + size_t(kvh) * a.cap * HD;
   const int8_t* vh = a.vc + size_t(kvh) * HD * a.vld;
@@ -247,13 +255,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     for (int dt = 0; dt < NDT; ++dt) o[tt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     mrun[tt] = -INFINITY;
     lsum[tt] = 0.f;
-    lim[tt] = m < Q ? a.P + m / a.G : -1;  // last visible key (causal); −1: padding row sees nothing
+    lim[tt] = m < Q ? P + m / a.G : -1;  // last visible key (causal); −1: padding row sees nothing
     lo_key[tt] = a.window > 0 ? lim[tt] - a.window + 1 : -2147483647;
-    tile_hi[tt] = live[tt] ? a.P + min(16 * qt + 15, Q - 1) / a.G : -1;
-    tile_lo[tt] = a.window > 0 ? a.P + (16 * qt) / a.G - a.window + 1 : -2147483647;
+    tile_hi[tt] = live[tt] ? P + min(16 * qt + 15, Q - 1) / a.G : -1;
+    tile_lo[tt] = a.window > 0 ? P + (16 * qt) / a.G - a.window + 1 : -2147483647;
     // Keys every row of the tile sees: up to the first row's causal limit (−1 if the tile has padding rows, which see
     // nothing and need the mask), from the last row's window start.
-    tile_lo_lim[tt] = (live[tt] && 16 * qt + 15 < Q) ? a.P + (16 * qt) / a.G : -1;
+    tile_lo_lim[tt] = (live[tt] && 16 * qt + 15 < Q) ? P + (16 * qt) / a.G : -1;
     tile_hi_lo[tt] = a.window > 0 ? tile_hi[tt] - a.window + 1 : -2147483647;
   }
 
@@ -564,13 +572,14 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __r
   float o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
-  for (int s0 = sg; s0 < a.nsplit; s0 += NB * SG) {
+  const int nsplit = attn_pos(a).nsplit;
+  for (int s0 = sg; s0 < nsplit; s0 += NB * SG) {
     float2 v[NB];
     uint4 raw[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int s = s0 + i * SG;
-      const bool ok = s < a.nsplit;
+      const bool ok = s < nsplit;
       const size_t idx = (size_t(kvh) * a.nsplit + (ok ? s : 0)) * a.Qpad + m;
       v[i] = a.ml[idx];
       raw[i] = *reinterpret_cast<const uint4*>(a.opart + idx * HD + 8 * dg);

@@ -32,8 +32,27 @@ struct AttnArgs {
   float2* ml;          // [KVH][nsplit][Qpad] (running max in log2 units, sum)
   int cap, ring, P, B, QH, KVH, HD, G, Qpad;  // cap: slots per head (the ring size of a sliding-window layer)
   int vld;                                    // row of the transposed V: cap rounded up to 32
-  int C, nsplit, s0, window, hadk;
+  int C, nsplit, s0, window, hadk;            // nsplit: launched splits (the partials' stride), s0: their first
   float theta, scale_log2;
+  // Chained rounds: P is read on the device from pos_dev[0] (the round state), within [pos_min, pos_max], the range
+  // the launch was sized for; flag_dev[0] is set to 1 when it falls outside (the step then writes nothing out of
+  // bounds). Null: P is the host value above.
+  const uint32_t* pos_dev;
+  uint32_t* flag_dev;
+  int pos_min, pos_max;
 };
+
+// The step's position and its key splits: P, the first split s0 (a sliding-window layer starts at the split of the
+// earliest window start, P − window + 1) and the number of splits from s0 that hold keys (at most the launched ones).
+struct AttnPos {
+  int P, s0, nsplit;
+};
+__device__ __forceinline__ AttnPos attn_pos(const AttnArgs& a) {
+  AttnPos r;
+  r.P = a.pos_dev ? int(min(a.pos_dev[0], uint32_t(a.pos_max))) : a.P;
+  r.s0 = a.window > 0 ? max(0, r.P - a.window + 1) / a.C : 0;
+  r.nsplit = min((r.P + a.B + a.C - 1) / a.C - r.s0, a.nsplit);
+  return r;
+}
 
 }  // namespace ih

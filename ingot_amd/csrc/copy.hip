@@ -133,15 +133,23 @@ __device__ __forceinline__ Top3 top3_wave(Top3 t) {
   return t;
 }
 
+// The history length n of a chained round is the round state's position + 1 (hist[P] is the anchor), read on the
+// device: pos_dev non-null gives n = min(pos_dev[0] + 1, n); a history shorter than 4 proposes nothing.
+__device__ __forceinline__ int copy_len(int n, const uint32_t* pos_dev) {
+  return pos_dev ? int(min(pos_dev[0] + 1u, uint32_t(n))) : n;
+}
+
 __global__ __launch_bounds__(COPY_THREADS) void copy_scan_kernel(const uint32_t* __restrict__ h, int n,
-                                                                 int* __restrict__ part) {
+                                                                 int* __restrict__ part,
+                                                                 const uint32_t* __restrict__ pos_dev) {
   __shared__ int red[COPY_THREADS / 64][3];
+  n = copy_len(n, pos_dev);
   const int cur = n - 1;
-  const uint32_t t0 = h[cur - 2], t1 = h[cur - 1], t2 = h[cur];
+  const uint32_t t0 = h[max(cur - 2, 0)], t1 = h[max(cur - 1, 0)], t2 = h[max(cur, 0)];
   const int lo = blockIdx.x * COPY_CH;
   Top3 t{{-1, -1, -1}};
   // Ascending positions per thread: a new match is always the largest so far.
-  for (int p = lo + threadIdx.x; p < lo + COPY_CH && p < cur; p += COPY_THREADS) {
+  for (int p = lo + threadIdx.x; p < lo + COPY_CH && p < cur && n >= 4; p += COPY_THREADS) {
     if (p < 2) continue;
     if (h[p] == t2 && h[p - 1] == t1 && h[p - 2] == t0) {
       t.v[2] = t.v[1];
@@ -165,8 +173,10 @@ __global__ __launch_bounds__(COPY_THREADS) void copy_scan_kernel(const uint32_t*
 // vtok (optional): the verify block [anchor = h[cur], proposal…, padding = h[cur]] of `rows` entries.
 __global__ __launch_bounds__(64) void copy_pick_kernel(const uint32_t* __restrict__ h, int n, const int* __restrict__ part,
                                                        int nparts, int max_k, int min_match, int max_match,
-                                                       uint32_t* __restrict__ out, uint32_t* __restrict__ vtok, int rows) {
+                                                       uint32_t* __restrict__ out, uint32_t* __restrict__ vtok, int rows,
+                                                       const uint32_t* __restrict__ pos_dev) {
   const int lane = threadIdx.x;
+  n = copy_len(n, pos_dev);
   const int cur = n - 1;
   Top3 t{{-1, -1, -1}};
   for (int i = lane; i < nparts; i += 64) t = top3_merge(t, Top3{{part[3 * i], part[3 * i + 1], part[3 * i + 2]}});
@@ -187,7 +197,7 @@ __global__ __launch_bounds__(64) void copy_pick_kernel(const uint32_t* __restric
   if (best_len >= min_match) cnt = min(cur, best + max_k) - best;
   else best_len = 0;
   for (int i = lane; i < max_k; i += 64) out[4 + i] = i < cnt ? h[best + 1 + i] : 0u;
-  if (vtok)
+  if (vtok && cur >= 0)
     for (int i = lane; i < rows; i += 64) vtok[i] = (i >= 1 && i <= cnt) ? h[best + i] : h[cur];
   if (lane == 0) {
     out[0] = uint32_t(cnt);
@@ -198,17 +208,17 @@ __global__ __launch_bounds__(64) void copy_pick_kernel(const uint32_t* __restric
 }
 
 int launch_copy_lookup(ih_ctx* c, const uint32_t* h, int n, int max_k, int min_match, int max_match, uint32_t* out,
-                       uint32_t* vtok, int rows) {
+                       uint32_t* vtok, int rows, const uint32_t* pos_dev) {
   const int nparts = std::max(1, (n - 1 + COPY_CH - 1) / COPY_CH);
   const size_t need = size_t(nparts) * 3 * sizeof(int);
   IH_TRY(ensure_part(c, need));
   int* part = reinterpret_cast<int*>(c->part);
   {
     TimedLaunch tl(c, TC_OTHER, double(n) * 4);
-    tlaunch(tl, copy_scan_kernel, dim3(nparts), dim3(COPY_THREADS), 0, c->stream, h, n, part);
+    tlaunch(tl, copy_scan_kernel, dim3(nparts), dim3(COPY_THREADS), 0, c->stream, h, n, part, pos_dev);
     IH_HIP(hipGetLastError());
   }
-  copy_pick_kernel<<<1, 64, 0, c->stream>>>(h, n, part, nparts, max_k, min_match, max_match, out, vtok, rows);
+  copy_pick_kernel<<<1, 64, 0, c->stream>>>(h, n, part, nparts, max_k, min_match, max_match, out, vtok, rows, pos_dev);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
@@ -277,7 +287,7 @@ int ih_copy_lookup_dev(ih_ctx* c, const uint32_t* hist_dev, int n, int max_k, in
   IH_CHECK(!vtok_dev || (rows >= 1 && rows <= IH_MAX_ROWS), IH_EINVAL, "ih_copy_lookup_dev: rows must be in 1..17");
   min_match = std::max(3, min_match);
   max_match = std::max(min_match, max_match);
-  return launch_copy_lookup(c, hist_dev, n, max_k, min_match, max_match, out_dev, vtok_dev, rows);
+  return launch_copy_lookup(c, hist_dev, n, max_k, min_match, max_match, out_dev, vtok_dev, rows, nullptr);
 }
 
 }  // extern "C"

@@ -1,0 +1,155 @@
+// Chained greedy decoding: the host loop of speculative decoding with the round state on the device.
+//
+// Reference: HybridModel.decodeSpec (Sources/Ingot/Generate.swift:240-504) and rewindExtraRound (:515-540). Each round
+// is drafter → verify → spec_accept, all reading and advancing the round state st on the device, so the host enqueues
+// round N+1 (and more) before it has read round N's record; it reads records a few rounds behind, and when it stops
+// (a stop token, the token budget or the context) the rounds already enqueued past the stop are rolled back by setting
+// the cache position after the last emitted token. The drafter here is the copy-from-context lookup over the
+// device-resident history (CopyIndex's rule, Sources/Ingot/CopySpec.swift:118-138), or none (one row per round: plain
+// chained decoding).
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "ih_internal.h"
+
+using namespace ih;
+
+namespace {
+
+constexpr int REC_RING = 8;  // records of the rounds in flight (≥ inflight + 1)
+
+// Device and host buffers of one decode call, released on every exit path.
+struct DecodeBuffers {
+  ih_ctx* c = nullptr;
+  uint32_t* st = nullptr;    // round state [8] (device)
+  uint32_t* vtok = nullptr;  // verify block [IH_MAX_ROWS] (device)
+  uint32_t* top1 = nullptr;  // [IH_MAX_ROWS] (device)
+  uint32_t* hist = nullptr;  // token at each position, the anchor last (device)
+  uint32_t* copy = nullptr;  // copy lookup output [4 + IH_MAX_ROWS] (device)
+  uint32_t* rec = nullptr;   // round records [REC_RING][IH_REC_STRIDE] (host-pinned, written by the device)
+  std::vector<hipEvent_t> ev;
+  ~DecodeBuffers() {
+    if (c) (void)hipStreamSynchronize(c->stream);
+    void* d[] = {st, vtok, top1, hist, copy};
+    for (void* p : d)
+      if (p) (void)hipFree(p);
+    if (rec) (void)hipHostFree(rec);
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int ih_decode_greedy(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first,
+                     const ih_decode_opts* o, uint32_t* out, int out_cap, int* n_out, ih_decode_stats* stats) {
+  IH_CHECK(m && kv && o && out && n_out, IH_EINVAL, "ih_decode_greedy: null argument");
+  ih_ctx* c = model_ctx(m);
+  const ih_model_desc& d = model_desc(m);
+  const int B = o->rows, P0 = ih_kv_pos(kv), cap = ih_kv_capacity(kv);
+  IH_CHECK(B >= 1 && B <= IH_MAX_ROWS, IH_EINVAL, "ih_decode_greedy: rows must be in 1..17");
+  IH_CHECK(o->max_tokens >= 1 && out_cap >= o->max_tokens, IH_EINVAL,
+           "ih_decode_greedy: need max_tokens >= 1 and out_cap >= max_tokens");
+  IH_CHECK(o->inflight >= 1 && o->inflight < REC_RING, IH_EINVAL, "ih_decode_greedy: inflight must be in 1..7");
+  IH_CHECK(first < uint32_t(d.vocab), IH_EINVAL, "ih_decode_greedy: first token beyond the vocabulary");
+  IH_CHECK(B == 1 || (history && n_history == P0), IH_EINVAL,
+           "ih_decode_greedy: the copy drafter needs the history of the cache's positions (n_history == position)");
+  IH_CHECK(o->n_stop >= 0 && (o->n_stop == 0 || o->stop_tokens), IH_EINVAL, "ih_decode_greedy: bad stop tokens");
+  const int min_match = std::max(3, o->min_match), max_match = std::max(min_match, o->max_match);
+  auto is_stop = [&](uint32_t t) {
+    for (int i = 0; i < o->n_stop; ++i)
+      if (o->stop_tokens[i] == t) return true;
+    return false;
+  };
+  ih_decode_stats sx{};
+  int n = 0;
+  out[n++] = first;
+  auto finish = [&](int why) {
+    sx.finish = why;
+    sx.emitted = n;
+    *n_out = n;
+    if (stats) *stats = sx;
+    return IH_OK;
+  };
+  if (is_stop(first)) return finish(IH_FINISH_STOP);
+  if (o->max_tokens <= 1) return finish(IH_FINISH_LENGTH);
+  if (P0 + B > cap) return finish(IH_FINISH_CONTEXT);
+
+  DecodeBuffers bf;
+  bf.c = c;
+  IH_HIP(hipMalloc(&bf.st, 8 * 4));
+  IH_HIP(hipMalloc(&bf.vtok, IH_MAX_ROWS * 4));
+  IH_HIP(hipMalloc(&bf.top1, IH_MAX_ROWS * 4));
+  IH_HIP(hipMalloc(&bf.copy, (4 + IH_MAX_ROWS) * 4));
+  IH_HIP(hipMalloc(&bf.hist, size_t(cap + 1) * 4));
+  // Records go straight to pinned host memory (coherent: the device's writes are visible to the host once the
+  // round's event has completed, with no copy queued behind later rounds).
+  IH_HIP(hipHostMalloc(&bf.rec, REC_RING * IH_REC_STRIDE * 4, hipHostMallocMapped | hipHostMallocCoherent));
+  uint32_t* rec_dev = nullptr;
+  IH_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&rec_dev), bf.rec, 0));
+  bf.ev.assign(REC_RING, nullptr);
+  for (auto& e : bf.ev) IH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  std::memset(bf.rec, 0, REC_RING * IH_REC_STRIDE * 4);
+  uint32_t st0[8] = {uint32_t(P0), 0, 0, 0, first, 0, uint32_t(B), 0};
+  uint32_t vt0[IH_MAX_ROWS];
+  for (auto& v : vt0) v = first;
+  hipStream_t s = c->stream;
+  IH_HIP(hipMemcpyAsync(bf.st, st0, sizeof(st0), hipMemcpyHostToDevice, s));
+  IH_HIP(hipMemcpyAsync(bf.vtok, vt0, sizeof(vt0), hipMemcpyHostToDevice, s));
+  if (B > 1) {
+    if (P0) IH_HIP(hipMemcpyAsync(bf.hist, history, size_t(P0) * 4, hipMemcpyHostToDevice, s));
+    IH_HIP(hipMemcpyAsync(bf.hist + P0, &first, 4, hipMemcpyHostToDevice, s));
+  }
+  IH_HIP(hipStreamSynchronize(s));  // the host buffers above are stack or caller memory
+
+  // Known position: P after the last round read (round `known` − 1), and the rounds enqueued so far.
+  int known = 0, enq = 0, Pk = P0;
+  int stop_pos = -1, why = IH_FINISH_LENGTH;
+  while (stop_pos < 0) {
+    // Enqueue rounds while fewer than `inflight` are unread and the cache has room for the worst case.
+    while (enq - known < o->inflight) {
+      const int pos_min = Pk + (enq - known), pos_max = Pk + (enq - known) * B;
+      if (pos_max + B > cap) break;
+      if (B > 1) IH_TRY(launch_copy_lookup(c, bf.hist, cap + 1, B - 1, min_match, max_match, bf.copy, bf.vtok, B, bf.st));
+      IH_TRY(ih_verify_step_chained(m, kv, bf.vtok, B, bf.top1, bf.st, pos_min, pos_max));
+      IH_TRY(launch_accept(c, bf.st, bf.vtok, bf.top1, rec_dev, REC_RING, B, B > 1 ? bf.hist : nullptr, cap + 1));
+      IH_HIP(hipEventRecord(bf.ev[enq % REC_RING], s));
+      ++enq;
+    }
+    if (enq == known) {  // no room even for one round at the known position
+      why = IH_FINISH_CONTEXT;
+      stop_pos = Pk;
+      break;
+    }
+    // Read the oldest unread round.
+    IH_HIP(hipEventSynchronize(bf.ev[known % REC_RING]));
+    const uint32_t* r = bf.rec + (known % REC_RING) * IH_REC_STRIDE;
+    const int mr = int(r[0]), pb = int(r[IH_REC_P]);
+    IH_CHECK(mr >= 0 && mr < B && pb == Pk, IH_ESTATE, "ih_decode_greedy: round record out of sequence");
+    ++sx.rounds;
+    sx.drafted += B - 1;
+    sx.accepted += mr;
+    for (int i = 0; i <= mr; ++i) {
+      const uint32_t t = r[1 + i];
+      out[n++] = t;
+      // Token i of the round sits at position pb + 1 + i; stopping on it keeps the cache up to the position before
+      // (the token itself is the anchor of the next call, its K/V not yet committed).
+      if (is_stop(t)) { why = IH_FINISH_STOP; stop_pos = pb + 1 + i; break; }
+      if (n >= o->max_tokens) { why = IH_FINISH_LENGTH; stop_pos = pb + 1 + i; break; }
+    }
+    Pk = pb + mr + 1;
+    ++known;
+  }
+  // Rounds enqueued past the stop ran (or are running) on a state we discard: wait for them, then roll the cache
+  // back to the last emitted token (rewindExtraRound for an attention-only model: positions only).
+  IH_HIP(hipStreamSynchronize(s));
+  uint32_t flag = 0;
+  IH_HIP(hipMemcpy(&flag, bf.st + 7, 4, hipMemcpyDeviceToHost));
+  IH_CHECK(flag == 0, IH_ESTATE, "ih_decode_greedy: a round ran outside the position range it was launched for");
+  IH_TRY(ih_kv_set_pos(kv, stop_pos));
+  return finish(why);
+}
+
+}  // extern "C"

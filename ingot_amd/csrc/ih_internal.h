@@ -186,4 +186,11 @@ int qmm_grid(const ih_qmat* W);
 int pack_int4(ih_ctx* c, ih_qmat* q, const uint32_t* w_dev, const uint16_t* s_dev, const uint16_t* b_dev);
 int qmat_int4_create_dev(ih_ctx* c, const void* w, const void* s, const void* b, int E, int N, int K, int il8,
                          ih_qmat** out);
+// Model internals other translation units read (model.hip).
+ih_ctx* model_ctx(const ih_model* m);
+const ih_model_desc& model_desc(const ih_model* m);
+int launch_copy_lookup(ih_ctx* c, const uint32_t* h, int n, int max_k, int min_match, int max_match, uint32_t* out,
+                       uint32_t* vtok, int rows, const uint32_t* pos_dev);
+int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows,
+                  uint32_t* hist, int hist_cap);
 }  // namespace ih

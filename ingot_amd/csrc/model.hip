@@ -18,9 +18,10 @@ namespace ih {
 // Launchers of the other translation units.
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                      float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a, float2* rope, int P, float theta,
-                     int RH);
+                     int RH, const uint32_t* pos_dev, int pos_max);
 int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out);
-int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows);
+int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows,
+                  uint32_t* hist, int hist_cap);
 int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_t K, uint64_t seed, uint64_t tensor,
                float sd);
 int synth_bf16(ih_ctx* c, uint16_t* out, size_t n, uint64_t seed, uint64_t tensor, float base, float amp);
@@ -243,15 +244,19 @@ static int ensure_partials(ih_model* m, int splits) {
   return IH_OK;
 }
 
-// The sequence of one verify step on B rows whose tokens are in tok (device); top1 → top1 (device).
-static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t* top1) {
+// The sequence of one verify step on B rows whose tokens are in tok (device); top1 → top1 (device). The step's position
+// is the host kv->P, or with st (chained rounds) st[0] on the device, known to lie in [pos_min, pos_max] (the launches
+// are sized for that range; st[7] is set to 1 if it does not).
+static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t* top1, uint32_t* st = nullptr,
+                    int pos_min = -1, int pos_max = -1) {
   ih_ctx* c = m->ctx;
   const auto& d = m->d;
   const int H = d.hidden, QH = d.n_q_heads, KVH = d.n_kv_heads, HD = d.head_dim, I = d.intermediate;
+  if (!st) pos_min = pos_max = kv->P;
   // The block's rows and the first RMSNorm input.
   IH_TRY(launch_embed_act(c, tok, m->emb_w, m->emb_s, m->emb_b, m->h, B, H, d.vocab, m->layers[0].attn_norm,
-                          m->act_attn, m->rope, kv->P, d.rope_theta, HD / 2));
-  const int total = kv->P + B;
+                          m->act_attn, m->rope, kv->P, d.rope_theta, HD / 2, st, pos_max));
+  const int total = pos_max + B;
   for (int l = 0; l < d.n_layers; ++l) {
     const ih_layer& L = m->layers[l];
     // Attention: q|k|v = r · (bf16(h ⊙ w_attn) · Wqkvᵀ).
@@ -274,7 +279,11 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
     a.ring = kv->ring[l];
     a.cap = a.ring ? a.ring : kv->cap;  // slots per head of this layer's cache (the ring of a sliding-window layer)
     a.vld = v_row(a.cap);
-    a.P = kv->P;
+    a.P = pos_max;
+    a.pos_dev = st;
+    a.flag_dev = st ? st + 7 : nullptr;
+    a.pos_min = pos_min;
+    a.pos_max = pos_max;
     a.B = B;
     a.QH = QH;
     a.KVH = KVH;
@@ -283,7 +292,9 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
     a.Qpad = m->Qpad;
     a.C = kv->chunk;
     a.window = a.ring ? d.sliding_window : 0;
-    a.s0 = a.window ? std::max(0, kv->P - a.window + 1) / a.C : 0;
+    // Launched splits: from the first split of the lowest position's window to the last key of the highest position
+    // (one position on the host path).
+    a.s0 = a.window ? std::max(0, pos_min - a.window + 1) / a.C : 0;
     a.nsplit = (total + a.C - 1) / a.C - a.s0;
     a.hadk = d.hadamard_k;
     a.theta = d.rope_theta;
@@ -344,7 +355,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
   IH_TRY(launch_qmm_ex(c, m->head, 0, m->act_attn, B, eh));
   IH_TRY(launch_argmax(c, m->logits, d.vocab, B, d.vocab, top1));
   kv->last_B = B;
-  kv->written = std::max(kv->written, kv->P + B);
+  kv->written = std::max(kv->written, pos_max + B);
   return IH_OK;
 }
 
@@ -591,6 +602,20 @@ int ih_verify_step_dev(ih_model* m, ih_kv* kv, const uint32_t* tokens_dev, int B
   return IH_OK;
 }
 
+int ih_verify_step_chained(ih_model* m, ih_kv* kv, const uint32_t* tokens_dev, int B, uint32_t* top1_dev,
+                           uint32_t* st_dev, int pos_min, int pos_max) {
+  IH_CHECK(m && kv && kv->model == m, IH_EINVAL, "ih_verify_step_chained: model and cache do not belong together");
+  IH_CHECK(tokens_dev && top1_dev && st_dev, IH_EINVAL, "ih_verify_step_chained: null buffer");
+  IH_CHECK(B >= 1 && B <= IH_MAX_ROWS, IH_EINVAL, "ih_verify_step_chained: B must be in 1..17");
+  IH_CHECK(pos_min >= 0 && pos_min <= pos_max, IH_EINVAL, "ih_verify_step_chained: need 0 <= pos_min <= pos_max");
+  IH_CHECK(pos_max + B <= kv->cap, IH_EINVAL,
+           "ih_verify_step_chained: context overflow (pos_max + B = " + std::to_string(pos_max + B) + " > capacity " +
+               std::to_string(kv->cap) + ")");
+  return run_step(m, kv, B, tokens_dev, top1_dev, st_dev, pos_min, pos_max);
+}
+
+int ih_kv_capacity(const ih_kv* kv) { return kv ? kv->cap : 0; }
+
 int ih_verify_step(ih_model* m, ih_kv* kv, const uint32_t* tokens, int B, float* logits_out, uint32_t* top1_out) {
   IH_TRY(check_step(m, kv, B));
   IH_CHECK(tokens && top1_out, IH_EINVAL, "ih_verify_step: null buffer");
@@ -625,3 +650,8 @@ int ih_model_moe_union(const ih_model* m, int* u_out) {
 const float* ih_model_logits_dev(const ih_model* m) { return m ? m->logits : nullptr; }
 
 }  // extern "C"
+
+namespace ih {
+ih_ctx* model_ctx(const ih_model* m) { return m->ctx; }
+const ih_model_desc& model_desc(const ih_model* m) { return m->d; }
+}  // namespace ih

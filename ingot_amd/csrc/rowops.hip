@@ -17,9 +17,11 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
                                                         float* __restrict__ h, int H, int ldh,
                                                         const uint16_t* __restrict__ nw, uint4* __restrict__ frag,
                                                         int nkb, int ntile, float* __restrict__ ss_out, int V,
-                                                        float2* __restrict__ rope, int P, float theta, int RH) {
+                                                        float2* __restrict__ rope, int P, float theta, int RH,
+                                                        const uint32_t* __restrict__ pos_dev, int pos_max) {
   __shared__ float red[4];
   const int row = blockIdx.x;
+  if (pos_dev) P = int(min(pos_dev[0], uint32_t(pos_max)));  // chained rounds: the position of the round state
   for (int i = threadIdx.x; i < RH; i += blockDim.x) {
     const double ang = double(P + row) * pow(double(theta), -double(i) / double(RH));
     rope[row * RH + i] = make_float2(float(cos(ang)), float(sin(ang)));
@@ -150,7 +152,8 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float2* __restri
 // Greedy acceptance on the device, one thread: m = drafts vtok[1..m] that equal top1[0..m−1]; rec[round % ring] = (m,
 // emitted tokens, REC_P = P before, REC_ROWS = rows); st = [P, nacc, pend, pendPos, anchor, round, rows] advanced:
 // P += m + 1 (the commit), anchor = top1[m], vtok[0] = anchor. spec_accept, Shaders/yy_model.metal:616-642.
-__global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows) {
+__global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows,
+                              uint32_t* hist, int hist_cap) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
   // Rows from the round state (rows = 0) are clamped to 1…IH_MAX_ROWS: vtok, top1 and a record hold at most that many.
   const uint32_t nr = rows ? uint32_t(rows) : min(max(st[6], 1u), uint32_t(IH_MAX_ROWS));
@@ -169,15 +172,23 @@ __global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1
   st[4] = top1[m];
   st[5] += 1;
   vtok[0] = top1[m];
+  // The token history of the copy drafter (hist[i] = token at position i, the anchor last): the emitted tokens go to
+  // the positions after the old anchor (the dtok write of the reference, the drafter's side of the round).
+  if (hist) {
+    const uint32_t p0 = st[3];  // P before this round
+    for (uint32_t i = 0; i < m; ++i)
+      if (p0 + 1 + i < uint32_t(hist_cap)) hist[p0 + 1 + i] = vtok[1 + i];
+    if (p0 + 1 + m < uint32_t(hist_cap)) hist[p0 + 1 + m] = top1[m];
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                      float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a, float2* rope, int P, float theta,
-                     int RH) {
+                     int RH, const uint32_t* pos_dev, int pos_max) {
   TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4 + 2));
   tlaunch(tl, embed_act_kernel, dim3(B), dim3(256), 0, c->stream, tok, w, s, b, h, H, H, nw, static_cast<uint4*>(a.frag),
-          a.nkb, a.ntile, a.ss, V, rope, P, theta, RH);
+          a.nkb, a.ntile, a.ss, V, rope, P, theta, RH, pos_dev, pos_max);
   IH_HIP(hipGetLastError());
   a.nss = 1;
   return IH_OK;
@@ -207,8 +218,9 @@ int init_noalloc_scratch(ih_ctx* c) {
   return IH_OK;
 }
 
-int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows) {
-  accept_kernel<<<1, 64, 0, c->stream>>>(st, vtok, top1, rec, ring, rows);
+int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows,
+                  uint32_t* hist, int hist_cap) {
+  accept_kernel<<<1, 64, 0, c->stream>>>(st, vtok, top1, rec, ring, rows, hist, hist_cap);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
@@ -258,7 +270,7 @@ int ih_spec_accept_dev(ih_ctx* c, uint32_t* st_dev, uint32_t* vtok_dev, const ui
                        int ring, int rows) {
   IH_CHECK(c && st_dev && vtok_dev && top1_dev && rec_dev, IH_EINVAL, "ih_spec_accept_dev: null argument");
   IH_CHECK(ring >= 1 && rows >= 0 && rows <= IH_MAX_ROWS, IH_EINVAL, "ih_spec_accept_dev: bad ring or rows");
-  return launch_accept(c, st_dev, vtok_dev, top1_dev, rec_dev, ring, rows);
+  return launch_accept(c, st_dev, vtok_dev, top1_dev, rec_dev, ring, rows, nullptr, 0);
 }
 
 }  // extern "C"

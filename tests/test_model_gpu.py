@@ -203,3 +203,25 @@ def test_commit_and_chained_rounds_match_plain_decode(ctx):
     finally:
         kv.free()
         m.free()
+
+
+@pytest.mark.parametrize("chunk", [96, 64, 0])
+def test_sliding_window_rows_are_block_invariant(ctx, chunk):
+    """In a sliding-window layer with sinks, row i of a block verified at P has the same logit bits as the same token
+    decoded alone at P + i after the block's first i rows were committed (the reference's 'same bits whatever the
+    block', verify_attn_pf.metal:41-45): the window's split and its pieces do not depend on the block's P, and the sink
+    merges after the splits."""
+    d, m, kv = make(ctx, SWA, P=1500, cap=1600, chunk=chunk)
+    try:
+        toks = np.random.default_rng(chunk + 5).integers(0, d.vocab, size=17).astype(np.uint32)
+        _, full = kv.verify(toks, want_logits=True)
+        for i in (1, 5, 12, 16):
+            kv.set_pos(1500)
+            kv.verify(toks[:i])
+            kv.commit(i)
+            _, one = kv.verify(toks[i: i + 1], want_logits=True)
+            assert np.array_equal(one[0].view(np.uint32), full[i].view(np.uint32)), i
+        kv.set_pos(1500)
+    finally:
+        kv.free()
+        m.free()
