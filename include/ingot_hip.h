@@ -154,12 +154,26 @@ typedef struct ih_model_desc {
   int sliding_window;                  /* 0 = none; > 0: even layers use this window (counting the row's own key) */
   int sinks;                           /* learned attention sinks, one logit per q head */
   int hadamard_k;                      /* store H·k and rotate q (the reference's default "hadk" scheme) */
+  int qk_norm;                         /* per-head RMSNorm of q and k before RoPE, weights [head_dim] (Qwen3) */
+  int qkv_bias;                        /* bias added to the q|k|v projection (Qwen2) */
 } ih_model_desc;
 
 /* Creates a model with synthetic weights of `desc`'s shapes, deterministically from `seed` (counter-based SplitMix64
  * streams per tensor; any element is reproducible on the CPU). Replaces HybridModel's loader for the benchmark
  * configurations (Sources/Ingot/Model.swift); an MLX safetensors loader is a later addition. */
 int ih_model_create_synthetic(ih_ctx* ctx, const ih_model_desc* desc, uint64_t seed, ih_model** out);
+/* Loads an mlx-lm quantized checkpoint directory (config.json + model.safetensors, or shards listed in
+ * model.safetensors.index.json; mapped with mmap): the loader of HybridModel (SafetensorsStore,
+ * Sources/Ingot/Loader/Safetensors.swift:1-248; QuantizedLinear, Loader/Quant.swift:13-88; DenseQ's q|k|v and gate|up
+ * row concatenation, Layers/Linear.swift:107-183; ModelConfig, Loader/Config.swift). Layer names of mlx-lm
+ * (model.layers.N.self_attn.{q,k,v,o}_proj, input_layernorm, post_attention_layernorm, mlp.{gate,up,down}_proj; MoE:
+ * mlp.gate + mlp.switch_mlp.{gate,up,down}_proj), lm_head or tied embeddings. Runs what the verify step runs: MLX
+ * affine 4-bit g64 (MXFP4 g32 experts), optional QK-norm (q_norm/k_norm) and q|k|v bias, a dense SwiGLU or a
+ * renormalised softmax top-k MoE; anything else (other bits, rope scaling, shared experts, o_proj bias, …) is
+ * IH_EINVAL with the reason in ih_last_error(). */
+int ih_model_load_mlx(ih_ctx* ctx, const char* dir, ih_model** out);
+/* The description ih_model_load_mlx would build, after checking the checkpoint's tensors; host only (no device). */
+int ih_mlx_describe(const char* dir, ih_model_desc* out);
 int ih_model_free(ih_model* model);
 /* Algorithmic bytes of the model's weights read by one verify step (all layers, head), MLX format. For MoE models the
  * experts count once per distinct routed expert, so this returns the dense part only. */

@@ -110,6 +110,8 @@ def _declare(L: C.CDLL) -> None:
         "ih_verify_step_chained": (i32, [vp, vp, vp, i32, vp, vp, i32, i32]),
         "ih_kv_capacity": (i32, [vp]),
         "ih_decode_greedy": (i32, [vp, vp, vp, i32, C.c_uint32, vp, vp, i32, P(i32), vp]),
+        "ih_model_load_mlx": (i32, [vp, C.c_char_p, P(vp)]),
+        "ih_mlx_describe": (i32, [C.c_char_p, vp]),
         "ih_timing_enable": (i32, [vp, i32]),
         "ih_timing_read": (i32, [vp, i32, P(C.c_double), P(C.c_int), P(C.c_double)]),
     }
@@ -300,6 +302,7 @@ class ModelDesc(C.Structure):
         ("rms_eps", C.c_float), ("n_experts", C.c_int), ("top_k", C.c_int), ("expert_intermediate", C.c_int),
         ("expert_format", C.c_int), ("router_bias", C.c_int), ("expert_bias", C.c_int), ("act", C.c_int),
         ("swiglu_limit", C.c_float), ("sliding_window", C.c_int), ("sinks", C.c_int), ("hadamard_k", C.c_int),
+        ("qk_norm", C.c_int), ("qkv_bias", C.c_int),
     ]
 
     @classmethod
@@ -345,6 +348,17 @@ class Model:
         check(lib().ih_model_create_synthetic(ctx.handle, C.byref(desc), seed, C.byref(h)))
         self.handle = h.value
 
+    @classmethod
+    def load_mlx(cls, ctx: Context, directory) -> "Model":
+        """An mlx-lm 4-bit checkpoint directory (ih_model_load_mlx)."""
+        d = describe_mlx(directory)
+        self = cls.__new__(cls)
+        self.ctx, self.desc, self.seed = ctx, d, None
+        h = vp()
+        check(lib().ih_model_load_mlx(ctx.handle, str(directory).encode(), C.byref(h)))
+        self.handle = h.value
+        return self
+
     @property
     def weight_bytes(self) -> int:
         return lib().ih_model_weight_bytes(self.handle)
@@ -353,6 +367,13 @@ class Model:
         if self.handle:
             lib().ih_model_free(self.handle)
             self.handle = None
+
+
+def describe_mlx(directory) -> ModelDesc:
+    """The model description of an mlx-lm checkpoint directory (ih_mlx_describe; host only)."""
+    d = ModelDesc()
+    check(lib().ih_mlx_describe(str(directory).encode(), C.byref(d)))
+    return d
 
 
 class KVCache:

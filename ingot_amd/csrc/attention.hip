@@ -67,6 +67,26 @@ __global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
   float x[NE];
 #pragma unroll
   for (int e = 0; e < NE; ++e) x[e] = row[lane + 64 * e];
+  if (a.qkv_bias) {
+#pragma unroll
+    for (int e = 0; e < NE; ++e) x[e] += a.qkv_bias[slot * HD + lane + 64 * e];
+  }
+  if ((isq || isk) && a.qnorm) {
+    // QK-norm: x · rsqrt(mean x² + eps) · w over the head, before RoPE (the AT_QKN branch of vattn_prework_i8).
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) ss += x[e] * x[e];
+    ss += lane_xor<32>(ss);
+    ss += lane_xor<16>(ss);
+    ss += lane_xor<8>(ss);
+    ss += lane_xor<4>(ss);
+    ss += lane_xor<2>(ss);
+    ss += lane_xor<1>(ss);
+    const float r = rsqrtf(ss / float(HD) + a.eps);
+    const uint16_t* w = isq ? a.qnorm : a.knorm;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) x[e] = x[e] * r * dbf16(w[lane + 64 * e]);
+  }
   if (isq || isk) {
     const float2 cs = a.rope[t * RH + (lane % RH)];
     if constexpr (NE == 2) {

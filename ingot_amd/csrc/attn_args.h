@@ -28,6 +28,10 @@ struct AttnArgs {
   __half* ks;          // [KVH][cap]
   __half* vs;          // [KVH][cap]
   const float* sinks;  // [QH] natural-log logits or null
+  const uint16_t* qnorm;    // [HD] bf16 weights of the per-head RMSNorm of q (QK-norm) or null
+  const uint16_t* knorm;    // [HD] the same for k
+  const float* qkv_bias;    // [QP] bias of the q|k|v projection or null
+  float eps;                // RMSNorm eps of the QK-norm
   __half* opart;       // [KVH][nsplit][Qpad][HD] fp16 O/l of each split (nsplit = launched splits)
   float2* ml;          // [KVH][nsplit][Qpad] (running max in log2 units, sum)
   int cap, ring, P, B, QH, KVH, HD, G, Qpad;  // cap: slots per head (the ring size of a sliding-window layer)

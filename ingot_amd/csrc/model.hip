@@ -12,6 +12,7 @@
 #include "act.h"
 #include "attn_args.h"
 #include "ih_internal.h"
+#include "model_internal.h"
 
 namespace ih {
 
@@ -26,7 +27,6 @@ int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_
                float sd);
 int synth_bf16(ih_ctx* c, uint16_t* out, size_t n, uint64_t seed, uint64_t tensor, float base, float amp);
 int synth_mxfp4(ih_ctx* c, uint32_t* w, uint8_t* s, size_t N, size_t K, uint64_t seed, uint64_t tensor);
-int qmat_mxfp4_create_dev(ih_ctx* c, const void* w, const void* s, int E, int N, int K, int il8, ih_qmat** out);
 struct GatherParams;
 int synth_f32(ih_ctx* c, float* out, size_t n, uint64_t seed, uint64_t tensor, float base, float amp);
 int synth_kv(ih_ctx* c, int8_t* kc, int8_t* vc, __half* ks, __half* vs, int KVH, int HD, int cap, int ring, int pos0,
@@ -49,7 +49,7 @@ int launch_moe_down(ih_ctx* c, const ih_qmat* W, const void* h_frag, int h_nkb, 
 // Tensor ids of the synthetic model (the generator's stream keys): globals, then 100 per layer.
 enum : uint64_t { T_EMBED = 1, T_FINAL_NORM = 2, T_HEAD = 3 };
 enum : uint64_t { L_ATTN_NORM = 0, L_QKV = 1, L_O = 2, L_MLP_NORM = 3, L_GATE_UP = 4, L_DOWN = 5, L_ROUTER = 6,
-                  L_ROUTER_BIAS = 7, L_SINKS = 9 };
+                  L_ROUTER_BIAS = 7, L_SINKS = 9, L_Q_NORM = 10, L_K_NORM = 11, L_QKV_BIAS = 12 };
 constexpr uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
 // Experts: 3·10^6 + 10^4·layer + 10^3·kind + expert (kinds: gate|up, down, gate|up bias, down bias).
 enum : uint64_t { X_GATE_UP = 0, X_DOWN = 1, X_GU_BIAS = 2, X_DOWN_BIAS = 3 };
@@ -62,69 +62,6 @@ constexpr float W_SD = 0.02f;  // |N(0, 0.02)| scales
 }  // namespace ih
 
 using namespace ih;
-
-struct ih_layer {
-  uint16_t* attn_norm = nullptr;
-  uint16_t* mlp_norm = nullptr;
-  float* sinks = nullptr;
-  ih_qmat* qkv = nullptr;
-  ih_qmat* o = nullptr;
-  // Dense FFN: gate|up [2I][H] (interleaved by eights), down [H][I]. MoE: the same, stacked over E experts (I = the
-  // expert intermediate), plus the router [E][H] in the experts' format and the optional biases.
-  ih_qmat* gate_up = nullptr;
-  ih_qmat* down = nullptr;
-  ih_qmat* router = nullptr;
-  float* router_bias = nullptr;   // [E]
-  uint16_t* gu_bias = nullptr;    // bf16 [E][2I] (gate then up)
-  uint16_t* down_bias = nullptr;  // bf16 [E][H]
-};
-
-struct ih_model {
-  ih_ctx* ctx = nullptr;
-  ih_model_desc d{};
-  uint64_t seed = 0;
-  std::vector<ih_layer> layers;
-  // Embedding table in MLX int4 layout (a row gather), final norm, head.
-  uint32_t* emb_w = nullptr;
-  uint16_t* emb_s = nullptr;
-  uint16_t* emb_b = nullptr;
-  uint16_t* final_norm = nullptr;
-  ih_qmat* head = nullptr;
-  // Scratch of one step.
-  float* h = nullptr;        // residual [MAX_TOK][H]
-  float* proj = nullptr;     // qkv output [MAX_TOK][QP]
-  float* logits = nullptr;   // [MAX_TOK][V]
-  uint32_t* tok = nullptr;   // [MAX_TOK]
-  uint32_t* top1 = nullptr;  // [MAX_TOK]
-  __half* q = nullptr;       // [KVH][Qpad][HD]
-  float2* rope = nullptr;    // [IH_MAX_ROWS][HD/2] (cos, sin) of the step's positions
-  // Activations: RMSNorm inputs bf16(h ⊙ w) with their sums of squares (attention / final norm, FFN norm), the
-  // attention output and the gated activation.
-  ActBuf act_attn, act_mlp, act_o, act_i;
-  __half* opart = nullptr;
-  float2* ml = nullptr;
-  size_t part_splits = 0;    // splits the attention partials can hold
-  int Qpad = 0, QP = 0;
-  // MoE scratch: router logits [MAX_TOK][E], the routing of the round, the pairs' gated activations (fragments, one
-  // "token" per pair) and their down outputs [pairs][H].
-  float* rlogits = nullptr;
-  int* nent = nullptr;
-  int* entries = nullptr;
-  int* x_row = nullptr;
-  float* pair_w = nullptr;
-  int* row_pair = nullptr;
-  void* hpair = nullptr;
-  float* opair = nullptr;
-  int hpair_nkb = 0, max_pairs = 0;
-};
-
-struct ih_kv {
-  ih_model* model = nullptr;
-  int cap = 0, P = 0, written = 0, last_B = 0, chunk = 256;
-  std::vector<int8_t*> kc, vc;
-  std::vector<__half*> ks, vs;
-  std::vector<int> ring;   // per layer: ring slots (sliding-window layers) or 0
-};
 
 namespace ih {
 
@@ -192,7 +129,55 @@ static int synth_stack(ih_ctx* c, Staging& st, int fmt, int E, int N, int K, uin
   return qmat_int4_create_dev(c, st.w, st.s, st.b, E, N, K, il8, out);
 }
 
-static int check_desc(const ih_model_desc& d) {
+ih_model* model_new(ih_ctx* c, const ih_model_desc& d) {
+  ih_model* m = new ih_model();
+  m->ctx = c;
+  m->d = d;
+  m->QP = (d.n_q_heads + 2 * d.n_kv_heads) * d.head_dim;
+  m->Qpad = (d.n_q_heads / d.n_kv_heads * IH_MAX_ROWS + 15) / 16 * 16;
+  m->layers.resize(d.n_layers);
+  return m;
+}
+
+int model_alloc_scratch(ih_model* m) {
+  ih_ctx* c = m->ctx;
+  const auto& d = m->d;
+  const int H = d.hidden, QH = d.n_q_heads, KVH = d.n_kv_heads, HD = d.head_dim, I = d.intermediate, V = d.vocab;
+  int st = IH_OK;
+  auto run = [&](int s) { if (st == IH_OK) st = s; };
+  run(dalloc_t(&m->h, size_t(MAX_TOK) * H));
+  run(dalloc_t(&m->proj, size_t(MAX_TOK) * m->QP));
+  run(dalloc_t(&m->logits, size_t(MAX_TOK) * V));
+  run(dalloc_t(&m->tok, MAX_TOK));
+  run(dalloc_t(&m->top1, MAX_TOK));
+  run(dalloc_t(&m->q, size_t(KVH) * m->Qpad * HD));
+  run(dalloc_t(&m->rope, size_t(IH_MAX_ROWS) * (HD / 2)));
+  const bool moe = d.n_experts > 0, moe_f16 = moe && d.expert_format == QF_MXFP4;
+  if (st == IH_OK) run(ensure_act(c, m->act_attn, H, false));
+  if (st == IH_OK) run(ensure_act(c, m->act_mlp, H, moe_f16));
+  if (st == IH_OK) run(ensure_act(c, m->act_o, QH * HD, false));
+  if (st == IH_OK && !moe) run(ensure_act(c, m->act_i, I, false));
+  if (moe) {
+    const int E = d.n_experts, IE = d.expert_intermediate;
+    m->max_pairs = (IH_MAX_ROWS * d.top_k + 15) / 16 * 16;  // pair "tokens" of the fragment layout, whole tiles
+    m->hpair_nkb = (IE + KBLK - 1) / KBLK;
+    run(dalloc_t(&m->rlogits, size_t(MAX_TOK) * E));
+    run(dalloc_t(&m->nent, d.n_layers));
+    run(dalloc_t(&m->entries, size_t(3) * E));
+    run(dalloc_t(&m->x_row, m->max_pairs));
+    run(dalloc_t(&m->pair_w, m->max_pairs));
+    run(dalloc_t(&m->row_pair, m->max_pairs));
+    const size_t hb = size_t(m->max_pairs) * m->hpair_nkb * 256;
+    run(dalloc(&m->hpair, hb));
+    run(dalloc_t(&m->opair, size_t(m->max_pairs) * H));
+    if (st == IH_OK) run(fill(c, m->hpair, 0, hb));
+  }
+  if (st == IH_OK) run(fill(c, m->q, 0, size_t(KVH) * m->Qpad * HD * 2));
+  if (st == IH_OK) run(hipStreamSynchronize(c->stream) == hipSuccess ? IH_OK : fail(IH_EDEVICE, "model: init failed"));
+  return st;
+}
+
+int check_desc(const ih_model_desc& d) {
   IH_CHECK(d.n_layers >= 1 && d.hidden >= 64 && d.hidden % 64 == 0, IH_EINVAL, "model: hidden must be a multiple of 64");
   IH_CHECK(d.head_dim == 64 || d.head_dim == 128, IH_EINVAL, "model: head_dim must be 64 or 128");
   IH_CHECK(d.n_kv_heads >= 1 && d.n_q_heads % d.n_kv_heads == 0, IH_EINVAL, "model: q heads must be a multiple of kv heads");
@@ -214,11 +199,12 @@ static int check_desc(const ih_model_desc& d) {
   return IH_OK;
 }
 
-static void model_release(ih_model* m) {
+void model_release(ih_model* m) {
   if (!m) return;
   for (auto& L : m->layers) {
     ih_qmat_free(L.qkv); ih_qmat_free(L.o); ih_qmat_free(L.gate_up); ih_qmat_free(L.down); ih_qmat_free(L.router);
-    void* lp[] = {L.attn_norm, L.mlp_norm, L.sinks, L.router_bias, L.gu_bias, L.down_bias};
+    void* lp[] = {L.attn_norm, L.mlp_norm, L.sinks, L.router_bias, L.gu_bias, L.down_bias, L.q_norm, L.k_norm,
+                  L.qkv_bias};
     for (void* p : lp)
       if (p) (void)hipFree(p);
   }
@@ -276,6 +262,10 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
     a.ks = kv->ks[l];
     a.vs = kv->vs[l];
     a.sinks = L.sinks;
+    a.qnorm = L.q_norm;
+    a.knorm = L.k_norm;
+    a.qkv_bias = L.qkv_bias;
+    a.eps = d.rms_eps;
     a.ring = kv->ring[l];
     a.cap = a.ring ? a.ring : kv->cap;  // slots per head of this layer's cache (the ring of a sliding-window layer)
     a.vld = v_row(a.cap);
@@ -375,19 +365,14 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
   IH_CHECK(c && desc && out, IH_EINVAL, "ih_model_create_synthetic: null argument");
   *out = nullptr;
   IH_TRY(check_desc(*desc));
-  ih_model* m = new ih_model();
-  m->ctx = c;
-  m->d = *desc;
+  ih_model* m = model_new(c, *desc);
   m->seed = seed;
   const auto& d = m->d;
-  const int H = d.hidden, QH = d.n_q_heads, KVH = d.n_kv_heads, HD = d.head_dim, I = d.intermediate, V = d.vocab;
-  m->QP = (QH + 2 * KVH) * HD;
-  m->Qpad = (QH / KVH * IH_MAX_ROWS + 15) / 16 * 16;
+  const int H = d.hidden, QH = d.n_q_heads, HD = d.head_dim, I = d.intermediate, V = d.vocab;
   int st = IH_OK;
   auto run = [&](int s) { if (st == IH_OK) st = s; };
   {
     Staging stg;
-    m->layers.resize(d.n_layers);
     for (int l = 0; l < d.n_layers && st == IH_OK; ++l) {
       ih_layer& L = m->layers[l];
       run(dalloc_t(&L.attn_norm, H));
@@ -398,6 +383,16 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
       if (d.sinks) {
         run(dalloc_t(&L.sinks, QH));
         if (st == IH_OK) run(synth_f32(c, L.sinks, QH, seed, layer_tensor(l, L_SINKS), 0.0f, 1.0f));
+      }
+      if (d.qk_norm) {
+        run(dalloc_t(&L.q_norm, HD));
+        run(dalloc_t(&L.k_norm, HD));
+        if (st == IH_OK) run(synth_bf16(c, L.q_norm, HD, seed, layer_tensor(l, L_Q_NORM), 1.0f, 0.125f));
+        if (st == IH_OK) run(synth_bf16(c, L.k_norm, HD, seed, layer_tensor(l, L_K_NORM), 1.0f, 0.125f));
+      }
+      if (d.qkv_bias) {
+        run(dalloc_t(&L.qkv_bias, m->QP));
+        if (st == IH_OK) run(synth_f32(c, L.qkv_bias, m->QP, seed, layer_tensor(l, L_QKV_BIAS), 0.0f, 0.1f));
       }
       run(synth_qmat(c, stg, m->QP, H, seed, layer_tensor(l, L_QKV), W_SD, &L.qkv));
       run(synth_qmat(c, stg, H, QH * HD, seed, layer_tensor(l, L_O), W_SD, &L.o));
@@ -436,35 +431,7 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
   run(dalloc_t(&m->final_norm, H));
   if (st == IH_OK) run(synth_int4(c, m->emb_w, m->emb_s, m->emb_b, V, H, seed, T_EMBED, W_SD));
   if (st == IH_OK) run(synth_bf16(c, m->final_norm, H, seed, T_FINAL_NORM, 1.0f, 0.125f));
-  run(dalloc_t(&m->h, size_t(MAX_TOK) * H));
-  run(dalloc_t(&m->proj, size_t(MAX_TOK) * m->QP));
-  run(dalloc_t(&m->logits, size_t(MAX_TOK) * V));
-  run(dalloc_t(&m->tok, MAX_TOK));
-  run(dalloc_t(&m->top1, MAX_TOK));
-  run(dalloc_t(&m->q, size_t(KVH) * m->Qpad * HD));
-  run(dalloc_t(&m->rope, size_t(IH_MAX_ROWS) * (HD / 2)));
-  const bool moe = d.n_experts > 0, moe_f16 = moe && d.expert_format == QF_MXFP4;
-  if (st == IH_OK) run(ensure_act(c, m->act_attn, H, false));
-  if (st == IH_OK) run(ensure_act(c, m->act_mlp, H, moe_f16));
-  if (st == IH_OK) run(ensure_act(c, m->act_o, QH * HD, false));
-  if (st == IH_OK && !moe) run(ensure_act(c, m->act_i, I, false));
-  if (moe) {
-    const int E = d.n_experts, IE = d.expert_intermediate;
-    m->max_pairs = (IH_MAX_ROWS * d.top_k + 15) / 16 * 16;  // pair "tokens" of the fragment layout, whole tiles
-    m->hpair_nkb = (IE + KBLK - 1) / KBLK;
-    run(dalloc_t(&m->rlogits, size_t(MAX_TOK) * E));
-    run(dalloc_t(&m->nent, d.n_layers));
-    run(dalloc_t(&m->entries, size_t(3) * E));
-    run(dalloc_t(&m->x_row, m->max_pairs));
-    run(dalloc_t(&m->pair_w, m->max_pairs));
-    run(dalloc_t(&m->row_pair, m->max_pairs));
-    const size_t hb = size_t(m->max_pairs) * m->hpair_nkb * 256;
-    run(dalloc(&m->hpair, hb));
-    run(dalloc_t(&m->opair, size_t(m->max_pairs) * H));
-    if (st == IH_OK) run(fill(c, m->hpair, 0, hb));
-  }
-  if (st == IH_OK) run(fill(c, m->q, 0, size_t(KVH) * m->Qpad * HD * 2));
-  if (st == IH_OK) run(hipStreamSynchronize(c->stream) == hipSuccess ? IH_OK : fail(IH_EDEVICE, "model: init failed"));
+  if (st == IH_OK) run(model_alloc_scratch(m));
   if (st != IH_OK) {
     model_release(m);
     return st;

@@ -419,7 +419,7 @@ struct or_model_desc {
   float rope_theta, rms_eps;
   int n_experts, top_k, expert_intermediate, expert_format, router_bias, expert_bias, act;
   float swiglu_limit;
-  int sliding_window, sinks, hadamard_k;
+  int sliding_window, sinks, hadamard_k, qk_norm, qkv_bias;
 };
 
 static uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
@@ -467,8 +467,8 @@ struct AnyMat {
 static uint64_t expert_tensor(int l, uint64_t kind, int e) { return 3000000 + 10000 * uint64_t(l) + 1000 * kind + e; }
 
 struct OrLayer {
-  std::vector<uint16_t> attn_norm, mlp_norm;
-  std::vector<float> sinks;
+  std::vector<uint16_t> attn_norm, mlp_norm, q_norm, k_norm;
+  std::vector<float> sinks, qkv_bias;
   QMat qkv, o, gate_up, down;
   // MoE: router [E][H], per expert gate|up [2I][H] (gate rows then up rows) and down [H][I], optional biases.
   AnyMat router;
@@ -511,6 +511,16 @@ void* or_model_create(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, i
     if (d->sinks) {
       L.sinks.resize(QH);
       or_synth_f32(seed, layer_tensor(l, 9), QH, 0.0f, 1.0f, L.sinks.data());
+    }
+    if (d->qk_norm) {
+      L.q_norm.resize(HD);
+      L.k_norm.resize(HD);
+      or_synth_bf16(seed, layer_tensor(l, 10), HD, 1.0f, 0.125f, L.q_norm.data());
+      or_synth_bf16(seed, layer_tensor(l, 11), HD, 1.0f, 0.125f, L.k_norm.data());
+    }
+    if (d->qkv_bias) {
+      L.qkv_bias.resize(QP);
+      or_synth_f32(seed, layer_tensor(l, 12), QP, 0.0f, 0.1f, L.qkv_bias.data());
     }
     L.qkv.make(seed, layer_tensor(l, 1), QP, H, sd);
     L.o.make(seed, layer_tensor(l, 2), H, QH * HD, sd);
@@ -637,6 +647,20 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
     or_rms_split(hres.data(), B, H, L.attn_norm.data(), d->rms_eps, x.data(), rr.data());
     L.qkv.apply(x.data(), B, proj.data());
     scale_rows(proj.data(), B, QP, rr.data());
+    // q|k|v bias, then the per-head RMSNorm of q and k (vattn_prework_i8's AT_QKVB and AT_QKN, verify_attn_nax.metal:
+    // 76-89), before RoPE.
+    for (int t = 0; t < B && !L.qkv_bias.empty(); ++t)
+      for (int i = 0; i < QP; ++i) proj[size_t(t) * QP + i] += L.qkv_bias[i];
+    if (!L.q_norm.empty())
+      for (int t = 0; t < B; ++t)
+        for (int hh = 0; hh < QH + KVH; ++hh) {
+          float* xr = proj.data() + size_t(t) * QP + size_t(hh) * HD;
+          double ss = 0;
+          for (int dd = 0; dd < HD; ++dd) ss += double(xr[dd]) * xr[dd];
+          const float r = 1.0f / std::sqrt(float(ss) / float(HD) + d->rms_eps);
+          const uint16_t* w = hh < QH ? L.q_norm.data() : L.k_norm.data();
+          for (int dd = 0; dd < HD; ++dd) xr[dd] = xr[dd] * r * or_bf16_to_f32(w[dd]);
+        }
     for (int t = 0; t < B; ++t) {
       const float* pr = proj.data() + size_t(t) * QP;
       for (int hh = 0; hh < QH; ++hh) {

@@ -27,6 +27,7 @@ import oracle
 
 T_EMBED, T_FINAL_NORM, T_HEAD = 1, 2, 3
 L_ATTN_NORM, L_QKV, L_O, L_MLP_NORM, L_GATE_UP, L_DOWN, L_ROUTER, L_ROUTER_BIAS, L_SINKS = 0, 1, 2, 3, 4, 5, 6, 7, 9
+L_Q_NORM, L_K_NORM, L_QKV_BIAS = 10, 11, 12
 X_GATE_UP, X_DOWN, X_GU_BIAS, X_DOWN_BIAS = 0, 1, 2, 3
 
 
@@ -146,7 +147,7 @@ def route(logits, k):
 
 
 def forward(desc, seed: int, kv_seed: int, P: int, tokens, mutate: str | None = None):
-    """Logits [B][vocab] in float64. mutate ∈ {None, "residual", "norm", "gqa", "renorm", "slots"} breaks one piece."""
+    """Logits [B][vocab] in float64. mutate ∈ {None, "residual", "norm", "gqa", "renorm", "slots", "qknorm", "qkvbias"} breaks one piece."""
     d = desc
     H, QH, KVH, HD, V = d.hidden, d.n_q_heads, d.n_kv_heads, d.head_dim, d.vocab
     G = QH // KVH
@@ -161,8 +162,13 @@ def forward(desc, seed: int, kv_seed: int, P: int, tokens, mutate: str | None = 
             wa, wm = wm, wa
         x = rmsnorm(h, wa, d.rms_eps)
         proj = x @ int4_dense(seed, layer_tensor(l, L_QKV), (QH + 2 * KVH) * HD, H).T
+        if d.qkv_bias and mutate != "qkvbias":
+            proj = proj + f32(seed, layer_tensor(l, L_QKV_BIAS), (QH + 2 * KVH) * HD, 0.0, 0.1)
         q = proj[:, : QH * HD].reshape(B, QH, HD)
         k = proj[:, QH * HD: (QH + KVH) * HD].reshape(B, KVH, HD)
+        if d.qk_norm and mutate != "qknorm":  # per-head RMSNorm before RoPE (Qwen3's q_norm / k_norm)
+            q = rmsnorm(q, bf16(seed, layer_tensor(l, L_Q_NORM), HD, 1.0, 0.125), d.rms_eps)
+            k = rmsnorm(k, bf16(seed, layer_tensor(l, L_K_NORM), HD, 1.0, 0.125), d.rms_eps)
         v = proj[:, (QH + KVH) * HD:].reshape(B, KVH, HD)
         pos = P + np.arange(B)
         qr = np.stack([rope(q[t], pos[t], d.rope_theta) for t in range(B)])

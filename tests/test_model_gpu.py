@@ -61,8 +61,13 @@ def make(ctx, shape, seed=7, kv_seed=11, P=100, cap=512, chunk=0, **extra):
     return d, m, kv
 
 
-@pytest.mark.parametrize("shape", [SMALL, GQA8, SWA, MOE4, MOEX],
-                         ids=["gqa2-hd128", "gqa8-hd64", "sinks-swa", "moe-int4", "moe-mxfp4"])
+QWEN = dict(SMALL, qk_norm=1, qkv_bias=1)
+QWEN64 = dict(GQA8, qk_norm=1, qkv_bias=1)
+
+
+@pytest.mark.parametrize("shape", [SMALL, GQA8, SWA, MOE4, MOEX, QWEN, QWEN64],
+                         ids=["gqa2-hd128", "gqa8-hd64", "sinks-swa", "moe-int4", "moe-mxfp4", "qknorm-bias-hd128",
+                              "qknorm-bias-hd64"])
 @pytest.mark.parametrize("B", [1, 5, 9, 10, 17])
 def test_verify_step_matches_oracle(ctx, shape, B):
     d, m, kv = make(ctx, shape)

@@ -20,6 +20,7 @@ MOE = dict(n_layers=2, hidden=128, n_q_heads=4, n_kv_heads=2, head_dim=64, inter
 MOEX = dict(n_layers=2, hidden=128, n_q_heads=8, n_kv_heads=2, head_dim=64, intermediate=0, vocab=300, n_experts=8,
             top_k=4, expert_intermediate=64, expert_format=1, router_bias=1, expert_bias=1, act=1, sinks=1,
             sliding_window=8, rope_theta=1e4)
+QWEN = dict(DENSE, qk_norm=1, qkv_bias=1)
 P = 24
 TOKS = np.array([5, 17, 250, 3, 9, 101, 77], np.uint32)
 
@@ -34,8 +35,9 @@ def rel_err(a, b):
 # renormalisation changes little, so the MXFP4 shape checks the slot order instead.)
 @pytest.mark.parametrize("shape,tol,muts", [(DENSE, 0.015, ["residual", "norm", "gqa"]),
                                             (MOE, 0.015, ["residual", "norm", "gqa", "renorm", "slots"]),
-                                            (MOEX, 0.03, ["residual", "norm", "gqa", "slots"])],
-                         ids=["dense", "moe-int4", "moe-mxfp4-sinks-swa"])
+                                            (MOEX, 0.03, ["residual", "norm", "gqa", "slots"]),
+                                            (QWEN, 0.015, ["residual", "gqa", "qknorm", "qkvbias"])],
+                         ids=["dense", "moe-int4", "moe-mxfp4-sinks-swa", "qknorm-qkvbias"])
 def test_oracle_composition_matches_float64_forward(shape, tol, muts):
     d = ModelDesc.make(**shape)
     logits, _ = oracle.verify_dense(d, 7, 11, P, TOKS)
