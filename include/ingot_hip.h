@@ -130,6 +130,45 @@ int ih_accept(const uint32_t* vtok, const uint32_t* top1, int B, ih_accept_resul
 int ih_spec_accept_dev(ih_ctx* ctx, uint32_t* st_dev, uint32_t* vtok_dev, const uint32_t* top1_dev, uint32_t* rec_dev,
                        int ring, int rows);
 
+/* ---- sampling (temperature > 0) and the verify-row chooser ------------------------------------------------- */
+
+#define IH_TOPK 64           /* candidates per row (the nucleus and min-p set are searched among them) */
+#define IH_RND_PER_ROUND 32  /* uniforms per round: 2 per row (accept, resample) */
+/* temperature → top-k → min-p → top-p, as the reference (SampleParams, Shaders/zz_sample.metal:16-25; penalties are not
+ * part of this path). */
+typedef struct ih_sample_params {
+  float temp;   /* > 0 */
+  float top_p;  /* (0, 1]; 1 = off */
+  int top_k;    /* 0 = off; ≤ 64 is exact */
+  float min_p;  /* 0 = off */
+} ih_sample_params;
+
+/* Per row of logits [rows][ldl] (fp32, device): the 64 best logits sorted (ties to the lower id) into idx [rows][64] and
+ * val [rows][64], and z [rows][2] = (max, Σ exp((x − max)/temp)) over the whole row (NaN logits left out).
+ * topk64_part + topk64_merge, Shaders/zz_sample.metal:27-171. Enqueued. */
+int ih_topk64_dev(ih_ctx* ctx, const float* logits_dev, int ldl, int rows, int V, float temp, uint32_t* idx_dev,
+                  float* val_dev, float* z_dev);
+/* Speculative verification by rejection (spec_accept_sample, Shaders/zz_sample.metal:241-281): draft vtok[i+1] is
+ * accepted with probability p_i(draft) under `p`, else the next token is drawn from p_i without the draft; the emitted
+ * tokens follow the target distribution exactly. Uniforms rnd_dev[st[5]·32 + 2i] (accept) and [… + 2i + 1]
+ * (resample) of row i. The record, state and vtok[0] as ih_spec_accept_dev. Enqueued. */
+int ih_spec_accept_sample_dev(ih_ctx* ctx, uint32_t* st_dev, uint32_t* vtok_dev, const uint32_t* idx_dev,
+                              const float* val_dev, const float* z_dev, uint32_t* rec_dev, const float* rnd_dev,
+                              const ih_sample_params* p, int ring, int rows);
+
+/* Calibration of the verify-row chooser (RowsParams, Shaders/yy_model.metal:644-653): Platt (a, b) per draft depth
+ * group 0, 1, 2, ≥ 3 and the cost (ms) of a round with k rows (index k, 2 … 17). */
+typedef struct ih_rows_params {
+  float a[4], b[4];
+  float cost[IH_MAX_ROWS + 1];  /* index k = rows */
+  int kmin, kmax;  /* 2 ≤ kmin ≤ kmax ≤ 17 */
+} ih_rows_params;
+/* spec_rows_choose (Shaders/yy_model.metal:654-675; SpecRows.swift): from the drafts' confidences conf_dev[kmax − 1],
+ * q_t = sigmoid(a_g·logit(conf_t) + b_g), E(k) = 1 + Σ_{i<k−1} Π_{t≤i} q_t; writes the k in [kmin, kmax] with the
+ * highest E(k)/cost[k] to st_dev[6], which the acceptance reads when called with rows = 0 (every row is still
+ * verified; only the first st[6] can be accepted). Enqueued. */
+int ih_spec_rows_choose_dev(ih_ctx* ctx, uint32_t* st_dev, const float* conf_dev, const ih_rows_params* p);
+
 /* ---- model and KV cache ------------------------------------------------------------------------------------- */
 
 typedef struct ih_model ih_model;
@@ -250,6 +289,14 @@ typedef struct ih_decode_stats {
  * tokens, identical to one-row greedy decoding. */
 int ih_decode_greedy(ih_model* model, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first,
                      const ih_decode_opts* opts, uint32_t* out, int out_cap, int* n_out, ih_decode_stats* stats);
+
+/* ih_decode_greedy with temperature sampling (decodeSpec with sampling): each round's rows go through ih_topk64 and the
+ * rejection acceptance of ih_spec_accept_sample_dev, with the uniforms of round r drawn from SplitMix64(seed) (24-bit,
+ * 32 per round; Sampling.swift:50-62). The emitted tokens follow the model's distribution under `sp` whatever the
+ * drafts; the same seed gives the same tokens. */
+int ih_decode_sample(ih_model* model, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first,
+                     const ih_decode_opts* opts, const ih_sample_params* sp, uint64_t seed, uint32_t* out, int out_cap,
+                     int* n_out, ih_decode_stats* stats);
 
 /* Verify, accept and commit in one call: runs the step on tokens (anchor + drafts), accepts the longest matching draft
  * prefix, advances P by m + 1 and returns the result (the non-chained round of generateSpec, Generate.swift:104-177). */

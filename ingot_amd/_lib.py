@@ -112,6 +112,10 @@ def _declare(L: C.CDLL) -> None:
         "ih_decode_greedy": (i32, [vp, vp, vp, i32, C.c_uint32, vp, vp, i32, P(i32), vp]),
         "ih_model_load_mlx": (i32, [vp, C.c_char_p, P(vp)]),
         "ih_mlx_describe": (i32, [C.c_char_p, vp]),
+        "ih_topk64_dev": (i32, [vp, vp, i32, i32, i32, C.c_float, vp, vp, vp]),
+        "ih_spec_accept_sample_dev": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32]),
+        "ih_spec_rows_choose_dev": (i32, [vp, vp, vp, vp]),
+        "ih_decode_sample": (i32, [vp, vp, vp, i32, C.c_uint32, vp, vp, C.c_uint64, vp, i32, P(i32), vp]),
         "ih_timing_enable": (i32, [vp, i32]),
         "ih_timing_read": (i32, [vp, i32, P(C.c_double), P(C.c_int), P(C.c_double)]),
     }
@@ -329,6 +333,20 @@ class DecodeStats(C.Structure):
 
 
 FINISH_LENGTH, FINISH_STOP, FINISH_CONTEXT = 0, 1, 2
+TOPK, RND_PER_ROUND = 64, 32
+
+
+class SampleParams(C.Structure):
+    """ih_sample_params: temperature → top-k → min-p → top-p."""
+
+    _fields_ = [("temp", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int), ("min_p", C.c_float)]
+
+
+class RowsParams(C.Structure):
+    """ih_rows_params: Platt (a, b) per draft depth group, cost per rows, kmin, kmax."""
+
+    _fields_ = [("a", C.c_float * 4), ("b", C.c_float * 4), ("cost", C.c_float * 18), ("kmin", C.c_int),
+                ("kmax", C.c_int)]
 
 
 def accept(vtok, top1) -> AcceptResult:
@@ -425,6 +443,21 @@ class KVCache:
         check(lib().ih_decode_greedy(self.model.handle, self.handle, ptr(hist) if hist is not None else None,
                                      0 if hist is None else hist.size, first, C.byref(o), ptr(out), max_tokens,
                                      C.byref(n), C.byref(st)))
+        return [int(x) for x in out[: n.value]], st
+
+    def decode_sample(self, first: int, max_tokens: int, params: "SampleParams", seed: int, rows: int = 1,
+                      history=None, stop=(), inflight: int = 2, min_match: int = 3, max_match: int = 64):
+        """Chained decoding with temperature sampling (ih_decode_sample): (emitted tokens, DecodeStats)."""
+        stop_a = np.ascontiguousarray(np.asarray(stop, np.uint32).reshape(-1))
+        o = DecodeOpts(max_tokens=max_tokens, stop_tokens=ptr(stop_a) if stop_a.size else None, n_stop=stop_a.size,
+                       rows=rows, min_match=min_match, max_match=max_match, inflight=inflight)
+        hist = None if history is None else np.ascontiguousarray(np.asarray(history, np.uint32))
+        out = np.zeros(max_tokens, np.uint32)
+        n = C.c_int()
+        st = DecodeStats()
+        check(lib().ih_decode_sample(self.model.handle, self.handle, ptr(hist) if hist is not None else None,
+                                     0 if hist is None else hist.size, first, C.byref(o), C.byref(params), seed,
+                                     ptr(out), max_tokens, C.byref(n), C.byref(st)))
         return [int(x) for x in out[: n.value]], st
 
     def verify_and_accept(self, tokens) -> AcceptResult:

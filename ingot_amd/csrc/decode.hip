@@ -6,7 +6,9 @@
 // (a stop token, the token budget or the context) the rounds already enqueued past the stop are rolled back by setting
 // the cache position after the last emitted token. The drafter here is the copy-from-context lookup over the
 // device-resident history (CopyIndex's rule, Sources/Ingot/CopySpec.swift:118-138), or none (one row per round: plain
-// chained decoding).
+// chained decoding). With a temperature the acceptance is the rejection sampling of spec_accept_sample over each row's
+// 64 candidates, with the uniforms of round r at rnd[32·r …] drawn from SplitMix64(seed) on the host
+// (roundUniforms, Generate.swift:505-512).
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -28,10 +30,14 @@ struct DecodeBuffers {
   uint32_t* hist = nullptr;  // token at each position, the anchor last (device)
   uint32_t* copy = nullptr;  // copy lookup output [4 + IH_MAX_ROWS] (device)
   uint32_t* rec = nullptr;   // round records [REC_RING][IH_REC_STRIDE] (host-pinned, written by the device)
+  uint32_t* cidx = nullptr;  // sampling: candidates [IH_MAX_ROWS][IH_TOPK] (device)
+  float* cval = nullptr;
+  float* cz = nullptr;       // [IH_MAX_ROWS][2]
+  float* rnd = nullptr;      // uniforms [rounds][IH_RND_PER_ROUND]
   std::vector<hipEvent_t> ev;
   ~DecodeBuffers() {
     if (c) (void)hipStreamSynchronize(c->stream);
-    void* d[] = {st, vtok, top1, hist, copy};
+    void* d[] = {st, vtok, top1, hist, copy, cidx, cval, cz, rnd};
     for (void* p : d)
       if (p) (void)hipFree(p);
     if (rec) (void)hipHostFree(rec);
@@ -39,24 +45,35 @@ struct DecodeBuffers {
   }
 };
 
-}  // namespace
+// SplitMix64 (Sampling.swift:50-62) and its 24-bit uniform in [0, 1).
+struct SplitMix64 {
+  uint64_t s;
+  uint64_t next() {
+    s += 0x9E3779B97F4A7C15ull;
+    uint64_t z = s;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  float uniform() { return float(next() >> 40) / float(1 << 24); }
+};
 
-extern "C" {
-
-int ih_decode_greedy(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first,
-                     const ih_decode_opts* o, uint32_t* out, int out_cap, int* n_out, ih_decode_stats* stats) {
-  IH_CHECK(m && kv && o && out && n_out, IH_EINVAL, "ih_decode_greedy: null argument");
+int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first, const ih_decode_opts* o,
+           const ih_sample_params* sp, uint64_t seed, uint32_t* out, int out_cap, int* n_out, ih_decode_stats* stats) {
+  IH_CHECK(m && kv && o && out && n_out, IH_EINVAL, "ih_decode: null argument");
+  IH_CHECK(!sp || (sp->temp > 0.f && sp->top_p > 0.f && sp->top_k >= 0 && sp->min_p >= 0.f), IH_EINVAL,
+           "ih_decode_sample: need temp > 0, top_p > 0, top_k >= 0, min_p >= 0");
   ih_ctx* c = model_ctx(m);
   const ih_model_desc& d = model_desc(m);
   const int B = o->rows, P0 = ih_kv_pos(kv), cap = ih_kv_capacity(kv);
-  IH_CHECK(B >= 1 && B <= IH_MAX_ROWS, IH_EINVAL, "ih_decode_greedy: rows must be in 1..17");
+  IH_CHECK(B >= 1 && B <= IH_MAX_ROWS, IH_EINVAL, "ih_decode: rows must be in 1..17");
   IH_CHECK(o->max_tokens >= 1 && out_cap >= o->max_tokens, IH_EINVAL,
-           "ih_decode_greedy: need max_tokens >= 1 and out_cap >= max_tokens");
-  IH_CHECK(o->inflight >= 1 && o->inflight < REC_RING, IH_EINVAL, "ih_decode_greedy: inflight must be in 1..7");
-  IH_CHECK(first < uint32_t(d.vocab), IH_EINVAL, "ih_decode_greedy: first token beyond the vocabulary");
+           "ih_decode: need max_tokens >= 1 and out_cap >= max_tokens");
+  IH_CHECK(o->inflight >= 1 && o->inflight < REC_RING, IH_EINVAL, "ih_decode: inflight must be in 1..7");
+  IH_CHECK(first < uint32_t(d.vocab), IH_EINVAL, "ih_decode: first token beyond the vocabulary");
   IH_CHECK(B == 1 || (history && n_history == P0), IH_EINVAL,
-           "ih_decode_greedy: the copy drafter needs the history of the cache's positions (n_history == position)");
-  IH_CHECK(o->n_stop >= 0 && (o->n_stop == 0 || o->stop_tokens), IH_EINVAL, "ih_decode_greedy: bad stop tokens");
+           "ih_decode: the copy drafter needs the history of the cache's positions (n_history == position)");
+  IH_CHECK(o->n_stop >= 0 && (o->n_stop == 0 || o->stop_tokens), IH_EINVAL, "ih_decode: bad stop tokens");
   const int min_match = std::max(3, o->min_match), max_match = std::max(min_match, o->max_match);
   auto is_stop = [&](uint32_t t) {
     for (int i = 0; i < o->n_stop; ++i)
@@ -91,6 +108,18 @@ int ih_decode_greedy(ih_model* m, ih_kv* kv, const uint32_t* history, int n_hist
   IH_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&rec_dev), bf.rec, 0));
   bf.ev.assign(REC_RING, nullptr);
   for (auto& e : bf.ev) IH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  if (sp) {
+    // Uniforms for every round this call can run (each round emits at least one token).
+    const size_t nr = size_t(o->max_tokens + o->inflight + 2) * IH_RND_PER_ROUND;
+    std::vector<float> u(nr);
+    SplitMix64 rng{seed};
+    for (auto& x : u) x = rng.uniform();
+    IH_HIP(hipMalloc(&bf.rnd, nr * 4));
+    IH_HIP(hipMemcpy(bf.rnd, u.data(), nr * 4, hipMemcpyHostToDevice));
+    IH_HIP(hipMalloc(&bf.cidx, IH_MAX_ROWS * IH_TOPK * 4));
+    IH_HIP(hipMalloc(&bf.cval, IH_MAX_ROWS * IH_TOPK * 4));
+    IH_HIP(hipMalloc(&bf.cz, IH_MAX_ROWS * 2 * 4));
+  }
   std::memset(bf.rec, 0, REC_RING * IH_REC_STRIDE * 4);
   uint32_t st0[8] = {uint32_t(P0), 0, 0, 0, first, 0, uint32_t(B), 0};
   uint32_t vt0[IH_MAX_ROWS];
@@ -114,7 +143,13 @@ int ih_decode_greedy(ih_model* m, ih_kv* kv, const uint32_t* history, int n_hist
       if (pos_max + B > cap) break;
       if (B > 1) IH_TRY(launch_copy_lookup(c, bf.hist, cap + 1, B - 1, min_match, max_match, bf.copy, bf.vtok, B, bf.st));
       IH_TRY(ih_verify_step_chained(m, kv, bf.vtok, B, bf.top1, bf.st, pos_min, pos_max));
-      IH_TRY(launch_accept(c, bf.st, bf.vtok, bf.top1, rec_dev, REC_RING, B, B > 1 ? bf.hist : nullptr, cap + 1));
+      if (sp) {
+        IH_TRY(launch_topk64(c, ih_model_logits_dev(m), d.vocab, B, d.vocab, sp->temp, bf.cidx, bf.cval, bf.cz));
+        IH_TRY(launch_accept_sample(c, bf.st, bf.vtok, bf.cidx, bf.cval, bf.cz, rec_dev, bf.rnd, *sp, REC_RING, B,
+                                    B > 1 ? bf.hist : nullptr, cap + 1));
+      } else {
+        IH_TRY(launch_accept(c, bf.st, bf.vtok, bf.top1, rec_dev, REC_RING, B, B > 1 ? bf.hist : nullptr, cap + 1));
+      }
       IH_HIP(hipEventRecord(bf.ev[enq % REC_RING], s));
       ++enq;
     }
@@ -127,7 +162,7 @@ int ih_decode_greedy(ih_model* m, ih_kv* kv, const uint32_t* history, int n_hist
     IH_HIP(hipEventSynchronize(bf.ev[known % REC_RING]));
     const uint32_t* r = bf.rec + (known % REC_RING) * IH_REC_STRIDE;
     const int mr = int(r[0]), pb = int(r[IH_REC_P]);
-    IH_CHECK(mr >= 0 && mr < B && pb == Pk, IH_ESTATE, "ih_decode_greedy: round record out of sequence");
+    IH_CHECK(mr >= 0 && mr < B && pb == Pk, IH_ESTATE, "ih_decode: round record out of sequence");
     ++sx.rounds;
     sx.drafted += B - 1;
     sx.accepted += mr;
@@ -147,9 +182,25 @@ int ih_decode_greedy(ih_model* m, ih_kv* kv, const uint32_t* history, int n_hist
   IH_HIP(hipStreamSynchronize(s));
   uint32_t flag = 0;
   IH_HIP(hipMemcpy(&flag, bf.st + 7, 4, hipMemcpyDeviceToHost));
-  IH_CHECK(flag == 0, IH_ESTATE, "ih_decode_greedy: a round ran outside the position range it was launched for");
+  IH_CHECK(flag == 0, IH_ESTATE, "ih_decode: a round ran outside the position range it was launched for");
   IH_TRY(ih_kv_set_pos(kv, stop_pos));
   return finish(why);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ih_decode_greedy(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first,
+                     const ih_decode_opts* o, uint32_t* out, int out_cap, int* n_out, ih_decode_stats* stats) {
+  return decode(m, kv, history, n_history, first, o, nullptr, 0, out, out_cap, n_out, stats);
+}
+
+int ih_decode_sample(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first,
+                     const ih_decode_opts* o, const ih_sample_params* sp, uint64_t seed, uint32_t* out, int out_cap,
+                     int* n_out, ih_decode_stats* stats) {
+  IH_CHECK(sp, IH_EINVAL, "ih_decode_sample: null sampling parameters");
+  return decode(m, kv, history, n_history, first, o, sp, seed, out, out_cap, n_out, stats);
 }
 
 }  // extern "C"

@@ -131,6 +131,9 @@ struct ih_ctx {
   int cu_count = 256;
   // Device address of the static argmax scratch on this context's device (ih_argmax_rows_noalloc).
   void* noalloc_scratch = nullptr;
+  // Chunk lists of the top-64 candidates (sampling), grown on demand.
+  void* samp = nullptr;
+  size_t samp_bytes = 0;
 };
 
 namespace ih {
@@ -193,4 +196,9 @@ int launch_copy_lookup(ih_ctx* c, const uint32_t* h, int n, int max_k, int min_m
                        uint32_t* vtok, int rows, const uint32_t* pos_dev);
 int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows,
                   uint32_t* hist, int hist_cap);
+int launch_topk64(ih_ctx* c, const float* x, int ldx, int rows, int V, float temp, uint32_t* idx, float* val,
+                  float* z);
+int launch_accept_sample(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* idx, const float* val,
+                         const float* z, uint32_t* rec, const float* rnd, const ih_sample_params& p, int ring, int rows,
+                         uint32_t* hist, int hist_cap);
 }  // namespace ih

@@ -1,0 +1,366 @@
+// Temperature > 0 verification by rejection sampling, and the verify-row chooser, on gfx950.
+//
+// Reference: Shaders/zz_sample.metal:1-281 (topk64_part / topk64_merge: per row the 64 best logits, ties to the lower
+// id, and the max and Σ exp((x − max)/T) over the whole vocabulary; sample_dist: temperature → top-k → min-p → top-p
+// over the 64 candidates; spec_accept_sample: draft d of row i accepted with probability p_i(d), otherwise the token is
+// drawn from p_i without d, so the emitted tokens follow the target distribution exactly) and spec_rows_choose
+// (Shaders/yy_model.metal:644-675, SpecRows.swift: the rows with the best expected tokens per cost).
+//
+// MI355X design: a 64-entry list is one value per lane of a wave. Each wave keeps its sorted top-64 in registers; a
+// batch of 64 new values that holds any candidate better than the list's last entry is sorted by a bitonic network of
+// lane exchanges and merged (the better of list[l] and batch[63 − l] is a bitonic sequence holding the 64 best, which
+// six exchange stages sort). The workgroup then merges its four waves' lists, and one wave per row merges the 32
+// chunk lists the same way.
+#include <cfloat>
+#include <cmath>
+
+#include "ih_internal.h"
+#include "lanes.h"
+
+namespace ih {
+
+constexpr int SK = IH_TOPK;      // candidates per row
+constexpr int SPG = 32;          // chunks (workgroups) per row
+constexpr int SPT = 256;         // threads per chunk workgroup
+constexpr uint32_t NO_ID = 0xFFFFFFFFu;
+
+// (v, i) ranks before (w, j): larger value, ties to the lower id (tk_better, yy_model.metal:503).
+__device__ __forceinline__ bool tk_better(float v, uint32_t i, float w, uint32_t j) {
+  return v > w || (v == w && i < j);
+}
+
+// Compare-exchange with lane ^ J: the lane ends with the better of the pair if keep_better, else the worse.
+template <int J>
+__device__ __forceinline__ void cx(float& v, uint32_t& id, bool keep_better) {
+  const float ov = __shfl_xor(v, J);
+  const uint32_t oi = uint32_t(__shfl_xor(int(id), J));
+  const bool take = keep_better ? tk_better(ov, oi, v, id) : tk_better(v, id, ov, oi);
+  if (take) { v = ov; id = oi; }
+}
+
+// Bitonic sort of one value per lane into descending rank order (lane 0 the best).
+__device__ __forceinline__ void sort64(float& v, uint32_t& id, int lane) {
+#define IH_CX(K, J) cx<J>(v, id, (((lane & (J)) == 0) == ((lane & (K)) == 0)))
+  IH_CX(2, 1);
+  IH_CX(4, 2); IH_CX(4, 1);
+  IH_CX(8, 4); IH_CX(8, 2); IH_CX(8, 1);
+  IH_CX(16, 8); IH_CX(16, 4); IH_CX(16, 2); IH_CX(16, 1);
+  IH_CX(32, 16); IH_CX(32, 8); IH_CX(32, 4); IH_CX(32, 2); IH_CX(32, 1);
+  IH_CX(64, 32); IH_CX(64, 16); IH_CX(64, 8); IH_CX(64, 4); IH_CX(64, 2); IH_CX(64, 1);
+#undef IH_CX
+}
+
+// The 64 best of two descending lists (the list in v/id, the other in bv/bi), descending, in v/id.
+__device__ __forceinline__ void merge64(float& v, uint32_t& id, float bv, uint32_t bi, int lane) {
+  const float rv = __shfl(bv, 63 - lane);
+  const uint32_t ri = uint32_t(__shfl(int(bi), 63 - lane));
+  if (tk_better(rv, ri, v, id)) { v = rv; id = ri; }
+  // v is now bitonic (descending, then ascending); six half-cleaners sort it.
+  cx<32>(v, id, (lane & 32) == 0);
+  cx<16>(v, id, (lane & 16) == 0);
+  cx<8>(v, id, (lane & 8) == 0);
+  cx<4>(v, id, (lane & 4) == 0);
+  cx<2>(v, id, (lane & 2) == 0);
+  cx<1>(v, id, (lane & 1) == 0);
+}
+
+// Online (max, Σ exp((x − max)/T)) of one lane, and their combination (the max starts at −FLT_MAX, as the
+// reference's, so −inf logits add exp(−inf) = 0). NaN logits are left out.
+__device__ __forceinline__ void lse_add(float c, float it, float& mt, float& s) {
+  if (c != c) return;
+  if (c > mt) {
+    s = s * __expf((mt - c) * it) + 1.0f;
+    mt = c;
+  } else {
+    s += __expf((c - mt) * it);
+  }
+}
+
+__global__ __launch_bounds__(SPT) void topk64_part_kernel(const float* __restrict__ x, int ldx, int V, float temp,
+                                                          uint32_t* __restrict__ pidx, float* __restrict__ pval,
+                                                          float2* __restrict__ pz) {
+  __shared__ float sv[SPT / 64][SK];
+  __shared__ uint32_t si[SPT / 64][SK];
+  __shared__ float rm[SPT / 64], rs[SPT / 64];
+  const int g = blockIdx.x, row = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float it = 1.0f / temp;
+  const float* xr = x + size_t(row) * ldx;
+  const int C = (V + SPG - 1) / SPG, lo = g * C, hi = min(V, lo + C);
+  float v = -FLT_MAX, mt = -FLT_MAX, s = 0.f;
+  uint32_t id = NO_ID;
+  for (int base = lo + wave * 64; base < hi; base += SPT) {
+    const int ci = base + lane;
+    const bool ok = ci < hi;
+    float c = ok ? xr[ci] : -FLT_MAX;
+    if (ok) lse_add(c, it, mt, s);
+    uint32_t cid = ok && c == c ? uint32_t(ci) : NO_ID;
+    if (cid == NO_ID) c = -FLT_MAX;
+    const float tv = __shfl(v, 63);
+    const uint32_t ti = uint32_t(__shfl(int(id), 63));
+    if (!__any(tk_better(c, cid, tv, ti))) continue;  // wave-uniform
+    sort64(c, cid, lane);
+    merge64(v, id, c, cid, lane);
+  }
+  // The wave's (max, sum), then the workgroup's lists and sums.
+  float m = mt;
+  m = fmaxf(m, lane_xor<32>(m));
+  m = fmaxf(m, lane_xor<16>(m));
+  m = fmaxf(m, lane_xor<8>(m));
+  m = fmaxf(m, lane_xor<4>(m));
+  m = fmaxf(m, lane_xor<2>(m));
+  m = fmaxf(m, lane_xor<1>(m));
+  float ss = s * __expf((mt - m) * it);
+  ss += lane_xor<32>(ss);
+  ss += lane_xor<16>(ss);
+  ss += lane_xor<8>(ss);
+  ss += lane_xor<4>(ss);
+  ss += lane_xor<2>(ss);
+  ss += lane_xor<1>(ss);
+  sv[wave][lane] = v;
+  si[wave][lane] = id;
+  if (lane == 0) {
+    rm[wave] = m;
+    rs[wave] = ss;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 1; w < SPT / 64; ++w) merge64(v, id, sv[w][lane], si[w][lane], lane);
+  const size_t o = (size_t(row) * SPG + g) * SK;
+  pval[o + lane] = v;
+  pidx[o + lane] = id;
+  if (lane == 0) {
+    float M = rm[0];
+    for (int w = 1; w < SPT / 64; ++w) M = fmaxf(M, rm[w]);
+    float Z = 0.f;
+    for (int w = 0; w < SPT / 64; ++w) Z += rs[w] * __expf((rm[w] - M) * it);
+    pz[size_t(row) * SPG + g] = make_float2(M, Z);
+  }
+}
+
+__global__ __launch_bounds__(64) void topk64_merge_kernel(const uint32_t* __restrict__ pidx,
+                                                          const float* __restrict__ pval,
+                                                          const float2* __restrict__ pz, float temp,
+                                                          uint32_t* __restrict__ idx, float* __restrict__ val,
+                                                          float* __restrict__ z) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const float it = 1.0f / temp;
+  const size_t o = size_t(row) * SPG * SK;
+  float v = pval[o + lane];
+  uint32_t id = pidx[o + lane];
+  for (int g = 1; g < SPG; ++g) merge64(v, id, pval[o + g * SK + lane], pidx[o + g * SK + lane], lane);
+  idx[size_t(row) * SK + lane] = id;
+  val[size_t(row) * SK + lane] = v;
+  if (lane == 0) {
+    const float2* p = pz + size_t(row) * SPG;
+    float M = p[0].x;
+    for (int g = 1; g < SPG; ++g) M = fmaxf(M, p[g].x);
+    float Z = 0.f;
+    for (int g = 0; g < SPG; ++g) Z += p[g].y * __expf((p[g].x - M) * it);
+    z[2 * row] = M;
+    z[2 * row + 1] = Z;
+  }
+}
+
+// Probabilities of a row's candidates after temperature, top-k, min-p and top-p, renormalised; returns how many
+// remain (sample_dist, zz_sample.metal:196-226).
+__device__ int sample_dist(const uint32_t* ci, const float* cv, float M, float Z, const ih_sample_params& p,
+                           float* pr) {
+  const float it = 1.0f / p.temp;
+  int n = 0;
+  while (n < SK && ci[n] != NO_ID) ++n;
+  float tot = Z;
+  if (p.top_k > 0 && p.top_k < n) n = p.top_k;
+  if (p.top_k > 0) {
+    tot = 0.f;
+    for (int j = 0; j < n; ++j) tot += __expf((cv[j] - M) * it);
+  }
+  for (int j = 0; j < n; ++j) pr[j] = __expf((cv[j] - M) * it) / tot;
+  if (p.min_p > 0.f) {
+    const float thr = p.min_p * pr[0];
+    int k = 1;
+    while (k < n && pr[k] >= thr) ++k;
+    n = k;
+    float s = 0.f;
+    for (int j = 0; j < n; ++j) s += pr[j];
+    for (int j = 0; j < n; ++j) pr[j] /= s;
+  }
+  if (p.top_p < 1.f) {
+    float c = 0.f;
+    int k = n;
+    for (int j = 0; j < n; ++j) {
+      c += pr[j];
+      if (c >= p.top_p) {
+        k = j + 1;
+        break;
+      }
+    }
+    n = max(k, 1);
+  }
+  float s = 0.f;
+  for (int j = 0; j < n; ++j) s += pr[j];
+  for (int j = 0; j < n; ++j) pr[j] /= s;
+  return n;
+}
+
+// A token from pr[0 … n) without `skip` (whose mass is q), with the uniform u (sample_pick, zz_sample.metal:228-239).
+__device__ uint32_t sample_pick(const uint32_t* ci, const float* pr, int n, uint32_t skip, float q, float u) {
+  const float target = u * (1.0f - q);
+  float acc = 0.f;
+  uint32_t last = NO_ID;
+  for (int j = 0; j < n; ++j) {
+    if (ci[j] == skip) continue;
+    acc += pr[j];
+    last = ci[j];
+    if (acc > target) return ci[j];
+  }
+  return last == NO_ID ? ci[0] : last;
+}
+
+// Acceptance by rejection (spec_accept_sample, zz_sample.metal:241-281): rows' candidates idx/val [rows][64] and
+// (max, Z) [rows][2]; uniforms rnd[round · 32 + 2i] (accept) and [… + 2i + 1] (resample) of row i. Writes the record
+// and advances the state as the greedy acceptance does (vtok[0] = the new anchor; the history as in accept_kernel).
+__global__ void accept_sample_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* cidx, const float* cval,
+                                     const float* z, uint32_t* rec, const float* rnd, ih_sample_params p, int ring,
+                                     int rows, uint32_t* hist, int hist_cap) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const uint32_t nr = rows ? uint32_t(rows) : min(max(st[6], 1u), uint32_t(IH_MAX_ROWS));
+  const float* u = rnd + size_t(st[5]) * IH_RND_PER_ROUND;
+  float pr[SK];
+  uint32_t m = 0, next = 0;
+  for (uint32_t i = 0; i < nr; ++i) {
+    const uint32_t* ci = cidx + i * SK;
+    const int n = sample_dist(ci, cval + i * SK, z[2 * i], z[2 * i + 1], p, pr);
+    if (i + 1 < nr) {
+      const uint32_t d = vtok[i + 1];
+      float q = 0.f;
+      for (int j = 0; j < n; ++j)
+        if (ci[j] == d) q = pr[j];
+      if (u[2 * i] < q) {
+        ++m;
+        continue;
+      }
+      next = sample_pick(ci, pr, n, d, q, u[2 * i + 1]);
+    } else {
+      next = sample_pick(ci, pr, n, NO_ID, 0.f, u[2 * i + 1]);
+    }
+    break;
+  }
+  uint32_t* r = rec + (st[5] % uint32_t(ring)) * IH_REC_STRIDE;
+  r[0] = m;
+  r[IH_REC_ROWS] = nr;
+  for (uint32_t i = 1; i <= m; ++i) r[i] = vtok[i];
+  r[m + 1] = next;
+  r[IH_REC_P] = st[0];
+  const uint32_t p0 = st[0];
+  st[3] = st[0];
+  st[2] = m + 1;
+  st[0] += m + 1;
+  st[1] = m + 1;
+  st[4] = next;
+  st[5] += 1;
+  if (hist) {
+    for (uint32_t i = 0; i < m; ++i)
+      if (p0 + 1 + i < uint32_t(hist_cap)) hist[p0 + 1 + i] = vtok[1 + i];
+    if (p0 + 1 + m < uint32_t(hist_cap)) hist[p0 + 1 + m] = next;
+  }
+  vtok[0] = next;
+}
+
+// Verification rows of the round (spec_rows_choose, yy_model.metal:654-675): with draft t's calibrated acceptance
+// q_t = sigmoid(a_g · logit(conf_t) + b_g) (g = min(t, 3)), expected tokens E(k) = 1 + Σ_{i<k−1} Π_{t≤i} q_t, the
+// k in [kmin, kmax] with the highest E(k) / cost(k) goes to st[6].
+__global__ void rows_choose_kernel(uint32_t* st, const float* conf, ih_rows_params p) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  float acc = 1.f, lp = 1.f, bv = -1.f;
+  uint32_t best = uint32_t(p.kmax);
+  for (int t = 0; t + 1 < p.kmax; ++t) {
+    const int g = min(t, 3);
+    const float c = fminf(fmaxf(conf[t], 1e-6f), 1.0f - 1e-6f);
+    const float q = 1.0f / (1.0f + __expf(-(p.a[g] * __logf(c / (1.0f - c)) + p.b[g])));
+    lp *= q;
+    acc += lp;
+    const int k = t + 2;
+    if (k >= p.kmin) {
+      const float v = acc / p.cost[k];
+      if (v > bv) {
+        bv = v;
+        best = uint32_t(k);
+      }
+    }
+  }
+  st[6] = best;
+}
+
+int ensure_samp(ih_ctx* c, size_t bytes) {
+  if (c->samp_bytes >= bytes) return IH_OK;
+  IH_HIP(hipStreamSynchronize(c->stream));
+  if (c->samp) IH_HIP(hipFree(c->samp));
+  c->samp = nullptr;
+  c->samp_bytes = 0;
+  if (hipMalloc(&c->samp, bytes) != hipSuccess) return fail(IH_ENOMEM, "sampling scratch allocation failed");
+  c->samp_bytes = bytes;
+  return IH_OK;
+}
+
+int launch_topk64(ih_ctx* c, const float* x, int ldx, int rows, int V, float temp, uint32_t* idx, float* val,
+                  float* z) {
+  const size_t n = size_t(rows) * SPG * SK;
+  IH_TRY(ensure_samp(c, n * 8 + size_t(rows) * SPG * sizeof(float2)));
+  uint32_t* pidx = static_cast<uint32_t*>(c->samp);
+  float* pval = reinterpret_cast<float*>(pidx + n);
+  float2* pz = reinterpret_cast<float2*>(pval + n);
+  {
+    TimedLaunch tl(c, TC_ARGMAX, double(rows) * V * 4);
+    tlaunch(tl, topk64_part_kernel, dim3(SPG, rows), dim3(SPT), 0, c->stream, x, ldx, V, temp, pidx, pval, pz);
+    IH_HIP(hipGetLastError());
+  }
+  topk64_merge_kernel<<<rows, 64, 0, c->stream>>>(pidx, pval, pz, temp, idx, val, z);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+int launch_accept_sample(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* idx, const float* val,
+                         const float* z, uint32_t* rec, const float* rnd, const ih_sample_params& p, int ring, int rows,
+                         uint32_t* hist, int hist_cap) {
+  accept_sample_kernel<<<1, 64, 0, c->stream>>>(st, vtok, idx, val, z, rec, rnd, p, ring, rows, hist, hist_cap);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+}  // namespace ih
+
+using namespace ih;
+
+extern "C" {
+
+int ih_topk64_dev(ih_ctx* c, const float* logits_dev, int ldl, int rows, int V, float temp, uint32_t* idx_dev,
+                  float* val_dev, float* z_dev) {
+  IH_CHECK(c && logits_dev && idx_dev && val_dev && z_dev, IH_EINVAL, "ih_topk64_dev: null argument");
+  IH_CHECK(rows >= 1 && rows <= 256 && V >= 1 && ldl >= V, IH_EINVAL, "ih_topk64_dev: bad shape");
+  IH_CHECK(temp > 0.f && std::isfinite(temp), IH_EINVAL, "ih_topk64_dev: temperature must be positive");
+  return launch_topk64(c, logits_dev, ldl, rows, V, temp, idx_dev, val_dev, z_dev);
+}
+
+int ih_spec_accept_sample_dev(ih_ctx* c, uint32_t* st_dev, uint32_t* vtok_dev, const uint32_t* idx_dev,
+                              const float* val_dev, const float* z_dev, uint32_t* rec_dev, const float* rnd_dev,
+                              const ih_sample_params* p, int ring, int rows) {
+  IH_CHECK(c && st_dev && vtok_dev && idx_dev && val_dev && z_dev && rec_dev && rnd_dev && p, IH_EINVAL,
+           "ih_spec_accept_sample_dev: null argument");
+  IH_CHECK(ring >= 1 && rows >= 0 && rows <= IH_MAX_ROWS, IH_EINVAL, "ih_spec_accept_sample_dev: bad ring or rows");
+  IH_CHECK(p->temp > 0.f && p->top_p > 0.f && p->top_k >= 0 && p->min_p >= 0.f, IH_EINVAL,
+           "ih_spec_accept_sample_dev: need temp > 0, top_p > 0, top_k >= 0, min_p >= 0");
+  return launch_accept_sample(c, st_dev, vtok_dev, idx_dev, val_dev, z_dev, rec_dev, rnd_dev, *p, ring, rows, nullptr,
+                              0);
+}
+
+int ih_spec_rows_choose_dev(ih_ctx* c, uint32_t* st_dev, const float* conf_dev, const ih_rows_params* p) {
+  IH_CHECK(c && st_dev && conf_dev && p, IH_EINVAL, "ih_spec_rows_choose_dev: null argument");
+  IH_CHECK(p->kmin >= 2 && p->kmin <= p->kmax && p->kmax <= IH_MAX_ROWS, IH_EINVAL,
+           "ih_spec_rows_choose_dev: need 2 <= kmin <= kmax <= 17");
+  rows_choose_kernel<<<1, 64, 0, c->stream>>>(st_dev, conf_dev, *p);
+  IH_HIP(hipGetLastError());
+  return IH_OK;
+}
+
+}  // extern "C"

@@ -87,6 +87,10 @@ _SIGS = [
     ("or_copy_index_append", None, [vp, vp, i32]),
     ("or_copy_index_propose", i32, [vp, i32, vp, vp]),
     ("or_splitmix64", None, [C.c_uint64, i32, vp]),
+    ("or_topk64", None, [vp, i32, i32, C.c_float, vp, vp, vp]),
+    ("or_sample_dist", i32, [vp, vp, C.c_float, C.c_float, vp, vp]),
+    ("or_accept_sample", i32, [vp, i32, vp, vp, vp, vp, vp, vp]),
+    ("or_rows_choose", i32, [vp, vp, vp, vp, i32, i32]),
 ]
 
 
@@ -340,3 +344,49 @@ def splitmix64(seed: int, n: int) -> np.ndarray:
     out = np.empty(n, np.uint64)
     lib().or_splitmix64(seed, n, _p(out))
     return out
+
+
+# ---- sampling -------------------------------------------------------------------------------------------------
+
+class SampleParams(C.Structure):
+    _fields_ = [("temp", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int), ("min_p", C.c_float)]
+
+
+def topk64(x, temp):
+    """(idx [rows][64] uint32, val [rows][64] f32, z [rows][2] = (max, Σ exp((x − max)/T)))."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, V = x.shape
+    idx = np.empty((rows, 64), np.uint32)
+    val = np.empty((rows, 64), np.float32)
+    z = np.empty((rows, 2), np.float32)
+    lib().or_topk64(_p(x), rows, V, temp, _p(idx), _p(val), _p(z))
+    return idx, val, z
+
+
+def sample_dist(idx_row, val_row, M, Z, p: SampleParams):
+    """(n, probabilities of the first n candidates)."""
+    ci = np.ascontiguousarray(idx_row, np.uint32)
+    cv = np.ascontiguousarray(val_row, np.float32)
+    pr = np.zeros(64, np.float32)
+    n = lib().or_sample_dist(_p(ci), _p(cv), M, Z, C.addressof(p), _p(pr))
+    return n, pr[:n].copy()
+
+
+def accept_sample(vtok, idx, val, z, u, p: SampleParams):
+    """(m, emitted [m + 1]) of the rejection acceptance with uniforms u [2·rows]."""
+    vtok = np.ascontiguousarray(vtok, np.uint32)
+    idx = np.ascontiguousarray(idx, np.uint32)
+    val = np.ascontiguousarray(val, np.float32)
+    z = np.ascontiguousarray(z, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    em = np.zeros(len(vtok), np.uint32)
+    m = lib().or_accept_sample(_p(vtok), len(vtok), _p(idx), _p(val), _p(z), _p(u), C.addressof(p), _p(em))
+    return m, em[: m + 1].copy()
+
+
+def rows_choose(conf, a, b, cost, kmin, kmax) -> int:
+    conf = np.ascontiguousarray(conf, np.float32)
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    cost = np.ascontiguousarray(cost, np.float32)
+    return int(lib().or_rows_choose(_p(conf), _p(a), _p(b), _p(cost), kmin, kmax))

@@ -911,4 +911,146 @@ int or_num_threads(void) {
 #endif
 }
 
+
+// ---------------------------------------------------------------------------------------------------------------
+// Sampling (temperature > 0). topk64_part/topk64_merge (Sources/Ingot/Shaders/zz_sample.metal:27-171): per row the
+// 64 best logits sorted by value, ties to the lower id (tk_better, yy_model.metal:503), and (max, Σ exp((x − max)/T))
+// over the row (in double here; NaN logits left out). idx/val [rows][64], z [rows][2].
+void or_topk64(const float* x, int rows, int V, float temp, uint32_t* idx, float* val, float* z) {
+  for (int r = 0; r < rows; ++r) {
+    const float* xr = x + size_t(r) * V;
+    std::vector<int> ids;
+    ids.reserve(V);
+    for (int i = 0; i < V; ++i)
+      if (!std::isnan(xr[i]) && xr[i] > -std::numeric_limits<float>::max()) ids.push_back(i);
+    const int k = std::min<int>(64, int(ids.size()));
+    std::partial_sort(ids.begin(), ids.begin() + k, ids.end(),
+                      [&](int a, int b) { return xr[a] > xr[b] || (xr[a] == xr[b] && a < b); });
+    for (int j = 0; j < 64; ++j) {
+      idx[size_t(r) * 64 + j] = j < k ? uint32_t(ids[j]) : 0xFFFFFFFFu;
+      val[size_t(r) * 64 + j] = j < k ? xr[ids[j]] : -std::numeric_limits<float>::max();
+    }
+    double M = -std::numeric_limits<float>::max();
+    for (int i = 0; i < V; ++i)
+      if (!std::isnan(xr[i])) M = std::max(M, double(xr[i]));
+    double Z = 0;
+    for (int i = 0; i < V; ++i)
+      if (!std::isnan(xr[i])) Z += std::exp((double(xr[i]) - M) / temp);
+    z[2 * r] = float(M);
+    z[2 * r + 1] = float(Z);
+  }
+}
+
+struct or_sample_params {
+  float temp, top_p;
+  int top_k;
+  float min_p;
+};
+
+// sample_dist (zz_sample.metal:196-226): the candidates' probabilities after temperature → top-k → min-p → top-p,
+// renormalised; returns how many remain.
+int or_sample_dist(const uint32_t* ci, const float* cv, float M, float Z, const or_sample_params* p, float* pr) {
+  const float it = 1.0f / p->temp;
+  int n = 0;
+  while (n < 64 && ci[n] != 0xFFFFFFFFu) ++n;
+  float tot = Z;
+  if (p->top_k > 0 && p->top_k < n) n = p->top_k;
+  if (p->top_k > 0) {
+    tot = 0;
+    for (int j = 0; j < n; ++j) tot += std::exp((cv[j] - M) * it);
+  }
+  for (int j = 0; j < n; ++j) pr[j] = std::exp((cv[j] - M) * it) / tot;
+  if (p->min_p > 0) {
+    const float thr = p->min_p * pr[0];
+    int k = 1;
+    while (k < n && pr[k] >= thr) ++k;
+    n = k;
+    float s = 0;
+    for (int j = 0; j < n; ++j) s += pr[j];
+    for (int j = 0; j < n; ++j) pr[j] /= s;
+  }
+  if (p->top_p < 1.0f) {
+    float c = 0;
+    int k = n;
+    for (int j = 0; j < n; ++j) {
+      c += pr[j];
+      if (c >= p->top_p) {
+        k = j + 1;
+        break;
+      }
+    }
+    n = std::max(k, 1);
+  }
+  float s = 0;
+  for (int j = 0; j < n; ++j) s += pr[j];
+  for (int j = 0; j < n; ++j) pr[j] /= s;
+  return n;
+}
+
+// sample_pick (zz_sample.metal:228-239): the token whose cumulative mass (without `skip`) first exceeds u·(1 − q).
+static uint32_t or_sample_pick(const uint32_t* ci, const float* pr, int n, uint32_t skip, float q, float u) {
+  const float target = u * (1.0f - q);
+  float acc = 0;
+  uint32_t last = 0xFFFFFFFFu;
+  for (int j = 0; j < n; ++j) {
+    if (ci[j] == skip) continue;
+    acc += pr[j];
+    last = ci[j];
+    if (acc > target) return ci[j];
+  }
+  return last == 0xFFFFFFFFu ? ci[0] : last;
+}
+
+// spec_accept_sample (zz_sample.metal:241-281) on the host: rows' candidates, uniforms u[2i] (accept) and u[2i + 1]
+// (resample) of row i; returns m and writes the emitted tokens (drafts 1..m, then the sampled token) to emitted.
+int or_accept_sample(const uint32_t* vtok, int nr, const uint32_t* cidx, const float* cval, const float* z,
+                     const float* u, const or_sample_params* p, uint32_t* emitted) {
+  float pr[64];
+  int m = 0;
+  uint32_t next = 0;
+  for (int i = 0; i < nr; ++i) {
+    const uint32_t* ci = cidx + size_t(i) * 64;
+    const int n = or_sample_dist(ci, cval + size_t(i) * 64, z[2 * i], z[2 * i + 1], p, pr);
+    if (i + 1 < nr) {
+      const uint32_t d = vtok[i + 1];
+      float q = 0;
+      for (int j = 0; j < n; ++j)
+        if (ci[j] == d) q = pr[j];
+      if (u[2 * i] < q) {
+        ++m;
+        continue;
+      }
+      next = or_sample_pick(ci, pr, n, d, q, u[2 * i + 1]);
+    } else {
+      next = or_sample_pick(ci, pr, n, 0xFFFFFFFFu, 0, u[2 * i + 1]);
+    }
+    break;
+  }
+  for (int i = 0; i < m; ++i) emitted[i] = vtok[i + 1];
+  emitted[m] = next;
+  return m;
+}
+
+// spec_rows_choose (yy_model.metal:654-675; SpecRowsConfig.chooseCPU, SpecRows.swift:93-105).
+int or_rows_choose(const float* conf, const float* a, const float* b, const float* cost, int kmin, int kmax) {
+  float acc = 1, lp = 1, bv = -1;
+  int best = kmax;
+  for (int t = 0; t + 1 < kmax; ++t) {
+    const int g = std::min(t, 3);
+    const float c = std::min(std::max(conf[t], 1e-6f), 1.0f - 1e-6f);
+    const float q = 1.0f / (1.0f + std::exp(-(a[g] * std::log(c / (1.0f - c)) + b[g])));
+    lp *= q;
+    acc += lp;
+    const int k = t + 2;
+    if (k >= kmin) {
+      const float v = acc / cost[k];
+      if (v > bv) {
+        bv = v;
+        best = k;
+      }
+    }
+  }
+  return best;
+}
+
 }  // extern "C"
