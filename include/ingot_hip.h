@@ -268,6 +268,7 @@ typedef struct ih_decode_opts {
   int rows;                    /* verify rows per round: 1 = plain chained decoding, 2…17 = anchor + copy drafts */
   int min_match, max_match;    /* copy-from-context rule (CopyIndex minMatch / maxMatch; ≥ 3) */
   int inflight;                /* rounds enqueued ahead of the record the host reads (1…7) */
+  struct ih_drafter* drafter;  /* non-null: DFlash2 drafts (rows = its block) instead of copy-from-context ones */
 } ih_decode_opts;
 #define IH_FINISH_LENGTH 0
 #define IH_FINISH_STOP 1
@@ -308,6 +309,49 @@ int ih_model_moe_union(const ih_model* model, int* u_out);
 
 /* The model's device scratch of the last step: logits fp32 [rows ≥ B][vocab] (row stride = vocab). */
 const float* ih_model_logits_dev(const ih_model* model);
+
+/* ---- DFlash2 drafter (the producer of the draft block) --------------------------------------------------------
+ * DFlash2Drafter (Sources/Ingot/Drafter.swift:1-554; kernels Shaders/yy_model.metal:94-104,151-614): dense qwen3 layers
+ * over the target's embedding, with a window of context taken from the target's hidden states after `target_layers`
+ * (captured by the verify step), a non-causal block [anchor, mask × (block − 1)], DFlash2's two-tap dynamic conv around
+ * each sublayer, the target's lm_head over rows 1 … block − 1, and the greedy rank-r selector over each row's top-16
+ * candidates (rank 0 and no conv: DFlash v1, the best candidate per row). 8 KV heads. */
+#define IH_DRAFTER_MAX_TARGETS 8
+typedef struct ih_drafter_desc {
+  int n_layers;
+  int hidden;          /* = the target's hidden size (it uses the target's embedding and head) */
+  int n_q_heads;       /* over 8 KV heads */
+  int head_dim;        /* 64 or 128 */
+  int intermediate;
+  int block;           /* rows of a draft block, anchor included: 2 … 16 ((q heads / 8)·block ≤ 64) */
+  int window;          /* context positions each block row sees (2048 in DFlash2), a multiple of 32 */
+  int n_targets;       /* captured target layers (1 … 8) */
+  int target_layers[IH_DRAFTER_MAX_TARGETS];
+  int rank;            /* selector rank (256 in DFlash2); 0 = each row's best candidate */
+  int dyn_conv;        /* DFlash2's dynamic conv (1) or none (0) */
+  uint32_t mask_token;
+  float rope_theta, rms_eps;
+} ih_drafter_desc;
+typedef struct ih_drafter ih_drafter;
+
+/* A drafter with synthetic weights for `target` (counter-based SplitMix64 streams, reproducible on the CPU). */
+int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, uint64_t seed, ih_drafter** out);
+int ih_drafter_free(ih_drafter* drafter);
+/* Attaches the drafter to its target (null detaches): every verify step then captures its rows' residual after the
+ * drafter's target layers (capture_rows, yy_model.metal:94-104; ModelRound.swift:72-75). */
+int ih_model_set_drafter(ih_model* model, ih_drafter* drafter);
+/* Rows of the drafter's block (anchor included). */
+int ih_drafter_block_rows(const ih_drafter* drafter);
+/* The captured rows bf16 [rows][n_targets · hidden] of the last verify step (device). */
+const uint16_t* ih_drafter_captures_dev(const ih_drafter* drafter);
+/* Context (encodeContext, Drafter.swift:300-330): the captured rows 0 … nvalid − 1 become positions pos0 … of every
+ * layer's window ring (fc → hidden_norm → k|v → k_norm + RoPE). With st_dev, nvalid = st[2] and pos0 = st[3] are read
+ * on the device (the rows the last acceptance committed). Enqueued. */
+int ih_drafter_context(ih_drafter* drafter, int rows, int nvalid, int pos0, const uint32_t* st_dev);
+/* Draft block (encodeBlock, Drafter.swift:369-550): anchor = vtok_dev[0] at position P (or st_dev[0]); writes the
+ * drafts to vtok_dev[1 … block − 1] and, if conf_dev is set, their confidences (softmax(score/1.5) of each pick over
+ * its 16 candidates) for the row chooser. Enqueued. */
+int ih_drafter_block(ih_drafter* drafter, uint32_t* vtok_dev, int P, const uint32_t* st_dev, float* conf_dev);
 
 /* ---- MXFP4 matrices and the MoE pieces (MoELayer.encode, Sources/Ingot/Layers/MoE.swift:346-428) ------------------ */
 

@@ -116,6 +116,13 @@ def _declare(L: C.CDLL) -> None:
         "ih_spec_accept_sample_dev": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32]),
         "ih_spec_rows_choose_dev": (i32, [vp, vp, vp, vp]),
         "ih_decode_sample": (i32, [vp, vp, vp, i32, C.c_uint32, vp, vp, C.c_uint64, vp, i32, P(i32), vp]),
+        "ih_drafter_create_synthetic": (i32, [vp, vp, C.c_uint64, P(vp)]),
+        "ih_drafter_free": (i32, [vp]),
+        "ih_model_set_drafter": (i32, [vp, vp]),
+        "ih_drafter_captures_dev": (vp, [vp]),
+        "ih_drafter_context": (i32, [vp, i32, i32, i32, vp]),
+        "ih_drafter_block": (i32, [vp, vp, i32, vp, vp]),
+        "ih_drafter_block_rows": (i32, [vp]),
         "ih_timing_enable": (i32, [vp, i32]),
         "ih_timing_read": (i32, [vp, i32, P(C.c_double), P(C.c_int), P(C.c_double)]),
     }
@@ -324,7 +331,66 @@ class DecodeOpts(C.Structure):
     """ih_decode_opts (include/ingot_hip.h)."""
 
     _fields_ = [("max_tokens", C.c_int), ("stop_tokens", vp), ("n_stop", C.c_int), ("rows", C.c_int),
-                ("min_match", C.c_int), ("max_match", C.c_int), ("inflight", C.c_int)]
+                ("min_match", C.c_int), ("max_match", C.c_int), ("inflight", C.c_int), ("drafter", vp)]
+
+
+class DrafterDesc(C.Structure):
+    """ih_drafter_desc (include/ingot_hip.h)."""
+
+    _fields_ = [("n_layers", C.c_int), ("hidden", C.c_int), ("n_q_heads", C.c_int), ("head_dim", C.c_int),
+                ("intermediate", C.c_int), ("block", C.c_int), ("window", C.c_int), ("n_targets", C.c_int),
+                ("target_layers", C.c_int * 8), ("rank", C.c_int), ("dyn_conv", C.c_int), ("mask_token", C.c_uint32),
+                ("rope_theta", C.c_float), ("rms_eps", C.c_float)]
+
+    @classmethod
+    def make(cls, targets=(), **kw) -> "DrafterDesc":
+        d = cls(rope_theta=1e6, rms_eps=1e-6, dyn_conv=1)
+        for k, v in kw.items():
+            setattr(d, k, v)
+        d.n_targets = len(targets)
+        for i, t in enumerate(targets):
+            d.target_layers[i] = t
+        return d
+
+
+class Drafter:
+    """A synthetic-weight DFlash2 drafter for a model (ih_drafter_*)."""
+
+    def __init__(self, model: "Model", desc: DrafterDesc, seed: int):
+        self.model, self.desc, self.seed = model, desc, seed
+        h = vp()
+        check(lib().ih_drafter_create_synthetic(model.handle, C.byref(desc), seed, C.byref(h)))
+        self.handle = h.value
+
+    def attach(self) -> None:
+        check(lib().ih_model_set_drafter(self.model.handle, self.handle))
+
+    def captures(self, rows: int) -> np.ndarray:
+        ctx = self.model.ctx
+        n = rows * self.desc.n_targets * self.model.desc.hidden
+        out = np.empty(n, np.uint16)
+        check(lib().ih_memcpy_dtoh(ctx.handle, ptr(out), lib().ih_drafter_captures_dev(self.handle), n * 2))
+        return out.reshape(rows, -1)
+
+    def context(self, rows: int, nvalid: int, pos0: int) -> None:
+        check(lib().ih_drafter_context(self.handle, rows, nvalid, pos0, None))
+
+    def block(self, anchor: int, P: int):
+        """(drafts [block − 1], conf [block − 1]) for the anchor at P."""
+        ctx = self.model.ctx
+        B = self.desc.block
+        vt = ctx.to_device(np.full(B, anchor, np.uint32))
+        cf = ctx.buffer(4 * B)
+        check(lib().ih_drafter_block(self.handle, vt.ptr, P, None, cf.ptr))
+        out = vt.download(np.uint32, (B,))[1:], cf.download(np.float32, (B - 1,))
+        vt.free()
+        cf.free()
+        return out
+
+    def free(self) -> None:
+        if self.handle:
+            lib().ih_drafter_free(self.handle)
+            self.handle = None
 
 
 class DecodeStats(C.Structure):
@@ -431,11 +497,12 @@ class KVCache:
         return lib().ih_kv_capacity(self.handle)
 
     def decode_greedy(self, first: int, max_tokens: int, rows: int = 1, history=None, stop=(), inflight: int = 2,
-                      min_match: int = 3, max_match: int = 64):
+                      min_match: int = 3, max_match: int = 64, drafter: "Drafter | None" = None):
         """Chained greedy decoding (ih_decode_greedy): (emitted tokens, DecodeStats)."""
         stop_a = np.ascontiguousarray(np.asarray(stop, np.uint32).reshape(-1))
         o = DecodeOpts(max_tokens=max_tokens, stop_tokens=ptr(stop_a) if stop_a.size else None, n_stop=stop_a.size,
-                       rows=rows, min_match=min_match, max_match=max_match, inflight=inflight)
+                       rows=rows, min_match=min_match, max_match=max_match, inflight=inflight,
+                       drafter=drafter.handle if drafter is not None else None)
         hist = None if history is None else np.ascontiguousarray(np.asarray(history, np.uint32))
         out = np.zeros(max_tokens, np.uint32)
         n = C.c_int()

@@ -71,7 +71,9 @@ int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint3
            "ih_decode: need max_tokens >= 1 and out_cap >= max_tokens");
   IH_CHECK(o->inflight >= 1 && o->inflight < REC_RING, IH_EINVAL, "ih_decode: inflight must be in 1..7");
   IH_CHECK(first < uint32_t(d.vocab), IH_EINVAL, "ih_decode: first token beyond the vocabulary");
-  IH_CHECK(B == 1 || (history && n_history == P0), IH_EINVAL,
+  IH_CHECK(!o->drafter || B == ih_drafter_block_rows(o->drafter), IH_EINVAL,
+           "ih_decode: with a drafter, rows must be the drafter's block");
+  IH_CHECK(B == 1 || o->drafter || (history && n_history == P0), IH_EINVAL,
            "ih_decode: the copy drafter needs the history of the cache's positions (n_history == position)");
   IH_CHECK(o->n_stop >= 0 && (o->n_stop == 0 || o->stop_tokens), IH_EINVAL, "ih_decode: bad stop tokens");
   const int min_match = std::max(3, o->min_match), max_match = std::max(min_match, o->max_match);
@@ -127,7 +129,7 @@ int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint3
   hipStream_t s = c->stream;
   IH_HIP(hipMemcpyAsync(bf.st, st0, sizeof(st0), hipMemcpyHostToDevice, s));
   IH_HIP(hipMemcpyAsync(bf.vtok, vt0, sizeof(vt0), hipMemcpyHostToDevice, s));
-  if (B > 1) {
+  if (B > 1 && !o->drafter) {
     if (P0) IH_HIP(hipMemcpyAsync(bf.hist, history, size_t(P0) * 4, hipMemcpyHostToDevice, s));
     IH_HIP(hipMemcpyAsync(bf.hist + P0, &first, 4, hipMemcpyHostToDevice, s));
   }
@@ -141,14 +143,22 @@ int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint3
     while (enq - known < o->inflight) {
       const int pos_min = Pk + (enq - known), pos_max = Pk + (enq - known) * B;
       if (pos_max + B > cap) break;
-      if (B > 1) IH_TRY(launch_copy_lookup(c, bf.hist, cap + 1, B - 1, min_match, max_match, bf.copy, bf.vtok, B, bf.st));
+      if (o->drafter) {
+        // The rows the last round committed become drafter context (nvalid = st[2] at pos0 = st[3]), then the
+        // drafter writes this round's drafts after the anchor (DFlash2 rounds of decodeSpec).
+        IH_TRY(ih_drafter_context(o->drafter, B, 0, 0, bf.st));
+        IH_TRY(ih_drafter_block(o->drafter, bf.vtok, 0, bf.st, nullptr));
+      } else if (B > 1) {
+        IH_TRY(launch_copy_lookup(c, bf.hist, cap + 1, B - 1, min_match, max_match, bf.copy, bf.vtok, B, bf.st));
+      }
       IH_TRY(ih_verify_step_chained(m, kv, bf.vtok, B, bf.top1, bf.st, pos_min, pos_max));
       if (sp) {
         IH_TRY(launch_topk64(c, ih_model_logits_dev(m), d.vocab, B, d.vocab, sp->temp, bf.cidx, bf.cval, bf.cz));
         IH_TRY(launch_accept_sample(c, bf.st, bf.vtok, bf.cidx, bf.cval, bf.cz, rec_dev, bf.rnd, *sp, REC_RING, B,
-                                    B > 1 ? bf.hist : nullptr, cap + 1));
+                                    B > 1 && !o->drafter ? bf.hist : nullptr, cap + 1));
       } else {
-        IH_TRY(launch_accept(c, bf.st, bf.vtok, bf.top1, rec_dev, REC_RING, B, B > 1 ? bf.hist : nullptr, cap + 1));
+        IH_TRY(launch_accept(c, bf.st, bf.vtok, bf.top1, rec_dev, REC_RING, B, B > 1 && !o->drafter ? bf.hist : nullptr,
+                             cap + 1));
       }
       IH_HIP(hipEventRecord(bf.ev[enq % REC_RING], s));
       ++enq;

@@ -318,6 +318,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
       IH_TRY(launch_moe_down(c, L.down, m->hpair, m->hpair_nkb, m->max_pairs, f16, B, K, nent, m->entries,
                              L.down_bias, m->opair, H));
       IH_TRY(launch_moe_combine(c, m->opair, H, m->row_pair, m->pair_w, K, B, m->h, H, next_norm, m->act_attn));
+      IH_TRY(drafter_capture(m, l, B));
       continue;
     }
     // Gated FFN: act(r · gate) · (r · up) straight into the down projection's activation.
@@ -336,6 +337,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
     ed.nw = next_norm;
     ed.act_out = &m->act_attn;
     IH_TRY(launch_qmm_ex(c, L.down, 0, m->act_i, B, ed));
+    IH_TRY(drafter_capture(m, l, B));
   }
   QmmEpilogue eh;
   eh.mode = QM_F32_SCALE;

@@ -26,8 +26,11 @@ struct ih_layer {
   uint16_t* down_bias = nullptr;  // bf16 [E][H]
 };
 
+struct ih_drafter;
+
 struct ih_model {
   ih_ctx* ctx = nullptr;
+  ih_drafter* drafter = nullptr;  // the drafter whose captures the verify step writes (ih_model_set_drafter)
   ih_model_desc d{};
   uint64_t seed = 0;
   std::vector<ih_layer> layers;
@@ -80,6 +83,8 @@ int check_desc(const ih_model_desc& d);
 // MoE buffers) and its release (weights included).
 ih_model* model_new(ih_ctx* c, const ih_model_desc& d);
 int model_alloc_scratch(ih_model* m);
+// The verify step's hidden-state captures after layer `layer` for the attached drafter (drafter.hip).
+int drafter_capture(ih_model* m, int layer, int B);
 void model_release(ih_model* m);
 int qmat_mxfp4_create_dev(ih_ctx* c, const void* w, const void* s, int E, int N, int K, int il8, ih_qmat** out);
 }  // namespace ih

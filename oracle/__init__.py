@@ -87,6 +87,12 @@ _SIGS = [
     ("or_copy_index_append", None, [vp, vp, i32]),
     ("or_copy_index_propose", i32, [vp, i32, vp, vp]),
     ("or_splitmix64", None, [C.c_uint64, i32, vp]),
+    ("or_model_set_capture", None, [vp, i32, vp]),
+    ("or_model_captures", None, [vp, vp]),
+    ("or_drafter_create", vp, [vp, C.c_uint64, vp, C.c_uint64]),
+    ("or_drafter_free", None, [vp]),
+    ("or_drafter_context", None, [vp, vp, i32, i32, i32]),
+    ("or_drafter_block", None, [vp, C.c_uint32, i32, vp, vp]),
     ("or_topk64", None, [vp, i32, i32, C.c_float, vp, vp, vp]),
     ("or_sample_dist", i32, [vp, vp, C.c_float, C.c_float, vp, vp]),
     ("or_accept_sample", i32, [vp, i32, vp, vp, vp, vp, vp, vp]),
@@ -275,6 +281,15 @@ class OracleModel:
         assert lib().or_model_verify(self.h, _p(t), len(t), _p(logits), _p(top1)) == 0
         return logits, top1
 
+    def set_capture(self, layers):
+        self.cap_layers = np.ascontiguousarray(layers, np.int32)
+        lib().or_model_set_capture(self.h, len(self.cap_layers), _p(self.cap_layers))
+
+    def captures(self, rows):
+        out = np.empty((rows, len(self.cap_layers) * self.desc.hidden), np.uint16)
+        lib().or_model_captures(self.h, _p(out))
+        return out
+
     def free(self):
         if self.h:
             lib().or_model_free(self.h)
@@ -390,3 +405,30 @@ def rows_choose(conf, a, b, cost, kmin, kmax) -> int:
     b = np.ascontiguousarray(b, np.float32)
     cost = np.ascontiguousarray(cost, np.float32)
     return int(lib().or_rows_choose(_p(conf), _p(a), _p(b), _p(cost), kmin, kmax))
+
+
+# ---- DFlash2 drafter ------------------------------------------------------------------------------------------
+
+class OracleDrafter:
+    """The drafter with the synthetic weights of `desc` (ingot_amd._lib.DrafterDesc, same layout) for the target
+    model `tdesc` (seed `tseed`): its window rings in host memory."""
+
+    def __init__(self, desc, seed: int, tdesc, tseed: int):
+        self.desc = desc
+        self.h = lib().or_drafter_create(C.addressof(desc), seed, C.addressof(tdesc), tseed)
+
+    def context(self, caps, nvalid: int, pos0: int):
+        caps = np.ascontiguousarray(caps, np.uint16)
+        lib().or_drafter_context(self.h, _p(caps), caps.shape[0], nvalid, pos0)
+
+    def block(self, anchor: int, P: int):
+        M = self.desc.block - 1
+        drafts = np.empty(M, np.uint32)
+        conf = np.empty(M, np.float32)
+        lib().or_drafter_block(self.h, anchor, P, _p(drafts), _p(conf))
+        return drafts, conf
+
+    def free(self):
+        if self.h:
+            lib().or_drafter_free(self.h)
+            self.h = None

@@ -483,6 +483,9 @@ struct OrLayer {
 struct OrModel {
   or_model_desc d;
   int P = 0, cap = 0;
+  // Captured residual rows after the listed layers, bf16 [B][n · H] (capture_rows, yy_model.metal:94-104).
+  std::vector<int> cap_layers;
+  std::vector<uint16_t> caps;
   std::vector<OrLayer> layers;
   QMat embed, head;
   std::vector<uint16_t> final_norm;
@@ -629,6 +632,26 @@ static void moe_forward(const or_model_desc* d, const OrLayer& L, float* hres, i
     }
 }
 
+static void capture(OrModel* m, int l, const float* hres, int B) {
+  const int H = m->d.hidden, n = int(m->cap_layers.size());
+  for (int j = 0; j < n; ++j) {
+    if (m->cap_layers[j] != l) continue;
+    m->caps.resize(size_t(B) * n * H);
+    for (int r = 0; r < B; ++r)
+      for (int c = 0; c < H; ++c) m->caps[(size_t(r) * n + j) * H + c] = or_f32_to_bf16(hres[size_t(r) * H + c]);
+  }
+}
+
+void or_model_set_capture(void* h, int n, const int* layers) {
+  OrModel* m = static_cast<OrModel*>(h);
+  m->cap_layers.assign(layers, layers + n);
+}
+
+void or_model_captures(void* h, uint16_t* out) {
+  OrModel* m = static_cast<OrModel*>(h);
+  std::memcpy(out, m->caps.data(), m->caps.size() * 2);
+}
+
 // One verify step of B rows at position P (not advancing it): logits [B][vocab], top1 [B].
 int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint32_t* top1) {
   OrModel* m = static_cast<OrModel*>(h);
@@ -687,6 +710,7 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
     for (size_t i = 0; i < hres.size(); ++i) hres[i] += y[i];
     if (d->n_experts > 0) {
       moe_forward(d, L, hres.data(), B);
+      capture(m, l, hres.data(), B);
       continue;
     }
     or_rms_split(hres.data(), B, H, L.mlp_norm.data(), d->rms_eps, x.data(), rr.data());
@@ -698,6 +722,7 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
             or_glu(gu[size_t(t) * 2 * I + i], gu[size_t(t) * 2 * I + I + i], d->act, d->swiglu_limit)));
     L.down.apply(a.data(), B, y.data());
     for (size_t i = 0; i < hres.size(); ++i) hres[i] += y[i];
+    capture(m, l, hres.data(), B);
   }
   or_rms_split(hres.data(), B, H, m->final_norm.data(), d->rms_eps, x.data(), rr.data());
   m->head.apply(x.data(), B, logits);
@@ -1051,6 +1076,296 @@ int or_rows_choose(const float* conf, const float* a, const float* b, const floa
     }
   }
   return best;
+}
+
+
+// ---------------------------------------------------------------------------------------------------------------
+// The DFlash2 drafter (DFlash2Drafter, Sources/Ingot/Drafter.swift:300-550; yy_model.metal:151-614), with the synthetic
+// weights of the library's generator and the rounding points of its GPU path: bf16 activations into every projection
+// (the RMSNorm outputs, the conv outputs, the attention output, the SwiGLU), fp16 q and K/V in the rings.
+struct or_drafter_desc {
+  int n_layers, hidden, n_q_heads, head_dim, intermediate, block, window, n_targets;
+  int target_layers[8];
+  int rank, dyn_conv;
+  uint32_t mask_token;
+  float rope_theta, rms_eps;
+};
+
+static uint64_t dl_tensor(int l, uint64_t kind) { return 7000000 + 1000 * uint64_t(l) + kind; }
+static uint64_t dg_tensor(uint64_t kind) { return 7900000 + kind; }
+static float rbf(float x) { return or_bf16_to_f32(or_f32_to_bf16(x)); }
+static float rhf(float x) { return or_f16_to_f32(or_f32_to_f16(x)); }
+
+struct OrDLayer {
+  std::vector<uint16_t> n1, n2, qn, kn, abase, mbase;
+  QMat qkv, o, gu, down, aproj, mproj;
+  std::vector<float> kc, vc;  // [8][slots][HD], fp16 values
+};
+
+struct OrDrafter {
+  or_drafter_desc d;
+  int H = 0, HD = 0, QH = 0, QP = 0, I = 0, V = 0, slots = 0, G = 0, DYN = 0, Ht = 0;
+  std::vector<OrDLayer> layers;
+  QMat fc, hproj, embed, head;
+  std::vector<uint16_t> hnorm, fnorm, pred, succ;
+};
+
+void* or_drafter_create(const or_drafter_desc* d, uint64_t seed, const or_model_desc* td, uint64_t tseed) {
+  OrDrafter* r = new OrDrafter();
+  r->d = *d;
+  r->H = d->hidden;
+  r->HD = d->head_dim;
+  r->QH = d->n_q_heads;
+  r->QP = (r->QH + 16) * r->HD;
+  r->I = d->intermediate;
+  r->V = td->vocab;
+  r->Ht = td->hidden;
+  r->G = r->QH / 8;
+  r->slots = (d->window + 16 + 31) / 32 * 32;
+  r->DYN = 4 * (r->H / 16);
+  const int H = r->H, HD = r->HD;
+  const float sd = 0.02f;
+  r->embed.make(tseed, 1, td->vocab, td->hidden, sd);
+  r->head.make(tseed, 3, td->vocab, td->hidden, sd);
+  r->layers.resize(d->n_layers);
+  for (int l = 0; l < d->n_layers; ++l) {
+    OrDLayer& L = r->layers[l];
+    L.n1.resize(H); L.n2.resize(H); L.qn.resize(HD); L.kn.resize(HD);
+    or_synth_bf16(seed, dl_tensor(l, 0), H, 1.0f, 0.125f, L.n1.data());
+    or_synth_bf16(seed, dl_tensor(l, 1), H, 1.0f, 0.125f, L.n2.data());
+    or_synth_bf16(seed, dl_tensor(l, 2), HD, 1.0f, 0.125f, L.qn.data());
+    or_synth_bf16(seed, dl_tensor(l, 3), HD, 1.0f, 0.125f, L.kn.data());
+    L.qkv.make(seed, dl_tensor(l, 4), r->QP, H, sd);
+    L.o.make(seed, dl_tensor(l, 5), H, r->QH * HD, sd);
+    L.gu.make(seed, dl_tensor(l, 6), 2 * r->I, H, sd);
+    L.down.make(seed, dl_tensor(l, 7), H, r->I, sd);
+    if (d->dyn_conv) {
+      L.aproj.make(seed, dl_tensor(l, 8), r->DYN, H, sd);
+      L.mproj.make(seed, dl_tensor(l, 9), r->DYN, H, sd);
+      L.abase.resize(4 * H);
+      L.mbase.resize(4 * H);
+      for (int k = 0; k < 4; ++k) {
+        or_synth_bf16(seed, dl_tensor(l, 10) + 100 * k, H, k % 2 ? 0.0f : 1.0f, 0.1f, L.abase.data() + k * H);
+        or_synth_bf16(seed, dl_tensor(l, 11) + 100 * k, H, k % 2 ? 0.0f : 1.0f, 0.1f, L.mbase.data() + k * H);
+      }
+    }
+    L.kc.assign(size_t(8) * r->slots * HD, 0.f);
+    L.vc.assign(size_t(8) * r->slots * HD, 0.f);
+  }
+  r->fc.make(seed, dg_tensor(1), H, d->n_targets * td->hidden, sd);
+  r->hnorm.resize(H);
+  r->fnorm.resize(H);
+  or_synth_bf16(seed, dg_tensor(2), H, 1.0f, 0.125f, r->hnorm.data());
+  or_synth_bf16(seed, dg_tensor(3), H, 1.0f, 0.125f, r->fnorm.data());
+  if (d->rank > 0) {
+    r->hproj.make(seed, dg_tensor(4), d->rank, H, sd);
+    r->pred.resize(size_t(r->V) * d->rank);
+    r->succ.resize(size_t(r->V) * d->rank);
+    or_synth_bf16(seed, dg_tensor(5), r->pred.size(), 0.0f, 0.25f, r->pred.data());
+    or_synth_bf16(seed, dg_tensor(6), r->succ.size(), 0.0f, 0.25f, r->succ.data());
+  }
+  return r;
+}
+
+void or_drafter_free(void* h) { delete static_cast<OrDrafter*>(h); }
+
+// bf16(x · rsqrt(mean x² + eps) · w) of `rows` rows.
+static void dnorm(const float* x, int rows, int H, const uint16_t* w, float eps, float* out) {
+  for (int t = 0; t < rows; ++t) {
+    double ss = 0;
+    for (int c = 0; c < H; ++c) ss += double(x[size_t(t) * H + c]) * x[size_t(t) * H + c];
+    const float rr = 1.0f / std::sqrt(float(ss) / float(H) + eps);
+    for (int c = 0; c < H; ++c) out[size_t(t) * H + c] = rbf(x[size_t(t) * H + c] * rr * or_bf16_to_f32(w[c]));
+  }
+}
+
+// Per-head RMSNorm + RoPE at position pos (dnorm_rope), in place on HD values.
+static void dnorm_rope(float* x, int HD, const uint16_t* w, float pos, float eps, float theta) {
+  double ss = 0;
+  for (int i = 0; i < HD; ++i) ss += double(x[i]) * x[i];
+  const float rr = 1.0f / std::sqrt(float(ss) / float(HD) + eps);
+  float y[256];
+  for (int i = 0; i < HD; ++i) y[i] = x[i] * rr * or_bf16_to_f32(w[i]);
+  const int RH = HD / 2;
+  for (int d = 0; d < HD; ++d) {
+    const int i = d % RH;
+    const double ang = double(pos) * std::pow(double(theta), -double(i) / double(RH));
+    const float c = float(std::cos(ang)), s = float(std::sin(ang));
+    x[d] = d < RH ? y[d] * c - y[d + RH] * s : y[d] * c + y[d - RH] * s;
+  }
+}
+
+// Context rows: captures (bf16 values [rows][nT·Ht]) of positions pos0 + t, t < nvalid, into every layer's ring.
+void or_drafter_context(void* h, const uint16_t* caps, int rows, int nvalid, int pos0) {
+  OrDrafter* r = static_cast<OrDrafter*>(h);
+  const int H = r->H, HD = r->HD, K = r->d.n_targets * r->Ht;
+  std::vector<float> c(size_t(rows) * K), y(size_t(rows) * H), e(size_t(rows) * H), kv(size_t(rows) * 16 * HD);
+  for (size_t i = 0; i < c.size(); ++i) c[i] = or_bf16_to_f32(caps[i]);
+  r->fc.apply(c.data(), rows, y.data());
+  dnorm(y.data(), rows, H, r->hnorm.data(), r->d.rms_eps, e.data());
+  for (auto& L : r->layers) {
+    // The k|v rows of q|k|v.
+    QMat kvm;
+    kvm.N = 16 * HD;
+    kvm.K = H;
+    const size_t w0 = size_t(r->QH) * HD * H / 8, s0 = size_t(r->QH) * HD * H / 64;
+    kvm.w.assign(L.qkv.w.begin() + w0, L.qkv.w.end());
+    kvm.s.assign(L.qkv.s.begin() + s0, L.qkv.s.end());
+    kvm.b.assign(L.qkv.b.begin() + s0, L.qkv.b.end());
+    kvm.apply(e.data(), rows, kv.data());
+    for (int t = 0; t < nvalid; ++t) {
+      const int pos = pos0 + t, ring = pos % r->d.window;
+      for (int hh = 0; hh < 8; ++hh) {
+        float xk[256];
+        std::memcpy(xk, &kv[size_t(t) * 16 * HD + hh * HD], sizeof(float) * HD);
+        dnorm_rope(xk, HD, L.kn.data(), float(pos), r->d.rms_eps, r->d.rope_theta);
+        for (int i = 0; i < HD; ++i) {
+          L.kc[(size_t(hh) * r->slots + ring) * HD + i] = rhf(xk[i]);
+          L.vc[(size_t(hh) * r->slots + ring) * HD + i] = rhf(kv[size_t(t) * 16 * HD + (8 + hh) * HD + i]);
+        }
+      }
+    }
+  }
+}
+
+static bool dvisible(int n, int t, int P, int B, int W) {
+  if (n >= W) return n < W + B;
+  int back = (P - 1 - n) % W;
+  if (back < 0) back += W;
+  const int k = P - 1 - back;
+  return k >= 0 && P + t - k < W;
+}
+
+// Draft block at position P with the anchor; drafts [block − 1], conf [block − 1].
+void or_drafter_block(void* h, uint32_t anchor, int P, uint32_t* drafts, float* conf) {
+  OrDrafter* r = static_cast<OrDrafter*>(h);
+  const auto& d = r->d;
+  const int B = d.block, M = B - 1, H = r->H, HD = r->HD, QH = r->QH, I = r->I, G = r->G, GC = H / 16;
+  const bool conv = d.dyn_conv != 0;
+  std::vector<float> x(size_t(B) * H), xn(size_t(B) * H), a(size_t(B) * H), dyn(size_t(B) * r->DYN);
+  std::vector<float> qkv(size_t(B) * r->QP), att(size_t(B) * QH * HD), y(size_t(B) * H), gu(size_t(B) * 2 * I),
+      hb(size_t(B) * I);
+  for (int t = 0; t < B; ++t) {
+    const uint32_t tok = t == 0 ? anchor : d.mask_token;
+    or_dequant_int4(r->embed.w.data() + size_t(tok) * H / 8, r->embed.s.data() + size_t(tok) * H / 64,
+                    r->embed.b.data() + size_t(tok) * H / 64, 1, H, x.data() + size_t(t) * H);
+  }
+  auto conv_prep = [&](const std::vector<uint16_t>& base) {
+    for (int t = 0; t < B; ++t)
+      for (int c = 0; c < H; ++c) {
+        const int g = c / 16;
+        const float x0 = xn[size_t(t) * H + c], x1 = t > 0 ? xn[size_t(t - 1) * H + c] : 0.f;
+        const float k0 = or_bf16_to_f32(base[c]) + dyn[size_t(t) * r->DYN + g];
+        const float k1 = or_bf16_to_f32(base[H + c]) + dyn[size_t(t) * r->DYN + GC + g];
+        a[size_t(t) * H + c] = rbf(k0 * x0 + k1 * x1);
+      }
+  };
+  auto conv_fin = [&](const std::vector<uint16_t>& base) {
+    for (int t = 0; t < B; ++t)
+      for (int c = 0; c < H; ++c) {
+        const float y0 = y[size_t(t) * H + c];
+        if (!conv) { x[size_t(t) * H + c] += y0; continue; }
+        const int g = c / 16;
+        const float y1 = t > 0 ? y[size_t(t - 1) * H + c] : 0.f;
+        const float k0 = or_bf16_to_f32(base[2 * H + c]) + dyn[size_t(t) * r->DYN + 2 * GC + g];
+        const float k1 = or_bf16_to_f32(base[3 * H + c]) + dyn[size_t(t) * r->DYN + 3 * GC + g];
+        x[size_t(t) * H + c] += k0 * y0 + k1 * y1;
+      }
+  };
+  const float scale = float(1.0 / std::sqrt(double(HD)));
+  for (auto& L : r->layers) {
+    dnorm(x.data(), B, H, L.n1.data(), d.rms_eps, xn.data());
+    if (conv) {
+      L.aproj.apply(xn.data(), B, dyn.data());
+      conv_prep(L.abase);
+    } else {
+      a = xn;
+    }
+    L.qkv.apply(a.data(), B, qkv.data());
+    // Block rows: q (fp16), k and v into the ring's block slots.
+    std::vector<float> q(size_t(B) * QH * HD);
+    for (int t = 0; t < B; ++t) {
+      for (int hh = 0; hh < QH + 8; ++hh) {
+        float xv[256];
+        std::memcpy(xv, &qkv[size_t(t) * r->QP + hh * HD], sizeof(float) * HD);
+        dnorm_rope(xv, HD, hh < QH ? L.qn.data() : L.kn.data(), float(P + t), d.rms_eps, d.rope_theta);
+        for (int i = 0; i < HD; ++i) {
+          if (hh < QH) q[(size_t(t) * QH + hh) * HD + i] = rhf(xv[i]);
+          else L.kc[(size_t(hh - QH) * r->slots + d.window + t) * HD + i] = rhf(xv[i]);
+        }
+      }
+      for (int hh = 0; hh < 8; ++hh)
+        for (int i = 0; i < HD; ++i)
+          L.vc[(size_t(hh) * r->slots + d.window + t) * HD + i] = rhf(qkv[size_t(t) * r->QP + (QH + 8 + hh) * HD + i]);
+    }
+    // Attention: every visible slot, softmax in fp32.
+    for (int t = 0; t < B; ++t)
+      for (int hh = 0; hh < QH; ++hh) {
+        const int kvh = hh / G;
+        std::vector<float> s(r->slots, -std::numeric_limits<float>::infinity());
+        float mx = -std::numeric_limits<float>::infinity();
+        for (int n = 0; n < r->slots; ++n) {
+          if (!dvisible(n, t, P, B, d.window)) continue;
+          float acc = 0;
+          for (int i = 0; i < HD; ++i) acc += q[(size_t(t) * QH + hh) * HD + i] * L.kc[(size_t(kvh) * r->slots + n) * HD + i];
+          s[n] = acc * scale;
+          mx = std::max(mx, s[n]);
+        }
+        float l = 0;
+        std::vector<float> o(HD, 0.f);
+        for (int n = 0; n < r->slots; ++n) {
+          if (s[n] == -std::numeric_limits<float>::infinity()) continue;
+          const float p = std::exp(s[n] - mx);
+          l += p;
+          for (int i = 0; i < HD; ++i) o[i] += p * L.vc[(size_t(kvh) * r->slots + n) * HD + i];
+        }
+        for (int i = 0; i < HD; ++i) att[size_t(t) * QH * HD + hh * HD + i] = rbf(o[i] / l);
+      }
+    L.o.apply(att.data(), B, y.data());
+    conv_fin(L.abase);
+    dnorm(x.data(), B, H, L.n2.data(), d.rms_eps, xn.data());
+    if (conv) {
+      L.mproj.apply(xn.data(), B, dyn.data());
+      conv_prep(L.mbase);
+    } else {
+      a = xn;
+    }
+    L.gu.apply(a.data(), B, gu.data());
+    for (int t = 0; t < B; ++t)
+      for (int i = 0; i < I; ++i) {
+        const float g = gu[size_t(t) * 2 * I + i], u = gu[size_t(t) * 2 * I + I + i];
+        hb[size_t(t) * I + i] = rbf(g / (1.0f + std::exp(-g)) * u);
+      }
+    L.down.apply(hb.data(), B, y.data());
+    conv_fin(L.mbase);
+  }
+  std::vector<float> hid(size_t(M) * H), logits(size_t(M) * r->V), hp(size_t(M) * std::max(1, d.rank));
+  dnorm(x.data() + H, M, H, r->fnorm.data(), d.rms_eps, hid.data());
+  r->head.apply(hid.data(), M, logits.data());
+  if (d.rank > 0) r->hproj.apply(hid.data(), M, hp.data());
+  uint32_t prev = anchor;
+  for (int t = 0; t < M; ++t) {
+    const float* lr = logits.data() + size_t(t) * r->V;
+    std::vector<int> ids(r->V);
+    for (int i = 0; i < r->V; ++i) ids[i] = i;
+    std::partial_sort(ids.begin(), ids.begin() + 16, ids.end(),
+                      [&](int u, int v) { return lr[u] > lr[v] || (lr[u] == lr[v] && u < v); });
+    float scs[16], bs = -std::numeric_limits<float>::infinity();
+    int best = 0;
+    for (int j = 0; j < 16; ++j) {
+      double e = 0;
+      for (int q = 0; q < d.rank; ++q)
+        e += double(or_bf16_to_f32(r->pred[size_t(prev) * d.rank + q])) * hp[size_t(t) * d.rank + q] *
+             or_bf16_to_f32(r->succ[size_t(ids[j]) * d.rank + q]);
+      scs[j] = lr[ids[j]] + float(e);
+      if (scs[j] > bs) { bs = scs[j]; best = j; }
+    }
+    drafts[t] = uint32_t(ids[best]);
+    float z = 0;
+    for (int j = 0; j < 16; ++j) z += std::exp((scs[j] - bs) / 1.5f);
+    conf[t] = 1.0f / z;
+    prev = drafts[t];
+  }
 }
 
 }  // extern "C"
