@@ -435,7 +435,18 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     if (p.ss_in) rms_factors(p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, KW, lane);
   }
   __syncthreads();
-  // Sum over waves of output (token m, tile r, row rn of the tile).
+  // Sum over waves, in wave order, of every partial at once (independent, coalesced LDS reads spread over the whole
+  // workgroup), into wave 0's slots; the epilogue then reads one value per output.
+  if constexpr (KW > 1) {
+    for (int i = threadIdx.x; i < WST; i += 64 * KW) {
+      float v = red[i];
+#pragma unroll
+      for (int w = 1; w < KW; ++w) v += red[w * WST + i];
+      red[i] = v;
+    }
+    __syncthreads();
+  }
+  // The finished output (token m, tile r, row rn of the tile).
   auto val = [&](int m, int r, int rn) -> float {
     int i;
     if (X16 && m == 16) {
@@ -444,10 +455,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       const int tt = m >> 4, mm = m & 15;
       i = ((r * T + tt) * 4 + (mm & 3)) * 64 + 16 * (mm >> 2) + rn;
     }
-    float v = red[i];
-#pragma unroll
-    for (int w = 1; w < KW; ++w) v += red[w * WST + i];
-    return v;
+    return red[i];
   };
   if constexpr (MODE == QM_PART) {
     float* part = p.part + size_t(blockIdx.y) * MAX_TOK * p.Npad;
