@@ -199,7 +199,7 @@ typedef struct ih_model_desc {
 
 /* Creates a model with synthetic weights of `desc`'s shapes, deterministically from `seed` (counter-based SplitMix64
  * streams per tensor; any element is reproducible on the CPU). Replaces HybridModel's loader for the benchmark
- * configurations (Sources/Ingot/Model.swift); an MLX safetensors loader is a later addition. */
+ * configurations (Sources/Ingot/Model.swift); ih_model_load_mlx below loads real checkpoints. */
 int ih_model_create_synthetic(ih_ctx* ctx, const ih_model_desc* desc, uint64_t seed, ih_model** out);
 /* Loads an mlx-lm quantized checkpoint directory (config.json + model.safetensors, or shards listed in
  * model.safetensors.index.json; mapped with mmap): the loader of HybridModel (SafetensorsStore,
