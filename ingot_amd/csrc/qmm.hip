@@ -302,6 +302,12 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 #pragma unroll
   for (int d = 0; d < D; ++d) load_stage(d, kb0 + d);
 
+  // The RMSNorm factors of the input rows, while the first stages are on their way: their partials were requested
+  // first, so waiting for them does not wait for the weights, and no accumulator is live yet.
+  if constexpr (RMS_PRE) {
+    if (p.ss_in) rms_finish(rpf, p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, KW, lane);
+  }
+
 #pragma unroll
   for (int j = 0; j < NSB; ++j) {
     const int e = j * 64 + lane;
@@ -427,11 +433,9 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       for (int r = 0; r < R; ++r) red[wave * WST + NEL + r * 16 + lane] = acc16[r];
     }
   }
-  // The RMSNorm factors of the input rows, once the accumulators are in LDS (their loads and shuffles would otherwise
-  // keep every accumulator live across them).
-  if constexpr (RMS_PRE) {
-    if (p.ss_in) rms_finish(rpf, p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, KW, lane);
-  } else if constexpr (RMS) {
+  // Without the entry prefetch (one-wave workgroups, more rows than a wave prefetches): the RMSNorm factors once the
+  // accumulators are in LDS (their loads and shuffles would otherwise keep every accumulator live across them).
+  if constexpr (RMS && !RMS_PRE) {
     if (p.ss_in) rms_factors(p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, KW, lane);
   }
   __syncthreads();
