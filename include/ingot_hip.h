@@ -269,6 +269,10 @@ typedef struct ih_decode_opts {
   int min_match, max_match;    /* copy-from-context rule (CopyIndex minMatch / maxMatch; ≥ 3) */
   int inflight;                /* rounds enqueued ahead of the record the host reads (1…7) */
   struct ih_drafter* drafter;  /* non-null: DFlash2 drafts (rows = its block) instead of copy-from-context ones */
+  /* With a drafter, non-null: each round's verify rows are chosen on the device from the drafts' confidences
+   * (ih_spec_rows_choose_dev, spec_rows_choose in yy_model.metal:644-675; kmin ≥ 2, kmax ≤ rows) and only those rows
+   * take part in the acceptance (st[6] = rows); null: every row. The emitted tokens do not depend on it. */
+  const ih_rows_params* rows_params;
 } ih_decode_opts;
 #define IH_FINISH_LENGTH 0
 #define IH_FINISH_STOP 1

@@ -331,7 +331,8 @@ class DecodeOpts(C.Structure):
     """ih_decode_opts (include/ingot_hip.h)."""
 
     _fields_ = [("max_tokens", C.c_int), ("stop_tokens", vp), ("n_stop", C.c_int), ("rows", C.c_int),
-                ("min_match", C.c_int), ("max_match", C.c_int), ("inflight", C.c_int), ("drafter", vp)]
+                ("min_match", C.c_int), ("max_match", C.c_int), ("inflight", C.c_int), ("drafter", vp),
+                ("rows_params", vp)]
 
 
 class DrafterDesc(C.Structure):
@@ -497,12 +498,14 @@ class KVCache:
         return lib().ih_kv_capacity(self.handle)
 
     def decode_greedy(self, first: int, max_tokens: int, rows: int = 1, history=None, stop=(), inflight: int = 2,
-                      min_match: int = 3, max_match: int = 64, drafter: "Drafter | None" = None):
+                      min_match: int = 3, max_match: int = 64, drafter: "Drafter | None" = None,
+                      rows_params: "RowsParams | None" = None):
         """Chained greedy decoding (ih_decode_greedy): (emitted tokens, DecodeStats)."""
         stop_a = np.ascontiguousarray(np.asarray(stop, np.uint32).reshape(-1))
         o = DecodeOpts(max_tokens=max_tokens, stop_tokens=ptr(stop_a) if stop_a.size else None, n_stop=stop_a.size,
                        rows=rows, min_match=min_match, max_match=max_match, inflight=inflight,
-                       drafter=drafter.handle if drafter is not None else None)
+                       drafter=drafter.handle if drafter is not None else None,
+                       rows_params=C.addressof(rows_params) if rows_params is not None else None)
         hist = None if history is None else np.ascontiguousarray(np.asarray(history, np.uint32))
         out = np.zeros(max_tokens, np.uint32)
         n = C.c_int()
@@ -513,11 +516,14 @@ class KVCache:
         return [int(x) for x in out[: n.value]], st
 
     def decode_sample(self, first: int, max_tokens: int, params: "SampleParams", seed: int, rows: int = 1,
-                      history=None, stop=(), inflight: int = 2, min_match: int = 3, max_match: int = 64):
+                      history=None, stop=(), inflight: int = 2, min_match: int = 3, max_match: int = 64,
+                      drafter: "Drafter | None" = None, rows_params: "RowsParams | None" = None):
         """Chained decoding with temperature sampling (ih_decode_sample): (emitted tokens, DecodeStats)."""
         stop_a = np.ascontiguousarray(np.asarray(stop, np.uint32).reshape(-1))
         o = DecodeOpts(max_tokens=max_tokens, stop_tokens=ptr(stop_a) if stop_a.size else None, n_stop=stop_a.size,
-                       rows=rows, min_match=min_match, max_match=max_match, inflight=inflight)
+                       rows=rows, min_match=min_match, max_match=max_match, inflight=inflight,
+                       drafter=drafter.handle if drafter is not None else None,
+                       rows_params=C.addressof(rows_params) if rows_params is not None else None)
         hist = None if history is None else np.ascontiguousarray(np.asarray(history, np.uint32))
         out = np.zeros(max_tokens, np.uint32)
         n = C.c_int()

@@ -34,10 +34,11 @@ struct DecodeBuffers {
   float* cval = nullptr;
   float* cz = nullptr;       // [IH_MAX_ROWS][2]
   float* rnd = nullptr;      // uniforms [rounds][IH_RND_PER_ROUND]
+  float* conf = nullptr;     // row chooser: the drafts' confidences [IH_MAX_ROWS]
   std::vector<hipEvent_t> ev;
   ~DecodeBuffers() {
     if (c) (void)hipStreamSynchronize(c->stream);
-    void* d[] = {st, vtok, top1, hist, copy, cidx, cval, cz, rnd};
+    void* d[] = {st, vtok, top1, hist, copy, cidx, cval, cz, rnd, conf};
     for (void* p : d)
       if (p) (void)hipFree(p);
     if (rec) (void)hipHostFree(rec);
@@ -76,6 +77,9 @@ int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint3
   IH_CHECK(B == 1 || o->drafter || (history && n_history == P0), IH_EINVAL,
            "ih_decode: the copy drafter needs the history of the cache's positions (n_history == position)");
   IH_CHECK(o->n_stop >= 0 && (o->n_stop == 0 || o->stop_tokens), IH_EINVAL, "ih_decode: bad stop tokens");
+  const ih_rows_params* rp = o->rows_params;
+  IH_CHECK(!rp || (o->drafter && rp->kmin >= 2 && rp->kmin <= rp->kmax && rp->kmax <= B), IH_EINVAL,
+           "ih_decode: a row chooser needs a drafter and 2 <= kmin <= kmax <= rows");
   const int min_match = std::max(3, o->min_match), max_match = std::max(min_match, o->max_match);
   auto is_stop = [&](uint32_t t) {
     for (int i = 0; i < o->n_stop; ++i)
@@ -110,6 +114,7 @@ int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint3
   IH_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&rec_dev), bf.rec, 0));
   bf.ev.assign(REC_RING, nullptr);
   for (auto& e : bf.ev) IH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  if (rp) IH_HIP(hipMalloc(&bf.conf, IH_MAX_ROWS * 4));
   if (sp) {
     // Uniforms for every round this call can run (each round emits at least one token).
     const size_t nr = size_t(o->max_tokens + o->inflight + 2) * IH_RND_PER_ROUND;
@@ -147,18 +152,22 @@ int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint3
         // The rows the last round committed become drafter context (nvalid = st[2] at pos0 = st[3]), then the
         // drafter writes this round's drafts after the anchor (DFlash2 rounds of decodeSpec).
         IH_TRY(ih_drafter_context(o->drafter, B, 0, 0, bf.st));
-        IH_TRY(ih_drafter_block(o->drafter, bf.vtok, 0, bf.st, nullptr));
+        IH_TRY(ih_drafter_block(o->drafter, bf.vtok, 0, bf.st, rp ? bf.conf : nullptr));
+        // The verify rows of the round from the drafts' confidences (st[6]); every row is still verified (a dense
+        // step costs the same for any row count), only the chosen ones are accepted.
+        if (rp) IH_TRY(ih_spec_rows_choose_dev(c, bf.st, bf.conf, rp));
       } else if (B > 1) {
         IH_TRY(launch_copy_lookup(c, bf.hist, cap + 1, B - 1, min_match, max_match, bf.copy, bf.vtok, B, bf.st));
       }
       IH_TRY(ih_verify_step_chained(m, kv, bf.vtok, B, bf.top1, bf.st, pos_min, pos_max));
       if (sp) {
         IH_TRY(launch_topk64(c, ih_model_logits_dev(m), d.vocab, B, d.vocab, sp->temp, bf.cidx, bf.cval, bf.cz));
-        IH_TRY(launch_accept_sample(c, bf.st, bf.vtok, bf.cidx, bf.cval, bf.cz, rec_dev, bf.rnd, *sp, REC_RING, B,
+        IH_TRY(launch_accept_sample(c, bf.st, bf.vtok, bf.cidx, bf.cval, bf.cz, rec_dev, bf.rnd, *sp, REC_RING,
+                                    rp ? 0 : B,
                                     B > 1 && !o->drafter ? bf.hist : nullptr, cap + 1));
       } else {
-        IH_TRY(launch_accept(c, bf.st, bf.vtok, bf.top1, rec_dev, REC_RING, B, B > 1 && !o->drafter ? bf.hist : nullptr,
-                             cap + 1));
+        IH_TRY(launch_accept(c, bf.st, bf.vtok, bf.top1, rec_dev, REC_RING, rp ? 0 : B,
+                             B > 1 && !o->drafter ? bf.hist : nullptr, cap + 1));
       }
       IH_HIP(hipEventRecord(bf.ev[enq % REC_RING], s));
       ++enq;
@@ -174,7 +183,7 @@ int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint3
     const int mr = int(r[0]), pb = int(r[IH_REC_P]);
     IH_CHECK(mr >= 0 && mr < B && pb == Pk, IH_ESTATE, "ih_decode: round record out of sequence");
     ++sx.rounds;
-    sx.drafted += B - 1;
+    sx.drafted += int(r[IH_REC_ROWS]) - 1;
     sx.accepted += mr;
     for (int i = 0; i <= mr; ++i) {
       const uint32_t t = r[1 + i];

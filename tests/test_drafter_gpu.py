@@ -104,3 +104,42 @@ def test_drafter_rounds_equal_plain_decode(ctx, inflight):
         dr.free()
         kv.free()
         m.free()
+
+
+@pytest.mark.parametrize("kmin,kmax", [(4, 4), (2, 8)])
+def test_row_chooser_rounds_equal_plain_decode(ctx, kmin, kmax):
+    """DFlash2 rounds whose verify rows are chosen on the device from the drafts' confidences (spec_rows_choose,
+    yy_model.metal:644-675) still emit exactly the greedy tokens; the rounds' records carry the chosen rows (a fixed
+    choice k gives k − 1 drafts a round), and temperature sampling at top-k 1 is the same greedy output."""
+    from ingot_amd._lib import RowsParams, SampleParams
+    d = ModelDesc.make(**SMALL)
+    m = Model(ctx, d, 7)
+    kv = KVCache(m, 1024)
+    dr = Drafter(m, DrafterDesc.make(targets=(0, 1), **DF2), 5)
+    rp = RowsParams(kmin=kmin, kmax=kmax)
+    for g in range(4):
+        rp.a[g], rp.b[g] = 1.0, 0.5 - 0.25 * g
+    for k in range(18):
+        rp.cost[k] = 1.0 + 0.15 * k
+    try:
+        kv.fill_synthetic(300, 11)
+        ref = []
+        t = 17
+        for _ in range(30):
+            t = kv.verify_and_accept([t]).tokens[0]
+            ref.append(int(t))
+        kv.set_pos(300)
+        dr.attach()
+        out, st = kv.decode_greedy(17, 31, rows=8, inflight=2, drafter=dr, rows_params=rp)
+        assert out == [17] + ref and kv.pos == 330
+        assert (kmin - 1) * st.rounds <= st.drafted <= (kmax - 1) * st.rounds
+        if kmin == kmax:
+            assert st.drafted == (kmin - 1) * st.rounds
+        kv.set_pos(300)
+        out2, _ = kv.decode_sample(17, 31, SampleParams(temp=0.8, top_p=1.0, top_k=1, min_p=0.0), seed=3, rows=8,
+                                   inflight=2, drafter=dr, rows_params=rp)
+        assert out2 == out
+    finally:
+        dr.free()
+        kv.free()
+        m.free()
