@@ -274,10 +274,20 @@ struct Store {
       }
       Tensor t;
       t.dtype = dt->str;
-      for (const auto& d : sh->arr) t.shape.push_back(int64_t(d.num));
-      const size_t o0 = size_t(off->arr[0].num), o1 = size_t(off->arr[1].num);
+      // Every number must be a non-negative integer that fits the file (a JSON number is a double: reject negative,
+      // fractional or huge values before converting, so that no size computation below can wrap).
+      const double lim = double(m->size);
+      auto whole = [lim](const Json& v) { return v.kind == Json::NUM && v.num >= 0 && v.num <= lim && v.num == double(int64_t(v.num)); };
+      bool ok = whole(off->arr[0]) && whole(off->arr[1]);
+      for (const auto& d : sh->arr) {
+        ok = ok && d.kind == Json::NUM && d.num >= 0 && d.num <= double(int64_t(1) << 40) && d.num == double(int64_t(d.num));
+        if (ok) t.shape.push_back(int64_t(d.num));
+      }
+      const size_t o0 = ok ? size_t(off->arr[0].num) : 0, o1 = ok ? size_t(off->arr[1].num) : 0;
       const size_t es = dtype_size(t.dtype);
-      if (o1 < o0 || start + o1 > m->size || (es && size_t(t.count()) * es != o1 - o0)) {
+      double elems = 1;
+      for (const int64_t d : t.shape) elems *= double(d);
+      if (!ok || o1 < o0 || o1 > m->size - start || (es && (elems * double(es) != double(o1 - o0)))) {
         err = path + ": inconsistent size of " + kv.first;
         return false;
       }

@@ -127,3 +127,32 @@ def test_load_names_the_missing_tensor(ctx, tmp_path):
     with pytest.raises(IngotError) as e:
         Model.load_mlx(ctx, r)
     assert "model.layers.1.mlp.down_proj.biases" in str(e.value)
+
+
+@pytest.mark.parametrize("bad", ["negative", "fraction", "past_end", "huge_dim", "swapped"])
+def test_describe_rejects_malformed_headers(tmp_path, bad):
+    """Tensor entries whose offsets or shapes are negative, fractional, past the end of the file or inconsistent are
+    refused with the tensor named, before any size is computed from them (SafetensorsStore's header checks,
+    Loader/Safetensors.swift)."""
+    import struct
+    p = write_checkpoint(tmp_path, DENSE, seed=7)
+    f = p / "model.safetensors"
+    raw = f.read_bytes()
+    n = struct.unpack("<Q", raw[:8])[0]
+    head = json.loads(raw[8:8 + n])
+    name = "model.norm.weight"
+    o0, o1 = head[name]["data_offsets"]
+    if bad == "negative":
+        head[name]["data_offsets"] = [-2, o1]
+    elif bad == "fraction":
+        head[name]["data_offsets"] = [o0 + 0.5, o1]
+    elif bad == "past_end":
+        head[name]["data_offsets"] = [o0, len(raw) * 4]
+    elif bad == "huge_dim":
+        head[name]["shape"] = [2 ** 62]
+    else:
+        head[name]["data_offsets"] = [o1, o0]
+    h = json.dumps(head).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    f.write_bytes(struct.pack("<Q", len(h)) + h + raw[8 + n:])
+    expect_error(p, name)
