@@ -340,6 +340,8 @@ typedef struct ih_drafter ih_drafter;
 
 /* A drafter with synthetic weights for `target` (counter-based SplitMix64 streams, reproducible on the CPU). */
 int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, uint64_t seed, ih_drafter** out);
+/* Frees a drafter (detaching it from its model). A drafter whose model was freed first refuses further work with
+ * IH_EINVAL and can still be freed. */
 int ih_drafter_free(ih_drafter* drafter);
 /* Attaches the drafter to its target (null detaches): every verify step then captures its rows' residual after the
  * drafter's target layers (capture_rows, yy_model.metal:94-104; ModelRound.swift:72-75). */

@@ -19,6 +19,7 @@
 #include <cmath>
 #include <vector>
 
+#include <algorithm>
 #include "act.h"
 #include "lanes.h"
 #include "model_internal.h"
@@ -441,6 +442,13 @@ static int dalloc_t(T** p, size_t n) {
   return IH_OK;
 }
 
+// The target model is being freed: its drafters stay allocated for ih_drafter_free but refuse further work.
+void model_drafters_orphan(ih_model* m) {
+  for (ih_drafter* r : m->drafters) r->target = nullptr;
+  m->drafters.clear();
+  m->drafter = nullptr;
+}
+
 static void drafter_release(ih_drafter* r) {
   if (!r) return;
   for (auto& L : r->layers) {
@@ -596,6 +604,7 @@ int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, u
     drafter_release(r);
     return st;
   }
+  target->drafters.push_back(r);  // registered only once complete (a failed creation is released above)
   *out = r;
   return IH_OK;
 }
@@ -603,13 +612,17 @@ int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, u
 int ih_drafter_free(ih_drafter* r) {
   if (!r) return IH_OK;
   (void)hipStreamSynchronize(r->ctx->stream);
-  if (r->target && r->target->drafter == r) r->target->drafter = nullptr;
+  if (ih_model* t = r->target) {
+    if (t->drafter == r) t->drafter = nullptr;
+    t->drafters.erase(std::remove(t->drafters.begin(), t->drafters.end(), r), t->drafters.end());
+  }
   drafter_release(r);
   return IH_OK;
 }
 
 int ih_model_set_drafter(ih_model* m, ih_drafter* r) {
   IH_CHECK(m, IH_EINVAL, "ih_model_set_drafter: null model");
+  IH_CHECK(!r || r->target, IH_EINVAL, "ih_model_set_drafter: the drafter's target model was freed");
   IH_CHECK(!r || r->target == m, IH_EINVAL, "ih_model_set_drafter: the drafter was made for another model");
   m->drafter = r;
   return IH_OK;
@@ -617,6 +630,7 @@ int ih_model_set_drafter(ih_model* m, ih_drafter* r) {
 
 int ih_drafter_context(ih_drafter* r, int rows, int nvalid, int pos0, const uint32_t* st_dev) {
   IH_CHECK(r, IH_EINVAL, "ih_drafter_context: null drafter");
+  IH_CHECK(r->target, IH_EINVAL, "ih_drafter_context: the drafter's target model was freed");
   IH_CHECK(rows >= 1 && rows <= IH_MAX_ROWS, IH_EINVAL, "ih_drafter_context: rows must be in 1..17");
   IH_CHECK(st_dev || (nvalid >= 0 && nvalid <= rows && pos0 >= 0), IH_EINVAL, "ih_drafter_context: bad nvalid/pos0");
   ih_ctx* c = r->ctx;
@@ -643,6 +657,7 @@ int ih_drafter_context(ih_drafter* r, int rows, int nvalid, int pos0, const uint
 
 int ih_drafter_block(ih_drafter* r, uint32_t* vtok_dev, int P, const uint32_t* st_dev, float* conf_dev) {
   IH_CHECK(r && vtok_dev, IH_EINVAL, "ih_drafter_block: null argument");
+  IH_CHECK(r->target, IH_EINVAL, "ih_drafter_block: the drafter's target model was freed");
   IH_CHECK(st_dev || P >= 0, IH_EINVAL, "ih_drafter_block: negative position");
   ih_ctx* c = r->ctx;
   const auto& d = r->d;

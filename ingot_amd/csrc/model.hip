@@ -199,8 +199,11 @@ int check_desc(const ih_model_desc& d) {
   return IH_OK;
 }
 
+void model_drafters_orphan(ih_model* m);  // drafter.hip
+
 void model_release(ih_model* m) {
   if (!m) return;
+  model_drafters_orphan(m);
   for (auto& L : m->layers) {
     ih_qmat_free(L.qkv); ih_qmat_free(L.o); ih_qmat_free(L.gate_up); ih_qmat_free(L.down); ih_qmat_free(L.router);
     void* lp[] = {L.attn_norm, L.mlp_norm, L.sinks, L.router_bias, L.gu_bias, L.down_bias, L.q_norm, L.k_norm,

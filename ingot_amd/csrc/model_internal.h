@@ -31,6 +31,7 @@ struct ih_drafter;
 struct ih_model {
   ih_ctx* ctx = nullptr;
   ih_drafter* drafter = nullptr;  // the drafter whose captures the verify step writes (ih_model_set_drafter)
+  std::vector<ih_drafter*> drafters;  // every live drafter made for this model (orphaned when the model is freed)
   ih_model_desc d{};
   uint64_t seed = 0;
   std::vector<ih_layer> layers;

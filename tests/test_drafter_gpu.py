@@ -143,3 +143,18 @@ def test_row_chooser_rounds_equal_plain_decode(ctx, kmin, kmax):
         dr.free()
         kv.free()
         m.free()
+
+
+def test_drafter_outliving_its_model_refuses_work(ctx):
+    """Freeing the target model first orphans its drafters: their calls return IH_EINVAL instead of touching the freed
+    model, and freeing them afterwards is still fine."""
+    from ingot_amd._lib import IngotError
+    d = ModelDesc.make(**SMALL)
+    m = Model(ctx, d, 7)
+    dr = Drafter(m, DrafterDesc.make(targets=(0, 1), **DF2), 5)
+    dr.attach()
+    m.free()
+    with pytest.raises(IngotError) as e:
+        dr.context(4, 4, 0)
+    assert "freed" in str(e.value)
+    dr.free()
