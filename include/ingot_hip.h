@@ -226,6 +226,8 @@ int ih_kv_create(ih_model* model, int capacity, ih_kv** out);
  * fixed ranges [s·C, (s+1)·C) and merges them in order (pattn_i8 chunks, Attention.swift:389-390); the automatic C
  * gives one workgroup per CU over all KV heads at full capacity. */
 int ih_kv_create_chunked(ih_model* model, int capacity, int chunk, ih_kv** out);
+/* Frees a cache. A cache whose model was freed first refuses calls that need the model (IH_EINVAL) and can still be
+ * freed. */
 int ih_kv_free(ih_kv* kv);
 /* Fills positions 0..P-1 of every layer with synthetic int8 K/V (N(0,1) vectors quantised per token and head) and sets
  * the position to P. */

@@ -9,6 +9,7 @@
 #include <cstring>
 #include <memory>
 
+#include <algorithm>
 #include "act.h"
 #include "attn_args.h"
 #include "ih_internal.h"
@@ -204,6 +205,8 @@ void model_drafters_orphan(ih_model* m);  // drafter.hip
 void model_release(ih_model* m) {
   if (!m) return;
   model_drafters_orphan(m);
+  for (ih_kv* kv : m->caches) kv->model = nullptr;
+  m->caches.clear();
   for (auto& L : m->layers) {
     ih_qmat_free(L.qkv); ih_qmat_free(L.o); ih_qmat_free(L.gate_up); ih_qmat_free(L.down); ih_qmat_free(L.router);
     void* lp[] = {L.attn_norm, L.mlp_norm, L.sinks, L.router_bias, L.gu_bias, L.down_bias, L.q_norm, L.k_norm,
@@ -473,6 +476,7 @@ int ih_kv_create_chunked(ih_model* m, int capacity, int chunk, ih_kv** out) {
   const auto& d = m->d;
   ih_kv* kv = new ih_kv();
   kv->model = m;
+  kv->ctx = m->ctx;
   kv->cap = capacity;
   // Key chunk: fixed per cache, so a row's result is the same for every block size and every position (the splits
   // are fixed key ranges [s·C, (s+1)·C)). At full capacity the splits of all KV heads are one workgroup per CU: C =
@@ -509,13 +513,15 @@ int ih_kv_create_chunked(ih_model* m, int capacity, int chunk, ih_kv** out) {
     ih_kv_free(kv);
     return st;
   }
+  m->caches.push_back(kv);
   *out = kv;
   return IH_OK;
 }
 
 int ih_kv_free(ih_kv* kv) {
   if (!kv) return IH_OK;
-  (void)hipStreamSynchronize(kv->model->ctx->stream);
+  (void)hipStreamSynchronize(kv->ctx->stream);
+  if (ih_model* m = kv->model) m->caches.erase(std::remove(m->caches.begin(), m->caches.end(), kv), m->caches.end());
   for (size_t l = 0; l < kv->kc.size(); ++l) {
     if (kv->kc[l]) (void)hipFree(kv->kc[l]);
     if (kv->vc[l]) (void)hipFree(kv->vc[l]);
@@ -528,6 +534,7 @@ int ih_kv_free(ih_kv* kv) {
 
 int ih_kv_fill_synthetic(ih_kv* kv, int P, uint64_t seed) {
   IH_CHECK(kv, IH_EINVAL, "ih_kv_fill_synthetic: null cache");
+  IH_CHECK(kv->model, IH_EINVAL, "ih_kv_fill_synthetic: the cache's model was freed");
   IH_CHECK(P >= 0 && P <= kv->cap, IH_EINVAL, "ih_kv_fill_synthetic: P beyond the capacity");
   ih_model* m = kv->model;
   const auto& d = m->d;

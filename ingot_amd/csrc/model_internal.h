@@ -32,6 +32,7 @@ struct ih_model {
   ih_ctx* ctx = nullptr;
   ih_drafter* drafter = nullptr;  // the drafter whose captures the verify step writes (ih_model_set_drafter)
   std::vector<ih_drafter*> drafters;  // every live drafter made for this model (orphaned when the model is freed)
+  std::vector<ih_kv*> caches;         // every live cache made for this model (orphaned likewise)
   ih_model_desc d{};
   uint64_t seed = 0;
   std::vector<ih_layer> layers;
@@ -70,7 +71,8 @@ struct ih_model {
 };
 
 struct ih_kv {
-  ih_model* model = nullptr;
+  ih_model* model = nullptr;  // null once the model was freed (the cache then only frees)
+  ih_ctx* ctx = nullptr;
   int cap = 0, P = 0, written = 0, last_B = 0, chunk = 256;
   std::vector<int8_t*> kc, vc;
   std::vector<__half*> ks, vs;

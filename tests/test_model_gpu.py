@@ -230,3 +230,17 @@ def test_sliding_window_rows_are_block_invariant(ctx, chunk):
     finally:
         kv.free()
         m.free()
+
+
+def test_cache_outliving_its_model_refuses_work(ctx):
+    """Freeing the model first orphans its caches: a cache call that needs the model returns IH_EINVAL instead of
+    touching freed memory, and the cache still frees."""
+    from ingot_amd._lib import IngotError
+    d = ModelDesc.make(**SMALL)
+    m = Model(ctx, d, 7)
+    kv = KVCache(m, 256)
+    m.free()
+    with pytest.raises(IngotError) as e:
+        kv.fill_synthetic(10, 1)
+    assert "freed" in str(e.value)
+    kv.free()
