@@ -43,6 +43,7 @@ int ih_version(void);
 /* Creates a context on HIP device `device` with its own stream. Replaces MetalContext (Sources/Ingot/GPU.swift:6-151:
  * device, queue, library). */
 int ih_init(int device, ih_ctx** out);
+/* Frees a context. Free the objects made on it (matrices, models, caches, drafters) first: they use its stream. */
 int ih_ctx_free(ih_ctx* ctx);
 /* Waits for all work enqueued on the context's stream (Metal: cb.waitUntilCompleted, Generate.swift:394-398). */
 int ih_sync(ih_ctx* ctx);
