@@ -612,6 +612,7 @@ int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, u
 int ih_drafter_free(ih_drafter* r) {
   if (!r) return IH_OK;
   (void)hipStreamSynchronize(r->ctx->stream);
+  ++r->ctx->gen;
   if (ih_model* t = r->target) {
     if (t->drafter == r) t->drafter = nullptr;
     t->drafters.erase(std::remove(t->drafters.begin(), t->drafters.end(), r), t->drafters.end());
@@ -624,6 +625,7 @@ int ih_model_set_drafter(ih_model* m, ih_drafter* r) {
   IH_CHECK(m, IH_EINVAL, "ih_model_set_drafter: null model");
   IH_CHECK(!r || r->target, IH_EINVAL, "ih_model_set_drafter: the drafter's target model was freed");
   IH_CHECK(!r || r->target == m, IH_EINVAL, "ih_model_set_drafter: the drafter was made for another model");
+  if (m->drafter != r) ++m->ctx->gen;
   m->drafter = r;
   return IH_OK;
 }

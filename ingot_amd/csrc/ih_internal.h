@@ -115,6 +115,9 @@ struct TimingRec {
 struct ih_ctx {
   int device = 0;
   bool timing = false;
+  // Bumped whenever a buffer that recorded verify steps may point to is freed or replaced (scratch growth, a cache
+  // or drafter freed, the drafter switched): replaying a step graph of an older generation is never allowed.
+  uint64_t gen = 0;
   std::vector<ih::TimingRec> trecs;
   std::vector<hipEvent_t> ev_pool;
   size_t ev_used = 0;
@@ -152,7 +155,8 @@ struct TimedLaunch {
 template <typename F, typename... Args>
 inline void tlaunch(const TimedLaunch& tl, F kernel, dim3 grid, dim3 block, unsigned shmem, hipStream_t s,
                     Args... args) {
-  hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, tl.a, tl.b, 0u, args...);
+  if (tl.a) hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, tl.a, tl.b, 0u, args...);
+  else hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
 }
 int fill(ih_ctx* c, void* dst, int byte, size_t bytes);
 int init_noalloc_scratch(ih_ctx* c);

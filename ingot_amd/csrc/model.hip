@@ -202,8 +202,16 @@ int check_desc(const ih_model_desc& d) {
 
 void model_drafters_orphan(ih_model* m);  // drafter.hip
 
+static void drop_graphs(ih_model* m) {
+  for (auto& g : m->graphs)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  m->graphs.clear();
+  m->has_last = false;
+}
+
 void model_release(ih_model* m) {
   if (!m) return;
+  drop_graphs(m);
   model_drafters_orphan(m);
   for (ih_kv* kv : m->caches) kv->model = nullptr;
   m->caches.clear();
@@ -226,6 +234,7 @@ void model_release(ih_model* m) {
 
 static int ensure_partials(ih_model* m, int splits) {
   if (size_t(splits) <= m->part_splits) return IH_OK;
+  ++m->ctx->gen;
   if (m->opart) (void)hipFree(m->opart);
   if (m->ml) (void)hipFree(m->ml);
   m->opart = nullptr; m->ml = nullptr;
@@ -354,6 +363,61 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
   IH_TRY(launch_argmax(c, m->logits, d.vocab, B, d.vocab, top1));
   kv->last_B = B;
   kv->written = std::max(kv->written, pos_max + B);
+  return IH_OK;
+}
+
+// run_step through the step graphs: a step whose key (StepGraph) matches a recorded graph is replayed with one
+// hipGraphLaunch instead of its ~230 kernel launches; a key seen on two consecutive calls is recorded on the second
+// (the first runs eagerly, so every scratch buffer has its final size before recording). Graphs are not used while
+// per-kernel timing is on (its events stamp individual launches) or with IH_NO_GRAPH set.
+constexpr size_t kMaxGraphs = 8;
+static int run_step_graphed(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t* top1, uint32_t* st = nullptr,
+                            int pos_min = -1, int pos_max = -1) {
+  ih_ctx* c = m->ctx;
+  static const bool off = getenv("IH_NO_GRAPH") != nullptr;
+  if (off || c->timing) return run_step(m, kv, B, tok, top1, st, pos_min, pos_max);
+  StepGraph k;
+  k.kv = kv; k.B = B; k.tok = tok; k.top1 = top1; k.st = st;
+  k.pos_min = st ? pos_min : -1; k.pos_max = st ? pos_max : -1; k.P = st ? -1 : kv->P;
+  k.drafter = m->drafter; k.gen = c->gen;
+  const int pend = (st ? pos_max : kv->P) + B;  // run_step's host bookkeeping, applied on replay
+  for (auto& g : m->graphs)
+    if (g.same(k)) {
+      IH_HIP(hipGraphLaunch(g.exec, c->stream));
+      kv->last_B = B;
+      kv->written = std::max(kv->written, pend);
+      return IH_OK;
+    }
+  if (!(m->has_last && m->last_eager.same(k))) {
+    IH_TRY(run_step(m, kv, B, tok, top1, st, pos_min, pos_max));
+    k.gen = c->gen;  // scratch grown by this step is part of what a recording of it would use
+    m->last_eager = k;
+    m->has_last = true;
+    return IH_OK;
+  }
+  hipGraph_t g = nullptr;
+  IH_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  const int rs = run_step(m, kv, B, tok, top1, st, pos_min, pos_max);
+  const hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (rs != IH_OK || e != hipSuccess || !g || c->gen != k.gen) {
+    if (g) (void)hipGraphDestroy(g);
+    m->has_last = false;
+    if (rs != IH_OK) return rs;
+    // Nothing of the recorded step ran: run it eagerly.
+    (void)hipGetLastError();
+    return run_step(m, kv, B, tok, top1, st, pos_min, pos_max);
+  }
+  hipGraphExec_t ex = nullptr;
+  const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (ei != hipSuccess) return fail(IH_EDEVICE, std::string("verify: graph instantiation failed: ") + hipGetErrorString(ei));
+  if (m->graphs.size() >= kMaxGraphs) {
+    (void)hipGraphExecDestroy(m->graphs.front().exec);
+    m->graphs.erase(m->graphs.begin());
+  }
+  k.exec = ex;
+  m->graphs.push_back(k);
+  IH_HIP(hipGraphLaunch(ex, c->stream));
   return IH_OK;
 }
 
@@ -521,6 +585,7 @@ int ih_kv_create_chunked(ih_model* m, int capacity, int chunk, ih_kv** out) {
 int ih_kv_free(ih_kv* kv) {
   if (!kv) return IH_OK;
   (void)hipStreamSynchronize(kv->ctx->stream);
+  ++kv->ctx->gen;
   if (ih_model* m = kv->model) m->caches.erase(std::remove(m->caches.begin(), m->caches.end(), kv), m->caches.end());
   for (size_t l = 0; l < kv->kc.size(); ++l) {
     if (kv->kc[l]) (void)hipFree(kv->kc[l]);
@@ -577,7 +642,7 @@ int ih_kv_commit(ih_kv* kv, int n) {
 int ih_verify_step_dev(ih_model* m, ih_kv* kv, const uint32_t* tokens_dev, int B, uint32_t* top1_dev) {
   IH_TRY(check_step(m, kv, B));
   IH_CHECK(tokens_dev && top1_dev, IH_EINVAL, "ih_verify_step_dev: null buffer");
-  IH_TRY(run_step(m, kv, B, tokens_dev, top1_dev));
+  IH_TRY(run_step_graphed(m, kv, B, tokens_dev, top1_dev));
   return IH_OK;
 }
 
@@ -590,7 +655,7 @@ int ih_verify_step_chained(ih_model* m, ih_kv* kv, const uint32_t* tokens_dev, i
   IH_CHECK(pos_max + B <= kv->cap, IH_EINVAL,
            "ih_verify_step_chained: context overflow (pos_max + B = " + std::to_string(pos_max + B) + " > capacity " +
                std::to_string(kv->cap) + ")");
-  return run_step(m, kv, B, tokens_dev, top1_dev, st_dev, pos_min, pos_max);
+  return run_step_graphed(m, kv, B, tokens_dev, top1_dev, st_dev, pos_min, pos_max);
 }
 
 int ih_kv_capacity(const ih_kv* kv) { return kv ? kv->cap : 0; }
@@ -602,7 +667,7 @@ int ih_verify_step(ih_model* m, ih_kv* kv, const uint32_t* tokens, int B, float*
     IH_CHECK(tokens[i] < uint32_t(m->d.vocab), IH_EINVAL, "ih_verify_step: token id beyond the vocabulary");
   hipStream_t s = m->ctx->stream;
   IH_HIP(hipMemcpyAsync(m->tok, tokens, B * 4, hipMemcpyHostToDevice, s));
-  IH_TRY(run_step(m, kv, B, m->tok, m->top1));
+  IH_TRY(run_step_graphed(m, kv, B, m->tok, m->top1));
   IH_HIP(hipMemcpyAsync(top1_out, m->top1, B * 4, hipMemcpyDeviceToHost, s));
   if (logits_out)
     IH_HIP(hipMemcpyAsync(logits_out, m->logits, size_t(B) * m->d.vocab * 4, hipMemcpyDeviceToHost, s));

@@ -28,6 +28,24 @@ struct ih_layer {
 
 struct ih_drafter;
 
+// A recorded verify step (HIP graph) and what it was recorded for: the cache, the rows, the token/top1/state
+// buffers, the position range (chained rounds) or the host position, the drafter and the context's generation.
+struct StepGraph {
+  const ih_kv* kv = nullptr;
+  int B = 0;
+  const uint32_t* tok = nullptr;
+  const uint32_t* top1 = nullptr;
+  const uint32_t* st = nullptr;
+  int pos_min = 0, pos_max = 0, P = 0;
+  const void* drafter = nullptr;
+  uint64_t gen = 0;
+  hipGraphExec_t exec = nullptr;
+  bool same(const StepGraph& o) const {
+    return kv == o.kv && B == o.B && tok == o.tok && top1 == o.top1 && st == o.st && pos_min == o.pos_min &&
+           pos_max == o.pos_max && P == o.P && drafter == o.drafter && gen == o.gen;
+  }
+};
+
 struct ih_model {
   ih_ctx* ctx = nullptr;
   ih_drafter* drafter = nullptr;  // the drafter whose captures the verify step writes (ih_model_set_drafter)
@@ -68,6 +86,11 @@ struct ih_model {
   void* hpair = nullptr;
   float* opair = nullptr;
   int hpair_nkb = 0, max_pairs = 0;
+  // Verify steps recorded as HIP graphs (at most kMaxGraphs, oldest evicted) and the key of the last step run
+  // eagerly: a key seen twice in a row is recorded, then replayed while it recurs.
+  std::vector<StepGraph> graphs;
+  StepGraph last_eager;
+  bool has_last = false;
 };
 
 struct ih_kv {

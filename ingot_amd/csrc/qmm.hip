@@ -115,6 +115,8 @@ struct QmmParams {
   // qmm_finish_kernel, which then runs the epilogue.
   float* part;
   int nsplit;
+  unsigned long long* stamp;  // clock stamps of an instrumented build ([workgroup][wave][32]), else unused
+  int noload;                 // instrumented build: skip the weight and x loads
 };
 
 // The epilogue of the R tiles tile0 … tile0+R−1 of a workgroup of nthr threads, given val(m, r, rn) = the finished
@@ -221,19 +223,39 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, int tile0, V va
 // p.part and qmm_finish_kernel adds the splits in order. No atomics and no cross-workgroup fences (an agent-scope
 // release on MI355X writes back the XCD's L2: ~15 µs per launch), and a row's summation order depends only on
 // (N, K), never on M.
+#ifdef IH_QMM_STAMP
+// Instrumented build: wave-private clock stamps (low 32 bits of the 100 MHz real-time counter) kept in LDS and written
+// out once at the end, so that the stamps add no live registers to the main loop.
+#define QSTAMP(i)                                                                                               \
+  do {                                                                                                          \
+    if constexpr (T == 1) qstamp_lds[wave][i] = unsigned(__builtin_amdgcn_s_memrealtime());                     \
+  } while (0)
+#else
+#define QSTAMP(i) do { } while (0)
+#endif
 template <int T, int R, int KW, bool X16, int D, int KPW, int MODE>
 __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   static_assert(KPW % D == 0, "the ring depth divides the K-blocks of a wave");
   // The wave index is uniform: readfirstlane keeps it (and everything derived from it) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, qd = lane >> 4;
+#ifdef IH_QMM_STAMP
+  __shared__ unsigned qstamp_lds[KW][32];
+#endif
+  QSTAMP(0);
   const int tile0 = blockIdx.x * R;
   constexpr int nk = KPW;                                // K-blocks of every wave
   const int kwg = int(blockIdx.y) * KW * nk;             // first K-block of the workgroup
   const int kb0 = kwg + wave * nk;                       // first K-block of this wave
   const unsigned tiles_total = unsigned(p.Npad / 16) * unsigned(p.nkb);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, tiles_total * 1024u), rsb = make_rsrc(p.s, tiles_total * 128u),
-                               rx = make_rsrc(p.xa, unsigned(MAX_TOK) * p.nkb * 256u);
+#ifdef IH_QMM_STAMP
+  // Instrumented build: with p.noload the weight and x loads read nothing (compute and launch cost alone).
+  const unsigned wlim = p.noload ? 0u : tiles_total * 1024u, xlim = p.noload ? 0u : unsigned(MAX_TOK) * p.nkb * 256u;
+#else
+  const unsigned wlim = tiles_total * 1024u, xlim = unsigned(MAX_TOK) * p.nkb * 256u;
+#endif
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, wlim), rsb = make_rsrc(p.s, tiles_total * 128u),
+                               rx = make_rsrc(p.xa, xlim);
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
 
   // Epilogue inputs that another kernel just wrote, requested first (consumed after the main loop). Rows per wave of
@@ -307,6 +329,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   if constexpr (RMS_PRE) {
     if (p.ss_in) rms_finish(rpf, p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, KW, lane);
   }
+  QSTAMP(18);
 
 #pragma unroll
   for (int j = 0; j < NSB; ++j) {
@@ -324,6 +347,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     }
   }
 
+  QSTAMP(19);
   f32x4 acc[R][T];
   float acc16[R];
 #pragma unroll
@@ -367,9 +391,14 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
         xs16[g] = z[0];
       }
     }
+    // The scale/bias words of all R tiles, requested together before the first product so that one LDS latency per
+    // K-block is exposed instead of one per tile (the fence after each tile keeps later reads from being hoisted).
+    uint2 sbv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) sbv[r] = sbl[(r * nk + kl) * 16];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint2 sb = sbl[(r * nk + kl) * 16];
+      const uint2 sb = sbv[r];
       const float s0 = __uint_as_float(sb.x << 16), s1 = __uint_as_float(sb.y << 16);
       const float c0 = fmaf(-128.f, s0, __uint_as_float(sb.x & 0xFFFF0000u));
       const float c1 = fmaf(-128.f, s1, __uint_as_float(sb.y & 0xFFFF0000u));
@@ -410,11 +439,16 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     for (int d = 0; d < D; ++d) {
       compute(d, i + d);
       load_stage(d, kb0 + i + d + D);
+      QSTAMP(2 + ((i + d) & 15));
     }
   }
 #pragma unroll
-  for (int d = 0; d < D; ++d) compute(d, i + d);
+  for (int d = 0; d < D; ++d) {
+    compute(d, i + d);
+    QSTAMP(2 + ((i + d) & 15));
+  }
 
+  QSTAMP(1);
   // Partial sums of every wave → LDS [wave][r][tt][e][lane] (+ token 16 [wave][r][row]), then fixed-order sums.
   constexpr int NEL = R * T * 4 * 64;
   constexpr int NEL16 = X16 ? R * 16 : 0;
@@ -468,8 +502,14 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       part[size_t(m) * p.Npad + tile0 * 16 + rr] = val(m, rr >> 4, rr & 15);
     }
   } else {
+    QSTAMP(26);
     qmm_epilogue<R, MODE>(p, tile0, val, rsc, ssu, 64 * KW, blockIdx.x, &hpf);
   }
+  QSTAMP(27);
+#ifdef IH_QMM_STAMP
+  if constexpr (T == 1)
+    if (p.stamp && lane < 32) p.stamp[(size_t(blockIdx.x) * 16 + wave) * 32 + lane] = qstamp_lds[wave][lane];
+#endif
 }
 
 // Adds the split partial sums in split order and runs the epilogue: workgroup = 4 tiles (64 rows), 256 threads.
@@ -604,6 +644,17 @@ int launch_act_from_f32(ih_ctx* c, const float* x, int ldx, int M, ActBuf& a) {
   return IH_OK;
 }
 
+#ifdef IH_QMM_STAMP
+static unsigned long long* g_stamp = nullptr;
+static int g_stamp_n = -1, g_stamp_k = -1;
+extern "C" int ih_dbg_qmm_stamp(void* dev, int N, int K) {
+  g_stamp = static_cast<unsigned long long*>(dev);
+  g_stamp_n = N;
+  g_stamp_k = K;
+  return 0;
+}
+#endif
+
 int qmm_grid(const ih_qmat* W) {
   const QmmShape sh = qmm_shape(W->Npad, W->nkb);
   return W->Npad / (16 * sh.R);
@@ -612,6 +663,7 @@ int qmm_grid(const ih_qmat* W) {
 // Split-K partial sums: grown on demand, the stream drained before an old buffer is freed.
 static int ensure_qpart(ih_ctx* c, size_t bytes) {
   if (c->qpart_bytes >= bytes) return IH_OK;
+  ++c->gen;
   IH_HIP(hipStreamSynchronize(c->stream));
   if (c->qpart) IH_HIP(hipFree(c->qpart));
   c->qpart = nullptr;
@@ -660,6 +712,10 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   p.kmask = 0x000F000Fu;
   p.kbias = 0x43004300u;
   p.nsplit = ks;
+#ifdef IH_QMM_STAMP
+  p.stamp = (W->N == g_stamp_n && W->K == g_stamp_k) ? g_stamp : nullptr;
+  p.noload = getenv("IH_QMM_NOLOAD") != nullptr;
+#endif
   if (ep.mode == QM_F32_SCALE || ep.mode == QM_GLU_ACT) {
     IH_CHECK(a.ss && a.nss > 0, IH_EINVAL, "qmm: the input activation carries no RMSNorm sums");
     p.ss_in = a.ss;

@@ -60,6 +60,7 @@ TimedLaunch::~TimedLaunch() {
 
 int ensure_part(ih_ctx* c, size_t bytes) {
   if (c->part_bytes >= bytes) return IH_OK;
+  ++c->gen;
   IH_HIP(hipStreamSynchronize(c->stream));  // kernels already queued may still read the old buffer
   if (c->part) IH_HIP(hipFree(c->part));
   c->part = nullptr;
@@ -84,6 +85,7 @@ int ensure_act(ih_ctx* c, ActBuf& a, int K, bool f16) {
     return IH_OK;
   }
   free_act(a);
+  ++c->gen;
   const int ss_cap = SS_CAP;
   size_t fb = size_t(MAX_TOK) * nkb * 256, sb = size_t(ss_cap) * MAX_TOK * 4;
   if (hipMalloc(&a.frag, fb) != hipSuccess || hipMalloc(&a.ss, sb) != hipSuccess) {

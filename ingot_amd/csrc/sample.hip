@@ -294,6 +294,7 @@ __global__ void rows_choose_kernel(uint32_t* st, const float* conf, ih_rows_para
 
 int ensure_samp(ih_ctx* c, size_t bytes) {
   if (c->samp_bytes >= bytes) return IH_OK;
+  ++c->gen;
   IH_HIP(hipStreamSynchronize(c->stream));
   if (c->samp) IH_HIP(hipFree(c->samp));
   c->samp = nullptr;

@@ -244,3 +244,31 @@ def test_cache_outliving_its_model_refuses_work(ctx):
         kv.fill_synthetic(10, 1)
     assert "freed" in str(e.value)
     kv.free()
+
+
+@pytest.mark.parametrize("shape", [GQA4, MOEX], ids=["dense-gqa4", "moe-mxfp4"])
+def test_recorded_step_replays_match_the_eager_step(shape):
+    """A verify step with the same key on consecutive calls is recorded as a HIP graph on the second call and replayed
+    afterwards. Every replay must give the bits of the first, eager step, also with other (eager) steps, host copies
+    and synchronisations between the replays, and a step that changes the key must not replay a stale recording."""
+    ctx = Context(0)
+    d, m, kv = make(ctx, shape, P=300)
+    toks = (np.arange(17, dtype=np.uint32) * 53 + 5) % d.vocab
+    top_ref, log_ref = kv.verify(toks, want_logits=True)  # eager (first sight of the key)
+    for i in range(4):  # recorded on the first of these, then replayed
+        top, logits = kv.verify(toks, want_logits=True)
+        assert np.array_equal(top, top_ref) and np.array_equal(logits, log_ref), f"replay {i} differs"
+        other = kv.verify(toks[: 5 + i])  # a different key in between (eager)
+        if not d.n_experts:  # dense rows do not depend on the block's other rows
+            assert np.array_equal(other, top_ref[: 5 + i])
+    # A new position is a new key: the first step there runs eagerly and its replays repeat it; none of them is a
+    # replay of the recording at P = 300 (the rows' positions, hence their logits, differ).
+    kv.set_pos(301)
+    top_new, log_new = kv.verify(toks, want_logits=True)
+    assert not np.array_equal(log_new, log_ref)
+    for i in range(3):
+        top, logits = kv.verify(toks, want_logits=True)
+        assert np.array_equal(top, top_new) and np.array_equal(logits, log_new), f"replay {i} at P = 301 differs"
+    kv.free()
+    m.free()
+    ctx.close()
