@@ -72,6 +72,7 @@ constexpr int MAX_TOK = 32;     // tokens per qmm (two 16-token MFMA tiles)
 // (token-major, SS_CAP partials per row, so that one row's partials are one contiguous read): the consumer adds them
 // in order and applies the per-row factor in its epilogue.
 constexpr int SS_CAP = 4096;
+constexpr int QCTR_CAP = 16384;  // row groups of one split-K qmm launch
 struct ActBuf {
   void* frag = nullptr;   // [nkb][ntile][4][1 KB] (bf16 or fp16 elements)
   int ntile = MAX_TOK / 16;
@@ -128,6 +129,7 @@ struct ih_ctx {
   // Split-K partial sums of the qmm ([split][MAX_TOK][Npad] fp32), grown on demand.
   float* qpart = nullptr;
   size_t qpart_bytes = 0;
+  unsigned* qctr = nullptr;  // arrival counters of the in-kernel split-K reduction [QCTR_CAP]
   // Staging for the kernel-level entry points that take a natural-layout activation.
   ih::ActBuf act;
   size_t act_cap_k = 0;

@@ -115,6 +115,8 @@ struct QmmParams {
   // qmm_finish_kernel, which then runs the epilogue.
   float* part;
   int nsplit;
+  // K split over workgroups with a fused epilogue: arrival counters, one per row group (zero between launches).
+  unsigned* ctr;
   unsigned long long* stamp;  // clock stamps of an instrumented build ([workgroup][wave][32]), else unused
   int noload;                 // instrumented build: skip the weight and x loads
 };
@@ -502,6 +504,63 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       part[size_t(m) * p.Npad + tile0 * 16 + rr] = val(m, rr >> 4, rr & 15);
     }
   } else {
+    if (gridDim.y > 1) {
+      // K split over gridDim.y workgroups: each writes its partial sums with agent-coherent stores (they bypass the
+      // XCD's L2, so no cache write-back is needed), then counts itself in on the row group's counter; the last to
+      // arrive adds the partials in split order (its own from LDS) and runs the epilogue, the others exit. No
+      // workgroup waits for another, and the sum's order depends only on the split, not on who arrives last.
+      const int nsp = int(gridDim.y), me = int(blockIdx.y);
+      const unsigned sstride = unsigned(MAX_TOK) * unsigned(p.Npad);  // floats per split
+      const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part, unsigned(nsp) * sstride * 4u);
+      // Quads of 4 consecutive rows of one token: slot of (m, 4q) in red, byte offset in a split's partials.
+      auto quad = [&](int u, int& i, unsigned& off) {
+        const int m = u / (4 * R), rr = 4 * (u % (4 * R)), r = rr >> 4, rn = rr & 15;
+        if (X16 && m == 16) {
+          i = NEL + r * 16 + rn;
+        } else {
+          const int tt = m >> 4, mm = m & 15;
+          i = ((r * T + tt) * 4 + (mm & 3)) * 64 + 16 * (mm >> 2) + rn;
+        }
+        off = (unsigned(m) * unsigned(p.Npad) + unsigned(tile0 * 16 + rr)) * 4u;
+      };
+      constexpr int SC1 = 16;  // cache policy: agent-coherent (sc1)
+      for (int u = threadIdx.x; u < p.M * 4 * R; u += 64 * KW) {
+        int i;
+        unsigned off;
+        quad(u, i, off);
+        const f32x4 v = f32x4{red[i], red[i + 1], red[i + 2], red[i + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp, off, unsigned(me) * sstride * 4u,
+                                               SC1);
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // every partial store of this thread has completed
+      __syncthreads();
+      __shared__ unsigned arrived;
+      if (threadIdx.x == 0) {
+        arrived = __hip_atomic_fetch_add(p.ctr + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (arrived == unsigned(nsp - 1))
+          __hip_atomic_store(p.ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (arrived != unsigned(nsp - 1)) return;  // workgroup-uniform
+      // The sums, in split order, into wave 0's partial slots (each thread reads back only slots it owns).
+      for (int u = threadIdx.x; u < p.M * 4 * R; u += 64 * KW) {
+        int i;
+        unsigned off;
+        quad(u, i, off);
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < nsp; ++sp) {
+          const f32x4 x = sp == me ? f32x4{red[i], red[i + 1], red[i + 2], red[i + 3]}
+                                   : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                   rp, off, unsigned(sp) * sstride * 4u, SC1));
+          v += x;
+        }
+        red[i] = v[0];
+        red[i + 1] = v[1];
+        red[i + 2] = v[2];
+        red[i + 3] = v[3];
+      }
+      __syncthreads();
+    }
     QSTAMP(26);
     qmm_epilogue<R, MODE>(p, tile0, val, rsc, ssu, 64 * KW, blockIdx.x, &hpf);
   }
@@ -615,7 +674,8 @@ static bool qmm_dispatch_mode(const TimedLaunch& tl, QmmShape sh, dim3 grid, hip
   // K = 4096 (32 K-blocks); K = 14336 (112); K = 2048 (16); K = 2880 (23, ragged); and the one-wave fallback.
   IH_QMM_CASE(1, 16, 2) IH_QMM_CASE(2, 16, 2) IH_QMM_CASE(2, 8, 4) IH_QMM_CASE(4, 8, 4) IH_QMM_CASE(4, 4, 8)
   IH_QMM_CASE(7, 4, 8) IH_QMM_CASE(1, 14, 8) IH_QMM_CASE(1, 8, 14) IH_QMM_CASE(4, 4, 2) IH_QMM_CASE(2, 8, 2)
-  IH_QMM_CASE(4, 8, 2) IH_QMM_CASE(2, 8, 3) IH_QMM_CASE(4, 8, 3) IH_QMM_CASE(1, 1, 1) IH_QMM_CASE(2, 1, 1) IH_QMM_CASE(4, 1, 1) IH_QMM_CASE(7, 1, 1)
+  IH_QMM_CASE(4, 8, 2) IH_QMM_CASE(2, 8, 3) IH_QMM_CASE(4, 8, 3) IH_QMM_CASE(2, 14, 4) IH_QMM_CASE(4, 7, 4)
+  IH_QMM_CASE(4, 14, 2) IH_QMM_CASE(3, 8, 2) IH_QMM_CASE(6, 4, 2) IH_QMM_CASE(2, 7, 8) IH_QMM_CASE(1, 1, 1) IH_QMM_CASE(2, 1, 1) IH_QMM_CASE(4, 1, 1) IH_QMM_CASE(7, 1, 1)
 #undef IH_QMM_CASE
   return false;  // not an instantiated shape
 }
@@ -662,6 +722,14 @@ int qmm_grid(const ih_qmat* W) {
 
 // Split-K partial sums: grown on demand, the stream drained before an old buffer is freed.
 static int ensure_qpart(ih_ctx* c, size_t bytes) {
+  if (!c->qctr) {
+    // Arrival counters of the in-kernel split-K reduction: zeroed once; the last workgroup of a row group resets its
+    // counter, so they are zero between launches.
+    ++c->gen;
+    if (hipMalloc(&c->qctr, QCTR_CAP * sizeof(unsigned)) != hipSuccess)
+      return fail(IH_ENOMEM, "qmm: split-K counter allocation failed");
+    IH_TRY(fill(c, c->qctr, 0, QCTR_CAP * sizeof(unsigned)));
+  }
   if (c->qpart_bytes >= bytes) return IH_OK;
   ++c->gen;
   IH_HIP(hipStreamSynchronize(c->stream));
@@ -693,9 +761,10 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   }
   IH_CHECK(qmm_shape_ok(sh, W->Npad, W->nkb), IH_EINVAL, "qmm: launch shape does not tile the matrix");
   const int ks = sh.ks;
-  // The kernel runs the epilogue itself when it sees the whole K range and the mode is one of the step's fused
-  // epilogues; otherwise it writes partial sums and qmm_finish_kernel adds them and applies the mode.
-  const bool finish = ks > 1 || !(ep.mode == QM_F32_SCALE || ep.mode == QM_RESID_ACT || ep.mode == QM_GLU_ACT);
+  // The kernel runs the step's fused epilogues itself (with K split over workgroups, in the last workgroup of each
+  // row group to arrive); the kernel-level modes write partial sums that qmm_finish_kernel adds and applies.
+  const bool fused = ep.mode == QM_F32_SCALE || ep.mode == QM_RESID_ACT || ep.mode == QM_GLU_ACT;
+  const bool finish = !fused;
   const int kmode = finish ? int(QM_PART) : ep.mode;
   QmmParams p{};
   const size_t tiles_per_e = size_t(W->Npad / 16) * W->nkb;
@@ -745,9 +814,13 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
     p.glu = ep.glu;
     p.limit = ep.limit;
   }
-  if (finish) {
+  if (finish || ks > 1) {
     IH_TRY(ensure_qpart(c, size_t(ks) * MAX_TOK * W->Npad * sizeof(float)));
     p.part = c->qpart;
+  }
+  if (!finish && ks > 1) {
+    IH_CHECK(grid_x <= QCTR_CAP, IH_EINVAL, "qmm: too many row groups for the split-K counters");
+    p.ctr = c->qctr;
   }
   // Algorithmic bytes: the matrix in its MLX format, x (bf16) read, y written (read too when accumulating).
   const double ybytes = double(M) * W->N *

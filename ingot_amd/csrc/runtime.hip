@@ -145,6 +145,7 @@ int ih_ctx_free(ih_ctx* c) {
   for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
   if (c->part) (void)hipFree(c->part);
   if (c->qpart) (void)hipFree(c->qpart);
+  if (c->qctr) (void)hipFree(c->qctr);
   if (c->samp) (void)hipFree(c->samp);
   free_act(c->act);
   (void)hipStreamDestroy(c->stream);

@@ -272,3 +272,34 @@ def test_recorded_step_replays_match_the_eager_step(shape):
     kv.free()
     m.free()
     ctx.close()
+
+
+def test_split_k_epilogues_match_the_whole_k_step(monkeypatch):
+    """K split over workgroups with the step's fused epilogues (RMSNorm-scaled projection, residual + next RMSNorm
+    input, gated activation): each workgroup writes its partial sums with agent-coherent stores and the last of a row
+    group to arrive adds them in split order and runs the epilogue. Forcing split shapes on every matrix of a model
+    must reproduce the whole-K step up to the changed summation order, and the split step must be deterministic."""
+    ctx = Context(0)
+    toks = (np.arange(17, dtype=np.uint32) * 29 + 3) % GQA4["vocab"]
+    d, m, kv = make(ctx, GQA4, P=200)
+    top_ref, log_ref = kv.verify(toks, want_logits=True)
+    kv.free()
+    m.free()
+    # qkv 1536×512, o 512×1024, gate|up 512×512, down 512×256: one-wave workgroups, one K-block each.
+    monkeypatch.setenv("IH_QMM_SHAPES", "1536:512=4,1,1;512:1024=2,1,1;512:512=2,1,1;512:256=2,1,1")
+    runs = []
+    for _ in range(2):
+        d, m, kv = make(ctx, GQA4, P=200)
+        runs.append(kv.verify(toks, want_logits=True))
+        kv.free()
+        m.free()
+    monkeypatch.delenv("IH_QMM_SHAPES")
+    (top, logits), (top2, logits2) = runs
+    assert np.array_equal(logits, logits2) and np.array_equal(top, top2), "split-K step is not deterministic"
+    err, cos = logits_close(logits, log_ref)
+    scale = float(np.abs(log_ref).max())
+    assert err <= 2e-3 * scale and cos >= 0.99999, (err, cos, scale)
+    srt = np.sort(log_ref, axis=1)
+    sure = (srt[:, -1] - srt[:, -2]) > 2 * err
+    assert np.array_equal(top[sure], top_ref[sure])
+    ctx.close()
