@@ -184,6 +184,11 @@ struct PieceRegs {
 // piece q is converted), each piece converted int8 → fp16 into one of two LDS buffers (K key-major, V transposed) and
 // multiplied while the later pieces are on their way; one barrier per piece (the buffer written for piece q + 2 was
 // last read for piece q, before the barrier of piece q + 1). Each wave runs its 16-query tiles over the piece with an online softmax in base 2.
+#ifdef IH_QMM_STAMP
+#define ASTAMP(i) do { astamp[wave][i] = unsigned(__builtin_amdgcn_s_memrealtime()); } while (0)
+#else
+#define ASTAMP(i) do { } while (0)
+#endif
 template <int HD, int TPW, bool RING, int NP>
 __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   constexpr int NC = HD / 32;    // 32-dim chunks (MFMA K steps of Sᵀ)
@@ -203,6 +208,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   const int sidx = blockIdx.x, split = sidx + ap.s0, kvh = blockIdx.y;
   if (sidx >= ap.nsplit) return;  // launched for a later position than the step's (chained rounds): no keys
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
+#ifdef IH_QMM_STAMP
+  __shared__ unsigned astamp[8][32];
+#endif
+  ASTAMP(0);
   const int Q = a.G * a.B;
   // Keys [k0, k1) of the split. In a sliding-window layer every row's window starts at or after P − window + 1, so
   // the split starts there (rounded down to 64 keys, which keeps pieces and the 32-slot V blocks aligned): the keys
@@ -483,8 +492,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
         load_piece(pr[1], min(q + 3, npieces - 1));
       }
       __syncthreads();
+      if (q < 16) ASTAMP(2 + q);
       piece_products(b0, kb0, min(PIECE, k1 - kb0));
       if (two) piece_products(b0 + 1, kb1, min(PIECE, k1 - kb1));
+      if (q < 16) ASTAMP(3 + q);
     }
   } else {
     for (int base = 0; base < npieces; base += NP) {
@@ -548,6 +559,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     if (!helper) lsum[0] = l;
   }
 
+  ASTAMP(20);
+#ifdef IH_QMM_STAMP
+  if (a.stamp && lane < 32)
+    a.stamp[((size_t(kvh) * gridDim.x + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
+#endif
   // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
@@ -682,7 +698,18 @@ static bool launch_attn_np(const TimedLaunch& tl, dim3 grid, hipStream_t st, con
   }
 }
 
-int launch_attention(ih_ctx* c, const AttnArgs& a) {
+#ifdef IH_QMM_STAMP
+static unsigned long long* g_astamp = nullptr;
+extern "C" int ih_dbg_attn_stamp(void* dev) {
+  g_astamp = static_cast<unsigned long long*>(dev);
+  return 0;
+}
+#endif
+int launch_attention(ih_ctx* c, const AttnArgs& a0) {
+  AttnArgs a = a0;
+#ifdef IH_QMM_STAMP
+  a.stamp = g_astamp;
+#endif
   const int Q = a.G * a.B;
   const int qtiles = (Q + 15) / 16;
   IH_CHECK(qtiles <= 16, IH_EINVAL, "attention: at most 256 query rows per KV head");

@@ -671,11 +671,12 @@ static bool qmm_dispatch_mode(const TimedLaunch& tl, QmmShape sh, dim3 grid, hip
       return true;                                                                                          \
     }                                                                                                       \
   }
-  // K = 4096 (32 K-blocks); K = 14336 (112); K = 2048 (16); K = 2880 (23, ragged); and the one-wave fallback.
+  // K = 4096 (32 K-blocks); K = 14336 (112; (4,7,4) and (2,7,8) split it over 4 and 2 workgroups); K = 2048 (16);
+  // K = 2880 (23, ragged); and the one-wave fallback.
   IH_QMM_CASE(1, 16, 2) IH_QMM_CASE(2, 16, 2) IH_QMM_CASE(2, 8, 4) IH_QMM_CASE(4, 8, 4) IH_QMM_CASE(4, 4, 8)
   IH_QMM_CASE(7, 4, 8) IH_QMM_CASE(1, 14, 8) IH_QMM_CASE(1, 8, 14) IH_QMM_CASE(4, 4, 2) IH_QMM_CASE(2, 8, 2)
-  IH_QMM_CASE(4, 8, 2) IH_QMM_CASE(2, 8, 3) IH_QMM_CASE(4, 8, 3) IH_QMM_CASE(2, 14, 4) IH_QMM_CASE(4, 7, 4)
-  IH_QMM_CASE(4, 14, 2) IH_QMM_CASE(3, 8, 2) IH_QMM_CASE(6, 4, 2) IH_QMM_CASE(2, 7, 8) IH_QMM_CASE(1, 1, 1) IH_QMM_CASE(2, 1, 1) IH_QMM_CASE(4, 1, 1) IH_QMM_CASE(7, 1, 1)
+  IH_QMM_CASE(4, 8, 2) IH_QMM_CASE(2, 8, 3) IH_QMM_CASE(4, 8, 3) IH_QMM_CASE(4, 7, 4) IH_QMM_CASE(2, 7, 8)
+  IH_QMM_CASE(1, 1, 1) IH_QMM_CASE(2, 1, 1) IH_QMM_CASE(4, 1, 1) IH_QMM_CASE(7, 1, 1)
 #undef IH_QMM_CASE
   return false;  // not an instantiated shape
 }
