@@ -235,9 +235,12 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, int tile0, V va
 #else
 #define QSTAMP(i) do { } while (0)
 #endif
-template <int T, int R, int KW, bool X16, int D, int KPW, int MODE>
+// KPW1 > 0: the second half of the waves (the second wave of each SIMD at KW = 8) take KPW1 K-blocks each instead of
+// KPW. A CU's loads come back roughly in issue order, so those waves receive their first stage after the first half's
+// first two stages; with fewer K-blocks they still end with the first half.
+template <int T, int R, int KW, bool X16, int D, int KPW, int MODE, int KPW1 = 0>
 __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
-  static_assert(KPW % D == 0, "the ring depth divides the K-blocks of a wave");
+  static_assert(KPW % D == 0 && KPW1 % D == 0, "the ring depth divides the K-blocks of a wave");
   // The wave index is uniform: readfirstlane keeps it (and everything derived from it) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, qd = lane >> 4;
@@ -246,13 +249,15 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
 #endif
   QSTAMP(0);
   const int tile0 = blockIdx.x * R;
-  constexpr int nk = KPW;                                // K-blocks of every wave
-  const int kwg = int(blockIdx.y) * KW * nk;             // first K-block of the workgroup
-  const int kb0 = kwg + wave * nk;                       // first K-block of this wave
+  constexpr int nk = KPW;                                // K-blocks of a wave of the first half (the LDS stride)
+  constexpr int HALF = KW / 2;
+  const int nkr = (KPW1 == 0 || wave < HALF) ? KPW : KPW1;  // K-blocks of this wave
+  const int kwg = int(blockIdx.y) * (KPW1 ? HALF * (KPW + KPW1) : KW * nk);  // first K-block of the workgroup
+  const int kb0 = kwg + (KPW1 == 0 ? wave * nk : wave < HALF ? wave * KPW : HALF * KPW + (wave - HALF) * KPW1);
   const unsigned tiles_total = unsigned(p.Npad / 16) * unsigned(p.nkb);
 #ifdef IH_QMM_STAMP
   // Instrumented build: with p.noload the weight and x loads read nothing (compute and launch cost alone).
-  const unsigned wlim = p.noload ? 0u : tiles_total * 1024u, xlim = p.noload ? 0u : unsigned(MAX_TOK) * p.nkb * 256u;
+  const unsigned wlim = (p.noload & 1) ? 0u : tiles_total * 1024u, xlim = (p.noload & 2) ? 0u : unsigned(MAX_TOK) * p.nkb * 256u;
 #else
   const unsigned wlim = tiles_total * 1024u, xlim = unsigned(MAX_TOK) * p.nkb * 256u;
 #endif
@@ -260,46 +265,13 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
                                rx = make_rsrc(p.xa, xlim);
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
 
-  // Epilogue inputs that another kernel just wrote, requested first (consumed after the main loop). Rows per wave of
-  // the RMSNorm prefetch: M ≤ 16 (T = 1), 17 (X16) or 32 (T = 2); more than eight (one-wave workgroups) are read after
-  // the loop instead.
+  // Epilogue inputs that another kernel just wrote, requested ahead of the weight stages (consumed after the main loop).
+  // Rows per wave of the RMSNorm prefetch: M ≤ 16 (T = 1), 17 (X16) or 32 (T = 2); more than eight (one-wave
+  // workgroups) are read after the loop instead.
   constexpr int NR = ((T == 2 ? 32 : X16 ? 17 : 16) + KW - 1) / KW;
   constexpr bool RMS = MODE == QM_F32_SCALE || MODE == QM_GLU_ACT, RMS_PRE = RMS && NR <= 8;
   RmsPrefetch<RMS_PRE ? NR : 1> rpf;
   ResidPrefetch hpf;
-  if constexpr (RMS_PRE)
-    if (p.ss_in) rms_prefetch(rpf, p.ss_in, SS_CAP, p.M, wave, KW, lane);
-  if constexpr (MODE == QM_RESID_ACT) resid_prefetch<R>(hpf, p, tile0);
-
-  // Wave-private staging in LDS: the scale/bias words of the R tiles over this wave's K-blocks ([r][i][row] 8 bytes)
-  // and token 16 of those K-blocks as [i][t][row ∈ {token 16, zeros}][qd] 16 bytes, so that lane (n, qd) reads
-  // row n ≠ 0 ? zeros : token 16 from an address that depends on the K-block only through an immediate. The loads go
-  // out first and only they are waited for before the LDS writes; no barrier: one wave's LDS operations complete in
-  // order and no other wave reads the region (a workgroup barrier here made every wave wait for the slowest wave's
-  // staging, queued behind all of the workgroup's first weight stages).
-  __shared__ u32x4 ssb[KW][R * nk * 8];
-  __shared__ u32x4 s16[KW][X16 ? nk * 32 : 1];
-  __shared__ float rsc[MAX_TOK];
-  constexpr int nsb = R * nk * 8;
-  constexpr int NSB = (nsb + 63) / 64, N16 = X16 ? (nk * 16 + 63) / 64 : 1;
-  u32x4 vsb[NSB], v16[N16];
-#pragma unroll
-  for (int j = 0; j < NSB; ++j) {
-    const int e = j * 64 + lane, r = e / (nk * 8), i = (e >> 3) % nk;
-    const unsigned off = (unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kb0 + i)) * 128u + unsigned(e & 7) * 16u;
-    const bool in = e < nsb && kb0 + i < p.nkb;  // K-blocks past the matrix: zero scale and bias, no contribution
-    vsb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, in ? off : OOB, 0, 0));
-  }
-  if constexpr (X16) {
-#pragma unroll
-    for (int j = 0; j < N16; ++j) {
-      const int e = j * 64 + lane, i = e >> 4, t = (e >> 2) & 3, q = e & 3;
-      const unsigned off = unsigned(kb0 + i) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * q;
-      v16[j] = __builtin_bit_cast(u32x4,
-                                  __builtin_amdgcn_raw_buffer_load_b128(rx, i < nk && kb0 + i < p.nkb ? off : OOB, 0, 0));
-    }
-  }
-
   unsigned xoff[T];
 #pragma unroll
   for (int tt = 0; tt < T; ++tt)
@@ -323,8 +295,50 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
                                                rw, woff, ((tile0 + r) * p.nkb + kb) * 1024, 0));
     __builtin_amdgcn_sched_barrier(0);
   };
+  // With the asymmetric split (two waves per SIMD), every wave's first stage goes out before anything else of the
+  // workgroup: a CU's loads come back roughly in issue order at its share of the bandwidth, and the second half's
+  // first stages would otherwise queue behind the first half's staging loads and second stages. The barrier orders
+  // only the issue. (With one wave per SIMD the staging loads go first: they are small and the first products wait
+  // for them.)
+  if constexpr (KPW1 > 0) {
+    load_stage(0, kb0);
+    __syncthreads();
+  }
+  if constexpr (RMS_PRE)
+    if (p.ss_in) rms_prefetch(rpf, p.ss_in, SS_CAP, p.M, wave, KW, lane);
+  if constexpr (MODE == QM_RESID_ACT) resid_prefetch<R>(hpf, p, tile0);
+
+  // Wave-private staging in LDS: the scale/bias words of the R tiles over this wave's K-blocks ([r][i][row] 8 bytes)
+  // and token 16 of those K-blocks as [i][t][row ∈ {token 16, zeros}][qd] 16 bytes, so that lane (n, qd) reads
+  // row n ≠ 0 ? zeros : token 16 from an address that depends on the K-block only through an immediate. The loads go
+  // out first and only they are waited for before the LDS writes; no barrier: one wave's LDS operations complete in
+  // order and no other wave reads the region (a workgroup barrier here made every wave wait for the slowest wave's
+  // staging, queued behind all of the workgroup's first weight stages).
+  __shared__ u32x4 ssb[KW][R * nk * 8];
+  __shared__ u32x4 s16[KW][X16 ? nk * 32 : 1];
+  __shared__ float rsc[MAX_TOK];
+  constexpr int nsb = R * nk * 8;
+  constexpr int NSB = (nsb + 63) / 64, N16 = X16 ? (nk * 16 + 63) / 64 : 1;
+  u32x4 vsb[NSB], v16[N16];
 #pragma unroll
-  for (int d = 0; d < D; ++d) load_stage(d, kb0 + d);
+  for (int j = 0; j < NSB; ++j) {
+    const int e = j * 64 + lane, r = e / (nk * 8), i = (e >> 3) % nk;
+    const unsigned off = (unsigned(tile0 + r) * unsigned(p.nkb) + unsigned(kb0 + i)) * 128u + unsigned(e & 7) * 16u;
+    const bool in = e < nsb && i < nkr && kb0 + i < p.nkb;  // K-blocks past the matrix: zero scale and bias
+    vsb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, in ? off : OOB, 0, 0));
+  }
+  if constexpr (X16) {
+#pragma unroll
+    for (int j = 0; j < N16; ++j) {
+      const int e = j * 64 + lane, i = e >> 4, t = (e >> 2) & 3, q = e & 3;
+      const unsigned off = unsigned(kb0 + i) * unsigned(MAX_TOK / 16) * 4096u + 4096u + 1024u * t + 16u * q;
+      v16[j] = __builtin_bit_cast(u32x4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(rx, i < nkr && kb0 + i < p.nkb ? off : OOB, 0, 0));
+    }
+  }
+
+#pragma unroll
+  for (int d = KPW1 > 0 ? 1 : 0; d < D; ++d) load_stage(d, kb0 + d);
 
   // The RMSNorm factors of the input rows, while the first stages are on their way: their partials were requested
   // first, so waiting for them does not wait for the weights, and no accumulator is live yet.
@@ -436,7 +450,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   // entry).
   int i = 0;
 #pragma unroll 1
-  for (; i < nk - D; i += D) {
+  for (; i < nkr - D; i += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       compute(d, i + d);
@@ -603,10 +617,10 @@ __global__ __launch_bounds__(256) void qmm_finish_kernel(QmmParams p) {
 // summation order is fixed. The K range tiles exactly (ks·KW·kpw = nkb, kpw a multiple of D), or, in one split, the
 // last wave runs past the end by less than its kpw: its K-blocks past the matrix re-stream the last block (clamped,
 // so every load stays inside the matrix) with zero scale and bias words, which add exactly nothing.
-struct QmmShape { int R, KW, D, kpw, ks; };
+struct QmmShape { int R, KW, D, kpw, ks, kpw1 = 0; };
 constexpr int qmm_ring_depth(int kpw) { return kpw % 2 == 0 ? 2 : kpw <= 3 ? kpw : 1; }
 static bool qmm_shape_ok(const QmmShape& sh, int Npad, int nkb) {
-  const int span = sh.KW * sh.kpw;
+  const int span = sh.kpw1 ? sh.KW / 2 * (sh.kpw + sh.kpw1) : sh.KW * sh.kpw;
   return sh.R >= 1 && sh.KW >= 1 && sh.D >= 1 && sh.kpw >= sh.D && sh.kpw % sh.D == 0 && sh.kpw <= 32 &&
          sh.R * sh.kpw <= 64 && (Npad / 16) % sh.R == 0 &&
          (sh.ks * span == nkb || (sh.ks == 1 && span > nkb && span - nkb < sh.kpw));
@@ -615,7 +629,16 @@ static bool qmm_shape_ok(const QmmShape& sh, int Npad, int nkb) {
 static constexpr int kQmmShapes[][3] = {{1, 16, 2}, {2, 16, 2}, {2, 8, 4}, {4, 4, 8}, {4, 8, 4}, {7, 4, 8},
                                         {1, 8, 14}, {1, 14, 8}, {4, 4, 2}, {2, 8, 2}, {4, 8, 2}, {1, 1, 1},
                                         {2, 1, 1},  {4, 1, 1},  {7, 1, 1},  {2, 8, 3},  {4, 8, 3}};
+static QmmShape qmm_shape_sym(int Npad, int nkb);
+// The symmetric choice below, except that seven-tile workgroups over 32 K-blocks (gate|up at K = 4096) run at two
+// waves per SIMD with the asymmetric split (7,8,6,2): the loop's VALU work issues ~2× faster per SIMD with two waves,
+// and the second wave of each SIMD, whose first stage arrives ~3 µs later, takes a third of the K-blocks of the first.
 static QmmShape qmm_shape(int Npad, int nkb) {
+  const QmmShape sh = qmm_shape_sym(Npad, nkb);
+  if (sh.R == 7 && sh.KW == 4 && sh.kpw == 8 && sh.ks == 1) return QmmShape{7, 8, 2, 6, 1, 2};
+  return sh;
+}
+static QmmShape qmm_shape_sym(int Npad, int nkb) {
   const int NT = Npad / 16;
   // Rows: R tiles per wave share x, and the workgroup count NT / R should be about one round over the 256 CUs (a
   // partial second round doubles the time of the CUs that run it): 7 for gate|up (1792 tiles → 256 workgroups), 4
@@ -665,7 +688,7 @@ template <int T, bool X16, int MODE>
 static bool qmm_dispatch_mode(const TimedLaunch& tl, QmmShape sh, dim3 grid, hipStream_t st, const QmmParams& p) {
 #define IH_QMM_CASE(R_, KW_, KPW_)                                                                          \
   if constexpr (qmm_fits<T, R_, KW_, X16, KPW_>()) {                                                        \
-    if (sh.R == R_ && sh.KW == KW_ && sh.kpw == KPW_) {                                                     \
+    if (sh.R == R_ && sh.KW == KW_ && sh.kpw == KPW_ && sh.kpw1 == 0) {                                     \
       tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, qmm_ring_depth(KPW_), KPW_, MODE>, grid, dim3(64 * KW_), 0, \
               st, p);                                                                                       \
       return true;                                                                                          \
@@ -678,6 +701,16 @@ static bool qmm_dispatch_mode(const TimedLaunch& tl, QmmShape sh, dim3 grid, hip
   IH_QMM_CASE(4, 8, 2) IH_QMM_CASE(2, 8, 3) IH_QMM_CASE(4, 8, 3) IH_QMM_CASE(4, 7, 4) IH_QMM_CASE(2, 7, 8)
   IH_QMM_CASE(1, 1, 1) IH_QMM_CASE(2, 1, 1) IH_QMM_CASE(4, 1, 1) IH_QMM_CASE(7, 1, 1)
 #undef IH_QMM_CASE
+  // Asymmetric K split (KPW for the first half of the waves, KPW1 for the second): gate|up at two waves per SIMD.
+#define IH_QMM_CASE1(R_, KW_, KPW_, KPW1_)                                                                       \
+  if constexpr (qmm_fits<T, R_, KW_, X16, KPW_>()) {                                                        \
+    if (sh.R == R_ && sh.KW == KW_ && sh.kpw == KPW_ && sh.kpw1 == KPW1_) {                                \
+      tlaunch(tl, qmm_int4_kernel<T, R_, KW_, X16, 2, KPW_, MODE, KPW1_>, grid, dim3(64 * KW_), 0, st, p);   \
+      return true;                                                                                          \
+    }                                                                                                       \
+  }
+  IH_QMM_CASE1(7, 8, 6, 2) IH_QMM_CASE1(7, 8, 4, 4)
+#undef IH_QMM_CASE1
   return false;  // not an instantiated shape
 }
 
@@ -748,16 +781,21 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   IH_CHECK(a.nkb == W->nkb && !a.f16, IH_EINVAL, "qmm: activation K does not match the matrix");
   QmmShape sh = qmm_shape(W->Npad, W->nkb);
   // Tuning overrides: IH_QMM_SHAPE = "R,KW,kpw" for every matrix, IH_QMM_SHAPES = "N:K=R,KW,kpw;…" per matrix.
-  auto apply = [&](int R, int KW, int kpw) {
-    sh = QmmShape{R, KW, qmm_ring_depth(kpw), kpw, std::max(1, W->nkb / std::max(1, KW * kpw))};
+  auto apply = [&](int R, int KW, int kpw, int kpw1) {
+    const int span = kpw1 ? KW / 2 * (kpw + kpw1) : KW * kpw;
+    sh = QmmShape{R, KW, kpw1 ? 2 : qmm_ring_depth(kpw), kpw, std::max(1, W->nkb / std::max(1, span)), kpw1};
   };
-  int oR, oKW, okpw;
-  if (const char* ov = getenv("IH_QMM_SHAPE"))
-    if (sscanf(ov, "%d,%d,%d", &oR, &oKW, &okpw) == 3) apply(oR, oKW, okpw);
+  int oR, oKW, okpw, okpw1 = 0;
+  if (const char* ov = getenv("IH_QMM_SHAPE")) {
+    const int nf = sscanf(ov, "%d,%d,%d,%d", &oR, &oKW, &okpw, &okpw1);
+    if (nf >= 3) apply(oR, oKW, okpw, nf == 4 ? okpw1 : 0);
+  }
   if (const char* ov = getenv("IH_QMM_SHAPES")) {
     for (const char* q = ov; q && *q; q = strchr(q, ';') ? strchr(q, ';') + 1 : nullptr) {
       int n, k;
-      if (sscanf(q, "%d:%d=%d,%d,%d", &n, &k, &oR, &oKW, &okpw) == 5 && n == W->N && k == W->K) apply(oR, oKW, okpw);
+      okpw1 = 0;
+      const int nf = sscanf(q, "%d:%d=%d,%d,%d,%d", &n, &k, &oR, &oKW, &okpw, &okpw1);
+      if (nf >= 5 && n == W->N && k == W->K) apply(oR, oKW, okpw, nf == 6 ? okpw1 : 0);
     }
   }
   IH_CHECK(qmm_shape_ok(sh, W->Npad, W->nkb), IH_EINVAL, "qmm: launch shape does not tile the matrix");
@@ -784,7 +822,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   p.nsplit = ks;
 #ifdef IH_QMM_STAMP
   p.stamp = (W->N == g_stamp_n && W->K == g_stamp_k) ? g_stamp : nullptr;
-  p.noload = getenv("IH_QMM_NOLOAD") != nullptr;
+  p.noload = getenv("IH_QMM_NOLOAD") ? atoi(getenv("IH_QMM_NOLOAD")) : 0;  // 1: no weight loads, 2: no x loads
 #endif
   if (ep.mode == QM_F32_SCALE || ep.mode == QM_GLU_ACT) {
     IH_CHECK(a.ss && a.nss > 0, IH_EINVAL, "qmm: the input activation carries no RMSNorm sums");
