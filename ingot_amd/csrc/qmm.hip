@@ -709,7 +709,7 @@ static bool qmm_dispatch_mode(const TimedLaunch& tl, QmmShape sh, dim3 grid, hip
       return true;                                                                                          \
     }                                                                                                       \
   }
-  IH_QMM_CASE1(7, 8, 6, 2) IH_QMM_CASE1(7, 8, 4, 4)
+  IH_QMM_CASE1(7, 8, 6, 2)
 #undef IH_QMM_CASE1
   return false;  // not an instantiated shape
 }
