@@ -561,8 +561,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 
   ASTAMP(20);
 #ifdef IH_QMM_STAMP
-  if (a.stamp && lane < 32)
-    a.stamp[((size_t(kvh) * gridDim.x + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
+  if (a.stamp && kvh < 8 && sidx < 64 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
+    a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
 #endif
   // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll

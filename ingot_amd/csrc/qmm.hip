@@ -581,7 +581,8 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   QSTAMP(27);
 #ifdef IH_QMM_STAMP
   if constexpr (T == 1)
-    if (p.stamp && lane < 32) p.stamp[(size_t(blockIdx.x) * 16 + wave) * 32 + lane] = qstamp_lds[wave][lane];
+    if (p.stamp && blockIdx.x < 256 && blockIdx.y == 0 && lane < 32)  // the stamp buffer holds 256 × 16 waves
+      p.stamp[(size_t(blockIdx.x) * 16 + wave) * 32 + lane] = qstamp_lds[wave][lane];
 #endif
 }
 
