@@ -9,13 +9,17 @@
 // (per token and head, symmetric). K holds H·k (orthonormal Walsh–Hadamard of the roped key) when hadk is set, and q is
 // rotated the same way, so (Hq)·(Hk) = q·k.
 //
-// MI355X design: one workgroup (8 waves) per (key split, KV head); the split size C is fixed per cache so that all
-// splits of all heads are one workgroup per CU. A split streams through LDS in pieces of 64 keys: every thread issues
-// the loads of all its pieces at entry, each piece is converted int8 → fp16 exactly into one of two LDS buffers (K
-// key-major, V transposed) as soon as it lands, and each wave runs its 16-query tiles over the piece: Sᵀ = K·Qᵀ (v_mfma_f32_16x16x32_f16, keys as rows so each lane holds 4 keys of one query), online softmax in
-// base 2 per query column, P stays in registers as the B operand of Oᵀ += Vᵀ·Pᵀ. A split writes O/l in fp16 with its
+// MI355X design: one workgroup (8 waves) per (key split, KV head, 80 query rows); the split size C is fixed per cache
+// so that all splits of all heads are one workgroup per CU. A split streams through LDS in pieces of 64 keys: every
+// thread issues the loads of its next pieces at entry, each piece is converted int8 → fp16 exactly into one of the LDS
+// buffers (K key-major, V transposed) as soon as it lands, and six waves multiply: the five 16-query tiles go in
+// groups {0, 1}, {2, 3}, {4}, and each group is run by two waves, one over the first and one over the second 32 keys
+// of every piece, so every K and V fragment read from LDS serves two tiles. Sᵀ = K·Qᵀ (v_mfma_f32_16x16x32_f16, keys
+// as rows so each lane holds 4 keys of one query), online softmax in base 2 per query column, P stays in registers as
+// the B operand of Oᵀ += Vᵀ·Pᵀ; the two halves' states are merged at the end. A split writes O/l in fp16 with its
 // (max, sum); the reduction merges the splits in a fixed order. A query's result does not depend on the other rows of
-// the block: blocks start at fixed key positions and the split boundaries are fixed multiples of C.
+// the block: blocks start at fixed key positions, the split boundaries are fixed multiples of C, and every row is
+// reduced in the same order whatever tile it falls in.
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
@@ -166,9 +170,9 @@ __device__ __forceinline__ float row_max4(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-constexpr int ATT_THREADS = 512;  // 8 waves: all load and convert, the first ceil(tiles / TPW) multiply
+constexpr int ATT_THREADS = 512;  // 8 waves: all load and convert, the first six multiply
 constexpr int PIECE = 64;         // keys per pipelined piece of a split
-constexpr int MAX_PIECES = 8;     // deepest ring of pieces in flight
+constexpr int MAX_PIECES = 2;     // deepest ring of pieces in flight (deeper rings spill the two tiles per wave)
 template <int HD> constexpr int krow() { return HD + 8; }
 constexpr int VROW = PIECE + 8;   // LDS row of Vᵀ in halves
 
@@ -179,7 +183,7 @@ struct PieceRegs {
   __half ks, vs;
 };
 
-// One workgroup per (split of C keys, KV head): every query row of the head's group (G·B ≤ 16·8·TPW) in one pass.
+// One workgroup per (split of C keys, KV head, 80 query rows of the head's group).
 // The split streams through LDS in pieces of 64 keys from a ring of NP pieces in registers (piece q + NP requested once
 // piece q is converted), each piece converted int8 → fp16 into one of two LDS buffers (K key-major, V transposed) and
 // multiplied while the later pieces are on their way; one barrier per piece (the buffer written for piece q + 2 was
@@ -189,7 +193,7 @@ struct PieceRegs {
 #else
 #define ASTAMP(i) do { } while (0)
 #endif
-template <int HD, int TPW, bool RING, int NP>
+template <int HD, bool RING, int NP>
 __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   constexpr int NC = HD / 32;    // 32-dim chunks (MFMA K steps of Sᵀ)
   constexpr int NDT = HD / 16;   // 16-dim tiles of Oᵀ
@@ -257,21 +261,22 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int p = 0; p < NP; ++p) load_piece(pr[p], min(p, npieces - 1));
 
-  // Query tiles of this wave: wave + 8·tt. With exactly 5 tiles (TPW = 1) the fifth is shared by waves 4-7, wave
-  // 4 + h taking the 16-key sub-tile h of every piece, so that no SIMD carries two tiles; their four (max, sum, O)
-  // states are merged at the end.
-  const bool sp5 = TPW == 1 && (Q + 15) / 16 == 5;  // workgroup-uniform
-  const bool helper = sp5 && wave >= 4;            // wave-uniform
-  const int hsub = wave - 4;
-  f16x8 qf[TPW][NC];
-  f32x4 o[TPW][NDT];
-  float mrun[TPW], lsum[TPW];
-  int lim[TPW], lo_key[TPW], tile_hi[TPW], tile_lo[TPW], tile_lo_lim[TPW], tile_hi_lo[TPW];
-  bool live[TPW];
+  // Query tiles: workgroup z holds the rows [80z, 80z + 80), five 16-row tiles in three groups {0, 1}, {2, 3}, {4};
+  // waves 2g and 2g + 1 (g < 2) and waves 4, 5 (g = 2) run group g over the first and second 32 keys of every piece,
+  // each with its own online-softmax state, and the two states are merged at the end. Every row, in every block and
+  // whatever its tile, is reduced in this same order — 32-key halves, one state per half, merged half 0 then half 1 —
+  // so a row's bits do not depend on the block. A wave reads each K and V fragment once for its group's two tiles.
+  const int grp = wave < 4 ? wave >> 1 : 2, half = wave & 1;
+  const bool active = wave < 6;  // wave-uniform
+  f16x8 qf[2][NC];
+  f32x4 o[2][NDT];
+  float mrun[2], lsum[2];
+  int lim[2], lo_key[2], tile_hi[2], tile_lo[2], tile_lo_lim[2], tile_hi_lo[2];
+  bool live[2];
 #pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) {
-    const int qt = helper ? 4 : wave + 8 * tt, m = 16 * qt + j;
-    live[tt] = 16 * qt < Q;
+  for (int tt = 0; tt < 2; ++tt) {
+    const int lt = 2 * grp + tt, qt = 5 * blockIdx.z + lt, m = 16 * qt + j;
+    live[tt] = active && lt < 5 && 16 * qt < Q;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       if (live[tt] && m < Q)
@@ -327,119 +332,71 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     }
   };
 
-  // The products of piece (buffer b) with keys kb …, nkeys of them staged (the rest are zero and masked).
-  // A helper wave's share of tile 4 in a piece: Sᵀ of its 16 keys (v_mfma_f32_16x16x32_f16), the online softmax on
-  // them, Oᵀ += Vᵀ·Pᵀ with v_mfma_f32_16x16x16_f16 (lane group qd holds keys 4qd … 4qd + 3 of the sub-tile, whose Vᵀ
-  // positions in the permuted 32-slot block are 8qd + 4·(h mod 2) …).
-  auto helper_products = [&](int b, int kb, int nkeys) {
-    if (kb > tile_hi[0] || kb + 63 < tile_lo[0]) return;
-    const int h = hsub;
-    if (16 * h >= nkeys) return;  // every key of the sub-tile is past the split (all masked)
-    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The products of this wave's half of a piece (buffer b, keys kb …, nkeys of them staged; the rest are zero and
+  // masked): keys kh0 = kb + 32·half … kh0 + 31. For each live tile of the group: Sᵀ of the two 16-key blocks
+  // (v_mfma_f32_16x16x32_f16, keys as rows: lane (j, qd) holds keys 16h + 4qd + r of query j), the online softmax in
+  // base 2 over the 32 keys, then Oᵀ += Vᵀ·Pᵀ with one v_mfma_f32_16x16x32_f16 per 16-dim tile (P in registers as
+  // the B operand; the transposed V block is permuted so that the lane's 8 keys are 8 consecutive halves).
+  auto piece_products = [&](int b, int kb, int nkeys) {
+    if (!active) return;
+    const int kh0 = kb + 32 * half, nh = nkeys - 32 * half;  // keys of the half and how many are staged
+    if (nh <= 0) return;                                    // uniform
+    bool go[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) go[tt] = live[tt] && kh0 <= tile_hi[tt] && kh0 + 31 >= tile_lo[tt];
+    if (!go[0] && !go[1]) return;
+    f32x4 sacc[2][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) sacc[tt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const f16x8 kf = *reinterpret_cast<const f16x8*>(&Kf[b][(16 * h + j) * KR + 32 * c + 8 * qd]);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][c], sacc, 0, 0, 0);
+      f16x8 kf[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        kf[h] = *reinterpret_cast<const f16x8*>(&Kf[b][(32 * half + 16 * h + j) * KR + 32 * c + 8 * qd]);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        if (go[tt]) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) sacc[tt][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h], qf[tt][c], sacc[tt][h], 0, 0, 0);
+        }
     }
-    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-    f16x4 vf[NDT];
+    // Vᵀ fragments of the half and the lane's key scales, read before the softmax so they have landed by the products.
+    f16x8 vf[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
-      vf[dt] = *reinterpret_cast<const f16x4*>(&Vt[b][(16 * dt + j) * VROW + 32 * (h >> 1) + 8 * qd + 4 * (h & 1)]);
-    const f32x4 ksv = *reinterpret_cast<const f32x4*>(&ksf[b][16 * h + 4 * qd]);
-    const f32x4 vsv = *reinterpret_cast<const f32x4*>(&vsf[b][16 * h + 4 * qd]);
-    float sv[4];
-    float mx = -INFINITY;
-    const bool full = nkeys == PIECE && kb + 63 <= tile_lo_lim[0] && kb >= tile_hi_lo[0];
+      vf[dt] = *reinterpret_cast<const f16x8*>(&Vt[b][(16 * dt + j) * VROW + 32 * half + 8 * qd]);
+    f32x4 ksv[2], vsv[2];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int kk = 16 * h + 4 * qd + r, key = kb + kk;
-      const bool vis = full || (kk < nkeys && key <= lim[0] && key >= lo_key[0]);
-      sv[r] = vis ? sacc[r] * ksv[r] : -INFINITY;
-      mx = fmaxf(mx, sv[r]);
-    }
-    mx = row_max4(mx);
-    const float mnew = fmaxf(mrun[0], mx);
-    const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[0] - mnew);
-    mrun[0] = mnew;
-    const float mref = mnew == -INFINITY ? 0.f : mnew;
-    float ps = 0.f;
-    f16x4 pb;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float pv = __builtin_amdgcn_exp2f(sv[r] - mref);
-      ps += pv;
-      pb[r] = (_Float16)(pv * vsv[r]);
-    }
-    lsum[0] = lsum[0] * alpha + ps;
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[0][dt] *= alpha;
+    for (int h = 0; h < 2; ++h) {
+      ksv[h] = *reinterpret_cast<const f32x4*>(&ksf[b][32 * half + 16 * h + 4 * qd]);
+      vsv[h] = *reinterpret_cast<const f32x4*>(&vsf[b][32 * half + 16 * h + 4 * qd]);
     }
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[dt], pb, o[0][dt], 0, 0, 0);
-  };
-
-  auto piece_products = [&](int b, int kb, int nkeys) {
-    if (helper) {
-      helper_products(b, kb, nkeys);
-      return;
-    }
-#pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-      if (!live[tt]) continue;  // uniform per wave
-      // Skip a piece no row of the tile can see (wave-uniform: past the last row's causal limit, or wholly before the
-      // first row's window).
-      if (kb > tile_hi[tt] || kb + 63 < tile_lo[tt]) continue;
-      const bool half2 = 32 < nkeys;  // the piece's second 32 keys are staged (uniform)
-      // The four Sᵀ tiles as interleaved independent MFMA chains, K fragments read one 32-dim step at a time.
-      f32x4 sacc[4];
-#pragma unroll
-      for (int h = 0; h < 4; ++h) sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        f16x8 kf[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h)
-          kf[h] = *reinterpret_cast<const f16x8*>(&Kf[b][(16 * h + j) * KR + 32 * c + 8 * qd]);
-#pragma unroll
-        for (int h = 0; h < 4; ++h) sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h], qf[tt][c], sacc[h], 0, 0, 0);
-      }
-      // Vᵀ fragments of the first 32 keys, read before the softmax so they have landed by the products (the second
-      // half's are read at its products, when it is staged).
-      auto vread = [&](int hs, int dt) {
-        return *reinterpret_cast<const f16x8*>(&Vt[b][(16 * dt + j) * VROW + (hs && half2 ? 32 : 0) + 8 * qd]);
-      };
-      f16x8 vf0[NDT];
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) vf0[dt] = vread(0, dt);
-      // This lane's keys 16h + 4qd + r: their scales as one 16-byte LDS read per tile.
-      f32x4 ksv[4], vsv[4];
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        ksv[h] = *reinterpret_cast<const f32x4*>(&ksf[b][16 * h + 4 * qd]);
-        vsv[h] = *reinterpret_cast<const f32x4*>(&vsf[b][16 * h + 4 * qd]);
-      }
-      float s[4][4];
+    for (int tt = 0; tt < 2; ++tt) {
+      if (!go[tt]) continue;  // uniform per wave
+      float s[2][4];
       float mx = -INFINITY;
-      // Every key of the piece visible to every row of the tile (the common case): no per-key mask.
-      const bool full = nkeys == PIECE && kb + 63 <= tile_lo_lim[tt] && kb >= tile_hi_lo[tt];
+      // Every key of the half visible to every row of the tile (the common case): no per-key mask.
+      const bool full = nh >= 32 && kh0 + 31 <= tile_lo_lim[tt] && kh0 >= tile_hi_lo[tt];
       if (full) {
 #pragma unroll
-        for (int h = 0; h < 4; ++h)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            s[h][r] = sacc[h][r] * ksv[h][r];
+            s[h][r] = sacc[tt][h][r] * ksv[h][r];
             mx = fmaxf(mx, s[h][r]);
           }
       } else {
 #pragma unroll
-        for (int h = 0; h < 4; ++h)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int kk = 16 * h + 4 * qd + r, key = kb + kk;
-            const bool vis = kk < nkeys && key <= lim[tt] && key >= lo_key[tt];
-            s[h][r] = vis ? sacc[h][r] * ksv[h][r] : -INFINITY;
+            const int kk = 16 * h + 4 * qd + r, key = kh0 + kk;
+            const bool vis = kk < nh && key <= lim[tt] && key >= lo_key[tt];
+            s[h][r] = vis ? sacc[tt][h][r] * ksv[h][r] : -INFINITY;
             mx = fmaxf(mx, s[h][r]);
           }
       }
@@ -451,15 +408,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       // against 0, not −inf: exp2(−inf − (−inf)) would be NaN.
       const float mref = mnew == -INFINITY ? 0.f : mnew;
       float ps = 0.f;
-      f16x8 pb[2];
+      f16x8 pb;
 #pragma unroll
-      for (int h = 0; h < 4; ++h)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           // v_exp_f32 directly: exp2(−inf) = 0, and no range reduction is needed for arguments ≤ 0.
           const float pv = __builtin_amdgcn_exp2f(s[h][r] - mref);
           ps += pv;
-          pb[h >> 1][4 * (h & 1) + r] = (_Float16)(pv * vsv[h][r]);
+          pb[4 * h + r] = (_Float16)(pv * vsv[h][r]);
         }
       lsum[tt] = lsum[tt] * alpha + ps;
       if (__any(alpha != 1.f)) {
@@ -467,13 +424,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
         for (int dt = 0; dt < NDT; ++dt) o[tt][dt] *= alpha;
       }
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-        o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf0[dt], pb[0], o[tt][dt], 0, 0, 0);
-      if (half2) {
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-          o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(1, dt), pb[1], o[tt][dt], 0, 0, 0);
-      }
+      for (int dt = 0; dt < NDT; ++dt) o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pb, o[tt][dt], 0, 0, 0);
     }
   };
 
@@ -512,76 +463,66 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     }
   }
 
-  // Tile 4's helper states merged into wave 4's (through the K staging buffer, free after the last piece): M = max
-  // of the maxima, L = Σ 2^(m_i − M)·l_i, O = Σ 2^(m_i − M)·O_i, in helper order.
-  if (sp5) {
-    float l = lsum[0];
+  // The row sums over the lane's keys summed over the query column's four lanes.
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    float l = lsum[tt];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    constexpr int HST = 16 * HD + 32;  // floats per helper state: O [dim][query], then (max, sum) per query
-    float* scr = reinterpret_cast<float*>(&Kf[0][0]);
-    static_assert(3 * HST * 4 <= sizeof(Kf), "the merge scratch fits the K staging buffers");
-    __syncthreads();  // every wave is past its last piece
-    if (helper && hsub > 0) {
-      float* st = scr + (hsub - 1) * HST;
+    lsum[tt] = l;
+  }
+  // The half-1 states merged into the half-0 states through the K and V staging buffers (free after the last piece):
+  // M = max(m0, m1), L = 2^(m0 − M)·l0 + 2^(m1 − M)·l1, O = 2^(m0 − M)·O0 + 2^(m1 − M)·O1.
+  constexpr int HST = 16 * HD + 32;  // floats per tile state: O [dim][query], then (max, sum) per query
+  auto scr = [&](int lt) {  // tiles 0-3 in the K buffers, tile 4 in the V buffers
+    return lt < 4 ? reinterpret_cast<float*>(&Kf[0][0]) + lt * HST : reinterpret_cast<float*>(&Vt[0][0]);
+  };
+  static_assert(4 * HST * 4 <= sizeof(Kf) && HST * 4 <= sizeof(Vt), "the merge scratch fits the staging buffers");
+  __syncthreads();  // every wave is past its last piece
+  if (half == 1) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      if (!live[tt]) continue;
+      float* st = scr(2 * grp + tt);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) st[(16 * dt + 4 * qd + r) * 16 + j] = o[0][dt][r];
+        for (int r = 0; r < 4; ++r) st[(16 * dt + 4 * qd + r) * 16 + j] = o[tt][dt][r];
       if (qd == 0) {
-        st[16 * HD + j] = mrun[0];
-        st[16 * HD + 16 + j] = l;
+        st[16 * HD + j] = mrun[tt];
+        st[16 * HD + 16 + j] = lsum[tt];
       }
     }
-    __syncthreads();
-    if (helper && hsub == 0) {
-      float M = mrun[0];
-#pragma unroll
-      for (int i = 0; i < 3; ++i) M = fmaxf(M, scr[i * HST + 16 * HD + j]);
-      const float w0 = mrun[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrun[0] - M);
-      float L = w0 * l;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[0][dt] *= w0;
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        const float mi = scr[i * HST + 16 * HD + j];
-        const float wi = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - M);
-        L += wi * scr[i * HST + 16 * HD + 16 + j];
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[0][dt][r] += wi * scr[i * HST + (16 * dt + 4 * qd + r) * 16 + j];
-      }
-      mrun[0] = M;
-      lsum[0] = L;  // already the row's total
-    }
-    if (helper && hsub > 0) return;
-    if (!helper) lsum[0] = l;
   }
-
+  __syncthreads();
   ASTAMP(20);
 #ifdef IH_QMM_STAMP
-  if (a.stamp && kvh < 8 && sidx < 64 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
+  if (a.stamp && kvh < 8 && sidx < 64 && blockIdx.z == 0 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
     a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
 #endif
+  if (half == 1) return;
   // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) {
+  for (int tt = 0; tt < 2; ++tt) {
     if (!live[tt]) continue;
-    float l = lsum[tt];
-    if (!sp5) {
-      l += __shfl_xor(l, 16);
-      l += __shfl_xor(l, 32);
-    }
-    const int m = 16 * ((helper ? 4 : wave) + 8 * tt) + j;
+    const float* st = scr(2 * grp + tt);
+    const float m1 = st[16 * HD + j], l1 = st[16 * HD + 16 + j];
+    const float M = fmaxf(mrun[tt], m1);
+    const float w0 = mrun[tt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrun[tt] - M);
+    const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
+    const float l = lsum[tt] * w0 + l1 * w1;
+    const int m = 16 * (5 * blockIdx.z + 2 * grp + tt) + j;
     if (m >= Q) continue;
     const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
-    if (qd == 0) a.ml[base + m] = make_float2(mrun[tt], l);
+    if (qd == 0) a.ml[base + m] = make_float2(M, l);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      __half2 p0 = __floats2half2_rn(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
-      __half2 p1 = __floats2half2_rn(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = (o[tt][dt][r] * w0 + st[(16 * dt + 4 * qd + r) * 16 + j] * w1) * inv;
+      __half2 p0 = __floats2half2_rn(v[0], v[1]);
+      __half2 p1 = __floats2half2_rn(v[2], v[3]);
       uint2 w;
       w.x = __builtin_bit_cast(unsigned, p0);
       w.y = __builtin_bit_cast(unsigned, p1);
@@ -687,12 +628,12 @@ int launch_prework(ih_ctx* c, const AttnArgs& a) {
   return IH_OK;
 }
 
-template <int HD, int TPW, bool RING>
+template <int HD, bool RING>
 static bool launch_attn_np(const TimedLaunch& tl, dim3 grid, hipStream_t st, const AttnArgs& a, int np) {
   switch (np) {
 #define IH_ATT_NP(N) \
-  case N: tlaunch(tl, attn_kernel<HD, TPW, RING, N>, grid, dim3(ATT_THREADS), 0, st, a); return true;
-    IH_ATT_NP(1) IH_ATT_NP(2) IH_ATT_NP(3) IH_ATT_NP(4) IH_ATT_NP(5) IH_ATT_NP(6) IH_ATT_NP(7) IH_ATT_NP(8)
+  case N: tlaunch(tl, attn_kernel<HD, RING, N>, grid, dim3(ATT_THREADS), 0, st, a); return true;
+    IH_ATT_NP(1) IH_ATT_NP(2)
 #undef IH_ATT_NP
     default: return false;
   }
@@ -719,22 +660,15 @@ int launch_attention(ih_ctx* c, const AttnArgs& a0) {
     return v ? std::max(1, std::min(MAX_PIECES, atoi(v))) : 2;
   }();
   const int np = std::min(ring_np, (a.C + PIECE - 1) / PIECE);
-  dim3 grid(a.nsplit, a.KVH);
+  dim3 grid(a.nsplit, a.KVH, (qtiles + 4) / 5);
   // Algorithmic bytes: the int8 K and V and their fp16 scales of every key the launched splits cover, and q.
   const double keys = double(a.P + a.B) - double(a.s0) * a.C;
   TimedLaunch tl(c, TC_ATTN, double(a.KVH) * keys * (2 * a.HD + 4) + double(a.KVH) * Q * a.HD * 2);
-  const bool two = qtiles > 8, ring = a.ring != 0;
-  const int npb = two ? std::min(np, 4) : np;  // two tiles per wave hold fewer pieces in registers
+  const bool ring = a.ring != 0;
   bool ok;
-  if (a.HD == 128) {
-    if (two) ok = ring ? launch_attn_np<128, 2, true>(tl, grid, c->stream, a, npb) : launch_attn_np<128, 2, false>(tl, grid, c->stream, a, npb);
-    else ok = ring ? launch_attn_np<128, 1, true>(tl, grid, c->stream, a, np) : launch_attn_np<128, 1, false>(tl, grid, c->stream, a, np);
-  } else if (a.HD == 64) {
-    if (two) ok = ring ? launch_attn_np<64, 2, true>(tl, grid, c->stream, a, npb) : launch_attn_np<64, 2, false>(tl, grid, c->stream, a, npb);
-    else ok = ring ? launch_attn_np<64, 1, true>(tl, grid, c->stream, a, np) : launch_attn_np<64, 1, false>(tl, grid, c->stream, a, np);
-  } else {
-    return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
-  }
+  if (a.HD == 128) ok = ring ? launch_attn_np<128, true>(tl, grid, c->stream, a, np) : launch_attn_np<128, false>(tl, grid, c->stream, a, np);
+  else if (a.HD == 64) ok = ring ? launch_attn_np<64, true>(tl, grid, c->stream, a, np) : launch_attn_np<64, false>(tl, grid, c->stream, a, np);
+  else return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
   IH_CHECK(ok, IH_EINVAL, "attention: unsupported key chunk");
   IH_HIP(hipGetLastError());
   return IH_OK;

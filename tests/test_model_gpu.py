@@ -179,6 +179,27 @@ def test_row_invariance_and_rollback(ctx):
         m.free()
 
 
+@pytest.mark.parametrize("shape", [SMALL, GQA4, SWA], ids=["small", "gqa4", "swa-gqa8"])
+def test_every_row_of_a_full_block_equals_its_row_decoded_alone(ctx, shape):
+    """Row r of a 17-row block is bit-identical to the same token verified alone (and as the first row of a shorter
+    block) once rows < r are in the cache: the speculative round's last row, which emits the bonus token, must give
+    the bits plain decoding gives at that position (KernelCaseTests.swift:66-86; verify_attn_pf.metal:41-45)."""
+    d, m, kv = make(ctx, shape)
+    try:
+        P = kv.pos
+        toks = np.random.default_rng(5).integers(0, d.vocab, size=17).astype(np.uint32)
+        _, full = kv.verify(toks, want_logits=True)
+        for r in (16, 15, 8, 1):
+            kv.set_pos(P + r)
+            _, alone = kv.verify(toks[r:r + 1], want_logits=True)
+            assert np.array_equal(alone[0].view(np.uint32), full[r].view(np.uint32)), r
+            _, tail = kv.verify(toks[r:], want_logits=True)
+            assert np.array_equal(tail.view(np.uint32), full[r:].view(np.uint32)), r
+    finally:
+        kv.free()
+        m.free()
+
+
 def test_commit_and_chained_rounds_match_plain_decode(ctx):
     """Speculative rounds give exactly the greedy tokens of plain one-token decoding (docs/adr/0002, 0005; gen
     --check): drafts that follow the greedy chain are all accepted, a wrong draft stops acceptance at its row."""
