@@ -264,6 +264,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, wlim), rsb = make_rsrc(p.s, tiles_total * 128u),
                                rx = make_rsrc(p.xa, xlim);
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
+  const unsigned shv[3] = {vgpr_of(4u), vgpr_of(8u), vgpr_of(12u)};  // 64-bit nibble shifts (nib_bf16_pair)
 
   // Epilogue inputs that another kernel just wrote, requested ahead of the weight stages (consumed after the main loop).
   // Rows per wave of the RMSNorm prefetch: M ≤ 16 (T = 1), 17 (X16) or 32 (T = 2); more than eight (one-wave
@@ -420,7 +421,8 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       const float c1 = fmaf(-128.f, s1, __uint_as_float(sb.y & 0xFFFF0000u));
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
-        const bf16x8 w0 = nib_bf16(wv[d][r][2 * g], km, kbias), w1 = nib_bf16(wv[d][r][2 * g + 1], km, kbias);
+        bf16x8 w0, w1;
+        nib_bf16_pair(wv[d][r][2 * g], wv[d][r][2 * g + 1], km, kbias, shv, w0, w1);
         const float sg = g ? s1 : s0, cg = g ? c1 : c0;
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) {

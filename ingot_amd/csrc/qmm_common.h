@@ -42,6 +42,27 @@ __device__ __forceinline__ bf16x8 nib_bf16(unsigned w, unsigned km, unsigned kb)
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// Two words of one group → their sixteen bf16 values (nib_bf16 of each): the three shifts of both words are three
+// 64-bit shifts of the pair (the low word's top bits, which the shifted pair fills from the high word, are masked
+// off), 11 instructions instead of 14. The shift amounts sh = {4, 8, 12} come in VGPRs (vgpr_of): with a constant
+// amount the compiler splits a 64-bit shift into two 32-bit instructions.
+__device__ __forceinline__ void nib_bf16_pair(unsigned wa, unsigned wb, unsigned km, unsigned kb, const unsigned (&sh)[3],
+                                              bf16x8& a, bf16x8& b) {
+  const uint64_t p = (uint64_t(wb) << 32) | wa;
+  const uint64_t s4 = p >> sh[0], s8 = p >> sh[1], s12 = p >> sh[2];
+  u32x4 va, vb;
+  va.x = and_or(wa, km, kb);
+  va.y = and_or(unsigned(s4), km, kb);
+  va.z = and_or(unsigned(s8), km, kb);
+  va.w = and_or(unsigned(s12), km, kb);
+  vb.x = and_or(wb, km, kb);
+  vb.y = and_or(unsigned(s4 >> 32), km, kb);
+  vb.z = and_or(unsigned(s8 >> 32), km, kb);
+  vb.w = and_or(unsigned(s12 >> 32), km, kb);
+  a = __builtin_bit_cast(bf16x8, va);
+  b = __builtin_bit_cast(bf16x8, vb);
+}
+
 // Buffer resources (base in SGPRs, 32-bit offsets; an offset past num_records reads as zero).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
