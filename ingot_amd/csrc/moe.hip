@@ -188,6 +188,7 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r][0] = acc[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
+  const unsigned shv[3] = {vgpr_of(4u), vgpr_of(8u), vgpr_of(12u)};  // 64-bit nibble shifts (nib_bf16_pair)
   auto compute = [&](const GStage<FMT, R>& st) {
     if constexpr (FMT == QF_INT4) {
       const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
@@ -210,7 +211,8 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
         const float c0 = fmaf(-128.f, s0, bf16f(st.s[r].x >> 16)), c1 = fmaf(-128.f, s1, bf16f(st.s[r].y >> 16));
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          const bf16x8 w0 = nib_bf16(st.w[r][2 * g], km, kbias), w1 = nib_bf16(st.w[r][2 * g + 1], km, kbias);
+          bf16x8 w0, w1;
+          nib_bf16_pair(st.w[r][2 * g], st.w[r][2 * g + 1], km, kbias, shv, w0, w1);
           const float sg = g ? s1 : s0, cg = g ? c1 : c0;
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) {
