@@ -193,7 +193,7 @@ struct PieceRegs {
 #else
 #define ASTAMP(i) do { } while (0)
 #endif
-template <int HD, bool RING, int NP>
+template <int HD, int TPW, bool RING, int NP>
 __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   constexpr int NC = HD / 32;    // 32-dim chunks (MFMA K steps of Sᵀ)
   constexpr int NDT = HD / 16;   // 16-dim tiles of Oᵀ
@@ -261,22 +261,26 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int p = 0; p < NP; ++p) load_piece(pr[p], min(p, npieces - 1));
 
-  // Query tiles: workgroup z holds the rows [80z, 80z + 80), five 16-row tiles in three groups {0, 1}, {2, 3}, {4};
-  // waves 2g and 2g + 1 (g < 2) and waves 4, 5 (g = 2) run group g over the first and second 32 keys of every piece,
-  // each with its own online-softmax state, and the two states are merged at the end. Every row, in every block and
-  // whatever its tile, is reduced in this same order — 32-key halves, one state per half, merged half 0 then half 1 —
-  // so a row's bits do not depend on the block. A wave reads each K and V fragment once for its group's two tiles.
-  const int grp = wave < 4 ? wave >> 1 : 2, half = wave & 1;
-  const bool active = wave < 6;  // wave-uniform
-  f16x8 qf[2][NC];
-  f32x4 o[2][NDT];
-  float mrun[2], lsum[2];
-  int lim[2], lo_key[2], tile_hi[2], tile_lo[2], tile_lo_lim[2], tile_hi_lo[2];
-  bool live[2];
+  // Query tiles. A row's bits must not depend on the block, so every row of a model is reduced in one order, chosen
+  // from the model's largest block (its padded row count Qpad):
+  //  * TPW = 0 (Qpad ≤ 80: up to five 16-row tiles, e.g. 4 q heads per KV head): the tiles go in groups {0, 1},
+  //    {2, 3}, {4}; waves 2g and 2g + 1 (g < 2) and waves 4, 5 (g = 2) run group g over the first and second 32 keys
+  //    of every piece, each with its own online-softmax state, and the two states are merged at the end (half 0 then
+  //    half 1). A wave reads each K and V fragment once for two tiles, and no SIMD carries more than 1.5 tiles.
+  //  * TPW = 1, 2 (larger groups): wave w runs tiles w and w + 8 over whole pieces with one state per row.
+  // Workgroup z holds the rows [80z, 80z + 80) with TPW = 0 (one z unless a model of that size ever sees more rows).
+  constexpr int NT = TPW == 0 ? 2 : TPW;
+  const int grp = wave < 4 ? wave >> 1 : 2, half = TPW == 0 ? wave & 1 : 0;
+  const bool active = TPW != 0 || wave < 6;  // wave-uniform
+  f16x8 qf[NT][NC];
+  f32x4 o[NT][NDT];
+  float mrun[NT], lsum[NT];
+  int lim[NT], lo_key[NT], tile_hi[NT], tile_lo[NT], tile_lo_lim[NT], tile_hi_lo[NT];
+  bool live[NT];
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int lt = 2 * grp + tt, qt = 5 * blockIdx.z + lt, m = 16 * qt + j;
-    live[tt] = active && lt < 5 && 16 * qt < Q;
+  for (int tt = 0; tt < NT; ++tt) {
+    const int lt = 2 * grp + tt, qt = TPW == 0 ? 5 * blockIdx.z + lt : wave + 8 * tt, m = 16 * qt + j;
+    live[tt] = active && (TPW != 0 || lt < 5) && 16 * qt < Q;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       if (live[tt] && m < Q)
@@ -337,17 +341,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   // (v_mfma_f32_16x16x32_f16, keys as rows: lane (j, qd) holds keys 16h + 4qd + r of query j), the online softmax in
   // base 2 over the 32 keys, then Oᵀ += Vᵀ·Pᵀ with one v_mfma_f32_16x16x32_f16 per 16-dim tile (P in registers as
   // the B operand; the transposed V block is permuted so that the lane's 8 keys are 8 consecutive halves).
-  auto piece_products = [&](int b, int kb, int nkeys) {
+  auto half_products = [&](auto b, int kb, int nkeys) {  // generic: instantiated where called
     if (!active) return;
     const int kh0 = kb + 32 * half, nh = nkeys - 32 * half;  // keys of the half and how many are staged
     if (nh <= 0) return;                                    // uniform
-    bool go[2];
+    bool go[NT];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) go[tt] = live[tt] && kh0 <= tile_hi[tt] && kh0 + 31 >= tile_lo[tt];
-    if (!go[0] && !go[1]) return;
-    f32x4 sacc[2][2];
+    for (int tt = 0; tt < NT; ++tt) go[tt] = live[tt] && kh0 <= tile_hi[tt] && kh0 + 31 >= tile_lo[tt];
+    if (!go[0] && !go[NT - 1]) return;
+    f32x4 sacc[NT][2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
       for (int h = 0; h < 2; ++h) sacc[tt][h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -357,7 +361,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       for (int h = 0; h < 2; ++h)
         kf[h] = *reinterpret_cast<const f16x8*>(&Kf[b][(32 * half + 16 * h + j) * KR + 32 * c + 8 * qd]);
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      for (int tt = 0; tt < NT; ++tt)
         if (go[tt]) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) sacc[tt][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h], qf[tt][c], sacc[tt][h], 0, 0, 0);
@@ -375,7 +379,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       vsv[h] = *reinterpret_cast<const f32x4*>(&vsf[b][32 * half + 16 * h + 4 * qd]);
     }
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < NT; ++tt) {
       if (!go[tt]) continue;  // uniform per wave
       float s[2][4];
       float mx = -INFINITY;
@@ -428,6 +432,107 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     }
   };
 
+  // TPW = 1, 2: the products of a whole piece for each tile of the wave — the four Sᵀ blocks, one online-softmax step
+  // over the 64 keys, Oᵀ += Vᵀ·Pᵀ over the two 32-key halves.
+  auto whole_products = [&](auto b, int kb, int nkeys) __attribute__((always_inline)) {  // generic: instantiated where called
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      if (!live[tt]) continue;  // uniform per wave
+      // Skip a piece no row of the tile can see (wave-uniform: past the last row's causal limit, or wholly before the
+      // first row's window).
+      if (kb > tile_hi[tt] || kb + 63 < tile_lo[tt]) continue;
+      const bool half2 = 32 < nkeys;  // the piece's second 32 keys are staged (uniform)
+      // The four Sᵀ tiles as interleaved independent MFMA chains, K fragments read one 32-dim step at a time.
+      f32x4 sacc[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        f16x8 kf[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          kf[h] = *reinterpret_cast<const f16x8*>(&Kf[b][(16 * h + j) * KR + 32 * c + 8 * qd]);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h], qf[tt][c], sacc[h], 0, 0, 0);
+      }
+      // Vᵀ fragments of the first 32 keys, read before the softmax so they have landed by the products (the second
+      // half's are read at its products, when it is staged).
+      auto vread = [&](int hs, int dt) {
+        return *reinterpret_cast<const f16x8*>(&Vt[b][(16 * dt + j) * VROW + (hs && half2 ? 32 : 0) + 8 * qd]);
+      };
+      f16x8 vf0[NDT];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) vf0[dt] = vread(0, dt);
+      // This lane's keys 16h + 4qd + r: their scales as one 16-byte LDS read per tile.
+      f32x4 ksv[4], vsv[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        ksv[h] = *reinterpret_cast<const f32x4*>(&ksf[b][16 * h + 4 * qd]);
+        vsv[h] = *reinterpret_cast<const f32x4*>(&vsf[b][16 * h + 4 * qd]);
+      }
+      float s[4][4];
+      float mx = -INFINITY;
+      // Every key of the piece visible to every row of the tile (the common case): no per-key mask.
+      const bool full = nkeys == PIECE && kb + 63 <= tile_lo_lim[tt] && kb >= tile_hi_lo[tt];
+      if (full) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            s[h][r] = sacc[h][r] * ksv[h][r];
+            mx = fmaxf(mx, s[h][r]);
+          }
+      } else {
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int kk = 16 * h + 4 * qd + r, key = kb + kk;
+            const bool vis = kk < nkeys && key <= lim[tt] && key >= lo_key[tt];
+            s[h][r] = vis ? sacc[h][r] * ksv[h][r] : -INFINITY;
+            mx = fmaxf(mx, s[h][r]);
+          }
+      }
+      mx = row_max4(mx);
+      const float mnew = fmaxf(mrun[tt], mx);
+      const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[tt] - mnew);
+      mrun[tt] = mnew;
+      // A row that has seen no key yet (every score −inf, e.g. a split wholly past its causal limit) takes exponents
+      // against 0, not −inf: exp2(−inf − (−inf)) would be NaN.
+      const float mref = mnew == -INFINITY ? 0.f : mnew;
+      float ps = 0.f;
+      f16x8 pb[2];
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          // v_exp_f32 directly: exp2(−inf) = 0, and no range reduction is needed for arguments ≤ 0.
+          const float pv = __builtin_amdgcn_exp2f(s[h][r] - mref);
+          ps += pv;
+          pb[h >> 1][4 * (h & 1) + r] = (_Float16)(pv * vsv[h][r]);
+        }
+      lsum[tt] = lsum[tt] * alpha + ps;
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[tt][dt] *= alpha;
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+        o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf0[dt], pb[0], o[tt][dt], 0, 0, 0);
+      if (half2) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+          o[tt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vread(1, dt), pb[1], o[tt][dt], 0, 0, 0);
+      }
+    }
+  };
+
+  // Inlined: as a call, the two-tile whole-piece variant kept its state in scratch memory.
+  auto piece_products = [&](int b, int kb, int nkeys) __attribute__((always_inline)) {
+    if constexpr (TPW == 0) half_products(b, kb, nkeys);
+    else whole_products(b, kb, nkeys);
+  };
+
   // Batches of NP pieces (one batch unless the split exceeds 64·NP keys). Pieces alternate between the two LDS
   // buffers; the barrier before a batch's loads keeps every wave's last reads of the batch before them.
   if constexpr (NP == 2) {
@@ -465,12 +570,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 
   // The row sums over the lane's keys summed over the query column's four lanes.
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
+  for (int tt = 0; tt < NT; ++tt) {
     float l = lsum[tt];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     lsum[tt] = l;
   }
+  if constexpr (TPW == 0) {
   // The half-1 states merged into the half-0 states through the K and V staging buffers (free after the last piece):
   // M = max(m0, m1), L = 2^(m0 − M)·l0 + 2^(m1 − M)·l1, O = 2^(m0 − M)·O0 + 2^(m1 − M)·O1.
   constexpr int HST = 16 * HD + 32;  // floats per tile state: O [dim][query], then (max, sum) per query
@@ -528,6 +634,33 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       w.y = __builtin_bit_cast(unsigned, p1);
       *reinterpret_cast<uint2*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = w;
     }
+  }
+  } else {
+  ASTAMP(20);
+#ifdef IH_QMM_STAMP
+  if (TPW != 0 && a.stamp && kvh < 8 && sidx < 64 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
+    a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
+#endif
+  // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    if (!live[tt]) continue;
+    const float l = lsum[tt];
+    const int m = 16 * (wave + 8 * tt) + j;
+    if (m >= Q) continue;
+    const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
+    if (qd == 0) a.ml[base + m] = make_float2(mrun[tt], l);
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      __half2 p0 = __floats2half2_rn(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
+      __half2 p1 = __floats2half2_rn(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
+      uint2 w;
+      w.x = __builtin_bit_cast(unsigned, p0);
+      w.y = __builtin_bit_cast(unsigned, p1);
+      *reinterpret_cast<uint2*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = w;
+    }
+  }
   }
 }
 
@@ -628,11 +761,11 @@ int launch_prework(ih_ctx* c, const AttnArgs& a) {
   return IH_OK;
 }
 
-template <int HD, bool RING>
+template <int HD, int TPW, bool RING>
 static bool launch_attn_np(const TimedLaunch& tl, dim3 grid, hipStream_t st, const AttnArgs& a, int np) {
   switch (np) {
 #define IH_ATT_NP(N) \
-  case N: tlaunch(tl, attn_kernel<HD, RING, N>, grid, dim3(ATT_THREADS), 0, st, a); return true;
+  case N: tlaunch(tl, attn_kernel<HD, TPW, RING, N>, grid, dim3(ATT_THREADS), 0, st, a); return true;
     IH_ATT_NP(1) IH_ATT_NP(2)
 #undef IH_ATT_NP
     default: return false;
@@ -660,15 +793,28 @@ int launch_attention(ih_ctx* c, const AttnArgs& a0) {
     return v ? std::max(1, std::min(MAX_PIECES, atoi(v))) : 2;
   }();
   const int np = std::min(ring_np, (a.C + PIECE - 1) / PIECE);
-  dim3 grid(a.nsplit, a.KVH, (qtiles + 4) / 5);
+  // The tile layout follows the model's largest block (Qpad rows), never this step's rows: see attn_kernel.
+  const int tpw = a.Qpad <= 80 ? 0 : qtiles > 8 ? 2 : 1;
+  dim3 grid(a.nsplit, a.KVH, tpw == 0 ? (qtiles + 4) / 5 : 1);
   // Algorithmic bytes: the int8 K and V and their fp16 scales of every key the launched splits cover, and q.
   const double keys = double(a.P + a.B) - double(a.s0) * a.C;
   TimedLaunch tl(c, TC_ATTN, double(a.KVH) * keys * (2 * a.HD + 4) + double(a.KVH) * Q * a.HD * 2);
   const bool ring = a.ring != 0;
-  bool ok;
-  if (a.HD == 128) ok = ring ? launch_attn_np<128, true>(tl, grid, c->stream, a, np) : launch_attn_np<128, false>(tl, grid, c->stream, a, np);
-  else if (a.HD == 64) ok = ring ? launch_attn_np<64, true>(tl, grid, c->stream, a, np) : launch_attn_np<64, false>(tl, grid, c->stream, a, np);
-  else return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
+  bool ok = false;
+#define IH_ATT_TPW(HD_, T_) \
+  ok = ring ? launch_attn_np<HD_, T_, true>(tl, grid, c->stream, a, np) : launch_attn_np<HD_, T_, false>(tl, grid, c->stream, a, np)
+  if (a.HD == 128) {
+    if (tpw == 0) IH_ATT_TPW(128, 0);
+    else if (tpw == 1) IH_ATT_TPW(128, 1);
+    else IH_ATT_TPW(128, 2);
+  } else if (a.HD == 64) {
+    if (tpw == 0) IH_ATT_TPW(64, 0);
+    else if (tpw == 1) IH_ATT_TPW(64, 1);
+    else IH_ATT_TPW(64, 2);
+  } else {
+    return fail(IH_EINVAL, "attention: head_dim must be 64 or 128");
+  }
+#undef IH_ATT_TPW
   IH_CHECK(ok, IH_EINVAL, "attention: unsupported key chunk");
   IH_HIP(hipGetLastError());
   return IH_OK;
