@@ -639,6 +639,13 @@ static QmmShape qmm_shape_sym(int Npad, int nkb);
 static QmmShape qmm_shape(int Npad, int nkb) {
   const QmmShape sh = qmm_shape_sym(Npad, nkb);
   if (sh.R == 7 && sh.KW == 4 && sh.kpw == 8 && sh.ks == 1) return QmmShape{7, 8, 2, 6, 1, 2};
+  // One-tile workgroups over 112 K-blocks (down at K = 14336): every workgroup reads the whole 487 KB activation from
+  // L2, which bounds the kernel; two-tile workgroups with K split in two read half as much per CU, and the split's
+  // reduction in the last-arriving workgroup costs less than that saves (config 1: 2.375 → 2.342 ms per step).
+  if (sh.R == 1 && sh.KW == 8 && sh.kpw == 14 && sh.ks == 1 && nkb == 112 && Npad % 32 == 0) {
+    const QmmShape s2{2, 7, qmm_ring_depth(8), 8, 2};
+    if (qmm_shape_ok(s2, Npad, nkb)) return s2;
+  }
   return sh;
 }
 static QmmShape qmm_shape_sym(int Npad, int nkb) {
