@@ -202,7 +202,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   constexpr int KITEMS = PIECE * KPK, VITEMS = HD * (PIECE / 16);
   // Four LDS buffers: with a ring of two, the pieces go in pairs (one barrier per pair, pairs alternating between
   // buffers {0, 1} and {2, 3}); otherwise one piece per barrier through buffers 0 and 1.
-  constexpr int NBUF = NP == 2 ? 4 : 2;
+  constexpr int NBUF = NP == 2 || TPW == 0 ? 4 : 2;
   __shared__ _Float16 Kf[NBUF][PIECE * KR];
   __shared__ _Float16 Vt[NBUF][HD * VROW];
   __shared__ __attribute__((aligned(16))) float ksf[NBUF][PIECE], vsf[NBUF][PIECE];
@@ -258,8 +258,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   // A ring of NP pieces: piece q in pr[q mod NP], refilled with piece q + NP as soon as piece q is converted (a
   // piece past the last re-reads the last one). The first piece lands without waiting for the whole split.
   const int npieces = (k1 - k0 + PIECE - 1) / PIECE;  // ≥ 1 for every launched split
+  if constexpr (TPW != 0) {
 #pragma unroll
-  for (int p = 0; p < NP; ++p) load_piece(pr[p], min(p, npieces - 1));
+    for (int p = 0; p < NP; ++p) load_piece(pr[p], min(p, npieces - 1));
+  }
 
   // Query tiles. A row's bits must not depend on the block, so every row of a model is reduced in one order, chosen
   // from the model's largest block (its padded row count Qpad):
@@ -533,9 +535,111 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     else whole_products(b, kb, nkeys);
   };
 
-  // Batches of NP pieces (one batch unless the split exceeds 64·NP keys). Pieces alternate between the two LDS
-  // buffers; the barrier before a batch's loads keeps every wave's last reads of the batch before them.
-  if constexpr (NP == 2) {
+  if constexpr (TPW == 0) {
+    // Key-half layout: waves 6 and 7 produce, waves 0-5 multiply. Pair i of pieces (2i, 2i + 1) goes into buffers
+    // 2(i mod 2), 2(i mod 2) + 1. Barrier B0 follows the producers' staging of pair 0; barrier B(i + 1) follows the
+    // products of pair i and the staging of pair i + 1, whose buffers pair i − 1 last read before B(i). Each producer
+    // thread holds two pairs of loads in flight (issued two pairs ahead), so the conversion of the next pair runs on
+    // SIMDs 2 and 3 alongside the products of the current one instead of in a phase of its own.
+    constexpr int KPT = KITEMS / 128, VPT = VITEMS / 128;  // items per producer thread and piece
+    static_assert(KITEMS % 128 == 0 && VITEMS % 128 == 0, "two producer waves split the items evenly");
+    const int npairs = (npieces + 1) / 2;
+    if (wave >= 6) {
+      const int ptid = tid - 384;
+      struct PairRegs {
+        uint4 k[2][KPT], v[2][VPT];
+        __half ks[2], vs[2];
+      };
+      PairRegs R[2];
+      auto load_pair = [&](PairRegs& r, int i) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int kb = k0 + PIECE * min(2 * i + h, npieces - 1);
+#pragma unroll
+          for (int e = 0; e < KPT; ++e) {
+            const int item = ptid + 128 * e, key = min(kb + item / KPK, k1 - 1), col = (item % KPK) * 16;
+            r.k[h][e] = *reinterpret_cast<const uint4*>(kh + size_t(slot_of(key)) * HD + col);
+          }
+#pragma unroll
+          for (int e = 0; e < VPT; ++e) {
+            const int item = ptid + 128 * e, dim = item / (PIECE / 16), pc = item % (PIECE / 16), pos = kb + 16 * pc;
+            const int blk = min(pos & ~31, (k1 - 1) & ~31);
+            r.v[h][e] = *reinterpret_cast<const uint4*>(vh + size_t(dim) * a.vld + slot_of(blk) + (pos & 31));
+          }
+          if (ptid < PIECE) {
+            const int key = min(kb + ptid, k1 - 1);
+            r.ks[h] = ksh[slot_of(key)];
+            r.vs[h] = vsh[slot_of(key)];
+          }
+        }
+      };
+      auto cvt16 = [](const uint4& w, u32x4& h0, u32x4& h1) {
+        __half2 lo, hi;
+        i8x4_to_h(w.x, lo, hi); h0.x = __builtin_bit_cast(unsigned, lo); h0.y = __builtin_bit_cast(unsigned, hi);
+        i8x4_to_h(w.y, lo, hi); h0.z = __builtin_bit_cast(unsigned, lo); h0.w = __builtin_bit_cast(unsigned, hi);
+        i8x4_to_h(w.z, lo, hi); h1.x = __builtin_bit_cast(unsigned, lo); h1.y = __builtin_bit_cast(unsigned, hi);
+        i8x4_to_h(w.w, lo, hi); h1.z = __builtin_bit_cast(unsigned, lo); h1.w = __builtin_bit_cast(unsigned, hi);
+      };
+      auto store_pair = [&](const PairRegs& r, int i) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int q = 2 * i + h;
+          if (q >= npieces) break;  // uniform
+          const int b = 2 * (i & 1) + h, kb = k0 + PIECE * q;
+#pragma unroll
+          for (int e = 0; e < KPT; ++e) {
+            const int item = ptid + 128 * e, key = item / KPK, col = (item % KPK) * 16;
+            u32x4 h0, h1;
+            cvt16(r.k[h][e], h0, h1);
+            *reinterpret_cast<u32x4*>(&Kf[b][key * KR + col]) = h0;
+            *reinterpret_cast<u32x4*>(&Kf[b][key * KR + col + 8]) = h1;
+          }
+#pragma unroll
+          for (int e = 0; e < VPT; ++e) {
+            const int item = ptid + 128 * e, dim = item / (PIECE / 16), pc = item % (PIECE / 16);
+            u32x4 h0, h1;
+            cvt16(r.v[h][e], h0, h1);
+            *reinterpret_cast<u32x4*>(&Vt[b][dim * VROW + 16 * pc]) = h0;
+            *reinterpret_cast<u32x4*>(&Vt[b][dim * VROW + 16 * pc + 8]) = h1;
+          }
+          if (ptid < PIECE) {
+            const bool ok = kb + ptid < k1;
+            ksf[b][ptid] = ok ? __half2float(r.ks[h]) * a.scale_log2 : 0.f;
+            vsf[b][ptid] = ok ? __half2float(r.vs[h]) : 0.f;
+          }
+        }
+      };
+      load_pair(R[0], 0);
+      load_pair(R[1], min(1, npairs - 1));
+      store_pair(R[0], 0);
+      load_pair(R[0], min(2, npairs - 1));
+      __syncthreads();  // B0
+      for (int i = 0; i < npairs; i += 2) {
+        if (i + 1 < npairs) {
+          store_pair(R[1], i + 1);
+          load_pair(R[1], min(i + 3, npairs - 1));
+        }
+        __syncthreads();  // B(i + 1)
+        if (i + 1 < npairs) {
+          if (i + 2 < npairs) {
+            store_pair(R[0], i + 2);
+            load_pair(R[0], min(i + 4, npairs - 1));
+          }
+          __syncthreads();  // B(i + 2)
+        }
+      }
+    } else {
+      __syncthreads();  // B0
+      for (int i = 0; i < npairs; ++i) {
+        const int q = 2 * i, b0 = 2 * (i & 1), kb0 = k0 + PIECE * q, kb1 = kb0 + PIECE;
+        if (q < 16) ASTAMP(2 + q);
+        piece_products(b0, kb0, min(PIECE, k1 - kb0));
+        if (q + 1 < npieces) piece_products(b0 + 1, kb1, min(PIECE, k1 - kb1));
+        if (q < 16) ASTAMP(3 + q);
+        __syncthreads();  // B(i + 1)
+      }
+    }
+  } else if constexpr (NP == 2) {
     // Pairs of pieces: both converted (pair i into buffers 2(i mod 2) and 2(i mod 2) + 1, last read by pair i − 2,
     // before the barrier of pair i − 1), one barrier, both multiplied.
     for (int q = 0; q < npieces; q += 2) {
