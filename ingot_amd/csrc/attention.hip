@@ -774,12 +774,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 // activation layout (column h·HD + d). One wave per (row, q head): lane = (split group sg, 8-dim group dg); a lane
 // merges splits sg, sg + SG, … in batches of NB whose loads are all issued before any is used (a load per trip of a
 // runtime loop would wait out a memory latency per split), keeping a running (M, L, o) rescaled per batch; then the
-// SG groups are merged by a fixed butterfly. Grid (B, QH/4), 256 threads.
+// SG groups are merged by a fixed butterfly. Grid (B, QH/w), 64·w threads (w = 1 by default).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb, int ntile) {
   constexpr int DG = HD / 8, SG = 64 / DG, NB = 8;
   static_assert(DG == 8 || DG == 16, "the split-group merge below runs the stages 8/16/32 of HD 64 and 128");
-  const int t = blockIdx.x, h = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int t = blockIdx.x, h = blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int dg = lane % DG, sg = lane / DG;
   const int kvh = h / a.G, m = t * a.G + h % a.G;
   float M = -INFINITY, L = 0.f;
@@ -925,12 +925,16 @@ int launch_attention(ih_ctx* c, const AttnArgs& a0) {
 }
 
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
-  IH_CHECK(a.QH % 4 == 0, IH_EINVAL, "attention reduce: the q head count must be a multiple of 4");
+  IH_CHECK(a.QH % 4 == 0, IH_EINVAL, "attention reduce: the q head count must be a multiple of 4");  // rw ≤ 4
   TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (2 * a.HD + 8) + double(a.B) * a.QH * a.HD * 2);
-  const dim3 grid(a.B, a.QH / 4);
+  // One wave (one (row, q head)) per workgroup: 4·B·QH/4 small workgroups spread over more CUs than four-wave ones
+  // (config 1: 0.146 against 0.149 ms per step). IH_REDUCE_WAVES: tuning override.
+  static const int rw = [] { const char* v = getenv("IH_REDUCE_WAVES"); return v ? atoi(v) : 1; }();
+  IH_CHECK(rw == 1 || rw == 2 || rw == 4, IH_EINVAL, "attention reduce: 1, 2 or 4 waves per workgroup");
+  const dim3 grid(a.B, a.QH / rw);
   uint4* of = static_cast<uint4*>(out.frag);
-  if (a.HD == 128) tlaunch(tl, attn_reduce_kernel<128>, grid, dim3(256), 0, c->stream, a, of, out.nkb, out.ntile);
-  else if (a.HD == 64) tlaunch(tl, attn_reduce_kernel<64>, grid, dim3(256), 0, c->stream, a, of, out.nkb, out.ntile);
+  if (a.HD == 128) tlaunch(tl, attn_reduce_kernel<128>, grid, dim3(64 * rw), 0, c->stream, a, of, out.nkb, out.ntile);
+  else if (a.HD == 64) tlaunch(tl, attn_reduce_kernel<64>, grid, dim3(64 * rw), 0, c->stream, a, of, out.nkb, out.ntile);
   else return fail(IH_EINVAL, "attention reduce: head_dim must be 64 or 128");
   IH_HIP(hipGetLastError());
   return IH_OK;
