@@ -82,6 +82,10 @@ def test_fullsize_verify_matches_oracle(ctx, name):
                oracle_step_s=round(t2 - t1, 2), top1=top1.tolist(), ref_top1=ref_top1.tolist())
         rel_tol, cos_tol = TOL["moe" if shape.get("n_experts") else "dense"]
         assert err <= rel_tol * scale and cos >= cos_tol, (err, scale, cos)
+        if not shape.get("n_experts"):
+            # The north star's example bound for the dense configurations: max-abs ≤ 2e-2 against the fp32 oracle
+            # (measured 0.009–0.013 at logit scale ~70).
+            assert err <= 2e-2, err
         assert flips == 0, (top1, ref_top1, margin, err)
         assert np.array_equal(top1, np.argmax(logits, axis=1).astype(np.uint32))
 
