@@ -10,15 +10,16 @@
 // rotated the same way, so (Hq)·(Hk) = q·k.
 //
 // MI355X design: one workgroup (8 waves) per (key split, KV head, 80 query rows); the split size C is fixed per cache
-// so that all splits of all heads are one workgroup per CU. A split streams through LDS in pieces of 64 keys: every
-// thread issues the loads of its next pieces at entry, each piece is converted int8 → fp16 exactly into one of the LDS
-// buffers (K key-major, V transposed) as soon as it lands, and six waves multiply: the five 16-query tiles go in
-// groups {0, 1}, {2, 3}, {4}, and each group is run by two waves, one over the first and one over the second 32 keys
-// of every piece, so every K and V fragment read from LDS serves two tiles. Sᵀ = K·Qᵀ (v_mfma_f32_16x16x32_f16, keys
-// as rows so each lane holds 4 keys of one query), online softmax in base 2 per query column, P stays in registers as
-// the B operand of Oᵀ += Vᵀ·Pᵀ; the two halves' states are merged at the end. A split writes O/l in fp16 with its
-// (max, sum); the reduction merges the splits in a fixed order. A query's result does not depend on the other rows of
-// the block: blocks start at fixed key positions, the split boundaries are fixed multiples of C, and every row is
+// so that all splits of all heads are one workgroup per CU. A split streams through LDS in pieces of 64 keys, each
+// converted int8 → fp16 exactly into LDS (K key-major, V transposed) while earlier pieces are multiplied. The tile
+// layout follows the model's largest block: up to five 16-query tiles (4 q heads per KV head) go in groups {0, 1},
+// {2, 3}, {4}, each run by two waves over the first and second 32 keys of every piece (every K and V fragment read
+// from LDS serves two tiles; the two halves' states are merged at the end) while waves 6 and 7 stage the pieces two
+// pairs ahead; larger groups run tiles w and w + 8 per wave over whole pieces, every wave staging. Sᵀ = K·Qᵀ
+// (v_mfma_f32_16x16x32_f16, keys as rows so each lane holds 4 keys of one query), online softmax in base 2 per query
+// column, P stays in registers as the B operand of Oᵀ += Vᵀ·Pᵀ. A split writes O/l in fp16 with its (max, sum); the
+// reduction merges the splits in a fixed order. A query's result does not depend on the other rows of the block:
+// blocks start at fixed key positions, the split boundaries are fixed multiples of C, and every row of a model is
 // reduced in the same order whatever tile it falls in.
 #include <hip/hip_fp16.h>
 
@@ -170,7 +171,7 @@ __device__ __forceinline__ float row_max4(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-constexpr int ATT_THREADS = 512;  // 8 waves: all load and convert, the first six multiply
+constexpr int ATT_THREADS = 512;  // 8 waves (roles per tile layout: see attn_kernel)
 constexpr int PIECE = 64;         // keys per pipelined piece of a split
 constexpr int MAX_PIECES = 2;     // deepest ring of pieces in flight (deeper rings spill the two tiles per wave)
 template <int HD> constexpr int krow() { return HD + 8; }
