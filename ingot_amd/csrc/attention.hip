@@ -682,90 +682,90 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
     lsum[tt] = l;
   }
   if constexpr (TPW == 0) {
-  // The half-1 states merged into the half-0 states through the K and V staging buffers (free after the last piece):
-  // M = max(m0, m1), L = 2^(m0 − M)·l0 + 2^(m1 − M)·l1, O = 2^(m0 − M)·O0 + 2^(m1 − M)·O1.
-  constexpr int HST = 16 * HD + 32;  // floats per tile state: O [dim][query], then (max, sum) per query
-  auto scr = [&](int lt) {  // tiles 0-3 in the K buffers, tile 4 in the V buffers
-    return lt < 4 ? reinterpret_cast<float*>(&Kf[0][0]) + lt * HST : reinterpret_cast<float*>(&Vt[0][0]);
-  };
-  static_assert(4 * HST * 4 <= sizeof(Kf) && HST * 4 <= sizeof(Vt), "the merge scratch fits the staging buffers");
-  __syncthreads();  // every wave is past its last piece
-  if (half == 1) {
+    // The half-1 states merged into the half-0 states through the K and V staging buffers (free after the last piece):
+    // M = max(m0, m1), L = 2^(m0 − M)·l0 + 2^(m1 − M)·l1, O = 2^(m0 − M)·O0 + 2^(m1 − M)·O1.
+    constexpr int HST = 16 * HD + 32;  // floats per tile state: O [dim][query], then (max, sum) per query
+    auto scr = [&](int lt) {  // tiles 0-3 in the K buffers, tile 4 in the V buffers
+      return lt < 4 ? reinterpret_cast<float*>(&Kf[0][0]) + lt * HST : reinterpret_cast<float*>(&Vt[0][0]);
+    };
+    static_assert(4 * HST * 4 <= sizeof(Kf) && HST * 4 <= sizeof(Vt), "the merge scratch fits the staging buffers");
+    __syncthreads();  // every wave is past its last piece
+    if (half == 1) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        if (!live[tt]) continue;
+        float* st = scr(2 * grp + tt);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) st[(16 * dt + 4 * qd + r) * 16 + j] = o[tt][dt][r];
+        if (qd == 0) {
+          st[16 * HD + j] = mrun[tt];
+          st[16 * HD + 16 + j] = lsum[tt];
+        }
+      }
+    }
+    __syncthreads();
+    ASTAMP(20);
+#ifdef IH_QMM_STAMP
+    if (a.stamp && kvh < 8 && sidx < 64 && blockIdx.z == 0 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
+      a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
+#endif
+    if (half == 1) return;
+    // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       if (!live[tt]) continue;
-      float* st = scr(2 * grp + tt);
+      const float* st = scr(2 * grp + tt);
+      const float m1 = st[16 * HD + j], l1 = st[16 * HD + 16 + j];
+      const float M = fmaxf(mrun[tt], m1);
+      const float w0 = mrun[tt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrun[tt] - M);
+      const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
+      const float l = lsum[tt] * w0 + l1 * w1;
+      const int m = 16 * (5 * blockIdx.z + 2 * grp + tt) + j;
+      if (m >= Q) continue;
+      const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
+      if (qd == 0) a.ml[base + m] = make_float2(M, l);
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+      for (int dt = 0; dt < NDT; ++dt) {
+        float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) st[(16 * dt + 4 * qd + r) * 16 + j] = o[tt][dt][r];
-      if (qd == 0) {
-        st[16 * HD + j] = mrun[tt];
-        st[16 * HD + 16 + j] = lsum[tt];
+        for (int r = 0; r < 4; ++r) v[r] = (o[tt][dt][r] * w0 + st[(16 * dt + 4 * qd + r) * 16 + j] * w1) * inv;
+        __half2 p0 = __floats2half2_rn(v[0], v[1]);
+        __half2 p1 = __floats2half2_rn(v[2], v[3]);
+        uint2 w;
+        w.x = __builtin_bit_cast(unsigned, p0);
+        w.y = __builtin_bit_cast(unsigned, p1);
+        *reinterpret_cast<uint2*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = w;
       }
     }
-  }
-  __syncthreads();
-  ASTAMP(20);
-#ifdef IH_QMM_STAMP
-  if (a.stamp && kvh < 8 && sidx < 64 && blockIdx.z == 0 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
-    a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
-#endif
-  if (half == 1) return;
-  // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    if (!live[tt]) continue;
-    const float* st = scr(2 * grp + tt);
-    const float m1 = st[16 * HD + j], l1 = st[16 * HD + 16 + j];
-    const float M = fmaxf(mrun[tt], m1);
-    const float w0 = mrun[tt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrun[tt] - M);
-    const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
-    const float l = lsum[tt] * w0 + l1 * w1;
-    const int m = 16 * (5 * blockIdx.z + 2 * grp + tt) + j;
-    if (m >= Q) continue;
-    const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
-    if (qd == 0) a.ml[base + m] = make_float2(M, l);
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = (o[tt][dt][r] * w0 + st[(16 * dt + 4 * qd + r) * 16 + j] * w1) * inv;
-      __half2 p0 = __floats2half2_rn(v[0], v[1]);
-      __half2 p1 = __floats2half2_rn(v[2], v[3]);
-      uint2 w;
-      w.x = __builtin_bit_cast(unsigned, p0);
-      w.y = __builtin_bit_cast(unsigned, p1);
-      *reinterpret_cast<uint2*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = w;
-    }
-  }
   } else {
-  ASTAMP(20);
+    ASTAMP(20);
 #ifdef IH_QMM_STAMP
-  if (TPW != 0 && a.stamp && kvh < 8 && sidx < 64 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
-    a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
+    if (TPW != 0 && a.stamp && kvh < 8 && sidx < 64 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
+      a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
 #endif
-  // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
+    // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    if (!live[tt]) continue;
-    const float l = lsum[tt];
-    const int m = 16 * (wave + 8 * tt) + j;
-    if (m >= Q) continue;
-    const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
-    if (qd == 0) a.ml[base + m] = make_float2(mrun[tt], l);
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    for (int tt = 0; tt < NT; ++tt) {
+      if (!live[tt]) continue;
+      const float l = lsum[tt];
+      const int m = 16 * (wave + 8 * tt) + j;
+      if (m >= Q) continue;
+      const size_t base = (size_t(kvh) * a.nsplit + sidx) * a.Qpad;
+      if (qd == 0) a.ml[base + m] = make_float2(mrun[tt], l);
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      __half2 p0 = __floats2half2_rn(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
-      __half2 p1 = __floats2half2_rn(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
-      uint2 w;
-      w.x = __builtin_bit_cast(unsigned, p0);
-      w.y = __builtin_bit_cast(unsigned, p1);
-      *reinterpret_cast<uint2*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = w;
+      for (int dt = 0; dt < NDT; ++dt) {
+        __half2 p0 = __floats2half2_rn(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
+        __half2 p1 = __floats2half2_rn(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
+        uint2 w;
+        w.x = __builtin_bit_cast(unsigned, p0);
+        w.y = __builtin_bit_cast(unsigned, p1);
+        *reinterpret_cast<uint2*>(a.opart + (base + m) * HD + 16 * dt + 4 * qd) = w;
+      }
     }
-  }
   }
 }
 
