@@ -301,7 +301,10 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   // first stages would otherwise queue behind the first half's staging loads and second stages. The barrier orders
   // only the issue. (With one wave per SIMD the staging loads go first: they are small and the first products wait
   // for them.)
-  if constexpr (KPW1 > 0) {
+  // The same for the seven-wave split-K shapes (down at K = 14336: 2.318 → 2.310 ms per step); at 16 waves (qkv, o) it
+  // loses (2.347).
+  constexpr bool FS = KPW1 > 0 || KW == 7;
+  if constexpr (FS) {
     load_stage(0, kb0);
     __syncthreads();
   }
@@ -339,7 +342,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   }
 
 #pragma unroll
-  for (int d = KPW1 > 0 ? 1 : 0; d < D; ++d) load_stage(d, kb0 + d);
+  for (int d = FS ? 1 : 0; d < D; ++d) load_stage(d, kb0 + d);
 
   // The RMSNorm factors of the input rows, while the first stages are on their way: their partials were requested
   // first, so waiting for them does not wait for the weights, and no accumulator is live yet.
