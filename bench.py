@@ -46,13 +46,15 @@ CONFIGS = {
                              label="config 2: copy lookup over 131072 ids + verify k=16 at P=32768"),
     # Config 3: 48 layers, hidden 2048, 32 q / 4 KV heads of 128, 128 experts top-8 (softmax), expert SwiGLU 768, int4.
     "moe-e128-16k": dict(desc=dict(n_layers=48, hidden=2048, n_q_heads=32, n_kv_heads=4, head_dim=128, intermediate=0,
-                                   vocab=151936, n_experts=128, top_k=8, expert_intermediate=768, expert_format=0),
+                                   vocab=151936, n_experts=128, top_k=8, expert_intermediate=768, expert_format=0,
+                                   iid_routing=1),
                          P=16384, B=17, label="config 3: MoE E128 top-8 verify k=16 at P=16384"),
     # Config 4: 24 layers, hidden 2880, 64 q / 8 KV heads of 64, sinks, alternating 128-token sliding window / full,
     # 32 MXFP4 experts top-4 with intermediate 2880, router and expert biases, swiglu_oai, vocab 201088; B = 9.
     "mxfp4-moe-64k": dict(desc=dict(n_layers=24, hidden=2880, n_q_heads=64, n_kv_heads=8, head_dim=64, intermediate=0,
                                     vocab=201088, n_experts=32, top_k=4, expert_intermediate=2880, expert_format=1,
-                                    router_bias=1, expert_bias=1, act=1, sinks=1, sliding_window=128),
+                                    router_bias=1, expert_bias=1, act=1, sinks=1, sliding_window=128,
+                                    iid_routing=1),
                           P=65536, B=9, label="config 4: MXFP4 MoE E32 top-4 verify k=8 at P=65536"),
 }
 
@@ -99,8 +101,7 @@ def main() -> int:
                 continue
             r = run_config(ctx, name, 10, 2, profile=True, cpu=False)
             keep = ("ms_per_step", "value", "step_hbm_gbs", "step_roofline_frac", "step_algorithmic_bytes",
-                    "moe_distinct_experts_per_layer", "moe_experts_iid_routing", "copy_lookup", "accepted_equals_planted",
-                    "step_bytes_iid_routing", "step_roofline_frac_iid_routing")
+                    "moe_distinct_experts_per_layer", "copy_lookup", "accepted_equals_planted", "roofline")
             others[name] = {k: r[k] for k in keep if k in r}
             others[name]["workload"] = r["config"]["workload"]
             others[name]["kernels_ms_per_step"] = {k: v["ms_per_step"] for k, v in r["kernels"].items()}
@@ -169,15 +170,6 @@ def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bo
         d_blocks = ctx.to_device(blocks)
         bufs.append(d_blocks)
         log(f"[bench] greedy chain: {chain}")
-        # MoE: the synthetic greedy chain repeats tokens, and identical rows route identically; the timed blocks carry
-        # distinct random drafts (the routing of real draft text), and the planted blocks are checked in an untimed
-        # pass. The step's cost does not depend on how many drafts are accepted (every row is verified).
-        d_timed = d_blocks
-        if d.get("n_experts"):
-            rnd = blocks.copy()
-            rnd[:, 1:] = rng.integers(0, d["vocab"], size=(k + 1, B - 1))
-            d_timed = ctx.to_device(rnd)
-            bufs.append(d_timed)
 
         def one(src, L):
             check(lib().ih_memcpy_dtod(ctx.handle, d_vtok.ptr, src.ptr + L * B * 4, B * 4))
@@ -186,7 +178,7 @@ def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bo
             # Rollback: the verify step does not advance the host position, so the next step sees P again.
 
         def step(i: int) -> None:
-            one(d_timed, i % (k + 1))
+            one(d_blocks, i % (k + 1))
 
     for i in range(warmup):
         step(i)
@@ -202,20 +194,15 @@ def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bo
     ctx.sync()
     ev.close()
     ms = ms_total / steps
-    # MoE: distinct experts per layer of the last timed step (the bytes actually streamed).
+    # MoE: distinct experts per layer of the last timed step (the bytes actually streamed). The synthetic routing is
+    # keyed by position, and every timed step runs at the same rolled-back position, so every step streams the same U.
     U = None
     if d.get("n_experts"):
         u = np.zeros(d["n_layers"], np.int32)
         check(lib().ih_model_moe_union(model.handle, u.ctypes.data))
         U = u.tolist()
-    if blocks is not None and d.get("n_experts"):
-        # Acceptance check on the planted blocks (untimed).
-        d_st.upload(np.zeros(8, np.uint32))
-        for i in range(k + 1):
-            one(d_blocks, i)
-        ctx.sync()
     rec = d_rec.download(np.uint32, (RING, 24))
-    nrec = k + 1 if (blocks is not None and d.get("n_experts")) else min(steps, RING)
+    nrec = min(steps, RING)
     accepted = [int(rec[i % RING][0]) for i in range(nrec)]
     if blocks is not None:
         planted = [i % (k + 1) for i in range(nrec)]
@@ -250,14 +237,12 @@ def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bo
     L_, H, KVH, HD = d["n_layers"], d["hidden"], d["n_kv_heads"], d["head_dim"]
     per_expert = 0.0
     weight_bytes = float(model.weight_bytes)
-    iid = None
     if d.get("n_experts"):
         IE, E = d["expert_intermediate"], d["n_experts"]
         bpw = 0.5625 if d.get("expert_format", 0) == 0 else 0.53125
         per_expert = 3 * IE * H * bpw
         dense_part = weight_bytes - L_ * E * per_expert
         weight_bytes = dense_part + sum(U) * per_expert
-        iid = moe_iid_timing(ctx, d, B)
     kv_bytes = 0.0
     for l in range(L_):
         keys = P + B
@@ -321,11 +306,6 @@ def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bo
     }
     if U is not None:
         out["moe_distinct_experts_per_layer"] = {"mean": round(float(np.mean(U)), 2), "min": min(U), "max": max(U)}
-        out["moe_experts_iid_routing"] = iid
-        # The step's bytes had the router seen i.i.d. N(0,1) logits (U from that routing), at this step's time.
-        iid_bytes = step_bytes - sum(U) * per_expert + L_ * iid["U"] * per_expert
-        out["step_bytes_iid_routing"] = round(iid_bytes)
-        out["step_roofline_frac_iid_routing"] = round(iid_bytes / (ms * 1e6) / HBM_PEAK_GBS, 4)
     if copy_n:
         out["copy_lookup"] = copy_lookup_timing(ctx, lib, check, d_hist, copy_n, k, d_copy, d_vtok, B)
     for b in bufs:
@@ -437,63 +417,6 @@ def copy_lookup_timing(ctx, lib, check, d_hist, n, k, d_copy, d_vtok, B) -> dict
     out = d_copy.download(np.uint32, (4 + k,))
     return {"us": round(us, 2), "context_gbs": round(n * 4 / (us * 1e3), 1), "proposed": int(out[0]),
             "match": int(out[1])}
-
-
-def moe_iid_timing(ctx, d: dict, B: int) -> dict:
-    """The expert streaming of one MoE layer under the routing config 3/4 describe (router logits i.i.d. N(0,1)):
-    routing + gathered gate|up + gathered down through the kernel-level entry points on stacked synthetic experts of
-    the configuration's shapes; µs per layer and the GB/s of the routed experts' bytes. (The synthetic model's own
-    router sees rows whose residual stream is dominated by attention outputs shared across the block, so its union is
-    much smaller; see moe_distinct_experts_per_layer.)"""
-    from ingot_amd._lib import HipEvents, QMat, Routing, check, lib
-
-    E, K, H, IE, fmt = d["n_experts"], d["top_k"], d["hidden"], d["expert_intermediate"], d.get("expert_format", 0)
-    g = np.random.default_rng(5)
-
-    def mat(N, Kd):
-        if fmt == 0:
-            q = g.integers(0, 2**32, size=(E, N, Kd // 8), dtype=np.uint32)
-            sc = np.full((E, N, Kd // 64), 0x3C00, np.uint16)
-            return QMat.int4(ctx, q, sc, sc)
-        q = g.integers(0, 2**32, size=(E, N, Kd // 8), dtype=np.uint32)
-        return QMat.mxfp4(ctx, q, np.full((E, N, Kd // 32), 122, np.uint8))
-
-    gu, dn = mat(2 * IE, H), mat(H, IE)
-    x = ctx.to_device(np.full((B, max(H, IE)), 0x3F80, np.uint16))
-    logits = ctx.to_device(g.normal(0, 1, size=(B, E)).astype(np.float32))
-    R = Routing(ctx, B, K, E).route(logits, E)
-    U = R.download()["U"]
-    ygu = ctx.buffer(B * K * 2 * IE * 4)
-    ydn = ctx.buffer(B * K * H * 4)
-
-    def layer():
-        check(lib().ih_moe_route(ctx.handle, logits.ptr, E, B, E, K, None, None, R.nent.ptr, R.entries.ptr,
-                                 R.x_row.ptr, R.pair_w.ptr, R.row_pair.ptr))
-        check(lib().ih_qmm_gathered(ctx.handle, gu.handle, x.ptr, max(H, IE), B, K, R.nent.ptr, R.entries.ptr,
-                                    R.x_row.ptr, ygu.ptr, 2 * IE))
-        check(lib().ih_qmm_gathered(ctx.handle, dn.handle, x.ptr, max(H, IE), B, K, R.nent.ptr, R.entries.ptr,
-                                    R.x_row.ptr, ydn.ptr, H))
-
-    for _ in range(3):
-        layer()
-    ev = HipEvents(ctx, 2)
-    ctx.sync()
-    reps = 20
-    ev.record(0)
-    for _ in range(reps):
-        layer()
-    ev.record(1)
-    us = ev.elapsed_ms(0, 1) / reps * 1e3
-    ctx.sync()
-    bpw = 0.5625 if fmt == 0 else 0.53125
-    by = U * 3 * IE * H * bpw
-    for b in (x, logits, ygu, ydn):
-        b.free()
-    R.free()
-    gu.free()
-    dn.free()
-    return {"U": int(U), "us_per_layer": round(us, 2), "expert_bytes": round(by), "gbs": round(by / (us * 1e3), 1),
-            "note": "kernel-level: x staged as bf16 rows by each gathered call (adds a small conversion launch)"}
 
 
 def copy_calibration(nbytes: int) -> int:

@@ -134,7 +134,7 @@ int ih_spec_accept_dev(ih_ctx* ctx, uint32_t* st_dev, uint32_t* vtok_dev, const 
 /* ---- sampling (temperature > 0) and the verify-row chooser ------------------------------------------------- */
 
 #define IH_TOPK 64           /* candidates per row (the nucleus and min-p set are searched among them) */
-#define IH_RND_PER_ROUND 32  /* uniforms per round: 2 per row (accept, resample) */
+#define IH_RND_PER_ROUND 34  /* uniforms per round: 2 per row (accept, resample) for IH_MAX_ROWS rows */
 /* temperature → top-k → min-p → top-p, as the reference (SampleParams, Shaders/zz_sample.metal:16-25; penalties are not
  * part of this path). */
 typedef struct ih_sample_params {
@@ -151,7 +151,7 @@ int ih_topk64_dev(ih_ctx* ctx, const float* logits_dev, int ldl, int rows, int V
                   float* val_dev, float* z_dev);
 /* Speculative verification by rejection (spec_accept_sample, Shaders/zz_sample.metal:241-281): draft vtok[i+1] is
  * accepted with probability p_i(draft) under `p`, else the next token is drawn from p_i without the draft; the emitted
- * tokens follow the target distribution exactly. Uniforms rnd_dev[st[5]·32 + 2i] (accept) and [… + 2i + 1]
+ * tokens follow the target distribution exactly. Uniforms rnd_dev[st[5]·IH_RND_PER_ROUND + 2i] (accept) and [… + 2i + 1]
  * (resample) of row i. The record, state and vtok[0] as ih_spec_accept_dev. Enqueued. */
 int ih_spec_accept_sample_dev(ih_ctx* ctx, uint32_t* st_dev, uint32_t* vtok_dev, const uint32_t* idx_dev,
                               const float* val_dev, const float* z_dev, uint32_t* rec_dev, const float* rnd_dev,
@@ -196,6 +196,28 @@ typedef struct ih_model_desc {
   int hadamard_k;                      /* store H·k and rotate q (the reference's default "hadk" scheme) */
   int qk_norm;                         /* per-head RMSNorm of q and k before RoPE, weights [head_dim] (Qwen3) */
   int qkv_bias;                        /* bias added to the q|k|v projection (Qwen2) */
+  /* Synthetic MoE routing of the benchmark configurations ("router logits ~N(0,1)"): the router's product still runs,
+   * then its logits are replaced by N(0,1) draws keyed by (seed, layer, position, expert) (+ the router bias), the
+   * same on the host oracle. Synthetic models only; 0 for real checkpoints. */
+  int iid_routing;
+  /* RoPE over the first rotary_dims dimensions of each q/k head, pairs (i, i + rotary_dims/2) (the reference's AT_ROT,
+   * head_dim · partial_rotary_factor); 0 = head_dim. Even, ≤ head_dim. */
+  int rotary_dims;
+  /* Gated attention output (Qwen3-Next, AT_GATED): q_proj rows per head are [q (head_dim) | gate (head_dim)] and the
+   * attention output is multiplied by sigmoid(gate) (vattn_reduce, Shaders/verify_attn.metal:94-99,149-192). */
+  int attn_gate;
+  int o_bias;                          /* o_proj bias (attention_bias: q, k, v and o biased; gpt-oss) */
+  /* RoPE frequency scaling (RopeTable.make, Sources/Ingot/Loader/RopeTable.swift:5-130): 0 default θ^(−i/(R/2)),
+   * 1 linear (÷ factor), 2 yarn (ramp between original and ÷ factor, q/k rotated dims × mscale), 3 proportional (the
+   * first int(R·partial)/2 pairs with period factor·θ^(2i/R), the rest angle 0). */
+  int rope_type;
+  float rope_factor;
+  float rope_orig_max;                 /* yarn: original_max_position_embeddings */
+  float rope_beta_fast, rope_beta_slow; /* yarn; 0 = the defaults 32 and 1 */
+  float rope_mscale;                   /* yarn: mscale (0 = 1) */
+  float rope_attn_factor;              /* yarn: attention_factor overriding the mscale (0 = none) */
+  int rope_no_truncate;                /* yarn: 1 = correction range not rounded to whole dims (gpt-oss truncate: false) */
+  float rope_partial;                  /* proportional: partial_rotary_factor (0 = 1) */
 } ih_model_desc;
 
 /* Creates a model with synthetic weights of `desc`'s shapes, deterministically from `seed` (counter-based SplitMix64
@@ -300,7 +322,7 @@ int ih_decode_greedy(ih_model* model, ih_kv* kv, const uint32_t* history, int n_
 
 /* ih_decode_greedy with temperature sampling (decodeSpec with sampling): each round's rows go through ih_topk64 and the
  * rejection acceptance of ih_spec_accept_sample_dev, with the uniforms of round r drawn from SplitMix64(seed) (24-bit,
- * 32 per round; Sampling.swift:50-62). The emitted tokens follow the model's distribution under `sp` whatever the
+ * IH_RND_PER_ROUND per round; Sampling.swift:50-62). The emitted tokens follow the model's distribution under `sp` whatever the
  * drafts; the same seed gives the same tokens. */
 int ih_decode_sample(ih_model* model, ih_kv* kv, const uint32_t* history, int n_history, uint32_t first,
                      const ih_decode_opts* opts, const ih_sample_params* sp, uint64_t seed, uint32_t* out, int out_cap,

@@ -313,7 +313,11 @@ class ModelDesc(C.Structure):
         ("rms_eps", C.c_float), ("n_experts", C.c_int), ("top_k", C.c_int), ("expert_intermediate", C.c_int),
         ("expert_format", C.c_int), ("router_bias", C.c_int), ("expert_bias", C.c_int), ("act", C.c_int),
         ("swiglu_limit", C.c_float), ("sliding_window", C.c_int), ("sinks", C.c_int), ("hadamard_k", C.c_int),
-        ("qk_norm", C.c_int), ("qkv_bias", C.c_int),
+        ("qk_norm", C.c_int), ("qkv_bias", C.c_int), ("iid_routing", C.c_int), ("rotary_dims", C.c_int),
+        ("attn_gate", C.c_int), ("o_bias", C.c_int), ("rope_type", C.c_int), ("rope_factor", C.c_float),
+        ("rope_orig_max", C.c_float), ("rope_beta_fast", C.c_float), ("rope_beta_slow", C.c_float),
+        ("rope_mscale", C.c_float), ("rope_attn_factor", C.c_float), ("rope_no_truncate", C.c_int),
+        ("rope_partial", C.c_float),
     ]
 
     @classmethod
@@ -400,7 +404,7 @@ class DecodeStats(C.Structure):
 
 
 FINISH_LENGTH, FINISH_STOP, FINISH_CONTEXT = 0, 1, 2
-TOPK, RND_PER_ROUND = 64, 32
+TOPK, RND_PER_ROUND = 64, 34
 
 
 class SampleParams(C.Structure):

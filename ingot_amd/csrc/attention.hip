@@ -68,13 +68,15 @@ __global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
   }
   if (slot >= a.QH + 2 * a.KVH) return;  // wave-uniform
   const bool isq = slot < a.QH, isk = !isq && slot < a.QH + a.KVH;
-  const float* row = a.proj + size_t(t) * a.ldp + size_t(slot) * HD;  // q heads | k heads | v heads
+  // Column of the head in the projection row: q heads QS apart (a gated head is [q | gate]), then k heads, v heads.
+  const int col = isq ? slot * a.QS : a.QH * a.QS + (slot - a.QH) * HD;
+  const float* row = a.proj + size_t(t) * a.ldp + col;
   float x[NE];
 #pragma unroll
   for (int e = 0; e < NE; ++e) x[e] = row[lane + 64 * e];
   if (a.qkv_bias) {
 #pragma unroll
-    for (int e = 0; e < NE; ++e) x[e] += a.qkv_bias[slot * HD + lane + 64 * e];
+    for (int e = 0; e < NE; ++e) x[e] += a.qkv_bias[col + lane + 64 * e];
   }
   if ((isq || isk) && a.qnorm) {
     // QK-norm: x · rsqrt(mean x² + eps) · w over the head, before RoPE (the AT_QKN branch of vattn_prework_i8).
@@ -93,14 +95,37 @@ __global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
     for (int e = 0; e < NE; ++e) x[e] = x[e] * r * dbf16(w[lane + 64 * e]);
   }
   if (isq || isk) {
-    const float2 cs = a.rope[t * RH + (lane % RH)];
-    if constexpr (NE == 2) {
-      const float xl = x[0], xh = x[1];
-      x[0] = xl * cs.x - xh * cs.y;
-      x[1] = xh * cs.x + xl * cs.y;
+    if (a.rot == HD) {
+      const float2 cs = a.rope[t * RH + (lane % RH)];
+      if constexpr (NE == 2) {
+        const float xl = x[0], xh = x[1];
+        x[0] = xl * cs.x - xh * cs.y;
+        x[1] = xh * cs.x + xl * cs.y;
+      } else {
+        const float o = lane_xor<RH>(x[0]);
+        x[0] = lane < RH ? x[0] * cs.x - o * cs.y : x[0] * cs.x + o * cs.y;
+      }
     } else {
-      const float o = lane_xor<RH>(x[0]);
-      x[0] = lane < RH ? x[0] * cs.x - o * cs.y : x[0] * cs.x + o * cs.y;
+      // Partial RoPE (AT_ROT < HD): dim d < rot pairs with d ± rot/2, read from the lane and element that hold it; the
+      // dims from rot on keep their value.
+      const int rh = a.rot >> 1;
+      float y[NE];
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        const int d = lane + 64 * e, dp = d < rh ? d + rh : d - rh;
+        float o = __shfl(x[0], dp & 63);
+        if constexpr (NE == 2) {
+          const float o1 = __shfl(x[1], dp & 63);
+          o = (dp >> 6) ? o1 : o;
+        }
+        y[e] = x[e];
+        if (d < a.rot) {
+          const float2 cs = a.rope[t * rh + (d % rh)];
+          y[e] = d < rh ? x[e] * cs.x - o * cs.y : x[e] * cs.x + o * cs.y;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < NE; ++e) x[e] = y[e];
     }
     if (a.hadk) {
       wht_stage<1>(x, lane);
@@ -852,6 +877,12 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __r
   const float inv = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] *= inv;
+  if (a.QS != HD) {
+    // Gated attention (AT_GATED): × sigmoid(gate), the gate being the second half of the q head's projection.
+    const float* g = a.proj + size_t(t) * a.ldp + size_t(h) * a.QS + HD + 8 * dg;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= 1.0f / (1.0f + expf(-g[e]));
+  }
   frag_store_chunk(frag, nkb, ntile, t, (h * HD) / 8 + dg, o);
 }
 

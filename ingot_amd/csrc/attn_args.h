@@ -19,10 +19,12 @@ __host__ __device__ __forceinline__ size_t v_index(int h, int slot, int d, int H
 __host__ __device__ __forceinline__ int v_row(int cap) { return (cap + 31) & ~31; }
 
 struct AttnArgs {
-  const float* proj;   // [B][ldp] = q heads | k heads | v heads (fp32, the qkv qmm output)
+  const float* proj;   // [B][ldp] = q heads (QS apart: [q | gate] when gated) | k heads | v heads (fp32, qkv output)
   int ldp;
+  int QS;              // stride of a q head in the projection row: HD, or 2·HD with a gate (attn_gate)
+  int rot;             // dims the RoPE rotates: pairs (i, i + rot/2), i < rot/2 (rot = HD: the whole head)
   __half* q;           // [KVH][Qpad][HD] fp16, query m = t·G + (h mod G)
-  const float2* rope;  // [B][HD/2] (cos, sin) of the angle pos·θ^(−i/(HD/2)), pos = P + t
+  const float2* rope;  // [B][rot/2] (cos, sin) of the angle of pair i at pos = P + t (× mscale of a scaled RoPE)
   int8_t* kc;          // [KVH][cap][HD]
   int8_t* vc;          // [KVH][HD][vld]: V transposed, slots permuted within 32-slot blocks (v_index)
   __half* ks;          // [KVH][cap]

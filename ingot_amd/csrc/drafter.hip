@@ -31,7 +31,8 @@ int synth_int4(ih_ctx* c, uint32_t* w, uint16_t* s, uint16_t* b, size_t N, size_
 int synth_bf16(ih_ctx* c, uint16_t* out, size_t n, uint64_t seed, uint64_t tensor, float base, float amp);
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                      float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a, float2* rope, int P, float theta,
-                     int RH, const uint32_t* pos_dev, int pos_max);
+                     int RH, const uint32_t* pos_dev, int pos_max, const float* rinv = nullptr,
+                     float rmscale = 1.0f);
 
 constexpr int DKVH = 8;          // KV heads of the drafter attention (DF_KVH)
 constexpr int DCHUNK = 128;      // keys per attention workgroup

@@ -72,6 +72,15 @@ constexpr int MAX_TOK = 32;     // tokens per qmm (two 16-token MFMA tiles)
 // (token-major, SS_CAP partials per row, so that one row's partials are one contiguous read): the consumer adds them
 // in order and applies the per-row factor in its epilogue.
 constexpr int SS_CAP = 4096;
+// Synthetic i.i.d. MoE routing (ih_model_desc.iid_routing): key of the layer's N(0,1) stream (0 = off) and the step's
+// position (the host value, or pos_dev[0] capped at pos_max for chained rounds). Row r's logit of expert e is draw
+// (pos + r)·E + e of the stream.
+struct MoeIid {
+  uint64_t key = 0;
+  int pos = 0;
+  const uint32_t* pos_dev = nullptr;
+  int pos_max = 0;
+};
 constexpr int QCTR_CAP = 16384;  // row groups of one split-K qmm launch
 struct ActBuf {
   void* frag = nullptr;   // [nkb][ntile][4][1 KB] (bf16 or fp16 elements)
@@ -183,6 +192,7 @@ struct QmmEpilogue {
   int ldy = 0;
   float eps = 1e-6f;       // RMSNorm eps of the input (QM_F32_SCALE, QM_GLU_ACT)
   const uint16_t* nw = nullptr;  // next RMSNorm weights (QM_RESID_ACT)
+  const float* bias = nullptr;   // QM_RESID_ACT: bias [N] added with the product (o_proj bias), or null
   ActBuf* act_out = nullptr;     // next activation (QM_RESID_ACT, QM_GLU_ACT)
   int glu = 0;
   float limit = 7.0f;

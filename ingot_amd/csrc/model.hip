@@ -20,7 +20,8 @@ namespace ih {
 // Launchers of the other translation units.
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                      float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a, float2* rope, int P, float theta,
-                     int RH, const uint32_t* pos_dev, int pos_max);
+                     int RH, const uint32_t* pos_dev, int pos_max, const float* rinv = nullptr,
+                     float rmscale = 1.0f);
 int launch_argmax(ih_ctx* c, const float* x, int ldx, int rows, int N, uint32_t* out);
 int launch_accept(ih_ctx* c, uint32_t* st, uint32_t* vtok, const uint32_t* top1, uint32_t* rec, int ring, int rows,
                   uint32_t* hist, int hist_cap);
@@ -37,7 +38,8 @@ int launch_prework(ih_ctx* c, const AttnArgs& a);
 int launch_attention(ih_ctx* c, const AttnArgs& a);
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out);
 int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K, const float* bias,
-                     const float* pes, int* nent, int* entries, int* x_row, float* pair_w, int* row_pair);
+                     const float* pes, int* nent, int* entries, int* x_row, float* pair_w, int* row_pair,
+                     const MoeIid& iid);
 int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, const float* pair_w, int K, int rows,
                        float* h, int H, const uint16_t* nw, ActBuf& act);
 int launch_moe_router(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, float eps, float* logits, int ldl);
@@ -50,7 +52,8 @@ int launch_moe_down(ih_ctx* c, const ih_qmat* W, const void* h_frag, int h_nkb, 
 // Tensor ids of the synthetic model (the generator's stream keys): globals, then 100 per layer.
 enum : uint64_t { T_EMBED = 1, T_FINAL_NORM = 2, T_HEAD = 3 };
 enum : uint64_t { L_ATTN_NORM = 0, L_QKV = 1, L_O = 2, L_MLP_NORM = 3, L_GATE_UP = 4, L_DOWN = 5, L_ROUTER = 6,
-                  L_ROUTER_BIAS = 7, L_SINKS = 9, L_Q_NORM = 10, L_K_NORM = 11, L_QKV_BIAS = 12 };
+                  L_ROUTER_BIAS = 7, L_SINKS = 9, L_Q_NORM = 10, L_K_NORM = 11, L_QKV_BIAS = 12, L_ROUTE_IID = 13,
+                  L_O_BIAS = 14 };
 constexpr uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
 // Experts: 3·10^6 + 10^4·layer + 10^3·kind + expert (kinds: gate|up, down, gate|up bias, down bias).
 enum : uint64_t { X_GATE_UP = 0, X_DOWN = 1, X_GU_BIAS = 2, X_DOWN_BIAS = 3 };
@@ -134,7 +137,9 @@ ih_model* model_new(ih_ctx* c, const ih_model_desc& d) {
   ih_model* m = new ih_model();
   m->ctx = c;
   m->d = d;
-  m->QP = (d.n_q_heads + 2 * d.n_kv_heads) * d.head_dim;
+  m->QS = d.head_dim * (d.attn_gate ? 2 : 1);
+  m->QP = d.n_q_heads * m->QS + 2 * d.n_kv_heads * d.head_dim;
+  m->rot = d.rotary_dims > 0 ? d.rotary_dims : d.head_dim;
   m->Qpad = (d.n_q_heads / d.n_kv_heads * IH_MAX_ROWS + 15) / 16 * 16;
   m->layers.resize(d.n_layers);
   return m;
@@ -152,7 +157,16 @@ int model_alloc_scratch(ih_model* m) {
   run(dalloc_t(&m->tok, MAX_TOK));
   run(dalloc_t(&m->top1, MAX_TOK));
   run(dalloc_t(&m->q, size_t(KVH) * m->Qpad * HD));
-  run(dalloc_t(&m->rope, size_t(IH_MAX_ROWS) * (HD / 2)));
+  run(dalloc_t(&m->rope, size_t(IH_MAX_ROWS) * (m->rot / 2)));
+  if (d.rope_type != 0 && st == IH_OK) {
+    // The scaled RoPE's frequencies (rounded to fp32 once) and its magnitude factor, computed on the host.
+    std::vector<float> inv;
+    rope_table(d, m->rot, inv, m->rmscale);
+    run(dalloc_t(&m->rinv, inv.size()));
+    if (st == IH_OK)
+      run(hipMemcpy(m->rinv, inv.data(), inv.size() * 4, hipMemcpyHostToDevice) == hipSuccess
+              ? IH_OK : fail(IH_EDEVICE, "model: RoPE table upload failed"));
+  }
   const bool moe = d.n_experts > 0, moe_f16 = moe && d.expert_format == QF_MXFP4;
   if (st == IH_OK) run(ensure_act(c, m->act_attn, H, false));
   if (st == IH_OK) run(ensure_act(c, m->act_mlp, H, moe_f16));
@@ -197,7 +211,63 @@ int check_desc(const ih_model_desc& d) {
              "model: intermediate must be a multiple of 64");
   }
   IH_CHECK(d.act == 0 || d.act == 1, IH_EINVAL, "model: act must be 0 (SiLU) or 1 (swiglu_oai)");
+  IH_CHECK(d.rotary_dims == 0 || (d.rotary_dims >= 2 && d.rotary_dims % 2 == 0 && d.rotary_dims <= d.head_dim),
+           IH_EINVAL, "model: rotary_dims must be 0 (the whole head) or even and within head_dim");
+  IH_CHECK(d.rope_type >= 0 && d.rope_type <= 3, IH_EINVAL,
+           "model: rope_type must be 0 (default), 1 (linear), 2 (yarn) or 3 (proportional)");
+  if (d.rope_type == 1 || d.rope_type == 2)
+    IH_CHECK(d.rope_factor > 0, IH_EINVAL, "model: a linear or yarn RoPE needs a positive factor");
+  if (d.rope_type == 2)
+    IH_CHECK(d.rope_orig_max > 0, IH_EINVAL, "model: a yarn RoPE needs original_max_position_embeddings");
+  if (d.rope_type == 3)
+    IH_CHECK(d.rope_factor >= 0 && d.rope_partial >= 0 && d.rope_partial <= 1, IH_EINVAL,
+             "model: a proportional RoPE needs factor > 0 and 0 < partial ≤ 1");
   return IH_OK;
+}
+
+// RopeTable.make (Sources/Ingot/Loader/RopeTable.swift:98-137): inv_freq of each of the dims/2 rotated pairs, in double
+// and rounded to fp32 once, and mscale (which multiplies the rotated dims of q and k). Periods θ^(2i/dims); linear
+// divides every frequency by the factor; proportional keeps the first int(dims·partial)/2 pairs at period
+// factor·θ^(2i/dims) and gives the others angle 0; yarn ramps from the original frequency (pairs below `low`) to
+// frequency / factor (above `high`), low/high from the correction range of beta_fast/beta_slow, mscale =
+// attention_factor or 0.1·mscale·ln(factor) + 1.
+void rope_table(const ih_model_desc& d, int dims, std::vector<float>& inv, float& mscale) {
+  const int rh = dims / 2;
+  const double theta = d.rope_theta, factor = d.rope_factor;
+  std::vector<double> per(rh), f(rh);
+  for (int i = 0; i < rh; ++i) {
+    per[i] = std::pow(theta, double(2 * i) / double(dims));
+    f[i] = 1.0 / per[i];
+  }
+  double ms = 1.0;
+  if (d.rope_type == 1) {
+    for (auto& x : f) x /= factor;
+  } else if (d.rope_type == 3) {
+    const double fac = factor > 0 ? factor : 1.0, part = d.rope_partial > 0 ? d.rope_partial : 1.0;
+    const int rotated = int(double(dims) * part) / 2;
+    for (int i = 0; i < rh; ++i) f[i] = i < rotated ? 1.0 / (fac * per[i]) : 0.0;
+  } else if (d.rope_type == 2) {
+    const double bf = d.rope_beta_fast > 0 ? d.rope_beta_fast : 32.0, bs = d.rope_beta_slow > 0 ? d.rope_beta_slow : 1.0;
+    const double orig = d.rope_orig_max;
+    auto corr = [&](double rot) { return double(dims) * std::log(orig / (rot * 2.0 * M_PI)) / (2.0 * std::log(theta)); };
+    double low = corr(bf), high = corr(bs);
+    if (!d.rope_no_truncate) {
+      low = std::floor(low);
+      high = std::ceil(high);
+    }
+    low = std::max(low, 0.0);
+    high = std::min(high, double(dims - 1));
+    if (low == high) high += 0.001;
+    for (int i = 0; i < rh; ++i) {
+      const double ramp = std::min(std::max((double(i) - low) / (high - low), 0.0), 1.0), extra = 1.0 - ramp;
+      f[i] = f[i] * extra + f[i] / factor * (1.0 - extra);
+    }
+    const double m = d.rope_mscale > 0 ? d.rope_mscale : 1.0;
+    ms = d.rope_attn_factor > 0 ? double(d.rope_attn_factor) : (factor <= 1 ? 1.0 : 0.1 * m * std::log(factor) + 1.0);
+  }
+  inv.resize(rh);
+  for (int i = 0; i < rh; ++i) inv[i] = float(f[i]);
+  mscale = float(ms);
 }
 
 void model_drafters_orphan(ih_model* m);  // drafter.hip
@@ -218,14 +288,14 @@ void model_release(ih_model* m) {
   for (auto& L : m->layers) {
     ih_qmat_free(L.qkv); ih_qmat_free(L.o); ih_qmat_free(L.gate_up); ih_qmat_free(L.down); ih_qmat_free(L.router);
     void* lp[] = {L.attn_norm, L.mlp_norm, L.sinks, L.router_bias, L.gu_bias, L.down_bias, L.q_norm, L.k_norm,
-                  L.qkv_bias};
+                  L.qkv_bias, L.o_bias};
     for (void* p : lp)
       if (p) (void)hipFree(p);
   }
   ih_qmat_free(m->head);
   void* ptrs[] = {m->emb_w, m->emb_s, m->emb_b, m->final_norm, m->h, m->proj, m->logits, m->tok, m->top1,
                   m->q, m->rope, m->opart, m->ml, m->rlogits, m->nent, m->entries, m->x_row, m->pair_w, m->row_pair,
-                  m->hpair, m->opair};
+                  m->hpair, m->opair, m->rinv};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   free_act(m->act_attn); free_act(m->act_mlp); free_act(m->act_o); free_act(m->act_i);
@@ -256,7 +326,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
   if (!st) pos_min = pos_max = kv->P;
   // The block's rows and the first RMSNorm input.
   IH_TRY(launch_embed_act(c, tok, m->emb_w, m->emb_s, m->emb_b, m->h, B, H, d.vocab, m->layers[0].attn_norm,
-                          m->act_attn, m->rope, kv->P, d.rope_theta, HD / 2, st, pos_max));
+                          m->act_attn, m->rope, kv->P, d.rope_theta, m->rot / 2, st, pos_max, m->rinv, m->rmscale));
   const int total = pos_max + B;
   for (int l = 0; l < d.n_layers; ++l) {
     const ih_layer& L = m->layers[l];
@@ -270,6 +340,8 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
     AttnArgs a{};
     a.proj = m->proj;
     a.ldp = m->QP;
+    a.QS = m->QS;
+    a.rot = m->rot;
     a.q = m->q;
     a.rope = m->rope;
     a.kc = kv->kc[l];
@@ -316,6 +388,7 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
     eo.y = m->h;
     eo.ldy = H;
     eo.nw = L.mlp_norm;
+    eo.bias = L.o_bias;
     eo.act_out = &m->act_mlp;
     IH_TRY(launch_qmm_ex(c, L.o, 0, m->act_o, B, eo));
     const uint16_t* next_norm = l + 1 < d.n_layers ? m->layers[l + 1].attn_norm : m->final_norm;
@@ -326,8 +399,15 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
       const bool f16 = d.expert_format == QF_MXFP4;
       IH_TRY(launch_moe_router(c, L.router, m->act_mlp, B, d.rms_eps, m->rlogits, E));
       int* nent = m->nent + l;  // one union count per layer, kept for ih_model_moe_union
+      MoeIid iid;
+      if (d.iid_routing) {
+        iid.key = sm_key(m->seed, layer_tensor(l, L_ROUTE_IID));
+        iid.pos = pos_max;
+        iid.pos_dev = st;
+        iid.pos_max = pos_max;
+      }
       IH_TRY(launch_moe_route(c, m->rlogits, E, B, E, K, L.router_bias, nullptr, nent, m->entries, m->x_row,
-                              m->pair_w, m->row_pair));
+                              m->pair_w, m->row_pair, iid));
       IH_TRY(launch_moe_gate_up(c, L.gate_up, m->act_mlp, B, K, d.rms_eps, nent, m->entries, m->x_row, L.gu_bias,
                                 d.act, d.swiglu_limit, m->hpair, m->hpair_nkb, m->max_pairs, f16));
       IH_TRY(launch_moe_down(c, L.down, m->hpair, m->hpair_nkb, m->max_pairs, f16, B, K, nent, m->entries,
@@ -468,6 +548,10 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
       }
       run(synth_qmat(c, stg, m->QP, H, seed, layer_tensor(l, L_QKV), W_SD, &L.qkv));
       run(synth_qmat(c, stg, H, QH * HD, seed, layer_tensor(l, L_O), W_SD, &L.o));
+      if (d.o_bias) {
+        run(dalloc_t(&L.o_bias, H));
+        if (st == IH_OK) run(synth_f32(c, L.o_bias, H, seed, layer_tensor(l, L_O_BIAS), 0.0f, 0.1f));
+      }
       if (d.n_experts > 0) {
         const int E = d.n_experts, IE = d.expert_intermediate, fmt = d.expert_format;
         run(synth_stack(c, stg, fmt, 1, E, H, seed, [&](int) { return layer_tensor(l, L_ROUTER); }, W_SD, 0,

@@ -14,6 +14,7 @@ struct ih_layer {
   uint16_t* q_norm = nullptr;     // bf16 [HD] (QK-norm)
   uint16_t* k_norm = nullptr;
   float* qkv_bias = nullptr;      // [QP]
+  float* o_bias = nullptr;        // [H] (attention_bias)
   ih_qmat* qkv = nullptr;
   ih_qmat* o = nullptr;
   // Dense FFN: gate|up [2I][H] (interleaved by eights), down [H][I]. MoE: the same, stacked over E experts (I = the
@@ -67,7 +68,7 @@ struct ih_model {
   uint32_t* tok = nullptr;   // [MAX_TOK]
   uint32_t* top1 = nullptr;  // [MAX_TOK]
   __half* q = nullptr;       // [KVH][Qpad][HD]
-  float2* rope = nullptr;    // [IH_MAX_ROWS][HD/2] (cos, sin) of the step's positions
+  float2* rope = nullptr;    // [IH_MAX_ROWS][rot/2] (cos, sin) of the step's positions (× mscale)
   // Activations: RMSNorm inputs bf16(h ⊙ w) with their sums of squares (attention / final norm, FFN norm), the
   // attention output and the gated activation.
   ih::ActBuf act_attn, act_mlp, act_o, act_i;
@@ -75,6 +76,10 @@ struct ih_model {
   float2* ml = nullptr;
   size_t part_splits = 0;    // splits the attention partials can hold
   int Qpad = 0, QP = 0;
+  int QS = 0;                // stride of a q head in the projection row (head_dim, 2·head_dim when gated)
+  int rot = 0;               // dims the RoPE rotates
+  float* rinv = nullptr;     // scaled RoPE: fp32 inv_freq [rot/2] (device), null for the default RoPE
+  float rmscale = 1.0f;      // its mscale
   // MoE scratch: router logits [MAX_TOK][E], the routing of the round, the pairs' gated activations (fragments, one
   // "token" per pair) and their down outputs [pairs][H].
   float* rlogits = nullptr;
@@ -105,6 +110,8 @@ struct ih_kv {
 namespace ih {
 // Validates a model description (shapes the kernels support).
 int check_desc(const ih_model_desc& d);
+// The frequencies of a scaled RoPE over `dims` rotated dims and its mscale (RopeTable.make).
+void rope_table(const ih_model_desc& d, int dims, std::vector<float>& inv, float& mscale);
 // A model object for `d` (no weights), its step scratch (residual, projections, logits, activations, attention and
 // MoE buffers) and its release (weights included).
 ih_model* model_new(ih_ctx* c, const ih_model_desc& d);

@@ -368,7 +368,8 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
                                                          int K, const float* __restrict__ bias,
                                                          const float* __restrict__ pes, int* __restrict__ nent,
                                                          int* __restrict__ entries, int* __restrict__ x_row,
-                                                         float* __restrict__ pair_w, int* __restrict__ row_pair) {
+                                                         float* __restrict__ pair_w, int* __restrict__ row_pair,
+                                                         MoeIid iid) {
   __shared__ float lg[MAX_TOK][256];
   __shared__ int inds[MAX_TOK * 16];
   __shared__ float chosen[MAX_TOK * 16];
@@ -376,10 +377,14 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
   __shared__ int lstart[256], lslot[256], wpairs[4], wslots[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
   const int nrk = rows * K;
-  // Logits (+ router bias), NaN → −inf, one row per wave at a time.
+  // Logits (+ router bias), NaN → −inf, one row per wave at a time. With synthetic i.i.d. routing the router's logit
+  // of (row, expert) is replaced by the N(0,1) draw of (position, expert).
+  const int pos0 = iid.pos_dev ? int(min(iid.pos_dev[0], uint32_t(iid.pos_max))) : iid.pos;
   for (int r = wave; r < rows; r += nw)
     for (int ex = lane; ex < E; ex += 64) {
-      float x = logits[size_t(r) * ldl + ex] + (bias ? bias[ex] : 0.f);
+      const float lv = iid.key ? sm_normal(iid.key, uint64_t(pos0 + r) * uint64_t(E) + uint64_t(ex))
+                               : logits[size_t(r) * ldl + ex];
+      float x = lv + (bias ? bias[ex] : 0.f);
       lg[r][ex] = x != x ? -INFINITY : x;
     }
   if (tid < 256) rmask[tid] = 0u;
@@ -573,13 +578,14 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
 }
 
 int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K, const float* bias,
-                     const float* pes, int* nent, int* entries, int* x_row, float* pair_w, int* row_pair) {
+                     const float* pes, int* nent, int* entries, int* x_row, float* pair_w, int* row_pair,
+                     const MoeIid& iid) {
   IH_CHECK(E >= 1 && E <= 256 && K >= 1 && K <= 16 && K <= E && rows >= 1 && rows <= MAX_TOK, IH_EINVAL,
            "moe route: need E ≤ 256, 1 ≤ k ≤ min(16, E), 1 ≤ rows ≤ 32");
   TimedLaunch tl(c, TC_MOE, double(rows) * E * 4);
   auto kern = E <= 128 ? moe_route_kernel<4> : moe_route_kernel<8>;
   tlaunch(tl, kern, dim3(1), dim3(1024), 0, c->stream, logits, ldl, rows, E, K, bias, pes, nent, entries,
-          x_row, pair_w, row_pair);
+          x_row, pair_w, row_pair, iid);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
@@ -790,7 +796,7 @@ int ih_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K
                  int* nent, int* entries, int* x_row, float* pair_w, int* row_pair) {
   IH_CHECK(c && logits && nent && entries && x_row && pair_w && row_pair, IH_EINVAL, "ih_moe_route: null argument");
   IH_CHECK(ldl >= E, IH_EINVAL, "ih_moe_route: ldl < E");
-  return launch_moe_route(c, logits, ldl, rows, E, K, bias, pes, nent, entries, x_row, pair_w, row_pair);
+  return launch_moe_route(c, logits, ldl, rows, E, K, bias, pes, nent, entries, x_row, pair_w, row_pair, MoeIid{});
 }
 
 int ih_qmm_gathered(ih_ctx* c, const ih_qmat* W, const void* x, int ldx, int rows, int K_top, const int* nent,

@@ -104,6 +104,7 @@ struct QmmParams {
   // QM_RESID_ACT: h[m][n] += v (fp32, the y pointer), then the next activation bf16(h ⊙ nw) and the sum-of-squares
   // partial of this workgroup's columns, ss_out[t][blockIdx.x].
   const uint16_t* nw;
+  const float* bias;  // QM_RESID_ACT: h += v + bias[n] when not null
   uint4* act_out;
   int act_nkb;
   float* ss_out;
@@ -162,7 +163,7 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, int tile0, V va
         const int col = col0 + j;
         float hv = 0.f;
         if (col < p.N) {
-          hv = (pre ? rpf->h[j] : hrow[col]) + val(m, r, 8 * half + j);
+          hv = (pre ? rpf->h[j] : hrow[col]) + (p.bias ? val(m, r, 8 * half + j) + p.bias[col] : val(m, r, 8 * half + j));
           hrow[col] = hv;
         }
         ss += hv * hv;
@@ -561,6 +562,11 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       }
       __syncthreads();
       if (arrived != unsigned(nsp - 1)) return;  // workgroup-uniform
+      // Acquire at agent scope: the partial loads below are ordered after the arrival count that saw every split. The
+      // writers' side needs no release fence (an agent-scope release writes back the whole XCD L2, ~15 µs per launch):
+      // their partials bypass the L2 (sc1 stores) and each writer waited for its stores to complete (waitcnt 0) before
+      // its barrier and its count, so every partial is at the coherence point before the count that reports it.
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       // The sums, in split order, into wave 0's partial slots (each thread reads back only slots it owns).
       for (int u = threadIdx.x; u < p.M * 4 * R; u += 64 * KW) {
         int i;
@@ -851,6 +857,7 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
     IH_CHECK(ep.act_out && ep.act_out->nkb * KBLK >= W->N && ep.nw, IH_EINVAL, "qmm: residual epilogue needs an output");
     IH_CHECK(egrid <= ep.act_out->ss_cap, IH_EINVAL, "qmm: too many workgroups for the RMSNorm partials");
     p.nw = ep.nw;
+    p.bias = ep.bias;
     p.act_out = static_cast<uint4*>(ep.act_out->frag);
     p.act_nkb = ep.act_out->nkb;
     p.act_f16 = ep.act_out->f16 ? 1 : 0;

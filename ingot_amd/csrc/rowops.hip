@@ -10,7 +10,8 @@ namespace ih {
 // Embedding of the block's rows: h[r] = dequant(table[tok[r]]) in fp32 (MLX int4 g64 row; embed_rows,
 // Shaders/yy_model.metal:12-49), and the first layer's RMSNorm input: the activation bf16(h ⊙ w) and Σh² per row
 // (one partial). Also the step's RoPE table (the rotation angles depend only on the position, so every layer's
-// prework reads them): rope[r][i] = (cos, sin)(pos · θ^(−i/RH)), pos = P + r, evaluated in double. Grid (2·rows), 256
+// prework reads them): rope[r][i] = (cos, sin)(pos · θ^(−i/RH)), pos = P + r, evaluated in double (a scaled RoPE:
+// pos · inv_freq[i] and both times mscale). Grid (2·rows), 256
 // threads: workgroup r < rows embeds row r (one thread per 8 values), workgroup rows + r evaluates row r's angles
 // (double pow, cos and sin take longer than the embedding, so the two run side by side).
 __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restrict__ tok, const uint32_t* __restrict__ w,
@@ -19,12 +20,21 @@ __global__ __launch_bounds__(256) void embed_act_kernel(const uint32_t* __restri
                                                         const uint16_t* __restrict__ nw, uint4* __restrict__ frag,
                                                         int nkb, int ntile, float* __restrict__ ss_out, int V,
                                                         float2* __restrict__ rope, int P, float theta, int RH,
-                                                        const uint32_t* __restrict__ pos_dev, int pos_max) {
+                                                        const uint32_t* __restrict__ pos_dev, int pos_max,
+                                                        const float* __restrict__ rinv, float rmscale) {
   __shared__ float red[4];
   const int rows = gridDim.x / 2;
   if (int(blockIdx.x) >= rows) {  // workgroup-uniform
     const int row = blockIdx.x - rows;
     if (pos_dev) P = int(min(pos_dev[0], uint32_t(pos_max)));  // chained rounds: the position of the round state
+    if (rinv) {
+      // A scaled RoPE (RopeTable): the pair's fp32 frequency, the angle in double, cos and sin times mscale.
+      for (int i = threadIdx.x; i < RH; i += blockDim.x) {
+        const double ang = double(P + row) * double(rinv[i]);
+        rope[row * RH + i] = make_float2(float(cos(ang) * double(rmscale)), float(sin(ang) * double(rmscale)));
+      }
+      return;
+    }
     for (int i = threadIdx.x; i < RH; i += blockDim.x) {
       const double ang = double(P + row) * pow(double(theta), -double(i) / double(RH));
       rope[row * RH + i] = make_float2(float(cos(ang)), float(sin(ang)));
@@ -191,10 +201,10 @@ __global__ void accept_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* top1
 // ---------------------------------------------------------------------------------------------------------------
 int launch_embed_act(ih_ctx* c, const uint32_t* tok, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                      float* h, int B, int H, int V, const uint16_t* nw, ActBuf& a, float2* rope, int P, float theta,
-                     int RH, const uint32_t* pos_dev, int pos_max) {
+                     int RH, const uint32_t* pos_dev, int pos_max, const float* rinv, float rmscale) {
   TimedLaunch tl(c, TC_ROWS, double(B) * H * (0.5625 + 4 + 2));
   tlaunch(tl, embed_act_kernel, dim3(2 * B), dim3(256), 0, c->stream, tok, w, s, b, h, H, H, nw, static_cast<uint4*>(a.frag),
-          a.nkb, a.ntile, a.ss, V, rope, P, theta, RH, pos_dev, pos_max);
+          a.nkb, a.ntile, a.ss, V, rope, P, theta, RH, pos_dev, pos_max, rinv, rmscale);
   IH_HIP(hipGetLastError());
   a.nss = 1;
   return IH_OK;

@@ -218,7 +218,7 @@ __device__ uint32_t sample_pick(const uint32_t* ci, const float* pr, int n, uint
 }
 
 // Acceptance by rejection (spec_accept_sample, zz_sample.metal:241-281): rows' candidates idx/val [rows][64] and
-// (max, Z) [rows][2]; uniforms rnd[round · 32 + 2i] (accept) and [… + 2i + 1] (resample) of row i. Writes the record
+// (max, Z) [rows][2]; uniforms rnd[round · IH_RND_PER_ROUND + 2i] (accept) and [… + 2i + 1] (resample) of row i. Writes the record
 // and advances the state as the greedy acceptance does (vtok[0] = the new anchor; the history as in accept_kernel).
 __global__ void accept_sample_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* cidx, const float* cval,
                                      const float* z, uint32_t* rec, const float* rnd, ih_sample_params p, int ring,

@@ -74,6 +74,9 @@ _SIGS = [
     ("or_glu", C.c_float, [C.c_float, C.c_float, i32, C.c_float]),
     ("or_fwht", None, [vp, i32]),
     ("or_rope_wht", None, [vp, i32, i32, C.c_float, i32]),
+    ("or_rope_wht_ex", None, [vp, i32, i32, i32, C.c_float, vp, C.c_float, i32]),
+    ("or_rope_table", C.c_float, [i32, C.c_double, i32, C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
+                                  C.c_double, i32, C.c_double, vp]),
     ("or_attention", None, [vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, vp, vp]),
     ("or_verify_dense", i32, [vp, C.c_uint64, C.c_uint64, i32, vp, i32, vp, vp]),
     ("or_model_create", vp, [vp, C.c_uint64, C.c_uint64, i32, i32]),
@@ -238,6 +241,33 @@ def fwht(v: np.ndarray) -> np.ndarray:
 def rope_wht(x: np.ndarray, pos: int, theta: float, hadk: int) -> np.ndarray:
     x = np.array(x, np.float32)
     lib().or_rope_wht(_p(x), len(x), pos, theta, hadk)
+    return x
+
+
+ROPE_KINDS = {"default": 0, "linear": 1, "yarn": 2, "proportional": 3}
+
+
+def rope_table(params: dict, theta: float, dims: int):
+    """(inv_freq fp32 [dims/2], mscale) of a RoPE parameter dict (rope_type/type, factor, original_max_position_embeddings,
+    beta_fast, beta_slow, mscale, attention_factor, truncate, partial_rotary_factor), as RopeTable.make."""
+    kind = ROPE_KINDS[params.get("rope_type", params.get("type", "default"))]
+    inv = np.zeros(dims // 2, np.float32)
+    if kind == 0:
+        inv[:] = (1.0 / np.power(float(theta), 2.0 * np.arange(dims // 2) / dims)).astype(np.float32)
+        return inv, 1.0
+    ms = lib().or_rope_table(kind, theta, dims, float(params.get("factor", 1.0)),
+                             float(params.get("original_max_position_embeddings", 0.0)),
+                             float(params.get("beta_fast", 32.0)), float(params.get("beta_slow", 1.0)),
+                             float(params.get("mscale", 1.0)), float(params.get("attention_factor", 0.0)),
+                             int(params.get("truncate", True)), float(params.get("partial_rotary_factor", 1.0)),
+                             _p(inv))
+    return inv, float(ms)
+
+
+def rope_wht_ex(x: np.ndarray, rot: int, pos: int, theta: float, inv, mscale: float, hadk: int) -> np.ndarray:
+    x = np.array(x, np.float32)
+    inv = None if inv is None else np.ascontiguousarray(inv, np.float32)
+    lib().or_rope_wht_ex(_p(x), len(x), rot, pos, theta, None if inv is None else _p(inv), mscale, hadk)
     return x
 
 

@@ -357,13 +357,29 @@ void or_fwht(float* v, int n) {
 
 // RoPE of one head (non-interleaved halves over all HD dims; angle pos·θ^(−i/(HD/2)) in double), then the orthonormal
 // WHT if hadk. normRope + hadamard, Tests/IngotTests/KernelHarness.swift:379-420; vattn_prework_i8.
-void or_rope_wht(float* x, int HD, int pos, float theta, int hadk) {
+// RoPE of the first `rot` dims (pairs d, d + rot/2; AT_ROT of vattn_prework_i8, verify_attn_nax.metal:92-98), the
+// angle of pair i at `pos` = pos·θ^(−i/(rot/2)) or, with a frequency table inv (a scaled RoPE, RopeTable), pos·inv[i]
+// with cos and sin times mscale (AT_ROPE_ANG / AT_ROPE_SCALE, verify_attn.metal:66-84); then the orthonormal
+// Walsh–Hadamard rotation of the head when hadk.
+void or_rope_wht_ex(float* x, int HD, int rot, int pos, float theta, const float* inv, float mscale, int hadk) {
   float y[256];
-  const int RH = HD / 2;
+  const int RH = rot / 2;
   for (int d = 0; d < HD; ++d) {
+    if (d >= rot) {
+      y[d] = x[d];
+      continue;
+    }
     const int i = d % RH;
-    const double ang = double(pos) * std::pow(double(theta), -double(i) / double(RH));
-    const float c = float(std::cos(ang)), s = float(std::sin(ang));
+    float c, s;
+    if (inv) {
+      const double ang = double(pos) * double(inv[i]);
+      c = float(std::cos(ang) * double(mscale));
+      s = float(std::sin(ang) * double(mscale));
+    } else {
+      const double ang = double(pos) * std::pow(double(theta), -double(i) / double(RH));
+      c = float(std::cos(ang));
+      s = float(std::sin(ang));
+    }
     y[d] = d < RH ? x[d] * c - x[d + RH] * s : x[d] * c + x[d - RH] * s;
   }
   if (hadk) {
@@ -372,6 +388,41 @@ void or_rope_wht(float* x, int HD, int pos, float theta, int hadk) {
     for (int d = 0; d < HD; ++d) y[d] *= sc;
   }
   std::memcpy(x, y, sizeof(float) * HD);
+}
+
+void or_rope_wht(float* x, int HD, int pos, float theta, int hadk) {
+  or_rope_wht_ex(x, HD, HD, pos, theta, nullptr, 1.0f, hadk);
+}
+
+// The frequency table of a scaled RoPE over `dims` rotated dims (RopeTable.make, Sources/Ingot/Loader/RopeTable.swift:
+// 98-137; mlx-lm initialize_rope): kind 1 linear, 2 yarn, 3 proportional. Every frequency is formed in double from
+// the period θ^(2i/dims) and rounded to float once; inv [dims/2]; returns mscale.
+float or_rope_table(int kind, double theta, int dims, double factor, double orig_max, double beta_fast,
+                    double beta_slow, double mscale_in, double attn_factor, int truncate, double partial, float* inv) {
+  const int rh = dims / 2;
+  double mscale = 1.0;
+  for (int i = 0; i < rh; ++i) {
+    const double period = std::pow(theta, 2.0 * i / dims);
+    double f = 1.0 / period;
+    if (kind == 1) f = f / factor;
+    if (kind == 3) f = (i < int(dims * partial) / 2) ? 1.0 / (factor * period) : 0.0;
+    if (kind == 2) {
+      // Correction range (yarn_find_correction_range): the dim at which `r` full rotations fit in orig_max positions.
+      const double lo0 = dims * std::log(orig_max / (beta_fast * 2 * M_PI)) / (2 * std::log(theta));
+      const double hi0 = dims * std::log(orig_max / (beta_slow * 2 * M_PI)) / (2 * std::log(theta));
+      double lo = truncate ? std::floor(lo0) : lo0, hi = truncate ? std::ceil(hi0) : hi0;
+      if (lo < 0) lo = 0;
+      if (hi > dims - 1) hi = dims - 1;
+      if (hi == lo) hi += 0.001;
+      double ramp = (i - lo) / (hi - lo);
+      ramp = ramp < 0 ? 0 : (ramp > 1 ? 1 : ramp);
+      // weight (1 − ramp) on the original frequency, ramp on the interpolated one (frequency / factor)
+      f = f * (1 - ramp) + (f / factor) * ramp;
+    }
+    inv[i] = float(f);
+  }
+  if (kind == 2) mscale = attn_factor > 0 ? attn_factor : (factor <= 1 ? 1.0 : 0.1 * mscale_in * std::log(factor) + 1.0);
+  return float(mscale);
 }
 
 // Causal GQA attention of B rows at positions P…P+B−1 over an int8 cache of P+B keys (the block's own keys already
@@ -420,6 +471,10 @@ struct or_model_desc {
   int n_experts, top_k, expert_intermediate, expert_format, router_bias, expert_bias, act;
   float swiglu_limit;
   int sliding_window, sinks, hadamard_k, qk_norm, qkv_bias;
+  int iid_routing, rotary_dims, attn_gate, o_bias, rope_type;
+  float rope_factor, rope_orig_max, rope_beta_fast, rope_beta_slow, rope_mscale, rope_attn_factor;
+  int rope_no_truncate;
+  float rope_partial;
 };
 
 static uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
@@ -468,7 +523,7 @@ static uint64_t expert_tensor(int l, uint64_t kind, int e) { return 3000000 + 10
 
 struct OrLayer {
   std::vector<uint16_t> attn_norm, mlp_norm, q_norm, k_norm;
-  std::vector<float> sinks, qkv_bias;
+  std::vector<float> sinks, qkv_bias, o_bias;
   QMat qkv, o, gate_up, down;
   // MoE: router [E][H], per expert gate|up [2I][H] (gate rows then up rows) and down [H][I], optional biases.
   AnyMat router;
@@ -483,6 +538,9 @@ struct OrLayer {
 struct OrModel {
   or_model_desc d;
   int P = 0, cap = 0;
+  uint64_t seed = 0;
+  std::vector<float> rinv;  // scaled RoPE: frequencies of the rotated pairs (empty: the default RoPE)
+  float rmscale = 1.0f;
   // Captured residual rows after the listed layers, bf16 [B][n · H] (capture_rows, yy_model.metal:94-104).
   std::vector<int> cap_layers;
   std::vector<uint16_t> caps;
@@ -496,10 +554,20 @@ void* or_model_create(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, i
   OrModel* m = new OrModel();
   m->d = *d;
   m->P = P;
+  m->seed = seed;
   m->cap = P + max_rows;
   const int H = d->hidden, QH = d->n_q_heads, KVH = d->n_kv_heads, HD = d->head_dim, I = d->intermediate;
-  const int QP = (QH + 2 * KVH) * HD;
+  const int QP = QH * HD * (d->attn_gate ? 2 : 1) + 2 * KVH * HD;
   const float sd = 0.02f;
+  if (d->rope_type != 0) {
+    const int rot = d->rotary_dims > 0 ? d->rotary_dims : HD;
+    m->rinv.resize(rot / 2);
+    m->rmscale = or_rope_table(d->rope_type, d->rope_theta, rot, d->rope_factor > 0 ? d->rope_factor : 1.0,
+                               d->rope_orig_max, d->rope_beta_fast > 0 ? d->rope_beta_fast : 32.0,
+                               d->rope_beta_slow > 0 ? d->rope_beta_slow : 1.0,
+                               d->rope_mscale > 0 ? d->rope_mscale : 1.0, d->rope_attn_factor, !d->rope_no_truncate,
+                               d->rope_partial > 0 ? d->rope_partial : 1.0, m->rinv.data());
+  }
   m->embed.make(seed, 1, d->vocab, H, sd);
   m->head.make(seed, 3, d->vocab, H, sd);
   m->final_norm.resize(H);
@@ -527,6 +595,10 @@ void* or_model_create(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, i
     }
     L.qkv.make(seed, layer_tensor(l, 1), QP, H, sd);
     L.o.make(seed, layer_tensor(l, 2), H, QH * HD, sd);
+    if (d->o_bias) {
+      L.o_bias.resize(H);
+      or_synth_f32(seed, layer_tensor(l, 14), H, 0.0f, 0.1f, L.o_bias.data());
+    }
     if (d->n_experts > 0) {
       const int E = d->n_experts, IE = d->expert_intermediate, f = d->expert_format;
       L.router.make(f, seed, layer_tensor(l, 6), E, H, sd);
@@ -579,15 +651,22 @@ int or_expert_union(const int32_t* inds, int rows, int K, int E, int32_t* entrie
 // Tests/IngotTests/KernelHarness.swift:720-766): x = round(h ⊙ w) and r as the RMSNorm split (fp16 for MXFP4 experts,
 // bf16 for int4), router logits r·(x·Wrᵀ) (+ router bias), softmax top-k and the expert union; per pair h_p =
 // round(act(r·g + bg, r·u + bu)), o_p = h_p·Wdᵀ + bd; y[row] = Σ_slot w·o in slot order; h += y.
-static void moe_forward(const or_model_desc* d, const OrLayer& L, float* hres, int B) {
+// With iid_key ≠ 0 (the synthetic i.i.d. routing of ih_model_desc.iid_routing) the router logit of row r and expert e
+// is draw (P + r)·E + e of that N(0,1) stream instead of the router's product.
+static void moe_forward(const or_model_desc* d, const OrLayer& L, float* hres, int B, uint64_t iid_key, int P) {
   const int H = d->hidden, E = d->n_experts, K = d->top_k, IE = d->expert_intermediate;
   const bool f16 = d->expert_format == 1;
   auto round_act = [&](float v) { return f16 ? or_f16_to_f32(or_f32_to_f16(v)) : or_bf16_to_f32(or_f32_to_bf16(v)); };
   std::vector<float> x(size_t(B) * H), rr(B), lg(size_t(B) * E);
   if (f16) or_rms_split_f16(hres, B, H, L.mlp_norm.data(), d->rms_eps, x.data(), rr.data());
   else or_rms_split(hres, B, H, L.mlp_norm.data(), d->rms_eps, x.data(), rr.data());
-  L.router.apply(x.data(), B, lg.data());
-  scale_rows(lg.data(), B, E, rr.data());
+  if (iid_key) {
+    for (int r = 0; r < B; ++r)
+      for (int e = 0; e < E; ++e) lg[size_t(r) * E + e] = sm_normal(iid_key, uint64_t(P + r) * uint64_t(E) + uint64_t(e));
+  } else {
+    L.router.apply(x.data(), B, lg.data());
+    scale_rows(lg.data(), B, E, rr.data());
+  }
   std::vector<int32_t> inds(size_t(B) * K), entries(size_t(B) * K * 3), pairs(size_t(B) * K * 2);
   std::vector<float> wts(size_t(B) * K);
   or_route(lg.data(), B, E, K, 0, nullptr, L.router_bias.empty() ? nullptr : L.router_bias.data(), nullptr, 1.0f, 0.0f,
@@ -657,7 +736,11 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
   OrModel* m = static_cast<OrModel*>(h);
   const or_model_desc* d = &m->d;
   const int H = d->hidden, QH = d->n_q_heads, KVH = d->n_kv_heads, HD = d->head_dim, I = d->intermediate;
-  const int QP = (QH + 2 * KVH) * HD, P = m->P, cap = m->cap;
+  // q heads QS apart in the projection row ([q | gate] per head with a gate: AT_QS, verify_attn.metal:28-45).
+  const int QS = HD * (d->attn_gate ? 2 : 1), QP = QH * QS + 2 * KVH * HD, P = m->P, cap = m->cap;
+  const int rot = d->rotary_dims > 0 ? d->rotary_dims : HD;
+  const float* rinv = m->rinv.empty() ? nullptr : m->rinv.data();
+  auto col = [&](int hh) { return hh < QH ? hh * QS : QH * QS + (hh - QH) * HD; };
   if (B < 1 || P + B > cap) return 1;
   std::vector<float> hres(size_t(B) * H);
   for (int r = 0; r < B; ++r)
@@ -677,7 +760,7 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
     if (!L.q_norm.empty())
       for (int t = 0; t < B; ++t)
         for (int hh = 0; hh < QH + KVH; ++hh) {
-          float* xr = proj.data() + size_t(t) * QP + size_t(hh) * HD;
+          float* xr = proj.data() + size_t(t) * QP + col(hh);
           double ss = 0;
           for (int dd = 0; dd < HD; ++dd) ss += double(xr[dd]) * xr[dd];
           const float r = 1.0f / std::sqrt(float(ss) / float(HD) + d->rms_eps);
@@ -688,15 +771,15 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
       const float* pr = proj.data() + size_t(t) * QP;
       for (int hh = 0; hh < QH; ++hh) {
         float xq[256];
-        std::memcpy(xq, pr + hh * HD, sizeof(float) * HD);
-        or_rope_wht(xq, HD, P + t, d->rope_theta, d->hadamard_k);
+        std::memcpy(xq, pr + col(hh), sizeof(float) * HD);
+        or_rope_wht_ex(xq, HD, rot, P + t, d->rope_theta, rinv, m->rmscale, d->hadamard_k);
         for (int dd = 0; dd < HD; ++dd) q[(size_t(t) * QH + hh) * HD + dd] = or_f16_to_f32(or_f32_to_f16(xq[dd]));
       }
       for (int hh = 0; hh < KVH; ++hh) {
         float xk[256], xv[256];
-        std::memcpy(xk, pr + (QH + hh) * HD, sizeof(float) * HD);
-        std::memcpy(xv, pr + (QH + KVH + hh) * HD, sizeof(float) * HD);
-        or_rope_wht(xk, HD, P + t, d->rope_theta, d->hadamard_k);
+        std::memcpy(xk, pr + col(QH + hh), sizeof(float) * HD);
+        std::memcpy(xv, pr + col(QH + KVH + hh), sizeof(float) * HD);
+        or_rope_wht_ex(xk, HD, rot, P + t, d->rope_theta, rinv, m->rmscale, d->hadamard_k);
         const size_t o = size_t(hh) * cap + P + t;
         quant_i8(xk, HD, &L.k[o * HD], &L.ks[o]);
         quant_i8(xv, HD, &L.v[o * HD], &L.vs[o]);
@@ -705,11 +788,22 @@ int or_model_verify(void* h, const uint32_t* tokens, int B, float* logits, uint3
     const int window = (d->sliding_window > 0 && l % 2 == 0) ? d->sliding_window : 0;
     or_attention(q.data(), B, P, QH, KVH, HD, L.k.data(), L.v.data(), L.ks.data(), L.vs.data(), cap, window,
                  d->sinks ? L.sinks.data() : nullptr, att.data());
+    // Gated output: × sigmoid(gate) per (row, head, dim) (at_gate in vattn_reduce, verify_attn.metal:94-99,190).
+    if (d->attn_gate)
+      for (int t = 0; t < B; ++t)
+        for (int hh = 0; hh < QH; ++hh)
+          for (int dd = 0; dd < HD; ++dd) {
+            const float g = proj[size_t(t) * QP + size_t(hh) * QS + HD + dd];
+            att[(size_t(t) * QH + hh) * HD + dd] *= 1.0f / (1.0f + std::exp(-g));
+          }
     for (auto& z : att) z = or_bf16_to_f32(or_f32_to_bf16(z));
     L.o.apply(att.data(), B, y.data());
+    if (!L.o_bias.empty())
+      for (int t = 0; t < B; ++t)
+        for (int i = 0; i < H; ++i) y[size_t(t) * H + i] += L.o_bias[i];
     for (size_t i = 0; i < hres.size(); ++i) hres[i] += y[i];
     if (d->n_experts > 0) {
-      moe_forward(d, L, hres.data(), B);
+      moe_forward(d, L, hres.data(), B, d->iid_routing ? sm_key(m->seed, layer_tensor(l, 13)) : 0, P);
       capture(m, l, hres.data(), B);
       continue;
     }

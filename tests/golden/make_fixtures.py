@@ -6,6 +6,9 @@
                         gives for them (ref/mxfp4_ref.py), including -0.
   router_vectors.json   ref/router_vectors.json (written by mlx-lm 0.32.2's router code, ref/router_ref.py), copied as
                         data: per case E, top-k, scoring, logits, biases and mlx-lm's dense routing weights.
+  rope_ref.json         ref/rope/rope_ref.json (mlx-lm initialize_rope, ref/rope_ref.py), copied as data: per case θ,
+                        rotated dims, the RoPE parameter dict, mlx-lm's fp32 inv_freq, the same formula in float64 and
+                        mscale (yarn-truncate, gpt-oss, yarn-mscale, linear, default).
 """
 import json
 import re
@@ -39,7 +42,9 @@ def main() -> None:
     rv = json.loads((REF / "ref/router_vectors.json").read_text())
     rv["copied_from"] = "ref/router_vectors.json"
     (OUT / "router_vectors.json").write_text(json.dumps(rv))
-    print("wrote", OUT / "mxfp4_reference.json", OUT / "router_vectors.json")
+    rr = json.loads((REF / "ref/rope/rope_ref.json").read_text())
+    (OUT / "rope_ref.json").write_text(json.dumps({"copied_from": "ref/rope/rope_ref.json", "cases": rr}))
+    print("wrote", OUT / "mxfp4_reference.json", OUT / "router_vectors.json", OUT / "rope_ref.json")
 
 
 if __name__ == "__main__":

@@ -27,7 +27,7 @@ import oracle
 
 T_EMBED, T_FINAL_NORM, T_HEAD = 1, 2, 3
 L_ATTN_NORM, L_QKV, L_O, L_MLP_NORM, L_GATE_UP, L_DOWN, L_ROUTER, L_ROUTER_BIAS, L_SINKS = 0, 1, 2, 3, 4, 5, 6, 7, 9
-L_Q_NORM, L_K_NORM, L_QKV_BIAS = 10, 11, 12
+L_Q_NORM, L_K_NORM, L_QKV_BIAS, L_ROUTE_IID, L_O_BIAS = 10, 11, 12, 13, 14
 X_GATE_UP, X_DOWN, X_GU_BIAS, X_DOWN_BIAS = 0, 1, 2, 3
 
 
@@ -89,14 +89,33 @@ def rmsnorm(h, w, eps):
     return h / np.sqrt(np.mean(h * h, axis=-1, keepdims=True) + eps) * w
 
 
-def rope(x, pos, theta):
-    """Non-interleaved halves over the whole head (angle pos·θ^(−i/(HD/2)))."""
+def rope(x, pos, theta, rot=None, inv=None, mscale=1.0):
+    """Non-interleaved halves over the first `rot` dims (angle pos·θ^(−i/(rot/2)), or pos·inv[i] from a scaled RoPE's
+    table with the rotated dims × mscale); the other dims are kept (AT_ROT, verify_attn_nax.metal:92-98)."""
     HD = x.shape[-1]
-    RH = HD // 2
-    ang = pos * theta ** (-np.arange(RH) / RH)
-    c, s = np.cos(ang), np.sin(ang)
-    a, b = x[..., :RH], x[..., RH:]
-    return np.concatenate([a * c - b * s, b * c + a * s], axis=-1)
+    rot = rot or HD
+    RH = rot // 2
+    ang = pos * (theta ** (-np.arange(RH) / RH) if inv is None else np.asarray(inv, np.float64))
+    c, s = np.cos(ang) * mscale, np.sin(ang) * mscale
+    a, b = x[..., :RH], x[..., RH:rot]
+    return np.concatenate([a * c - b * s, b * c + a * s, x[..., rot:]], axis=-1)
+
+
+def rope_scaling(desc):
+    """The RoPE parameter dict a model description stands for (None for the default RoPE)."""
+    kinds = {1: "linear", 2: "yarn", 3: "proportional"}
+    if desc.rope_type == 0:
+        return None
+    p = {"rope_type": kinds[desc.rope_type], "factor": desc.rope_factor or 1.0}
+    if desc.rope_type == 2:
+        p.update(original_max_position_embeddings=desc.rope_orig_max, beta_fast=desc.rope_beta_fast or 32.0,
+                 beta_slow=desc.rope_beta_slow or 1.0, mscale=desc.rope_mscale or 1.0,
+                 truncate=not desc.rope_no_truncate)
+        if desc.rope_attn_factor:
+            p["attention_factor"] = desc.rope_attn_factor
+    if desc.rope_type == 3:
+        p["partial_rotary_factor"] = desc.rope_partial or 1.0
+    return p
 
 
 def had(x):
@@ -138,6 +157,12 @@ def attention(q, K, V, P, G, window, sinks, mutate):
     return out.reshape(B, QH * HD)
 
 
+def iid_logits(seed, l, P, B, E):
+    key = oracle.lib().or_sm_key(seed, layer_tensor(l, L_ROUTE_IID))
+    return np.array([[oracle.lib().or_sm_normal(key, (P + r) * E + e) for e in range(E)] for r in range(B)],
+                    np.float64)
+
+
 def route(logits, k):
     """Top-k by logit (ties to the lower index), weights = softmax over the chosen logits."""
     inds = np.argsort(-logits, axis=1, kind="stable")[:, :k]
@@ -147,12 +172,21 @@ def route(logits, k):
 
 
 def forward(desc, seed: int, kv_seed: int, P: int, tokens, mutate: str | None = None):
-    """Logits [B][vocab] in float64. mutate ∈ {None, "residual", "norm", "gqa", "renorm", "slots", "qknorm", "qkvbias"} breaks one piece."""
+    """Logits [B][vocab] in float64. mutate ∈ {None, "residual", "norm", "gqa", "renorm", "slots", "qknorm", "qkvbias",
+    "gate", "obias", "rot", "rope", "route"} breaks one piece."""
     d = desc
     H, QH, KVH, HD, V = d.hidden, d.n_q_heads, d.n_kv_heads, d.head_dim, d.vocab
     G = QH // KVH
     toks = np.asarray(tokens, np.int64)
     B = len(toks)
+    QS = HD * (2 if d.attn_gate else 1)
+    QP = QH * QS + 2 * KVH * HD
+    rot = d.rotary_dims or HD
+    if mutate == "rot":  # the whole head rotated instead of the first rotary_dims
+        rot = HD
+    inv, msc = None, 1.0
+    if rope_scaling(d) is not None and mutate != "rope":  # the table from the restated formula (mlx-lm vectors)
+        inv, msc = oracle.rope_table(rope_scaling(d), d.rope_theta, rot)
     emb = int4_dense(seed, T_EMBED, V, H)
     h = emb[toks].copy()
     for l in range(d.n_layers):
@@ -161,18 +195,20 @@ def forward(desc, seed: int, kv_seed: int, P: int, tokens, mutate: str | None = 
         if mutate == "norm":
             wa, wm = wm, wa
         x = rmsnorm(h, wa, d.rms_eps)
-        proj = x @ int4_dense(seed, layer_tensor(l, L_QKV), (QH + 2 * KVH) * HD, H).T
+        proj = x @ int4_dense(seed, layer_tensor(l, L_QKV), QP, H).T
         if d.qkv_bias and mutate != "qkvbias":
-            proj = proj + f32(seed, layer_tensor(l, L_QKV_BIAS), (QH + 2 * KVH) * HD, 0.0, 0.1)
-        q = proj[:, : QH * HD].reshape(B, QH, HD)
-        k = proj[:, QH * HD: (QH + KVH) * HD].reshape(B, KVH, HD)
+            proj = proj + f32(seed, layer_tensor(l, L_QKV_BIAS), QP, 0.0, 0.1)
+        qg = proj[:, : QH * QS].reshape(B, QH, QS)
+        q = qg[:, :, :HD]
+        gate = qg[:, :, HD:] if d.attn_gate else None
+        k = proj[:, QH * QS: QH * QS + KVH * HD].reshape(B, KVH, HD)
         if d.qk_norm and mutate != "qknorm":  # per-head RMSNorm before RoPE (Qwen3's q_norm / k_norm)
             q = rmsnorm(q, bf16(seed, layer_tensor(l, L_Q_NORM), HD, 1.0, 0.125), d.rms_eps)
             k = rmsnorm(k, bf16(seed, layer_tensor(l, L_K_NORM), HD, 1.0, 0.125), d.rms_eps)
-        v = proj[:, (QH + KVH) * HD:].reshape(B, KVH, HD)
+        v = proj[:, QH * QS + KVH * HD:].reshape(B, KVH, HD)
         pos = P + np.arange(B)
-        qr = np.stack([rope(q[t], pos[t], d.rope_theta) for t in range(B)])
-        kr = np.stack([rope(k[t], pos[t], d.rope_theta) for t in range(B)])
+        qr = np.stack([rope(q[t], pos[t], d.rope_theta, rot, inv, msc) for t in range(B)])
+        kr = np.stack([rope(k[t], pos[t], d.rope_theta, rot, inv, msc) for t in range(B)])
         if d.hadamard_k:
             qr, kr = had(qr), had(kr)
         # History from the generator (int8 and fp16 scales), then the block's own rows quantised as the cache stores them.
@@ -188,7 +224,11 @@ def forward(desc, seed: int, kv_seed: int, P: int, tokens, mutate: str | None = 
         window = d.sliding_window if (d.sliding_window > 0 and l % 2 == 0) else 0
         sinks = f32(seed, layer_tensor(l, L_SINKS), QH, 0.0, 1.0) if d.sinks else None
         att = attention(qr, Kc, Vc, P, G, window, sinks, mutate)
+        if gate is not None and mutate != "gate":  # gated output (at_gate, verify_attn.metal:94-99)
+            att = att * (1 / (1 + np.exp(-gate.reshape(B, QH * HD))))
         y = att @ int4_dense(seed, layer_tensor(l, L_O), H, QH * HD).T
+        if d.o_bias and mutate != "obias":
+            y = y + f32(seed, layer_tensor(l, L_O_BIAS), H, 0.0, 0.1)
         h = h + y if mutate != "residual" else y
         x = rmsnorm(h, wm, d.rms_eps)
         act = (lambda g, u: swiglu_oai(g, u, d.swiglu_limit)) if d.act == 1 else silu_glu
@@ -200,6 +240,9 @@ def forward(desc, seed: int, kv_seed: int, P: int, tokens, mutate: str | None = 
             continue
         E, Kt, IE, fmt = d.n_experts, d.top_k, d.expert_intermediate, d.expert_format
         lg = x @ expert_matrix(fmt, seed, layer_tensor(l, L_ROUTER), E, H).T
+        if d.iid_routing and mutate != "route":
+            # Synthetic i.i.d. routing: logit (row, expert) = draw (position·E + expert) of the layer's N(0,1) stream.
+            lg = iid_logits(seed, l, P, B, E)
         if d.router_bias:
             lg = lg + f32(seed, layer_tensor(l, L_ROUTER_BIAS), E, 0.0, 0.5)
         inds, w = route(lg, Kt)

@@ -16,17 +16,18 @@ import numpy as np
 import pytest
 
 import oracle
-from ingot_amd._lib import KVCache, Model, ModelDesc, accept
+from ingot_amd._lib import KVCache, Model, ModelDesc, accept, check, lib
 from synth import cosine
 
 pytestmark = pytest.mark.gpu
 
 DENSE8B = dict(n_layers=32, hidden=4096, n_q_heads=32, n_kv_heads=8, head_dim=128, intermediate=14336, vocab=151936)
+# The MoE configurations' routing: router logits ~N(0,1) per layer and row (iid_routing), U ≈ 85 of 128 / ≈ 22 of 32.
 MOE3 = dict(n_layers=2, hidden=2048, n_q_heads=32, n_kv_heads=4, head_dim=128, intermediate=0, vocab=151936,
-            n_experts=128, top_k=8, expert_intermediate=768, expert_format=0)
+            n_experts=128, top_k=8, expert_intermediate=768, expert_format=0, iid_routing=1)
 MOE4 = dict(n_layers=2, hidden=2880, n_q_heads=64, n_kv_heads=8, head_dim=64, intermediate=0, vocab=201088,
             n_experts=32, top_k=4, expert_intermediate=2880, expert_format=1, router_bias=1, expert_bias=1, act=1,
-            sinks=1, sliding_window=128)
+            sinks=1, sliding_window=128, iid_routing=1)
 CASES = {
     "cfg1-dense8b-P8192": (DENSE8B, 8192, 17),
     "cfg2-dense8b-P32768": (DENSE8B, 32768, 17),
@@ -38,9 +39,25 @@ SEED, KV_SEED = 2026, 11
 # Logits tolerance. Dense: max-abs ≤ 1% of max |ref| and cosine ≥ 0.9999. Both sides round the activations to bf16
 # at the same points, so the difference is the occasional one-ulp flip of a bf16 (2^-8 relative) or of an int8 KV
 # level where the pre-rounding values differ in the last fp32 bits; at config 1's logit scale (~70) one bf16 ulp of a
-# logit is 0.25–0.5. MoE: the softmax router turns such flips into changed expert weights (and near a tie into a
-# changed expert), measured as up to 3% of the scale on the small MoE models; cosine ≥ 0.999.
-TOL = {"dense": (0.01, 0.9999), "moe": (0.03, 0.999)}
+# logit is 0.25–0.5.
+# MoE (the configurations' i.i.d. routing, identical on both sides): cosine ≥ 0.9999 and max-abs ≤ 1e-3 of the scale
+# or, where the function itself is less well conditioned than that, 1.5 × how far the oracle's own logits move when
+# RoPE θ changes by one part in 10^7 (which flips the same kind of last-bit roundings). Config 4's MXFP4 experts
+# (weights up to 1.5 over 2880 inputs) move the oracle by 3–5e-3 of the scale that way; config 3's by ~5e-4.
+TOL = {"dense": (0.01, 0.9999), "moe": (1e-3, 0.9999)}
+
+
+def oracle_sensitivity(d, shape, P, toks, ref_logits):
+    """Max-abs change of the oracle's logits under RoPE θ·(1 ± 1e-7)."""
+    sens = 0.0
+    for eps in (1e-7, -1e-7):
+        alt = ModelDesc.make(**shape)
+        alt.rope_theta = d.rope_theta * (1 + eps)
+        om = oracle.OracleModel(alt, SEED, KV_SEED, P)
+        other, _ = om.verify(toks)
+        om.free()
+        sens = max(sens, float(np.abs(other - ref_logits).max()))
+    return sens
 
 
 def report(name, **kv):
@@ -63,6 +80,11 @@ def test_fullsize_verify_matches_oracle(ctx, name):
         kv.fill_synthetic(P, KV_SEED)
         toks = np.random.default_rng(P + B).integers(0, d.vocab, size=B).astype(np.uint32)
         top1, logits = kv.verify(toks, want_logits=True)
+        union = None
+        if shape.get("n_experts"):
+            u = np.zeros(d.n_layers, np.int32)
+            check(lib().ih_model_moe_union(m.handle, u.ctypes.data))
+            union = u.tolist()
         t0 = time.time()
         om = oracle.OracleModel(d, SEED, KV_SEED, P)
         t1 = time.time()
@@ -78,10 +100,15 @@ def test_fullsize_verify_matches_oracle(ctx, name):
         near_ties = int(np.sum(~sure))
         near_tie_flips = int(np.sum(top1[~sure] != ref_top1[~sure]))
         report(name, max_abs=err, rel=err / scale, cosine=cos, scale=scale, near_tie_rows=near_ties,
-               near_tie_flips=near_tie_flips, flips=flips, oracle_build_s=round(t1 - t0, 2),
+               near_tie_flips=near_tie_flips, flips=flips, moe_union=union, oracle_build_s=round(t1 - t0, 2),
                oracle_step_s=round(t2 - t1, 2), top1=top1.tolist(), ref_top1=ref_top1.tolist())
         rel_tol, cos_tol = TOL["moe" if shape.get("n_experts") else "dense"]
-        assert err <= rel_tol * scale and cos >= cos_tol, (err, scale, cos)
+        bound = rel_tol * scale
+        if shape.get("n_experts"):
+            sens = oracle_sensitivity(d, shape, P, toks, ref_logits)
+            report(name + " conditioning", oracle_sensitivity=sens, rel_sensitivity=sens / scale)
+            bound = max(bound, 1.5 * sens)
+        assert err <= bound and cos >= cos_tol, (err, bound, scale, cos)
         if not shape.get("n_experts"):
             # The north star's example bound for the dense configurations: max-abs ≤ 2e-2 against the fp32 oracle
             # (measured 0.009–0.013 at logit scale ~70).
@@ -107,7 +134,8 @@ def test_fullsize_verify_matches_oracle(ctx, name):
         first_tie = int(np.argmax(tie)) if tie.any() else B
         assert np.array_equal(gt[~tie], ot[~tie])
         gm, om_m = accept(blk, gt).m, oracle.accept(blk, ot)[0]
-        report(name + " chain", block_max_abs=berr, near_tie_rows=tie.nonzero()[0].tolist(), gpu_m=gm, oracle_m=om_m)
+        report(name + " chain", block_max_abs=berr, near_tie_rows=tie.nonzero()[0].tolist(), gpu_m=gm, oracle_m=om_m,
+               distinct_tokens=len(set(blk.tolist())), chain=blk.tolist())
         assert gm == B - 1
         assert om_m == B - 1 or om_m >= first_tie
         L = B // 3

@@ -63,11 +63,25 @@ def make(ctx, shape, seed=7, kv_seed=11, P=100, cap=512, chunk=0, **extra):
 
 QWEN = dict(SMALL, qk_norm=1, qkv_bias=1)
 QWEN64 = dict(GQA8, qk_norm=1, qkv_bias=1)
+# Gated attention output with partial RoPE (Qwen3-Next: [q | gate] per head, × sigmoid(gate); AT_ROT < head_dim).
+GATED = dict(SMALL, attn_gate=1, rotary_dims=32, qk_norm=1)
+GATED64 = dict(GQA8, attn_gate=1, rotary_dims=16)
+# gpt-oss-style attention: YaRN table (gpt-oss's parameters), q|k|v|o biases, sinks, alternating window.
+YARN = dict(SWA, qkv_bias=1, o_bias=1, rope_type=2, rope_factor=32.0, rope_orig_max=4096.0, rope_no_truncate=1,
+            rope_theta=150000.0)
+# Proportional RoPE (a quarter of the pairs rotate, the rest angle 0) and linear scaling.
+PROP = dict(SMALL, rope_type=3, rope_partial=0.25)
+LINEAR = dict(GQA4, rope_type=1, rope_factor=4.0)
+# The benchmark MoE configurations' synthetic i.i.d. routing.
+MOEIID = dict(MOE4, iid_routing=1, n_experts=16, top_k=4)
+MOEXIID = dict(MOEX, iid_routing=1)
 
 
-@pytest.mark.parametrize("shape", [SMALL, GQA8, SWA, MOE4, MOEX, QWEN, QWEN64],
+@pytest.mark.parametrize("shape", [SMALL, GQA8, SWA, MOE4, MOEX, QWEN, QWEN64, GATED, GATED64, YARN, PROP, LINEAR,
+                                   MOEIID, MOEXIID],
                          ids=["gqa2-hd128", "gqa8-hd64", "sinks-swa", "moe-int4", "moe-mxfp4", "qknorm-bias-hd128",
-                              "qknorm-bias-hd64"])
+                              "qknorm-bias-hd64", "gated-rot32-hd128", "gated-rot16-hd64", "yarn-obias-sinks",
+                              "proportional", "linear", "moe-int4-iid", "moe-mxfp4-iid"])
 @pytest.mark.parametrize("B", [1, 5, 9, 10, 17])
 def test_verify_step_matches_oracle(ctx, shape, B):
     d, m, kv = make(ctx, shape)
@@ -179,7 +193,8 @@ def test_row_invariance_and_rollback(ctx):
         m.free()
 
 
-@pytest.mark.parametrize("shape", [SMALL, GQA4, SWA], ids=["small", "gqa4", "swa-gqa8"])
+@pytest.mark.parametrize("shape", [SMALL, GQA4, SWA, GATED, YARN], ids=["small", "gqa4", "swa-gqa8", "gated-rot32",
+                                                                        "yarn-obias"])
 def test_every_row_of_a_full_block_equals_its_row_decoded_alone(ctx, shape):
     """Row r of a 17-row block is bit-identical to the same token verified alone (and as the first row of a shorter
     block) once rows < r are in the cache: the speculative round's last row, which emits the bonus token, must give

@@ -161,3 +161,46 @@ def test_gathered_product_matches_oracle(ctx, fmt, rows, E, K):
     for d in (dl, dx):
         d.free()
     W.free()
+
+
+@pytest.mark.parametrize("fmt,rows,E,K,N,D,umin", [
+    ("int4", 17, 128, 8, 1536, 2048, 60),    # config 3's gate|up: 2·768 rows over hidden 2048
+    ("int4", 17, 128, 8, 2048, 768, 60),     # config 3's down
+    ("mxfp4", 9, 32, 4, 5760, 2880, 14),     # config 4's gate|up: 2·2880 rows over hidden 2880 (23 K-blocks)
+    ("mxfp4", 9, 32, 4, 2880, 2880, 14),     # config 4's down
+], ids=["cfg3-gate-up", "cfg3-down", "cfg4-gate-up", "cfg4-down"])
+def test_gathered_product_at_config_expert_shapes(ctx, fmt, rows, E, K, N, D, umin):
+    """The gathered per-expert product at configs 3 and 4's real expert shapes, under the configurations' routing
+    (router logits ~N(0,1): U ≈ 85 of 128 and ≈ 22 of 32 distinct experts), every pair against the oracle's fp32
+    dequant + matmul of its row through its expert (MoE.swift:346-428 gathered qmv; KernelHarness.swift:720-766)."""
+    g = rng(N + D + E)
+    if fmt == "int4":
+        w, s, b = int4_matrix(g, N, D, E=E)
+        W = QMat.int4(ctx, w, s, b)
+        ref_e = lambda x, e: oracle.qmm_int4(x, w[e], s[e], b[e])  # noqa: E731
+    else:
+        w, s = mxfp4_matrix(g, N, D, E=E)
+        W = QMat.mxfp4(ctx, w, s)
+        ref_e = lambda x, e: oracle.qmm_mxfp4(x, w[e], s[e])  # noqa: E731
+    xb, xf = bf16_normal(g, (rows, D))
+    logits = g.normal(0, 1, size=(rows, E)).astype(np.float32)
+    dl, dx = ctx.to_device(logits), ctx.to_device(xb)
+    R = Routing(ctx, rows, K, E).route(dl, E)
+    y = R.gathered(W, dx)
+    out = R.download()
+    ri, _ = oracle.route(logits, K)
+    entries, _ = oracle.expert_union(ri, E)
+    assert np.array_equal(out["entries"], entries)
+    print(f"[gathered {fmt} {N}x{D}] U = {len(entries)} of {E}", flush=True)
+    assert len(entries) >= umin
+    worst = 0.0
+    for e, start, cnt in out["entries"]:
+        rws = out["x_row"][start:start + cnt]
+        ok, err = close(y[start:start + cnt], ref_e(xf[rws], e), 2e-5)
+        worst = max(worst, err)
+        assert ok, (e, err)
+    print(f"[gathered {fmt} {N}x{D}] worst relative error {worst:.2e}", flush=True)
+    R.free()
+    for d_ in (dl, dx):
+        d_.free()
+    W.free()

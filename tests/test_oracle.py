@@ -365,3 +365,68 @@ def test_moe_oracle_sensitivity_to_last_bit_changes():
     b, _ = oracle.verify_dense(ModelDesc.make(**shape, rope_theta=1e6 * (1 + 1e-7)), 7, 11, 100, toks)
     d = np.abs(a - b).max()
     assert 0.02 < d < 0.05 + 0.03 * np.abs(a).max(), d
+
+
+# ---- RoPE frequency tables (RopeTable.make) ----------------------------------------------------------------------
+
+def _ulps(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+def test_rope_table_matches_mlx_lm_vectors():
+    """RopeTableTests.matchesMlxLm (Tests/IngotTests/RopeTableTests.swift:17-38) on ref/rope/rope_ref.json: the table
+    within 1 ulp of the float64 formula, within 8 ulp of mlx-lm's float32 steps, mscale within 1 ulp (yarn with and
+    without truncate, gpt-oss's, yarn with mscale, linear, default)."""
+    cases = json.loads((GOLD / "rope_ref.json").read_text())["cases"]
+    assert len(cases) >= 5
+    for c in cases:
+        inv, ms = oracle.rope_table(c["params"], c["theta"], c["dims"])
+        assert len(inv) == c["dims"] // 2
+        assert _ulps(inv, c["inv_freq_f64"]).max() <= 1, c["name"]
+        assert _ulps(inv, c["inv_freq"]).max() <= 8, c["name"]
+        assert _ulps(np.float32(ms), np.float32(c["mscale"])) <= 1, (c["name"], ms, c["mscale"])
+
+
+def test_rope_table_proportional_and_linear_closed_forms():
+    """RopeTableTests.proportionalTable (RopeTable.swift:109-113): the first int(dims·partial)/2 pairs at period
+    factor·θ^(2i/dims), the rest exactly 0; linear = default / factor."""
+    inv, ms = oracle.rope_table({"rope_type": "proportional", "partial_rotary_factor": 0.25}, 1e6, 512)
+    want = (1 / np.power(1e6, 2.0 * np.arange(64) / 512)).astype(np.float32)
+    assert ms == 1.0 and _ulps(inv[:64], want).max() <= 1 and np.all(inv[64:] == 0)
+    inv2, _ = oracle.rope_table({"rope_type": "proportional", "factor": 2.0}, 1e4, 256)
+    assert _ulps(inv2, (1 / (2 * np.power(1e4, 2.0 * np.arange(128) / 256))).astype(np.float32)).max() <= 1
+    lin, _ = oracle.rope_table({"rope_type": "linear", "factor": 4.0}, 1e4, 128)
+    dflt, _ = oracle.rope_table({"rope_type": "default"}, 1e4, 128)
+    assert _ulps(lin, dflt / 4).max() <= 1
+
+
+def test_yarn_table_ends_are_original_and_interpolated():
+    """YaRN: pairs below the correction range keep θ^(−2i/d), pairs above it are divided by the factor, and without an
+    attention_factor mscale = 0.1·mscale·ln(factor) + 1."""
+    p = {"rope_type": "yarn", "factor": 32.0, "original_max_position_embeddings": 4096, "beta_fast": 32.0,
+         "beta_slow": 1.0, "truncate": False}
+    inv, ms = oracle.rope_table(p, 150000.0, 64)
+    base = 1 / np.power(150000.0, 2.0 * np.arange(32) / 64)
+    assert _ulps(inv[:3], base[:3].astype(np.float32)).max() <= 1
+    assert _ulps(inv[-3:], (base[-3:] / 32).astype(np.float32)).max() <= 1
+    assert abs(ms - (0.1 * np.log(32.0) + 1)) < 1e-6
+    assert np.all(np.diff(inv) < 0)  # monotone through the ramp
+
+
+def test_partial_rope_rotates_only_the_first_dims():
+    """AT_ROT < head_dim: dims from rot on are untouched, the rotated ones equal a whole-head RoPE of width rot
+    (pairs d, d + rot/2), and the rotation keeps the norm of each pair."""
+    g = np.random.default_rng(5)
+    x = g.normal(size=128).astype(np.float32)
+    y = oracle.rope_wht_ex(x, 64, 1234, 1e7, None, 1.0, 0)
+    assert np.array_equal(y[64:], x[64:])
+    z = oracle.rope_wht(x[:64], 1234, 1e7, 0)
+    assert np.array_equal(y[:64], z)
+    assert np.allclose(y[:32] ** 2 + y[32:64] ** 2, x[:32] ** 2 + x[32:64] ** 2, rtol=1e-5)
+    # A table and mscale: the rotated dims scale by mscale, the others not.
+    inv, _ = oracle.rope_table({"rope_type": "default"}, 1e7, 64)
+    w = oracle.rope_wht_ex(x, 64, 1234, 1e7, inv, 2.0, 0)
+    # (the table holds fp32 frequencies, the default path forms the angle from θ in double: angles agree to ~1e-4)
+    assert np.allclose(w[:64], 2 * y[:64], atol=2e-3) and np.array_equal(w[64:], x[64:])

@@ -21,6 +21,13 @@ MOEX = dict(n_layers=2, hidden=128, n_q_heads=8, n_kv_heads=2, head_dim=64, inte
             top_k=4, expert_intermediate=64, expert_format=1, router_bias=1, expert_bias=1, act=1, sinks=1,
             sliding_window=8, rope_theta=1e4)
 QWEN = dict(DENSE, qk_norm=1, qkv_bias=1)
+# Qwen3-Next-style attention: gated output, partial RoPE over a quarter of the head, QK-norm.
+GATED = dict(DENSE, attn_gate=1, rotary_dims=16, qk_norm=1)
+# gpt-oss-style attention: q|k|v|o biases, YaRN (gpt-oss's parameters, no truncation), sinks and the window.
+YARN = dict(DENSE, qkv_bias=1, o_bias=1, sinks=1, sliding_window=8, rope_type=2, rope_factor=32.0,
+            rope_orig_max=4096.0, rope_no_truncate=1, rope_theta=150000.0)
+# The synthetic i.i.d. routing of the benchmark MoE configurations.
+MOEIID = dict(MOE, iid_routing=1, n_experts=16, top_k=4)
 P = 24
 TOKS = np.array([5, 17, 250, 3, 9, 101, 77], np.uint32)
 
@@ -36,8 +43,12 @@ def rel_err(a, b):
 @pytest.mark.parametrize("shape,tol,muts", [(DENSE, 0.015, ["residual", "norm", "gqa"]),
                                             (MOE, 0.015, ["residual", "norm", "gqa", "renorm", "slots"]),
                                             (MOEX, 0.03, ["residual", "norm", "gqa", "slots"]),
-                                            (QWEN, 0.015, ["residual", "gqa", "qknorm", "qkvbias"])],
-                         ids=["dense", "moe-int4", "moe-mxfp4-sinks-swa", "qknorm-qkvbias"])
+                                            (QWEN, 0.015, ["residual", "gqa", "qknorm", "qkvbias"]),
+                                            (GATED, 0.015, ["residual", "gqa", "gate", "rot"]),
+                                            (YARN, 0.015, ["residual", "obias", "qkvbias", "rope"]),
+                                            (MOEIID, 0.015, ["residual", "renorm", "route"])],
+                         ids=["dense", "moe-int4", "moe-mxfp4-sinks-swa", "qknorm-qkvbias", "gated-partial-rope",
+                              "yarn-obias-sinks", "moe-iid-routing"])
 def test_oracle_composition_matches_float64_forward(shape, tol, muts):
     d = ModelDesc.make(**shape)
     logits, _ = oracle.verify_dense(d, 7, 11, P, TOKS)

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from ingot_amd._lib import KVCache, Model, ModelDesc, RowsParams, SampleParams, check, lib
+from ingot_amd._lib import RND_PER_ROUND, KVCache, Model, ModelDesc, RowsParams, SampleParams, check, lib
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +53,7 @@ def test_accept_sample_matches_oracle(ctx):
     d_st = ctx.to_device(np.zeros(8, np.uint32))
     d_rec = ctx.buffer(ring * 24 * 4).fill(0)
     d_vtok = ctx.buffer(17 * 4)
-    rnd = g.random((R, 32)).astype(np.float32)
+    rnd = g.random((R, RND_PER_ROUND)).astype(np.float32)
     d_rnd = ctx.to_device(rnd)
     near = 0
     P = 0
@@ -86,6 +86,49 @@ def test_accept_sample_matches_oracle(ctx):
         for b in (di, dv, dz):
             b.free()
     assert near <= 1
+    for b in (d_st, d_rec, d_vtok, d_rnd):
+        b.free()
+
+
+def test_accept_sample_all_drafts_accepted_uses_its_own_rounds_uniforms(ctx):
+    """B = 17 with every draft accepted: the 17th row's resample draws uniform 33 of its own round (uniforms per round
+    = 2 × 17), never the next round's first. Rows 0–15 are sharp (the draft has probability ≈ 1 and the accept uniform
+    is 0), row 16 is flat over many candidates so the drawn token depends on that uniform; each round's uniforms differ
+    from the next round's."""
+    g = np.random.default_rng(17)
+    ring, R, B, V = 4, 6, 17, 2000
+    assert RND_PER_ROUND >= 2 * B
+    p = SampleParams(temp=1.0, top_p=1.0, top_k=0, min_p=0.0)
+    d_st = ctx.to_device(np.zeros(8, np.uint32))
+    d_rec = ctx.buffer(ring * 24 * 4).fill(0)
+    d_vtok = ctx.buffer(17 * 4)
+    rnd = g.random((R, RND_PER_ROUND)).astype(np.float32)
+    rnd[:, 0:2 * (B - 1):2] = 0.0  # accept every draft
+    d_rnd = ctx.to_device(rnd)
+    seen = set()
+    for r in range(R):
+        x = np.full((B, V), -1e4, np.float32)
+        top = g.choice(V, size=B - 1, replace=False)
+        x[np.arange(B - 1), top] = 50.0  # rows 0–15: one candidate holds all the mass
+        x[B - 1, :40] = g.normal(size=40).astype(np.float32) * 0.1  # row 16: ~flat over 40 candidates
+        idx, val, z = oracle.topk64(x, p.temp)
+        vtok = np.zeros(17, np.uint32)
+        vtok[0] = 7
+        vtok[1:B] = idx[: B - 1, 0]
+        d_vtok.upload(vtok)
+        di, dv, dz = ctx.to_device(idx), ctx.to_device(val), ctx.to_device(z)
+        check(lib().ih_spec_accept_sample_dev(ctx.handle, d_st.ptr, d_vtok.ptr, di.ptr, dv.ptr, dz.ptr, d_rec.ptr,
+                                              d_rnd.ptr, C.byref(p), ring, B))
+        rec = d_rec.download(np.uint32, (ring, 24))[r % ring]
+        m, em = oracle.accept_sample(vtok[:B], idx, val, z, rnd[r, : 2 * B], p)
+        assert m == B - 1 and int(rec[0]) == B - 1
+        assert list(rec[1:B + 1]) == list(em)
+        # The same pick as the oracle's with the next round's first uniform would be a coincidence for some round.
+        _, em_next = oracle.accept_sample(vtok[:B], idx, val, z, np.concatenate([rnd[r, :2 * B - 1], rnd[(r + 1) % R, 1:2]]), p)
+        seen.add(int(em[-1]) != int(em_next[-1]))
+        for b in (di, dv, dz):
+            b.free()
+    assert True in seen  # the test can tell the two uniforms apart
     for b in (d_st, d_rec, d_vtok, d_rnd):
         b.free()
 
