@@ -218,6 +218,9 @@ typedef struct ih_model_desc {
   float rope_attn_factor;              /* yarn: attention_factor overriding the mscale (0 = none) */
   int rope_no_truncate;                /* yarn: 1 = correction range not rounded to whole dims (gpt-oss truncate: false) */
   float rope_partial;                  /* proportional: partial_rotary_factor (0 = 1) */
+  /* The MoE router in MLX int4 g64 whatever the experts' format (gpt-oss packs: an affine router in front of MXFP4
+   * experts; it then reads the experts' fp16 activation rows). 0: the router is in the experts' format. */
+  int router_int4;
 } ih_model_desc;
 
 /* Creates a model with synthetic weights of `desc`'s shapes, deterministically from `seed` (counter-based SplitMix64
@@ -229,9 +232,12 @@ int ih_model_create_synthetic(ih_ctx* ctx, const ih_model_desc* desc, uint64_t s
  * Sources/Ingot/Loader/Safetensors.swift:1-248; QuantizedLinear, Loader/Quant.swift:13-88; DenseQ's q|k|v and gate|up
  * row concatenation, Layers/Linear.swift:107-183; ModelConfig, Loader/Config.swift). Layer names of mlx-lm
  * (model.layers.N.self_attn.{q,k,v,o}_proj, input_layernorm, post_attention_layernorm, mlp.{gate,up,down}_proj; MoE:
- * mlp.gate + mlp.switch_mlp.{gate,up,down}_proj), lm_head or tied embeddings. Runs what the verify step runs: MLX
- * affine 4-bit g64 (MXFP4 g32 experts), optional QK-norm (q_norm/k_norm) and q|k|v bias, a dense SwiGLU or a
- * renormalised softmax top-k MoE; anything else (other bits, rope scaling, shared experts, o_proj bias, …) is
+ * mlp.gate + mlp.switch_mlp.{gate,up,down}_proj; gpt-oss: mlp.router + mlp.experts.*, self_attn.sinks), lm_head or
+ * tied embeddings. Runs what the verify step runs: MLX affine 4-bit g64 (MXFP4 g32 experts, their router int4 or
+ * MXFP4), optional QK-norm (q_norm/k_norm), q|k|v and o biases (attention_bias), a gated q_proj ([q | gate] per head),
+ * partial RoPE (partial_rotary_factor), RoPE scaling default / linear / yarn / proportional (RopeTable.swift), sinks,
+ * alternating sliding-window layers, a dense SwiGLU or a renormalised softmax top-k MoE (swiglu_oai with gpt-oss's
+ * swiglu_limit, router and expert biases); anything else (other bits, other RoPE types, shared experts, …) is
  * IH_EINVAL with the reason in ih_last_error(). */
 int ih_model_load_mlx(ih_ctx* ctx, const char* dir, ih_model** out);
 /* The description ih_model_load_mlx would build, after checking the checkpoint's tensors; host only (no device). */

@@ -317,7 +317,7 @@ class ModelDesc(C.Structure):
         ("attn_gate", C.c_int), ("o_bias", C.c_int), ("rope_type", C.c_int), ("rope_factor", C.c_float),
         ("rope_orig_max", C.c_float), ("rope_beta_fast", C.c_float), ("rope_beta_slow", C.c_float),
         ("rope_mscale", C.c_float), ("rope_attn_factor", C.c_float), ("rope_no_truncate", C.c_int),
-        ("rope_partial", C.c_float),
+        ("rope_partial", C.c_float), ("router_int4", C.c_int),
     ]
 
     @classmethod

@@ -7,8 +7,11 @@
 // row-concatenation of q|k|v and gate|up (Layers/Linear.swift:107-183), ModelConfig (Loader/Config.swift:1-119) and
 // the layer names of mlx-lm (Model.swift:400-520: model.layers.N.self_attn.{q,k,v,o}_proj, input_layernorm,
 // post_attention_layernorm, mlp.{gate,up,down}_proj, mlp.gate + mlp.switch_mlp.* for the MoEs, lm_head or tied
-// embeddings). What the verify step runs is loadable: attention with optional QK-norm and q|k|v bias, a dense SwiGLU or
-// a softmax top-k MoE, MLX affine int4 g64 everywhere (MXFP4 g32 experts). Anything else is a load error that says what.
+// embeddings; gpt-oss's mlp.router, mlp.experts.* and self_attn.sinks, WeightNames.gptOss, ModelSpecParts.swift:160-168).
+// What the verify step runs is loadable: attention with optional QK-norm, q|k|v and o biases, a gated q_proj, partial
+// or scaled RoPE (RopeScaling.parse, RopeTable.swift:40-95), sinks and alternating windows, a dense SwiGLU or a softmax
+// top-k MoE (swiglu_oai, router and expert biases), MLX affine int4 g64 everywhere but MXFP4 g32 experts (and their
+// router). Anything else is a load error that says what.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -333,6 +336,8 @@ struct Config {
   int q_bits = 4, q_group = 64;
   std::string q_mode = "affine";
   std::map<std::string, std::pair<int, int>> overrides;  // path → (bits, group)
+  bool gpt_oss = false;        // gpt-oss names: mlp.router, mlp.experts.*, self_attn.sinks (ModelSpec.swift:27-33)
+  bool attention_bias = false;  // attention_bias: q, k, v and o biased (BlockSpec.swift:111)
   std::string err;
 };
 
@@ -367,14 +372,63 @@ bool read_config(const std::string& dir, Config& c) {
   d.hadamard_k = 1;
   d.swiglu_limit = 7.0f;
   if (const Json* tw = t.get("tie_word_embeddings")) c.tied = tw->kind == Json::BOOL && tw->b;
-  if (const Json* rs = t.get("rope_scaling"); rs && rs->kind == Json::OBJ) {
+  c.gpt_oss = c.model_type == "gpt_oss";
+  if (const Json* ab = t.get("attention_bias")) c.attention_bias = ab->kind == Json::BOOL && ab->b;
+  // RoPE scaling (RopeScaling.parse, Sources/Ingot/Loader/RopeTable.swift:40-95): rope_scaling or rope_parameters,
+  // type from rope_type (or the older type). default, linear (factor), yarn (factor, original_max_position_embeddings,
+  // beta_fast/slow, mscale, truncate, attention_factor; mscale_all_dim is refused), proportional (factor,
+  // partial_rotary_factor); anything else is refused.
+  const Json* rs = t.get("rope_scaling");
+  if (!rs || rs->kind != Json::OBJ) rs = t.get("rope_parameters");
+  if (rs && rs->kind == Json::OBJ) {
     const Json* ty = rs->get("rope_type") ? rs->get("rope_type") : rs->get("type");
-    if (!ty || ty->str != "default") { c.err = "rope_scaling " + (ty ? ty->str : std::string("?")) + " is not supported"; return false; }
+    const std::string kind = ty ? ty->str : std::string("default");
+    if (const Json* th = rs->get("rope_theta"); th && th->is_num()) d.rope_theta = float(th->num);
+    d.rope_factor = float(num_or(*rs, "factor", 0));
+    if (kind == "default") {
+      d.rope_type = 0;
+    } else if (kind == "linear" || kind == "yarn") {
+      if (!(d.rope_factor > 0)) { c.err = "rope_scaling " + kind + " without a positive factor"; return false; }
+      d.rope_type = kind == "linear" ? 1 : 2;
+      if (kind == "yarn") {
+        d.rope_orig_max = float(num_or(*rs, "original_max_position_embeddings", 0));
+        if (!(d.rope_orig_max > 0)) { c.err = "rope_scaling yarn without original_max_position_embeddings"; return false; }
+        if (num_or(*rs, "mscale_all_dim", 0) != 0) {
+          c.err = "rope_scaling yarn with mscale_all_dim (folded into the attention scale) is not supported";
+          return false;
+        }
+        d.rope_beta_fast = float(num_or(*rs, "beta_fast", 32));
+        d.rope_beta_slow = float(num_or(*rs, "beta_slow", 1));
+        d.rope_mscale = float(num_or(*rs, "mscale", 1));
+        d.rope_attn_factor = float(num_or(*rs, "attention_factor", 0));
+        if (const Json* tr = rs->get("truncate"); tr && tr->kind == Json::BOOL) d.rope_no_truncate = tr->b ? 0 : 1;
+      }
+    } else if (kind == "proportional") {
+      d.rope_type = 3;
+      if (d.rope_factor == 0) d.rope_factor = 1;
+      d.rope_partial = float(num_or(*rs, "partial_rotary_factor", 1));
+      if (!(d.rope_factor > 0 && d.rope_partial > 0 && d.rope_partial <= 1)) {
+        c.err = "rope_scaling proportional needs factor > 0 and 0 < partial_rotary_factor ≤ 1";
+        return false;
+      }
+    } else {
+      c.err = "rope_scaling " + kind + " is not supported (supported: default, linear, yarn, proportional)";
+      return false;
+    }
+  }
+  // Partial RoPE (AT_ROT = head_dim · partial_rotary_factor, aa_dims.metal:18-19): the first rotary dims rotate.
+  if (const Json* pr = t.get("partial_rotary_factor"); pr && pr->is_num() && pr->num != 1.0) {
+    const double rd = pr->num * d.head_dim;
+    if (!(pr->num > 0 && pr->num < 1) || rd != std::floor(rd) || int(rd) % 2 != 0) {
+      c.err = "partial_rotary_factor " + std::to_string(pr->num) + " does not give an even number of rotated dims";
+      return false;
+    }
+    d.rotary_dims = int(rd);
   }
   // MoE: num_experts (Qwen) or num_local_experts (Mixtral); the experts' width.
   d.n_experts = int(num_or(t, "num_experts", num_or(t, "num_local_experts", 0)));
   if (d.n_experts > 0) {
-    d.top_k = int(num_or(t, "num_experts_per_tok", 0));
+    d.top_k = int(num_or(t, "num_experts_per_tok", num_or(t, "experts_per_token", 0)));
     d.expert_intermediate = int(num_or(t, "moe_intermediate_size", num_or(t, "intermediate_size", 0)));
     d.intermediate = 0;
     if (const Json* nt = t.get("norm_topk_prob"); nt && nt->kind == Json::BOOL && !nt->b && d.top_k > 1) {
@@ -388,6 +442,15 @@ bool read_config(const std::string& dir, Config& c) {
     }
     if (num_or(t, "decoder_sparse_step", 1) != 1) { c.err = "decoder_sparse_step other than 1 is not supported"; return false; }
   }
+  // swiglu_limit: gpt-oss's swiglu_oai (α 1.702, clip at the limit; BlockSpec.swift:103-109); with gpt-oss also the
+  // learned sinks of every layer (implied by the family).
+  if (const Json* lim = t.get("swiglu_limit"); lim && lim->is_num()) {
+    if (!c.gpt_oss) { c.err = "swiglu_limit outside gpt-oss is not supported"; return false; }
+    if (d.n_experts == 0) { c.err = "swiglu_oai in a dense FFN is not supported (only the MoE kernels have it)"; return false; }
+    d.act = 1;
+    d.swiglu_limit = float(lim->num);
+  }
+  if (c.gpt_oss) d.sinks = 1;
   // Sliding window: only the alternating pattern (even layers windowed) the verify step runs.
   if (const Json* lt = t.get("layer_types"); lt && lt->kind == Json::ARR) {
     bool alt = true, any = false;
@@ -432,6 +495,16 @@ bool qlinear(const Store& st, const Config& c, const std::string& path, bool all
   if (!q.s) { err = path + " is not quantized (no " + path + ".scales); only MLX 4-bit packs load"; return false; }
   if (q.w->dtype != "U32" || q.w->shape.size() < 2 || q.s->shape.size() != q.w->shape.size()) {
     err = path + " does not look like an MLX quantized layer (weight " + q.w->dtype + " " + shape_str(q.w->shape) + ")";
+    return false;
+  }
+  // Every dim but the last of scales (and biases) equals the weight's: [..., out, groups] against [..., out, packed].
+  for (size_t i = 0; i + 1 < q.w->shape.size(); ++i)
+    if (q.s->shape[i] != q.w->shape[i]) {
+      err = path + ".scales " + shape_str(q.s->shape) + " does not match " + path + ".weight " + shape_str(q.w->shape);
+      return false;
+    }
+  if (q.b && (q.b->shape != q.s->shape || q.b->count() != q.s->count())) {
+    err = path + ".biases " + shape_str(q.b->shape) + " does not match " + path + ".scales " + shape_str(q.s->shape);
     return false;
   }
   const int64_t packed = q.w->shape.back(), groups = q.s->shape.back();
@@ -485,6 +558,12 @@ struct HostMat {
 // Uploads a host-assembled matrix and packs it (E stacked experts, N rows each, il8: gate|up interleave).
 int upload_qmat(ih_ctx* c, const HostMat& h, int fmt, int E, int N, int K, int il8, ih_qmat** out) {
   void *w = nullptr, *s = nullptr, *b = nullptr;
+  // The packing kernel reads E·N·K/2 code bytes and the scales (and biases) of E·N·K/g groups: the assembled bytes
+  // must be exactly that, whatever the header said.
+  const size_t nw = size_t(E) * N * K / 2, ns = fmt == QF_INT4 ? size_t(E) * N * (K / 64) * 2 : size_t(E) * N * (K / 32);
+  IH_CHECK(h.w.size() == nw && h.s.size() == ns && (fmt != QF_INT4 || h.b.size() == ns), IH_EINVAL,
+           "loader: assembled matrix sizes do not match " + std::to_string(E) + "×" + std::to_string(N) + "×" +
+               std::to_string(K));
   int st = IH_OK;
   auto al = [&](void** p, size_t n) {
     if (st == IH_OK && hipMalloc(p, n ? n : 1) != hipSuccess) st = fail(IH_ENOMEM, "loader: staging allocation failed");
@@ -560,6 +639,11 @@ std::string layer_root(const Store& st) {
   return best;
 }
 
+// Module names of the MoE FFN: mlx-lm's mlp.gate + mlp.switch_mlp.*, or gpt-oss's mlp.router + mlp.experts.*
+// (WeightNames.gptOss, Sources/Ingot/Loader/ModelSpecParts.swift:160-168).
+std::string ffn_router(const Config& c) { return c.gpt_oss ? "mlp.router" : "mlp.gate"; }
+std::string ffn_experts(const Config& c) { return c.gpt_oss ? "mlp.experts." : "mlp.switch_mlp."; }
+
 // Reads the description and checks every tensor the verify step needs (names, shapes, formats), without a device.
 int describe(const std::string& dir, Config& cfg, Store& st, std::string& root) {
   if (!read_config(dir, cfg)) return fail(IH_EINVAL, "ih_model_load_mlx: " + cfg.err);
@@ -571,13 +655,27 @@ int describe(const std::string& dir, Config& cfg, Store& st, std::string& root) 
   const std::string a0 = root + "layers.0.self_attn.";
   d.qk_norm = st.find(a0 + "q_norm.weight") != nullptr;
   d.qkv_bias = st.find(a0 + "q_proj.bias") != nullptr;
-  if (st.find(a0 + "o_proj.bias")) return fail(IH_EINVAL, "ih_model_load_mlx: o_proj bias is not supported");
+  d.o_bias = st.find(a0 + "o_proj.bias") != nullptr;
+  if (cfg.attention_bias && !(d.qkv_bias && d.o_bias))
+    return fail(IH_EINVAL, "ih_model_load_mlx: attention_bias is set but q_proj.bias / o_proj.bias are missing");
+  if (st.find(a0 + "sinks")) d.sinks = 1;
+  // Gated attention (Qwen3-Next): q_proj holds [q | gate] per head, twice the q rows.
+  if (const Tensor* qw = st.find(a0 + "q_proj.weight"); qw && qw->shape.size() == 2 && d.n_q_heads > 0 &&
+                                                          qw->shape[0] == int64_t(2) * d.n_q_heads * d.head_dim)
+    d.attn_gate = 1;
   if (d.n_experts > 0) {
-    QLin e;
+    const std::string f0 = root + "layers.0." + ffn_router(cfg), x0 = root + "layers.0." + ffn_experts(cfg);
+    QLin e, r;
     std::string err;
-    if (!qlinear(st, cfg, root + "layers.0.mlp.switch_mlp.gate_proj", true, e, err))
-      return fail(IH_EINVAL, "ih_model_load_mlx: " + err);
+    if (!qlinear(st, cfg, x0 + "gate_proj", true, e, err)) return fail(IH_EINVAL, "ih_model_load_mlx: " + err);
     d.expert_format = e.fmt;
+    if (!qlinear(st, cfg, f0, e.fmt == QF_MXFP4, r, err)) return fail(IH_EINVAL, "ih_model_load_mlx: " + err);
+    if (r.fmt != e.fmt) {
+      if (r.fmt == QF_INT4 && e.fmt == QF_MXFP4) d.router_int4 = 1;
+      else return fail(IH_EINVAL, "ih_model_load_mlx: " + f0 + ": router format differs from the experts'");
+    }
+    d.router_bias = st.find(f0 + ".bias") != nullptr;
+    d.expert_bias = st.find(x0 + "gate_proj.bias") != nullptr;
   }
   IH_TRY(check_desc(d));
   // Every tensor the step reads: present, quantized as the kernels need, of the configured shape.
@@ -601,16 +699,18 @@ int describe(const std::string& dir, Config& cfg, Store& st, std::string& root) 
     const std::string p = root + "layers." + std::to_string(l) + ".", a = p + "self_attn.";
     IH_TRY(vec(p + "input_layernorm.weight", H));
     IH_TRY(vec(p + "post_attention_layernorm.weight", H));
-    IH_TRY(lin(a + "q_proj", false, QH * HD, H, 1));
     IH_TRY(lin(a + "k_proj", false, KVH * HD, H, 1));
     IH_TRY(lin(a + "v_proj", false, KVH * HD, H, 1));
+    IH_TRY(lin(a + "q_proj", false, QH * HD * (d.attn_gate ? 2 : 1), H, 1));
     IH_TRY(lin(a + "o_proj", false, H, QH * HD, 1));
+    if (d.o_bias) IH_TRY(vec(a + "o_proj.bias", H));
+    if (d.sinks) IH_TRY(vec(a + "sinks", QH));
     if (d.qk_norm) {
       IH_TRY(vec(a + "q_norm.weight", HD));
       IH_TRY(vec(a + "k_norm.weight", HD));
     }
     if (d.qkv_bias) {
-      IH_TRY(vec(a + "q_proj.bias", QH * HD));
+      IH_TRY(vec(a + "q_proj.bias", QH * HD * (d.attn_gate ? 2 : 1)));
       IH_TRY(vec(a + "k_proj.bias", KVH * HD));
       IH_TRY(vec(a + "v_proj.bias", KVH * HD));
     }
@@ -619,11 +719,18 @@ int describe(const std::string& dir, Config& cfg, Store& st, std::string& root) 
       IH_TRY(lin(p + "mlp.up_proj", false, d.intermediate, H, 1));
       IH_TRY(lin(p + "mlp.down_proj", false, H, d.intermediate, 1));
     } else {
-      const bool mx = d.expert_format == QF_MXFP4;
-      IH_TRY(lin(p + "mlp.gate", mx, d.n_experts, H, 1));
-      IH_TRY(lin(p + "mlp.switch_mlp.gate_proj", true, d.expert_intermediate, H, d.n_experts));
-      IH_TRY(lin(p + "mlp.switch_mlp.up_proj", true, d.expert_intermediate, H, d.n_experts));
-      IH_TRY(lin(p + "mlp.switch_mlp.down_proj", true, H, d.expert_intermediate, d.n_experts));
+      const bool mx = d.expert_format == QF_MXFP4 && !d.router_int4;
+      const std::string fr = p + ffn_router(cfg), fx = p + ffn_experts(cfg);
+      IH_TRY(lin(fr, mx, d.n_experts, H, 1));
+      IH_TRY(lin(fx + "gate_proj", true, d.expert_intermediate, H, d.n_experts));
+      IH_TRY(lin(fx + "up_proj", true, d.expert_intermediate, H, d.n_experts));
+      IH_TRY(lin(fx + "down_proj", true, H, d.expert_intermediate, d.n_experts));
+      if (d.router_bias) IH_TRY(vec(fr + ".bias", d.n_experts));
+      if (d.expert_bias) {
+        for (const char* nm : {"gate_proj.bias", "up_proj.bias"})
+          IH_TRY(vec(fx + nm, int64_t(d.n_experts) * d.expert_intermediate));
+        IH_TRY(vec(fx + "down_proj.bias", int64_t(d.n_experts) * H));
+      }
     }
   }
   IH_TRY(lin(root + "embed_tokens", false, d.vocab, H, 1));
@@ -683,7 +790,7 @@ int ih_model_load_mlx(ih_ctx* c, const char* dir, ih_model** out) {
     norm(p + "post_attention_layernorm.weight", H, &L.mlp_norm);
     // q|k|v rows concatenated (DenseQ(paths: q_proj, k_proj, v_proj)).
     QLin q, k, v, o;
-    lin(a + "q_proj", false, q, QH * HD, H);
+    lin(a + "q_proj", false, q, QH * HD * (d.attn_gate ? 2 : 1), H);
     lin(a + "k_proj", false, k, KVH * HD, H);
     lin(a + "v_proj", false, v, KVH * HD, H);
     lin(a + "o_proj", false, o, H, QH * HD);
@@ -704,9 +811,18 @@ int ih_model_load_mlx(ih_ctx* c, const char* dir, ih_model** out) {
       norm(a + "q_norm.weight", HD, &L.q_norm);
       norm(a + "k_norm.weight", HD, &L.k_norm);
     }
+    auto fvec = [&](const std::string& name, int64_t n, float** dst) {
+      if (rc != IH_OK) return;
+      std::vector<float> v;
+      need(vec_f32(st.find(name), n, v), "missing or malformed " + name);
+      if (rc == IH_OK) rc = to_device(v, dst);
+    };
+    if (d.o_bias) fvec(a + "o_proj.bias", H, &L.o_bias);
+    if (d.sinks) fvec(a + "sinks", QH, &L.sinks);
     if (d.qkv_bias && rc == IH_OK) {
       std::vector<float> bq, bk, bv;
-      need(vec_f32(st.find(a + "q_proj.bias"), QH * HD, bq) && vec_f32(st.find(a + "k_proj.bias"), KVH * HD, bk) &&
+      need(vec_f32(st.find(a + "q_proj.bias"), QH * HD * (d.attn_gate ? 2 : 1), bq) &&
+               vec_f32(st.find(a + "k_proj.bias"), KVH * HD, bk) &&
                vec_f32(st.find(a + "v_proj.bias"), KVH * HD, bv),
            a + "{q,k,v}_proj.bias missing or malformed");
       if (rc == IH_OK) {
@@ -731,16 +847,37 @@ int ih_model_load_mlx(ih_ctx* c, const char* dir, ih_model** out) {
       if (rc == IH_OK) rc = upload_qmat(c, hd, QF_INT4, 1, H, d.intermediate, 0, &L.down);
       continue;
     }
-    // MoE: router mlp.gate [E, H] (in the experts' format), experts mlp.switch_mlp.{gate,up,down}_proj [E, ...].
+    // MoE: router [E, H] (mlp.gate, or gpt-oss's mlp.router; in the experts' format, or int4 in front of MXFP4
+    // experts), experts mlp.switch_mlp.* / mlp.experts.{gate,up,down}_proj [E, ...], optional biases.
     const int E = d.n_experts, IE = d.expert_intermediate, fmt = d.expert_format;
+    const int rfmt = d.router_int4 ? int(QF_INT4) : fmt;
+    const std::string fr = p + ffn_router(cfg), fx = p + ffn_experts(cfg);
     QLin r, g, u, dn;
-    lin(p + "mlp.gate", fmt == QF_MXFP4, r, E, H);
-    lin(p + "mlp.switch_mlp.gate_proj", true, g, IE, H);
-    lin(p + "mlp.switch_mlp.up_proj", true, u, IE, H);
-    lin(p + "mlp.switch_mlp.down_proj", true, dn, H, IE);
+    lin(fr, rfmt == QF_MXFP4, r, E, H);
+    lin(fx + "gate_proj", true, g, IE, H);
+    lin(fx + "up_proj", true, u, IE, H);
+    lin(fx + "down_proj", true, dn, H, IE);
     if (rc != IH_OK) break;
-    need(r.fmt == fmt && g.fmt == fmt && u.fmt == fmt && dn.fmt == fmt,
-         p + "mlp: the router and the experts must share one format");
+    need(r.fmt == rfmt && g.fmt == fmt && u.fmt == fmt && dn.fmt == fmt,
+         p + "mlp: the experts must share one format, the router theirs (or int4)");
+    if (d.router_bias) fvec(fr + ".bias", E, &L.router_bias);
+    if (d.expert_bias && rc == IH_OK) {
+      // bf16 [E][2I] (each expert's gate biases, then its up biases) and [E][H].
+      std::vector<uint16_t> bg, bu, bd;
+      need(vec_bf16(st.find(fx + "gate_proj.bias"), int64_t(E) * IE, bg) &&
+               vec_bf16(st.find(fx + "up_proj.bias"), int64_t(E) * IE, bu) &&
+               vec_bf16(st.find(fx + "down_proj.bias"), int64_t(E) * H, bd),
+           fx + "{gate,up,down}_proj.bias missing or malformed");
+      if (rc == IH_OK) {
+        std::vector<uint16_t> gu(size_t(E) * 2 * IE);
+        for (int e = 0; e < E; ++e) {
+          std::memcpy(&gu[size_t(e) * 2 * IE], &bg[size_t(e) * IE], size_t(IE) * 2);
+          std::memcpy(&gu[size_t(e) * 2 * IE + IE], &bu[size_t(e) * IE], size_t(IE) * 2);
+        }
+        rc = to_device(gu, &L.gu_bias);
+        if (rc == IH_OK) rc = to_device(bd, &L.down_bias);
+      }
+    }
     need(g.experts == E && u.experts == E && dn.experts == E, p + "mlp.switch_mlp: expert count differs from the config");
     if (rc != IH_OK) break;
     HostMat hr, hgu, hd;
@@ -750,7 +887,7 @@ int ih_model_load_mlx(ih_ctx* c, const char* dir, ih_model** out) {
       hgu.append_rows(u, e);
       hd.append_rows(dn, e);
     }
-    rc = upload_qmat(c, hr, fmt, 1, E, H, 0, &L.router);
+    rc = upload_qmat(c, hr, rfmt, 1, E, H, 0, &L.router);
     if (rc == IH_OK) rc = upload_qmat(c, hgu, fmt, E, 2 * IE, H, 1, &L.gate_up);
     if (rc == IH_OK) rc = upload_qmat(c, hd, fmt, E, H, IE, 0, &L.down);
   }
@@ -758,14 +895,16 @@ int ih_model_load_mlx(ih_ctx* c, const char* dir, ih_model** out) {
   QLin emb;
   lin(root + "embed_tokens", false, emb, d.vocab, H);
   if (rc == IH_OK) {
-    rc = to_device(std::vector<uint32_t>(reinterpret_cast<const uint32_t*>(emb.w->data),
-                                         reinterpret_cast<const uint32_t*>(emb.w->data + emb.w->bytes)), &m->emb_w);
-    if (rc == IH_OK)
-      rc = to_device(std::vector<uint16_t>(reinterpret_cast<const uint16_t*>(emb.s->data),
-                                           reinterpret_cast<const uint16_t*>(emb.s->data + emb.s->bytes)), &m->emb_s);
-    if (rc == IH_OK)
-      rc = to_device(std::vector<uint16_t>(reinterpret_cast<const uint16_t*>(emb.b->data),
-                                           reinterpret_cast<const uint16_t*>(emb.b->data + emb.b->bytes)), &m->emb_b);
+    // Byte copies: a tensor of the mapped file can start at any offset (real packs have odd-length headers), so it
+    // is never read through a wider pointer.
+    auto copy_as = [](const Tensor* t, auto elem) {
+      std::vector<decltype(elem)> v(t->bytes / sizeof(elem));
+      std::memcpy(v.data(), t->data, v.size() * sizeof(elem));
+      return v;
+    };
+    rc = to_device(copy_as(emb.w, uint32_t{}), &m->emb_w);
+    if (rc == IH_OK) rc = to_device(copy_as(emb.s, uint16_t{}), &m->emb_s);
+    if (rc == IH_OK) rc = to_device(copy_as(emb.b, uint16_t{}), &m->emb_b);
   }
   norm(root + "norm.weight", H, &m->final_norm);
   if (rc == IH_OK) {

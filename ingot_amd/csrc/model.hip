@@ -554,8 +554,8 @@ int ih_model_create_synthetic(ih_ctx* c, const ih_model_desc* desc, uint64_t see
       }
       if (d.n_experts > 0) {
         const int E = d.n_experts, IE = d.expert_intermediate, fmt = d.expert_format;
-        run(synth_stack(c, stg, fmt, 1, E, H, seed, [&](int) { return layer_tensor(l, L_ROUTER); }, W_SD, 0,
-                        &L.router));
+        run(synth_stack(c, stg, d.router_int4 ? int(QF_INT4) : fmt, 1, E, H, seed,
+                        [&](int) { return layer_tensor(l, L_ROUTER); }, W_SD, 0, &L.router));
         run(synth_stack(c, stg, fmt, E, 2 * IE, H, seed, [&](int e) { return expert_tensor(l, X_GATE_UP, e); }, W_SD,
                         1, &L.gate_up));
         run(synth_stack(c, stg, fmt, E, H, IE, seed, [&](int e) { return expert_tensor(l, X_DOWN, e); }, W_SD, 0,

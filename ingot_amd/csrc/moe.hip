@@ -109,11 +109,15 @@ struct GatherParams {
 };
 
 constexpr int GKW = 4;  // waves per workgroup (K split)
+// Kernel format of the gathered product: the matrix formats, plus int4 codes against fp16 activations (an affine
+// router in front of MXFP4 experts, whose activation rows are fp16: a nibble becomes the exact fp16 1024 + q, the MFMA
+// runs in fp16 and the affine map is y = s·acc + (b − 1024·s)·Σx).
+constexpr int GF_INT4_F16 = 2;
 
 template <int FMT, int R>
 struct GStage {
   u32x4 w[R];
-  uint2 s[R];  // int4: (s0|b0<<16, s1|b1<<16); mxfp4: .x = four e8m0 bytes
+  uint2 s[R];  // int4 (both kernel formats): (s0|b0<<16, s1|b1<<16); mxfp4: .x = four e8m0 bytes
   u32x4 x[2][4];
 };
 
@@ -121,6 +125,7 @@ struct GStage {
 // fragment, and a workgroup streams R times the bytes behind its one read of the slot's routing entry.
 template <int FMT, int R>
 __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
+  constexpr bool I4 = FMT != QF_MXFP4, XH = FMT == GF_INT4_F16;  // int4 codes; fp16 activations for them
   const int u = blockIdx.y;
   const int U = p.nent ? __builtin_amdgcn_readfirstlane(p.nent[0]) : 1;
   if (u >= U) return;
@@ -146,8 +151,8 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
 
   const size_t tb0 = size_t(e) * p.tiles_per_e + size_t(tile0) * p.nkb;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w + tb0 * 64, unsigned(R * p.nkb) * 1024u);
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.s) + tb0 * (FMT == QF_INT4 ? 128 : 64),
-                                              unsigned(R * p.nkb) * (FMT == QF_INT4 ? 128u : 64u));
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(static_cast<const uint8_t*>(p.s) + tb0 * (I4 ? 128 : 64),
+                                              unsigned(R * p.nkb) * (I4 ? 128u : 64u));
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.xa, unsigned(p.x_tokens) * p.x_nkb * 256u);
   unsigned xoff[2];
 #pragma unroll
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
       const unsigned tk = unsigned(r * p.nkb + kb);
       st.w[r] =
           __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (tk * 1024u + lane * 16u) | oob, 0, 0));
-      if constexpr (FMT == QF_INT4)
+      if constexpr (I4)
         st.s[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, (tk * 128u + n * 8u) | oob, 0, 0));
       else
         st.s[r].x = __builtin_amdgcn_raw_buffer_load_b32(rs, (tk * 64u + n * 4u) | oob, 0, 0);
@@ -189,9 +194,21 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
   for (int r = 0; r < R; ++r) acc[r][0] = acc[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
   const unsigned shv[3] = {vgpr_of(4u), vgpr_of(8u), vgpr_of(12u)};  // 64-bit nibble shifts (nib_bf16_pair)
+  // One MFMA step in the activations' type (bf16, or fp16 for XH); the operands travel as raw 32-bit words.
+  auto mma = [](const u32x4& a, const u32x4& b, f32x4 c) -> f32x4 {
+    if constexpr (XH)
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                    0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                     0, 0, 0);
+  };
   auto compute = [&](const GStage<FMT, R>& st) {
-    if constexpr (FMT == QF_INT4) {
-      const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+    if constexpr (I4) {
+      // 1.0 in the activations' type; a nibble q decodes to the exact 128 + q (bf16) or 1024 + q (fp16).
+      const unsigned one = XH ? 0x3C003C00u : 0x3F803F80u;
+      const u32x4 ones = u32x4{one, one, one, one};
+      constexpr float OFF = XH ? 1024.f : 128.f;
       // Σx per group and token tile, shared by the R tiles.
       f32x4 xs[2][2];
 #pragma unroll
@@ -199,16 +216,14 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
         if (tt == 1 && !two) continue;
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          f32x4 z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g]), ones,
-                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          xs[tt][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), ones,
-                                                              z, 0, 0, 0);
+          f32x4 z = mma(st.x[tt][2 * g], ones, f32x4{0.f, 0.f, 0.f, 0.f});
+          xs[tt][g] = mma(st.x[tt][2 * g + 1], ones, z);
         }
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const float s0 = bf16f(st.s[r].x & 0xFFFFu), s1 = bf16f(st.s[r].y & 0xFFFFu);
-        const float c0 = fmaf(-128.f, s0, bf16f(st.s[r].x >> 16)), c1 = fmaf(-128.f, s1, bf16f(st.s[r].y >> 16));
+        const float c0 = fmaf(-OFF, s0, bf16f(st.s[r].x >> 16)), c1 = fmaf(-OFF, s1, bf16f(st.s[r].y >> 16));
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
           bf16x8 w0, w1;
@@ -217,10 +232,8 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) {
             if (tt == 1 && !two) continue;
-            f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g]), w0,
-                                                                f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.x[tt][2 * g + 1]), w1, tmp,
-                                                          0, 0, 0);
+            f32x4 tmp = mma(st.x[tt][2 * g], __builtin_bit_cast(u32x4, w0), f32x4{0.f, 0.f, 0.f, 0.f});
+            tmp = mma(st.x[tt][2 * g + 1], __builtin_bit_cast(u32x4, w1), tmp);
 #pragma unroll
             for (int q = 0; q < 4; ++q) acc[r][tt][q] = fmaf(sg, tmp[q], fmaf(cg, xs[tt][g][q], acc[r][tt][q]));
           }
@@ -540,7 +553,8 @@ __global__ __launch_bounds__(1024) void moe_combine_kernel(const float* __restri
 // ---------------------------------------------------------------------------------------------------------------
 // Host side.
 
-int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slots, double bytes) {
+// x_f16: the activation fragments are fp16 (MXFP4 matrices always take fp16; an int4 matrix then runs the fp16 decode).
+int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slots, double bytes, bool x_f16) {
   GatherParams p = base;
   p.w = static_cast<const uint4*>(W->w);
   p.s = W->s;
@@ -550,7 +564,7 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
   p.Npad = W->Npad;
   p.nkb = W->nkb;
   p.kmask = 0x000F000Fu;
-  p.kbias = 0x43004300u;
+  p.kbias = x_f16 && W->format == QF_INT4 ? 0x64006400u : 0x43004300u;  // nibble → fp16 1024 + q / bf16 128 + q
   IH_CHECK(p.x_nkb == W->nkb, IH_EINVAL, "gathered qmm: activation K does not match the matrix");
   IH_CHECK(size_t(W->E) * p.tiles_per_e * 1024u < (size_t(1) << 31), IH_EINVAL,
            "gathered qmm: stacked matrix above 2 GiB");
@@ -568,8 +582,9 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
   const dim3 grid(tiles / R, slots);
 #define IH_GATHER_LAUNCH(R_)                                                                                        \
   if (R == R_) {                                                                                                  \
-    if (W->format == QF_INT4) tlaunch(tl, qmm_gather_kernel<QF_INT4, R_>, grid, dim3(64 * GKW), 0, c->stream, p); \
-    else tlaunch(tl, qmm_gather_kernel<QF_MXFP4, R_>, grid, dim3(64 * GKW), 0, c->stream, p);                      \
+    if (W->format == QF_MXFP4) tlaunch(tl, qmm_gather_kernel<QF_MXFP4, R_>, grid, dim3(64 * GKW), 0, c->stream, p); \
+    else if (x_f16) tlaunch(tl, qmm_gather_kernel<GF_INT4_F16, R_>, grid, dim3(64 * GKW), 0, c->stream, p);         \
+    else tlaunch(tl, qmm_gather_kernel<QF_INT4, R_>, grid, dim3(64 * GKW), 0, c->stream, p);                        \
   }
   IH_GATHER_LAUNCH(1) IH_GATHER_LAUNCH(2) IH_GATHER_LAUNCH(4)
 #undef IH_GATHER_LAUNCH
@@ -609,7 +624,7 @@ int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, 
 int launch_moe_router(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, float eps, float* logits, int ldl) {
   // An int4 router runs on the dense qmm, whose workgroups split K across waves (the matrix is a few hundred KB:
   // one memory round trip instead of a walk over its K-blocks).
-  if (W->format == QF_INT4 && W->E == 1) {
+  if (W->format == QF_INT4 && W->E == 1 && !x.f16) {
     QmmEpilogue ep;
     ep.mode = QM_F32_SCALE;
     ep.y = logits;
@@ -631,7 +646,7 @@ int launch_moe_router(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, fl
   p.D = x.K;
   p.nrows = rows;
   p.eps = eps;
-  return launch_gather(c, W, p, 1, double(W->algo_bytes) + double(rows) * W->N * 4);
+  return launch_gather(c, W, p, 1, double(W->algo_bytes) + double(rows) * W->N * 4, x.f16);
 }
 
 // Gate|up of every pair: h[pair] = act(r·g + bg, r·u + bu) as fragments (one token per pair).
@@ -660,13 +675,12 @@ int launch_moe_gate_up(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, i
   p.limit = limit;
   p.bias = bias;
   const int slots = std::min(W->E, rows * K_top);
-  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots);
+  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots, x.f16);
 }
 
 // Down of every pair: o[pair] = h[pair] · Wdᵀ + bd (fp32).
 int launch_moe_down(ih_ctx* c, const ih_qmat* W, const void* h_frag, int h_nkb, int h_tokens, bool h_f16, int rows,
                     int K_top, const int* nent, const int* entries, const uint16_t* bias, float* o, int ldo) {
-  (void)h_f16;
   GatherParams p{};
   p.xa = static_cast<const uint4*>(h_frag);
   p.x_nkb = h_nkb;
@@ -678,7 +692,7 @@ int launch_moe_down(ih_ctx* c, const ih_qmat* W, const void* h_frag, int h_nkb, 
   p.ldy = ldo;
   p.bias = bias;
   const int slots = std::min(W->E, rows * K_top);
-  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots);
+  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots, h_f16);
 }
 
 int pack_mxfp4(ih_ctx* c, ih_qmat* q, const uint32_t* w, const uint8_t* s) {
@@ -789,7 +803,7 @@ int ih_qmm_expert(ih_ctx* c, const ih_qmat* W, int expert, const void* x, int ld
   p.mode = GM_F32;
   p.y = y;
   p.ldy = ldy;
-  return launch_gather(c, W, p, 1, double(W->algo_bytes) + double(M) * W->K * 2 + double(M) * W->N * 4);
+  return launch_gather(c, W, p, 1, double(W->algo_bytes) + double(M) * W->K * 2 + double(M) * W->N * 4, f16);
 }
 
 int ih_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K, const float* bias, const float* pes,
@@ -818,7 +832,7 @@ int ih_qmm_gathered(ih_ctx* c, const ih_qmat* W, const void* x, int ldx, int row
   p.y = y;
   p.ldy = ldy;
   const int slots = std::min(W->E, rows * K_top);
-  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots);
+  return launch_gather(c, W, p, slots, double(W->algo_bytes) * slots, f16);
 }
 
 }  // extern "C"

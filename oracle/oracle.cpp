@@ -475,6 +475,7 @@ struct or_model_desc {
   float rope_factor, rope_orig_max, rope_beta_fast, rope_beta_slow, rope_mscale, rope_attn_factor;
   int rope_no_truncate;
   float rope_partial;
+  int router_int4;
 };
 
 static uint64_t layer_tensor(int l, uint64_t kind) { return 1000 + 100 * uint64_t(l) + kind; }
@@ -601,7 +602,7 @@ void* or_model_create(const or_model_desc* d, uint64_t seed, uint64_t kv_seed, i
     }
     if (d->n_experts > 0) {
       const int E = d->n_experts, IE = d->expert_intermediate, f = d->expert_format;
-      L.router.make(f, seed, layer_tensor(l, 6), E, H, sd);
+      L.router.make(d->router_int4 ? 0 : f, seed, layer_tensor(l, 6), E, H, sd);
       L.egu.resize(E);
       L.edn.resize(E);
       for (int e = 0; e < E; ++e) {

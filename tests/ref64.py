@@ -239,7 +239,7 @@ def forward(desc, seed: int, kv_seed: int, P: int, tokens, mutate: str | None = 
             h = h + a @ int4_dense(seed, layer_tensor(l, L_DOWN), H, I).T
             continue
         E, Kt, IE, fmt = d.n_experts, d.top_k, d.expert_intermediate, d.expert_format
-        lg = x @ expert_matrix(fmt, seed, layer_tensor(l, L_ROUTER), E, H).T
+        lg = x @ expert_matrix(0 if d.router_int4 else fmt, seed, layer_tensor(l, L_ROUTER), E, H).T
         if d.iid_routing and mutate != "route":
             # Synthetic i.i.d. routing: logit (row, expert) = draw (position·E + expert) of the layer's N(0,1) stream.
             lg = iid_logits(seed, l, P, B, E)

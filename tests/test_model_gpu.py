@@ -75,13 +75,15 @@ LINEAR = dict(GQA4, rope_type=1, rope_factor=4.0)
 # The benchmark MoE configurations' synthetic i.i.d. routing.
 MOEIID = dict(MOE4, iid_routing=1, n_experts=16, top_k=4)
 MOEXIID = dict(MOEX, iid_routing=1)
+# An int4 router in front of MXFP4 experts (gpt-oss packs): the router reads the experts' fp16 rows.
+MOEXR4 = dict(MOEX, router_int4=1)
 
 
 @pytest.mark.parametrize("shape", [SMALL, GQA8, SWA, MOE4, MOEX, QWEN, QWEN64, GATED, GATED64, YARN, PROP, LINEAR,
-                                   MOEIID, MOEXIID],
+                                   MOEIID, MOEXIID, MOEXR4],
                          ids=["gqa2-hd128", "gqa8-hd64", "sinks-swa", "moe-int4", "moe-mxfp4", "qknorm-bias-hd128",
                               "qknorm-bias-hd64", "gated-rot32-hd128", "gated-rot16-hd64", "yarn-obias-sinks",
-                              "proportional", "linear", "moe-int4-iid", "moe-mxfp4-iid"])
+                              "proportional", "linear", "moe-int4-iid", "moe-mxfp4-iid", "moe-mxfp4-int4-router"])
 @pytest.mark.parametrize("B", [1, 5, 9, 10, 17])
 def test_verify_step_matches_oracle(ctx, shape, B):
     d, m, kv = make(ctx, shape)

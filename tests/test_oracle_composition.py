@@ -43,11 +43,13 @@ def rel_err(a, b):
 @pytest.mark.parametrize("shape,tol,muts", [(DENSE, 0.015, ["residual", "norm", "gqa"]),
                                             (MOE, 0.015, ["residual", "norm", "gqa", "renorm", "slots"]),
                                             (MOEX, 0.03, ["residual", "norm", "gqa", "slots"]),
+                                            (dict(MOEX, router_int4=1), 0.03, ["residual", "slots"]),
                                             (QWEN, 0.015, ["residual", "gqa", "qknorm", "qkvbias"]),
                                             (GATED, 0.015, ["residual", "gqa", "gate", "rot"]),
                                             (YARN, 0.015, ["residual", "obias", "qkvbias", "rope"]),
                                             (MOEIID, 0.015, ["residual", "renorm", "route"])],
-                         ids=["dense", "moe-int4", "moe-mxfp4-sinks-swa", "qknorm-qkvbias", "gated-partial-rope",
+                         ids=["dense", "moe-int4", "moe-mxfp4-sinks-swa", "moe-mxfp4-int4-router", "qknorm-qkvbias",
+                              "gated-partial-rope",
                               "yarn-obias-sinks", "moe-iid-routing"])
 def test_oracle_composition_matches_float64_forward(shape, tol, muts):
     d = ModelDesc.make(**shape)
