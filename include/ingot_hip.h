@@ -371,12 +371,28 @@ typedef struct ih_drafter ih_drafter;
 
 /* A drafter with synthetic weights for `target` (counter-based SplitMix64 streams, reproducible on the CPU). */
 int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, uint64_t seed, ih_drafter** out);
+/* A trained DFlash2 (or DFlash v1) drafter for `target` from its directory (DFlash2Drafter.init,
+ * Sources/Ingot/Drafter.swift:114-256): config.json with dflash_config (target_layer_ids, mask_token_id, block_size)
+ * and the qwen3 fields (8 KV heads; sliding_window = the context window), safetensors with layers.N.{input,
+ * post_attention}_layernorm, self_attn.{q,k,v,o}_proj and {q,k}_norm, mlp.{gate,up,down}_proj, fc, hidden_norm, norm,
+ * and for DFlash2 {attention,mlp}_conv.{kernel_projection,base_kernel} and candidate_selector.{hidden_projection,
+ * predecessor_codebook,successor_codebook}. bf16 projections are quantized to MLX int4 g64 at load (as the reference,
+ * ih_quantize_int4_g64); projections already in MLX int4 g64 are taken as they are. Attention or MLP biases and a
+ * scaled RoPE are IH_EINVAL. */
+int ih_drafter_load_mlx(ih_model* target, const char* dir, ih_drafter** out);
+/* MLX affine quantization of a bf16 matrix [N, K] to int4 in groups of 64 (DenseQ.quantizeAffine,
+ * Sources/Ingot/Layers/Linear.swift:592-628): per row and group scale = bf16((max − min)/15), bias = bf16(min),
+ * q = round((w − bias)/scale) (half away from zero) clamped to 0…15, 0 where the scale is 0; w uint32 [N, K/8] (low
+ * nibble first), scales and biases bf16 [N, K/64]. Host only. */
+int ih_quantize_int4_g64(const uint16_t* w_bf16, int N, int K, uint32_t* w, uint16_t* scales, uint16_t* biases);
 /* Frees a drafter (detaching it from its model). A drafter whose model was freed first refuses further work with
  * IH_EINVAL and can still be freed. */
 int ih_drafter_free(ih_drafter* drafter);
 /* Attaches the drafter to its target (null detaches): every verify step then captures its rows' residual after the
  * drafter's target layers (capture_rows, yy_model.metal:94-104; ModelRound.swift:72-75). */
 int ih_model_set_drafter(ih_model* model, ih_drafter* drafter);
+/* The description a drafter runs with (as created or as read from its checkpoint). */
+int ih_drafter_describe(const ih_drafter* drafter, ih_drafter_desc* out);
 /* Rows of the drafter's block (anchor included). */
 int ih_drafter_block_rows(const ih_drafter* drafter);
 /* The captured rows bf16 [rows][n_targets · hidden] of the last verify step (device). */

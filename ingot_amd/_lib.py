@@ -117,6 +117,9 @@ def _declare(L: C.CDLL) -> None:
         "ih_spec_rows_choose_dev": (i32, [vp, vp, vp, vp]),
         "ih_decode_sample": (i32, [vp, vp, vp, i32, C.c_uint32, vp, vp, C.c_uint64, vp, i32, P(i32), vp]),
         "ih_drafter_create_synthetic": (i32, [vp, vp, C.c_uint64, P(vp)]),
+        "ih_drafter_load_mlx": (i32, [vp, C.c_char_p, P(vp)]),
+        "ih_drafter_describe": (i32, [vp, vp]),
+        "ih_quantize_int4_g64": (i32, [vp, i32, i32, vp, vp, vp]),
         "ih_drafter_free": (i32, [vp]),
         "ih_model_set_drafter": (i32, [vp, vp]),
         "ih_drafter_captures_dev": (vp, [vp]),
@@ -367,6 +370,18 @@ class Drafter:
         check(lib().ih_drafter_create_synthetic(model.handle, C.byref(desc), seed, C.byref(h)))
         self.handle = h.value
 
+    @classmethod
+    def load_mlx(cls, model: "Model", directory) -> "Drafter":
+        """A trained drafter from its checkpoint directory (ih_drafter_load_mlx)."""
+        self = cls.__new__(cls)
+        self.model, self.seed = model, None
+        h = vp()
+        check(lib().ih_drafter_load_mlx(model.handle, str(directory).encode(), C.byref(h)))
+        self.handle = h.value
+        self.desc = DrafterDesc()
+        check(lib().ih_drafter_describe(self.handle, C.byref(self.desc)))
+        return self
+
     def attach(self) -> None:
         check(lib().ih_model_set_drafter(self.model.handle, self.handle))
 
@@ -456,6 +471,17 @@ class Model:
         if self.handle:
             lib().ih_model_free(self.handle)
             self.handle = None
+
+
+def quantize_int4_g64(w_bf16: np.ndarray):
+    """(w uint32 [N, K/8], scales, biases bf16 [N, K/64]) of a bf16 matrix (ih_quantize_int4_g64; host only)."""
+    a = np.ascontiguousarray(w_bf16, np.uint16)
+    N, K = a.shape
+    w = np.empty((N, K // 8), np.uint32)
+    s = np.empty((N, K // 64), np.uint16)
+    b = np.empty((N, K // 64), np.uint16)
+    check(lib().ih_quantize_int4_g64(ptr(a), N, K, ptr(w), ptr(s), ptr(b)))
+    return w, s, b
 
 
 def describe_mlx(directory) -> ModelDesc:

@@ -22,6 +22,7 @@
 #include <algorithm>
 #include "act.h"
 #include "lanes.h"
+#include "drafter_ckpt.h"
 #include "model_internal.h"
 
 namespace ih {
@@ -489,90 +490,55 @@ static int dsynth_qmat(ih_ctx* c, int N, int K, uint64_t seed, uint64_t tensor, 
   return st;
 }
 
-}  // namespace ih
-
-extern "C" {
-
-int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, uint64_t seed, ih_drafter** out) {
-  IH_CHECK(target && desc && out, IH_EINVAL, "ih_drafter_create_synthetic: null argument");
-  *out = nullptr;
+// The shapes the drafter kernels run (DFlash2Drafter's mismatch rules for the shapes this build supports).
+static int drafter_check(const ih_model* target, const ih_drafter_desc& d, const std::string& who) {
   const ih_model_desc& td = target->d;
-  const ih_drafter_desc& d = *desc;
   IH_CHECK(d.n_layers >= 1 && d.hidden == td.hidden, IH_EINVAL,
-           "ih_drafter_create_synthetic: the drafter's hidden size must be the target's (it uses its embedding and head)");
-  IH_CHECK(d.head_dim == 64 || d.head_dim == 128, IH_EINVAL, "ih_drafter_create_synthetic: head_dim must be 64 or 128");
+           who + "the drafter's hidden size must be the target's (it uses its embedding and head)");
+  IH_CHECK(d.head_dim == 64 || d.head_dim == 128, IH_EINVAL, who + "head_dim must be 64 or 128");
   IH_CHECK(d.n_q_heads >= DKVH && d.n_q_heads % DKVH == 0 && d.n_q_heads * d.head_dim % 512 == 0, IH_EINVAL,
-           "ih_drafter_create_synthetic: q heads must be a multiple of the 8 KV heads (q heads · head_dim % 512 == 0)");
+           who + "q heads must be a multiple of the 8 KV heads (q heads · head_dim % 512 == 0)");
   IH_CHECK(d.block >= 2 && d.block <= 16 && d.n_q_heads / DKVH * d.block <= 64, IH_EINVAL,
-           "ih_drafter_create_synthetic: block must be in 2..16 with (q heads / 8)·block ≤ 64");
+           who + "block must be in 2..16 with (q heads / 8)·block ≤ 64");
   IH_CHECK(d.window >= d.block && d.window % 32 == 0, IH_EINVAL,
-           "ih_drafter_create_synthetic: window must be a multiple of 32, at least the block");
+           who + "window must be a multiple of 32, at least the block");
   IH_CHECK(d.hidden % 64 == 0 && d.intermediate >= 64 && d.intermediate % 64 == 0, IH_EINVAL,
-           "ih_drafter_create_synthetic: hidden and intermediate must be multiples of 64");
-  IH_CHECK(d.n_targets >= 1 && d.n_targets <= IH_DRAFTER_MAX_TARGETS, IH_EINVAL,
-           "ih_drafter_create_synthetic: 1..8 target layers");
+           who + "hidden and intermediate must be multiples of 64");
+  IH_CHECK(d.n_targets >= 1 && d.n_targets <= IH_DRAFTER_MAX_TARGETS, IH_EINVAL, who + "1..8 target layers");
   for (int j = 0; j < d.n_targets; ++j)
     IH_CHECK(d.target_layers[j] >= 0 && d.target_layers[j] < td.n_layers, IH_EINVAL,
-             "ih_drafter_create_synthetic: a target layer is outside the target model");
+             who + "a target layer is outside the target model");
   IH_CHECK(d.rank == 0 || (d.rank % 64 == 0 && d.rank <= 1024), IH_EINVAL,
-           "ih_drafter_create_synthetic: rank must be 0 or a multiple of 64 up to 1024");
-  IH_CHECK(d.mask_token < uint32_t(td.vocab), IH_EINVAL, "ih_drafter_create_synthetic: mask token beyond the vocabulary");
-  ih_ctx* c = target->ctx;
+           who + "rank must be 0 or a multiple of 64 up to 1024");
+  IH_CHECK(d.mask_token < uint32_t(td.vocab), IH_EINVAL, who + "mask token beyond the vocabulary");
+  return IH_OK;
+}
+
+static ih_drafter* drafter_new(ih_model* target, const ih_drafter_desc& d) {
   ih_drafter* r = new ih_drafter();
-  r->ctx = c;
+  r->ctx = target->ctx;
   r->d = d;
   r->target = target;
-  const int H = d.hidden, HD = d.head_dim, QH = d.n_q_heads, I = d.intermediate, V = td.vocab;
-  r->QP = (QH + 2 * DKVH) * HD;
-  r->G = QH / DKVH;
+  r->QP = (d.n_q_heads + 2 * DKVH) * d.head_dim;
+  r->G = d.n_q_heads / DKVH;
   r->slots = (d.window + 16 + 31) / 32 * 32;
-  r->DYN = 4 * (H / DCG);
-  int st = IH_OK;
-  auto run = [&](int s) { if (st == IH_OK) st = s; };
+  r->DYN = 4 * (d.hidden / DCG);
   r->layers.resize(d.n_layers);
-  for (int l = 0; l < d.n_layers && st == IH_OK; ++l) {
-    ih_drafter_layer& L = r->layers[l];
-    run(dalloc_t(&L.n1, H));
-    run(dalloc_t(&L.n2, H));
-    run(dalloc_t(&L.qn, HD));
-    run(dalloc_t(&L.kn, HD));
-    if (st != IH_OK) break;
-    run(synth_bf16(c, L.n1, H, seed, dl_tensor(l, D_N1), 1.0f, 0.125f));
-    run(synth_bf16(c, L.n2, H, seed, dl_tensor(l, D_N2), 1.0f, 0.125f));
-    run(synth_bf16(c, L.qn, HD, seed, dl_tensor(l, D_QN), 1.0f, 0.125f));
-    run(synth_bf16(c, L.kn, HD, seed, dl_tensor(l, D_KN), 1.0f, 0.125f));
-    run(dsynth_qmat(c, r->QP, H, seed, dl_tensor(l, D_QKV), &L.qkv));
-    run(dsynth_qmat(c, r->QP, H, seed, dl_tensor(l, D_QKV), &L.kv, QH * HD, 2 * DKVH * HD));
-    run(dsynth_qmat(c, H, QH * HD, seed, dl_tensor(l, D_O), &L.o));
-    run(dsynth_qmat(c, 2 * I, H, seed, dl_tensor(l, D_GU), &L.gu));
-    run(dsynth_qmat(c, H, I, seed, dl_tensor(l, D_DOWN), &L.down));
-    if (d.dyn_conv) {
-      run(dsynth_qmat(c, r->DYN, H, seed, dl_tensor(l, D_APROJ), &L.aproj));
-      run(dsynth_qmat(c, r->DYN, H, seed, dl_tensor(l, D_MPROJ), &L.mproj));
-      run(dalloc_t(&L.abase, 4 * H));
-      run(dalloc_t(&L.mbase, 4 * H));
-      // Taps: [prep|finish][tap][H]; the current tap near 1, the previous near 0.
-      for (int k = 0; k < 4 && st == IH_OK; ++k) {
-        run(synth_bf16(c, L.abase + k * H, H, seed, dl_tensor(l, D_ABASE) + 100 * k, k % 2 ? 0.0f : 1.0f, 0.1f));
-        run(synth_bf16(c, L.mbase + k * H, H, seed, dl_tensor(l, D_MBASE) + 100 * k, k % 2 ? 0.0f : 1.0f, 0.1f));
-      }
-    }
+  return r;
+}
+
+// The context rings and the scratch of one pass, then registration with the target (st: the weights' status).
+static int drafter_finish(ih_drafter* r, int st, ih_drafter** out) {
+  ih_ctx* c = r->ctx;
+  const auto& d = r->d;
+  const ih_model_desc& td = r->target->d;
+  const int H = d.hidden, HD = d.head_dim, QH = d.n_q_heads, I = d.intermediate, V = td.vocab;
+  auto run = [&](int s) { if (st == IH_OK) st = s; };
+  for (auto& L : r->layers) {
     run(dalloc_t(&L.kc, size_t(DKVH) * r->slots * HD));
     run(dalloc_t(&L.vc, size_t(DKVH) * r->slots * HD));
     if (st == IH_OK) run(fill(c, L.kc, 0, size_t(DKVH) * r->slots * HD * 2));
     if (st == IH_OK) run(fill(c, L.vc, 0, size_t(DKVH) * r->slots * HD * 2));
-  }
-  run(dsynth_qmat(c, H, d.n_targets * td.hidden, seed, dg_tensor(D_FC), &r->fc));
-  run(dalloc_t(&r->hnorm, H));
-  run(dalloc_t(&r->fnorm, H));
-  if (st == IH_OK) run(synth_bf16(c, r->hnorm, H, seed, dg_tensor(D_HNORM), 1.0f, 0.125f));
-  if (st == IH_OK) run(synth_bf16(c, r->fnorm, H, seed, dg_tensor(D_FNORM), 1.0f, 0.125f));
-  if (d.rank > 0) {
-    run(dsynth_qmat(c, d.rank, H, seed, dg_tensor(D_HPROJ), &r->hproj));
-    run(dalloc_t(&r->pred, size_t(V) * d.rank));
-    run(dalloc_t(&r->succ, size_t(V) * d.rank));
-    if (st == IH_OK) run(synth_bf16(c, r->pred, size_t(V) * d.rank, seed, dg_tensor(D_PRED), 0.0f, 0.25f));
-    if (st == IH_OK) run(synth_bf16(c, r->succ, size_t(V) * d.rank, seed, dg_tensor(D_SUCC), 0.0f, 0.25f));
   }
   const int nchunk = (r->slots + DCHUNK - 1) / DCHUNK, Q = r->G * d.block;
   run(dalloc_t(&r->caps, size_t(MAX_TOK) * d.n_targets * td.hidden));
@@ -605,9 +571,117 @@ int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, u
     drafter_release(r);
     return st;
   }
-  target->drafters.push_back(r);  // registered only once complete (a failed creation is released above)
+  r->target->drafters.push_back(r);  // registered only once complete (a failed creation is released above)
   *out = r;
   return IH_OK;
+}
+
+}  // namespace ih
+
+extern "C" {
+
+int ih_drafter_create_synthetic(ih_model* target, const ih_drafter_desc* desc, uint64_t seed, ih_drafter** out) {
+  IH_CHECK(target && desc && out, IH_EINVAL, "ih_drafter_create_synthetic: null argument");
+  *out = nullptr;
+  IH_TRY(drafter_check(target, *desc, "ih_drafter_create_synthetic: "));
+  ih_drafter* r = drafter_new(target, *desc);
+  ih_ctx* c = target->ctx;
+  const auto& d = r->d;
+  const int H = d.hidden, HD = d.head_dim, QH = d.n_q_heads, I = d.intermediate, V = target->d.vocab;
+  int st = IH_OK;
+  auto run = [&](int s) { if (st == IH_OK) st = s; };
+  for (int l = 0; l < d.n_layers && st == IH_OK; ++l) {
+    ih_drafter_layer& L = r->layers[l];
+    run(dalloc_t(&L.n1, H));
+    run(dalloc_t(&L.n2, H));
+    run(dalloc_t(&L.qn, HD));
+    run(dalloc_t(&L.kn, HD));
+    if (st != IH_OK) break;
+    run(synth_bf16(c, L.n1, H, seed, dl_tensor(l, D_N1), 1.0f, 0.125f));
+    run(synth_bf16(c, L.n2, H, seed, dl_tensor(l, D_N2), 1.0f, 0.125f));
+    run(synth_bf16(c, L.qn, HD, seed, dl_tensor(l, D_QN), 1.0f, 0.125f));
+    run(synth_bf16(c, L.kn, HD, seed, dl_tensor(l, D_KN), 1.0f, 0.125f));
+    run(dsynth_qmat(c, r->QP, H, seed, dl_tensor(l, D_QKV), &L.qkv));
+    run(dsynth_qmat(c, r->QP, H, seed, dl_tensor(l, D_QKV), &L.kv, QH * HD, 2 * DKVH * HD));
+    run(dsynth_qmat(c, H, QH * HD, seed, dl_tensor(l, D_O), &L.o));
+    run(dsynth_qmat(c, 2 * I, H, seed, dl_tensor(l, D_GU), &L.gu));
+    run(dsynth_qmat(c, H, I, seed, dl_tensor(l, D_DOWN), &L.down));
+    if (d.dyn_conv) {
+      run(dsynth_qmat(c, r->DYN, H, seed, dl_tensor(l, D_APROJ), &L.aproj));
+      run(dsynth_qmat(c, r->DYN, H, seed, dl_tensor(l, D_MPROJ), &L.mproj));
+      run(dalloc_t(&L.abase, 4 * H));
+      run(dalloc_t(&L.mbase, 4 * H));
+      // Taps: [prep|finish][tap][H]; the current tap near 1, the previous near 0.
+      for (int k = 0; k < 4 && st == IH_OK; ++k) {
+        run(synth_bf16(c, L.abase + k * H, H, seed, dl_tensor(l, D_ABASE) + 100 * k, k % 2 ? 0.0f : 1.0f, 0.1f));
+        run(synth_bf16(c, L.mbase + k * H, H, seed, dl_tensor(l, D_MBASE) + 100 * k, k % 2 ? 0.0f : 1.0f, 0.1f));
+      }
+    }
+  }
+  run(dsynth_qmat(c, H, d.n_targets * target->d.hidden, seed, dg_tensor(D_FC), &r->fc));
+  run(dalloc_t(&r->hnorm, H));
+  run(dalloc_t(&r->fnorm, H));
+  if (st == IH_OK) run(synth_bf16(c, r->hnorm, H, seed, dg_tensor(D_HNORM), 1.0f, 0.125f));
+  if (st == IH_OK) run(synth_bf16(c, r->fnorm, H, seed, dg_tensor(D_FNORM), 1.0f, 0.125f));
+  if (d.rank > 0) {
+    run(dsynth_qmat(c, d.rank, H, seed, dg_tensor(D_HPROJ), &r->hproj));
+    run(dalloc_t(&r->pred, size_t(V) * d.rank));
+    run(dalloc_t(&r->succ, size_t(V) * d.rank));
+    if (st == IH_OK) run(synth_bf16(c, r->pred, size_t(V) * d.rank, seed, dg_tensor(D_PRED), 0.0f, 0.25f));
+    if (st == IH_OK) run(synth_bf16(c, r->succ, size_t(V) * d.rank, seed, dg_tensor(D_SUCC), 0.0f, 0.25f));
+  }
+  return drafter_finish(r, st, out);
+}
+
+int ih_drafter_load_mlx(ih_model* target, const char* dir, ih_drafter** out) {
+  IH_CHECK(target && dir && out, IH_EINVAL, "ih_drafter_load_mlx: null argument");
+  *out = nullptr;
+  DrafterCkpt ck;
+  IH_TRY(read_drafter_mlx(dir, target->d, ck));
+  IH_TRY(drafter_check(target, ck.d, "ih_drafter_load_mlx: "));
+  ih_drafter* r = drafter_new(target, ck.d);
+  ih_ctx* c = target->ctx;
+  const auto& d = r->d;
+  const int QH = d.n_q_heads, HD = d.head_dim;
+  int st = IH_OK;
+  auto run = [&](int s) { if (st == IH_OK) st = s; };
+  auto q4 = [&](const HostQ4& h, ih_qmat** q) {
+    run(ih_qmat_int4_create(c, h.w.data(), h.s.data(), h.b.data(), 1, h.N, h.K, q));
+  };
+  auto vec = [&](const std::vector<uint16_t>& v, uint16_t** p) {
+    run(dalloc_t(p, v.size()));
+    if (st == IH_OK)
+      run(hipMemcpy(*p, v.data(), v.size() * 2, hipMemcpyHostToDevice) == hipSuccess
+              ? IH_OK : fail(IH_EDEVICE, "ih_drafter_load_mlx: upload failed"));
+  };
+  for (int l = 0; l < d.n_layers && st == IH_OK; ++l) {
+    ih_drafter_layer& L = r->layers[l];
+    const DrafterLayerCkpt& K = ck.layers[l];
+    vec(K.n1, &L.n1);
+    vec(K.n2, &L.n2);
+    vec(K.qn, &L.qn);
+    vec(K.kn, &L.kn);
+    q4(K.qkv, &L.qkv);
+    q4(K.qkv.rows(QH * HD, 2 * DKVH * HD), &L.kv);
+    q4(K.o, &L.o);
+    q4(K.gu, &L.gu);
+    q4(K.down, &L.down);
+    if (d.dyn_conv) {
+      q4(K.aproj, &L.aproj);
+      q4(K.mproj, &L.mproj);
+      vec(K.abase, &L.abase);
+      vec(K.mbase, &L.mbase);
+    }
+  }
+  q4(ck.fc, &r->fc);
+  vec(ck.hnorm, &r->hnorm);
+  vec(ck.fnorm, &r->fnorm);
+  if (d.rank > 0) {
+    q4(ck.hproj, &r->hproj);
+    vec(ck.pred, &r->pred);
+    vec(ck.succ, &r->succ);
+  }
+  return drafter_finish(r, st, out);
 }
 
 int ih_drafter_free(ih_drafter* r) {
@@ -754,6 +828,12 @@ int ih_drafter_block(ih_drafter* r, uint32_t* vtok_dev, int P, const uint32_t* s
 const uint16_t* ih_drafter_captures_dev(const ih_drafter* r) { return r ? r->caps : nullptr; }
 
 int ih_drafter_block_rows(const ih_drafter* r) { return r ? r->d.block : 0; }
+
+int ih_drafter_describe(const ih_drafter* r, ih_drafter_desc* out) {
+  IH_CHECK(r && out, IH_EINVAL, "ih_drafter_describe: null argument");
+  *out = r->d;
+  return IH_OK;
+}
 
 }  // extern "C"
 

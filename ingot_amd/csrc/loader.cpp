@@ -17,6 +17,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -25,6 +26,7 @@
 #include <string>
 #include <vector>
 
+#include "drafter_ckpt.h"
 #include "model_internal.h"
 
 namespace ih {
@@ -739,11 +741,213 @@ int describe(const std::string& dir, Config& cfg, Store& st, std::string& root) 
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------------------------------------------
+// DFlash2 drafter checkpoints (DFlash2Drafter.init, Sources/Ingot/Drafter.swift:114-256): config.json with
+// dflash_config (target_layer_ids, mask_token_id, block_size) and the qwen3 fields, layers.N.* without a model
+// prefix, fc, hidden_norm, norm and DFlash2's candidate_selector.{hidden_projection, predecessor_codebook,
+// successor_codebook} and {attention,mlp}_conv.{kernel_projection, base_kernel}. Projections are bf16 and quantized to
+// int4 g64 here, or already MLX int4 g64 (weight/scales/biases), taken as they are.
+
+HostQ4 HostQ4::rows(int r0, int n) const {
+  HostQ4 o;
+  o.N = n;
+  o.K = K;
+  const size_t wr = size_t(K) / 8, gr = size_t(K) / 64;
+  o.w.assign(w.begin() + r0 * wr, w.begin() + (r0 + n) * wr);
+  o.s.assign(s.begin() + r0 * gr, s.begin() + (r0 + n) * gr);
+  o.b.assign(b.begin() + r0 * gr, b.begin() + (r0 + n) * gr);
+  return o;
+}
+
+void HostQ4::append(const HostQ4& o) {
+  if (N == 0) K = o.K;
+  N += o.N;
+  w.insert(w.end(), o.w.begin(), o.w.end());
+  s.insert(s.end(), o.s.begin(), o.s.end());
+  b.insert(b.end(), o.b.begin(), o.b.end());
+}
+
+// Per row and group of 64: scale = bf16((max − min)/15), bias = bf16(min), q = round((w − bias)/scale) clamped to
+// 0…15 (0 when the scale is 0), rounding half away from zero; packed low nibble first.
+void quantize_int4_g64(const uint16_t* src, int N, int K, HostQ4& out) {
+  out.N = N;
+  out.K = K;
+  out.w.assign(size_t(N) * K / 8, 0u);
+  out.s.assign(size_t(N) * K / 64, 0);
+  out.b.assign(size_t(N) * K / 64, 0);
+  float v[64];
+  for (int n = 0; n < N; ++n)
+    for (int g = 0; g < K / 64; ++g) {
+      const size_t base = size_t(n) * K + size_t(g) * 64;
+      float mn = INFINITY, mx = -INFINITY;
+      for (int j = 0; j < 64; ++j) {
+        v[j] = bf16_to_f32(src[base + j]);
+        mn = std::min(mn, v[j]);
+        mx = std::max(mx, v[j]);
+      }
+      const uint16_t sb = f32_to_bf16((mx - mn) / 15.0f), bb = f32_to_bf16(mn);
+      const float sc = bf16_to_f32(sb), bi = bf16_to_f32(bb);
+      const size_t gi = size_t(n) * (K / 64) + g;
+      out.s[gi] = sb;
+      out.b[gi] = bb;
+      for (int j = 0; j < 64; ++j) {
+        const float q = sc > 0 ? std::min(15.0f, std::max(0.0f, std::round((v[j] - bi) / sc))) : 0.0f;
+        out.w[base / 8 + j / 8] |= uint32_t(q) << (4 * (j % 8));
+      }
+    }
+}
+
+namespace {
+// One projection of the drafter as int4: `name`.weight in bf16 [N, K] (quantized), or an MLX int4 g64 layer.
+bool drafter_q4(const Store& st, const std::string& name, int N, int K, HostQ4& out, std::string& err) {
+  const Tensor* w = st.find(name + ".weight");
+  if (!w) { err = "missing tensor " + name + ".weight"; return false; }
+  if (const Tensor* s = st.find(name + ".scales")) {
+    const Tensor* b = st.find(name + ".biases");
+    if (w->dtype != "U32" || s->dtype != "BF16" || !b || b->dtype != "BF16" || w->shape != std::vector<int64_t>{N, K / 8} ||
+        s->shape != std::vector<int64_t>{N, K / 64} || b->shape != s->shape) {
+      err = name + ": expected MLX int4 g64 [" + std::to_string(N) + ", " + std::to_string(K) + "]";
+      return false;
+    }
+    out.N = N;
+    out.K = K;
+    out.w.resize(size_t(N) * K / 8);
+    out.s.resize(size_t(N) * K / 64);
+    out.b.resize(out.s.size());
+    std::memcpy(out.w.data(), w->data, out.w.size() * 4);
+    std::memcpy(out.s.data(), s->data, out.s.size() * 2);
+    std::memcpy(out.b.data(), b->data, out.b.size() * 2);
+    return true;
+  }
+  if (w->dtype != "BF16" || w->shape != std::vector<int64_t>{N, K}) {
+    err = name + ".weight: expected bf16 [" + std::to_string(N) + ", " + std::to_string(K) + "], found " + w->dtype +
+          " " + shape_str(w->shape);
+    return false;
+  }
+  std::vector<uint16_t> raw(size_t(N) * K);
+  std::memcpy(raw.data(), w->data, raw.size() * 2);
+  quantize_int4_g64(raw.data(), N, K, out);
+  return true;
+}
+}  // namespace
+
+int read_drafter_mlx(const std::string& dir, const ih_model_desc& t, DrafterCkpt& out) {
+  const char* who = "ih_drafter_load_mlx: ";
+  std::string txt, jerr;
+  if (!read_file(dir + "/config.json", txt)) return fail(IH_EINVAL, who + std::string("no config.json in ") + dir);
+  Json cj;
+  if (!parse_json(txt.data(), txt.size(), cj, jerr) || cj.kind != Json::OBJ)
+    return fail(IH_EINVAL, who + std::string("config.json: ") + jerr);
+  const Json* dc = cj.get("dflash_config");
+  if (!dc || dc->kind != Json::OBJ) return fail(IH_EINVAL, who + std::string("config.json without dflash_config"));
+  Store st;
+  if (!st.open_dir(dir)) return fail(IH_EINVAL, who + st.err);
+  ih_drafter_desc& d = out.d;
+  d = ih_drafter_desc{};
+  d.hidden = int(num_or(cj, "hidden_size", 0));
+  d.n_layers = int(num_or(cj, "num_hidden_layers", 0));
+  d.n_q_heads = int(num_or(cj, "num_attention_heads", 0));
+  d.head_dim = int(num_or(cj, "head_dim", 128));
+  d.intermediate = int(num_or(cj, "intermediate_size", 0));
+  d.rms_eps = float(num_or(cj, "rms_norm_eps", 1e-6));
+  d.rope_theta = float(num_or(cj, "rope_theta", 1e6));
+  d.mask_token = uint32_t(num_or(*dc, "mask_token_id", -1));
+  IH_CHECK(d.hidden == t.hidden, IH_EINVAL,
+           who + std::string("hidden ") + std::to_string(d.hidden) + " vs the target's " + std::to_string(t.hidden));
+  IH_CHECK(num_or(cj, "num_key_value_heads", 0) == 8, IH_EINVAL, who + std::string("the drafter needs 8 KV heads"));
+  if (const Json* ab = cj.get("attention_bias"); ab && ab->kind == Json::BOOL && ab->b)
+    return fail(IH_EINVAL, who + std::string("attention biases are not supported in the drafter"));
+  if (const Json* mb = cj.get("mlp_bias"); mb && mb->kind == Json::BOOL && mb->b)
+    return fail(IH_EINVAL, who + std::string("MLP biases are not supported in the drafter"));
+  for (const char* k : {"rope_scaling", "rope_parameters"})
+    if (const Json* rs = cj.get(k); rs && rs->kind == Json::OBJ) {
+      const Json* ty = rs->get("rope_type") ? rs->get("rope_type") : rs->get("type");
+      if (ty && ty->str != "default") return fail(IH_EINVAL, who + std::string("a scaled RoPE is not supported in the drafter"));
+    }
+  const Json* ids = dc->get("target_layer_ids");
+  IH_CHECK(ids && ids->kind == Json::ARR && !ids->arr.empty() && ids->arr.size() <= IH_DRAFTER_MAX_TARGETS, IH_EINVAL,
+           who + std::string("dflash_config.target_layer_ids must list 1…8 layers"));
+  d.n_targets = int(ids->arr.size());
+  for (int j = 0; j < d.n_targets; ++j) d.target_layers[j] = int(ids->arr[size_t(j)].num);
+  // DFlash2 (a candidate selector) or DFlash v1 (each row's best candidate, block of 8, no conv).
+  const bool v2 = st.find("candidate_selector.hidden_projection.weight") != nullptr;
+  d.dyn_conv = v2 ? 1 : 0;
+  d.block = v2 ? int(num_or(*dc, "block_size", 0)) : 8;
+  d.window = int(num_or(cj, "sliding_window", 2048));
+  if (const Json* lt = cj.get("layer_types"); lt && lt->kind == Json::ARR)
+    for (const auto& x : lt->arr)
+      if (x.str == "full_attention" && !v2)
+        return fail(IH_EINVAL, who + std::string("per-layer context windows (full_attention layers) are not supported"));
+  const int H = d.hidden, HD = d.head_dim, QH = d.n_q_heads, I = d.intermediate, KVH = 8;
+  std::string err;
+  auto q4 = [&](const std::string& n, int N, int K, HostQ4& o) {
+    return drafter_q4(st, n, N, K, o, err) ? int(IH_OK) : fail(IH_EINVAL, who + err);
+  };
+  auto vec = [&](const std::string& n, int64_t cnt, std::vector<uint16_t>& o) {
+    return vec_bf16(st.find(n), cnt, o) ? int(IH_OK) : fail(IH_EINVAL, who + std::string("missing or malformed ") + n);
+  };
+  IH_CHECK(d.n_layers >= 1 && QH >= 8 && HD > 0 && I > 0, IH_EINVAL, who + std::string("incomplete config.json"));
+  out.layers.resize(d.n_layers);
+  for (int l = 0; l < d.n_layers; ++l) {
+    DrafterLayerCkpt& L = out.layers[l];
+    const std::string p = "layers." + std::to_string(l) + ".", a = p + "self_attn.";
+    IH_TRY(vec(p + "input_layernorm.weight", H, L.n1));
+    IH_TRY(vec(p + "post_attention_layernorm.weight", H, L.n2));
+    IH_TRY(vec(a + "q_norm.weight", HD, L.qn));
+    IH_TRY(vec(a + "k_norm.weight", HD, L.kn));
+    HostQ4 q, k, v, g, u;
+    IH_TRY(q4(a + "q_proj", QH * HD, H, q));
+    IH_TRY(q4(a + "k_proj", KVH * HD, H, k));
+    IH_TRY(q4(a + "v_proj", KVH * HD, H, v));
+    L.qkv = q;
+    L.qkv.append(k);
+    L.qkv.append(v);
+    IH_TRY(q4(a + "o_proj", H, QH * HD, L.o));
+    IH_TRY(q4(p + "mlp.gate_proj", I, H, g));
+    IH_TRY(q4(p + "mlp.up_proj", I, H, u));
+    L.gu = g;
+    L.gu.append(u);
+    IH_TRY(q4(p + "mlp.down_proj", H, I, L.down));
+    if (v2) {
+      const int DYN = 4 * (H / 16);
+      IH_TRY(q4(p + "attention_conv.kernel_projection", DYN, H, L.aproj));
+      IH_TRY(q4(p + "mlp_conv.kernel_projection", DYN, H, L.mproj));
+      IH_TRY(vec(p + "attention_conv.base_kernel", 4 * int64_t(H), L.abase));
+      IH_TRY(vec(p + "mlp_conv.base_kernel", 4 * int64_t(H), L.mbase));
+    }
+  }
+  IH_TRY(q4("fc", H, d.n_targets * t.hidden, out.fc));
+  IH_TRY(vec("hidden_norm.weight", H, out.hnorm));
+  IH_TRY(vec("norm.weight", H, out.fnorm));
+  if (v2) {
+    const Tensor* hp = st.find("candidate_selector.hidden_projection.weight");
+    d.rank = hp->shape.empty() ? 0 : int(hp->shape[0]);
+    IH_TRY(q4("candidate_selector.hidden_projection", d.rank, H, out.hproj));
+    // The codebooks may or may not carry the .weight suffix (DFlash2Drafter: the converters differ).
+    const std::string cb = st.find("candidate_selector.predecessor_codebook") ? "" : ".weight";
+    IH_TRY(vec("candidate_selector.predecessor_codebook" + cb, int64_t(t.vocab) * d.rank, out.pred));
+    IH_TRY(vec("candidate_selector.successor_codebook" + cb, int64_t(t.vocab) * d.rank, out.succ));
+  }
+  return IH_OK;
+}
+
 }  // namespace ih
 
 using namespace ih;
 
 extern "C" {
+
+int ih_quantize_int4_g64(const uint16_t* w_bf16, int N, int K, uint32_t* w, uint16_t* scales, uint16_t* biases) {
+  IH_CHECK(w_bf16 && w && scales && biases, IH_EINVAL, "ih_quantize_int4_g64: null argument");
+  IH_CHECK(N >= 1 && K >= 64 && K % 64 == 0, IH_EINVAL, "ih_quantize_int4_g64: N ≥ 1 and K a multiple of 64");
+  HostQ4 q;
+  quantize_int4_g64(w_bf16, N, K, q);
+  std::memcpy(w, q.w.data(), q.w.size() * 4);
+  std::memcpy(scales, q.s.data(), q.s.size() * 2);
+  std::memcpy(biases, q.b.data(), q.b.size() * 2);
+  return IH_OK;
+}
 
 int ih_mlx_describe(const char* dir, ih_model_desc* out) {
   IH_CHECK(dir && out, IH_EINVAL, "ih_mlx_describe: null argument");
