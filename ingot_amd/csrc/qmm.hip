@@ -562,11 +562,13 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       }
       __syncthreads();
       if (arrived != unsigned(nsp - 1)) return;  // workgroup-uniform
-      // Acquire at agent scope: the partial loads below are ordered after the arrival count that saw every split. The
-      // writers' side needs no release fence (an agent-scope release writes back the whole XCD L2, ~15 µs per launch):
-      // their partials bypass the L2 (sc1 stores) and each writer waited for its stores to complete (waitcnt 0) before
-      // its barrier and its count, so every partial is at the coherence point before the count that reports it.
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      // Ordering without agent-scope fences (an agent-scope release writes back the XCD's L2, ~15 µs per launch; an
+      // acquire, which invalidates the CU's caches, measured 0.14 ms per configuration-1 step): every writer's
+      // partials are agent-coherent stores (sc1: they bypass the XCD's L2), completed (waitcnt 0) before its barrier
+      // and its count, so they are at the coherence point before the count that reports them; the reads below are
+      // sc1 loads (they do not hit stale lines of this CU's caches), issued after the workgroup barrier that follows
+      // the count (a workgroup-scope acquire: the compiler cannot hoist them above it) and under the branch on the
+      // count's value (the hardware issues no load of a branch before the branch resolves).
       // The sums, in split order, into wave 0's partial slots (each thread reads back only slots it owns).
       for (int u = threadIdx.x; u < p.M * 4 * R; u += 64 * KW) {
         int i;
