@@ -111,6 +111,32 @@ def main() -> int:
     return 0
 
 
+def decode_loop(model, P: int, anchor: int) -> dict:
+    """Side measurement: the chained decode loop (ih_decode_greedy, decodeSpec's hot loop) from position P with
+    advancing positions (a cache of P + 1024 positions, the same synthetic history), copy-from-context drafts
+    (rows = 17) and plain one-row chained decoding (rows = 1), two rounds in flight. Host wall clock around each call
+    (the call synchronises); the first call of each kind warms up the recorded steps and is not reported."""
+    from ingot_amd._lib import KVCache
+
+    kv = KVCache(model, P + 1024)
+    kv.fill_synthetic(P, KV_SEED)
+    out = {"cache_positions": P + 1024, "key_chunk": kv.chunk}
+    for rows, ntok in ((17, 17 * 48), (1, 96)):
+        hist = np.full(P, anchor, np.uint32)  # the context the copy drafter indexes (the greedy chain's token)
+        kv.set_pos(P)
+        kv.decode_greedy(anchor, ntok, rows=rows, history=hist, inflight=2)
+        kv.set_pos(P)
+        t0 = time.perf_counter()
+        toks, st = kv.decode_greedy(anchor, ntok, rows=rows, history=hist, inflight=2)
+        dt = time.perf_counter() - t0
+        kv.set_pos(P)
+        out[f"rows{rows}"] = {"tokens": len(toks), "rounds": st.rounds, "accepted": st.accepted,
+                              "finish": st.finish, "ms": round(dt * 1e3, 2),
+                              "ms_per_round": round(dt * 1e3 / max(st.rounds, 1), 4), "tok_s": round(len(toks) / dt, 1)}
+    kv.free()
+    return out
+
+
 def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bool) -> dict:
     """Builds one configuration's model and cache, times `steps` verify rounds and returns the JSON line's fields."""
     from ingot_amd._lib import HipEvents, KVCache, Model, ModelDesc, check, lib
@@ -271,6 +297,10 @@ def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bo
         if traffic is not None:
             roofline["traffic"] = traffic
 
+    loop = None
+    if config == "dense8b-8k" and profile:
+        loop = decode_loop(model, P, ANCHOR)
+
     cpu_res = None
     if cpu:
         cpu_res = cpu_baseline(desc, P, blocks[k] if blocks is not None else np.full(B, ANCHOR, np.uint32), kv)
@@ -304,6 +334,8 @@ def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bo
         "roofline": roofline,
         "cpu_baseline": cpu_res,
     }
+    if loop is not None:
+        out["decode_loop"] = loop
     if U is not None:
         out["moe_distinct_experts_per_layer"] = {"mean": round(float(np.mean(U)), 2), "min": min(U), "max": max(U)}
     if copy_n:

@@ -20,6 +20,7 @@ using namespace ih;
 namespace {
 
 constexpr int REC_RING = 8;  // records of the rounds in flight (≥ inflight + 1)
+constexpr int kPosBucket = 256;  // positions of one chained-step range bucket (graph replay across rounds)
 
 // Device and host buffers of one decode call, released on every exit path.
 struct DecodeBuffers {
@@ -159,7 +160,12 @@ int decode(ih_model* m, ih_kv* kv, const uint32_t* history, int n_history, uint3
       } else if (B > 1) {
         IH_TRY(launch_copy_lookup(c, bf.hist, cap + 1, B - 1, min_match, max_match, bf.copy, bf.vtok, B, bf.st));
       }
-      IH_TRY(ih_verify_step_chained(m, kv, bf.vtok, B, bf.top1, bf.st, pos_min, pos_max));
+      // The step's launches are sized for a position range; the range is widened to whole 256-position buckets
+      // (within the cache) so that consecutive rounds present the same range and the step recorded for it replays
+      // (the launched attention splits past the device position exit at once).
+      const int lo = pos_min / kPosBucket * kPosBucket;
+      const int hi = std::max(pos_max, std::min((pos_max / kPosBucket + 1) * kPosBucket - 1, cap - B));
+      IH_TRY(ih_verify_step_chained(m, kv, bf.vtok, B, bf.top1, bf.st, lo, hi));
       if (sp) {
         IH_TRY(launch_topk64(c, ih_model_logits_dev(m), d.vocab, B, d.vocab, sp->temp, bf.cidx, bf.cval, bf.cz));
         IH_TRY(launch_accept_sample(c, bf.st, bf.vtok, bf.cidx, bf.cval, bf.cz, rec_dev, bf.rnd, *sp, REC_RING,
