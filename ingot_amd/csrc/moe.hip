@@ -106,6 +106,7 @@ struct GatherParams {
   float limit;
   const uint16_t* bias;    // bf16; GM_GLU: [E][2·(N/2)] gate then up; GM_DOWN: [E][N]; null: none
   unsigned kmask, kbias;
+  int trips;               // ring trips of D K-blocks per wave: ⌈⌈nkb / GKW⌉ / D⌉ (set by the launch)
 };
 
 constexpr int GKW = 4;  // waves per workgroup (K split)
@@ -118,12 +119,19 @@ template <int FMT, int R>
 struct GStage {
   u32x4 w[R];
   uint2 s[R];  // int4 (both kernel formats): (s0|b0<<16, s1|b1<<16); mxfp4: .x = four e8m0 bytes
-  u32x4 x[2][4];
+  u32x4 x[4];  // one token tile's activation fragments of the K-block
 };
 
 // R row tiles × (one slot of the round): grid (Npad/(16·R), slots), 64·GKW threads. The R tiles of a wave share each x
 // fragment, and a workgroup streams R times the bytes behind its one read of the slot's routing entry.
-template <int FMT, int R>
+//
+// Wave w takes K-blocks w, w + GKW, w + 2·GKW, … through a ring of D stages, all D requested at entry, and the stage
+// just multiplied refilled D·GKW K-blocks ahead. Many slots run at D = 1: the registers of deeper rings cost waves
+// per SIMD, and other workgroups' waves hide a stage's latency better (the launch picks D). K-blocks past the matrix
+// load as zeros (out-of-range buffer offsets: no memory traffic) and add exactly nothing. A slot with more than 16
+// pairs (one expert chosen by more than 16 rows) runs the K loop again for its second token tile, so the ring holds
+// one token tile's activations.
+template <int FMT, int R, int D>
 __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
   constexpr bool I4 = FMT != QF_MXFP4, XH = FMT == GF_INT4_F16;  // int4 codes; fp16 activations for them
   const int u = blockIdx.y;
@@ -145,7 +153,7 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, qd = lane >> 4;
   const int tile0 = blockIdx.x * R;
-  const bool two = cnt > 16;  // second token tile (uniform)
+  const int ntt = cnt > 16 ? 2 : 1;  // token tiles (uniform)
   __shared__ float rsc[MAX_TOK];
   __shared__ int arow_s[MAX_TOK];
 
@@ -166,9 +174,8 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
     arow_s[j] = j < cnt ? (p.x_row ? p.x_row[start + j] : start + j) : 0;
   }
 
-  auto load = [&](GStage<FMT, R>& st, int kb) {
+  auto load = [&](GStage<FMT, R>& st, int kb, unsigned xo) {
     const unsigned oob = kb < p.nkb ? 0u : OOB;
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const unsigned tk = unsigned(r * p.nkb + kb);
@@ -181,17 +188,11 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
     }
     const unsigned kx = unsigned(kb) * unsigned(p.x_tokens / 16) * 4096u;  // [kb][tile][t][1 KB]
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      st.x[0][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xoff[0] + kx + 1024 * t) | oob, 0, 0));
-      st.x[1][t] = two ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xoff[1] + kx + 1024 * t) | oob, 0, 0))
-                       : u32x4{0u, 0u, 0u, 0u};
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    for (int t = 0; t < 4; ++t)
+      st.x[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (xo + kx + 1024 * t) | oob, 0, 0));
   };
 
-  f32x4 acc[R][2];
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r][0] = acc[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[R];
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
   const unsigned shv[3] = {vgpr_of(4u), vgpr_of(8u), vgpr_of(12u)};  // 64-bit nibble shifts (nib_bf16_pair)
   // One MFMA step in the activations' type (bf16, or fp16 for XH); the operands travel as raw 32-bit words.
@@ -209,17 +210,10 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
       const unsigned one = XH ? 0x3C003C00u : 0x3F803F80u;
       const u32x4 ones = u32x4{one, one, one, one};
       constexpr float OFF = XH ? 1024.f : 128.f;
-      // Σx per group and token tile, shared by the R tiles.
-      f32x4 xs[2][2];
+      // Σx per group, shared by the R tiles.
+      f32x4 xs[2];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        if (tt == 1 && !two) continue;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          f32x4 z = mma(st.x[tt][2 * g], ones, f32x4{0.f, 0.f, 0.f, 0.f});
-          xs[tt][g] = mma(st.x[tt][2 * g + 1], ones, z);
-        }
-      }
+      for (int g = 0; g < 2; ++g) xs[g] = mma(st.x[2 * g + 1], ones, mma(st.x[2 * g], ones, f32x4{0.f, 0.f, 0.f, 0.f}));
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const float s0 = bf16f(st.s[r].x & 0xFFFFu), s1 = bf16f(st.s[r].y & 0xFFFFu);
@@ -229,14 +223,10 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
           bf16x8 w0, w1;
           nib_bf16_pair(st.w[r][2 * g], st.w[r][2 * g + 1], km, kbias, shv, w0, w1);
           const float sg = g ? s1 : s0, cg = g ? c1 : c0;
+          f32x4 tmp = mma(st.x[2 * g], __builtin_bit_cast(u32x4, w0), f32x4{0.f, 0.f, 0.f, 0.f});
+          tmp = mma(st.x[2 * g + 1], __builtin_bit_cast(u32x4, w1), tmp);
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            if (tt == 1 && !two) continue;
-            f32x4 tmp = mma(st.x[tt][2 * g], __builtin_bit_cast(u32x4, w0), f32x4{0.f, 0.f, 0.f, 0.f});
-            tmp = mma(st.x[tt][2 * g + 1], __builtin_bit_cast(u32x4, w1), tmp);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) acc[r][tt][q] = fmaf(sg, tmp[q], fmaf(cg, xs[tt][g][q], acc[r][tt][q]));
-          }
+          for (int q = 0; q < 4; ++q) acc[r][q] = fmaf(sg, tmp[q], fmaf(cg, xs[g][q], acc[r][q]));
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -247,46 +237,47 @@ __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
         for (int t = 0; t < 4; ++t) {
           const f16x8 wf = e2m1_f16(st.w[r][t]);
           const float sc = e8m0f((st.s[r].x >> (8 * t)) & 0xFFu);
+          const f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, st.x[t]), wf,
+                                                                   f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            if (tt == 1 && !two) continue;
-            const f32x4 tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, st.x[tt][t]), wf,
-                                                                     f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) acc[r][tt][q] = fmaf(sc, tmp[q], acc[r][tt][q]);
-          }
+          for (int q = 0; q < 4; ++q) acc[r][q] = fmaf(sc, tmp[q], acc[r][q]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
 
-  // K-blocks wave, wave + GKW, …; two stages; single-exit loop (loads past the end read zeros).
-  GStage<FMT, R> a, b;
-  int kb = wave;
-  load(a, kb);
-  const int nk = kb < p.nkb ? (p.nkb - kb + GKW - 1) / GKW : 0;
-  for (int it = 0; it < nk / 2; ++it) {
-    load(b, kb + GKW);
-    compute(a);
-    load(a, kb + 2 * GKW);
-    compute(b);
-    kb += 2 * GKW;
+  // Waves' partial sums → LDS [wave][r][tt][q][lane], then added in wave order.
+  constexpr int WST = R * 2 * 4 * 64;
+  __shared__ float red[GKW * WST];
+#pragma unroll 1
+  for (int tt = 0; tt < ntt; ++tt) {
+    const unsigned xo = tt ? xoff[1] : xoff[0];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    GStage<FMT, R> st[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(st[d], wave + d * GKW, xo);
+    int kb = wave + D * GKW;
+#pragma unroll 1
+    for (int t = 0; t < p.trips; ++t) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        compute(st[d]);
+        // The last trip's refills lie past the matrix (trips·D·GKW ≥ nkb): zeros, no memory traffic.
+        load(st[d], kb + d * GKW, xo);
+      }
+      kb += D * GKW;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wave * WST + ((r * 2 + tt) * 4 + q) * 64 + lane] = acc[r][q];
   }
-  if (nk & 1) compute(a);
 
   // RMSNorm factors of the activation rows.
   if (p.ss_in) rms_factors(p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.nrows, rsc, wave, GKW, lane);
 
-  // Waves' partial sums → LDS [wave][r][tt][q][lane], then added in wave order.
-  constexpr int WST = R * 2 * 4 * 64;
-  __shared__ float red[GKW * WST];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) red[wave * WST + ((r * 2 + tt) * 4 + q) * 64 + lane] = acc[r][tt][q];
   __syncthreads();
   auto val = [&](int r, int j, int rn) {
     const int tt = j >> 4, jj = j & 15;
@@ -569,24 +560,29 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
   IH_CHECK(size_t(W->E) * p.tiles_per_e * 1024u < (size_t(1) << 31), IH_EINVAL,
            "gathered qmm: stacked matrix above 2 GiB");
   TimedLaunch tl(c, TC_MOE, bytes);
-  // Row tiles per workgroup (IH_GATHER_R: tuning override). Measured on the MoE configurations (i.i.d. routing): int4
-  // experts gain from two tiles sharing the x fragments (E128 top-8: 111 → 100 µs per layer), MXFP4 experts do not
-  // (E32 top-4: 120 µs at one tile, 140 at two, 132 at four); four tiles lose on both (fewer workgroups in flight).
+  // Row tiles per workgroup and ring depth, measured on the MoE configurations (i.i.d. routing, per step): two tiles
+  // sharing each x fragment beat one (E128 top-8 int4: 5.13 → 3.95 ms; E32 top-4 MXFP4: 2.64 → 2.32), four gain
+  // nothing over two; and with many slots a ring of one stage beats deeper ones (E128: 3.95 at D = 1, 4.47 at 2,
+  // 5.70 at 3): the stages' registers cost waves per SIMD, and the waves of other workgroups hide a stage's latency
+  // better than a wave's own second stage. A single slot (a router, or one expert) has few workgroups, and there
+  // every K-block of a wave is requested at entry.
   const int tiles = W->Npad / 16;
-  int R = 1;
-  if (W->format == QF_INT4 && tiles % 2 == 0 && (tiles / 2) * slots >= 2 * c->cu_count) R = 2;
-  if (const char* ov = getenv("IH_GATHER_R")) {
-    const int r = atoi(ov);
-    if ((r == 1 || r == 2 || r == 4) && tiles % r == 0) R = r;
-  }
+  const int kpw = (W->nkb + GKW - 1) / GKW;
+  int R = 1, D = 1;
+  if (tiles % 2 == 0 && (tiles / 2) * slots >= 2 * c->cu_count) R = 2;
+  if (slots == 1) D = kpw <= 1 ? 1 : (kpw <= 2 ? 2 : 4);
+  p.trips = (kpw + D - 1) / D;
   const dim3 grid(tiles / R, slots);
-#define IH_GATHER_LAUNCH(R_)                                                                                        \
-  if (R == R_) {                                                                                                  \
-    if (W->format == QF_MXFP4) tlaunch(tl, qmm_gather_kernel<QF_MXFP4, R_>, grid, dim3(64 * GKW), 0, c->stream, p); \
-    else if (x_f16) tlaunch(tl, qmm_gather_kernel<GF_INT4_F16, R_>, grid, dim3(64 * GKW), 0, c->stream, p);         \
-    else tlaunch(tl, qmm_gather_kernel<QF_INT4, R_>, grid, dim3(64 * GKW), 0, c->stream, p);                        \
+#define IH_GATHER_LAUNCH(R_, D_)                                                                                    \
+  if (R == R_ && D == D_) {                                                                                       \
+    if (W->format == QF_MXFP4)                                                                                    \
+      tlaunch(tl, qmm_gather_kernel<QF_MXFP4, R_, D_>, grid, dim3(64 * GKW), 0, c->stream, p);                    \
+    else if (x_f16)                                                                                               \
+      tlaunch(tl, qmm_gather_kernel<GF_INT4_F16, R_, D_>, grid, dim3(64 * GKW), 0, c->stream, p);                 \
+    else                                                                                                          \
+      tlaunch(tl, qmm_gather_kernel<QF_INT4, R_, D_>, grid, dim3(64 * GKW), 0, c->stream, p);                     \
   }
-  IH_GATHER_LAUNCH(1) IH_GATHER_LAUNCH(2) IH_GATHER_LAUNCH(4)
+  IH_GATHER_LAUNCH(1, 1) IH_GATHER_LAUNCH(1, 2) IH_GATHER_LAUNCH(1, 4) IH_GATHER_LAUNCH(2, 1)
 #undef IH_GATHER_LAUNCH
   IH_HIP(hipGetLastError());
   return IH_OK;
