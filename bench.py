@@ -75,7 +75,7 @@ def main() -> int:
     ap.add_argument("--cpu-baseline", action="store_true", help="also for the non-default configurations")
     ap.add_argument("--no-kernel-profile", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the side measurements (config 0's qmm, the other configurations' step times)")
+                    help="skip the side measurements (config 0's qmm, the decode loop, the other configurations' step times)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only copy BYTES device-to-device 4 times (the reference kernel that scales the HBM counters)")
     args = ap.parse_args()
@@ -90,7 +90,8 @@ def main() -> int:
 
     ctx = Context(0)
     want_cpu = not args.no_cpu_baseline and (args.config == "dense8b-8k" or args.cpu_baseline)
-    out = run_config(ctx, args.config, args.steps, args.warmup, profile=not args.no_kernel_profile, cpu=want_cpu)
+    out = run_config(ctx, args.config, args.steps, args.warmup, profile=not args.no_kernel_profile, cpu=want_cpu,
+                     extra=not args.no_extra)
     if not args.no_extra and args.config == "dense8b-8k":
         # Side measurements in the same run (not the headline `value`): config 0's single qmm, and the step time of
         # every other configuration (fewer steps each).
@@ -137,7 +138,7 @@ def decode_loop(model, P: int, anchor: int) -> dict:
     return out
 
 
-def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bool) -> dict:
+def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bool, extra: bool = False) -> dict:
     """Builds one configuration's model and cache, times `steps` verify rounds and returns the JSON line's fields."""
     from ingot_amd._lib import HipEvents, KVCache, Model, ModelDesc, check, lib
 
@@ -298,7 +299,7 @@ def run_config(ctx, config: str, steps: int, warmup: int, profile: bool, cpu: bo
             roofline["traffic"] = traffic
 
     loop = None
-    if config == "dense8b-8k" and profile:
+    if config == "dense8b-8k" and profile and extra:
         loop = decode_loop(model, P, ANCHOR)
 
     cpu_res = None

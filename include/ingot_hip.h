@@ -93,6 +93,13 @@ size_t ih_qmat_bytes(const ih_qmat* q);
 int ih_qmm_int4(ih_ctx* ctx, const ih_qmat* W, const void* x_bf16_dev, int ldx, int M, void* y_dev, int ldy,
                 int out_mode);
 
+/* Launch-shape override of the int4 qmm for one matrix size, for testing and tuning: every later product of an N×K
+ * matrix on this context runs R 16-row tiles per wave, KW waves per workgroup and kpw K-blocks of 128 per wave, with
+ * K split over ⌈K/128 / (KW·kpw)⌉ workgroups (reduced in the kernel by the last one of each row group to arrive);
+ * R = 0 removes the override. A shape that is not instantiated or does not tile the matrix makes those products fail
+ * with IH_EINVAL. No counterpart in the reference (one launch shape per kernel there). */
+int ih_qmm_shape_override(ih_ctx* ctx, int N, int K, int R, int KW, int kpw);
+
 
 /* ---- row kernels -------------------------------------------------------------------------------------------- */
 

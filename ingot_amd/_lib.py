@@ -127,6 +127,7 @@ def _declare(L: C.CDLL) -> None:
         "ih_drafter_block": (i32, [vp, vp, i32, vp, vp]),
         "ih_drafter_block_rows": (i32, [vp]),
         "ih_timing_enable": (i32, [vp, i32]),
+        "ih_qmm_shape_override": (i32, [vp, i32, i32, i32, i32, i32]),
         "ih_timing_read": (i32, [vp, i32, P(C.c_double), P(C.c_int), P(C.c_double)]),
     }
     for name, (res, args) in sig.items():

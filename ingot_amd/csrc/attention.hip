@@ -214,11 +214,6 @@ struct PieceRegs {
 // piece q is converted), each piece converted int8 → fp16 into one of two LDS buffers (K key-major, V transposed) and
 // multiplied while the later pieces are on their way; one barrier per piece (the buffer written for piece q + 2 was
 // last read for piece q, before the barrier of piece q + 1). Each wave runs its 16-query tiles over the piece with an online softmax in base 2.
-#ifdef IH_QMM_STAMP
-#define ASTAMP(i) do { astamp[wave][i] = unsigned(__builtin_amdgcn_s_memrealtime()); } while (0)
-#else
-#define ASTAMP(i) do { } while (0)
-#endif
 template <int HD, int TPW, bool RING, int NP>
 __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
   constexpr int NC = HD / 32;    // 32-dim chunks (MFMA K steps of Sᵀ)
@@ -235,13 +230,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 
   const AttnPos ap = attn_pos(a);
   const int P = ap.P;
-  const int sidx = blockIdx.x, split = sidx + ap.s0, kvh = blockIdx.y;
+  // Grid (KV head, split): consecutive workgroup ids go round-robin over the 8 XCDs, so with 8 KV heads every split of
+  // head h runs on XCD h and the head's queries are fetched into one L2 instead of all eight.
+  const int sidx = blockIdx.y, split = sidx + ap.s0, kvh = blockIdx.x;
   if (sidx >= ap.nsplit) return;  // launched for a later position than the step's (chained rounds): no keys
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
-#ifdef IH_QMM_STAMP
-  __shared__ unsigned astamp[8][32];
-#endif
-  ASTAMP(0);
   const int Q = a.G * a.B;
   // Keys [k0, k1) of the split. In a sliding-window layer every row's window starts at or after P − window + 1, so
   // the split starts there (rounded down to 64 keys, which keeps pieces and the 32-slot V blocks aligned): the keys
@@ -658,10 +651,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       __syncthreads();  // B0
       for (int i = 0; i < npairs; ++i) {
         const int q = 2 * i, b0 = 2 * (i & 1), kb0 = k0 + PIECE * q, kb1 = kb0 + PIECE;
-        if (q < 16) ASTAMP(2 + q);
         piece_products(b0, kb0, min(PIECE, k1 - kb0));
         if (q + 1 < npieces) piece_products(b0 + 1, kb1, min(PIECE, k1 - kb1));
-        if (q < 16) ASTAMP(3 + q);
         __syncthreads();  // B(i + 1)
       }
     }
@@ -678,10 +669,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
         load_piece(pr[1], min(q + 3, npieces - 1));
       }
       __syncthreads();
-      if (q < 16) ASTAMP(2 + q);
       piece_products(b0, kb0, min(PIECE, k1 - kb0));
       if (two) piece_products(b0 + 1, kb1, min(PIECE, k1 - kb1));
-      if (q < 16) ASTAMP(3 + q);
     }
   } else {
     for (int base = 0; base < npieces; base += NP) {
@@ -731,11 +720,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       }
     }
     __syncthreads();
-    ASTAMP(20);
-#ifdef IH_QMM_STAMP
-    if (a.stamp && kvh < 8 && sidx < 64 && blockIdx.z == 0 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
-      a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
-#endif
     if (half == 1) return;
     // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll
@@ -766,11 +750,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
       }
     }
   } else {
-    ASTAMP(20);
-#ifdef IH_QMM_STAMP
-    if (TPW != 0 && a.stamp && kvh < 8 && sidx < 64 && lane < 32)  // the stamp buffer holds [8][64][8 waves][32]
-      a.stamp[((size_t(kvh) * 64 + sidx) * 8 + wave) * 32 + lane] = astamp[wave][lane];
-#endif
     // Partials of this split: (max, sum) per query and O / sum in fp16 (lane holds dims 16dt + 4qd + r of query m).
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
@@ -890,9 +869,7 @@ int launch_prework(ih_ctx* c, const AttnArgs& a) {
   TimedLaunch tl(c, TC_PREWORK, double(a.B) * (a.QH + 2 * a.KVH) * a.HD * 4 + double(a.B) * a.KVH * (2 * a.HD + 4) +
                                     double(a.B) * a.QH * a.HD * 2);
   // One wave (one (head slot, token)) per workgroup (config 1: 2.306 against 2.312 ms per step with four).
-  // IH_PREWORK_WAVES: tuning override.
-  static const int pw = [] { const char* v = getenv("IH_PREWORK_WAVES"); return v ? atoi(v) : 1; }();
-  IH_CHECK(pw == 1 || pw == 2 || pw == 4, IH_EINVAL, "attention prework: 1, 2 or 4 waves per workgroup");
+  constexpr int pw = 1;
   dim3 grid((a.QH + 2 * a.KVH + pw - 1) / pw, a.B);
   if (a.HD == 128) tlaunch(tl, prework_kernel<128>, grid, dim3(64 * pw), 0, c->stream, a);
   else if (a.HD == 64) tlaunch(tl, prework_kernel<64>, grid, dim3(64 * pw), 0, c->stream, a);
@@ -912,30 +889,16 @@ static bool launch_attn_np(const TimedLaunch& tl, dim3 grid, hipStream_t st, con
   }
 }
 
-#ifdef IH_QMM_STAMP
-static unsigned long long* g_astamp = nullptr;
-extern "C" int ih_dbg_attn_stamp(void* dev) {
-  g_astamp = static_cast<unsigned long long*>(dev);
-  return 0;
-}
-#endif
 int launch_attention(ih_ctx* c, const AttnArgs& a0) {
   AttnArgs a = a0;
-#ifdef IH_QMM_STAMP
-  a.stamp = g_astamp;
-#endif
   const int Q = a.G * a.B;
   const int qtiles = (Q + 15) / 16;
   IH_CHECK(qtiles <= 16, IH_EINVAL, "attention: at most 256 query rows per KV head");
-  // Ring depth: pieces in flight per thread (IH_ATTN_RING: tuning override).
-  static const int ring_np = [] {
-    const char* v = getenv("IH_ATTN_RING");
-    return v ? std::max(1, std::min(MAX_PIECES, atoi(v))) : 2;
-  }();
-  const int np = std::min(ring_np, (a.C + PIECE - 1) / PIECE);
+  // Ring depth: two pieces in flight per thread (one when the split is a single piece).
+  const int np = std::min(2, (a.C + PIECE - 1) / PIECE);
   // The tile layout follows the model's largest block (Qpad rows), never this step's rows: see attn_kernel.
   const int tpw = a.Qpad <= 80 ? 0 : qtiles > 8 ? 2 : 1;
-  dim3 grid(a.nsplit, a.KVH, tpw == 0 ? (qtiles + 4) / 5 : 1);
+  dim3 grid(a.KVH, a.nsplit, tpw == 0 ? (qtiles + 4) / 5 : 1);
   // Algorithmic bytes: the int8 K and V and their fp16 scales of every key the launched splits cover, and q.
   const double keys = double(a.P + a.B) - double(a.s0) * a.C;
   TimedLaunch tl(c, TC_ATTN, double(a.KVH) * keys * (2 * a.HD + 4) + double(a.KVH) * Q * a.HD * 2);
@@ -964,9 +927,8 @@ int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
   IH_CHECK(a.QH % 4 == 0, IH_EINVAL, "attention reduce: the q head count must be a multiple of 4");  // rw ≤ 4
   TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (2 * a.HD + 8) + double(a.B) * a.QH * a.HD * 2);
   // One wave (one (row, q head)) per workgroup: 4·B·QH/4 small workgroups spread over more CUs than four-wave ones
-  // (config 1: 0.146 against 0.149 ms per step). IH_REDUCE_WAVES: tuning override.
-  static const int rw = [] { const char* v = getenv("IH_REDUCE_WAVES"); return v ? atoi(v) : 1; }();
-  IH_CHECK(rw == 1 || rw == 2 || rw == 4, IH_EINVAL, "attention reduce: 1, 2 or 4 waves per workgroup");
+  // (config 1: 0.146 against 0.149 ms per step).
+  constexpr int rw = 1;
   const dim3 grid(a.B, a.QH / rw);
   uint4* of = static_cast<uint4*>(out.frag);
   if (a.HD == 128) tlaunch(tl, attn_reduce_kernel<128>, grid, dim3(64 * rw), 0, c->stream, a, of, out.nkb, out.ntile);

@@ -46,7 +46,6 @@ struct AttnArgs {
   const uint32_t* pos_dev;
   uint32_t* flag_dev;
   int pos_min, pos_max;
-  unsigned long long* stamp;  // clock stamps of an instrumented build ([KV head][split][wave][32]), else unused
 };
 
 // The step's position and its key splits: P, the first split s0 (a sliding-window layer starts at the split of the

@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <cstddef>
 #include <string>
+#include <array>
 #include <vector>
 
 #include "../../include/ingot_hip.h"
@@ -148,6 +149,8 @@ struct ih_ctx {
   // Chunk lists of the top-64 candidates (sampling), grown on demand.
   void* samp = nullptr;
   size_t samp_bytes = 0;
+  // qmm launch shapes set by ih_qmm_shape_override: {N, K, R, KW, kpw, kpw1}.
+  std::vector<std::array<int, 6>> qmm_shapes;
 };
 
 namespace ih {

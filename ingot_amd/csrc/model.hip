@@ -634,7 +634,6 @@ int ih_kv_create_chunked(ih_model* m, int capacity, int chunk, ih_kv** out) {
   const int per_head = std::max(1, m->ctx->cu_count / std::max(1, d.n_kv_heads));
   int C = (capacity + per_head - 1) / per_head;
   C = std::max(64, (C + 63) / 64 * 64);
-  if (const char* ov = getenv("IH_ATTN_CHUNK")) C = std::max(32, atoi(ov) / 32 * 32);  // tuning override
   if (chunk) C = chunk;
   kv->chunk = C;
   const int L = d.n_layers, KVH = d.n_kv_heads, HD = d.head_dim;

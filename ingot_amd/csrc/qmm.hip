@@ -118,8 +118,6 @@ struct QmmParams {
   int nsplit;
   // K split over workgroups with a fused epilogue: arrival counters, one per row group (zero between launches).
   unsigned* ctr;
-  unsigned long long* stamp;  // clock stamps of an instrumented build ([workgroup][wave][32]), else unused
-  int noload;                 // instrumented build: skip the weight and x loads
 };
 
 // The epilogue of the R tiles tile0 … tile0+R−1 of a workgroup of nthr threads, given val(m, r, rn) = the finished
@@ -226,16 +224,6 @@ __device__ __forceinline__ void qmm_epilogue(const QmmParams& p, int tile0, V va
 // p.part and qmm_finish_kernel adds the splits in order. No atomics and no cross-workgroup fences (an agent-scope
 // release on MI355X writes back the XCD's L2: ~15 µs per launch), and a row's summation order depends only on
 // (N, K), never on M.
-#ifdef IH_QMM_STAMP
-// Instrumented build: wave-private clock stamps (low 32 bits of the 100 MHz real-time counter) kept in LDS and written
-// out once at the end, so that the stamps add no live registers to the main loop.
-#define QSTAMP(i)                                                                                               \
-  do {                                                                                                          \
-    if constexpr (T == 1) qstamp_lds[wave][i] = unsigned(__builtin_amdgcn_s_memrealtime());                     \
-  } while (0)
-#else
-#define QSTAMP(i) do { } while (0)
-#endif
 // KPW1 > 0: the second half of the waves (the second wave of each SIMD at KW = 8) take KPW1 K-blocks each instead of
 // KPW. A CU's loads come back roughly in issue order, so those waves receive their first stage after the first half's
 // first two stages; with fewer K-blocks they still end with the first half.
@@ -245,10 +233,6 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   // The wave index is uniform: readfirstlane keeps it (and everything derived from it) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n = lane & 15, qd = lane >> 4;
-#ifdef IH_QMM_STAMP
-  __shared__ unsigned qstamp_lds[KW][32];
-#endif
-  QSTAMP(0);
   const int tile0 = blockIdx.x * R;
   constexpr int nk = KPW;                                // K-blocks of a wave of the first half (the LDS stride)
   constexpr int HALF = KW / 2;
@@ -256,12 +240,7 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   const int kwg = int(blockIdx.y) * (KPW1 ? HALF * (KPW + KPW1) : KW * nk);  // first K-block of the workgroup
   const int kb0 = kwg + (KPW1 == 0 ? wave * nk : wave < HALF ? wave * KPW : HALF * KPW + (wave - HALF) * KPW1);
   const unsigned tiles_total = unsigned(p.Npad / 16) * unsigned(p.nkb);
-#ifdef IH_QMM_STAMP
-  // Instrumented build: with p.noload the weight and x loads read nothing (compute and launch cost alone).
-  const unsigned wlim = (p.noload & 1) ? 0u : tiles_total * 1024u, xlim = (p.noload & 2) ? 0u : unsigned(MAX_TOK) * p.nkb * 256u;
-#else
   const unsigned wlim = tiles_total * 1024u, xlim = unsigned(MAX_TOK) * p.nkb * 256u;
-#endif
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, wlim), rsb = make_rsrc(p.s, tiles_total * 128u),
                                rx = make_rsrc(p.xa, xlim);
   const unsigned km = vgpr_of(p.kmask), kbias = p.kbias;
@@ -350,7 +329,6 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
   if constexpr (RMS_PRE) {
     if (p.ss_in) rms_finish(rpf, p.ss_in, SS_CAP, p.nss_in, p.D, p.eps, p.M, rsc, wave, KW, lane);
   }
-  QSTAMP(18);
 
 #pragma unroll
   for (int j = 0; j < NSB; ++j) {
@@ -368,7 +346,6 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     }
   }
 
-  QSTAMP(19);
   f32x4 acc[R][T];
   float acc16[R];
 #pragma unroll
@@ -461,16 +438,13 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
     for (int d = 0; d < D; ++d) {
       compute(d, i + d);
       load_stage(d, kb0 + i + d + D);
-      QSTAMP(2 + ((i + d) & 15));
     }
   }
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     compute(d, i + d);
-    QSTAMP(2 + ((i + d) & 15));
   }
 
-  QSTAMP(1);
   // Partial sums of every wave → LDS [wave][r][tt][e][lane] (+ token 16 [wave][r][row]), then fixed-order sums.
   constexpr int NEL = R * T * 4 * 64;
   constexpr int NEL16 = X16 ? R * 16 : 0;
@@ -588,15 +562,8 @@ __global__ __launch_bounds__(64 * KW) void qmm_int4_kernel(QmmParams p) {
       }
       __syncthreads();
     }
-    QSTAMP(26);
     qmm_epilogue<R, MODE>(p, tile0, val, rsc, ssu, 64 * KW, blockIdx.x, &hpf);
   }
-  QSTAMP(27);
-#ifdef IH_QMM_STAMP
-  if constexpr (T == 1)
-    if (p.stamp && blockIdx.x < 256 && blockIdx.y == 0 && lane < 32)  // the stamp buffer holds 256 × 16 waves
-      p.stamp[(size_t(blockIdx.x) * 16 + wave) * 32 + lane] = qstamp_lds[wave][lane];
-#endif
 }
 
 // Adds the split partial sums in split order and runs the epilogue: workgroup = 4 tiles (64 rows), 256 threads.
@@ -759,16 +726,6 @@ int launch_act_from_f32(ih_ctx* c, const float* x, int ldx, int M, ActBuf& a) {
   return IH_OK;
 }
 
-#ifdef IH_QMM_STAMP
-static unsigned long long* g_stamp = nullptr;
-static int g_stamp_n = -1, g_stamp_k = -1;
-extern "C" int ih_dbg_qmm_stamp(void* dev, int N, int K) {
-  g_stamp = static_cast<unsigned long long*>(dev);
-  g_stamp_n = N;
-  g_stamp_k = K;
-  return 0;
-}
-#endif
 
 int qmm_grid(const ih_qmat* W) {
   const QmmShape sh = qmm_shape(W->Npad, W->nkb);
@@ -801,23 +758,10 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   IH_CHECK(M >= 1 && M <= MAX_TOK, IH_EINVAL, "qmm: M must be in 1..32");
   IH_CHECK(a.nkb == W->nkb && !a.f16, IH_EINVAL, "qmm: activation K does not match the matrix");
   QmmShape sh = qmm_shape(W->Npad, W->nkb);
-  // Tuning overrides: IH_QMM_SHAPE = "R,KW,kpw" for every matrix, IH_QMM_SHAPES = "N:K=R,KW,kpw;…" per matrix.
-  auto apply = [&](int R, int KW, int kpw, int kpw1) {
-    const int span = kpw1 ? KW / 2 * (kpw + kpw1) : KW * kpw;
-    sh = QmmShape{R, KW, kpw1 ? 2 : qmm_ring_depth(kpw), kpw, std::max(1, W->nkb / std::max(1, span)), kpw1};
-  };
-  int oR, oKW, okpw, okpw1 = 0;
-  if (const char* ov = getenv("IH_QMM_SHAPE")) {
-    const int nf = sscanf(ov, "%d,%d,%d,%d", &oR, &oKW, &okpw, &okpw1);
-    if (nf >= 3) apply(oR, oKW, okpw, nf == 4 ? okpw1 : 0);
-  }
-  if (const char* ov = getenv("IH_QMM_SHAPES")) {
-    for (const char* q = ov; q && *q; q = strchr(q, ';') ? strchr(q, ';') + 1 : nullptr) {
-      int n, k;
-      okpw1 = 0;
-      const int nf = sscanf(q, "%d:%d=%d,%d,%d,%d", &n, &k, &oR, &oKW, &okpw, &okpw1);
-      if (nf >= 5 && n == W->N && k == W->K) apply(oR, oKW, okpw, nf == 6 ? okpw1 : 0);
-    }
+  for (const auto& o : c->qmm_shapes) {
+    if (o[0] != W->N || o[1] != W->K) continue;
+    const int span = o[5] ? o[3] / 2 * (o[4] + o[5]) : o[3] * o[4];
+    sh = QmmShape{o[2], o[3], o[5] ? 2 : qmm_ring_depth(o[4]), o[4], std::max(1, W->nkb / std::max(1, span)), o[5]};
   }
   IH_CHECK(qmm_shape_ok(sh, W->Npad, W->nkb), IH_EINVAL, "qmm: launch shape does not tile the matrix");
   const int ks = sh.ks;
@@ -841,10 +785,6 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   p.kmask = 0x000F000Fu;
   p.kbias = 0x43004300u;
   p.nsplit = ks;
-#ifdef IH_QMM_STAMP
-  p.stamp = (W->N == g_stamp_n && W->K == g_stamp_k) ? g_stamp : nullptr;
-  p.noload = getenv("IH_QMM_NOLOAD") ? atoi(getenv("IH_QMM_NOLOAD")) : 0;  // 1: no weight loads, 2: no x loads
-#endif
   if (ep.mode == QM_F32_SCALE || ep.mode == QM_GLU_ACT) {
     IH_CHECK(a.ss && a.nss > 0, IH_EINVAL, "qmm: the input activation carries no RMSNorm sums");
     p.ss_in = a.ss;
@@ -1006,6 +946,19 @@ int ih_qmat_free(ih_qmat* q) {
 }
 
 size_t ih_qmat_bytes(const ih_qmat* q) { return q ? q->algo_bytes * q->E : 0; }
+
+int ih_qmm_shape_override(ih_ctx* c, int N, int K, int R, int KW, int kpw) {
+  IH_CHECK(c && N >= 1 && K >= 64, IH_EINVAL, "ih_qmm_shape_override: null context or empty matrix");
+  IH_CHECK(R >= 0 && KW >= 0 && kpw >= 0, IH_EINVAL, "ih_qmm_shape_override: negative shape");
+  auto& v = c->qmm_shapes;
+  for (size_t i = 0; i < v.size();) {
+    if (v[i][0] == N && v[i][1] == K) v.erase(v.begin() + i);
+    else ++i;
+  }
+  if (R > 0) v.push_back({N, K, R, KW, kpw, 0});
+  ++c->gen;  // recorded steps launched the previous shapes
+  return IH_OK;
+}
 
 int ih_qmm_int4(ih_ctx* c, const ih_qmat* W, const void* x, int ldx, int M, void* y, int ldy, int out_mode) {
   IH_CHECK(c && W && x && y, IH_EINVAL, "ih_qmm_int4: null argument");

@@ -91,6 +91,7 @@ _SIGS = [
     ("or_copy_index_propose", i32, [vp, i32, vp, vp]),
     ("or_splitmix64", None, [C.c_uint64, i32, vp]),
     ("or_model_set_capture", None, [vp, i32, vp]),
+    ("or_model_tie_head", None, [vp]),
     ("or_model_captures", None, [vp, vp]),
     ("or_drafter_create", vp, [vp, C.c_uint64, vp, C.c_uint64]),
     ("or_drafter_free", None, [vp]),
@@ -310,6 +311,10 @@ class OracleModel:
         top1 = np.empty(len(t), np.uint32)
         assert lib().or_model_verify(self.h, _p(t), len(t), _p(logits), _p(top1)) == 0
         return logits, top1
+
+    def tie_head(self):
+        """The head becomes the embedding table (tie_word_embeddings)."""
+        lib().or_model_tie_head(self.h)
 
     def set_capture(self, layers):
         self.cap_layers = np.ascontiguousarray(layers, np.int32)

@@ -722,6 +722,12 @@ static void capture(OrModel* m, int l, const float* hres, int B) {
   }
 }
 
+// tie_word_embeddings: the head is the embedding table itself (Sources/Ingot/Model.swift:269-276).
+void or_model_tie_head(void* h) {
+  OrModel* m = static_cast<OrModel*>(h);
+  m->head = m->embed;
+}
+
 void or_model_set_capture(void* h, int n, const int* layers) {
   OrModel* m = static_cast<OrModel*>(h);
   m->cap_layers.assign(layers, layers + n);

@@ -12,6 +12,8 @@ import sys
 from pathlib import Path
 
 import numpy as np
+
+import oracle
 import pytest
 
 from ingot_amd._lib import IngotError, KVCache, Model, ModelDesc, describe_mlx
@@ -145,8 +147,9 @@ def test_loaded_model_equals_synthetic(ctx, tmp_path, shape, shards, pad):
 
 @pytest.mark.gpu
 def test_tied_head_is_the_embedding(ctx, tmp_path):
-    """tie_word_embeddings: the head is the embedding table. The same checkpoint with lm_head written as an explicit
-    copy of embed_tokens loads into bit-identical logits, and differs from the synthetic model's own head."""
+    """tie_word_embeddings: the head is the embedding table. The tied checkpoint's logits match the oracle with its
+    head replaced by the embedding (within the dense tolerance, top-1 equal outside near ties), and the same checkpoint
+    with lm_head written as an explicit copy of embed_tokens loads into bit-identical logits."""
     write_checkpoint(tmp_path / "tied", DENSE, seed=7, tied=True)
     untied = write_checkpoint(tmp_path / "copy", DENSE, seed=7, tied=False)
     raw = (untied / "model.safetensors").read_bytes()
@@ -171,6 +174,16 @@ def test_tied_head_is_the_embedding(ctx, tmp_path):
         la, lb, lc = (kv.verify(toks, want_logits=True)[1] for kv in kvs)
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
         assert not np.array_equal(la, lc)
+        om = oracle.OracleModel(ModelDesc.make(**DENSE), 7, 11, 100)
+        om.tie_head()
+        ol, ot = om.verify(toks)
+        om.free()
+        err = float(np.abs(la - ol).max())
+        scale = float(np.abs(ol).max())
+        assert err <= 0.01 * scale, (err, scale)
+        srt = np.sort(ol, axis=1)
+        sure = (srt[:, -1] - srt[:, -2]) > 2 * err
+        assert np.array_equal(np.argmax(la, axis=1)[sure], ot[sure])
     finally:
         for x in kvs + [a, b, c]:
             x.free()

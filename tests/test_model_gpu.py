@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from ingot_amd._lib import Context, KVCache, Model, ModelDesc, accept
+from ingot_amd._lib import Context, KVCache, Model, ModelDesc, accept, check, lib
 from synth import cosine
 
 pytestmark = pytest.mark.gpu
@@ -312,7 +312,7 @@ def test_recorded_step_replays_match_the_eager_step(shape):
     ctx.close()
 
 
-def test_split_k_epilogues_match_the_whole_k_step(monkeypatch):
+def test_split_k_epilogues_match_the_whole_k_step():
     """K split over workgroups with the step's fused epilogues (RMSNorm-scaled projection, residual + next RMSNorm
     input, gated activation): each workgroup writes its partial sums with agent-coherent stores and the last of a row
     group to arrive adds them in split order and runs the epilogue. Forcing split shapes on every matrix of a model
@@ -324,14 +324,17 @@ def test_split_k_epilogues_match_the_whole_k_step(monkeypatch):
     kv.free()
     m.free()
     # qkv 1536×512, o 512×1024, gate|up 512×512, down 512×256: one-wave workgroups, one K-block each.
-    monkeypatch.setenv("IH_QMM_SHAPES", "1536:512=4,1,1;512:1024=2,1,1;512:512=2,1,1;512:256=2,1,1")
+    shapes = ((1536, 512, 4, 1, 1), (512, 1024, 2, 1, 1), (512, 512, 2, 1, 1), (512, 256, 2, 1, 1))
+    for n, k, r, kw, kpw in shapes:
+        check(lib().ih_qmm_shape_override(ctx.handle, n, k, r, kw, kpw))
     runs = []
     for _ in range(2):
         d, m, kv = make(ctx, GQA4, P=200)
         runs.append(kv.verify(toks, want_logits=True))
         kv.free()
         m.free()
-    monkeypatch.delenv("IH_QMM_SHAPES")
+    for n, k, *_ in shapes:
+        check(lib().ih_qmm_shape_override(ctx.handle, n, k, 0, 0, 0))
     (top, logits), (top2, logits2) = runs
     assert np.array_equal(logits, logits2) and np.array_equal(top, top2), "split-K step is not deterministic"
     err, cos = logits_close(logits, log_ref)
