@@ -109,7 +109,6 @@ struct GatherParams {
   int trips;               // ring trips of D K-blocks per wave: ⌈⌈nkb / GKW⌉ / D⌉ (set by the launch)
 };
 
-constexpr int GKW = 4;  // waves per workgroup (K split)
 // Kernel format of the gathered product: the matrix formats, plus int4 codes against fp16 activations (an affine
 // router in front of MXFP4 experts, whose activation rows are fp16: a nibble becomes the exact fp16 1024 + q, the MFMA
 // runs in fp16 and the affine map is y = s·acc + (b − 1024·s)·Σx).
@@ -122,8 +121,9 @@ struct GStage {
   u32x4 x[4];  // one token tile's activation fragments of the K-block
 };
 
-// R row tiles × (one slot of the round): grid (Npad/(16·R), slots), 64·GKW threads. The R tiles of a wave share each x
-// fragment, and a workgroup streams R times the bytes behind its one read of the slot's routing entry.
+// R row tiles × (one slot of the round): grid (⌈N/16/R⌉, slots), 64·GKW threads (GKW waves splitting K). The R
+// tiles of a wave share each x fragment, and a workgroup streams R times the bytes behind its one read of the slot's
+// routing entry.
 //
 // Wave w takes K-blocks w, w + GKW, w + 2·GKW, … through a ring of D stages, all D requested at entry, and the stage
 // just multiplied refilled D·GKW K-blocks ahead. Many slots run at D = 1: the registers of deeper rings cost waves
@@ -131,7 +131,7 @@ struct GStage {
 // load as zeros (out-of-range buffer offsets: no memory traffic) and add exactly nothing. A slot with more than 16
 // pairs (one expert chosen by more than 16 rows) runs the K loop again for its second token tile, so the ring holds
 // one token tile's activations.
-template <int FMT, int R, int D>
+template <int FMT, int R, int D, int GKW>
 __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
   constexpr bool I4 = FMT != QF_MXFP4, XH = FMT == GF_INT4_F16;  // int4 codes; fp16 activations for them
   const int u = blockIdx.y;
@@ -560,29 +560,35 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
   IH_CHECK(size_t(W->E) * p.tiles_per_e * 1024u < (size_t(1) << 31), IH_EINVAL,
            "gathered qmm: stacked matrix above 2 GiB");
   TimedLaunch tl(c, TC_MOE, bytes);
-  // Row tiles per workgroup and ring depth, measured on the MoE configurations (i.i.d. routing, per step): two tiles
-  // sharing each x fragment beat one (E128 top-8 int4: 5.13 → 3.95 ms; E32 top-4 MXFP4: 2.64 → 2.32), four gain
-  // nothing over two; and with many slots a ring of one stage beats deeper ones (E128: 3.95 at D = 1, 4.47 at 2,
-  // 5.70 at 3): the stages' registers cost waves per SIMD, and the waves of other workgroups hide a stage's latency
-  // better than a wave's own second stage. A single slot (a router, or one expert) has few workgroups, and there
-  // every K-block of a wave is requested at entry.
-  const int tiles = W->Npad / 16;
+  // Waves per workgroup, row tiles per workgroup and ring depth, measured on the MoE configurations (i.i.d. routing,
+  // MoE kernels per step): two tiles sharing each x fragment beat one (E128 top-8 int4: 5.13 → 3.95 ms; E32 top-4
+  // MXFP4: 2.64 → 2.32), four gain nothing over two; with many slots a ring of one stage beats deeper ones (E128: 3.95
+  // at D = 1, 4.47 at 2, 5.70 at 3): the stages' registers cost waves per SIMD, and the waves of other workgroups hide
+  // a stage's latency better than a wave's own second stage. K split over two waves wins where K has at most 16
+  // K-blocks (E128, K = 2048 and 768: 3.95 → 3.72 ms), over four where it has more (E32, K = 2880: 2.24 against 2.55
+  // with two waves, 2.46 with eight). A single slot (a router, or one expert) has few workgroups, and there every
+  // K-block of a wave is requested at entry.
+  // Only tiles with a live row are launched (rows are padded to 256 in memory, so the odd tile of a pair stays inside
+  // the matrix: its rows read as the zero padding and are not stored).
+  const int tiles = (W->N + 15) / 16;
+  const int GKW = W->nkb <= 16 ? 2 : 4;
   const int kpw = (W->nkb + GKW - 1) / GKW;
   int R = 1, D = 1;
-  if (tiles % 2 == 0 && (tiles / 2) * slots >= 2 * c->cu_count) R = 2;
+  if (((tiles + 1) / 2) * slots >= 2 * c->cu_count) R = 2;
   if (slots == 1) D = kpw <= 1 ? 1 : (kpw <= 2 ? 2 : 4);
   p.trips = (kpw + D - 1) / D;
-  const dim3 grid(tiles / R, slots);
-#define IH_GATHER_LAUNCH(R_, D_)                                                                                    \
-  if (R == R_ && D == D_) {                                                                                       \
+  const dim3 grid((tiles + R - 1) / R, slots);
+#define IH_GATHER_LAUNCH(R_, D_, W_)                                                                                \
+  if (R == R_ && D == D_ && GKW == W_) {                                                                          \
     if (W->format == QF_MXFP4)                                                                                    \
-      tlaunch(tl, qmm_gather_kernel<QF_MXFP4, R_, D_>, grid, dim3(64 * GKW), 0, c->stream, p);                    \
+      tlaunch(tl, qmm_gather_kernel<QF_MXFP4, R_, D_, W_>, grid, dim3(64 * W_), 0, c->stream, p);                 \
     else if (x_f16)                                                                                               \
-      tlaunch(tl, qmm_gather_kernel<GF_INT4_F16, R_, D_>, grid, dim3(64 * GKW), 0, c->stream, p);                 \
+      tlaunch(tl, qmm_gather_kernel<GF_INT4_F16, R_, D_, W_>, grid, dim3(64 * W_), 0, c->stream, p);              \
     else                                                                                                          \
-      tlaunch(tl, qmm_gather_kernel<QF_INT4, R_, D_>, grid, dim3(64 * GKW), 0, c->stream, p);                     \
+      tlaunch(tl, qmm_gather_kernel<QF_INT4, R_, D_, W_>, grid, dim3(64 * W_), 0, c->stream, p);                  \
   }
-  IH_GATHER_LAUNCH(1, 1) IH_GATHER_LAUNCH(1, 2) IH_GATHER_LAUNCH(1, 4) IH_GATHER_LAUNCH(2, 1)
+  IH_GATHER_LAUNCH(1, 1, 2) IH_GATHER_LAUNCH(1, 2, 2) IH_GATHER_LAUNCH(1, 4, 2) IH_GATHER_LAUNCH(2, 1, 2)
+  IH_GATHER_LAUNCH(1, 1, 4) IH_GATHER_LAUNCH(1, 2, 4) IH_GATHER_LAUNCH(1, 4, 4) IH_GATHER_LAUNCH(2, 1, 4)
 #undef IH_GATHER_LAUNCH
   IH_HIP(hipGetLastError());
   return IH_OK;
