@@ -127,7 +127,7 @@ struct GStage {
 //
 // Wave w takes K-blocks w, w + GKW, w + 2·GKW, … through a ring of D stages, all D requested at entry, and the stage
 // just multiplied refilled D·GKW K-blocks ahead. Many slots run at D = 1: the registers of deeper rings cost waves
-// per SIMD, and other workgroups' waves hide a stage's latency better (the launch picks D). K-blocks past the matrix
+// per SIMD, and other workgroups' waves hide a stage's latency better (the launch picks GKW, R and D). K-blocks past the matrix
 // load as zeros (out-of-range buffer offsets: no memory traffic) and add exactly nothing. A slot with more than 16
 // pairs (one expert chosen by more than 16 rows) runs the K loop again for its second token tile, so the ring holds
 // one token tile's activations.
@@ -560,22 +560,31 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
   IH_CHECK(size_t(W->E) * p.tiles_per_e * 1024u < (size_t(1) << 31), IH_EINVAL,
            "gathered qmm: stacked matrix above 2 GiB");
   TimedLaunch tl(c, TC_MOE, bytes);
-  // Waves per workgroup, row tiles per workgroup and ring depth, measured on the MoE configurations (i.i.d. routing,
-  // MoE kernels per step): two tiles sharing each x fragment beat one (E128 top-8 int4: 5.13 → 3.95 ms; E32 top-4
-  // MXFP4: 2.64 → 2.32), four gain nothing over two; with many slots a ring of one stage beats deeper ones (E128: 3.95
-  // at D = 1, 4.47 at 2, 5.70 at 3): the stages' registers cost waves per SIMD, and the waves of other workgroups hide
-  // a stage's latency better than a wave's own second stage. K split over two waves wins where K has at most 16
-  // K-blocks (E128, K = 2048 and 768: 3.95 → 3.72 ms), over four where it has more (E32, K = 2880: 2.24 against 2.55
-  // with two waves, 2.46 with eight). A single slot (a router, or one expert) has few workgroups, and there every
-  // K-block of a wave is requested at entry.
-  // Only tiles with a live row are launched (rows are padded to 256 in memory, so the odd tile of a pair stays inside
-  // the matrix: its rows read as the zero padding and are not stored).
+  // Waves per workgroup (K split), row tiles per workgroup and ring depth, measured on the MoE configurations (i.i.d.
+  // routing, MoE kernels per step). Many slots: with K at most 16 K-blocks (E128 top-8, K = 2048 and 768) one wave
+  // per workgroup over four tiles (3.27 ms) beats two waves over four tiles (3.30), over two tiles (3.72) and four
+  // waves over two (3.95) or one (5.13); with more K-blocks (E32 top-4, K = 2880) four waves over two tiles (2.22)
+  // beat two waves (2.52), eight (2.46), and four tiles (2.43). A slot holds few pairs, so a workgroup's life is a
+  // few memory latencies and the rate is set by how much each wave streams behind them: longer waves win until the
+  // registers cost waves per SIMD (eight tiles: 171 VGPRs, 3.53 ms; a ring of two or three stages: 4.47, 5.70). A
+  // single slot (a router, or one expert) has few workgroups; there K is split over waves and every K-block of a
+  // wave is requested at entry.
+  // Only tiles with a live row are launched (rows are padded to 256 in memory, so the tiles of a group past N stay
+  // inside the matrix: their rows read as the zero padding and are not stored).
   const int tiles = (W->N + 15) / 16;
-  const int GKW = W->nkb <= 16 ? 2 : 4;
+  int GKW, R = 1, D = 1;
+  if (slots == 1) {
+    GKW = W->nkb <= 16 ? 2 : 4;
+    const int kpw = (W->nkb + GKW - 1) / GKW;
+    D = kpw <= 1 ? 1 : (kpw <= 2 ? 2 : 4);
+  } else if (W->nkb <= 16) {
+    GKW = 1;
+    R = 4;
+  } else {
+    GKW = 4;
+    if (((tiles + 1) / 2) * slots >= 2 * c->cu_count) R = 2;
+  }
   const int kpw = (W->nkb + GKW - 1) / GKW;
-  int R = 1, D = 1;
-  if (((tiles + 1) / 2) * slots >= 2 * c->cu_count) R = 2;
-  if (slots == 1) D = kpw <= 1 ? 1 : (kpw <= 2 ? 2 : 4);
   p.trips = (kpw + D - 1) / D;
   const dim3 grid((tiles + R - 1) / R, slots);
 #define IH_GATHER_LAUNCH(R_, D_, W_)                                                                                \
@@ -587,8 +596,8 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
     else                                                                                                          \
       tlaunch(tl, qmm_gather_kernel<QF_INT4, R_, D_, W_>, grid, dim3(64 * W_), 0, c->stream, p);                  \
   }
-  IH_GATHER_LAUNCH(1, 1, 2) IH_GATHER_LAUNCH(1, 2, 2) IH_GATHER_LAUNCH(1, 4, 2) IH_GATHER_LAUNCH(2, 1, 2)
-  IH_GATHER_LAUNCH(1, 1, 4) IH_GATHER_LAUNCH(1, 2, 4) IH_GATHER_LAUNCH(1, 4, 4) IH_GATHER_LAUNCH(2, 1, 4)
+  IH_GATHER_LAUNCH(1, 1, 2) IH_GATHER_LAUNCH(1, 2, 2) IH_GATHER_LAUNCH(1, 4, 2) IH_GATHER_LAUNCH(1, 1, 4)
+  IH_GATHER_LAUNCH(1, 2, 4) IH_GATHER_LAUNCH(1, 4, 4) IH_GATHER_LAUNCH(2, 1, 4) IH_GATHER_LAUNCH(4, 1, 1)
 #undef IH_GATHER_LAUNCH
   IH_HIP(hipGetLastError());
   return IH_OK;

