@@ -38,16 +38,17 @@ int launch_prework(ih_ctx* c, const AttnArgs& a);
 int launch_attention(ih_ctx* c, const AttnArgs& a);
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out);
 int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K, const float* bias,
-                     const float* pes, int* nent, int* entries, int* x_row, float* pair_w, int* row_pair,
+                     const float* pes, int* nent, int* entries, int4* slots, int* x_row, float* pair_w, int* row_pair,
                      const MoeIid& iid);
 int launch_moe_combine(ih_ctx* c, const float* o, int ldo, const int* row_pair, const float* pair_w, int K, int rows,
                        float* h, int H, const uint16_t* nw, ActBuf& act);
 int launch_moe_router(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, float eps, float* logits, int ldl);
 int launch_moe_gate_up(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, int K_top, float eps,
-                       const int* nent, const int* entries, const int* x_row, const uint16_t* bias, int glu,
+                       const int* nent, const int* entries, const int4* slots, const int* x_row, const uint16_t* bias, int glu,
                        float limit, void* h_frag, int h_nkb, int h_tokens, bool h_f16);
 int launch_moe_down(ih_ctx* c, const ih_qmat* W, const void* h_frag, int h_nkb, int h_tokens, bool h_f16, int rows,
-                    int K_top, const int* nent, const int* entries, const uint16_t* bias, float* o, int ldo);
+                    int K_top, const int* nent, const int* entries, const int4* slots, const uint16_t* bias, float* o,
+                    int ldo);
 
 // Tensor ids of the synthetic model (the generator's stream keys): globals, then 100 per layer.
 enum : uint64_t { T_EMBED = 1, T_FINAL_NORM = 2, T_HEAD = 3 };
@@ -179,6 +180,7 @@ int model_alloc_scratch(ih_model* m) {
     run(dalloc_t(&m->rlogits, size_t(MAX_TOK) * E));
     run(dalloc_t(&m->nent, d.n_layers));
     run(dalloc_t(&m->entries, size_t(3) * E));
+    run(dalloc_t(&m->slots, size_t(E)));
     run(dalloc_t(&m->x_row, m->max_pairs));
     run(dalloc_t(&m->pair_w, m->max_pairs));
     run(dalloc_t(&m->row_pair, m->max_pairs));
@@ -294,7 +296,7 @@ void model_release(ih_model* m) {
   }
   ih_qmat_free(m->head);
   void* ptrs[] = {m->emb_w, m->emb_s, m->emb_b, m->final_norm, m->h, m->proj, m->logits, m->tok, m->top1,
-                  m->q, m->rope, m->opart, m->ml, m->rlogits, m->nent, m->entries, m->x_row, m->pair_w, m->row_pair,
+                  m->q, m->rope, m->opart, m->ml, m->rlogits, m->nent, m->entries, m->slots, m->x_row, m->pair_w, m->row_pair,
                   m->hpair, m->opair, m->rinv};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
@@ -406,12 +408,12 @@ static int run_step(ih_model* m, ih_kv* kv, int B, const uint32_t* tok, uint32_t
         iid.pos_dev = st;
         iid.pos_max = pos_max;
       }
-      IH_TRY(launch_moe_route(c, m->rlogits, E, B, E, K, L.router_bias, nullptr, nent, m->entries, m->x_row,
+      IH_TRY(launch_moe_route(c, m->rlogits, E, B, E, K, L.router_bias, nullptr, nent, m->entries, m->slots, m->x_row,
                               m->pair_w, m->row_pair, iid));
-      IH_TRY(launch_moe_gate_up(c, L.gate_up, m->act_mlp, B, K, d.rms_eps, nent, m->entries, m->x_row, L.gu_bias,
-                                d.act, d.swiglu_limit, m->hpair, m->hpair_nkb, m->max_pairs, f16));
+      IH_TRY(launch_moe_gate_up(c, L.gate_up, m->act_mlp, B, K, d.rms_eps, nent, m->entries, m->slots, m->x_row,
+                                L.gu_bias, d.act, d.swiglu_limit, m->hpair, m->hpair_nkb, m->max_pairs, f16));
       IH_TRY(launch_moe_down(c, L.down, m->hpair, m->hpair_nkb, m->max_pairs, f16, B, K, nent, m->entries,
-                             L.down_bias, m->opair, H));
+                             m->slots, L.down_bias, m->opair, H));
       IH_TRY(launch_moe_combine(c, m->opair, H, m->row_pair, m->pair_w, K, B, m->h, H, next_norm, m->act_attn));
       IH_TRY(drafter_capture(m, l, B));
       continue;

@@ -85,6 +85,7 @@ struct ih_model {
   float* rlogits = nullptr;
   int* nent = nullptr;
   int* entries = nullptr;
+  int4* slots = nullptr;  // [E] one record per possible slot: (expert, first pair, pairs, live)
   int* x_row = nullptr;
   float* pair_w = nullptr;
   int* row_pair = nullptr;

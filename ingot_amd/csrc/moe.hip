@@ -93,6 +93,7 @@ struct GatherParams {
   const int* x_row;        // pair → activation row (null: the pair index itself)
   const int* entries;      // [U][3] (expert, first pair, pairs); null: one entry (dense_e, 0, M)
   const int* nent;         // U on the device (null: 1)
+  const int4* slots;       // one record per possible slot, (expert, first pair, pairs, live); null: entries + nent
   int dense_e, M;
   int N, Npad, nkb, mode;
   void* y;
@@ -135,10 +136,17 @@ template <int FMT, int R, int D, int GKW>
 __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
   constexpr bool I4 = FMT != QF_MXFP4, XH = FMT == GF_INT4_F16;  // int4 codes; fp16 activations for them
   const int u = blockIdx.y;
-  const int U = p.nent ? __builtin_amdgcn_readfirstlane(p.nent[0]) : 1;
-  if (u >= U) return;
   int e, start, cnt;
-  if (p.entries) {
+  if (p.slots) {
+    // One 16-byte read names the slot's expert and pairs, or that it is unused (one memory latency, not two).
+    const int4 r = p.slots[u];
+    if (!r.w) return;
+    e = r.x;
+    start = r.y;
+    cnt = r.z;
+  } else if (p.entries) {
+    const int U = p.nent ? __builtin_amdgcn_readfirstlane(p.nent[0]) : 1;
+    if (u >= U) return;
     e = p.entries[3 * u];
     start = p.entries[3 * u + 1];
     cnt = p.entries[3 * u + 2];
@@ -371,7 +379,8 @@ template <int NE>
 __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict__ logits, int ldl, int rows, int E,
                                                          int K, const float* __restrict__ bias,
                                                          const float* __restrict__ pes, int* __restrict__ nent,
-                                                         int* __restrict__ entries, int* __restrict__ x_row,
+                                                         int* __restrict__ entries, int4* __restrict__ slots,
+                                                         int nslots, int* __restrict__ x_row,
                                                          float* __restrict__ pair_w, int* __restrict__ row_pair,
                                                          MoeIid iid) {
   __shared__ float lg[MAX_TOK][256];
@@ -458,8 +467,11 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
     entries[3 * sl] = tid;
     entries[3 * sl + 1] = st;
     entries[3 * sl + 2] = c;
+    if (slots) slots[sl] = make_int4(tid, st, c, 1);
   }
-  if (tid == 0) nent[0] = (wslots[0] + wslots[1]) + (wslots[2] + wslots[3]);
+  const int U = (wslots[0] + wslots[1]) + (wslots[2] + wslots[3]);
+  if (tid == 0) nent[0] = U;
+  if (slots && tid >= U && tid < nslots) slots[tid] = make_int4(0, 0, 0, 0);
   // Pair (row r, slot) of expert e goes to first[e] + #{rows r' < r that chose e}.
   if (tid < nrk) {
     const int e = inds[tid], r = tid / K;
@@ -603,15 +615,16 @@ int launch_gather(ih_ctx* c, const ih_qmat* W, const GatherParams& base, int slo
   return IH_OK;
 }
 
+// slots (may be null): the one-record slot table of the gathered launches, min(E, rows·K) records.
 int launch_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K, const float* bias,
-                     const float* pes, int* nent, int* entries, int* x_row, float* pair_w, int* row_pair,
+                     const float* pes, int* nent, int* entries, int4* slots, int* x_row, float* pair_w, int* row_pair,
                      const MoeIid& iid) {
   IH_CHECK(E >= 1 && E <= 256 && K >= 1 && K <= 16 && K <= E && rows >= 1 && rows <= MAX_TOK, IH_EINVAL,
            "moe route: need E ≤ 256, 1 ≤ k ≤ min(16, E), 1 ≤ rows ≤ 32");
   TimedLaunch tl(c, TC_MOE, double(rows) * E * 4);
   auto kern = E <= 128 ? moe_route_kernel<4> : moe_route_kernel<8>;
-  tlaunch(tl, kern, dim3(1), dim3(1024), 0, c->stream, logits, ldl, rows, E, K, bias, pes, nent, entries,
-          x_row, pair_w, row_pair, iid);
+  tlaunch(tl, kern, dim3(1), dim3(1024), 0, c->stream, logits, ldl, rows, E, K, bias, pes, nent, entries, slots,
+          std::min(E, rows * K), x_row, pair_w, row_pair, iid);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
@@ -662,8 +675,8 @@ int launch_moe_router(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, fl
 
 // Gate|up of every pair: h[pair] = act(r·g + bg, r·u + bu) as fragments (one token per pair).
 int launch_moe_gate_up(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, int K_top, float eps, const int* nent,
-                       const int* entries, const int* x_row, const uint16_t* bias, int glu, float limit, void* h_frag,
-                       int h_nkb, int h_tokens, bool h_f16) {
+                       const int* entries, const int4* slot_tab, const int* x_row, const uint16_t* bias, int glu,
+                       float limit, void* h_frag, int h_nkb, int h_tokens, bool h_f16) {
   IH_CHECK(W->il8, IH_EINVAL, "moe gate|up: the matrix must be interleaved by eights");
   GatherParams p{};
   p.xa = static_cast<const uint4*>(x.frag);
@@ -672,6 +685,7 @@ int launch_moe_gate_up(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, i
   p.x_row = x_row;
   p.entries = entries;
   p.nent = nent;
+  p.slots = slot_tab;
   p.mode = GM_GLU;
   p.ss_in = x.ss;
   p.nss_in = x.nss;
@@ -691,13 +705,15 @@ int launch_moe_gate_up(ih_ctx* c, const ih_qmat* W, const ActBuf& x, int rows, i
 
 // Down of every pair: o[pair] = h[pair] · Wdᵀ + bd (fp32).
 int launch_moe_down(ih_ctx* c, const ih_qmat* W, const void* h_frag, int h_nkb, int h_tokens, bool h_f16, int rows,
-                    int K_top, const int* nent, const int* entries, const uint16_t* bias, float* o, int ldo) {
+                    int K_top, const int* nent, const int* entries, const int4* slot_tab, const uint16_t* bias, float* o,
+                    int ldo) {
   GatherParams p{};
   p.xa = static_cast<const uint4*>(h_frag);
   p.x_nkb = h_nkb;
   p.x_tokens = h_tokens;
   p.entries = entries;
   p.nent = nent;
+  p.slots = slot_tab;
   p.mode = GM_DOWN;
   p.y = o;
   p.ldy = ldo;
@@ -821,7 +837,8 @@ int ih_moe_route(ih_ctx* c, const float* logits, int ldl, int rows, int E, int K
                  int* nent, int* entries, int* x_row, float* pair_w, int* row_pair) {
   IH_CHECK(c && logits && nent && entries && x_row && pair_w && row_pair, IH_EINVAL, "ih_moe_route: null argument");
   IH_CHECK(ldl >= E, IH_EINVAL, "ih_moe_route: ldl < E");
-  return launch_moe_route(c, logits, ldl, rows, E, K, bias, pes, nent, entries, x_row, pair_w, row_pair, MoeIid{});
+  return launch_moe_route(c, logits, ldl, rows, E, K, bias, pes, nent, entries, nullptr, x_row, pair_w, row_pair,
+                          MoeIid{});
 }
 
 int ih_qmm_gathered(ih_ctx* c, const ih_qmat* W, const void* x, int ldx, int rows, int K_top, const int* nent,
