@@ -57,12 +57,17 @@ __device__ __forceinline__ void wht_stage(float (&x)[NE], int lane) {
 // per (token, head): sc = fp16(amax/127) (1 when amax = 0), q = clamp(rint(x/sc), ±127), written at slot P + t.
 // One wave per (head slot, token), lane l holding dims l + 64e: the RoPE partner of dim d is d ± HD/2 (the lane's
 // other value at HD 128, the lane 32 away at HD 64), WHT stages h < 64 are lane exchanges (lane_xor) and h = 64 is
-// in-lane — no LDS, no barrier. Grid (QH + 2·KVH, B), one wave per workgroup.
+// in-lane — no LDS, no barrier. Grid (KVH, (G + 2)·B), one wave per workgroup: workgroup (kvh, j) takes token
+// j / (G + 2) and, by j mod (G + 2), one of the group's G q heads, its k head or its v head. Consecutive workgroup ids
+// go round-robin over the 8 XCDs, so with 8 KV heads a group's q and new K/V rows are written on XCD kvh, where the
+// attention kernel's splits of that KV head run.
 template <int HD>
-__global__ __launch_bounds__(256) void prework_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64) void prework_kernel(AttnArgs a) {
   constexpr int NE = HD / 64, RH = HD / 2;
-  const int slot = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6), t = blockIdx.y, lane = threadIdx.x & 63;
-  if (a.pos_dev && blockIdx.x == 0 && t == 0 && threadIdx.x == 0) {
+  const int kvh = blockIdx.x, u = int(blockIdx.y) % (a.G + 2), t = int(blockIdx.y) / (a.G + 2);
+  const int slot = u < a.G ? kvh * a.G + u : (u == a.G ? a.QH + kvh : a.QH + a.KVH + kvh);
+  const int lane = threadIdx.x & 63;
+  if (a.pos_dev && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
     const uint32_t p = a.pos_dev[0];
     if (p < uint32_t(a.pos_min) || p > uint32_t(a.pos_max)) a.flag_dev[0] = 1u;
   }
@@ -781,12 +786,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(AttnArgs a) {
 // runtime loop would wait out a memory latency per split), keeping a running (M, L, o) rescaled per batch; then the
 // SG groups are merged by a fixed butterfly. Grid (B, QH/w), 64·w threads (w = 1 by default).
 template <int HD>
-__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb, int ntile) {
+__global__ __launch_bounds__(64) void attn_reduce_kernel(AttnArgs a, uint4* __restrict__ frag, int nkb, int ntile) {
   constexpr int DG = HD / 8, SG = 64 / DG, NB = 8;
   static_assert(DG == 8 || DG == 16, "the split-group merge below runs the stages 8/16/32 of HD 64 and 128");
-  const int t = blockIdx.x, h = blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // Grid (KVH, B·G), one wave per workgroup: workgroup (kvh, j) merges q head kvh·G + j mod G of token j / G, on the
+  // XCD where that KV head's splits ran and wrote their partials (consecutive workgroup ids go round-robin over the 8
+  // XCDs; the attention grid is (KV head, split)).
+  const int kvh = blockIdx.x, t = int(blockIdx.y) / a.G, h = kvh * a.G + int(blockIdx.y) % a.G;
+  const int lane = threadIdx.x & 63;
   const int dg = lane % DG, sg = lane / DG;
-  const int kvh = h / a.G, m = t * a.G + h % a.G;
+  const int m = t * a.G + h % a.G;
   float M = -INFINITY, L = 0.f;
   float o[8];
 #pragma unroll
@@ -869,10 +878,10 @@ int launch_prework(ih_ctx* c, const AttnArgs& a) {
   TimedLaunch tl(c, TC_PREWORK, double(a.B) * (a.QH + 2 * a.KVH) * a.HD * 4 + double(a.B) * a.KVH * (2 * a.HD + 4) +
                                     double(a.B) * a.QH * a.HD * 2);
   // One wave (one (head slot, token)) per workgroup (config 1: 2.306 against 2.312 ms per step with four).
-  constexpr int pw = 1;
-  dim3 grid((a.QH + 2 * a.KVH + pw - 1) / pw, a.B);
-  if (a.HD == 128) tlaunch(tl, prework_kernel<128>, grid, dim3(64 * pw), 0, c->stream, a);
-  else if (a.HD == 64) tlaunch(tl, prework_kernel<64>, grid, dim3(64 * pw), 0, c->stream, a);
+  IH_CHECK(a.QH == a.G * a.KVH, IH_EINVAL, "attention prework: q heads must be G per KV head");
+  const dim3 grid(a.KVH, (a.G + 2) * a.B);
+  if (a.HD == 128) tlaunch(tl, prework_kernel<128>, grid, dim3(64), 0, c->stream, a);
+  else if (a.HD == 64) tlaunch(tl, prework_kernel<64>, grid, dim3(64), 0, c->stream, a);
   else return fail(IH_EINVAL, "attention prework: head_dim must be 64 or 128");
   IH_HIP(hipGetLastError());
   return IH_OK;
@@ -924,15 +933,14 @@ int launch_attention(ih_ctx* c, const AttnArgs& a0) {
 }
 
 int launch_attn_reduce(ih_ctx* c, const AttnArgs& a, ActBuf& out) {
-  IH_CHECK(a.QH % 4 == 0, IH_EINVAL, "attention reduce: the q head count must be a multiple of 4");  // rw ≤ 4
   TimedLaunch tl(c, TC_REDUCE, double(a.KVH) * a.nsplit * a.G * a.B * (2 * a.HD + 8) + double(a.B) * a.QH * a.HD * 2);
-  // One wave (one (row, q head)) per workgroup: 4·B·QH/4 small workgroups spread over more CUs than four-wave ones
+  // One wave (one (row, q head)) per workgroup: B·QH small workgroups spread over more CUs than four-wave ones
   // (config 1: 0.146 against 0.149 ms per step).
-  constexpr int rw = 1;
-  const dim3 grid(a.B, a.QH / rw);
+  IH_CHECK(a.QH == a.G * a.KVH, IH_EINVAL, "attention reduce: q heads must be G per KV head");
+  const dim3 grid(a.KVH, a.B * a.G);
   uint4* of = static_cast<uint4*>(out.frag);
-  if (a.HD == 128) tlaunch(tl, attn_reduce_kernel<128>, grid, dim3(64 * rw), 0, c->stream, a, of, out.nkb, out.ntile);
-  else if (a.HD == 64) tlaunch(tl, attn_reduce_kernel<64>, grid, dim3(64 * rw), 0, c->stream, a, of, out.nkb, out.ntile);
+  if (a.HD == 128) tlaunch(tl, attn_reduce_kernel<128>, grid, dim3(64), 0, c->stream, a, of, out.nkb, out.ntile);
+  else if (a.HD == 64) tlaunch(tl, attn_reduce_kernel<64>, grid, dim3(64), 0, c->stream, a, of, out.nkb, out.ntile);
   else return fail(IH_EINVAL, "attention reduce: head_dim must be 64 or 128");
   IH_HIP(hipGetLastError());
   return IH_OK;
