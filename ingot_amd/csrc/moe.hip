@@ -128,10 +128,10 @@ struct GStage {
 //
 // Wave w takes K-blocks w, w + GKW, w + 2·GKW, … through a ring of D stages, all D requested at entry, and the stage
 // just multiplied refilled D·GKW K-blocks ahead. Many slots run at D = 1: the registers of deeper rings cost waves
-// per SIMD, and other workgroups' waves hide a stage's latency better (the launch picks GKW, R and D). K-blocks past the matrix
-// load as zeros (out-of-range buffer offsets: no memory traffic) and add exactly nothing. A slot with more than 16
-// pairs (one expert chosen by more than 16 rows) runs the K loop again for its second token tile, so the ring holds
-// one token tile's activations.
+// per SIMD, and other workgroups' waves hide a stage's latency better (the launch picks GKW, R and D). K-blocks past
+// the matrix load as zeros (out-of-range buffer offsets: no memory traffic) and add exactly nothing. A slot with more
+// than 16 pairs (one expert chosen by more than 16 rows) runs the K loop again for its second token tile, so the ring
+// holds one token tile's activations.
 template <int FMT, int R, int D, int GKW>
 __global__ __launch_bounds__(64 * GKW) void qmm_gather_kernel(GatherParams p) {
   constexpr bool I4 = FMT != QF_MXFP4, XH = FMT == GF_INT4_F16;  // int4 codes; fp16 activations for them
