@@ -8,11 +8,12 @@
 //
 // MI355X design:
 //   - One launch covers every expert of the round: the grid is (row tiles, expert slots) with as many slots as the
-//     union can have (min(E, B·k)); a workgroup reads the union's size on the device and returns when its slot is
-//     unused, so the host never waits for the routing. A slot's tokens are gathered through a row map: the round's
-//     rows for gate|up, the expert's own pair rows for down.
-//   - Weights stream as 16-row × 128-K tiles, one 1024-byte dwordx4 load per wave and tile (the dense qmm's layout),
-//     K split over the waves of the workgroup and added in wave order in LDS.
+//     union can have (min(E, B·k)); a workgroup reads its slot's record (written by the routing on the device) and
+//     returns when the slot is unused, so the host never waits for the routing. A slot's tokens are gathered through
+//     a row map: the round's rows for gate|up, the expert's own pair rows for down.
+//   - Weights stream as 16-row × 128-K tiles, one 1024-byte dwordx4 load per wave and tile (the dense qmm's layout);
+//     a workgroup of one wave takes four tiles over all of K (few K-blocks), or four waves split K over two tiles,
+//     added in wave order in LDS (many K-blocks).
 //   - int4 g64: bf16 MFMA on 128 + q with the affine map applied per group (as the dense qmm). MXFP4: an e2m1 code
 //     becomes its exact fp16 value with one v_perm_b32 table lookup per pair and the sign OR-ed in; the MFMA runs in
 //     fp16 against fp16 activations, and one e8m0 scale per 32 K (= one MFMA step) multiplies the step's products.
