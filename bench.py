@@ -113,27 +113,51 @@ def main() -> int:
 
 
 def decode_loop(model, P: int, anchor: int) -> dict:
-    """Side measurement: the chained decode loop (ih_decode_greedy, decodeSpec's hot loop) from position P with
-    advancing positions (a cache of P + 1024 positions, the same synthetic history), copy-from-context drafts
-    (rows = 17) and plain one-row chained decoding (rows = 1), two rounds in flight. Host wall clock around each call
-    (the call synchronises); the first call of each kind warms up the recorded steps and is not reported."""
-    from ingot_amd._lib import KVCache
+    """Side measurement: the chained decode loop (ih_decode_greedy / ih_decode_sample, decodeSpec's hot loop) from
+    position P with advancing positions (a cache of P + 1024 positions, the same synthetic history), two rounds in
+    flight: copy-from-context drafts (rows = 17), plain one-row chained decoding (rows = 1), temperature sampling with
+    copy drafts (rows = 17), and a synthetic DFlash2 drafter (rows = its block, 16; its drafts are noise against the synthetic
+    target, so this times the round, not an acceptance rate). Host wall clock around each call (the call
+    synchronises); the first call of each kind warms up the recorded steps and is not reported."""
+    from ingot_amd._lib import Drafter, DrafterDesc, KVCache, SampleParams, check, lib
 
     kv = KVCache(model, P + 1024)
     kv.fill_synthetic(P, KV_SEED)
     out = {"cache_positions": P + 1024, "key_chunk": kv.chunk}
-    for rows, ntok in ((17, 17 * 48), (1, 96)):
-        hist = np.full(P, anchor, np.uint32)  # the context the copy drafter indexes (the greedy chain's token)
-        kv.set_pos(P)
-        kv.decode_greedy(anchor, ntok, rows=rows, history=hist, inflight=2)
-        kv.set_pos(P)
+    hist = np.full(P, anchor, np.uint32)  # the context the copy drafter indexes (the greedy chain's token)
+    # A drafter of the size class DFlash2 ships for 8B targets: 5 layers at the target's hidden size, 32 q heads of
+    # 128, intermediate 12288, 5 target layers, 16-token blocks, a 2048-position window, a rank-256 selector.
+    L_ = model.desc.n_layers
+    ddesc = DrafterDesc.make(targets=tuple(range(1, L_, max(1, L_ // 5)))[:5], n_layers=5, hidden=model.desc.hidden,
+                             n_q_heads=32, head_dim=128, intermediate=12288, block=16, window=2048, rank=256,
+                             dyn_conv=1, mask_token=model.desc.vocab - 1)
+    dr = Drafter(model, ddesc, SEED + 1)
+    sp = SampleParams(temp=0.8, top_p=0.95, top_k=64, min_p=0.0)
+    kinds = (("rows17", 17, 17 * 48, {"history": hist}, False),
+             ("rows1", 1, 96, {"history": hist}, False),
+             ("sample_rows17", 17, 17 * 48, {"history": hist}, True),
+             ("drafter_rows16", 16, 16 * 24, {"drafter": dr}, False))
+    for name, rows, ntok, extra, sample in kinds:
+        if "drafter" in extra:
+            dr.attach()  # the verify steps then capture the drafter's target layers
+
+        def call():
+            kv.set_pos(P)
+            if sample:
+                return kv.decode_sample(anchor, ntok, sp, 7, rows=rows, inflight=2, **extra)
+            return kv.decode_greedy(anchor, ntok, rows=rows, inflight=2, **extra)
+        call()
         t0 = time.perf_counter()
-        toks, st = kv.decode_greedy(anchor, ntok, rows=rows, history=hist, inflight=2)
+        toks, st = call()
         dt = time.perf_counter() - t0
-        kv.set_pos(P)
-        out[f"rows{rows}"] = {"tokens": len(toks), "rounds": st.rounds, "accepted": st.accepted,
-                              "finish": st.finish, "ms": round(dt * 1e3, 2),
-                              "ms_per_round": round(dt * 1e3 / max(st.rounds, 1), 4), "tok_s": round(len(toks) / dt, 1)}
+        out[name] = {"tokens": len(toks), "rounds": st.rounds, "accepted": st.accepted, "finish": st.finish,
+                     "ms": round(dt * 1e3, 2), "ms_per_round": round(dt * 1e3 / max(st.rounds, 1), 4),
+                     "tok_s": round(len(toks) / dt, 1)}
+    kv.set_pos(P)
+    check(lib().ih_model_set_drafter(model.handle, None))
+    out["drafter"] = {"n_layers": 5, "hidden": int(model.desc.hidden), "q_heads": 32, "intermediate": 12288,
+                      "block": 16, "window": 2048, "rank": 256, "targets": list(ddesc.target_layers[:ddesc.n_targets])}
+    dr.free()
     kv.free()
     return out
 

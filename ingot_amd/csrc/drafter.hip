@@ -295,59 +295,96 @@ __device__ __forceinline__ bool dvisible(int n, int t, int P, int B, int W) {
 
 // Attention of the block's Q = G·B queries of one KV head over one chunk of 128 slots: scores in fp32 (q·k / √HD),
 // the chunk's (max, Σ e^(s − max)) per query and its unnormalised O = Σ e^(s − max)·v. Grid (nchunk, KVH), 256
-// threads; the chunk's K, then its V, staged in LDS (HD ≤ 128, Q ≤ 64).
+// threads; the queries, the chunk's K, then its V, staged in LDS (HD ≤ 128, Q ≤ 64). Wave w takes query tile w (16
+// rows): S = Q·Kᵀ on v_mfma_f32_16x16x32_f16 (fp16 products exact in fp32), O += P·V on v_mfma_f32_16x16x4_f32 with
+// the weights in fp32 (no rounding of P).
+typedef _Float16 dh8 __attribute__((ext_vector_type(8)));
+typedef float df4 __attribute__((ext_vector_type(4)));
 template <int HD>
 __global__ __launch_bounds__(256) void dattn_kernel(DAttn a, float* __restrict__ opart, float2* __restrict__ ml,
                                                     int nchunk) {
+  constexpr int KS = HD + 8;  // halves per LDS row: 16-byte aligned fragment reads, rows 4 banks apart
+  constexpr int RV = HD / 8;  // 16-byte vectors per row
   const int ch = blockIdx.x, kvh = blockIdx.y, Q = a.G * a.B;
   const int P = a.st ? int(a.st[0]) : a.P;
-  const int n0 = ch * DCHUNK;
-  __shared__ __half ks[DCHUNK][HD + 2];
-  __shared__ float sc[64][DCHUNK + 1];
-  for (int i = threadIdx.x; i < DCHUNK * HD; i += 256) {
-    const int n = i / HD, dd = i % HD;
-    ks[n][dd] = n0 + n < a.slots ? a.kc[(size_t(kvh) * a.slots + n0 + n) * HD + dd] : __float2half(0.f);
-  }
+  const int n0 = ch * DCHUNK, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, qd = lane >> 4;
+  __shared__ __attribute__((aligned(16))) __half ks[DCHUNK][KS];
+  __shared__ __attribute__((aligned(16))) __half qs[64][KS];
+  __shared__ float sc[64][DCHUNK + 4];
+  // Rows of fp16 staged 16 bytes at a time (rows past the cache or the block read as zero).
+  auto stage = [&](__half (*dst)[KS], const __half* src, int rows, int live) {
+    for (int i = tid; i < rows * RV; i += 256) {
+      const int r = i / RV, c = i % RV;
+      const uint4 v = r < live ? *reinterpret_cast<const uint4*>(src + size_t(r) * HD + 8 * c) : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(&dst[r][8 * c]) = v;
+    }
+  };
+  const int live_keys = max(0, min(DCHUNK, a.slots - n0));
+  stage(ks, a.kc + (size_t(kvh) * a.slots + n0) * HD, DCHUNK, live_keys);
+  stage(qs, a.q + size_t(kvh) * Q * HD, 64, Q);
   __syncthreads();
   const float scale = 1.0f / sqrtf(float(HD));
-  for (int i = threadIdx.x; i < Q * DCHUNK; i += 256) {
-    const int m = i / DCHUNK, n = i % DCHUNK, t = m / a.G;
-    float s = -INFINITY;
-    if (n0 + n < a.slots && dvisible(n0 + n, t, P, a.B, a.win)) {
-      const __half* qr = a.q + (size_t(kvh) * Q + m) * HD;
-      float acc = 0.f;
-      for (int dd = 0; dd < HD; ++dd) acc += __half2float(qr[dd]) * __half2float(ks[n][dd]);
-      s = acc * scale;
+  // Scores of query tile `wave` against the chunk's 8 key tiles: lane (n, qd) holds S[16w + 4qd + e][16t + n].
+  df4 sacc[DCHUNK / 16];
+#pragma unroll
+  for (int t = 0; t < DCHUNK / 16; ++t) {
+    df4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) {
+      const dh8 qa = *reinterpret_cast<const dh8*>(&qs[16 * wave + n][32 * s + 8 * qd]);
+      const dh8 kb = *reinterpret_cast<const dh8*>(&ks[16 * t + n][32 * s + 8 * qd]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa, kb, acc, 0, 0, 0);
     }
-    sc[m][n] = s;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 16 * wave + 4 * qd + e, key = 16 * t + n;
+      const bool vis = m < Q && key < live_keys && dvisible(n0 + key, m / a.G, P, a.B, a.win);
+      acc[e] = vis ? acc[e] * scale : -INFINITY;
+    }
+    sacc[t] = acc;
+  }
+  // Per query row (4qd + e of the tile): the chunk's max and Σ e^(s − max) over its 128 keys — 8 in each lane, then
+  // across the row's 16 lanes — and the weights e^(s − max) to LDS for the products.
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < DCHUNK / 16; ++t) mx = fmaxf(mx, sacc[t][e]);
+    mx = fmaxf(mx, lane_xor<1>(mx));
+    mx = fmaxf(mx, lane_xor<2>(mx));
+    mx = fmaxf(mx, lane_xor<4>(mx));
+    mx = fmaxf(mx, lane_xor<8>(mx));
+    const int m = 16 * wave + 4 * qd + e;
+    float l = 0.f;
+#pragma unroll
+    for (int t = 0; t < DCHUNK / 16; ++t) {
+      const float p = mx == -INFINITY ? 0.f : __expf(sacc[t][e] - mx);
+      sc[m][16 * t + n] = p;
+      l += p;
+    }
+    l += lane_xor<1>(l);
+    l += lane_xor<2>(l);
+    l += lane_xor<4>(l);
+    l += lane_xor<8>(l);
+    if (n == 0 && m < Q) ml[(size_t(kvh) * nchunk + ch) * Q + m] = make_float2(mx, l);
   }
   __syncthreads();
   // The chunk's V replaces its K in LDS.
-  for (int i = threadIdx.x; i < DCHUNK * HD; i += 256) {
-    const int n = i / HD, dd = i % HD;
-    ks[n][dd] = n0 + n < a.slots ? a.vc[(size_t(kvh) * a.slots + n0 + n) * HD + dd] : __float2half(0.f);
-  }
-  // Per query: the chunk's max and Σ e^(s − max) (one thread per query), the weights in place.
-  if (int(threadIdx.x) < Q) {
-    const int m = threadIdx.x;
-    float mx = -INFINITY;
-    for (int n = 0; n < DCHUNK; ++n) mx = fmaxf(mx, sc[m][n]);
-    float l = 0.f;
-    for (int n = 0; n < DCHUNK; ++n) {
-      const float p = mx == -INFINITY ? 0.f : __expf(sc[m][n] - mx);
-      sc[m][n] = p;
-      l += p;
-    }
-    ml[(size_t(kvh) * nchunk + ch) * Q + m] = make_float2(mx, l);
-  }
+  stage(ks, a.vc + (size_t(kvh) * a.slots + n0) * HD, DCHUNK, live_keys);
   __syncthreads();
-  for (int i = threadIdx.x; i < Q * HD; i += 256) {
-    const int m = i / HD, dd = i % HD;
-    float o = 0.f;
-    for (int n = 0; n < DCHUNK; ++n) {
-      o += sc[m][n] * __half2float(ks[n][dd]);
+  // O of query tile `wave`: dims tile d, four keys per step; lane (n, qd) ends with O[16w + 4qd + e][16d + n].
+  for (int d = 0; d < HD / 16; ++d) {
+    df4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < DCHUNK; k += 4) {
+      const float pa = sc[16 * wave + n][k + qd];
+      const float vb = __half2float(ks[k + qd][16 * d + n]);
+      o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vb, o, 0, 0, 0);
     }
-    opart[((size_t(kvh) * nchunk + ch) * Q + m) * HD + dd] = o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 16 * wave + 4 * qd + e;
+      if (m < Q) opart[((size_t(kvh) * nchunk + ch) * Q + m) * HD + 16 * d + n] = o[e];
+    }
   }
 }
 

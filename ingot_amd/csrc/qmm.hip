@@ -671,7 +671,8 @@ constexpr bool qmm_fits() {
 
 // Instantiated launch shapes (R, KW, KPW; ring depth qmm_ring_depth(KPW)) for each epilogue. Epilogues are compile-time:
 // the code of every mode in one kernel raised its register demand past the ring's (302 VGPRs at R = 7, KW = 4).
-// The kernel-level modes (QM_F32, QM_F32_ADD, QM_BF16) run as QM_PART + qmm_finish_kernel.
+// The kernel-level modes QM_F32_ADD and QM_BF16 run as QM_PART + qmm_finish_kernel; QM_F32 and the fused modes run in
+// the kernel itself.
 template <int T, bool X16, int MODE>
 static bool qmm_dispatch_mode(const TimedLaunch& tl, QmmShape sh, dim3 grid, hipStream_t st, const QmmParams& p) {
 #define IH_QMM_CASE(R_, KW_, KPW_)                                                                          \
@@ -706,6 +707,7 @@ template <int T, bool X16>
 static bool qmm_dispatch(const TimedLaunch& tl, QmmShape sh, dim3 grid, hipStream_t st, const QmmParams& p,
                          int mode) {
   switch (mode) {
+    case QM_F32: return qmm_dispatch_mode<T, X16, QM_F32>(tl, sh, grid, st, p);
     case QM_F32_SCALE: return qmm_dispatch_mode<T, X16, QM_F32_SCALE>(tl, sh, grid, st, p);
     case QM_RESID_ACT: return qmm_dispatch_mode<T, X16, QM_RESID_ACT>(tl, sh, grid, st, p);
     case QM_GLU_ACT: return qmm_dispatch_mode<T, X16, QM_GLU_ACT>(tl, sh, grid, st, p);
@@ -765,9 +767,10 @@ int launch_qmm_ex(ih_ctx* c, const ih_qmat* W, int expert, const ActBuf& a, int 
   }
   IH_CHECK(qmm_shape_ok(sh, W->Npad, W->nkb), IH_EINVAL, "qmm: launch shape does not tile the matrix");
   const int ks = sh.ks;
-  // The kernel runs the step's fused epilogues itself (with K split over workgroups, in the last workgroup of each
-  // row group to arrive); the kernel-level modes write partial sums that qmm_finish_kernel adds and applies.
-  const bool fused = ep.mode == QM_F32_SCALE || ep.mode == QM_RESID_ACT || ep.mode == QM_GLU_ACT;
+  // The kernel runs the step's fused epilogues and the plain fp32 output itself (with K split over workgroups, in the
+  // last workgroup of each row group to arrive); the other kernel-level modes (accumulate, bf16) write partial sums
+  // that qmm_finish_kernel adds and applies.
+  const bool fused = ep.mode == QM_F32_SCALE || ep.mode == QM_RESID_ACT || ep.mode == QM_GLU_ACT || ep.mode == QM_F32;
   const bool finish = !fused;
   const int kmode = finish ? int(QM_PART) : ep.mode;
   QmmParams p{};

@@ -29,11 +29,13 @@ __device__ __forceinline__ bool tk_better(float v, uint32_t i, float w, uint32_t
   return v > w || (v == w && i < j);
 }
 
-// Compare-exchange with lane ^ J: the lane ends with the better of the pair if keep_better, else the worse.
+// Compare-exchange with lane ^ J: the lane ends with the better of the pair if keep_better, else the worse. The
+// partner's value and id come through DPP / row-swap lane patterns (lane_xor), not an LDS round trip; every lane of
+// the wave is active wherever these run.
 template <int J>
 __device__ __forceinline__ void cx(float& v, uint32_t& id, bool keep_better) {
-  const float ov = __shfl_xor(v, J);
-  const uint32_t oi = uint32_t(__shfl_xor(int(id), J));
+  const float ov = lane_xor<J>(v);
+  const uint32_t oi = __float_as_uint(lane_xor<J>(__uint_as_float(id)));
   const bool take = keep_better ? tk_better(ov, oi, v, id) : tk_better(v, id, ov, oi);
   if (take) { v = ov; id = oi; }
 }
@@ -51,9 +53,14 @@ __device__ __forceinline__ void sort64(float& v, uint32_t& id, int lane) {
 }
 
 // The 64 best of two descending lists (the list in v/id, the other in bv/bi), descending, in v/id.
+// x of lane 63 − lane (= lane ^ 63): the row mirror (i ^ 15 within 16 lanes), then the row swaps 16 and 32.
+__device__ __forceinline__ float rev64(float x) {
+  return lane_xor<32>(lane_xor<16>(__int_as_float(dpp_mov<0x140>(__float_as_int(x)))));
+}
+
 __device__ __forceinline__ void merge64(float& v, uint32_t& id, float bv, uint32_t bi, int lane) {
-  const float rv = __shfl(bv, 63 - lane);
-  const uint32_t ri = uint32_t(__shfl(int(bi), 63 - lane));
+  const float rv = rev64(bv);
+  const uint32_t ri = __float_as_uint(rev64(__uint_as_float(bi)));
   if (tk_better(rv, ri, v, id)) { v = rv; id = ri; }
   // v is now bitonic (descending, then ascending); six half-cleaners sort it.
   cx<32>(v, id, (lane & 32) == 0);
@@ -95,8 +102,8 @@ __global__ __launch_bounds__(SPT) void topk64_part_kernel(const float* __restric
     if (ok) lse_add(c, it, mt, s);
     uint32_t cid = ok && c == c ? uint32_t(ci) : NO_ID;
     if (cid == NO_ID) c = -FLT_MAX;
-    const float tv = __shfl(v, 63);
-    const uint32_t ti = uint32_t(__shfl(int(id), 63));
+    const float tv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    const uint32_t ti = uint32_t(__builtin_amdgcn_readlane(int(id), 63));
     if (!__any(tk_better(c, cid, tv, ti))) continue;  // wave-uniform
     sort64(c, cid, lane);
     merge64(v, id, c, cid, lane);
@@ -220,29 +227,46 @@ __device__ uint32_t sample_pick(const uint32_t* ci, const float* pr, int n, uint
 // Acceptance by rejection (spec_accept_sample, zz_sample.metal:241-281): rows' candidates idx/val [rows][64] and
 // (max, Z) [rows][2]; uniforms rnd[round · IH_RND_PER_ROUND + 2i] (accept) and [… + 2i + 1] (resample) of row i. Writes the record
 // and advances the state as the greedy acceptance does (vtok[0] = the new anchor; the history as in accept_kernel).
-__global__ void accept_sample_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* cidx, const float* cval,
-                                     const float* z, uint32_t* rec, const float* rnd, ih_sample_params p, int ring,
-                                     int rows, uint32_t* hist, int hist_cap) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// One wave: every row's distribution is computed at once, one lane per row (each in the same sequential order as
+// before, so the results do not change), into LDS; lane 0 then walks the rows in order.
+__global__ __launch_bounds__(64) void accept_sample_kernel(uint32_t* st, uint32_t* vtok, const uint32_t* cidx,
+                                                           const float* cval, const float* z, uint32_t* rec,
+                                                           const float* rnd, ih_sample_params p, int ring, int rows,
+                                                           uint32_t* hist, int hist_cap) {
+  __shared__ float prs[IH_MAX_ROWS][SK];
+  __shared__ int ns[IH_MAX_ROWS];
+  __shared__ float qs[IH_MAX_ROWS];
+  const int lane = threadIdx.x;
   const uint32_t nr = rows ? uint32_t(rows) : min(max(st[6], 1u), uint32_t(IH_MAX_ROWS));
+  if (lane < int(nr)) {
+    const uint32_t* ci = cidx + lane * SK;
+    const int n = sample_dist(ci, cval + lane * SK, z[2 * lane], z[2 * lane + 1], p, prs[lane]);
+    float q = 0.f;
+    if (lane + 1 < int(nr)) {
+      const uint32_t d = vtok[lane + 1];
+      for (int j = 0; j < n; ++j)
+        if (ci[j] == d) q = prs[lane][j];
+    }
+    ns[lane] = n;
+    qs[lane] = q;
+  }
+  __syncthreads();
+  if (lane != 0) return;
   const float* u = rnd + size_t(st[5]) * IH_RND_PER_ROUND;
-  float pr[SK];
   uint32_t m = 0, next = 0;
   for (uint32_t i = 0; i < nr; ++i) {
     const uint32_t* ci = cidx + i * SK;
-    const int n = sample_dist(ci, cval + i * SK, z[2 * i], z[2 * i + 1], p, pr);
+    const int n = ns[i];
     if (i + 1 < nr) {
       const uint32_t d = vtok[i + 1];
-      float q = 0.f;
-      for (int j = 0; j < n; ++j)
-        if (ci[j] == d) q = pr[j];
+      const float q = qs[i];
       if (u[2 * i] < q) {
         ++m;
         continue;
       }
-      next = sample_pick(ci, pr, n, d, q, u[2 * i + 1]);
+      next = sample_pick(ci, prs[i], n, d, q, u[2 * i + 1]);
     } else {
-      next = sample_pick(ci, pr, n, NO_ID, 0.f, u[2 * i + 1]);
+      next = sample_pick(ci, prs[i], n, NO_ID, 0.f, u[2 * i + 1]);
     }
     break;
   }
