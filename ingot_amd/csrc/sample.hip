@@ -26,7 +26,7 @@ constexpr uint32_t NO_ID = 0xFFFFFFFFu;
 
 // (v, i) ranks before (w, j): larger value, ties to the lower id (tk_better, yy_model.metal:503).
 __device__ __forceinline__ bool tk_better(float v, uint32_t i, float w, uint32_t j) {
-  return v > w || (v == w && i < j);
+  return (v > w) | ((v == w) & (i < j));  // no short circuit: compares and masks, no branches
 }
 
 // Compare-exchange with lane ^ J: the lane ends with the better of the pair if keep_better, else the worse. The
@@ -36,8 +36,9 @@ template <int J>
 __device__ __forceinline__ void cx(float& v, uint32_t& id, bool keep_better) {
   const float ov = lane_xor<J>(v);
   const uint32_t oi = __float_as_uint(lane_xor<J>(__uint_as_float(id)));
-  const bool take = keep_better ? tk_better(ov, oi, v, id) : tk_better(v, id, ov, oi);
-  if (take) { v = ov; id = oi; }
+  const bool take = (keep_better & tk_better(ov, oi, v, id)) | (!keep_better & tk_better(v, id, ov, oi));
+  v = take ? ov : v;
+  id = take ? oi : id;
 }
 
 // Bitonic sort of one value per lane into descending rank order (lane 0 the best).
@@ -61,7 +62,9 @@ __device__ __forceinline__ float rev64(float x) {
 __device__ __forceinline__ void merge64(float& v, uint32_t& id, float bv, uint32_t bi, int lane) {
   const float rv = rev64(bv);
   const uint32_t ri = __float_as_uint(rev64(__uint_as_float(bi)));
-  if (tk_better(rv, ri, v, id)) { v = rv; id = ri; }
+  const bool take = tk_better(rv, ri, v, id);
+  v = take ? rv : v;
+  id = take ? ri : id;
   // v is now bitonic (descending, then ascending); six half-cleaners sort it.
   cx<32>(v, id, (lane & 32) == 0);
   cx<16>(v, id, (lane & 16) == 0);
@@ -74,20 +77,25 @@ __device__ __forceinline__ void merge64(float& v, uint32_t& id, float bv, uint32
 // Online (max, Σ exp((x − max)/T)) of one lane, and their combination (the max starts at −FLT_MAX, as the
 // reference's, so −inf logits add exp(−inf) = 0). NaN logits are left out.
 __device__ __forceinline__ void lse_add(float c, float it, float& mt, float& s) {
-  if (c != c) return;
-  if (c > mt) {
-    s = s * __expf((mt - c) * it) + 1.0f;
-    mt = c;
-  } else {
-    s += __expf((c - mt) * it);
-  }
+  // Written with selects: exp(0) is taken as exactly 1 where either operand is the new max.
+  const float nm = fmaxf(mt, c);  // NaN c leaves the max
+  const float add = c != c ? 0.f : (c == nm ? 1.0f : __expf((c - nm) * it));
+  s = (mt == nm ? s : s * __expf((mt - nm) * it)) + add;
+  mt = nm;
 }
 
+// A chunk's 64 best (value, id) and its (max, Σ exp((x − max)/T)). Each wave keeps its sorted list in registers and
+// a buffer of pending candidates in LDS: an element enters the buffer only if it beats the list's 64th entry (which
+// only rises), and the buffer is sorted and merged into the list whenever it holds 64 — a few times per wave instead
+// of once per batch of 64 elements. The list is exactly the 64 best of the wave's elements: an element that does not
+// beat the 64th best seen so far is not among the 64 best of all.
 __global__ __launch_bounds__(SPT) void topk64_part_kernel(const float* __restrict__ x, int ldx, int V, float temp,
                                                           uint32_t* __restrict__ pidx, float* __restrict__ pval,
                                                           float2* __restrict__ pz) {
   __shared__ float sv[SPT / 64][SK];
   __shared__ uint32_t si[SPT / 64][SK];
+  __shared__ float bv[SPT / 64][2 * SK];
+  __shared__ uint32_t bi[SPT / 64][2 * SK];
   __shared__ float rm[SPT / 64], rs[SPT / 64];
   const int g = blockIdx.x, row = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float it = 1.0f / temp;
@@ -95,18 +103,78 @@ __global__ __launch_bounds__(SPT) void topk64_part_kernel(const float* __restric
   const int C = (V + SPG - 1) / SPG, lo = g * C, hi = min(V, lo + C);
   float v = -FLT_MAX, mt = -FLT_MAX, s = 0.f;
   uint32_t id = NO_ID;
-  for (int base = lo + wave * 64; base < hi; base += SPT) {
-    const int ci = base + lane;
+  int pend = 0;  // candidates in the wave's buffer (uniform)
+  // Sort the buffer's first 64 and merge them into the list; the rest (fewer than 64) move to the front.
+  auto flush = [&]() {
+    float c = lane < pend ? bv[wave][lane] : -FLT_MAX;
+    uint32_t cid = lane < pend ? bi[wave][lane] : NO_ID;
+    sort64(c, cid, lane);
+    merge64(v, id, c, cid, lane);
+    const int rest = max(0, pend - SK);
+    float nv = 0.f;
+    uint32_t ni = 0;
+    if (lane < rest) {
+      nv = bv[wave][SK + lane];
+      ni = bi[wave][SK + lane];
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < rest) {
+      bv[wave][lane] = nv;
+      bi[wave][lane] = ni;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    pend = rest;
+  };
+  auto process = [&](float c, int ci) {
     const bool ok = ci < hi;
-    float c = ok ? xr[ci] : -FLT_MAX;
     if (ok) lse_add(c, it, mt, s);
     uint32_t cid = ok && c == c ? uint32_t(ci) : NO_ID;
     if (cid == NO_ID) c = -FLT_MAX;
     const float tv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
     const uint32_t ti = uint32_t(__builtin_amdgcn_readlane(int(id), 63));
-    if (!__any(tk_better(c, cid, tv, ti))) continue;  // wave-uniform
-    sort64(c, cid, lane);
-    merge64(v, id, c, cid, lane);
+    const bool take = tk_better(c, cid, tv, ti);
+    const unsigned long long m = __ballot(take);
+    if (m == 0ull) return;  // wave-uniform
+    const int at = pend + int(__popcll(m & ((1ull << lane) - 1ull)));
+    if (take) {
+      bv[wave][at] = c;
+      bi[wave][at] = cid;
+    }
+    pend += int(__popcll(m));
+    if (pend >= SK) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the other lanes' buffer writes, in order
+      __builtin_amdgcn_wave_barrier();
+      flush();
+    }
+  };
+  // The wave's tiles of 256: element base + 64k + lane for k < 4 (coalesced loads, the next tile's requested before
+  // this one is processed; indices clamped to the chunk, so the loads need no branches).
+  auto ld = [&](int i) { return xr[min(i, hi - 1)]; };
+  int base = lo + wave * 256;
+  float c0 = 0.f, c1 = 0.f, c2 = 0.f, c3 = 0.f;
+  if (base < hi) {
+    c0 = ld(base + lane);
+    c1 = ld(base + 64 + lane);
+    c2 = ld(base + 128 + lane);
+    c3 = ld(base + 192 + lane);
+  }
+  for (; base < hi; base += SPT * 4) {
+    const int nb = base + SPT * 4;
+    const float n0 = ld(nb + lane), n1 = ld(nb + 64 + lane), n2 = ld(nb + 128 + lane), n3 = ld(nb + 192 + lane);
+    process(c0, base + lane);
+    process(c1, base + 64 + lane);
+    process(c2, base + 128 + lane);
+    process(c3, base + 192 + lane);
+    c0 = n0;
+    c1 = n1;
+    c2 = n2;
+    c3 = n3;
+  }
+  if (pend > 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    flush();
   }
   // The wave's (max, sum), then the workgroup's lists and sums.
   float m = mt;
@@ -145,17 +213,28 @@ __global__ __launch_bounds__(SPT) void topk64_part_kernel(const float* __restric
   }
 }
 
-__global__ __launch_bounds__(64) void topk64_merge_kernel(const uint32_t* __restrict__ pidx,
-                                                          const float* __restrict__ pval,
-                                                          const float2* __restrict__ pz, float temp,
-                                                          uint32_t* __restrict__ idx, float* __restrict__ val,
-                                                          float* __restrict__ z) {
-  const int row = blockIdx.x, lane = threadIdx.x;
+// One workgroup of 4 waves per row: wave w merges the chunk lists 8w … 8w + 7, then wave 0 merges the four results
+// (the merge is exact, so its order does not change the list); lane 0 combines the chunks' (max, sum) in chunk order.
+__global__ __launch_bounds__(256) void topk64_merge_kernel(const uint32_t* __restrict__ pidx,
+                                                           const float* __restrict__ pval,
+                                                           const float2* __restrict__ pz, float temp,
+                                                           uint32_t* __restrict__ idx, float* __restrict__ val,
+                                                           float* __restrict__ z) {
+  constexpr int NW = 4, PER = SPG / NW;
+  __shared__ float wv[NW][SK];
+  __shared__ uint32_t wi[NW][SK];
+  const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float it = 1.0f / temp;
   const size_t o = size_t(row) * SPG * SK;
-  float v = pval[o + lane];
-  uint32_t id = pidx[o + lane];
-  for (int g = 1; g < SPG; ++g) merge64(v, id, pval[o + g * SK + lane], pidx[o + g * SK + lane], lane);
+  const int g0 = wave * PER;
+  float v = pval[o + g0 * SK + lane];
+  uint32_t id = pidx[o + g0 * SK + lane];
+  for (int g = g0 + 1; g < g0 + PER; ++g) merge64(v, id, pval[o + g * SK + lane], pidx[o + g * SK + lane], lane);
+  wv[wave][lane] = v;
+  wi[wave][lane] = id;
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w = 1; w < NW; ++w) merge64(v, id, wv[w][lane], wi[w][lane], lane);
   idx[size_t(row) * SK + lane] = id;
   val[size_t(row) * SK + lane] = v;
   if (lane == 0) {
@@ -340,7 +419,7 @@ int launch_topk64(ih_ctx* c, const float* x, int ldx, int rows, int V, float tem
     tlaunch(tl, topk64_part_kernel, dim3(SPG, rows), dim3(SPT), 0, c->stream, x, ldx, V, temp, pidx, pval, pz);
     IH_HIP(hipGetLastError());
   }
-  topk64_merge_kernel<<<rows, 64, 0, c->stream>>>(pidx, pval, pz, temp, idx, val, z);
+  topk64_merge_kernel<<<rows, 256, 0, c->stream>>>(pidx, pval, pz, temp, idx, val, z);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
