@@ -82,6 +82,7 @@ struct ih_drafter {
   float2* ml = nullptr;     // [KVH][nchunk][G·block]
   uint32_t* cidx = nullptr; // [block][64] candidates (the first 16 are the top-16)
   float *cval = nullptr, *cz = nullptr, *conf = nullptr;
+  float* esel = nullptr;      // [block][16][16] selector scores per (position, previous pick, candidate)
   ActBuf act_h, act_a, act_i, act_c, act_f;  // [H]: norm/conv outputs; [QH·HD]: attention; [I]: MLP; caps; fc out
 };
 
@@ -414,51 +415,98 @@ __global__ void dattn_reduce_kernel(const float* __restrict__ opart, const float
 // The greedy selector (dselect, yy_model.metal:569-614): at position t the candidate j with the highest
 // val[t][j] + Σ_r pred[prev][r]·hp[t][r]·succ[cand_j][r] (prev = the anchor at t = 0, else the pick at t − 1; the first
 // if tied); tok[1 + t] = the pick, conf[t] = its softmax(score/τ) over the 16. rank = 0: the best candidate
-// (dpick_top1). One workgroup of `rank` threads (a multiple of 64, ≤ 1024).
-__global__ void dselect_kernel(const uint32_t* __restrict__ cand, const float* __restrict__ val, int ldc,
-                               const float* __restrict__ hp, const uint16_t* __restrict__ pred,
-                               const uint16_t* __restrict__ succ, int rank, uint32_t* __restrict__ tok, int M,
-                               float* __restrict__ conf) {
+// (dpick_top1).
+//
+// The pick at t − 1 is one of the 16 candidates of t − 1, so the bilinear term depends on the chain only through
+// that index: dselect_pairs_kernel computes it for every (t, i, j) — i the index of the previous pick among the
+// candidates of t − 1 (only i = 0, the anchor, at t = 0) — in parallel, one workgroup of `rank` threads (a multiple
+// of 64, ≤ 1024) per (t, i); dselect_kernel then walks t in one wave over those scores in LDS. Each E[t][i][j] is
+// summed in one fixed order (64-lane butterfly, then the waves in order) whatever the chain.
+constexpr int DSEL = DTOPK * DTOPK;  // E entries per position
+__global__ void dselect_pairs_kernel(const uint32_t* __restrict__ cand, int ldc, const float* __restrict__ hp,
+                                     const uint16_t* __restrict__ pred, const uint16_t* __restrict__ succ, int rank,
+                                     const uint32_t* __restrict__ tok, float* __restrict__ E) {
   __shared__ float part[16][DTOPK];
-  __shared__ uint32_t chosen;
-  const int r = threadIdx.x, wave = r >> 6, lane = r & 63, nw = int(blockDim.x) >> 6;
-  uint32_t prev = tok[0];
+  const int t = blockIdx.x, i = blockIdx.y, r = threadIdx.x, wave = r >> 6, lane = r & 63, nw = int(blockDim.x) >> 6;
+  if (t == 0 && i > 0) return;  // the anchor is the only previous token at t = 0
+  const uint32_t prev = t == 0 ? tok[0] : cand[size_t(t - 1) * ldc + i];
+  const float a = dbf16(pred[size_t(prev) * rank + r]) * hp[size_t(t) * rank + r];
+  for (int j = 0; j < DTOPK; ++j) {
+    float e = a * dbf16(succ[size_t(cand[size_t(t) * ldc + j]) * rank + r]);
+    e += lane_xor<32>(e);
+    e += lane_xor<16>(e);
+    e += lane_xor<8>(e);
+    e += lane_xor<4>(e);
+    e += lane_xor<2>(e);
+    e += lane_xor<1>(e);
+    if (lane == 0) part[wave][j] = e;
+  }
+  __syncthreads();
+  if (r < DTOPK) {
+    float e = 0.f;
+    for (int q = 0; q < nw; ++q) e += part[q][r];
+    E[size_t(t) * DSEL + i * DTOPK + r] = e;
+  }
+}
+
+// 256 threads stage the scores of all positions in LDS (every load issued before the first store), then one wave
+// walks the chain (E = nullptr: rank 0).
+__global__ __launch_bounds__(256) void dselect_kernel(const uint32_t* __restrict__ cand, const float* __restrict__ val,
+                                                      int ldc, const float* __restrict__ E, uint32_t* __restrict__ tok,
+                                                      int M, float* __restrict__ conf) {
+  constexpr int NE = 16 * DSEL / 4 / 256;  // float4 loads of E per thread
+  __shared__ float4 es4[16 * DSEL / 4];
+  __shared__ float vs[16][DTOPK];
+  __shared__ uint32_t cs[16][DTOPK];
+  const int tid = threadIdx.x;
+  float4 q[NE];
+#pragma unroll
+  for (int u = 0; u < NE; ++u) {
+    const int k = tid + 256 * u;
+    q[u] = E && k < M * DSEL / 4 ? reinterpret_cast<const float4*>(E)[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const int t0 = tid / DTOPK, j0 = tid % DTOPK;
+  float v0 = 0.f;
+  uint32_t c0 = 0;
+  if (t0 < M) {
+    v0 = val[size_t(t0) * ldc + j0];
+    c0 = cand[size_t(t0) * ldc + j0];
+  }
+#pragma unroll
+  for (int u = 0; u < NE; ++u) es4[tid + 256 * u] = q[u];
+  vs[t0][j0] = v0;
+  cs[t0][j0] = c0;
+  __syncthreads();
+  if (tid >= 64) return;
+  // Wave 0 walks the chain, lane j (mod 16) on candidate j: the first maximum by a butterfly over the 16 (NaN scores
+  // never picked, as with a strict > from −inf), then Σ exp((s − s_best)/τ) by another.
+  const float* es = reinterpret_cast<const float*>(es4);
+  const int j = tid & (DTOPK - 1);
+  int pi = 0;  // index of the previous pick among the previous position's candidates (0: the anchor)
   for (int t = 0; t < M; ++t) {
-    if (rank > 0) {
-      const float a = dbf16(pred[size_t(prev) * rank + r]) * hp[size_t(t) * rank + r];
-      for (int j = 0; j < DTOPK; ++j) {
-        float e = a * dbf16(succ[size_t(cand[size_t(t) * ldc + j]) * rank + r]);
-        e += lane_xor<32>(e);
-        e += lane_xor<16>(e);
-        e += lane_xor<8>(e);
-        e += lane_xor<4>(e);
-        e += lane_xor<2>(e);
-        e += lane_xor<1>(e);
-        if (lane == 0) part[wave][j] = e;
-      }
+    const float sc = vs[t][j] + es[t * DSEL + pi * DTOPK + j];
+    float bs = sc != sc ? -INFINITY : sc;
+    int best = j;
+#define IH_PICK(H)                                                                           \
+    {                                                                                        \
+      const float ob = lane_xor<H>(bs);                                                      \
+      const int oj = __float_as_int(lane_xor<H>(__int_as_float(best)));                      \
+      const bool take = (ob > bs) | ((ob == bs) & (oj < best));                              \
+      bs = take ? ob : bs;                                                                   \
+      best = take ? oj : best;                                                               \
     }
-    __syncthreads();
-    if (r == 0) {
-      int best = 0;
-      float bs = -INFINITY, scs[DTOPK];
-      for (int j = 0; j < DTOPK; ++j) {
-        float e = 0.f;
-        for (int q = 0; q < nw && rank > 0; ++q) e += part[q][j];
-        const float s = val[size_t(t) * ldc + j] + e;
-        scs[j] = s;
-        if (s > bs) {
-          bs = s;
-          best = j;
-        }
-      }
-      chosen = cand[size_t(t) * ldc + best];
-      tok[1 + t] = chosen;
-      float z = 0.f;
-      for (int j = 0; j < DTOPK; ++j) z += __expf((scs[j] - bs) / CONF_TAU);
+    IH_PICK(1) IH_PICK(2) IH_PICK(4) IH_PICK(8)
+#undef IH_PICK
+    float z = __expf((sc - bs) / CONF_TAU);
+    z += lane_xor<1>(z);
+    z += lane_xor<2>(z);
+    z += lane_xor<4>(z);
+    z += lane_xor<8>(z);
+    if (tid == 0) {
+      tok[1 + t] = cs[t][best];
       conf[t] = 1.0f / z;
     }
-    __syncthreads();
-    prev = chosen;
+    pi = best;
   }
 }
 
@@ -501,7 +549,7 @@ static void drafter_release(ih_drafter* r) {
   for (void* p : {(void*)r->hnorm, (void*)r->fnorm, (void*)r->pred, (void*)r->succ, (void*)r->caps, (void*)r->dtok, (void*)r->rope,
                   (void*)r->x, (void*)r->proj, (void*)r->dyn, (void*)r->y, (void*)r->gu, (void*)r->logits,
                   (void*)r->hp, (void*)r->xn, (void*)r->q, (void*)r->opart, (void*)r->ml, (void*)r->cidx,
-                  (void*)r->cval, (void*)r->cz, (void*)r->conf})
+                  (void*)r->cval, (void*)r->cz, (void*)r->conf, (void*)r->esel})
     if (p) (void)hipFree(p);
   for (ActBuf* a : {&r->act_h, &r->act_a, &r->act_i, &r->act_c, &r->act_f}) free_act(*a);
   delete r;
@@ -596,6 +644,7 @@ static int drafter_finish(ih_drafter* r, int st, ih_drafter** out) {
   run(dalloc_t(&r->cval, size_t(16) * IH_TOPK));
   run(dalloc_t(&r->cz, 32));
   run(dalloc_t(&r->conf, 16));
+  run(dalloc_t(&r->esel, size_t(16) * DSEL));
   if (st == IH_OK) run(ensure_act(c, r->act_h, H, false));
   if (st == IH_OK) run(ensure_act(c, r->act_a, QH * HD, false));
   if (st == IH_OK) run(ensure_act(c, r->act_i, I, false));
@@ -856,8 +905,13 @@ int ih_drafter_block(ih_drafter* r, uint32_t* vtok_dev, int P, const uint32_t* s
   IH_TRY(launch_qmm(c, t->head, 0, r->act_f, M, r->logits, V, QM_F32));
   IH_TRY(launch_topk64(c, r->logits, V, M, V, 1.0f, r->cidx, r->cval, r->cz));
   if (d.rank > 0) IH_TRY(launch_qmm(c, r->hproj, 0, r->act_f, M, r->hp, d.rank, QM_F32));
-  dselect_kernel<<<1, d.rank > 0 ? d.rank : 64, 0, c->stream>>>(r->cidx, r->cval, IH_TOPK, r->hp, r->pred, r->succ,
-                                                                 d.rank, vtok_dev, M, conf_dev ? conf_dev : r->conf);
+  if (d.rank > 0) {
+    dselect_pairs_kernel<<<dim3(M, DTOPK), d.rank, 0, c->stream>>>(r->cidx, IH_TOPK, r->hp, r->pred, r->succ, d.rank,
+                                                                   vtok_dev, r->esel);
+    IH_HIP(hipGetLastError());
+  }
+  dselect_kernel<<<1, 256, 0, c->stream>>>(r->cidx, r->cval, IH_TOPK, d.rank > 0 ? r->esel : nullptr, vtok_dev, M,
+                                          conf_dev ? conf_dev : r->conf);
   IH_HIP(hipGetLastError());
   return IH_OK;
 }
