@@ -134,37 +134,97 @@ __global__ __launch_bounds__(256) void dconv_prep_kernel(const uint16_t* __restr
                                                          int ldd, const uint16_t* __restrict__ base, int H, int G,
                                                          uint4* __restrict__ frag, int nkb, int ntile) {
   const int t = blockIdx.x;
+  // Eight consecutive channels (one conv group) per thread and chunk, 16-byte loads of the bf16 rows.
+#pragma unroll 2
   for (int c8 = threadIdx.x; c8 < H / 8; c8 += 256) {
+    const int c = 8 * c8, g = c / DCG;
+    const uint4 a0 = *reinterpret_cast<const uint4*>(xn + size_t(t) * H + c);
+    const uint4 a1 = t > 0 ? *reinterpret_cast<const uint4*>(xn + size_t(t - 1) * H + c) : make_uint4(0, 0, 0, 0);
+    const uint4 b0 = *reinterpret_cast<const uint4*>(base + c), b1 = *reinterpret_cast<const uint4*>(base + H + c);
+    const float d0 = dyn[size_t(t) * ldd + g], d1 = dyn[size_t(t) * ldd + G + g];
+    const uint32_t x0w[4] = {a0.x, a0.y, a0.z, a0.w}, x1w[4] = {a1.x, a1.y, a1.z, a1.w};
+    const uint32_t k0w[4] = {b0.x, b0.y, b0.z, b0.w}, k1w[4] = {b1.x, b1.y, b1.z, b1.w};
     float v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int c = 8 * c8 + j, g = c / DCG;
-      const float x0 = dbf16(xn[size_t(t) * H + c]), x1 = t > 0 ? dbf16(xn[size_t(t - 1) * H + c]) : 0.f;
-      const float k0 = dbf16(base[c]) + dyn[size_t(t) * ldd + g];
-      const float k1 = dbf16(base[H + c]) + dyn[size_t(t) * ldd + G + g];
+      const int sh = 16 * (j & 1);
+      const float x0 = dbf16(uint16_t(x0w[j / 2] >> sh)), x1 = dbf16(uint16_t(x1w[j / 2] >> sh));
+      const float k0 = dbf16(uint16_t(k0w[j / 2] >> sh)) + d0;
+      const float k1 = dbf16(uint16_t(k1w[j / 2] >> sh)) + d1;
       v[j] = k0 * x0 + k1 * x1;
     }
     frag_store_chunk(frag, nkb, ntile, t, c8, v);
   }
 }
 
-// The conv after a sublayer, added to the residual (dconv_fin_add): x_t += (base[1][0] + dyn_t[2][g])·y_t +
-// (base[1][1] + dyn_t[3][g])·y_{t−1}. Without dyn (DFlash v1) x += y. Grid (rows), 256 threads.
-__global__ __launch_bounds__(256) void dconv_fin_kernel(const float* __restrict__ y, const float* __restrict__ dyn,
+// The conv after a sublayer added to the residual (dconv_fin_add): x_t += (base[1][0] + dyn_t[2][g])·y_t +
+// (base[1][1] + dyn_t[3][g])·y_{t−1}, without dyn (DFlash v1) x += y; then, in the same launch, the next RMSNorm of
+// the row (rows t ≥ first; fragment row t − first). Grid (rows), 256 threads; H a multiple of 8.
+__global__ __launch_bounds__(256) void dfin_norm_kernel(const float* __restrict__ y, const float* __restrict__ dyn,
                                                         int ldd, const uint16_t* __restrict__ base, int H, int G,
-                                                        float* __restrict__ x) {
+                                                        float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                        float eps, int first, uint4* __restrict__ frag, int nkb,
+                                                        int ntile, uint16_t* __restrict__ xn) {
+  __shared__ float red[4];
   const int t = blockIdx.x;
-  for (int c = threadIdx.x; c < H; c += 256) {
-    const float y0 = y[size_t(t) * H + c];
+  float* xr = x + size_t(t) * H;
+  float ss = 0.f;
+  // Eight consecutive channels per thread (one conv group: DCG is a multiple of 8), 16-byte loads, two chunks of
+  // eight per pass so that their loads are in flight together.
+#pragma unroll 2
+  for (int c8 = threadIdx.x; c8 < H / 8; c8 += 256) {
+    const int c = 8 * c8;
+    const float4* yp = reinterpret_cast<const float4*>(y + size_t(t) * H + c);
+    float4* xp = reinterpret_cast<float4*>(xr + c);
+    const float4 ya = yp[0], yb = yp[1], xa = xp[0], xb = xp[1];
+    float y0[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+    float nx[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
     if (!dyn) {
-      x[size_t(t) * H + c] += y0;
-      continue;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) nx[j] += y0[j];
+    } else {
+      const int g = c / DCG;
+      float y1[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (t > 0) {
+        const float4* qp = reinterpret_cast<const float4*>(y + size_t(t - 1) * H + c);
+        const float4 qa = qp[0], qb = qp[1];
+        y1[0] = qa.x; y1[1] = qa.y; y1[2] = qa.z; y1[3] = qa.w;
+        y1[4] = qb.x; y1[5] = qb.y; y1[6] = qb.z; y1[7] = qb.w;
+      }
+      const uint4 b2 = *reinterpret_cast<const uint4*>(base + 2 * H + c);
+      const uint4 b3 = *reinterpret_cast<const uint4*>(base + 3 * H + c);
+      const float d2 = dyn[size_t(t) * ldd + 2 * G + g], d3 = dyn[size_t(t) * ldd + 3 * G + g];
+      const uint32_t w2[4] = {b2.x, b2.y, b2.z, b2.w}, w3[4] = {b3.x, b3.y, b3.z, b3.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float k0 = dbf16(uint16_t(w2[j / 2] >> (16 * (j & 1)))) + d2;
+        const float k1 = dbf16(uint16_t(w3[j / 2] >> (16 * (j & 1)))) + d3;
+        nx[j] = nx[j] + (k0 * y0[j] + k1 * y1[j]);
+      }
     }
-    const int g = c / DCG;
-    const float y1 = t > 0 ? y[size_t(t - 1) * H + c] : 0.f;
-    const float k0 = dbf16(base[2 * H + c]) + dyn[size_t(t) * ldd + 2 * G + g];
-    const float k1 = dbf16(base[3 * H + c]) + dyn[size_t(t) * ldd + 3 * G + g];
-    x[size_t(t) * H + c] += k0 * y0 + k1 * y1;
+    xp[0] = make_float4(nx[0], nx[1], nx[2], nx[3]);
+    xp[1] = make_float4(nx[4], nx[5], nx[6], nx[7]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += nx[j] * nx[j];
+  }
+  if (t < first) return;  // whole workgroup
+  ss += lane_xor<32>(ss);
+  ss += lane_xor<16>(ss);
+  ss += lane_xor<8>(ss);
+  ss += lane_xor<4>(ss);
+  ss += lane_xor<2>(ss);
+  ss += lane_xor<1>(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();  // also makes the row's new values visible across the workgroup
+  const float rr = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / float(H) + eps);
+  for (int c8 = threadIdx.x; c8 < H / 8; c8 += 256) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] = xr[8 * c8 + j] * rr * dbf16(w[8 * c8 + j]);
+      if (xn) xn[size_t(t) * H + 8 * c8 + j] = dround_bf16(v[j]);
+    }
+    frag_store_chunk(frag, nkb, ntile, t - first, c8, v);
   }
 }
 
@@ -396,16 +456,22 @@ __global__ void dattn_reduce_kernel(const float* __restrict__ opart, const float
   const int t = blockIdx.x, h = blockIdx.y, kvh = h / G, m = t * G + h % G, Q = G * B;
   const int c8 = threadIdx.x;  // dims 8·c8 …
   float M = -INFINITY;
+#pragma unroll 8
   for (int s = 0; s < nchunk; ++s) M = fmaxf(M, ml[(size_t(kvh) * nchunk + s) * Q + m].x);
   float L = 0.f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  // Loads without branches (an empty chunk's partial is read and not added), so an unrolled group's requests are in
+  // flight together.
+#pragma unroll 4
   for (int s = 0; s < nchunk; ++s) {
     const float2 v = ml[(size_t(kvh) * nchunk + s) * Q + m];
-    if (v.x == -INFINITY) continue;
-    const float w = __expf(v.x - M);
-    L += w * v.y;
-    const float* op = opart + ((size_t(kvh) * nchunk + s) * Q + m) * HD + 8 * c8;
+    const float4* op = reinterpret_cast<const float4*>(opart + ((size_t(kvh) * nchunk + s) * Q + m) * HD + 8 * c8);
+    const float4 p0 = op[0], p1 = op[1];
+    const bool live = v.x != -INFINITY;
+    const float w = live ? __expf(v.x - M) : 0.f;
+    L = live ? L + w * v.y : L;
+    const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] += w * op[j];
+    for (int j = 0; j < 8; ++j) o[j] = live ? o[j] + w * pv[j] : o[j];
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = L > 0.f ? o[j] / L : 0.f;
@@ -848,11 +914,13 @@ int ih_drafter_block(ih_drafter* r, uint32_t* vtok_dev, int P, const uint32_t* s
   a.st = st_dev;
   a.P = P;
   const bool conv = d.dyn_conv != 0;
-  for (auto& L : r->layers) {
-    // Attention sublayer.
-    dnorm_kernel<<<B, 256, 0, c->stream>>>(r->x, H, L.n1, d.rms_eps, 0, static_cast<uint4*>(r->act_h.frag),
-                                           r->act_h.nkb, r->act_h.ntile, conv ? r->xn : nullptr);
-    IH_HIP(hipGetLastError());
+  // The first layer's attention norm; every later norm is launched with the conv that precedes it.
+  dnorm_kernel<<<B, 256, 0, c->stream>>>(r->x, H, r->layers[0].n1, d.rms_eps, 0, static_cast<uint4*>(r->act_h.frag),
+                                         r->act_h.nkb, r->act_h.ntile, conv ? r->xn : nullptr);
+  IH_HIP(hipGetLastError());
+  for (size_t li = 0; li < r->layers.size(); ++li) {
+    auto& L = r->layers[li];
+    const bool last = li + 1 == r->layers.size();
     if (conv) {
       IH_TRY(launch_qmm(c, L.aproj, 0, r->act_h, B, r->dyn, r->DYN, QM_F32));
       dconv_prep_kernel<<<B, 256, 0, c->stream>>>(r->xn, r->dyn, r->DYN, L.abase, H, G,
@@ -878,11 +946,10 @@ int ih_drafter_block(ih_drafter* r, uint32_t* vtok_dev, int P, const uint32_t* s
                                                                 r->act_a.ntile);
     IH_HIP(hipGetLastError());
     IH_TRY(launch_qmm(c, L.o, 0, r->act_a, B, r->y, H, QM_F32));
-    dconv_fin_kernel<<<B, 256, 0, c->stream>>>(r->y, conv ? r->dyn : nullptr, r->DYN, L.abase, H, G, r->x);
-    IH_HIP(hipGetLastError());
-    // MLP sublayer.
-    dnorm_kernel<<<B, 256, 0, c->stream>>>(r->x, H, L.n2, d.rms_eps, 0, static_cast<uint4*>(r->act_h.frag),
-                                           r->act_h.nkb, r->act_h.ntile, conv ? r->xn : nullptr);
+    // The conv into the residual and the MLP sublayer's norm.
+    dfin_norm_kernel<<<B, 256, 0, c->stream>>>(r->y, conv ? r->dyn : nullptr, r->DYN, L.abase, H, G, r->x, L.n2,
+                                               d.rms_eps, 0, static_cast<uint4*>(r->act_h.frag), r->act_h.nkb,
+                                               r->act_h.ntile, conv ? r->xn : nullptr);
     IH_HIP(hipGetLastError());
     if (conv) {
       IH_TRY(launch_qmm(c, L.mproj, 0, r->act_h, B, r->dyn, r->DYN, QM_F32));
@@ -895,13 +962,20 @@ int ih_drafter_block(ih_drafter* r, uint32_t* vtok_dev, int P, const uint32_t* s
                                              r->act_i.ntile);
     IH_HIP(hipGetLastError());
     IH_TRY(launch_qmm(c, L.down, 0, r->act_i, B, r->y, H, QM_F32));
-    dconv_fin_kernel<<<B, 256, 0, c->stream>>>(r->y, conv ? r->dyn : nullptr, r->DYN, L.mbase, H, G, r->x);
+    // The conv into the residual and the next layer's attention norm, after the last layer the final norm of rows
+    // 1 … B − 1.
+    if (!last)
+      dfin_norm_kernel<<<B, 256, 0, c->stream>>>(r->y, conv ? r->dyn : nullptr, r->DYN, L.mbase, H, G, r->x,
+                                                 r->layers[li + 1].n1, d.rms_eps, 0,
+                                                 static_cast<uint4*>(r->act_h.frag), r->act_h.nkb, r->act_h.ntile,
+                                                 conv ? r->xn : nullptr);
+    else
+      dfin_norm_kernel<<<B, 256, 0, c->stream>>>(r->y, conv ? r->dyn : nullptr, r->DYN, L.mbase, H, G, r->x,
+                                                 r->fnorm, d.rms_eps, 1, static_cast<uint4*>(r->act_f.frag),
+                                                 r->act_f.nkb, r->act_f.ntile, nullptr);
     IH_HIP(hipGetLastError());
   }
-  // Final norm of rows 1 … B − 1, the target's head, the top-16 candidates and the selector.
-  dnorm_kernel<<<M, 256, 0, c->stream>>>(r->x, H, r->fnorm, d.rms_eps, 1, static_cast<uint4*>(r->act_f.frag),
-                                         r->act_f.nkb, r->act_f.ntile, nullptr);
-  IH_HIP(hipGetLastError());
+  // The target's head over rows 1 … B − 1, the top-16 candidates and the selector.
   IH_TRY(launch_qmm(c, t->head, 0, r->act_f, M, r->logits, V, QM_F32));
   IH_TRY(launch_topk64(c, r->logits, V, M, V, 1.0f, r->cidx, r->cval, r->cz));
   if (d.rank > 0) IH_TRY(launch_qmm(c, r->hproj, 0, r->act_f, M, r->hp, d.rank, QM_F32));
