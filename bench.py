@@ -78,9 +78,21 @@ def main() -> int:
                     help="skip the side measurements (config 0's qmm, the decode loop, the other configurations' step times)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only copy BYTES device-to-device 4 times (the reference kernel that scales the HBM counters)")
+    ap.add_argument("--decode-loop-only", action="store_true",
+                    help="only the decode-loop side measurement on config 1's model (for kernel traces of its rounds)")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.decode_loop_only:
+        from ingot_amd._lib import Context, Model, ModelDesc
+
+        ctx = Context(0)
+        cfg = CONFIGS["dense8b-8k"]
+        model = Model(ctx, ModelDesc.make(**cfg["desc"]), SEED)
+        print(json.dumps({"decode_loop": decode_loop(model, cfg["P"], ANCHOR)}), flush=True)
+        model.free()
+        ctx.close()
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (sharding the verify step "
               "across GPUs is designed, not built)", file=sys.stderr)
