@@ -42,6 +42,26 @@ def test_topk64_matches_oracle(ctx, rows, V):
         assert np.allclose(gz[:, 1], oz[:, 1], rtol=2e-5)
 
 
+@pytest.mark.parametrize("order", ["ascending", "descending", "sawtooth"])
+def test_topk64_buffer_paths_match_oracle(ctx, order):
+    """Orders that drive the chunk kernel's candidate buffer to its extremes: ascending logits make every element beat
+    the running 64th best (a flush per 64 elements), descending ones admit only the first 64 of each wave, a sawtooth
+    mixes both with ties across the teeth."""
+    rows, V = 5, 151936
+    base = np.arange(V, dtype=np.float32)
+    x = {"ascending": base / 1000.0, "descending": -base / 1000.0, "sawtooth": np.float32(0.25) * (base % 997)}[order]
+    x = np.tile(x, (rows, 1)).astype(np.float32)
+    x[1] *= -1.0
+    x[2, ::5] = np.nan
+    for temp in (0.7, 1.0):
+        gi, gv, gz = gpu_topk(ctx, x, temp)
+        oi, ov, oz = oracle.topk64(x, temp)
+        assert np.array_equal(gi, oi)
+        assert np.array_equal(gv, ov)
+        assert np.array_equal(gz[:, 0], oz[:, 0])
+        assert np.allclose(gz[:, 1], oz[:, 1], rtol=2e-5)
+
+
 def test_accept_sample_matches_oracle(ctx):
     """Many rounds on one device state: drafts planted from each row's likely candidates, uniforms random; m and the
     emitted tokens equal the oracle's on the same candidates and uniforms (a uniform within 1e-5 of an acceptance
