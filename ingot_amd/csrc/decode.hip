@@ -7,7 +7,7 @@
 // the cache position after the last emitted token. The drafter here is the copy-from-context lookup over the
 // device-resident history (CopyIndex's rule, Sources/Ingot/CopySpec.swift:118-138), or none (one row per round: plain
 // chained decoding). With a temperature the acceptance is the rejection sampling of spec_accept_sample over each row's
-// 64 candidates, with the uniforms of round r at rnd[32·r …] drawn from SplitMix64(seed) on the host
+// 64 candidates, with the uniforms of round r at rnd[IH_RND_PER_ROUND·r …] drawn from SplitMix64(seed) on the host
 // (roundUniforms, Generate.swift:505-512).
 #include <algorithm>
 #include <cstring>
