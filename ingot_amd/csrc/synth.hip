@@ -1,10 +1,10 @@
-// Synthetic weights and KV of the benchmark configurations (random int4 weights, N(0,1) int8 KV),
+// Synthetic weights and KV of the benchmark configurations (benchmark configurations: random int4 weights, N(0,1) int8 KV),
 // generated on the GPU from counter-based SplitMix64 streams (act.h) so that any element is a pure function of
 // (seed, tensor id, index) and the CPU oracle regenerates the same bits.
 //
 //   int4 codes   word j of a tensor = 32-bit half (j & 1) of h(key_w, j >> 1)            (uniform nibbles 0..15)
-//   scales       bf16(|n(key_s, g)| · sd), n ≈ N(0,1) (act.h sm_normal), biases bf16(−8 · scale)  (BASELINE cfg 0)
-//   mxfp4        codes as int4; e8m0 scale of group g = 119 + h(key_s, g) mod 7      (2^-8 … 2^-2, BASELINE cfg 4)
+//   scales       bf16(|n(key_s, g)| · sd), n ≈ N(0,1) (act.h sm_normal), biases bf16(−8 · scale)  (benchmark configuration 0)
+//   mxfp4        codes as int4; e8m0 scale of group g = 119 + h(key_s, g) mod 7      (2^-8 … 2^-2, benchmark configuration 4)
 //   norm weights bf16(1 + 0.125 · n(key, i))
 //   KV           per (head, position): x_d = n(key, ((head << 24) + pos) · HD + d), symmetric int8 with fp16 scale
 //                sc = fp16(amax / 127) (1 when amax = 0), q = clamp(rint(x / sc), ±127)

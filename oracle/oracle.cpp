@@ -264,7 +264,7 @@ float or_f16_to_f32(uint16_t h) {
 
 // Symmetric int8 of one head vector with an fp16 scale: sc = fp16(amax/127) (1 when amax = 0), q = clamp(rint(x/sc),
 // ±127). CPU.quantI8 (Tests/IngotTests/KernelHarness.swift:249-254) and vattn_prework_i8 (verify_attn_nax.metal:112-139),
-// with the scale stored in fp16 instead of fp32.
+// with the scale stored in fp16 (benchmark configuration 1) instead of fp32.
 static void quant_i8(const float* x, int n, int8_t* q, uint16_t* sc16) {
   float amax = 0.f;
   for (int i = 0; i < n; ++i) amax = std::max(amax, std::fabs(x[i]));

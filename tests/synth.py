@@ -11,7 +11,7 @@ def rng(seed: int) -> np.random.Generator:
 
 
 def int4_matrix(g: np.random.Generator, N: int, K: int, E: int | None = None, scale_sd: float = 0.02):
-    """MLX int4 g64: uniform codes, bf16 scale ~ |N(0, scale_sd)|, bias = -8·scale."""
+    """MLX int4 g64: uniform codes, bf16 scale ~ |N(0, scale_sd)|, bias = -8·scale (benchmark configuration 0)."""
     shape = (N, K) if E is None else (E, N, K)
     q = g.integers(0, 16, size=shape, dtype=np.uint32)
     w = pack_nibbles(q)
@@ -67,7 +67,7 @@ def zipf_context(seed: int, n: int = 131072, vocab: int = 151936, s: float = 1.1
 
 def mxfp4_matrix(g: np.random.Generator, N: int, K: int, E: int | None = None, lo: int = 119, hi: int = 125):
     """MLX mxfp4: uniform e2m1 codes (8 per uint32, low nibble first), e8m0 scales uniform in [lo, hi]
-    (2^-8 … 2^-2 by default)."""
+    (2^-8 … 2^-2 by default: benchmark configuration 4)."""
     shape = (N, K) if E is None else (E, N, K)
     q = g.integers(0, 16, size=shape, dtype=np.uint32)
     s = g.integers(lo, hi + 1, size=shape[:-1] + (K // 32,), dtype=np.uint8)

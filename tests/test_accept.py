@@ -30,7 +30,7 @@ def test_host_accept_matches_oracle_and_brute_force():
 
 
 def test_accept_config0_forced_prefix():
-    """logits [8, 32000] ~ N(0,1), 7 drafts with the first 3 forced to the argmax → m ≥ 3."""
+    """Benchmark configuration 0: logits [8, 32000] ~ N(0,1), 7 drafts with the first 3 forced to the argmax → m ≥ 3."""
     g = np.random.default_rng(0)
     logits = g.normal(0, 1, size=(8, 32000)).astype(np.float32)
     top1 = oracle.argmax_rows(logits)

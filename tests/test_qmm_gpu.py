@@ -35,7 +35,7 @@ def run_qmm(ctx, W, xb, M, out_mode=0, y0=None):
 @pytest.mark.parametrize(
     "M,N,K,seed",
     [
-        (8, 4096, 4096, 0),
+        (8, 4096, 4096, 0),      # benchmark configuration 0
         (1, 256, 2048, 1),
         (5, 512, 4096, 2),
         (16, 1024, 1024, 3),
