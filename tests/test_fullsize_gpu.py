@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from ingot_amd._lib import KVCache, Model, ModelDesc, accept, check, lib
+from ingot_amd._lib import Drafter, DrafterDesc, KVCache, Model, ModelDesc, accept, check, lib
 from synth import cosine
 
 pytestmark = pytest.mark.gpu
@@ -160,5 +160,44 @@ def test_fullsize_verify_matches_oracle(ctx, name):
         om.free()
         assert kv.pos == P
     finally:
+        kv.free()
+        m.free()
+
+
+def test_fullsize_drafter_block_matches_oracle(ctx):
+    """The DFlash2 drafter of the bench's decode loop at its full shape (5 layers at config 1's hidden size, 32 q heads
+    of 128, intermediate 12288, block 16, window 2048, rank 256, captures of target layers 1, 7, 13, 19, 25) on config
+    1's target: the GPU's captures of a 17-row verify step at P = 8192 as context (three writes), then blocks at
+    P = 51, against oracle.OracleDrafter on the same captures: drafts bit-exact (measured: equal, with confidences
+    within 1e-3), confidences within 2e-2 (a confidence is softmax(score/1.5) over the 16 candidates; the scores carry
+    the head's logit error, ~0.01 at config 1)."""
+    print("[fullsize] drafter: building", flush=True)
+    d = ModelDesc.make(**DENSE8B)
+    m = Model(ctx, d, SEED)
+    P = 8192
+    kv = KVCache(m, P + 64)
+    dd = DrafterDesc.make(targets=(1, 7, 13, 19, 25), n_layers=5, hidden=4096, n_q_heads=32, head_dim=128,
+                          intermediate=12288, block=16, window=2048, rank=256, dyn_conv=1, mask_token=d.vocab - 1)
+    dr = Drafter(m, dd, SEED + 1)
+    od = oracle.OracleDrafter(dd, SEED + 1, d, SEED)
+    try:
+        kv.fill_synthetic(P, KV_SEED)
+        dr.attach()
+        toks = np.random.default_rng(5).integers(0, d.vocab, size=17).astype(np.uint32)
+        kv.verify(toks)
+        caps = dr.captures(17)
+        for pos0 in (0, 17, 34):
+            dr.context(17, 17, pos0)
+            od.context(caps, 17, pos0)
+        for anchor in (int(toks[3]), int(toks[11])):
+            gd, gc = dr.block(anchor, 51)
+            odr, oc = od.block(anchor, 51)
+            report("drafter-fullsize", anchor=anchor, drafts=[int(x) for x in gd], oracle_drafts=[int(x) for x in odr],
+                   conf_max_abs=float(np.abs(gc - oc).max()))
+            assert list(gd) == list(odr), (anchor, gd, odr)
+            assert np.abs(gc - oc).max() <= 2e-2, (gc, oc)
+    finally:
+        od.free()
+        dr.free()
         kv.free()
         m.free()
