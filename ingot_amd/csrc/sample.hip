@@ -249,43 +249,64 @@ __global__ __launch_bounds__(256) void topk64_merge_kernel(const uint32_t* __res
 }
 
 // Probabilities of a row's candidates after temperature, top-k, min-p and top-p, renormalised; returns how many
-// remain (sample_dist, zz_sample.metal:196-226).
-__device__ int sample_dist(const uint32_t* ci, const float* cv, float M, float Z, const ih_sample_params& p,
-                           float* pr) {
+// remain (sample_dist, zz_sample.metal:196-226). The loops run over all SK slots, unrolled, with the slots past the
+// count predicated off, so pr stays in registers; every sum still runs over j = 0, 1, … in order.
+__device__ __forceinline__ int sample_dist(const uint32_t* ci, const float* cv, float M, float Z,
+                                           const ih_sample_params& p, float (&pr)[SK]) {
   const float it = 1.0f / p.temp;
+  float e[SK];
   int n = 0;
-  while (n < SK && ci[n] != NO_ID) ++n;
+#pragma unroll
+  for (int j = 0; j < SK; ++j) {
+    n += int((n == j) & (ci[j] != NO_ID));  // the leading candidates that exist
+    e[j] = __expf((cv[j] - M) * it);
+  }
   float tot = Z;
   if (p.top_k > 0 && p.top_k < n) n = p.top_k;
   if (p.top_k > 0) {
     tot = 0.f;
-    for (int j = 0; j < n; ++j) tot += __expf((cv[j] - M) * it);
+#pragma unroll
+    for (int j = 0; j < SK; ++j)
+      if (j < n) tot += e[j];
   }
-  for (int j = 0; j < n; ++j) pr[j] = __expf((cv[j] - M) * it) / tot;
+#pragma unroll
+  for (int j = 0; j < SK; ++j) pr[j] = j < n ? e[j] / tot : 0.f;
   if (p.min_p > 0.f) {
     const float thr = p.min_p * pr[0];
     int k = 1;
-    while (k < n && pr[k] >= thr) ++k;
+#pragma unroll
+    for (int j = 1; j < SK; ++j) k += int((k == j) & (j < n) & (pr[j] >= thr));
     n = k;
-    float s = 0.f;
-    for (int j = 0; j < n; ++j) s += pr[j];
-    for (int j = 0; j < n; ++j) pr[j] /= s;
+    float sm = 0.f;
+#pragma unroll
+    for (int j = 0; j < SK; ++j)
+      if (j < n) sm += pr[j];
+#pragma unroll
+    for (int j = 0; j < SK; ++j)
+      if (j < n) pr[j] /= sm;
   }
   if (p.top_p < 1.f) {
     float c = 0.f;
     int k = n;
-    for (int j = 0; j < n; ++j) {
-      c += pr[j];
-      if (c >= p.top_p) {
-        k = j + 1;
-        break;
+    bool done = false;
+#pragma unroll
+    for (int j = 0; j < SK; ++j) {
+      if (j < n && !done) {
+        c += pr[j];
+        if (c >= p.top_p) {
+          k = j + 1;
+          done = true;
+        }
       }
     }
     n = max(k, 1);
   }
-  float s = 0.f;
-  for (int j = 0; j < n; ++j) s += pr[j];
-  for (int j = 0; j < n; ++j) pr[j] /= s;
+  float sm = 0.f;
+#pragma unroll
+  for (int j = 0; j < SK; ++j)
+    if (j < n) sm += pr[j];
+#pragma unroll
+  for (int j = 0; j < SK; ++j) pr[j] = j < n ? pr[j] / sm : 0.f;
   return n;
 }
 
@@ -315,56 +336,63 @@ __global__ __launch_bounds__(64) void accept_sample_kernel(uint32_t* st, uint32_
   __shared__ float prs[IH_MAX_ROWS][SK];
   __shared__ int ns[IH_MAX_ROWS];
   __shared__ float qs[IH_MAX_ROWS];
+  __shared__ float us[IH_RND_PER_ROUND];   // the round's uniforms
+  __shared__ uint32_t vts[IH_MAX_ROWS];    // the verify block
   const int lane = threadIdx.x;
   const uint32_t nr = rows ? uint32_t(rows) : min(max(st[6], 1u), uint32_t(IH_MAX_ROWS));
+  const uint32_t round = st[5], p0 = st[0];
+  // The walk below reads the uniforms and the block in LDS: loaded here by all lanes at once, not one dependent read
+  // per row.
+  if (lane < 2 * int(nr)) us[lane] = rnd[size_t(round) * IH_RND_PER_ROUND + lane];
+  if (lane < int(nr)) vts[lane] = vtok[lane];
   if (lane < int(nr)) {
     const uint32_t* ci = cidx + lane * SK;
-    const int n = sample_dist(ci, cval + lane * SK, z[2 * lane], z[2 * lane + 1], p, prs[lane]);
+    float pr[SK];
+    const int n = sample_dist(ci, cval + lane * SK, z[2 * lane], z[2 * lane + 1], p, pr);
     float q = 0.f;
-    if (lane + 1 < int(nr)) {
-      const uint32_t d = vtok[lane + 1];
-      for (int j = 0; j < n; ++j)
-        if (ci[j] == d) q = prs[lane][j];
+    const uint32_t d = lane + 1 < int(nr) ? vtok[lane + 1] : NO_ID;
+#pragma unroll
+    for (int j = 0; j < SK; ++j) {
+      if (j < n && ci[j] == d) q = pr[j];
+      prs[lane][j] = pr[j];
     }
     ns[lane] = n;
     qs[lane] = q;
   }
   __syncthreads();
   if (lane != 0) return;
-  const float* u = rnd + size_t(st[5]) * IH_RND_PER_ROUND;
   uint32_t m = 0, next = 0;
   for (uint32_t i = 0; i < nr; ++i) {
     const uint32_t* ci = cidx + i * SK;
     const int n = ns[i];
     if (i + 1 < nr) {
-      const uint32_t d = vtok[i + 1];
+      const uint32_t d = vts[i + 1];
       const float q = qs[i];
-      if (u[2 * i] < q) {
+      if (us[2 * i] < q) {
         ++m;
         continue;
       }
-      next = sample_pick(ci, prs[i], n, d, q, u[2 * i + 1]);
+      next = sample_pick(ci, prs[i], n, d, q, us[2 * i + 1]);
     } else {
-      next = sample_pick(ci, prs[i], n, NO_ID, 0.f, u[2 * i + 1]);
+      next = sample_pick(ci, prs[i], n, NO_ID, 0.f, us[2 * i + 1]);
     }
     break;
   }
-  uint32_t* r = rec + (st[5] % uint32_t(ring)) * IH_REC_STRIDE;
+  uint32_t* r = rec + (round % uint32_t(ring)) * IH_REC_STRIDE;
   r[0] = m;
   r[IH_REC_ROWS] = nr;
-  for (uint32_t i = 1; i <= m; ++i) r[i] = vtok[i];
+  for (uint32_t i = 1; i <= m; ++i) r[i] = vts[i];
   r[m + 1] = next;
-  r[IH_REC_P] = st[0];
-  const uint32_t p0 = st[0];
-  st[3] = st[0];
+  r[IH_REC_P] = p0;
+  st[3] = p0;
   st[2] = m + 1;
-  st[0] += m + 1;
+  st[0] = p0 + m + 1;
   st[1] = m + 1;
   st[4] = next;
-  st[5] += 1;
+  st[5] = round + 1;
   if (hist) {
     for (uint32_t i = 0; i < m; ++i)
-      if (p0 + 1 + i < uint32_t(hist_cap)) hist[p0 + 1 + i] = vtok[1 + i];
+      if (p0 + 1 + i < uint32_t(hist_cap)) hist[p0 + 1 + i] = vts[1 + i];
     if (p0 + 1 + m < uint32_t(hist_cap)) hist[p0 + 1 + m] = next;
   }
   vtok[0] = next;
